@@ -1,0 +1,353 @@
+"""Benchmark of the quantized decode hot path on one MI355X.
+
+Headline (BASELINE.json metric, configs[1]): Q4_K matvec throughput at the
+Llama-3-8B layer shapes, N=1.  One "step" = one decoder layer's four
+STREAM_DOTs with their ACT_Q8 prologues, weights resident in HBM:
+  ACT_Q8(x 4096) + QKV 6144x4096, ACT_Q8(x 4096) + O 4096x4096,
+  ACT_Q8(x 4096) + gate/up 28672x4096, ACT_Q8(h 14336) + down 4096x14336.
+Steps rotate over L layer copies (L * 122.7 MB > 2x the 256 MB Infinity
+Cache) so HBM, not MALL, is measured.  Each layer's step is a captured HIP
+graph; the timed region is K graph launches bracketed by stream syncs and
+HIP events.  value = weight bytes streamed / second (GB/s, 1e9).
+
+Also reported (same JSON line):
+  ops      -- per-op us and GB/s for every BASELINE config: Q8_0 4096^2,
+              each Q4_K layer shape, Q6_K vocab head and down, spec-verify
+              N in {2,4,8}, MoE top-2 of 8 at batch 1 and 8 (graph of R
+              launches rotating over weight copies, HIP events);
+  roofline -- the dominant kernel (Q4_K gate/up): algorithmic bytes per
+              launch / average launch time vs the 8 TB/s HBM peak;
+  cpu_baseline -- the reference CPU path on the host cores (oracle/_ref,
+              the reference's own code, if built; else the C restatement).
+Inputs are synthetic: weights N(0, 0.02^2) quantized on the device, x
+N(0,1) with 1 % x20 outliers for Q4_K.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+MALL_BYTES = 256 << 20
+METRIC = "Q4_K/Q6_K matvec GB/s (% of HBM peak) + us/op at Llama-3-8B shapes, N=1"
+
+Q8_0, Q4_K, Q6_K = 1, 3, 4
+LAYER = [("qkv", 6144, 4096), ("o", 4096, 4096), ("gate_up", 28672, 4096), ("down", 4096, 14336)]
+
+
+def col_stride(flh, cols):
+    return ((flh.x_alloc_bytes(cols) + 127) & ~127) // 4
+
+
+class Bench:
+    def __init__(self, flh, stream):
+        self.flh, self.s = flh, stream
+        self.bufs = []
+
+    def buf(self, nbytes):
+        b = self.flh.DeviceBuffer(nbytes)
+        self.bufs.append(b)
+        return b
+
+    def weights(self, fmt, rows, cols, copies, seed, staging):
+        """`copies` quantized matrices of N(0, 0.02^2) weights, made on the device."""
+        flh = self.flh
+        rb = flh.row_bytes(fmt, cols)
+        out = []
+        for c in range(copies):
+            w = self.buf(rows * rb)
+            step = max(1, staging.nbytes // (cols * 4))
+            for r0 in range(0, rows, step):
+                nr = min(step, rows - r0)
+                flh.fill_normal(staging, nr * cols, seed * 1000003 + c * 7919 + r0, self.s, std=0.02)
+                flh.quantize(fmt, staging, nr, cols, w.ptr + r0 * rb, self.s)
+            out.append(w)
+        self.s.sync()
+        return out
+
+    def activation(self, cols, nx, seed, outliers):
+        st = col_stride(self.flh, cols)
+        x = self.buf(nx * st * 4)
+        x.zero(self.s)
+        for p in range(nx):
+            self.flh.fill_normal(x.ptr + p * st * 4, cols, seed + p, self.s,
+                                 outlier_frac=0.01 if outliers else 0.0, outlier_scale=20.0)
+        self.flh.act_q8(x, cols, self.s, nx=nx, xstride=st)
+        return x, st
+
+    def time_graph(self, issue, reps):
+        """Capture issue() `reps` times in one graph; return us per rep."""
+        flh = self.flh
+        with flh.Graph.capture(self.s) as g:
+            for i in range(reps):
+                issue(i)
+        g.launch()                      # warm
+        self.s.sync()
+        e0, e1 = flh.Event(), flh.Event()
+        best = None
+        for _ in range(3):
+            e0.record(self.s)
+            g.launch()
+            e1.record(self.s)
+            self.s.sync()
+            t = e0.elapsed_ms(e1) * 1e3 / reps
+            best = t if best is None else min(best, t)
+        g.close()
+        e0.close()
+        e1.close()
+        return best
+
+
+def copies_for(nbytes):
+    return max(2, -(-3 * MALL_BYTES // nbytes))
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-ops", action="store_true", help="headline only")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU only (the matvec shards by rows; "
+              "see DESIGN.md); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import __graft_entry__ as ge
+    flh = ge._pkg()
+    flh.init(0)
+    info = flh.device_info()
+    s = flh.Stream()
+    B = Bench(flh, s)
+    staging = B.buf(256 << 20)
+
+    # ------------------------------------------------ headline: layer step
+    layer_bytes = sum(flh.row_bytes(Q4_K, c) * r for _, r, c in LAYER)
+    L = max(2, -(-3 * MALL_BYTES // layer_bytes))
+    W = {name: [] for name, _, _ in LAYER}
+    for name, r, c in LAYER:
+        W[name] = B.weights(Q4_K, r, c, L, seed=101 + r + 7 * c, staging=staging)
+    xin = {name: B.activation(c, 1, 10 + i, outliers=True) for i, (name, r, c) in enumerate(LAYER)}
+    yout = {name: B.buf(r * 4) for name, r, c in LAYER}
+    for y in yout.values():
+        y.zero(s)
+
+    def issue_layer(l):
+        for name, r, c in LAYER:
+            x, st = xin[name]
+            flh.act_q8(x, c, s)
+            flh.stream_dot(Q4_K, W[name][l], r, c, x, yout[name], s)
+
+    graphs = []
+    for l in range(L):
+        with flh.Graph.capture(s) as g:
+            issue_layer(l)
+        graphs.append(g)
+    for i in range(args.warmup):
+        graphs[i % L].launch()
+    s.sync()
+    e0, e1 = flh.Event(), flh.Event()
+    t0 = time.perf_counter()
+    e0.record(s)
+    for i in range(args.steps):
+        graphs[i % L].launch()
+    e1.record(s)
+    s.sync()
+    wall = time.perf_counter() - t0
+    ms = e0.elapsed_ms(e1)
+    ms_per_step = ms / args.steps
+    value = layer_bytes * args.steps / (ms * 1e-3) / 1e9
+
+    result = {
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic (weights N(0,0.02^2) quantized on device; x N(0,1), 1% x20 outliers)",
+        "config": {"workload": "Llama-3-8B layer Q4_K matvecs, N=1 (BASELINE configs[1])",
+                   "format": "Q4_K", "n": 1,
+                   "shapes": {n: [r, c] for n, r, c in LAYER},
+                   "weight_bytes_per_step": layer_bytes, "layer_copies": L,
+                   "device": info["arch"], "cus": info["num_cus"]},
+        "pct_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
+        "us_per_step": round(ms_per_step * 1e3, 2),
+        "wall_s_timed": round(wall, 4),
+    }
+
+    # ------------------------------------------------- per-op measurements
+    ops = {}
+
+    def op_entry(name, us, wbytes, extra=None):
+        e = {"us": round(us, 3), "weight_bytes": wbytes, "GBs": round(wbytes / us / 1e3, 1),
+             "pct_hbm": round(100 * wbytes / us / 1e3 / HBM_PEAK_GBS, 2)}
+        if extra:
+            e.update(extra)
+        ops[name] = e
+
+    REPS = 64
+    for name, r, c in LAYER:
+        x, st = xin[name]
+        nb = r * flh.row_bytes(Q4_K, c)
+        us = B.time_graph(lambda i: flh.stream_dot(Q4_K, W[name][i % L], r, c, x, yout[name], s), REPS)
+        op_entry(f"q4_K_{name}_{r}x{c}", us, nb)
+    # dominant kernel roofline: gate/up
+    r, c = 28672, 4096
+    gu = ops[f"q4_K_gate_up_{r}x{c}"]
+    alg = r * flh.row_bytes(Q4_K, c) + (c // 256) * 292 + r * 8
+    result["roofline"] = {"bound": "hbm", "achieved": round(alg / gu["us"] / 1e3, 1),
+                          "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                          "frac": round(alg / gu["us"] / 1e3 / HBM_PEAK_GBS, 4),
+                          "traffic": None, "kernel": "k_dot_i8k<Q4_K,1> gate/up 28672x4096",
+                          "alg_bytes_per_launch": alg, "us_per_launch": gu["us"]}
+
+    if not args.no_ops:
+        staging_cols = {}
+        # Q6_K vocab head and down
+        for name, r, c in [("vocab", 128256, 4096), ("down", 4096, 14336)]:
+            nb = r * flh.row_bytes(Q6_K, c)
+            ws = B.weights(Q6_K, r, c, copies_for(nb), seed=77 + r, staging=staging)
+            x, st = B.activation(c, 1, 30, outliers=False)
+            y = B.buf(r * 4)
+            us = B.time_graph(lambda i: flh.stream_dot(Q6_K, ws[i % len(ws)], r, c, x, y, s),
+                              8 if r > 100000 else REPS)
+            op_entry(f"q6_K_{name}_{r}x{c}", us, nb)
+            del ws
+        # Q8_0
+        r = c = 4096
+        nb = r * flh.row_bytes(Q8_0, c)
+        ws = B.weights(Q8_0, r, c, copies_for(nb), seed=5, staging=staging)
+        x, st = B.activation(c, 1, 40, outliers=False)
+        y = B.buf(r * 4)
+        us = B.time_graph(lambda i: flh.stream_dot(Q8_0, ws[i % len(ws)], r, c, x, y, s), REPS)
+        op_entry(f"q8_0_{r}x{c}", us, nb)
+        # spec-verify small N
+        for r, c in [(14336, 4096), (4096, 14336)]:
+            nb = r * flh.row_bytes(Q4_K, c)
+            ws = B.weights(Q4_K, r, c, copies_for(nb), seed=9 + r, staging=staging)
+            for n in (2, 4, 8):
+                x, st = B.activation(c, n, 50, outliers=True)
+                y = B.buf(n * r * 4)
+                us = B.time_graph(lambda i: flh.stream_dot(Q4_K, ws[i % len(ws)], r, c, x, y, s,
+                                                           nx=n, xstride=st, ystride=r), REPS)
+                op_entry(f"q4_K_verify_n{n}_{r}x{c}", us, nb, {"n": n})
+        # MoE decode: 8 experts, top-2, d_model 4096, d_ff 14336
+        result["moe"] = bench_moe(flh, B, s, staging)
+        ops.update(result["moe"].pop("ops"))
+    result["ops"] = ops
+
+    # ------------------------------------------------------- CPU baseline
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(flh, s, W, xin)
+    print(json.dumps(result), flush=True)
+
+
+def bench_moe(flh, B, s, staging):
+    """Mixtral-style MoE FFN: router -> grouped gate/up -> silu*up -> ACT_Q8 ->
+    grouped down -> weighted merge.  Two copies of the expert set alternate."""
+    E, K, D, F = 8, 2, 4096, 14336
+    gu_b = 2 * F * flh.row_bytes(Q4_K, D)
+    dn_b = D * flh.row_bytes(Q4_K, F)
+    copies = 2
+    gu = [B.weights(Q4_K, E * 2 * F, D, 1, seed=300 + c, staging=staging)[0] for c in range(copies)]
+    dn = [B.weights(Q4_K, E * D, F, 1, seed=400 + c, staging=staging)[0] for c in range(copies)]
+    out = {"ops": {}}
+    rng = np.random.default_rng(2)
+    for ntok in (1, 8):
+        stD, stF = col_stride(flh, D), col_stride(flh, F)
+        x, _ = B.activation(D, ntok, 60, outliers=False)
+        logits = B.buf(ntok * E * 4)
+        lg = [rng.standard_normal(ntok * E).astype(np.float32) for _ in range(copies)]
+        ids = B.buf(ntok * K * 4)
+        gates = B.buf(ntok * K * 4)
+        ygu = B.buf(ntok * K * 2 * F * 4)
+        h = B.buf(ntok * K * stF * 4)
+        h.zero(s)
+        ydn = B.buf(ntok * K * D * 4)
+        yo = B.buf(ntok * D * 4)
+        lbufs = []
+        for c in range(copies):
+            lb = B.buf(ntok * E * 4)
+            lb.upload(lg[c], s)
+            lbufs.append(lb)
+
+        def issue(i):
+            c = i % copies
+            flh.router_sel(lbufs[c], ntok, E, K, 1, 1.0, ids, gates, s)
+            flh.moe_dot(Q4_K, gu[c], gu_b, 2 * F, D, ids, ntok, K, E, x, stD, False, ygu, 2 * F, s)
+            flh.silu_mul(ygu, ygu.ptr + F * 4, h, F, ntok * K, 2 * F, stF, s)
+            flh.act_q8(h, F, s, nx=ntok * K, xstride=stF)
+            flh.moe_dot(Q4_K, dn[c], dn_b, D, F, ids, ntok, K, E, h, stF, True, ydn, D, s)
+            flh.wmerge(ydn, gates, None, None, yo, 1.0, K, D, 0, ntok, K * D, D, s)
+
+        us = B.time_graph(issue, 16)
+        # bytes actually streamed: distinct experts per step
+        distinct = []
+        for c in range(copies):
+            ll = lg[c].reshape(ntok, E)
+            sel = set()
+            for t in range(ntok):
+                sel.update(np.argsort(-ll[t], kind="stable")[:K].tolist())
+            distinct.append(len(sel))
+        nb = int(np.mean(distinct) * (gu_b + dn_b))
+        out["ops"][f"moe_q4_K_top2of8_batch{ntok}"] = {
+            "us": round(us, 3), "weight_bytes": nb, "distinct_experts": float(np.mean(distinct)),
+            "GBs": round(nb / us / 1e3, 1), "pct_hbm": round(100 * nb / us / 1e3 / HBM_PEAK_GBS, 2)}
+    return out
+
+
+def cpu_baseline(flh, s, W, xin):
+    """The reference CPU quantized-dot path on the host cores, same layer step
+    (4 Q4_K matvecs on the same bytes and appendices), rows split over T
+    threads like tools/membench.cu:276-300."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    from oracle import Oracle, REF_SO
+    kind = "reference" if os.path.exists(REF_SO) else "port"
+    orc = Oracle(ref=(kind == "reference"))
+    T = min(16, os.cpu_count() or 1)
+    host = {}
+    for name, r, c in LAYER:
+        w = W[name][0].download(np.uint8, r * flh.row_bytes(Q4_K, c), s)
+        x, st = xin[name]
+        xb = x.download(np.float32, st, s)
+        host[name] = (w, xb, r, c)
+    nbytes = sum(w.size for w, _, _, _ in host.values())
+
+    def run(threads):
+        for name, (w, xb, r, c) in host.items():
+            y = np.zeros(r, dtype=np.float32)
+            orc.stream_dot(Q4_K, w, r, c, xb, y, fast=True, threads=threads)
+    res = {}
+    for threads in (T, 1):
+        run(threads)
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            run(threads)
+            reps += 1
+            el = time.perf_counter() - t0
+            if el > (6.0 if threads > 1 else 4.0) or reps >= 50:
+                break
+        res[threads] = nbytes * reps / el / 1e9
+    cpu_model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round(res[T], 3), "unit": "GB/s", "cores": T, "kind": kind,
+            "value_1thread": round(res[1], 3), "cpu": cpu_model,
+            "sample": f"the same layer step (4 Q4_K matvecs, {nbytes} weight bytes) on the "
+                      f"host, i8k int8 path (exec_task_cpu, fast + default masks), repeated "
+                      f">= 4-6 s per thread count"}
+
+
+if __name__ == "__main__":
+    main()

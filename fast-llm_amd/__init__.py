@@ -1,0 +1,393 @@
+"""Host-side mirror of the reference runtime's task interface over the HIP C-ABI.
+
+The reference (qdox-labs/fast-llm) is C++17; its operator interface for this
+path is the ``Task`` record with ``TaskKind`` / ``Fmt`` codes
+(include/fastllm/fastllm.h:19-97) executed by ``exec_task_block`` /
+``exec_task_cpu``.  This module binds ``include/fastllm_hip.h`` with ctypes
+and exposes the same names and argument meanings, so parity tests read like
+the reference's own tests.  It loads ONLY the in-tree ``libfastllm_hip.so``;
+there is no CPU fallback: every op raises if the library or a GPU is absent.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import enum
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libfastllm_hip.so")
+
+
+class TaskKind(enum.IntEnum):
+    """include/fastllm/fastllm.h:19-45 (stable numeric values)."""
+    STREAM_DOT = 0
+    MERGE = 1
+    SIGNAL = 2
+    ACT_Q8 = 3
+    STREAM_DOT_IDX = 4
+    RMSNORM = 5
+    ADD2 = 6
+    ROPE_DS2 = 7
+    KV_APPEND = 8
+    ATTN_HEAD = 9
+    ROUTER_SEL = 10
+    SILU_MUL = 11
+    WMERGE = 12
+
+
+class Fmt(enum.IntEnum):
+    """include/fastllm/fastllm.h:56-57."""
+    F32 = 0
+    Q8_0 = 1
+    Q5_0 = 2
+    Q4_K = 3
+    Q6_K = 4
+    IQ2_XXS = 5
+    IQ3_XXS = 6
+
+
+BLK_ELEMS = {Fmt.F32: 1, Fmt.Q8_0: 32, Fmt.Q5_0: 32, Fmt.Q4_K: 256, Fmt.Q6_K: 256,
+             Fmt.IQ2_XXS: 256, Fmt.IQ3_XXS: 256}
+BLK_BYTES = {Fmt.F32: 4, Fmt.Q8_0: 34, Fmt.Q5_0: 22, Fmt.Q4_K: 144, Fmt.Q6_K: 210,
+             Fmt.IQ2_XXS: 66, Fmt.IQ3_XXS: 98}
+MAX_DOT_COLS = 16
+
+OK, ERR_ARG, ERR_HIP, ERR_UNSUPPORTED, ERR_NOMEM, ERR_STATE = 0, -1, -2, -3, -4, -5
+
+# reference CPU default masks (src/runtime/kernels.h:920,937)
+I8_MASK_DEFAULT = (1 << Fmt.Q8_0) | (1 << Fmt.Q5_0) | (1 << Fmt.Q4_K) | (1 << Fmt.Q6_K)
+I8K_MASK_DEFAULT = (1 << Fmt.Q4_K) | (1 << Fmt.Q6_K)
+
+
+def row_bytes(fmt: int, cols: int) -> int:
+    """fl_row_bytes (src/runtime/quants.h:97-99)."""
+    return (cols // BLK_ELEMS[Fmt(fmt)]) * BLK_BYTES[Fmt(fmt)]
+
+
+def xq_offset(cols: int) -> int:
+    """fl_xq_of offset (src/runtime/quants.h:302-304)."""
+    return (cols * 4 + 15) & ~15
+
+
+def xqk_offset(cols: int) -> int:
+    """fl_xqk_of offset (src/runtime/quants.h:321-325)."""
+    return xq_offset(cols) + (((cols // 32) * 36 + 15) & ~15)
+
+
+def x_alloc_bytes(cols: int) -> int:
+    """fl_x_alloc_bytes (src/runtime/quants.h:326-330)."""
+    return xqk_offset(cols) + (cols // 256) * 292
+
+
+class Task(C.Structure):
+    """Byte layout of fastllm::Task (include/fastllm/fastllm.h:65-97)."""
+    _fields_ = [
+        ("id", C.c_uint32), ("kind", C.c_uint8), ("affinity", C.c_uint8),
+        ("fmt", C.c_uint8), ("n_consumers", C.c_uint16),
+        ("consumers", C.c_uint32 * 6), ("w", C.c_void_p), ("w_bytes", C.c_uint64),
+        ("x", C.c_void_p), ("y", C.c_void_p), ("rows", C.c_uint32), ("cols", C.c_uint32),
+        ("dep_init", C.c_int32), ("dep_count", C.c_int32), ("epoch", C.c_uint32),
+        ("handoff_ts", C.c_uint64), ("aux", C.c_void_p), ("aux2", C.c_uint64),
+        ("nx", C.c_uint32), ("xstride", C.c_uint32), ("ystride", C.c_uint32),
+        ("_pad", C.c_uint8 * (256 - 132)),
+    ]
+
+
+class RouterP(C.Structure):
+    """RouterP (src/runtime/decode_params.h:68-75)."""
+    _fields_ = [("logits", C.c_void_p), ("ids", C.c_void_p), ("gates", C.c_void_p),
+                ("n_expert", C.c_uint32), ("top_k", C.c_uint32), ("norm", C.c_uint32),
+                ("scale", C.c_float)]
+
+
+class SiluMulP(C.Structure):
+    """SiluMulP (src/runtime/decode_params.h:77-82)."""
+    _fields_ = [("gate", C.c_void_p), ("up", C.c_void_p), ("h", C.c_void_p), ("n", C.c_uint32)]
+
+
+class WmergeP(C.Structure):
+    """WmergeP (src/runtime/decode_params.h:84-97)."""
+    _fields_ = [("parts", C.c_void_p), ("gates", C.c_void_p), ("add1", C.c_void_p),
+                ("add2", C.c_void_p), ("y", C.c_void_p), ("scale", C.c_float),
+                ("n_parts", C.c_uint32), ("n", C.c_uint32), ("n_full", C.c_uint32)]
+
+
+class FlhError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"fastllm_hip error {code}: {msg}")
+        self.code = code
+
+
+_lib = None
+
+_U32, _U64, _I, _P, _F, _SZ = C.c_uint32, C.c_uint64, C.c_int, C.c_void_p, C.c_float, C.c_size_t
+_SIGS = {
+    "flh_last_error": (C.c_char_p, []),
+    "flh_init": (_I, [_I]),
+    "flh_device_info": (_I, [C.POINTER(_I), C.POINTER(_SZ), C.POINTER(_I), C.c_char_p, _SZ]),
+    "flh_default_masks": (None, [C.POINTER(_U32), C.POINTER(_U32)]),
+    "flh_row_bytes": (_U64, [_I, _U32]),
+    "flh_x_alloc_bytes": (_SZ, [_U32]),
+    "flh_arena_create": (_I, [_SZ, C.POINTER(_P)]),
+    "flh_arena_alloc": (_I, [_P, _SZ, _SZ, C.POINTER(_P)]),
+    "flh_arena_used": (_SZ, [_P]),
+    "flh_arena_destroy": (_I, [_P]),
+    "flh_malloc": (_I, [_SZ, C.POINTER(_P)]),
+    "flh_free": (_I, [_P]),
+    "flh_upload": (_I, [_P, _P, _SZ, _P]),
+    "flh_download": (_I, [_P, _P, _SZ, _P]),
+    "flh_zero": (_I, [_P, _SZ, _P]),
+    "flh_stream_create": (_I, [C.POINTER(_P)]),
+    "flh_stream_sync": (_I, [_P]),
+    "flh_stream_destroy": (_I, [_P]),
+    "flh_event_create": (_I, [C.POINTER(_P)]),
+    "flh_event_record": (_I, [_P, _P]),
+    "flh_event_elapsed_ms": (_I, [_P, _P, C.POINTER(_F)]),
+    "flh_event_destroy": (_I, [_P]),
+    "flh_graph_capture_begin": (_I, [_P]),
+    "flh_graph_capture_end": (_I, [_P, C.POINTER(_P)]),
+    "flh_graph_launch": (_I, [_P, _P]),
+    "flh_graph_destroy": (_I, [_P]),
+    "flh_act_q8": (_I, [_P, _P, _U32, _U32, _U32, _P]),
+    "flh_stream_dot": (_I, [_I, _P, _U64, _U32, _U32, _P, _P, _U32, _U32, _U32, _P, _U64,
+                            _I, _U32, _U32, _P]),
+    "flh_exec_tasks": (_I, [_P, _U32, _I, _U32, _U32, _P]),
+    "flh_dequant": (_I, [_I, _P, _U32, _U32, _P, _P]),
+    "flh_moe_dot": (_I, [_I, _P, _U64, _U32, _U32, _P, _U32, _U32, _U32, _P, _U32, _U32, _P,
+                         _U32, _P]),
+    "flh_router_sel": (_I, [_P, _U32, _U32, _U32, _U32, _F, _P, _P, _P]),
+    "flh_silu_mul": (_I, [_P, _P, _P, _U32, _U32, _U32, _U32, _P]),
+    "flh_wmerge": (_I, [_P, _P, _P, _P, _P, _F, _U32, _U32, _U32, _U32, _U32, _U32, _P]),
+    "flh_fill_normal": (_I, [_P, _SZ, _U64, _F, _F, _F, _F, _P]),
+    "flh_quantize": (_I, [_I, _P, _U32, _U32, _P, _P]),
+    "flh_quantize_host": (_I, [_I, _P, _U32, _U32, _P]),
+}
+
+
+def lib():
+    """Load the in-tree HIP library (raises if it was not built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise FlhError(ERR_STATE, f"{LIB_PATH} not built: run __graft_entry__.build()")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(rc: int) -> None:
+    if rc != OK:
+        raise FlhError(rc, lib().flh_last_error().decode())
+
+
+def _p(v):
+    """Device pointer argument: DeviceBuffer, int address or None."""
+    if v is None:
+        return None
+    if isinstance(v, DeviceBuffer):
+        return v.ptr
+    return int(v)
+
+
+_initialised = False
+
+
+def init(device: int = 0) -> None:
+    global _initialised
+    check(lib().flh_init(device))
+    _initialised = True
+
+
+def device_info() -> dict:
+    cus, hbm, ws = C.c_int(), C.c_size_t(), C.c_int()
+    name = C.create_string_buffer(128)
+    check(lib().flh_device_info(C.byref(cus), C.byref(hbm), C.byref(ws), name, 128))
+    return {"num_cus": cus.value, "hbm_bytes": hbm.value, "wave_size": ws.value,
+            "arch": name.value.decode()}
+
+
+class Stream:
+    def __init__(self):
+        h = C.c_void_p()
+        check(lib().flh_stream_create(C.byref(h)))
+        self.handle = h.value
+
+    def sync(self):
+        check(lib().flh_stream_sync(self.handle))
+
+    def close(self):
+        if self.handle:
+            check(lib().flh_stream_destroy(self.handle))
+            self.handle = None
+
+
+class Event:
+    def __init__(self):
+        h = C.c_void_p()
+        check(lib().flh_event_create(C.byref(h)))
+        self.handle = h.value
+
+    def record(self, stream: Stream):
+        check(lib().flh_event_record(self.handle, stream.handle))
+
+    def elapsed_ms(self, end: "Event") -> float:
+        ms = C.c_float()
+        check(lib().flh_event_elapsed_ms(self.handle, end.handle, C.byref(ms)))
+        return ms.value
+
+    def close(self):
+        if self.handle:
+            check(lib().flh_event_destroy(self.handle))
+            self.handle = None
+
+
+class Graph:
+    """A captured HIP graph: `with Graph.capture(stream) as g: <issue work>`."""
+
+    def __init__(self, stream: Stream):
+        self.stream = stream
+        self.handle = None
+
+    @classmethod
+    def capture(cls, stream: Stream) -> "Graph":
+        return cls(stream)
+
+    def __enter__(self):
+        check(lib().flh_graph_capture_begin(self.stream.handle))
+        return self
+
+    def __exit__(self, et, ev, tb):
+        h = C.c_void_p()
+        rc = lib().flh_graph_capture_end(self.stream.handle, C.byref(h))
+        if et is None:
+            check(rc)
+            self.handle = h.value
+        return False
+
+    def launch(self, stream: Stream | None = None) -> None:
+        check(lib().flh_graph_launch(self.handle, (stream or self.stream).handle))
+
+    def close(self):
+        if self.handle:
+            check(lib().flh_graph_destroy(self.handle))
+            self.handle = None
+
+
+class DeviceBuffer:
+    """A hipMalloc'd device buffer (freed on close / garbage collection)."""
+
+    def __init__(self, nbytes: int):
+        h = C.c_void_p()
+        check(lib().flh_malloc(max(int(nbytes), 1), C.byref(h)))
+        self.ptr = h.value
+        self.nbytes = int(nbytes)
+
+    @classmethod
+    def from_array(cls, arr: np.ndarray, stream: Stream, extra: int = 0) -> "DeviceBuffer":
+        arr = np.ascontiguousarray(arr)
+        b = cls(arr.nbytes + extra)
+        b.upload(arr, stream)
+        return b
+
+    def upload(self, arr: np.ndarray, stream: Stream, offset: int = 0) -> None:
+        arr = np.ascontiguousarray(arr)
+        assert offset + arr.nbytes <= self.nbytes
+        check(lib().flh_upload(self.ptr + offset, arr.ctypes.data, arr.nbytes, stream.handle))
+
+    def download(self, dtype, count: int, stream: Stream, offset: int = 0) -> np.ndarray:
+        out = np.empty(count, dtype=dtype)
+        assert offset + out.nbytes <= self.nbytes
+        check(lib().flh_download(out.ctypes.data, self.ptr + offset, out.nbytes, stream.handle))
+        return out
+
+    def zero(self, stream: Stream) -> None:
+        check(lib().flh_zero(self.ptr, self.nbytes, stream.handle))
+
+    def close(self):
+        if self.ptr and lib():
+            lib().flh_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+# ---------------------------------------------------------------- ops --
+def act_q8(x, cols: int, stream: Stream, nx: int = 1, xstride: int = 0, y_q81=None) -> None:
+    """ACT_Q8 (fl_exec_act_q8, src/runtime/quants.h:404-416) on nx columns."""
+    check(lib().flh_act_q8(_p(x), _p(y_q81), cols, nx, xstride, stream.handle))
+
+
+def stream_dot(fmt: int, w, rows: int, cols: int, x, y, stream: Stream, nx: int = 1,
+               xstride: int = 0, ystride: int = 0, id_slot=None, estride: int = 0,
+               fast: bool = True, i8_mask: int = I8_MASK_DEFAULT,
+               i8k_mask: int = I8K_MASK_DEFAULT, w_bytes: int | None = None) -> None:
+    """One STREAM_DOT / STREAM_DOT_IDX tile (exec_task_cpu semantics, y +=)."""
+    if w_bytes is None:
+        w_bytes = rows * row_bytes(fmt, cols)
+    check(lib().flh_stream_dot(int(fmt), _p(w), w_bytes, rows, cols, _p(x), _p(y), nx,
+                               xstride, ystride, _p(id_slot), estride, int(bool(fast)),
+                               i8_mask, i8k_mask, stream.handle))
+
+
+def exec_tasks(tasks, stream: Stream, fast: bool = True, i8_mask: int = I8_MASK_DEFAULT,
+               i8k_mask: int = I8K_MASK_DEFAULT) -> None:
+    """Run a task table in order (the executor's per-task dispatch)."""
+    arr = (Task * len(tasks))(*tasks)
+    check(lib().flh_exec_tasks(C.cast(arr, C.c_void_p), len(tasks), int(bool(fast)),
+                               i8_mask, i8k_mask, stream.handle))
+
+
+def dequant(fmt: int, w, rows: int, cols: int, out, stream: Stream) -> None:
+    check(lib().flh_dequant(int(fmt), _p(w), rows, cols, _p(out), stream.handle))
+
+
+def moe_dot(fmt: int, w, estride: int, rows: int, cols: int, ids, ntok: int, top_k: int,
+            n_expert: int, x, xstride: int, x_per_slot: bool, y, ystride: int,
+            stream: Stream) -> None:
+    check(lib().flh_moe_dot(int(fmt), _p(w), estride, rows, cols, _p(ids), ntok, top_k,
+                            n_expert, _p(x), xstride, int(bool(x_per_slot)), _p(y), ystride,
+                            stream.handle))
+
+
+def router_sel(logits, ntok, n_expert, top_k, norm, scale, ids, gates, stream: Stream):
+    check(lib().flh_router_sel(_p(logits), ntok, n_expert, top_k, norm, scale, _p(ids),
+                               _p(gates), stream.handle))
+
+
+def silu_mul(gate, up, h, n, ncol, gstride, hstride, stream: Stream):
+    check(lib().flh_silu_mul(_p(gate), _p(up), _p(h), n, ncol, gstride, hstride, stream.handle))
+
+
+def wmerge(parts, gates, add1, add2, y, scale, n_parts, n, n_full, ncol, pstride, ystride,
+           stream: Stream):
+    check(lib().flh_wmerge(_p(parts), _p(gates), _p(add1), _p(add2), _p(y), scale, n_parts, n,
+                           n_full, ncol, pstride, ystride, stream.handle))
+
+
+def fill_normal(dst, n: int, seed: int, stream: Stream, mean: float = 0.0, std: float = 1.0,
+                outlier_frac: float = 0.0, outlier_scale: float = 1.0) -> None:
+    check(lib().flh_fill_normal(_p(dst), n, seed, mean, std, outlier_frac, outlier_scale,
+                                stream.handle))
+
+
+def quantize(fmt: int, src, rows: int, cols: int, dst, stream: Stream) -> None:
+    check(lib().flh_quantize(int(fmt), _p(src), rows, cols, _p(dst), stream.handle))
+
+
+def quantize_host(fmt: int, w: np.ndarray) -> np.ndarray:
+    """fp32 [rows, cols] -> block bytes, same bytes as the device quantizer."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    rows, cols = w.shape
+    out = np.zeros(rows * row_bytes(fmt, cols), dtype=np.uint8)
+    check(lib().flh_quantize_host(int(fmt), w.ctypes.data, rows, cols, out.ctypes.data))
+    return out

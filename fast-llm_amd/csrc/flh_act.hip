@@ -1,0 +1,158 @@
+// flh_act.hip -- ACT_Q8 (activation quantisation) and bit-exact dequant.
+//
+// ACT_Q8 writes, per column, the q8_1 appendix (per 32: f16 d, f16 s, i8 qs)
+// and the q8_K appendix (per 256: f32 d, i16 bsums[16], i8 qs) with the same
+// bytes as the reference's fl_quantize_q8_1_block / fl_quantize_q8_K_block
+// (src/runtime/quants.h:360-416): amax is a max (order free), d = amax/127
+// and id = 127/amax are correctly rounded IEEE divisions, q = roundf(x*id)
+// clamped to +-127, sums are exact integers, halves are RNE.
+//
+// One wave per 256-element chunk of one column: lane i owns elements
+// 4i..4i+3 (one 16-B load, one packed dword store per appendix); 8-lane
+// groups form the q8_1 blocks, 4-lane groups the q8_K 16-sums.
+#include "flh_common.h"
+#include "flh_internal.h"
+#include "flh_status.h"
+
+namespace flh {
+
+__device__ __forceinline__ float wave_max8(float v) {      // within 8 lanes
+    v = fmaxf(v, __shfl_xor(v, 1));
+    v = fmaxf(v, __shfl_xor(v, 2));
+    v = fmaxf(v, __shfl_xor(v, 4));
+    return v;
+}
+__device__ __forceinline__ int isum8(int v) {
+    v += __shfl_xor(v, 1);
+    v += __shfl_xor(v, 2);
+    v += __shfl_xor(v, 4);
+    return v;
+}
+
+__device__ __forceinline__ uint32_t quant4(const float (&v)[4], float id, int & sum) {
+    uint32_t packed = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        float q = roundf(v[j] * id);
+        if (q > 127.f) q = 127.f;
+        if (q < -127.f) q = -127.f;
+        const int qi = (int)q;
+        sum += qi;
+        packed |= ((uint32_t)qi & 0xFFu) << (8 * j);
+    }
+    return packed;
+}
+
+__global__ __launch_bounds__(64) void k_act_q8(float * x, uint8_t * yq, uint32_t cols,
+                                               uint32_t xstride) {
+    const uint32_t lane = threadIdx.x, chunk = blockIdx.x, col = blockIdx.y;
+    float * xc = x + (size_t)col * xstride;
+    uint8_t * q81 = yq ? yq + (size_t)col * xstride * 4 : (uint8_t *)xc + xq_off(cols);
+    uint8_t * q8k = (uint8_t *)xc + xqk_off(cols);
+    const uint32_t e0 = chunk * 256 + lane * 4;
+    float v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = (e0 + j < cols) ? xc[e0 + j] : 0.f;
+    float am = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+
+    // q8_1: block of 32 = 8 lanes
+    {
+        const uint32_t blk = chunk * 8 + (lane >> 3);
+        const float amax = wave_max8(am);
+        const float d = amax / 127.f;
+        const float id = amax > 0.f ? 127.f / amax : 0.f;
+        int s = 0;
+        const uint32_t pk = quant4(v, id, s);
+        const int sum = isum8(s);
+        if ((blk + 1) * 32 <= cols) {
+            uint8_t * o = q81 + (size_t)blk * 36;
+            *(uint32_t *)(o + 4 + 4 * (lane & 7)) = pk;
+            if ((lane & 7) == 0) *(uint32_t *)o = f2h(d) | (f2h(d * (float)sum) << 16);
+        }
+    }
+    // q8_K: whole chunk
+    if ((chunk + 1) * 256 <= cols) {
+        float amax = wave_max8(am);
+        amax = fmaxf(amax, __shfl_xor(amax, 8));
+        amax = fmaxf(amax, __shfl_xor(amax, 16));
+        amax = fmaxf(amax, __shfl_xor(amax, 32));
+        const float d = amax / 127.f;
+        const float id = amax > 0.f ? 127.f / amax : 0.f;
+        int s = 0;
+        const uint32_t pk = quant4(v, id, s);
+        s += __shfl_xor(s, 1);
+        s += __shfl_xor(s, 2);
+        uint8_t * o = q8k + (size_t)chunk * 292;
+        *(uint32_t *)(o + 36 + 4 * lane) = pk;
+        if ((lane & 3) == 0) *(int16_t *)(o + 4 + 2 * (lane >> 2)) = (int16_t)s;
+        if (lane == 0) *(float *)o = d;
+    }
+}
+
+int launch_act_q8(float * x, void * y_q81, uint32_t cols, uint32_t nx,
+                  uint32_t xstride, hipStream_t s) {
+    if (cols == 0 || nx == 0) return FLH_OK;
+    const uint32_t chunks = (cols + 255) / 256;
+    hipLaunchKernelGGL(k_act_q8, dim3(chunks, nx), dim3(64), 0, s, x, (uint8_t *)y_q81,
+                       cols, xstride);
+    return hip_check(hipGetLastError(), "k_act_q8 launch");
+}
+
+// ---------------------------------------------------------------- dequant --
+// Bit-exact restatement of dequant_chunk's value formulas; byte loads (this
+// is a correctness/embedding path, not the streamed hot loop).  One thread
+// per 32 outputs (Q8_0: a block; Q4_K: 16 nibble pairs; Q6_K: 16 positions x
+// 4 groups... split as 32 outputs of one group pair).
+__global__ void k_dequant(int fmt, const uint8_t * __restrict__ w, uint32_t rows,
+                          uint32_t cols, float * __restrict__ out) {
+    const uint64_t units_per_row = cols / 32;
+    const uint64_t u = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (u >= units_per_row * rows) return;
+    const uint32_t r = (uint32_t)(u / units_per_row), j = (uint32_t)(u % units_per_row);
+    float * o = out + (size_t)r * cols;
+    if (fmt == FMT_Q8_0) {
+        const uint8_t * b = w + (size_t)r * (cols / 32) * 34 + (size_t)j * 34;
+        const float d = h2f(b[0] | (b[1] << 8));
+        for (int i = 0; i < 32; ++i) o[32 * j + i] = d * (float)(int8_t)b[2 + i];
+    } else if (fmt == FMT_Q4_K) {
+        const uint32_t sb = j >> 3, g = j & 7, c = g >> 1;   // group g of superblock sb
+        const uint8_t * b = w + (size_t)r * (cols / 256) * 144 + (size_t)sb * 144;
+        const float d = h2f(b[0] | (b[1] << 8)), dmin = h2f(b[2] | (b[3] << 8));
+        const uint8_t * s = b + 4;
+        uint32_t sc, mn;
+        if (g < 4) { sc = s[g] & 63; mn = s[g + 4] & 63; }
+        else { sc = (s[g + 4] & 0xF) | ((s[g - 4] >> 6) << 4); mn = (s[g + 4] >> 4) | ((s[g] >> 6) << 4); }
+        const float d1 = d * (float)sc, m1 = dmin * (float)mn;
+        const uint8_t * q = b + 16 + 32 * c;
+        float * oo = o + 256 * sb + 64 * c + 32 * (g & 1);
+        for (int l = 0; l < 32; ++l) {
+            const uint32_t nib = (g & 1) ? (q[l] >> 4) : (q[l] & 0xF);
+            oo[l] = d1 * (float)nib - m1;
+        }
+    } else {  // Q6_K: group (h, gg) of superblock sb, positions l < 32
+        const uint32_t sb = j >> 3, h = (j >> 2) & 1, gg = j & 3;
+        const uint8_t * b = w + (size_t)r * (cols / 256) * 210 + (size_t)sb * 210;
+        const float d = h2f(b[208] | (b[209] << 8));
+        const uint8_t * ql = b + 64 * h, * qh = b + 128 + 32 * h;
+        const int8_t * sc = (const int8_t *)(b + 192) + 8 * h;
+        float * oo = o + 256 * sb + 128 * h + 32 * gg;
+        for (int l = 0; l < 32; ++l) {
+            const uint8_t lb = ql[l + 32 * (gg & 1)];
+            const int q6 = ((gg < 2) ? (lb & 0xF) : (lb >> 4)) | (((qh[l] >> (2 * gg)) & 3) << 4);
+            oo[l] = d * (float)sc[l / 16 + 2 * gg] * (float)(q6 - 32);
+        }
+    }
+}
+
+int launch_dequant(int fmt, const uint8_t * w, uint32_t rows, uint32_t cols,
+                   float * out, hipStream_t s) {
+    if (fmt != FMT_Q8_0 && fmt != FMT_Q4_K && fmt != FMT_Q6_K)
+        return set_error(FLH_ERR_UNSUPPORTED, "dequant: format not supported");
+    const uint64_t units = (uint64_t)rows * (cols / 32);
+    if (units == 0) return FLH_OK;
+    hipLaunchKernelGGL(k_dequant, dim3((uint32_t)((units + 255) / 256)), dim3(256), 0, s,
+                       fmt, w, rows, cols, out);
+    return hip_check(hipGetLastError(), "k_dequant launch");
+}
+
+}  // namespace flh

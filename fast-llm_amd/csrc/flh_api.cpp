@@ -1,0 +1,382 @@
+// flh_api.cpp -- the C-ABI boundary (include/fastllm_hip.h): device setup,
+// device arena, streams/events, argument validation mirroring the
+// reference's Graph::freeze() rules, per-task dispatch and row-tile fusion.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string.h>
+#include <string>
+#include <mutex>
+#include "../../include/fastllm_hip.h"
+#include "flh_common.h"
+#include "flh_internal.h"
+#include "flh_status.h"
+
+namespace flh {
+
+static thread_local std::string g_err;
+static int g_device = -1;
+static int g_cus = 256;
+
+int set_error(int code, const char * msg) {
+    g_err = msg ? msg : "";
+    return code;
+}
+int hip_check(hipError_t e, const char * what) {
+    if (e == hipSuccess) return FLH_OK;
+    g_err = std::string(what) + ": " + hipGetErrorString(e);
+    return FLH_ERR_HIP;
+}
+int num_cus() { return g_cus; }
+
+int launch_zero(void * p, size_t n, hipStream_t s);
+int quantize_host(int fmt, const float * src, uint32_t rows, uint32_t cols, uint8_t * dst);
+
+static uint32_t blk_elems(int fmt) {
+    switch (fmt) {
+        case FLH_FMT_Q8_0: case FLH_FMT_Q5_0: return 32;
+        case FLH_FMT_Q4_K: case FLH_FMT_Q6_K: case FLH_FMT_IQ2_XXS: case FLH_FMT_IQ3_XXS: return 256;
+        default: return 1;
+    }
+}
+static uint32_t blk_bytes(int fmt) {
+    switch (fmt) {
+        case FLH_FMT_Q8_0: return 34; case FLH_FMT_Q5_0: return 22; case FLH_FMT_Q4_K: return 144;
+        case FLH_FMT_Q6_K: return 210; case FLH_FMT_IQ2_XXS: return 66; case FLH_FMT_IQ3_XXS: return 98;
+        default: return 4;
+    }
+}
+
+static int need_init() {
+    if (g_device < 0) return set_error(FLH_ERR_STATE, "flh_init() has not been called");
+    return FLH_OK;
+}
+
+// freeze()-style validation of one dot tile (src/runtime/graph.cpp:84-90)
+static int validate_dot(int fmt, const void * w, uint64_t w_bytes, uint32_t rows, uint32_t cols,
+                        const float * x, float * y, uint32_t nx, const uint32_t * id_slot,
+                        uint64_t estride) {
+    if (fmt < FLH_FMT_F32 || fmt > FLH_FMT_IQ3_XXS) return set_error(FLH_ERR_ARG, "unknown weight format");
+    if (cols % blk_elems(fmt) != 0)
+        return set_error(FLH_ERR_ARG, "STREAM_DOT cols not a multiple of the format block size");
+    if (w_bytes != (uint64_t)rows * flh_row_bytes(fmt, cols))
+        return set_error(FLH_ERR_ARG, "STREAM_DOT w_bytes mismatch");
+    if (id_slot && estride == 0) return set_error(FLH_ERR_ARG, "STREAM_DOT_IDX without id slot / stride");
+    if (nx > FLH_MAX_DOT_COLS) return set_error(FLH_ERR_ARG, "nx exceeds kMaxDotCols (16)");
+    if (rows && (!w || !x || !y)) return set_error(FLH_ERR_ARG, "null weight / activation / output pointer");
+    if (((uintptr_t)w & 3) || (estride & 3) || ((uintptr_t)x & 3) || ((uintptr_t)y & 3))
+        return set_error(FLH_ERR_ARG, "w, x, y and the expert stride must be 4-byte aligned");
+    return FLH_OK;
+}
+
+static int dispatch_dot(int fmt, const DotArgs & a, int fast, uint32_t i8_mask, uint32_t i8k_mask,
+                        hipStream_t s) {
+    if (!fast) return launch_dot_canonical(fmt, a, s);
+    if ((fmt == FLH_FMT_Q4_K || fmt == FLH_FMT_Q6_K) && ((i8k_mask >> fmt) & 1u))
+        return launch_dot_i8k(fmt, a, s);
+    if (fmt != FLH_FMT_F32 && ((i8_mask >> fmt) & 1u)) {
+        if (fmt == FLH_FMT_Q8_0) return launch_dot_i8_q8_0(a, s);
+        return set_error(FLH_ERR_UNSUPPORTED,
+                         "q8_1 int8 path is implemented for Q8_0 only (use the i8k mask for K formats)");
+    }
+    return launch_dot_fast_f32(fmt, a, s);
+}
+
+}  // namespace flh
+
+using namespace flh;
+
+struct flh_arena {
+    uint8_t * base;
+    size_t cap, used;
+};
+
+extern "C" {
+
+const char * flh_last_error(void) { return g_err.c_str(); }
+
+int flh_init(int device) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n == 0)
+        return set_error(FLH_ERR_STATE, "no HIP device visible");
+    if (device < 0 || device >= n) return set_error(FLH_ERR_ARG, "device index out of range");
+    if (int rc = hip_check(hipSetDevice(device), "hipSetDevice")) return rc;
+    hipDeviceProp_t p;
+    if (int rc = hip_check(hipGetDeviceProperties(&p, device), "hipGetDeviceProperties")) return rc;
+    g_cus = p.multiProcessorCount > 0 ? p.multiProcessorCount : 256;
+    g_device = device;
+    return FLH_OK;
+}
+
+int flh_device_info(int * num_cus, size_t * hbm_bytes, int * wave_size, char * name, size_t name_len) {
+    if (int rc = need_init()) return rc;
+    hipDeviceProp_t p;
+    if (int rc = hip_check(hipGetDeviceProperties(&p, g_device), "hipGetDeviceProperties")) return rc;
+    if (num_cus) *num_cus = p.multiProcessorCount;
+    if (hbm_bytes) *hbm_bytes = p.totalGlobalMem;
+    if (wave_size) *wave_size = p.warpSize;
+    if (name && name_len) {
+        strncpy(name, p.gcnArchName, name_len - 1);
+        name[name_len - 1] = 0;
+    }
+    return FLH_OK;
+}
+
+void flh_default_masks(uint32_t * i8_mask, uint32_t * i8k_mask) {
+    // kI8MaskCpuDefault / kI8KMaskCpuDefault (src/runtime/kernels.h:920,937)
+    if (i8_mask) *i8_mask = (1u << FLH_FMT_Q8_0) | (1u << FLH_FMT_Q5_0) | (1u << FLH_FMT_Q4_K) | (1u << FLH_FMT_Q6_K);
+    if (i8k_mask) *i8k_mask = (1u << FLH_FMT_Q4_K) | (1u << FLH_FMT_Q6_K);
+}
+
+uint64_t flh_row_bytes(int fmt, uint32_t cols) {
+    return (uint64_t)(cols / blk_elems(fmt)) * blk_bytes(fmt);
+}
+size_t flh_x_alloc_bytes(uint32_t cols) { return flh::x_alloc_bytes(cols); }
+
+// ---------------------------------------------------------------- memory --
+int flh_arena_create(size_t bytes, flh_arena ** out) {
+    if (int rc = need_init()) return rc;
+    if (!out) return set_error(FLH_ERR_ARG, "null out");
+    void * p = nullptr;
+    if (hipMalloc(&p, bytes ? bytes : 256) != hipSuccess)
+        return set_error(FLH_ERR_NOMEM, "arena hipMalloc failed");
+    *out = new flh_arena{(uint8_t *)p, bytes, 0};
+    return FLH_OK;
+}
+int flh_arena_alloc(flh_arena * a, size_t bytes, size_t align, void ** out) {
+    if (!a || !out) return set_error(FLH_ERR_ARG, "null arena / out");
+    if (align < 16) align = 16;
+    if (align & (align - 1)) return set_error(FLH_ERR_ARG, "alignment must be a power of two");
+    const size_t off = (a->used + align - 1) & ~(align - 1);
+    if (off + bytes > a->cap) return set_error(FLH_ERR_NOMEM, "arena exhausted");
+    a->used = off + bytes;
+    *out = a->base + off;
+    return FLH_OK;
+}
+size_t flh_arena_used(const flh_arena * a) { return a ? a->used : 0; }
+int flh_arena_destroy(flh_arena * a) {
+    if (!a) return FLH_OK;
+    const int rc = hip_check(hipFree(a->base), "arena hipFree");
+    delete a;
+    return rc;
+}
+int flh_malloc(size_t bytes, void ** out) {
+    if (int rc = need_init()) return rc;
+    if (!out) return set_error(FLH_ERR_ARG, "null out");
+    if (hipMalloc(out, bytes ? bytes : 256) != hipSuccess) return set_error(FLH_ERR_NOMEM, "hipMalloc failed");
+    return FLH_OK;
+}
+int flh_free(void * p) { return p ? hip_check(hipFree(p), "hipFree") : FLH_OK; }
+int flh_upload(void * dst, const void * src, size_t n, void * stream) {
+    if (int rc = hip_check(hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, (hipStream_t)stream), "upload")) return rc;
+    return hip_check(hipStreamSynchronize((hipStream_t)stream), "upload sync");
+}
+int flh_download(void * dst, const void * src, size_t n, void * stream) {
+    if (int rc = hip_check(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, (hipStream_t)stream), "download")) return rc;
+    return hip_check(hipStreamSynchronize((hipStream_t)stream), "download sync");
+}
+int flh_zero(void * dst, size_t n, void * stream) { return launch_zero(dst, n, (hipStream_t)stream); }
+
+// --------------------------------------------------------------- streams --
+int flh_stream_create(void ** out) {
+    if (int rc = need_init()) return rc;
+    hipStream_t s;
+    if (int rc = hip_check(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreate")) return rc;
+    *out = (void *)s;
+    return FLH_OK;
+}
+int flh_stream_sync(void * s) { return hip_check(hipStreamSynchronize((hipStream_t)s), "hipStreamSynchronize"); }
+int flh_stream_destroy(void * s) { return s ? hip_check(hipStreamDestroy((hipStream_t)s), "hipStreamDestroy") : FLH_OK; }
+int flh_event_create(void ** out) {
+    hipEvent_t e;
+    if (int rc = hip_check(hipEventCreate(&e), "hipEventCreate")) return rc;
+    *out = (void *)e;
+    return FLH_OK;
+}
+int flh_event_record(void * e, void * s) { return hip_check(hipEventRecord((hipEvent_t)e, (hipStream_t)s), "hipEventRecord"); }
+int flh_event_elapsed_ms(void * a, void * b, float * ms) {
+    if (int rc = hip_check(hipEventSynchronize((hipEvent_t)b), "hipEventSynchronize")) return rc;
+    return hip_check(hipEventElapsedTime(ms, (hipEvent_t)a, (hipEvent_t)b), "hipEventElapsedTime");
+}
+int flh_event_destroy(void * e) { return e ? hip_check(hipEventDestroy((hipEvent_t)e), "hipEventDestroy") : FLH_OK; }
+
+// ---------------------------------------------------------------- graphs --
+int flh_graph_capture_begin(void * stream) {
+    if (int rc = need_init()) return rc;
+    return hip_check(hipStreamBeginCapture((hipStream_t)stream, hipStreamCaptureModeThreadLocal),
+                     "hipStreamBeginCapture");
+}
+int flh_graph_capture_end(void * stream, void ** graph_exec) {
+    hipGraph_t g = nullptr;
+    if (int rc = hip_check(hipStreamEndCapture((hipStream_t)stream, &g), "hipStreamEndCapture")) return rc;
+    hipGraphExec_t ge = nullptr;
+    const int rc = hip_check(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0), "hipGraphInstantiate");
+    hipGraphDestroy(g);
+    if (rc) return rc;
+    *graph_exec = (void *)ge;
+    return FLH_OK;
+}
+int flh_graph_launch(void * ge, void * stream) {
+    return hip_check(hipGraphLaunch((hipGraphExec_t)ge, (hipStream_t)stream), "hipGraphLaunch");
+}
+int flh_graph_destroy(void * ge) {
+    return ge ? hip_check(hipGraphExecDestroy((hipGraphExec_t)ge), "hipGraphExecDestroy") : FLH_OK;
+}
+
+// ------------------------------------------------------------------- ops --
+int flh_act_q8(float * x, void * y_q81, uint32_t cols, uint32_t nx, uint32_t xstride, void * stream) {
+    if (int rc = need_init()) return rc;
+    if (nx == 0) nx = 1;
+    if (!x || ((uintptr_t)x & 15) || (nx > 1 && (xstride & 3)))
+        return set_error(FLH_ERR_ARG, "act_q8: x must be non-null and 16-byte aligned, xstride a multiple of 4");
+    if (y_q81 && ((uintptr_t)y_q81 & 3)) return set_error(FLH_ERR_ARG, "act_q8: y must be 4-byte aligned");
+    return launch_act_q8(x, y_q81, cols, nx, xstride, (hipStream_t)stream);
+}
+
+int flh_stream_dot(int fmt, const void * w, uint64_t w_bytes, uint32_t rows, uint32_t cols,
+                   const float * x, float * y, uint32_t nx, uint32_t xstride, uint32_t ystride,
+                   const uint32_t * id_slot, uint64_t estride, int fast, uint32_t i8_mask,
+                   uint32_t i8k_mask, void * stream) {
+    if (nx == 0) nx = 1;
+    if (int rc = validate_dot(fmt, w, w_bytes, rows, cols, x, y, nx, id_slot, estride)) return rc;
+    if (int rc = need_init()) return rc;
+    DotArgs a{(const uint8_t *)w, id_slot, estride, x, y, rows, cols, nx, xstride, ystride};
+    return dispatch_dot(fmt, a, fast, i8_mask, i8k_mask, (hipStream_t)stream);
+}
+
+int flh_dequant(int fmt, const void * w, uint32_t rows, uint32_t cols, float * out, void * stream) {
+    if (int rc = need_init()) return rc;
+    if (cols % blk_elems(fmt)) return set_error(FLH_ERR_ARG, "dequant: cols not a multiple of the block size");
+    return launch_dequant(fmt, (const uint8_t *)w, rows, cols, out, (hipStream_t)stream);
+}
+
+int flh_exec_tasks(const flh_task * t, uint32_t n, int fast, uint32_t i8_mask, uint32_t i8k_mask,
+                   void * stream) {
+    if (n && !t) return set_error(FLH_ERR_ARG, "null task table");
+    // validate the whole table before launching anything
+    for (uint32_t i = 0; i < n; ++i) {
+        const flh_task & k = t[i];
+        switch (k.kind) {
+            case FLH_TASK_STREAM_DOT: case FLH_TASK_STREAM_DOT_IDX: {
+                const uint32_t * slot = k.kind == FLH_TASK_STREAM_DOT_IDX ? (const uint32_t *)k.aux : nullptr;
+                if (k.kind == FLH_TASK_STREAM_DOT_IDX && (!k.aux || !k.aux2))
+                    return set_error(FLH_ERR_ARG, "STREAM_DOT_IDX without id slot / stride");
+                if (int rc = validate_dot(k.fmt, k.w, k.w_bytes, k.rows, k.cols, (const float *)k.x,
+                                          (float *)k.y, k.nx ? k.nx : 1, slot, k.aux2)) return rc;
+                break;
+            }
+            case FLH_TASK_ACT_Q8:
+                if (!k.x || ((uintptr_t)k.x & 15)) return set_error(FLH_ERR_ARG, "ACT_Q8: x must be 16-byte aligned");
+                break;
+            case FLH_TASK_MERGE: case FLH_TASK_SIGNAL: break;
+            case FLH_TASK_ROUTER_SEL: case FLH_TASK_SILU_MUL: case FLH_TASK_WMERGE:
+                if (!k.aux) return set_error(FLH_ERR_ARG, "decode op without aux param block");
+                break;
+            default:
+                return set_error(FLH_ERR_UNSUPPORTED, "task kind not supported by the HIP backend");
+        }
+    }
+    if (int rc = need_init()) return rc;
+    hipStream_t s = (hipStream_t)stream;
+    for (uint32_t i = 0; i < n; ++i) {
+        const flh_task & k = t[i];
+        int rc = FLH_OK;
+        switch (k.kind) {
+            case FLH_TASK_STREAM_DOT: case FLH_TASK_STREAM_DOT_IDX: {
+                const bool idx = k.kind == FLH_TASK_STREAM_DOT_IDX;
+                DotArgs a{(const uint8_t *)k.w, idx ? (const uint32_t *)k.aux : nullptr, idx ? k.aux2 : 0,
+                          (const float *)k.x, (float *)k.y, k.rows, k.cols, k.nx ? k.nx : 1u,
+                          k.xstride, k.ystride};
+                // fuse following row tiles of the same matrix into this launch
+                while (i + 1 < n) {
+                    const flh_task & q = t[i + 1];
+                    if (q.kind != k.kind || q.fmt != k.fmt || q.cols != k.cols || q.x != k.x ||
+                        (q.nx ? q.nx : 1u) != a.nx || q.xstride != k.xstride || q.ystride != k.ystride ||
+                        q.aux != k.aux || q.aux2 != k.aux2 ||
+                        (const uint8_t *)q.w != a.w + (uint64_t)a.rows * flh_row_bytes(k.fmt, k.cols) ||
+                        (float *)q.y != a.y + a.rows)
+                        break;
+                    a.rows += q.rows;
+                    ++i;
+                }
+                rc = dispatch_dot(k.fmt, a, fast, i8_mask, i8k_mask, s);
+                break;
+            }
+            case FLH_TASK_ACT_Q8:
+                rc = launch_act_q8((float *)k.x, k.y, k.cols, 1, 0, s);
+                break;
+            case FLH_TASK_MERGE:
+                rc = launch_merge((const float *)k.x, (float *)k.y, k.rows, k.cols, s);
+                break;
+            case FLH_TASK_SIGNAL: break;
+            case FLH_TASK_ROUTER_SEL: {
+                const flh_router_p & p = *(const flh_router_p *)k.aux;
+                rc = launch_router_sel(p.logits, 1, p.n_expert, p.top_k, p.norm, p.scale, p.ids, p.gates, s);
+                break;
+            }
+            case FLH_TASK_SILU_MUL: {
+                const flh_silu_mul_p & p = *(const flh_silu_mul_p *)k.aux;
+                rc = launch_silu_mul(p.gate, p.up, p.h, p.n, 1, 0, 0, s);
+                break;
+            }
+            case FLH_TASK_WMERGE: {
+                const flh_wmerge_p & p = *(const flh_wmerge_p *)k.aux;
+                rc = launch_wmerge(p.parts, p.gates, p.add1, p.add2, p.y, p.scale, p.n_parts, p.n,
+                                   p.n_full, 1, 0, 0, s);
+                break;
+            }
+        }
+        if (rc) return rc;
+    }
+    return FLH_OK;
+}
+
+// ------------------------------------------------------------------- MoE --
+int flh_moe_dot(int fmt, const void * w, uint64_t estride, uint32_t rows, uint32_t cols,
+                const uint32_t * ids, uint32_t ntok, uint32_t top_k, uint32_t n_expert,
+                const float * x, uint32_t xstride, uint32_t x_per_slot, float * y, uint32_t ystride,
+                void * stream) {
+    if (int rc = need_init()) return rc;
+    if (fmt != FLH_FMT_Q4_K && fmt != FLH_FMT_Q6_K)
+        return set_error(FLH_ERR_UNSUPPORTED, "moe_dot: K formats (q8_K path) only");
+    if (cols % 256) return set_error(FLH_ERR_ARG, "moe_dot: cols not a multiple of 256");
+    if (!w || !ids || !x || !y || n_expert == 0) return set_error(FLH_ERR_ARG, "moe_dot: null argument");
+    if (estride < (uint64_t)rows * flh_row_bytes(fmt, cols) || (estride & 3) || ((uintptr_t)w & 3))
+        return set_error(FLH_ERR_ARG, "moe_dot: expert stride smaller than one expert or misaligned");
+    MoeArgs a{(const uint8_t *)w, estride, ids, x, y, rows, cols, ntok, top_k, n_expert, xstride, ystride,
+              x_per_slot};
+    return launch_moe_i8k(fmt, a, (hipStream_t)stream);
+}
+
+int flh_router_sel(const float * logits, uint32_t ntok, uint32_t n_expert, uint32_t top_k, uint32_t norm,
+                   float scale, uint32_t * ids, float * gates, void * stream) {
+    if (int rc = need_init()) return rc;
+    return launch_router_sel(logits, ntok, n_expert, top_k, norm, scale, ids, gates, (hipStream_t)stream);
+}
+int flh_silu_mul(const float * gate, const float * up, float * h, uint32_t n, uint32_t ncol,
+                 uint32_t gstride, uint32_t hstride, void * stream) {
+    if (int rc = need_init()) return rc;
+    return launch_silu_mul(gate, up, h, n, ncol, gstride, hstride, (hipStream_t)stream);
+}
+int flh_wmerge(const float * parts, const float * gates, const float * add1, const float * add2, float * y,
+               float scale, uint32_t n_parts, uint32_t n, uint32_t n_full, uint32_t ncol, uint32_t pstride,
+               uint32_t ystride, void * stream) {
+    if (int rc = need_init()) return rc;
+    return launch_wmerge(parts, gates, add1, add2, y, scale, n_parts, n, n_full, ncol, pstride, ystride,
+                         (hipStream_t)stream);
+}
+
+// ------------------------------------------------------- synthetic inputs --
+int flh_fill_normal(float * dst, size_t n, uint64_t seed, float mean, float stddev, float outlier_frac,
+                    float outlier_scale, void * stream) {
+    if (int rc = need_init()) return rc;
+    return launch_fill_normal(dst, n, seed, mean, stddev, outlier_frac, outlier_scale, (hipStream_t)stream);
+}
+int flh_quantize(int fmt, const float * src, uint32_t rows, uint32_t cols, void * dst, void * stream) {
+    if (int rc = need_init()) return rc;
+    return launch_quantize_weights(fmt, src, rows, cols, (uint8_t *)dst, (hipStream_t)stream);
+}
+int flh_quantize_host(int fmt, const float * src, uint32_t rows, uint32_t cols, void * dst) {
+    return quantize_host(fmt, src, rows, cols, (uint8_t *)dst);
+}
+
+}  // extern "C"

@@ -1,0 +1,90 @@
+// flh_common.h -- device helpers shared by the gfx950 kernels.
+//
+// Everything here is exact integer / bit work, or a single IEEE operation,
+// so kernels built on it reproduce the reference CPU path bit for bit when
+// the translation units are compiled with -ffp-contract=off.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <type_traits>
+
+namespace flh {
+
+// Fmt numeric values (reference include/fastllm/fastllm.h:56-57).
+enum : int { FMT_F32 = 0, FMT_Q8_0 = 1, FMT_Q5_0 = 2, FMT_Q4_K = 3, FMT_Q6_K = 4 };
+
+// Activation appendix offsets of one column (reference
+// src/runtime/quants.h:302-330): [f32 x cols][pad16][q8_1 x cols/32][pad16]
+// [q8_K x cols/256].  q8_1 = {f16 d, f16 s, i8 qs[32]} (36 B); q8_K =
+// {f32 d, i16 bsums[16], i8 qs[256]} (292 B).
+__host__ __device__ inline size_t xq_off(uint32_t cols) {
+    return ((size_t)cols * 4 + 15) & ~(size_t)15;
+}
+__host__ __device__ inline size_t xqk_off(uint32_t cols) {
+    return xq_off(cols) + ((((size_t)cols / 32) * 36 + 15) & ~(size_t)15);
+}
+__host__ __device__ inline size_t x_alloc_bytes(uint32_t cols) {
+    return xqk_off(cols) + ((size_t)cols / 256) * 292;
+}
+
+// binary16 -> binary32.  v_cvt_f32_f16 is exact for every finite half
+// (f16 denormals are preserved in the default HIP float mode).
+__device__ __forceinline__ float h2f(uint32_t h16) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h16);
+}
+
+// binary32 -> binary16, round to nearest even, NaN -> 0x7E00|sign; the same
+// mapping as the reference's fl_float2half (src/runtime/quants.h:333-356),
+// written from the IEEE definition.
+__device__ __forceinline__ uint32_t f2h(float f) {
+    const uint32_t u = __float_as_uint(f);
+    const uint32_t sign = (u >> 16) & 0x8000u, a = u & 0x7FFFFFFFu;
+    if (a >= 0x47800000u) return sign | (a > 0x7F800000u ? 0x7E00u : 0x7C00u);
+    if (a < 0x38800000u) {
+        const uint32_t e = a >> 23;
+        if (e < 102u) return sign;
+        const uint32_t m = (a & 0x7FFFFFu) | 0x800000u, sh = 126u - e;
+        uint32_t q = m >> sh;
+        const uint32_t r = m & ((1u << sh) - 1u), hb = 1u << (sh - 1u);
+        if (r > hb || (r == hb && (q & 1u))) ++q;
+        return sign | q;
+    }
+    uint32_t q = (((a >> 23) - 112u) << 10) | ((a >> 13) & 0x3FFu);
+    const uint32_t r = a & 0x1FFFu;
+    if (r > 0x1000u || (r == 0x1000u && (q & 1u))) ++q;
+    return sign | q;
+}
+
+// 4 x int8 dot product accumulate (v_dot4_i32_i8).
+__device__ __forceinline__ int dot4(int a, int b, int c) {
+    return __builtin_amdgcn_sdot4(a, b, c, false);
+}
+
+// ({hi,lo} >> 8*sh)[31:0], sh in 0..3 (v_alignbyte_b32).
+__device__ __forceinline__ uint32_t alignb(uint32_t hi, uint32_t lo, uint32_t sh) {
+    return __builtin_amdgcn_alignbyte(hi, lo, sh);
+}
+
+// DPP quad permutations: exchange with lane^1 / lane^2 inside each quad.
+__device__ __forceinline__ int qx1(int v) {
+    return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);   // [1,0,3,2]
+}
+__device__ __forceinline__ int qx2(int v) {
+    return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false);   // [2,3,0,1]
+}
+__device__ __forceinline__ float qx1f(float v) { return __int_as_float(qx1(__float_as_int(v))); }
+__device__ __forceinline__ float qx2f(float v) { return __int_as_float(qx2(__float_as_int(v))); }
+
+// Plain 4-byte-aligned global loads (dword alignment is all gfx950 needs
+// for multi-dword global loads).
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4), aligned(4)));
+__device__ __forceinline__ u32x4 ld4(const uint8_t * p) { return *(const u32x4 *)p; }
+__device__ __forceinline__ uint32_t ld1(const uint8_t * p) { return *(const uint32_t *)p; }
+__device__ __forceinline__ uint32_t ldh(const uint8_t * p) { return *(const uint16_t *)p; }
+// streamed-once weight loads: non-temporal hint keeps them from evicting the
+// reused activations from L2.
+__device__ __forceinline__ u32x4 ld4_nt(const uint8_t * p) {
+    return __builtin_nontemporal_load((const u32x4 *)p);
+}
+
+}  // namespace flh

@@ -1,0 +1,574 @@
+// flh_dot_int8.hip -- int8 STREAM_DOT kernels for gfx950 (wave64, CDNA4).
+//
+// Replaces the reference's GPU row-dots gdot_i8k_q4_K / gdot_i8k_q6_K /
+// gdot_i8_q8_0 (src/runtime/kernels_gpu.h:307-343,535-675) and matches the
+// reference CPU int8 path (src/runtime/quants.h:438-447,538-594) BIT FOR BIT:
+//
+//  * every integer partial (per-superblock iacc / imins, per-block idot) is
+//    exact, so it may be computed by any lanes in any order;
+//  * the only float work is the per-superblock (per-block for Q8_0) fmaf
+//    fold into acc[t & 3] followed by (a0 + a1) + (a2 + a3).  That fold runs
+//    in exactly the reference order, one lane per (row, column, accumulator).
+//
+// Work decomposition (one workgroup = 256 lanes = 4 waves):
+//  K formats: 4 lanes per 256-weight superblock.  Lane (slot s, part c) owns
+//    superblock position sb = s mod P (P = next pow2 >= superblocks per row)
+//    of row-sub s / P.  Its activation slice (64 int8 of the q8_K column) is
+//    loaded ONCE into registers and reused for every row the workgroup
+//    streams; weights stream straight from HBM into registers (dwordx4,
+//    non-temporal), two iterations in flight.  Integer partials are reduced
+//    across the 4 lanes with DPP quad permutes and parked in LDS as
+//    (row, column, sb) terms; after each batch of rows, lanes re-map to
+//    (row, column, accumulator) and run the ordered float chains.
+//  Q8_0: one lane per 34-byte block, same scheme with per-block terms.
+//
+// Layout facts used: Q4_K superblocks are 144 B, so with a 16-B aligned row
+// every superblock is 16-B aligned.  Q6_K (210 B) and Q8_0 (34 B) blocks are
+// only 2-B aligned; they are read as dword windows from the 4-B aligned
+// address below and realigned with v_alignbyte (never an unaligned or
+// out-of-block access).
+#include "flh_common.h"
+#include "flh_internal.h"
+#include "flh_status.h"
+
+namespace flh {
+
+__host__ __device__ inline uint32_t ceil_log2(uint32_t v) {
+    uint32_t l = 0;
+    while ((1u << l) < v) ++l;
+    return l;
+}
+
+// ------------------------------------------------------------ Q4_K x q8_K --
+struct Q4W { u32x4 h, qa, qb; };
+
+__device__ __forceinline__ Q4W q4_load(const uint8_t * blk, uint32_t c) {
+    Q4W r;
+    r.h  = ld4_nt(blk);
+    r.qa = ld4_nt(blk + 16 + 32 * c);
+    r.qb = ld4_nt(blk + 32 + 32 * c);
+    return r;
+}
+
+template <int NX>
+struct Q4X {                    // activation slice of one lane, NX columns
+    int q[NX][16];              // x[64c .. 64c+64) of this superblock
+    int b0[NX], b1[NX];         // bsums[4c]+bsums[4c+1], bsums[4c+2]+bsums[4c+3]
+};
+
+template <int NX>
+__device__ __forceinline__ void q4x_load(Q4X<NX> & X, const uint8_t * const * xk,
+                                         uint32_t nx, uint32_t sb, uint32_t c) {
+#pragma unroll
+    for (int p = 0; p < NX; ++p) {
+        const uint8_t * b = xk[p < (int)nx ? p : 0] + (size_t)sb * 292;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const u32x4 v = ld4(b + 36 + 64 * c + 16 * k);
+            X.q[p][4 * k + 0] = v.x; X.q[p][4 * k + 1] = v.y;
+            X.q[p][4 * k + 2] = v.z; X.q[p][4 * k + 3] = v.w;
+        }
+        const uint32_t s0 = ld1(b + 4 + 8 * c), s1 = ld1(b + 8 + 8 * c);
+        X.b0[p] = (int)(int16_t)(s0 & 0xFFFF) + (int)(int16_t)(s0 >> 16);
+        X.b1[p] = (int)(int16_t)(s1 & 0xFFFF) + (int)(int16_t)(s1 >> 16);
+    }
+}
+
+// ------------------------------------------------------------ Q6_K x q8_K --
+struct Q6W { u32x4 a, b, h, s; uint32_t a4, b4, h4, s4, sh; };
+
+__device__ __forceinline__ Q6W q6_load(const uint8_t * blk, uint32_t c) {
+    const uint32_t hh = c >> 1, bb = c & 1;
+    const uintptr_t ba = (uintptr_t)blk;
+    const uint8_t * f = (const uint8_t *)(ba & ~(uintptr_t)3);
+    Q6W r;
+    r.sh = (uint32_t)(ba & 3);
+    const uint32_t oa = 64 * hh + 16 * bb, ob = oa + 32, oh = 128 + 32 * hh + 16 * bb;
+    r.a = ld4_nt(f + oa); r.a4 = ld1(f + oa + 16);
+    r.b = ld4_nt(f + ob); r.b4 = ld1(f + ob + 16);
+    r.h = ld4_nt(f + oh); r.h4 = ld1(f + oh + 16);
+    r.s = ld4(f + 192);
+    r.s4 = ldh(f + 208) | (ldh(blk + 208) << 16);
+    return r;
+}
+
+template <int NX>
+struct Q6X {
+    int q[NX][4][4];            // [column][group g][dword i]
+    int b32[NX][4];             // 32 * bsums[8h + 2g + b]
+};
+
+template <int NX>
+__device__ __forceinline__ void q6x_load(Q6X<NX> & X, const uint8_t * const * xk,
+                                         uint32_t nx, uint32_t sb, uint32_t c) {
+    const uint32_t hh = c >> 1, bb = c & 1;
+#pragma unroll
+    for (int p = 0; p < NX; ++p) {
+        const uint8_t * b = xk[p < (int)nx ? p : 0] + (size_t)sb * 292;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const u32x4 v = ld4(b + 36 + 128 * hh + 32 * g + 16 * bb);
+            X.q[p][g][0] = v.x; X.q[p][g][1] = v.y; X.q[p][g][2] = v.z; X.q[p][g][3] = v.w;
+            X.b32[p][g] = 32 * (int)*(const int16_t *)(b + 4 + 2 * (8 * hh + 2 * g + bb));
+        }
+    }
+}
+
+// ------------------------------------------------------ K-format kernel core --
+// smem layout (ints): TI[nr][NX][P] (+ TM[nr][NX][P] for Q4_K), TH[nr][P],
+// XD[NX][P] (float, q8_K d of each column/superblock).
+template <int FMT>
+__host__ __device__ inline size_t kq_smem_bytes(uint32_t nr, uint32_t nx_t, uint32_t P) {
+    const size_t terms = (size_t)nr * nx_t * P * (FMT == FMT_Q4_K ? 2 : 1);
+    return 4 * (terms + (size_t)nr * P + (size_t)nx_t * P);
+}
+
+template <int FMT, int NX>
+__device__ __forceinline__ void kq_core(const uint8_t * __restrict__ w, uint32_t rows,
+                                        uint32_t cols, const uint8_t * const * xk,
+                                        float * const * yc, uint32_t nx, uint32_t nr,
+                                        uint32_t batch0, uint32_t bstep, int * smem) {
+    constexpr uint32_t BLK = FMT == FMT_Q4_K ? 144 : 210;
+    const uint32_t nsb = cols >> 8;
+    const uint32_t lgP = ceil_log2(nsb), P = 1u << lgP;
+    const uint32_t rpi = 64u >> lgP;
+    const uint64_t rb = (uint64_t)nsb * BLK;
+    const uint32_t tid = threadIdx.x, c = tid & 3, slot = tid >> 2;
+    const uint32_t rsub = slot >> lgP, sbl = slot & (P - 1);
+    const bool act = sbl < nsb;
+    const uint32_t sb = act ? sbl : nsb - 1;
+
+    int * TI = smem;
+    int * TM = TI + (size_t)nr * NX * P;
+    uint32_t * TH = (uint32_t *)(FMT == FMT_Q4_K ? TM + (size_t)nr * NX * P : TM);
+    float * XD = (float *)(TH + (size_t)nr * P);
+
+    for (uint32_t i = tid; i < NX * P; i += 256) {
+        const uint32_t p = i >> lgP, q = i & (P - 1);
+        XD[i] = (p < nx && q < nsb) ? *(const float *)(xk[p] + (size_t)q * 292) : 0.f;
+    }
+
+    // per-lane activation slice, resident for the whole launch
+    typename std::conditional<FMT == FMT_Q4_K, Q4X<NX>, Q6X<NX>>::type X;
+    if constexpr (FMT == FMT_Q4_K) q4x_load<NX>(X, xk, nx, sb, c);
+    else                           q6x_load<NX>(X, xk, nx, sb, c);
+
+    using WT = typename std::conditional<FMT == FMT_Q4_K, Q4W, Q6W>::type;
+    auto wload = [&](uint32_t row) -> WT {
+        const uint8_t * blk = w + (size_t)row * rb + (size_t)sb * BLK;
+        if constexpr (FMT == FMT_Q4_K) return q4_load(blk, c);
+        else                           return q6_load(blk, c);
+    };
+
+    const uint32_t nbatch = (rows + nr - 1) / nr;
+    const uint32_t nit = (nr + rpi - 1) / rpi;
+    for (uint32_t bt = batch0; bt < nbatch; bt += bstep) {
+        const uint32_t row0 = bt * nr;
+        const uint32_t nrow = min(nr, rows - row0);
+        auto row_of = [&](uint32_t it) { return it * rpi + rsub; };
+        auto clamp_row = [&](uint32_t rl) { return row0 + (rl < nrow ? rl : nrow - 1); };
+
+        WT cur = wload(clamp_row(row_of(0)));
+        for (uint32_t it = 0; it < nit; ++it) {
+            WT nxt = cur;
+            if (it + 1 < nit) nxt = wload(clamp_row(row_of(it + 1)));
+            const uint32_t rl = row_of(it);
+            const bool wr = act && c == 0 && rl < nrow;
+            if constexpr (FMT == FMT_Q4_K) {
+                const Q4W & W = cur;
+                const bool hi = c >= 2;
+                const uint32_t sh = (c & 1) * 16;
+                const uint32_t scp = hi ? ((W.h.w & 0x0F0F0F0Fu) | ((W.h.y >> 2) & 0x30303030u))
+                                        : (W.h.y & 0x3F3F3F3Fu);
+                const uint32_t mp  = hi ? (((W.h.w >> 4) & 0x0F0F0F0Fu) | ((W.h.z >> 2) & 0x30303030u))
+                                        : (W.h.z & 0x3F3F3F3Fu);
+                const int sc0 = (scp >> sh) & 0xFF, sc1 = (scp >> (sh + 8)) & 0xFF;
+                const int m0 = (mp >> sh) & 0xFF, m1 = (mp >> (sh + 8)) & 0xFF;
+                const uint32_t q[8] = {W.qa.x, W.qa.y, W.qa.z, W.qa.w,
+                                       W.qb.x, W.qb.y, W.qb.z, W.qb.w};
+                int lo[8], hv[8];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    lo[k] = (int)(q[k] & 0x0F0F0F0Fu);
+                    hv[k] = (int)((q[k] >> 4) & 0x0F0F0F0Fu);
+                }
+#pragma unroll
+                for (int p = 0; p < NX; ++p) {
+                    int dl = 0, dh = 0;
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) {
+                        dl = dot4(lo[k], X.q[p][k], dl);
+                        dh = dot4(hv[k], X.q[p][8 + k], dh);
+                    }
+                    int ia = sc0 * dl + sc1 * dh;
+                    int im = m0 * X.b0[p] + m1 * X.b1[p];
+                    ia += qx1(ia); ia += qx2(ia);
+                    im += qx1(im); im += qx2(im);
+                    if (wr && p < (int)nx) {
+                        TI[((rl * NX + p) << lgP) + sb] = ia;
+                        TM[((rl * NX + p) << lgP) + sb] = im;
+                    }
+                }
+                if (wr) TH[(rl << lgP) + sb] = W.h.x;
+            } else {
+                const Q6W & W = cur;
+                const uint32_t sh = W.sh;
+                const uint32_t A[5] = {W.a.x, W.a.y, W.a.z, W.a.w, W.a4};
+                const uint32_t B[5] = {W.b.x, W.b.y, W.b.z, W.b.w, W.b4};
+                const uint32_t H[5] = {W.h.x, W.h.y, W.h.z, W.h.w, W.h4};
+                const uint32_t S[5] = {W.s.x, W.s.y, W.s.z, W.s.w, W.s4};
+                uint32_t Sa[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) Sa[i] = alignb(S[i + 1], S[i], sh);
+                const uint32_t dbits = alignb(W.s4, W.s4, sh) & 0xFFFFu;
+                const uint32_t hh = c >> 1, bb = c & 1;
+                const uint32_t sd0 = hh ? Sa[2] : Sa[0], sd1 = hh ? Sa[3] : Sa[1];
+                const int sc[4] = {(int)(int8_t)(sd0 >> (8 * bb)), (int)(int8_t)(sd0 >> (8 * bb + 16)),
+                                   (int)(int8_t)(sd1 >> (8 * bb)), (int)(int8_t)(sd1 >> (8 * bb + 16))};
+                int g[4][4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t a = alignb(A[i + 1], A[i], sh);
+                    const uint32_t b = alignb(B[i + 1], B[i], sh);
+                    const uint32_t h = alignb(H[i + 1], H[i], sh);
+                    g[0][i] = (int)((a & 0x0F0F0F0Fu) | ((h & 0x03030303u) << 4));
+                    g[1][i] = (int)((b & 0x0F0F0F0Fu) | ((h << 2) & 0x30303030u));
+                    g[2][i] = (int)(((a >> 4) & 0x0F0F0F0Fu) | (h & 0x30303030u));
+                    g[3][i] = (int)(((b >> 4) & 0x0F0F0F0Fu) | ((h >> 2) & 0x30303030u));
+                }
+#pragma unroll
+                for (int p = 0; p < NX; ++p) {
+                    int ia = 0;
+#pragma unroll
+                    for (int gg = 0; gg < 4; ++gg) {
+                        int d = 0;
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) d = dot4(g[gg][i], X.q[p][gg][i], d);
+                        ia += sc[gg] * (d - X.b32[p][gg]);
+                    }
+                    ia += qx1(ia); ia += qx2(ia);
+                    if (wr && p < (int)nx) TI[((rl * NX + p) << lgP) + sb] = ia;
+                }
+                if (wr) TH[(rl << lgP) + sb] = dbits;
+            }
+            cur = nxt;
+        }
+        __syncthreads();
+        // ordered float fold: lane -> (row, column, accumulator k)
+        {
+            const uint32_t k = tid & 3, p = (tid >> 2) % NX, rl = tid / (4 * NX);
+            const bool ok = rl < nrow && p < nx && rl < nr;
+            float acc = 0.f;
+            if (ok) {
+                const int * ti = TI + ((rl * NX + p) << lgP);
+                const int * tm = TM + ((rl * NX + p) << lgP);
+                const uint32_t * th = TH + (rl << lgP);
+                const float * xd = XD + (p << lgP);
+                for (uint32_t s = k; s < nsb; s += 4) {
+                    const float dk = xd[s];
+                    if constexpr (FMT == FMT_Q4_K) {
+                        const float d = h2f(th[s] & 0xFFFFu), dmin = h2f(th[s] >> 16);
+                        acc = fmaf(d * dk, (float)ti[s], acc);
+                        acc = fmaf(-(dmin * dk), (float)tm[s], acc);
+                    } else {
+                        const float d = h2f(th[s]);
+                        acc = fmaf(d * dk, (float)ti[s], acc);
+                    }
+                }
+            }
+            const float s01 = acc + qx1f(acc);          // lane k=0: a0+a1, k=2: a2+a3
+            const float r = s01 + qx2f(s01);            // lane k=0: (a0+a1)+(a2+a3)
+            if (ok && k == 0) {
+                float * yp = yc[p] + row0 + rl;
+                *yp = *yp + r;
+            }
+        }
+        __syncthreads();
+    }
+}
+
+template <int FMT, int NX>
+__global__ __launch_bounds__(256) void k_dot_i8k(DotArgs a, uint32_t nr) {
+    extern __shared__ int smem[];
+    const uint8_t * w = a.w + (a.id_slot ? (size_t)(*a.id_slot) * a.estride : 0);
+    const uint8_t * xk[NX];
+    float * yc[NX];
+#pragma unroll
+    for (int p = 0; p < NX; ++p) {
+        const uint32_t pp = p < (int)a.nx ? p : 0;
+        xk[p] = (const uint8_t *)(a.x + (size_t)pp * a.xstride) + xqk_off(a.cols);
+        yc[p] = a.y + (size_t)pp * a.ystride;
+    }
+    kq_core<FMT, NX>(w, a.rows, a.cols, xk, yc, a.nx, nr, blockIdx.x, gridDim.x, smem);
+}
+
+// Grouped expert kernel: blockIdx.y = expert.  The workgroup scans the
+// routing table for its expert; with no routed (token, slot) pair it exits
+// before touching a weight byte.  Columns are processed NX at a time.
+template <int FMT, int NX>
+__global__ __launch_bounds__(256) void k_moe_i8k(MoeArgs a, uint32_t nr) {
+    extern __shared__ int smem[];
+    __shared__ uint32_t cols_s[256];
+    __shared__ uint32_t ncols_s;
+    const uint32_t e = blockIdx.y;
+    if (threadIdx.x == 0) {
+        uint32_t n = 0;
+        for (uint32_t i = 0; i < a.ntok * a.top_k && n < 256; ++i)
+            if (a.ids[i] == e) cols_s[n++] = i;          // i = tok*top_k + slot
+        ncols_s = n;
+    }
+    __syncthreads();
+    const uint32_t ncols = ncols_s;
+    if (ncols == 0) return;
+    const uint8_t * w = a.w + (size_t)e * a.estride;
+    for (uint32_t p0 = 0; p0 < ncols; p0 += NX) {
+        const uint32_t nx = min((uint32_t)NX, ncols - p0);
+        const uint8_t * xk[NX];
+        float * yc[NX];
+#pragma unroll
+        for (int p = 0; p < NX; ++p) {
+            const uint32_t ts = cols_s[p0 + (p < (int)nx ? p : 0)];
+            const uint32_t xi = a.x_per_slot ? ts : ts / a.top_k;
+            xk[p] = (const uint8_t *)(a.x + (size_t)xi * a.xstride) + xqk_off(a.cols);
+            yc[p] = a.y + (size_t)ts * a.ystride;
+        }
+        kq_core<FMT, NX>(w, a.rows, a.cols, xk, yc, nx, nr, blockIdx.x, gridDim.x, smem);
+        __syncthreads();
+    }
+}
+
+// ------------------------------------------------------------ Q8_0 x q8_1 --
+// One lane per 32-weight block; NK blocks per lane (row of up to 256*NK
+// blocks).  Terms: idot per (row, column, block) and the weight scale bits
+// per (row, block); chain acc[b & 3] = fmaf(dw * dx, idot, .).
+__host__ __device__ inline size_t q8_smem_bytes(uint32_t nr, uint32_t nx_t, uint32_t P) {
+    return 4 * ((size_t)nr * nx_t * P + (size_t)nr * P + (size_t)nx_t * P);
+}
+
+template <int NX, int NK>
+__global__ __launch_bounds__(256) void k_dot_i8_q8_0(DotArgs a, uint32_t nr) {
+    extern __shared__ int smem[];
+    const uint8_t * w = a.w + (a.id_slot ? (size_t)(*a.id_slot) * a.estride : 0);
+    const uint32_t nb = a.cols >> 5;
+    const uint32_t lgP = ceil_log2(nb), P = 1u << lgP;   // P <= 256*NK
+    const uint32_t rpi = NK == 1 ? (256u >> lgP) : 1u;
+    const uint64_t rb = (uint64_t)nb * 34;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t rsub = NK == 1 ? (tid >> lgP) : 0u;
+    uint32_t bl[NK];
+    bool act[NK];
+#pragma unroll
+    for (int k = 0; k < NK; ++k) {
+        const uint32_t b = NK == 1 ? (tid & (P - 1)) : tid + 256u * k;
+        act[k] = b < nb;
+        bl[k] = act[k] ? b : nb - 1;
+    }
+    int * TI = smem;
+    uint32_t * TH = (uint32_t *)(TI + (size_t)nr * NX * P);
+    float * XD = (float *)(TH + (size_t)nr * P);
+
+    const uint8_t * xq[NX];
+#pragma unroll
+    for (int p = 0; p < NX; ++p) {
+        const uint32_t pp = p < (int)a.nx ? p : 0;
+        xq[p] = (const uint8_t *)(a.x + (size_t)pp * a.xstride) + xq_off(a.cols);
+    }
+    for (uint32_t i = tid; i < NX * P; i += 256) {
+        const uint32_t p = i >> lgP, q = i & (P - 1);
+        XD[i] = (p < a.nx && q < nb) ? h2f(ldh(xq[p] + (size_t)q * 36)) : 0.f;
+    }
+    int X[NX][NK][8];
+#pragma unroll
+    for (int p = 0; p < NX; ++p)
+#pragma unroll
+        for (int k = 0; k < NK; ++k) {
+            const uint8_t * b = xq[p] + (size_t)bl[k] * 36 + 4;
+            const u32x4 v0 = ld4(b), v1 = ld4(b + 16);
+            X[p][k][0] = v0.x; X[p][k][1] = v0.y; X[p][k][2] = v0.z; X[p][k][3] = v0.w;
+            X[p][k][4] = v1.x; X[p][k][5] = v1.y; X[p][k][6] = v1.z; X[p][k][7] = v1.w;
+        }
+
+    struct W8 { u32x4 d0, d1; uint32_t d8, sh; };
+    auto wload = [&](uint32_t row, uint32_t b) -> W8 {
+        const uint8_t * blk = w + (size_t)row * rb + (size_t)b * 34;
+        const uintptr_t ba = (uintptr_t)blk;
+        const uint8_t * f = (const uint8_t *)(ba & ~(uintptr_t)3);
+        W8 r;
+        r.sh = (uint32_t)(ba & 3);
+        r.d0 = ld4_nt(f); r.d1 = ld4_nt(f + 16);
+        r.d8 = ldh(f + 32) | (ldh(blk + 32) << 16);
+        return r;
+    };
+
+    const uint32_t nbatch = (a.rows + nr - 1) / nr;
+    const uint32_t nit = (nr + rpi - 1) / rpi;
+    for (uint32_t bt = blockIdx.x; bt < nbatch; bt += gridDim.x) {
+        const uint32_t row0 = bt * nr, nrow = min(nr, a.rows - row0);
+        auto clamp_row = [&](uint32_t rl) { return row0 + (rl < nrow ? rl : nrow - 1); };
+        W8 cur[NK];
+#pragma unroll
+        for (int k = 0; k < NK; ++k) cur[k] = wload(clamp_row(rsub), bl[k]);
+        for (uint32_t it = 0; it < nit; ++it) {
+            W8 nxt[NK];
+#pragma unroll
+            for (int k = 0; k < NK; ++k) nxt[k] = cur[k];
+            if (it + 1 < nit) {
+#pragma unroll
+                for (int k = 0; k < NK; ++k) nxt[k] = wload(clamp_row((it + 1) * rpi + rsub), bl[k]);
+            }
+            const uint32_t rl = it * rpi + rsub;
+#pragma unroll
+            for (int k = 0; k < NK; ++k) {
+                const W8 & W = cur[k];
+                const uint32_t D[9] = {W.d0.x, W.d0.y, W.d0.z, W.d0.w,
+                                       W.d1.x, W.d1.y, W.d1.z, W.d1.w, W.d8};
+                const uint32_t dbits = W.sh ? (D[0] >> 16) : (D[0] & 0xFFFFu);
+                int qs[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    qs[j] = (int)(W.sh ? D[j + 1] : alignb(D[j + 1], D[j], 2));
+                const bool wr = act[k] && rl < nrow && rl < nr;
+#pragma unroll
+                for (int p = 0; p < NX; ++p) {
+                    int d = 0;
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) d = dot4(qs[j], X[p][k][j], d);
+                    if (wr && p < (int)a.nx) TI[((rl * NX + p) << lgP) + bl[k]] = d;
+                }
+                if (wr) TH[(rl << lgP) + bl[k]] = dbits;
+            }
+#pragma unroll
+            for (int k = 0; k < NK; ++k) cur[k] = nxt[k];
+        }
+        __syncthreads();
+        for (uint32_t base = 0; base < nr * NX * 4; base += 256) {
+            const uint32_t t = base + tid;
+            const uint32_t k = t & 3, p = (t >> 2) % NX, rl = t / (4 * NX);
+            const bool ok = rl < nrow && p < a.nx;
+            float acc = 0.f;
+            if (ok) {
+                const int * ti = TI + ((rl * NX + p) << lgP);
+                const uint32_t * th = TH + (rl << lgP);
+                const float * xd = XD + (p << lgP);
+                for (uint32_t b = k; b < nb; b += 4)
+                    acc = fmaf(h2f(th[b]) * xd[b], (float)ti[b], acc);
+            }
+            const float s01 = acc + qx1f(acc);
+            const float r = s01 + qx2f(s01);
+            if (ok && k == 0) {
+                float * yp = a.y + (size_t)p * a.ystride + row0 + rl;
+                *yp = *yp + r;
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// ----------------------------------------------------------------- launch --
+static uint32_t pick_nr(uint32_t rows, uint32_t rpi, uint32_t nr_max) {
+    const uint32_t target = (uint32_t)num_cus() * 8u;
+    uint32_t nr = (rows + target - 1) / target;
+    if (nr < 1) nr = 1;
+    if (nr > nr_max) nr = nr_max;
+    if (nr > rpi) nr = (nr / rpi) * rpi;
+    return nr;
+}
+
+template <int FMT, int NX>
+static int launch_kq(const DotArgs & a, hipStream_t s) {
+    const uint32_t nsb = a.cols >> 8;
+    const uint32_t P = 1u << ceil_log2(nsb), rpi = 64u / P;
+    const uint32_t nr = pick_nr(a.rows, rpi, 64u / NX);
+    const size_t sm = kq_smem_bytes<FMT>(nr, NX, P);
+    const uint32_t grid = (a.rows + nr - 1) / nr;
+    hipLaunchKernelGGL((k_dot_i8k<FMT, NX>), dim3(grid), dim3(256), sm, s, a, nr);
+    return hip_check(hipGetLastError(), "k_dot_i8k launch");
+}
+
+int launch_dot_i8k(int fmt, const DotArgs & a0, hipStream_t s) {
+    const uint32_t nsb = a0.cols >> 8;
+    if (nsb == 0 || nsb > 64 || (a0.cols & 255))
+        return set_error(FLH_ERR_UNSUPPORTED, "i8k dot: cols must be a multiple of 256, <= 16384");
+    if (a0.rows == 0 || a0.nx == 0) return FLH_OK;
+    for (uint32_t p0 = 0; p0 < a0.nx; p0 += 4) {
+        DotArgs a = a0;
+        a.nx = a0.nx - p0 < 4 ? a0.nx - p0 : 4;
+        a.x = a0.x + (size_t)p0 * a0.xstride;
+        a.y = a0.y + (size_t)p0 * a0.ystride;
+        int rc;
+        if (fmt == FMT_Q4_K) {
+            rc = a.nx == 1 ? launch_kq<FMT_Q4_K, 1>(a, s)
+               : a.nx == 2 ? launch_kq<FMT_Q4_K, 2>(a, s) : launch_kq<FMT_Q4_K, 4>(a, s);
+        } else if (fmt == FMT_Q6_K) {
+            rc = a.nx == 1 ? launch_kq<FMT_Q6_K, 1>(a, s)
+               : a.nx == 2 ? launch_kq<FMT_Q6_K, 2>(a, s) : launch_kq<FMT_Q6_K, 4>(a, s);
+        } else {
+            return set_error(FLH_ERR_UNSUPPORTED, "i8k dot: format has no q8_K path");
+        }
+        if (rc) return rc;
+    }
+    return FLH_OK;
+}
+
+template <int FMT, int NX>
+static int launch_moe_t(const MoeArgs & a, hipStream_t s) {
+    const uint32_t nsb = a.cols >> 8;
+    const uint32_t P = 1u << ceil_log2(nsb), rpi = 64u / P;
+    // experts split the chip: aim for ~8 workgroups per CU over all experts
+    const uint32_t per_e = (a.rows + 1) / 1;
+    uint32_t nr = (uint32_t)(((uint64_t)a.rows * a.n_expert + num_cus() * 8u - 1) / (num_cus() * 8u));
+    (void)per_e;
+    if (nr < 1) nr = 1;
+    if (nr > 64u / NX) nr = 64u / NX;
+    if (nr > rpi) nr = (nr / rpi) * rpi;
+    const size_t sm = kq_smem_bytes<FMT>(nr, NX, P);
+    const uint32_t grid = (a.rows + nr - 1) / nr;
+    hipLaunchKernelGGL((k_moe_i8k<FMT, NX>), dim3(grid, a.n_expert), dim3(256), sm, s, a, nr);
+    return hip_check(hipGetLastError(), "k_moe_i8k launch");
+}
+
+int launch_moe_i8k(int fmt, const MoeArgs & a, hipStream_t s) {
+    const uint32_t nsb = a.cols >> 8;
+    if (nsb == 0 || nsb > 64 || (a.cols & 255))
+        return set_error(FLH_ERR_UNSUPPORTED, "moe i8k: cols must be a multiple of 256, <= 16384");
+    if (a.rows == 0 || a.ntok == 0 || a.top_k == 0) return FLH_OK;
+    if (a.ntok * a.top_k > 256) return set_error(FLH_ERR_UNSUPPORTED, "moe: ntok*top_k > 256");
+    if (fmt == FMT_Q4_K) return launch_moe_t<FMT_Q4_K, 4>(a, s);
+    if (fmt == FMT_Q6_K) return launch_moe_t<FMT_Q6_K, 4>(a, s);
+    return set_error(FLH_ERR_UNSUPPORTED, "moe i8k: format has no q8_K path");
+}
+
+template <int NX, int NK>
+static int launch_q8(const DotArgs & a, hipStream_t s) {
+    const uint32_t nb = a.cols >> 5;
+    const uint32_t P = 1u << ceil_log2(nb);
+    const uint32_t rpi = NK == 1 ? 256u / P : 1u;
+    // LDS budget 48 KiB for the terms
+    uint32_t nr_max = 64u / NX;
+    while (nr_max > 1 && q8_smem_bytes(nr_max, NX, P) > 48u * 1024u) nr_max >>= 1;
+    const uint32_t nr = pick_nr(a.rows, rpi, nr_max);
+    const size_t sm = q8_smem_bytes(nr, NX, P);
+    const uint32_t grid = (a.rows + nr - 1) / nr;
+    hipLaunchKernelGGL((k_dot_i8_q8_0<NX, NK>), dim3(grid), dim3(256), sm, s, a, nr);
+    return hip_check(hipGetLastError(), "k_dot_i8_q8_0 launch");
+}
+
+int launch_dot_i8_q8_0(const DotArgs & a0, hipStream_t s) {
+    const uint32_t nb = a0.cols >> 5;
+    if (nb == 0 || nb > 512 || (a0.cols & 31))
+        return set_error(FLH_ERR_UNSUPPORTED, "q8_0 dot: cols must be a multiple of 32, <= 16384");
+    if (a0.rows == 0 || a0.nx == 0) return FLH_OK;
+    for (uint32_t p0 = 0; p0 < a0.nx; p0 += 4) {
+        DotArgs a = a0;
+        a.nx = a0.nx - p0 < 4 ? a0.nx - p0 : 4;
+        a.x = a0.x + (size_t)p0 * a0.xstride;
+        a.y = a0.y + (size_t)p0 * a0.ystride;
+        int rc;
+        if (nb <= 256) rc = a.nx == 1 ? launch_q8<1, 1>(a, s) : a.nx == 2 ? launch_q8<2, 1>(a, s) : launch_q8<4, 1>(a, s);
+        else           rc = a.nx == 1 ? launch_q8<1, 2>(a, s) : a.nx == 2 ? launch_q8<2, 2>(a, s) : launch_q8<4, 2>(a, s);
+        if (rc) return rc;
+    }
+    return FLH_OK;
+}
+
+}  // namespace flh

@@ -1,0 +1,298 @@
+// flh_f32.hip -- fp32-activation STREAM_DOT modes and the small decode ops.
+//
+//  * canonical (fast = 0): one thread per (row, column) runs the reference's
+//    single-accumulator ascending-element chain (fl_dot_row_any,
+//    src/runtime/quants.h:132-230,625-642), so it is bitwise equal to
+//    run_serial.  Inherently serial per row; it is the reference's
+//    correctness mode, not a throughput path.
+//  * fast fp32 (fast = 1, format not routed to an int8 path): the
+//    reference's fixed 16-lane order (src/runtime/kernels.h:11-19):
+//    dot_row_fast / dot_row_fast_q8_0 / dot_row_fast_dequant, again one
+//    thread per (row, column), bitwise.
+//  * ROUTER_SEL / SILU_MUL / WMERGE / MERGE: the reference's single-thread
+//    canonical ops (src/runtime/decode_params.h:234-295,
+//    runtime_internal.h:274-281), one thread per token / element.  expf is
+//    the device libm (the reference runs glibc's), so these match to within
+//    float rounding of expf, not bitwise.
+#include "flh_common.h"
+#include "flh_internal.h"
+#include "flh_status.h"
+
+namespace flh {
+
+__device__ __forceinline__ uint32_t ld16u(const uint8_t * p) { return p[0] | (p[1] << 8); }
+
+__device__ void dq_block(int fmt, const uint8_t * b, float * o) {
+    // value formulas of dequant_chunk (src/runtime/kernels.h:182-240)
+    if (fmt == FMT_Q8_0) {
+        const float d = h2f(ld16u(b));
+        for (int j = 0; j < 32; ++j) o[j] = d * (float)(int8_t)b[2 + j];
+    } else if (fmt == FMT_Q4_K) {
+        const float d = h2f(ld16u(b)), dmin = h2f(ld16u(b + 2));
+        const uint8_t * s = b + 4;
+        for (int c = 0; c < 4; ++c) {
+            uint32_t sc[2], mn[2];
+            for (int t = 0; t < 2; ++t) {
+                const int g = 2 * c + t;
+                if (g < 4) { sc[t] = s[g] & 63; mn[t] = s[g + 4] & 63; }
+                else { sc[t] = (s[g + 4] & 0xF) | ((s[g - 4] >> 6) << 4);
+                       mn[t] = (s[g + 4] >> 4) | ((s[g] >> 6) << 4); }
+            }
+            const float d1 = d * (float)sc[0], m1 = dmin * (float)mn[0];
+            const float d2 = d * (float)sc[1], m2 = dmin * (float)mn[1];
+            const uint8_t * q = b + 16 + 32 * c;
+            for (int l = 0; l < 32; ++l) o[64 * c + l] = d1 * (float)(q[l] & 0xF) - m1;
+            for (int l = 0; l < 32; ++l) o[64 * c + 32 + l] = d2 * (float)(q[l] >> 4) - m2;
+        }
+    } else {
+        const float d = h2f(ld16u(b + 208));
+        const int8_t * sc = (const int8_t *)(b + 192);
+        for (int h = 0; h < 2; ++h)
+            for (int g = 0; g < 4; ++g)
+                for (int l = 0; l < 32; ++l) {
+                    const uint8_t lb = b[64 * h + l + 32 * (g & 1)];
+                    const int q6 = ((g < 2) ? (lb & 0xF) : (lb >> 4)) |
+                                   (((b[128 + 32 * h + l] >> (2 * g)) & 3) << 4);
+                    o[128 * h + 32 * g + l] = d * (float)sc[8 * h + 2 * g + l / 16] * (float)(q6 - 32);
+                }
+    }
+}
+
+__device__ float canon_dot(int fmt, const uint8_t * row, const float * x, uint32_t cols) {
+    float acc = 0.f;
+    if (fmt == FMT_F32) {
+        const float * r = (const float *)row;
+        for (uint32_t c = 0; c < cols; ++c) acc += r[c] * x[c];
+    } else if (fmt == FMT_Q8_0) {
+        for (uint32_t b = 0; b < cols / 32; ++b) {
+            const uint8_t * B = row + (size_t)b * 34;
+            const float d = h2f(ld16u(B));
+            for (int i = 0; i < 32; ++i) acc += d * (float)(int8_t)B[2 + i] * x[b * 32 + i];
+        }
+    } else if (fmt == FMT_Q4_K) {
+        for (uint32_t sb = 0; sb < cols / 256; ++sb) {
+            const uint8_t * B = row + (size_t)sb * 144;
+            const float d = h2f(ld16u(B)), dmin = h2f(ld16u(B + 2));
+            const uint8_t * s = B + 4;
+            for (int c = 0; c < 4; ++c) {
+                uint32_t sc[2], mn[2];
+                for (int t = 0; t < 2; ++t) {
+                    const int g = 2 * c + t;
+                    if (g < 4) { sc[t] = s[g] & 63; mn[t] = s[g + 4] & 63; }
+                    else { sc[t] = (s[g + 4] & 0xF) | ((s[g - 4] >> 6) << 4);
+                           mn[t] = (s[g + 4] >> 4) | ((s[g] >> 6) << 4); }
+                }
+                const float d1 = d * (float)sc[0], m1 = dmin * (float)mn[0];
+                const float d2 = d * (float)sc[1], m2 = dmin * (float)mn[1];
+                const uint8_t * q = B + 16 + 32 * c;
+                const float * xb = x + sb * 256 + 64 * c;
+                for (int l = 0; l < 32; ++l) acc += (d1 * (float)(q[l] & 0xF) - m1) * xb[l];
+                for (int l = 0; l < 32; ++l) acc += (d2 * (float)(q[l] >> 4) - m2) * xb[32 + l];
+            }
+        }
+    } else {
+        for (uint32_t sb = 0; sb < cols / 256; ++sb) {
+            const uint8_t * B = row + (size_t)sb * 210;
+            const float d = h2f(ld16u(B + 208));
+            const int8_t * sc = (const int8_t *)(B + 192);
+            for (int h = 0; h < 2; ++h)
+                for (int g = 0; g < 4; ++g)
+                    for (int l = 0; l < 32; ++l) {
+                        const uint8_t lb = B[64 * h + l + 32 * (g & 1)];
+                        const int q6 = ((g < 2) ? (lb & 0xF) : (lb >> 4)) |
+                                       (((B[128 + 32 * h + l] >> (2 * g)) & 3) << 4);
+                        acc += d * (float)sc[8 * h + 2 * g + l / 16] * (float)(q6 - 32)
+                             * x[sb * 256 + 128 * h + 32 * g + l];
+                    }
+        }
+    }
+    return acc;
+}
+
+__device__ float tree16(const float * L) {
+    float s[4];
+    for (int j = 0; j < 4; ++j) s[j] = (L[j] + L[4 + j]) + (L[8 + j] + L[12 + j]);
+    return (s[0] + s[1]) + (s[2] + s[3]);
+}
+
+__device__ float fast_dot(int fmt, const uint8_t * row, const float * x, uint32_t cols) {
+    if (fmt == FMT_F32) {
+        const float * r = (const float *)row;
+        const uint32_t n16 = cols & ~15u;
+        float L[16] = {0};
+        for (uint32_t k = 0; k < n16; k += 16)
+            for (int j = 0; j < 16; ++j) L[j] += r[k + j] * x[k + j];
+        const float head = tree16(L);
+        float tail = 0.f;
+        for (uint32_t k = n16; k < cols; ++k) tail += r[k] * x[k];
+        return head + tail;
+    }
+    if (fmt == FMT_Q8_0) {
+        float L[16] = {0};
+        for (uint32_t b = 0; b < cols / 32; ++b) {
+            const uint8_t * B = row + (size_t)b * 34;
+            const float d = h2f(ld16u(B));
+            for (int g = 0; g < 8; ++g)
+                for (int j = 0; j < 4; ++j)
+                    L[(g & 3) * 4 + j] += d * (float)(int8_t)B[2 + 4 * g + j] * x[b * 32 + 4 * g + j];
+        }
+        return tree16(L);
+    }
+    const uint32_t bb = fmt == FMT_Q4_K ? 144 : 210;
+    float acc = 0.f, buf[256];
+    for (uint32_t e = 0; e < cols; e += 256) {
+        dq_block(fmt, row + (size_t)(e / 256) * bb, buf);
+        float L[16] = {0};
+        for (uint32_t k = 0; k < 256; k += 16)
+            for (int j = 0; j < 16; ++j) L[j] += buf[k + j] * x[e + k + j];
+        acc += tree16(L);
+    }
+    return acc;
+}
+
+template <bool FAST>
+__global__ void k_dot_f32(int fmt, DotArgs a) {
+    const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= (uint64_t)a.rows * a.nx) return;
+    const uint32_t r = (uint32_t)(t % a.rows), p = (uint32_t)(t / a.rows);
+    const uint8_t * w = a.w + (a.id_slot ? (size_t)(*a.id_slot) * a.estride : 0);
+    const uint64_t rb = fmt == FMT_F32 ? (uint64_t)a.cols * 4
+                      : fmt == FMT_Q8_0 ? (uint64_t)(a.cols / 32) * 34
+                      : (uint64_t)(a.cols / 256) * (fmt == FMT_Q4_K ? 144 : 210);
+    const float * x = a.x + (size_t)p * a.xstride;
+    const float v = FAST ? fast_dot(fmt, w + r * rb, x, a.cols) : canon_dot(fmt, w + r * rb, x, a.cols);
+    float * y = a.y + (size_t)p * a.ystride + r;
+    *y = *y + v;
+}
+
+static int launch_f32(bool fast, int fmt, const DotArgs & a, hipStream_t s) {
+    if (fmt != FMT_F32 && fmt != FMT_Q8_0 && fmt != FMT_Q4_K && fmt != FMT_Q6_K)
+        return set_error(FLH_ERR_UNSUPPORTED, "fp32 dot: format not supported");
+    const uint64_t n = (uint64_t)a.rows * a.nx;
+    if (n == 0) return FLH_OK;
+    const dim3 g((uint32_t)((n + 63) / 64));
+    if (fast) hipLaunchKernelGGL(k_dot_f32<true>, g, dim3(64), 0, s, fmt, a);
+    else      hipLaunchKernelGGL(k_dot_f32<false>, g, dim3(64), 0, s, fmt, a);
+    return hip_check(hipGetLastError(), "k_dot_f32 launch");
+}
+int launch_dot_canonical(int fmt, const DotArgs & a, hipStream_t s) { return launch_f32(false, fmt, a, s); }
+int launch_dot_fast_f32(int fmt, const DotArgs & a, hipStream_t s) { return launch_f32(true, fmt, a, s); }
+
+// ------------------------------------------------------------ decode ops --
+__global__ void k_router_sel(const float * logits, uint32_t ntok, uint32_t n_expert,
+                             uint32_t top_k, uint32_t norm, float scale,
+                             uint32_t * ids, float * gates) {
+    const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= ntok) return;
+    const float * lg = logits + (size_t)t * n_expert;
+    uint32_t * id = ids + (size_t)t * top_k;
+    float * gt = gates + (size_t)t * top_k;
+    float w[256];
+    float mx = -1e30f, sum = 0.f, tsum = 0.f;
+    for (uint32_t i = 0; i < n_expert; ++i) if (lg[i] > mx) mx = lg[i];
+    for (uint32_t i = 0; i < n_expert; ++i) { w[i] = expf(lg[i] - mx); sum += w[i]; }
+    for (uint32_t i = 0; i < n_expert; ++i) w[i] /= sum;
+    for (uint32_t k = 0; k < top_k; ++k) {
+        uint32_t best = 0;
+        float bw = -1.f;
+        for (uint32_t i = 0; i < n_expert; ++i) {
+            bool taken = false;
+            for (uint32_t k2 = 0; k2 < k; ++k2) if (id[k2] == i) { taken = true; break; }
+            if (!taken && w[i] > bw) { bw = w[i]; best = i; }
+        }
+        id[k] = best; gt[k] = bw; tsum += bw;
+    }
+    for (uint32_t k = 0; k < top_k; ++k) {
+        if (norm) gt[k] /= tsum;
+        gt[k] *= scale;
+    }
+}
+
+__global__ void k_silu_mul(const float * gate, const float * up, float * h, uint32_t n,
+                           uint32_t gstride, uint32_t hstride) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x, c = blockIdx.y;
+    if (i >= n) return;
+    const float g = gate[(size_t)c * gstride + i];
+    h[(size_t)c * hstride + i] = (g / (1.0f + expf(-g))) * up[(size_t)c * gstride + i];
+}
+
+__global__ void k_wmerge(const float * parts, const float * gates, const float * add1,
+                         const float * add2, float * y, float scale, uint32_t n_parts,
+                         uint32_t n, uint32_t n_full, uint32_t pstride, uint32_t ystride) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x, c = blockIdx.y;
+    if (i >= n) return;
+    const float * pc = parts + (size_t)c * pstride;
+    const float * gc = gates ? gates + (size_t)c * (n_full > n_parts ? n_full : n_parts) : nullptr;
+    float gsc = 1.0f;
+    if (gc && n_full > n_parts) {
+        float s = 0.f, sf = 0.f;
+        for (uint32_t q = 0; q < n_parts; ++q) s += gc[q];
+        for (uint32_t q = 0; q < n_full; ++q) sf += gc[q];
+        if (s > 0.f) gsc = sf / s;
+    }
+    float acc = 0.f;
+    for (uint32_t q = 0; q < n_parts; ++q)
+        acc += (gc ? gsc * gc[q] : 1.0f) * pc[(size_t)q * n + i];
+    acc *= scale;
+    if (add1) acc += add1[(size_t)c * ystride + i];
+    if (add2) acc += add2[(size_t)c * ystride + i];
+    y[(size_t)c * ystride + i] = acc;
+}
+
+__global__ void k_merge(const float * x, float * y, uint32_t rows, uint32_t nparts) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= rows) return;
+    float acc = 0.f;
+    for (uint32_t p = 0; p < nparts; ++p) acc += x[(size_t)p * rows + i];
+    y[i] = acc;
+}
+
+int launch_router_sel(const float * logits, uint32_t ntok, uint32_t n_expert, uint32_t top_k,
+                      uint32_t norm, float scale, uint32_t * ids, float * gates, hipStream_t s) {
+    if (n_expert == 0 || n_expert > 256 || top_k == 0 || top_k > n_expert)
+        return set_error(FLH_ERR_ARG, "router_sel: need 0 < top_k <= n_expert <= 256");
+    if (ntok == 0) return FLH_OK;
+    hipLaunchKernelGGL(k_router_sel, dim3((ntok + 63) / 64), dim3(64), 0, s, logits, ntok,
+                       n_expert, top_k, norm, scale, ids, gates);
+    return hip_check(hipGetLastError(), "k_router_sel launch");
+}
+int launch_silu_mul(const float * gate, const float * up, float * h, uint32_t n, uint32_t ncol,
+                    uint32_t gstride, uint32_t hstride, hipStream_t s) {
+    if (n == 0 || ncol == 0) return FLH_OK;
+    hipLaunchKernelGGL(k_silu_mul, dim3((n + 255) / 256, ncol), dim3(256), 0, s, gate, up, h, n,
+                       gstride, hstride);
+    return hip_check(hipGetLastError(), "k_silu_mul launch");
+}
+int launch_wmerge(const float * parts, const float * gates, const float * add1, const float * add2,
+                  float * y, float scale, uint32_t n_parts, uint32_t n, uint32_t n_full,
+                  uint32_t ncol, uint32_t pstride, uint32_t ystride, hipStream_t s) {
+    if (n == 0 || ncol == 0) return FLH_OK;
+    hipLaunchKernelGGL(k_wmerge, dim3((n + 255) / 256, ncol), dim3(256), 0, s, parts, gates, add1,
+                       add2, y, scale, n_parts, n, n_full, pstride, ystride);
+    return hip_check(hipGetLastError(), "k_wmerge launch");
+}
+int launch_merge(const float * x, float * y, uint32_t rows, uint32_t nparts, hipStream_t s) {
+    if (rows == 0) return FLH_OK;
+    hipLaunchKernelGGL(k_merge, dim3((rows + 255) / 256), dim3(256), 0, s, x, y, rows, nparts);
+    return hip_check(hipGetLastError(), "k_merge launch");
+}
+
+__global__ void k_zero(uint32_t * p, size_t nw, uint8_t * tail, uint32_t ntail) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < nw) p[i] = 0u;
+    if (i < ntail) tail[i] = 0;
+}
+// zero n bytes with a kernel (no hipMemsetAsync: this may run inside a
+// captured HIP graph).  p must be 4-byte aligned.
+int launch_zero(void * p, size_t n, hipStream_t s) {
+    if (n == 0) return FLH_OK;
+    if ((uintptr_t)p & 3) return set_error(FLH_ERR_ARG, "zero: pointer must be 4-byte aligned");
+    const size_t nw = n / 4;
+    const uint32_t nt = (uint32_t)(n & 3);
+    const size_t m = nw > nt ? nw : nt;
+    hipLaunchKernelGGL(k_zero, dim3((uint32_t)((m + 255) / 256)), dim3(256), 0, s, (uint32_t *)p, nw,
+                       (uint8_t *)p + nw * 4, nt);
+    return hip_check(hipGetLastError(), "k_zero launch");
+}
+
+}  // namespace flh

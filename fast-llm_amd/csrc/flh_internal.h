@@ -1,0 +1,67 @@
+// flh_internal.h -- launcher interface between the C-ABI layer (flh_api.cpp)
+// and the kernel translation units.  Not installed; include/fastllm_hip.h is
+// the public boundary.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+namespace flh {
+
+// One STREAM_DOT launch: y[p*ystride + r] += dot(W[r], x + p*xstride),
+// r < rows, p < nx.  W = w (+ *id_slot * estride when id_slot != nullptr,
+// resolved on the device: the id is written by an earlier kernel).
+struct DotArgs {
+    const uint8_t * w;
+    const uint32_t * id_slot;
+    uint64_t estride;
+    const float * x;
+    float * y;
+    uint32_t rows, cols, nx, xstride, ystride;
+};
+
+// Grouped expert launch (MoE): for every expert e with at least one routed
+// (token, slot) pair, the columns are those pairs:
+//   y[(tok*top_k + slot)*ystride + r] += dot(W_e[r], x + xcol(tok,slot)*xstride)
+// where xcol = tok when x_per_slot == 0 (shared hidden state per token) and
+// tok*top_k + slot otherwise (per-slot activations, e.g. the down input).
+struct MoeArgs {
+    const uint8_t * w;        // expert 0 base
+    uint64_t estride;         // bytes between experts
+    const uint32_t * ids;     // [ntok * top_k] expert ids
+    const float * x;
+    float * y;
+    uint32_t rows, cols, ntok, top_k, n_expert, xstride, ystride, x_per_slot;
+};
+
+int num_cus();
+
+// Each returns hipSuccess-style 0 or a negative flh error code.
+int launch_act_q8(float * x, void * y_q81, uint32_t cols, uint32_t nx,
+                  uint32_t xstride, hipStream_t s);
+int launch_dot_i8k(int fmt, const DotArgs & a, hipStream_t s);    // Q4_K, Q6_K x q8_K
+int launch_dot_i8_q8_0(const DotArgs & a, hipStream_t s);         // Q8_0 x q8_1
+int launch_dot_i8_k(int fmt, const DotArgs & a, hipStream_t s);   // Q4_K, Q6_K x q8_1
+int launch_dot_canonical(int fmt, const DotArgs & a, hipStream_t s);
+int launch_dot_fast_f32(int fmt, const DotArgs & a, hipStream_t s);
+int launch_dequant(int fmt, const uint8_t * w, uint32_t rows, uint32_t cols,
+                   float * out, hipStream_t s);
+int launch_moe_i8k(int fmt, const MoeArgs & a, hipStream_t s);
+int launch_router_sel(const float * logits, uint32_t ntok, uint32_t n_expert,
+                      uint32_t top_k, uint32_t norm, float scale,
+                      uint32_t * ids, float * gates, hipStream_t s);
+int launch_silu_mul(const float * gate, const float * up, float * h, uint32_t n,
+                    uint32_t ncol, uint32_t gstride, uint32_t hstride, hipStream_t s);
+int launch_wmerge(const float * parts, const float * gates, const float * add1,
+                  const float * add2, float * y, float scale, uint32_t n_parts,
+                  uint32_t n, uint32_t n_full, uint32_t ncol, uint32_t pstride,
+                  uint32_t ystride, hipStream_t s);
+int launch_merge(const float * x, float * y, uint32_t rows, uint32_t nparts,
+                 hipStream_t s);
+int launch_quantize_weights(int fmt, const float * src, uint32_t rows,
+                            uint32_t cols, uint8_t * dst, hipStream_t s);
+int launch_fill_normal(float * dst, size_t n, uint64_t seed, float mean,
+                       float stddev, float outlier_frac, float outlier_scale,
+                       hipStream_t s);
+
+}  // namespace flh

@@ -1,0 +1,254 @@
+/*
+ * fastllm_hip.h -- C-ABI of the MI355X (gfx950) quantized-matvec backend.
+ *
+ * Drop-in for the reference runtime's CUDA execution path of the quantized
+ * decode hot path (qdox-labs/fast-llm): the ACT_Q8 / STREAM_DOT /
+ * STREAM_DOT_IDX task kinds and the GGUF Q8_0 / Q4_K / Q6_K row-dots behind
+ * them.  Plain C types only: device pointers are void* / float*, streams and
+ * events are opaque void* (hipStream_t / hipEvent_t), sizes are integers.
+ *
+ * Every entry point returns FLH_OK (0) or a negative FLH_ERR_* code and
+ * records a message readable with flh_last_error() (per calling thread).
+ * The reference aborts on every error (src/runtime/gpu_exec.cu:15-17,
+ * src/runtime/graph.cpp:100-103); a host wrapper that wants that behaviour
+ * aborts on a non-zero return.
+ *
+ * Numerics contract: with fast=1 and the reference default masks, every
+ * STREAM_DOT output is BITWISE equal to the reference CPU int8 path
+ * (src/runtime/kernels.h:1002-1258 on x86: fl_dot_i8_q8_0, fl_dot_i8k_q4_K,
+ * fl_dot_i8k_q6_K), ACT_Q8 bytes equal fl_exec_act_q8, and flh_dequant
+ * equals dequant_chunk (src/runtime/kernels.h:162-242).
+ */
+#ifndef FASTLLM_HIP_H
+#define FASTLLM_HIP_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------- codes -- */
+enum {
+    FLH_OK = 0,
+    FLH_ERR_ARG = -1,          /* invalid argument (freeze()-style validation) */
+    FLH_ERR_HIP = -2,          /* HIP runtime error */
+    FLH_ERR_UNSUPPORTED = -3,  /* task kind / format / shape not implemented */
+    FLH_ERR_NOMEM = -4,        /* arena exhausted or hipMalloc failed */
+    FLH_ERR_STATE = -5         /* flh_init not called / no device */
+};
+
+/* TaskKind values (include/fastllm/fastllm.h:19-45), stable. */
+enum {
+    FLH_TASK_STREAM_DOT = 0, FLH_TASK_MERGE = 1, FLH_TASK_SIGNAL = 2,
+    FLH_TASK_ACT_Q8 = 3, FLH_TASK_STREAM_DOT_IDX = 4, FLH_TASK_RMSNORM = 5,
+    FLH_TASK_ADD2 = 6, FLH_TASK_ROPE_DS2 = 7, FLH_TASK_KV_APPEND = 8,
+    FLH_TASK_ATTN_HEAD = 9, FLH_TASK_ROUTER_SEL = 10, FLH_TASK_SILU_MUL = 11,
+    FLH_TASK_WMERGE = 12
+};
+
+/* Fmt values (include/fastllm/fastllm.h:56-57), stable. */
+enum {
+    FLH_FMT_F32 = 0, FLH_FMT_Q8_0 = 1, FLH_FMT_Q5_0 = 2, FLH_FMT_Q4_K = 3,
+    FLH_FMT_Q6_K = 4, FLH_FMT_IQ2_XXS = 5, FLH_FMT_IQ3_XXS = 6
+};
+
+/* Max activation columns per multi-column tile (fastllm.h:61 kMaxDotCols). */
+#define FLH_MAX_DOT_COLS 16u
+
+/*
+ * Task record, byte-for-byte the layout of fastllm::Task
+ * (include/fastllm/fastllm.h:65-97; enum class members are uint8_t), so a
+ * frozen graph's task table can be passed as-is.  Pointers w / x / y / aux
+ * are DEVICE pointers here (the reference uses unified memory), except that
+ * for ROUTER_SEL / SILU_MUL / WMERGE aux points to a HOST-readable param
+ * block (flh_router_p etc.) whose own pointers are device pointers.
+ */
+typedef struct __attribute__((aligned(128))) flh_task {
+    uint32_t id;
+    uint8_t kind;              /* FLH_TASK_* */
+    uint8_t affinity;
+    uint8_t fmt;               /* FLH_FMT_* */
+    uint16_t n_consumers;
+    uint32_t consumers[6];
+    const void * w;
+    uint64_t w_bytes;
+    const void * x;
+    void * y;
+    uint32_t rows, cols;
+    int32_t dep_init;
+    int32_t dep_count;
+    uint32_t epoch;
+    uint64_t handoff_ts;
+    const void * aux;          /* STREAM_DOT_IDX: device u32 expert-id slot */
+    uint64_t aux2;             /* STREAM_DOT_IDX: expert stride in bytes */
+    uint32_t nx, xstride, ystride;
+} flh_task;
+
+/* Decode-op param blocks, layouts of RouterP / SiluMulP / WmergeP
+ * (src/runtime/decode_params.h:68-97). */
+typedef struct flh_router_p {
+    const float * logits; uint32_t * ids; float * gates;
+    uint32_t n_expert, top_k, norm; float scale;
+} flh_router_p;
+typedef struct flh_silu_mul_p {
+    const float * gate; const float * up; float * h; uint32_t n;
+} flh_silu_mul_p;
+typedef struct flh_wmerge_p {
+    const float * parts; const float * gates; const float * add1;
+    const float * add2; float * y; float scale; uint32_t n_parts, n, n_full;
+} flh_wmerge_p;
+
+/* ------------------------------------------------------------- runtime -- */
+/* Last error message of the calling thread ("" if none). */
+const char * flh_last_error(void);
+
+/* Select and initialise a device; must precede every call below that touches
+ * the GPU.  Replaces the device setup inside gpu_start()
+ * (src/runtime/gpu_exec.cu:457-496; prototype runtime_internal.h:292). */
+int flh_init(int device);
+
+/* Device facts: compute units, HBM bytes, wave size, name. */
+int flh_device_info(int * num_cus, size_t * hbm_bytes, int * wave_size,
+                    char * name, size_t name_len);
+
+/* Reference default dispatch masks for the CPU int8 path this backend
+ * matches (src/runtime/kernels.h:920,937). */
+void flh_default_masks(uint32_t * i8_mask, uint32_t * i8k_mask);
+
+/* Row bytes of a weight row and the activation buffer size with both q8
+ * appendices (src/runtime/quants.h:97-99, 326-330). */
+uint64_t flh_row_bytes(int fmt, uint32_t cols);
+size_t flh_x_alloc_bytes(uint32_t cols);
+
+/* ------------------------------------------------------------- memory -- */
+/* Device bump arena over one hipMalloc: replaces Arena::create's
+ * cudaMallocManaged arena (src/runtime/arena.cpp:54-74).  Allocations are
+ * never freed individually; destroy releases everything. */
+typedef struct flh_arena flh_arena;
+int flh_arena_create(size_t bytes, flh_arena ** out);
+int flh_arena_alloc(flh_arena * a, size_t bytes, size_t align, void ** out);
+size_t flh_arena_used(const flh_arena * a);
+int flh_arena_destroy(flh_arena * a);
+
+/* Plain device buffers (outside any arena). */
+int flh_malloc(size_t bytes, void ** out);
+int flh_free(void * p);
+int flh_upload(void * dst_dev, const void * src_host, size_t n, void * stream);
+int flh_download(void * dst_host, const void * src_dev, size_t n, void * stream);
+/* zero n bytes with a fill kernel (safe inside HIP graph capture) */
+int flh_zero(void * dst_dev, size_t n, void * stream);
+
+/* ------------------------------------------------------------ streams -- */
+/* Replaces gpu_make_stream / gpu_stop_sync (src/runtime/gpu_exec.cu:387,498).
+ * Streams are created at default priority. */
+int flh_stream_create(void ** out);
+int flh_stream_sync(void * stream);
+int flh_stream_destroy(void * stream);
+int flh_event_create(void ** out);
+int flh_event_record(void * event, void * stream);
+int flh_event_elapsed_ms(void * start, void * stop, float * ms);
+int flh_event_destroy(void * event);
+
+/* HIP graph capture of work issued on one stream (replaces the reference's
+ * persistent-kernel launch amortisation, src/runtime/gpu_exec.cu:156-344,
+ * for a frozen graph: capture once, replay per token).  Every kernel of
+ * this library is capture-safe (no hipMemsetAsync, no host syncs). */
+int flh_graph_capture_begin(void * stream);
+int flh_graph_capture_end(void * stream, void ** graph_exec);
+int flh_graph_launch(void * graph_exec, void * stream);
+int flh_graph_destroy(void * graph_exec);
+
+/* ---------------------------------------------------------------- ops -- */
+/* ACT_Q8 (TaskKind 3; fl_exec_act_q8, src/runtime/quants.h:404-416; GPU
+ * gact_q8, src/runtime/kernels_gpu.h:881-891): for each of nx columns
+ * x_p = x + p*xstride (16-B aligned, fl_x_alloc_bytes(cols) bytes each),
+ * write the q8_1 appendix at y_q81 + p*xstride floats (NULL = the canonical
+ * fl_xq_of(x_p, cols)) and the q8_K appendix at fl_xqk_of(x_p, cols). */
+int flh_act_q8(float * x, void * y_q81, uint32_t cols, uint32_t nx,
+               uint32_t xstride, void * stream);
+
+/* STREAM_DOT / STREAM_DOT_IDX tile (TaskKind 0/4; exec_task_block,
+ * src/runtime/gpu_exec.cu:64-140, exec_task_cpu, src/runtime/kernels.h:
+ * 1002-1258):  y[p*ystride + r] += dot(W[r], x + p*xstride), r < rows,
+ * p < nx (0 means 1), W = w + (id_slot ? *id_slot * estride : 0) with the
+ * id read ON THE DEVICE.  Validation as Graph::freeze
+ * (src/runtime/graph.cpp:84-90): cols % block == 0, w_bytes == rows *
+ * row_bytes, id_slot => estride != 0.
+ * fast = 0: canonical fp32 dequant-dot (fl_dot_row_any order, bitwise);
+ * fast = 1: q8_K path for K formats whose bit is in i8k_mask, else q8_1
+ * path for formats in i8_mask, else the "fast" fp32 dequant order
+ * (dot_row_fast_dequant / dot_row_fast_q8_0), exactly as exec_task_cpu.
+ * int8 paths read the appendices written by flh_act_q8. */
+int flh_stream_dot(int fmt, const void * w, uint64_t w_bytes, uint32_t rows,
+                   uint32_t cols, const float * x, float * y, uint32_t nx,
+                   uint32_t xstride, uint32_t ystride, const uint32_t * id_slot,
+                   uint64_t estride, int fast, uint32_t i8_mask,
+                   uint32_t i8k_mask, void * stream);
+
+/* Execute a task table in array order on one stream (replaces the persistent
+ * executor's per-task dispatch, exec_task_block, src/runtime/gpu_exec.cu:
+ * 64-140, for a topologically ordered table such as run_serial walks,
+ * src/runtime/graph.cpp:116-148).  Supported kinds: STREAM_DOT,
+ * STREAM_DOT_IDX, ACT_Q8, MERGE, SIGNAL, ROUTER_SEL, SILU_MUL, WMERGE;
+ * anything else -> FLH_ERR_UNSUPPORTED before any launch.  Consecutive
+ * STREAM_DOT row tiles of one matrix (same fmt/cols/x/nx/strides, w and y
+ * contiguous) are fused into one launch; results are unchanged. */
+int flh_exec_tasks(const flh_task * tasks, uint32_t n, int fast,
+                   uint32_t i8_mask, uint32_t i8k_mask, void * stream);
+
+/* Bit-exact dequantisation of whole rows to fp32, out[r*cols + c]
+ * (dequant_chunk, src/runtime/kernels.h:162-242). */
+int flh_dequant(int fmt, const void * w, uint32_t rows, uint32_t cols,
+                float * out, void * stream);
+
+/* ------------------------------------------------------------------ MoE -- */
+/* Grouped expert matvec (the STREAM_DOT_IDX expert tiles of
+ * src/model/decoder.cpp:941-996, grouped by expert): for every routed pair
+ * i = tok*top_k + slot with e = ids[i],
+ *   y[i*ystride + r] += dot(W_e[r], x + xi*xstride),  W_e = w + e*estride,
+ * xi = tok (x_per_slot = 0) or i (x_per_slot = 1).  Each expert's weights
+ * are streamed once for all of its pairs; every output is bitwise equal to
+ * the per-pair STREAM_DOT_IDX tile.  q8_K path (K formats). */
+int flh_moe_dot(int fmt, const void * w, uint64_t estride, uint32_t rows,
+                uint32_t cols, const uint32_t * ids, uint32_t ntok,
+                uint32_t top_k, uint32_t n_expert, const float * x,
+                uint32_t xstride, uint32_t x_per_slot, float * y,
+                uint32_t ystride, void * stream);
+
+/* ROUTER_SEL for ntok tokens (fl_op_router_sel, decode_params.h:234-265):
+ * logits [ntok][n_expert], ids/gates [ntok][top_k]. */
+int flh_router_sel(const float * logits, uint32_t ntok, uint32_t n_expert,
+                   uint32_t top_k, uint32_t norm, float scale, uint32_t * ids,
+                   float * gates, void * stream);
+/* SILU_MUL over ncol columns (fl_op_silu_mul, decode_params.h:267-272):
+ * h[c*hstride + i] = silu(g[c*gstride + i]) * u[c*gstride + i]. */
+int flh_silu_mul(const float * gate, const float * up, float * h, uint32_t n,
+                 uint32_t ncol, uint32_t gstride, uint32_t hstride, void * stream);
+/* WMERGE over ncol columns (fl_op_wmerge, decode_params.h:274-295): column c
+ * reads parts + c*pstride ([n_parts][n]), gates + c*n_parts, add1/add2 +
+ * c*ystride, writes y + c*ystride. */
+int flh_wmerge(const float * parts, const float * gates, const float * add1,
+               const float * add2, float * y, float scale, uint32_t n_parts,
+               uint32_t n, uint32_t n_full, uint32_t ncol, uint32_t pstride,
+               uint32_t ystride, void * stream);
+
+/* ----------------------------------------------------- synthetic inputs -- */
+/* dst[i] = mean + stddev * N(0,1) from a counter-based generator keyed by
+ * (seed, i); a fraction outlier_frac of entries is multiplied by
+ * outlier_scale.  Deterministic for a given (seed, n). */
+int flh_fill_normal(float * dst, size_t n, uint64_t seed, float mean,
+                    float stddev, float outlier_frac, float outlier_scale,
+                    void * stream);
+/* fp32 rows -> Q8_0 / Q4_K / Q6_K blocks on the device; flh_quantize_host
+ * produces the same bytes on the host.  (The reference ships no weight
+ * quantizer; these are this backend's own, for synthetic weights.) */
+int flh_quantize(int fmt, const float * src, uint32_t rows, uint32_t cols,
+                 void * dst, void * stream);
+int flh_quantize_host(int fmt, const float * src, uint32_t rows, uint32_t cols,
+                      void * dst);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* FASTLLM_HIP_H */

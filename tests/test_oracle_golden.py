@@ -1,0 +1,78 @@
+"""The C oracle reproduces the reference's own outputs bit for bit.
+
+Fixtures: tests/golden/golden_ref.npz, written by tests/golden/make_golden.py
+from the reference's quants.h / kernels.h / decode_params.h compiled in the
+build container (oracle/_ref).  Every comparison here is bitwise.
+"""
+import numpy as np
+import pytest
+
+from oracle import x_alloc_bytes
+
+
+def bits(a):
+    return np.ascontiguousarray(a).view(np.uint32)
+
+
+def test_float2half_matches_reference(orc, golden):
+    f, h = golden["f2h_in"], golden["f2h_out"]
+    got = np.array([orc.float2half(float(v)) for v in f], dtype=np.uint16)
+    assert np.array_equal(got, h)
+
+
+@pytest.mark.parametrize("cols", [96, 256, 512, 2816, 4096])
+def test_act_q8_matches_reference(orc, golden, cols):
+    x = golden[f"act_{cols}_x"]
+    want = golden[f"act_{cols}_buf"]
+    got = orc.act_q8(x)
+    assert got.size == x_alloc_bytes(cols)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("fmt,cols", [(1, 512), (3, 1024), (4, 1024)])
+def test_dequant_matches_reference(orc, golden, fmt, cols):
+    w = golden[f"dq_{fmt}_w"]
+    want = golden[f"dq_{fmt}_out"]
+    got = orc.dequant(fmt, w, 3, cols)
+    assert np.array_equal(bits(got), bits(want))
+
+
+def test_stream_dot_every_mode_matches_reference(orc, golden):
+    n = int(golden["dot_count"][0])
+    assert n >= 40
+    for i in range(n):
+        fmt, cols, rows, nx, st, fast, i8, i8k = (int(v) for v in golden[f"dot{i}_meta"])
+        y = golden[f"dot{i}_y0"].copy()
+        orc.stream_dot(fmt, golden[f"dot{i}_w"], rows, cols, golden[f"dot{i}_x"], y, nx=nx,
+                       xstride=st, ystride=rows, fast=fast, i8_mask=i8, i8k_mask=i8k)
+        assert np.array_equal(bits(y), bits(golden[f"dot{i}_y"])), (i, fmt, cols, nx, fast, i8, i8k)
+
+
+def test_stream_dot_idx_matches_reference(orc, golden):
+    from oracle import row_bytes
+    y = np.zeros(5, dtype=np.float32)
+    orc.stream_dot(3, golden["idx_w"], 5, 1024, golden["idx_x"], y, fast=1,
+                   id_slot=2, estride=5 * row_bytes(3, 1024))
+    assert np.array_equal(bits(y), bits(golden["idx_y"]))
+
+
+def test_router_kat(orc, golden):
+    # tests/test_decode_ops.cpp:84-102: ties -> lower index first
+    for norm in (0, 1):
+        ids, gates = orc.router_sel(golden["router_kat_in"], 3, norm=norm)
+        assert list(ids) == [1, 3, 5]
+        assert np.array_equal(ids, golden[f"router_kat_ids_{norm}"])
+        assert np.array_equal(bits(gates), bits(golden[f"router_kat_gates_{norm}"]))
+    ids, gates = orc.router_sel(golden["router_kat_in"], 3, norm=1)
+    assert abs(float(gates.sum()) - 1.0) < 1e-6
+
+
+def test_router_silu_wmerge_match_reference(orc, golden):
+    for t in range(golden["router_in"].shape[0]):
+        ids, gates = orc.router_sel(golden["router_in"][t], 2, norm=1)
+        assert np.array_equal(ids, golden["router_ids"][t])
+        assert np.array_equal(bits(gates), bits(golden["router_gates"][t]))
+    h = orc.silu_mul(golden["silu_g"], golden["silu_u"])
+    assert np.array_equal(bits(h), bits(golden["silu_h"]))
+    y = orc.wmerge(golden["wm_parts"], golden["wm_gates"], add1=golden["wm_add1"])
+    assert np.array_equal(bits(y), bits(golden["wm_y"]))

@@ -1,0 +1,33 @@
+"""Input generators shared by the tests (not a checker: inputs only)."""
+import numpy as np
+
+from oracle import row_bytes, Q8_0, Q4_K, Q6_K
+
+BLOCK_BYTES = {Q8_0: 34, Q4_K: 144, Q6_K: 210}
+
+
+def sane_rows(fmt, rows, cols, rng):
+    """Random block bytes with finite fp16 scales, the reference tests' recipe
+    (tests/test_quants.cpp:109-128, tests/test_runtime.cpp:477-487)."""
+    w = rng.integers(0, 256, size=rows * row_bytes(fmt, cols), dtype=np.uint8)
+    blocks = w.reshape(-1, BLOCK_BYTES[fmt])
+    def half():
+        return (0x2000 | (rng.integers(0, 1 << 16, size=blocks.shape[0]) & 0x0BFF)).astype(np.uint16)
+    if fmt == Q6_K:
+        blocks[:, 208:210] = half().view(np.uint8).reshape(-1, 2)
+    else:
+        blocks[:, 0:2] = half().view(np.uint8).reshape(-1, 2)
+        if fmt == Q4_K:
+            blocks[:, 2:4] = half().view(np.uint8).reshape(-1, 2)
+    return w
+
+
+def normal_weights(rows, cols, rng, std=0.02):
+    return (rng.standard_normal((rows, cols)) * std).astype(np.float32)
+
+
+def activations(nx, cols, rng, outliers=False):
+    x = rng.standard_normal((nx, cols)).astype(np.float32)
+    if outliers:
+        x[rng.random(x.shape) < 0.01] *= 20.0
+    return x
