@@ -83,8 +83,15 @@ __device__ __forceinline__ uint32_t ld1(const uint8_t * p) { return *(const uint
 __device__ __forceinline__ uint32_t ldh(const uint8_t * p) { return *(const uint16_t *)p; }
 // streamed-once weight loads: non-temporal hint keeps them from evicting the
 // reused activations from L2.
+#ifndef FLH_NT
+#define FLH_NT 1
+#endif
 __device__ __forceinline__ u32x4 ld4_nt(const uint8_t * p) {
+#if FLH_NT
     return __builtin_nontemporal_load((const u32x4 *)p);
+#else
+    return *(const u32x4 *)p;
+#endif
 }
 
 }  // namespace flh

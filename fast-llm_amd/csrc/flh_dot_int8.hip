@@ -30,6 +30,8 @@
 #include "flh_common.h"
 #include "flh_internal.h"
 #include "flh_status.h"
+#include <stdio.h>
+#include <stdlib.h>
 
 namespace flh {
 
@@ -42,35 +44,39 @@ __host__ __device__ inline uint32_t ceil_log2(uint32_t v) {
 // ------------------------------------------------------------ Q4_K x q8_K --
 struct Q4W { u32x4 h, qa, qb; };
 
+// Lane c of a superblock loads qs[16c, 16c+16) and qs[64+16c, 64+16c+16),
+// so the 4 lanes of a superblock read two contiguous 64-byte runs.  Lane c
+// then owns positions l in [16(c&1), 16(c&1)+16) of groups
+// g0 = 2(c>>1), g0+1 (low/high nibbles of the first run) and g0+4, g0+5
+// (second run).
 __device__ __forceinline__ Q4W q4_load(const uint8_t * blk, uint32_t c) {
     Q4W r;
     r.h  = ld4_nt(blk);
-    r.qa = ld4_nt(blk + 16 + 32 * c);
-    r.qb = ld4_nt(blk + 32 + 32 * c);
+    r.qa = ld4_nt(blk + 16 + 16 * c);
+    r.qb = ld4_nt(blk + 80 + 16 * c);
     return r;
 }
 
 template <int NX>
 struct Q4X {                    // activation slice of one lane, NX columns
-    int q[NX][16];              // x[64c .. 64c+64) of this superblock
-    int b0[NX], b1[NX];         // bsums[4c]+bsums[4c+1], bsums[4c+2]+bsums[4c+3]
+    int q[NX][4][4];            // [column][group slot][dword]: x[32g + 16(c&1) ..+16)
+    int bs[NX][4];              // bsums[2g + (c&1)] of the lane's 4 groups
 };
 
 template <int NX>
 __device__ __forceinline__ void q4x_load(Q4X<NX> & X, const uint8_t * const * xk,
                                          uint32_t nx, uint32_t sb, uint32_t c) {
+    const uint32_t g0 = 2 * (c >> 1), h = c & 1;
+    const uint32_t gs[4] = {g0, g0 + 1, g0 + 4, g0 + 5};
 #pragma unroll
     for (int p = 0; p < NX; ++p) {
         const uint8_t * b = xk[p < (int)nx ? p : 0] + (size_t)sb * 292;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            const u32x4 v = ld4(b + 36 + 64 * c + 16 * k);
-            X.q[p][4 * k + 0] = v.x; X.q[p][4 * k + 1] = v.y;
-            X.q[p][4 * k + 2] = v.z; X.q[p][4 * k + 3] = v.w;
+            const u32x4 v = ld4(b + 36 + 32 * gs[k] + 16 * h);
+            X.q[p][k][0] = v.x; X.q[p][k][1] = v.y; X.q[p][k][2] = v.z; X.q[p][k][3] = v.w;
+            X.bs[p][k] = (int)*(const int16_t *)(b + 4 + 2 * (2 * gs[k] + h));
         }
-        const uint32_t s0 = ld1(b + 4 + 8 * c), s1 = ld1(b + 8 + 8 * c);
-        X.b0[p] = (int)(int16_t)(s0 & 0xFFFF) + (int)(int16_t)(s0 >> 16);
-        X.b1[p] = (int)(int16_t)(s1 & 0xFFFF) + (int)(int16_t)(s1 >> 16);
     }
 }
 
@@ -123,7 +129,7 @@ __host__ __device__ inline size_t kq_smem_bytes(uint32_t nr, uint32_t nx_t, uint
     return 4 * (terms + (size_t)nr * P + (size_t)nx_t * P);
 }
 
-template <int FMT, int NX>
+template <int FMT, int NX, int D>
 __device__ __forceinline__ void kq_core(const uint8_t * __restrict__ w, uint32_t rows,
                                         uint32_t cols, const uint8_t * const * xk,
                                         float * const * yc, uint32_t nx, uint32_t nr,
@@ -160,104 +166,123 @@ __device__ __forceinline__ void kq_core(const uint8_t * __restrict__ w, uint32_t
         else                           return q6_load(blk, c);
     };
 
+    // integer partials of one (row-sub, superblock, part) item -> LDS terms
+    auto process = [&](const WT & Wv, uint32_t rl, uint32_t nrow) {
+        const bool wr = act && c == 0 && rl < nrow;
+        if constexpr (FMT == FMT_Q4_K) {
+            const Q4W & W = Wv;
+            // 6-bit scale/min unpack for all 8 groups, packed one byte per group
+            const uint32_t sclo = W.h.y & 0x3F3F3F3Fu;
+            const uint32_t mlo  = W.h.z & 0x3F3F3F3Fu;
+            const uint32_t schi = (W.h.w & 0x0F0F0F0Fu) | ((W.h.y >> 2) & 0x30303030u);
+            const uint32_t mhi  = ((W.h.w >> 4) & 0x0F0F0F0Fu) | ((W.h.z >> 2) & 0x30303030u);
+            const uint32_t sh = (c >> 1) * 16;
+            const int sc[4] = {(int)((sclo >> sh) & 0xFF), (int)((sclo >> (sh + 8)) & 0xFF),
+                               (int)((schi >> sh) & 0xFF), (int)((schi >> (sh + 8)) & 0xFF)};
+            const int mn[4] = {(int)((mlo >> sh) & 0xFF), (int)((mlo >> (sh + 8)) & 0xFF),
+                               (int)((mhi >> sh) & 0xFF), (int)((mhi >> (sh + 8)) & 0xFF)};
+            const uint32_t q[2][4] = {{W.qa.x, W.qa.y, W.qa.z, W.qa.w},
+                                      {W.qb.x, W.qb.y, W.qb.z, W.qb.w}};
+            int nib[4][4];          // [group slot][dword]
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                nib[0][k] = (int)(q[0][k] & 0x0F0F0F0Fu);
+                nib[1][k] = (int)((q[0][k] >> 4) & 0x0F0F0F0Fu);
+                nib[2][k] = (int)(q[1][k] & 0x0F0F0F0Fu);
+                nib[3][k] = (int)((q[1][k] >> 4) & 0x0F0F0F0Fu);
+            }
+#pragma unroll
+            for (int p = 0; p < NX; ++p) {
+                int ia = 0, im = 0;
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    int d = 0;
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) d = dot4(nib[g][k], X.q[p][g][k], d);
+                    ia += sc[g] * d;
+                    im += mn[g] * X.bs[p][g];
+                }
+                ia += qx1(ia); ia += qx2(ia);
+                im += qx1(im); im += qx2(im);
+                if (wr && p < (int)nx) {
+                    TI[((rl * NX + p) << lgP) + sb] = ia;
+                    TM[((rl * NX + p) << lgP) + sb] = im;
+                }
+            }
+            if (wr) TH[(rl << lgP) + sb] = W.h.x;
+        } else {
+            const Q6W & W = Wv;
+            const uint32_t sh = W.sh;
+            const uint32_t A[5] = {W.a.x, W.a.y, W.a.z, W.a.w, W.a4};
+            const uint32_t B[5] = {W.b.x, W.b.y, W.b.z, W.b.w, W.b4};
+            const uint32_t H[5] = {W.h.x, W.h.y, W.h.z, W.h.w, W.h4};
+            const uint32_t S[5] = {W.s.x, W.s.y, W.s.z, W.s.w, W.s4};
+            uint32_t Sa[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) Sa[i] = alignb(S[i + 1], S[i], sh);
+            const uint32_t dbits = alignb(W.s4, W.s4, sh) & 0xFFFFu;
+            const uint32_t hh = c >> 1, bb = c & 1;
+            const uint32_t sd0 = hh ? Sa[2] : Sa[0], sd1 = hh ? Sa[3] : Sa[1];
+            const int sc[4] = {(int)(int8_t)(sd0 >> (8 * bb)), (int)(int8_t)(sd0 >> (8 * bb + 16)),
+                               (int)(int8_t)(sd1 >> (8 * bb)), (int)(int8_t)(sd1 >> (8 * bb + 16))};
+            int g[4][4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t a = alignb(A[i + 1], A[i], sh);
+                const uint32_t b = alignb(B[i + 1], B[i], sh);
+                const uint32_t h = alignb(H[i + 1], H[i], sh);
+                g[0][i] = (int)((a & 0x0F0F0F0Fu) | ((h & 0x03030303u) << 4));
+                g[1][i] = (int)((b & 0x0F0F0F0Fu) | ((h << 2) & 0x30303030u));
+                g[2][i] = (int)(((a >> 4) & 0x0F0F0F0Fu) | (h & 0x30303030u));
+                g[3][i] = (int)(((b >> 4) & 0x0F0F0F0Fu) | ((h >> 2) & 0x30303030u));
+            }
+#pragma unroll
+            for (int p = 0; p < NX; ++p) {
+                int ia = 0;
+#pragma unroll
+                for (int gg = 0; gg < 4; ++gg) {
+                    int d = 0;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) d = dot4(g[gg][i], X.q[p][gg][i], d);
+                    ia += sc[gg] * (d - X.b32[p][gg]);
+                }
+                ia += qx1(ia); ia += qx2(ia);
+                if (wr && p < (int)nx) TI[((rl * NX + p) << lgP) + sb] = ia;
+            }
+            if (wr) TH[(rl << lgP) + sb] = dbits;
+        }
+    };
+
     const uint32_t nbatch = (rows + nr - 1) / nr;
     const uint32_t nit = (nr + rpi - 1) / rpi;
+    const uint32_t fk = tid & 3, fp = (tid >> 2) % NX, frl = tid / (4 * NX);
     for (uint32_t bt = batch0; bt < nbatch; bt += bstep) {
         const uint32_t row0 = bt * nr;
         const uint32_t nrow = min(nr, rows - row0);
-        auto row_of = [&](uint32_t it) { return it * rpi + rsub; };
         auto clamp_row = [&](uint32_t rl) { return row0 + (rl < nrow ? rl : nrow - 1); };
-
-        WT cur = wload(clamp_row(row_of(0)));
-        for (uint32_t it = 0; it < nit; ++it) {
-            WT nxt = cur;
-            if (it + 1 < nit) nxt = wload(clamp_row(row_of(it + 1)));
-            const uint32_t rl = row_of(it);
-            const bool wr = act && c == 0 && rl < nrow;
-            if constexpr (FMT == FMT_Q4_K) {
-                const Q4W & W = cur;
-                const bool hi = c >= 2;
-                const uint32_t sh = (c & 1) * 16;
-                const uint32_t scp = hi ? ((W.h.w & 0x0F0F0F0Fu) | ((W.h.y >> 2) & 0x30303030u))
-                                        : (W.h.y & 0x3F3F3F3Fu);
-                const uint32_t mp  = hi ? (((W.h.w >> 4) & 0x0F0F0F0Fu) | ((W.h.z >> 2) & 0x30303030u))
-                                        : (W.h.z & 0x3F3F3F3Fu);
-                const int sc0 = (scp >> sh) & 0xFF, sc1 = (scp >> (sh + 8)) & 0xFF;
-                const int m0 = (mp >> sh) & 0xFF, m1 = (mp >> (sh + 8)) & 0xFF;
-                const uint32_t q[8] = {W.qa.x, W.qa.y, W.qa.z, W.qa.w,
-                                       W.qb.x, W.qb.y, W.qb.z, W.qb.w};
-                int lo[8], hv[8];
+        // The fold lane's y value, fetched before the weight stream starts.
+        // Every load in this loop nest is unconditional (addresses clamped
+        // to valid rows) so the compiler can count outstanding loads
+        // statically and keep D iterations in flight; a conditional load
+        // makes it fall back to waiting for all of them.
+        const bool fok = frl < nrow && fp < nx;
+        const float yold = yc[fp][row0 + (frl < nrow ? frl : nrow - 1)];
+        WT buf[D];
 #pragma unroll
-                for (int k = 0; k < 8; ++k) {
-                    lo[k] = (int)(q[k] & 0x0F0F0F0Fu);
-                    hv[k] = (int)((q[k] >> 4) & 0x0F0F0F0Fu);
-                }
+        for (int j = 0; j < D; ++j) buf[j] = wload(clamp_row(j * rpi + rsub));
+        for (uint32_t it0 = 0; it0 < nit; it0 += D) {
 #pragma unroll
-                for (int p = 0; p < NX; ++p) {
-                    int dl = 0, dh = 0;
-#pragma unroll
-                    for (int k = 0; k < 8; ++k) {
-                        dl = dot4(lo[k], X.q[p][k], dl);
-                        dh = dot4(hv[k], X.q[p][8 + k], dh);
-                    }
-                    int ia = sc0 * dl + sc1 * dh;
-                    int im = m0 * X.b0[p] + m1 * X.b1[p];
-                    ia += qx1(ia); ia += qx2(ia);
-                    im += qx1(im); im += qx2(im);
-                    if (wr && p < (int)nx) {
-                        TI[((rl * NX + p) << lgP) + sb] = ia;
-                        TM[((rl * NX + p) << lgP) + sb] = im;
-                    }
-                }
-                if (wr) TH[(rl << lgP) + sb] = W.h.x;
-            } else {
-                const Q6W & W = cur;
-                const uint32_t sh = W.sh;
-                const uint32_t A[5] = {W.a.x, W.a.y, W.a.z, W.a.w, W.a4};
-                const uint32_t B[5] = {W.b.x, W.b.y, W.b.z, W.b.w, W.b4};
-                const uint32_t H[5] = {W.h.x, W.h.y, W.h.z, W.h.w, W.h4};
-                const uint32_t S[5] = {W.s.x, W.s.y, W.s.z, W.s.w, W.s4};
-                uint32_t Sa[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) Sa[i] = alignb(S[i + 1], S[i], sh);
-                const uint32_t dbits = alignb(W.s4, W.s4, sh) & 0xFFFFu;
-                const uint32_t hh = c >> 1, bb = c & 1;
-                const uint32_t sd0 = hh ? Sa[2] : Sa[0], sd1 = hh ? Sa[3] : Sa[1];
-                const int sc[4] = {(int)(int8_t)(sd0 >> (8 * bb)), (int)(int8_t)(sd0 >> (8 * bb + 16)),
-                                   (int)(int8_t)(sd1 >> (8 * bb)), (int)(int8_t)(sd1 >> (8 * bb + 16))};
-                int g[4][4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const uint32_t a = alignb(A[i + 1], A[i], sh);
-                    const uint32_t b = alignb(B[i + 1], B[i], sh);
-                    const uint32_t h = alignb(H[i + 1], H[i], sh);
-                    g[0][i] = (int)((a & 0x0F0F0F0Fu) | ((h & 0x03030303u) << 4));
-                    g[1][i] = (int)((b & 0x0F0F0F0Fu) | ((h << 2) & 0x30303030u));
-                    g[2][i] = (int)(((a >> 4) & 0x0F0F0F0Fu) | (h & 0x30303030u));
-                    g[3][i] = (int)(((b >> 4) & 0x0F0F0F0Fu) | ((h >> 2) & 0x30303030u));
-                }
-#pragma unroll
-                for (int p = 0; p < NX; ++p) {
-                    int ia = 0;
-#pragma unroll
-                    for (int gg = 0; gg < 4; ++gg) {
-                        int d = 0;
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) d = dot4(g[gg][i], X.q[p][gg][i], d);
-                        ia += sc[gg] * (d - X.b32[p][gg]);
-                    }
-                    ia += qx1(ia); ia += qx2(ia);
-                    if (wr && p < (int)nx) TI[((rl * NX + p) << lgP) + sb] = ia;
-                }
-                if (wr) TH[(rl << lgP) + sb] = dbits;
+            for (int j = 0; j < D; ++j) {
+                const uint32_t it = it0 + j;
+                process(buf[j], it * rpi + rsub, nrow);     // writes nothing past nrow
+                buf[j] = wload(clamp_row((it + D) * rpi + rsub));
             }
-            cur = nxt;
         }
         __syncthreads();
         // ordered float fold: lane -> (row, column, accumulator k)
         {
-            const uint32_t k = tid & 3, p = (tid >> 2) % NX, rl = tid / (4 * NX);
-            const bool ok = rl < nrow && p < nx && rl < nr;
+            const uint32_t k = fk, p = fp, rl = frl;
+            const bool ok = fok;
             float acc = 0.f;
             if (ok) {
                 const int * ti = TI + ((rl * NX + p) << lgP);
@@ -278,16 +303,13 @@ __device__ __forceinline__ void kq_core(const uint8_t * __restrict__ w, uint32_t
             }
             const float s01 = acc + qx1f(acc);          // lane k=0: a0+a1, k=2: a2+a3
             const float r = s01 + qx2f(s01);            // lane k=0: (a0+a1)+(a2+a3)
-            if (ok && k == 0) {
-                float * yp = yc[p] + row0 + rl;
-                *yp = *yp + r;
-            }
+            if (ok && k == 0) yc[p][row0 + rl] = yold + r;
         }
         __syncthreads();
     }
 }
 
-template <int FMT, int NX>
+template <int FMT, int NX, int D>
 __global__ __launch_bounds__(256) void k_dot_i8k(DotArgs a, uint32_t nr) {
     extern __shared__ int smem[];
     const uint8_t * w = a.w + (a.id_slot ? (size_t)(*a.id_slot) * a.estride : 0);
@@ -299,7 +321,7 @@ __global__ __launch_bounds__(256) void k_dot_i8k(DotArgs a, uint32_t nr) {
         xk[p] = (const uint8_t *)(a.x + (size_t)pp * a.xstride) + xqk_off(a.cols);
         yc[p] = a.y + (size_t)pp * a.ystride;
     }
-    kq_core<FMT, NX>(w, a.rows, a.cols, xk, yc, a.nx, nr, blockIdx.x, gridDim.x, smem);
+    kq_core<FMT, NX, D>(w, a.rows, a.cols, xk, yc, a.nx, nr, blockIdx.x, gridDim.x, smem);
 }
 
 // Grouped expert kernel: blockIdx.y = expert.  The workgroup scans the
@@ -332,7 +354,7 @@ __global__ __launch_bounds__(256) void k_moe_i8k(MoeArgs a, uint32_t nr) {
             xk[p] = (const uint8_t *)(a.x + (size_t)xi * a.xstride) + xqk_off(a.cols);
             yc[p] = a.y + (size_t)ts * a.ystride;
         }
-        kq_core<FMT, NX>(w, a.rows, a.cols, xk, yc, nx, nr, blockIdx.x, gridDim.x, smem);
+        kq_core<FMT, NX, 2>(w, a.rows, a.cols, xk, yc, nx, nr, blockIdx.x, gridDim.x, smem);
         __syncthreads();
     }
 }
@@ -465,6 +487,23 @@ __global__ __launch_bounds__(256) void k_dot_i8_q8_0(DotArgs a, uint32_t nr) {
 }
 
 // ----------------------------------------------------------------- launch --
+// Launch shape of the K-format kernels: a persistent grid of at most
+// wgs_per_cu workgroups per CU, each looping over batches of nr rows with a
+// D-deep weight pipeline.  FLH_KQ_TUNE="wgs_per_cu,nr,D" overrides the
+// defaults (development sweeps only).
+struct KqTune { uint32_t wgs_per_cu, nr, D; };
+static KqTune kq_tune() {
+    static KqTune t = [] {
+        KqTune d{4, 0, 2};
+        if (const char * e = getenv("FLH_KQ_TUNE")) {
+            unsigned a = 0, b = 0, c = 0;
+            if (sscanf(e, "%u,%u,%u", &a, &b, &c) == 3) d = KqTune{a, b, c};
+        }
+        return d;
+    }();
+    return t;
+}
+
 static uint32_t pick_nr(uint32_t rows, uint32_t rpi, uint32_t nr_max) {
     const uint32_t target = (uint32_t)num_cus() * 8u;
     uint32_t nr = (rows + target - 1) / target;
@@ -474,15 +513,33 @@ static uint32_t pick_nr(uint32_t rows, uint32_t rpi, uint32_t nr_max) {
     return nr;
 }
 
+template <int FMT, int NX, int D>
+static int launch_kq_d(const DotArgs & a, uint32_t nr, uint32_t grid, size_t sm, hipStream_t s) {
+    hipLaunchKernelGGL((k_dot_i8k<FMT, NX, D>), dim3(grid), dim3(256), sm, s, a, nr);
+    return hip_check(hipGetLastError(), "k_dot_i8k launch");
+}
+
 template <int FMT, int NX>
 static int launch_kq(const DotArgs & a, hipStream_t s) {
     const uint32_t nsb = a.cols >> 8;
     const uint32_t P = 1u << ceil_log2(nsb), rpi = 64u / P;
-    const uint32_t nr = pick_nr(a.rows, rpi, 64u / NX);
+    const KqTune t = kq_tune();
+    uint32_t nr;
+    if (t.nr) {
+        nr = t.nr > 64u / NX ? 64u / NX : t.nr;
+        if (nr > rpi) nr = (nr / rpi) * rpi;
+    } else {
+        nr = pick_nr(a.rows, rpi, 64u / NX);
+    }
     const size_t sm = kq_smem_bytes<FMT>(nr, NX, P);
-    const uint32_t grid = (a.rows + nr - 1) / nr;
-    hipLaunchKernelGGL((k_dot_i8k<FMT, NX>), dim3(grid), dim3(256), sm, s, a, nr);
-    return hip_check(hipGetLastError(), "k_dot_i8k launch");
+    const uint32_t nbatch = (a.rows + nr - 1) / nr;
+    const uint32_t cap = (uint32_t)num_cus() * (t.wgs_per_cu ? t.wgs_per_cu : 4u);
+    const uint32_t grid = nbatch < cap ? nbatch : cap;
+    switch (t.D) {
+        case 1: return launch_kq_d<FMT, NX, 1>(a, nr, grid, sm, s);
+        case 4: return launch_kq_d<FMT, NX, 4>(a, nr, grid, sm, s);
+        default: return launch_kq_d<FMT, NX, 2>(a, nr, grid, sm, s);
+    }
 }
 
 int launch_dot_i8k(int fmt, const DotArgs & a0, hipStream_t s) {
@@ -495,7 +552,11 @@ int launch_dot_i8k(int fmt, const DotArgs & a0, hipStream_t s) {
         a.nx = a0.nx - p0 < 4 ? a0.nx - p0 : 4;
         a.x = a0.x + (size_t)p0 * a0.xstride;
         a.y = a0.y + (size_t)p0 * a0.ystride;
-        int rc;
+        int rc = launch_dot_kstream(fmt, a, s);
+        if (rc != FLH_ERR_UNSUPPORTED) {
+            if (rc) return rc;
+            continue;
+        }
         if (fmt == FMT_Q4_K) {
             rc = a.nx == 1 ? launch_kq<FMT_Q4_K, 1>(a, s)
                : a.nx == 2 ? launch_kq<FMT_Q4_K, 2>(a, s) : launch_kq<FMT_Q4_K, 4>(a, s);

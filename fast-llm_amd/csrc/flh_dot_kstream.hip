@@ -1,0 +1,405 @@
+// flh_dot_kstream.hip -- LDS-staged int8 x q8_K row-dots for Q4_K / Q6_K.
+//
+// The streamed weight bytes go HBM -> LDS with gfx950's direct-to-LDS
+// dwordx4 loads (global_load_lds_dwordx4), one fully coalesced pass: every
+// 64-byte line of the matrix is requested from L2 exactly once.  (Loading a
+// superblock's header and nibbles straight into the lanes that use them asks
+// L2 for each line ~3x, and that request rate, not HBM, becomes the limit.)
+//
+// Work unit: a CHUNK of 16 consecutive superblocks of the row-major matrix
+// (rows are contiguous, so a chunk may straddle a row boundary).  A workgroup
+// (4 waves) owns a batch of nr whole rows; its chunks are dealt round-robin
+// to the waves, each wave keeping D chunks in flight in a private LDS ring.
+// Lane (slot s = lane/4, part c = lane%4) of a wave handles superblock s of
+// the chunk, quarter c, exactly as in flh_dot_int8.hip: integer partials,
+// DPP quad reduction, (row, column, superblock) terms parked in LDS, then the
+// reference-order float fold per (row, column, accumulator).  Results are
+// bitwise equal to fl_dot_i8k_q4_K / fl_dot_i8k_q6_K
+// (src/runtime/quants.h:538-594).
+//
+// The activation (q8_K appendix) is re-laid in LDS once per workgroup as
+// 80-byte per-lane records (64 int8 + 4 int32 block sums), so every lane
+// reads its slice with five conflict-free 16-byte LDS reads.
+#include "flh_common.h"
+#include "flh_internal.h"
+#include "flh_status.h"
+#include <stdio.h>
+#include <stdlib.h>
+
+namespace flh {
+
+#define GPTR(p) ((const void __attribute__((address_space(1))) *)(p))
+#define LPTR(p) ((void __attribute__((address_space(3))) *)(p))
+
+// s_waitcnt vmcnt(n) only (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14])
+#define WAIT_VM(n) __builtin_amdgcn_s_waitcnt(((n) & 0xF) | (0x7 << 4) | (0xF << 8) | (((n) >> 4) << 14))
+#define WAIT_LGKM0() __builtin_amdgcn_s_waitcnt(0xC07F)
+
+template <int FMT> struct KS;
+template <> struct KS<FMT_Q4_K> {
+    static constexpr uint32_t BLK = 144;
+    static constexpr uint32_t WIN = 2304;            // LDS bytes per chunk stage
+    static constexpr int NI = 3;                     // DMA instructions per chunk
+};
+template <> struct KS<FMT_Q6_K> {
+    static constexpr uint32_t BLK = 210;
+    static constexpr uint32_t WIN = 4096;            // 3360 B + realignment slack
+    static constexpr int NI = 4;
+};
+
+constexpr uint32_t XREC = 80;                        // bytes per (sb, part) activation record
+
+template <int FMT>
+__host__ __device__ inline size_t ks_smem_bytes(uint32_t nr, uint32_t nx, uint32_t nsb, int D) {
+    const size_t stages = (size_t)4 * D * KS<FMT>::WIN;
+    const size_t xrec = (size_t)nx * nsb * 4 * XREC + (size_t)nx * nsb * 4;
+    const size_t terms = (size_t)nr * nx * nsb * 4 * (FMT == FMT_Q4_K ? 2 : 1) + (size_t)nr * nsb * 4;
+    return stages + xrec + terms;
+}
+
+// Issue the DMA of chunk `ch` (batch-local) into a stage.  Lanes past the
+// chunk's valid bytes re-read the last valid 16 bytes (never out of bounds).
+template <int FMT>
+__device__ __forceinline__ void ks_issue(const uint8_t * wb, uint32_t ch, uint32_t nsb_batch,
+                                         uint8_t * stage, uint32_t lane) {
+    constexpr uint32_t B = KS<FMT>::BLK;
+    const uint32_t f0 = ch * 16;
+    const uint32_t nact = nsb_batch - f0 < 16 ? nsb_batch - f0 : 16;
+    if constexpr (FMT == FMT_Q4_K) {
+        const uint8_t * g = wb + (size_t)f0 * B;
+        const uint32_t last16 = nact * B - 16, last4 = nact * B - 4;
+        const uint32_t o0 = 16 * lane, o1 = 1024 + 16 * lane, o2 = 2048 + 4 * lane;
+        __builtin_amdgcn_global_load_lds(GPTR(g + (o0 <= last16 ? o0 : last16)), LPTR(stage), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(GPTR(g + (o1 <= last16 ? o1 : last16)), LPTR(stage + 1024), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(GPTR(g + (o2 <= last4 ? o2 : last4)), LPTR(stage + 2048), 4, 0, 0);
+    } else {
+        const uintptr_t gs = (uintptr_t)(wb + (size_t)f0 * B);
+        const uint8_t * g = (const uint8_t *)(gs & ~(uintptr_t)15);
+        const uint32_t last16 = (uint32_t)((gs + nact * B - 1) - (uintptr_t)g) & ~15u;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t o = 1024 * i + 16 * lane;
+            __builtin_amdgcn_global_load_lds(GPTR(g + (o <= last16 ? o : last16)), LPTR(stage + 1024 * i), 16, 0, 0);
+        }
+    }
+}
+
+__device__ __forceinline__ void wait_vm_upto(uint32_t n) {
+    switch (n) {
+        case 0: WAIT_VM(0); break;
+        case 3: WAIT_VM(3); break;
+        case 4: WAIT_VM(4); break;
+        case 6: WAIT_VM(6); break;
+        case 8: WAIT_VM(8); break;
+        case 9: WAIT_VM(9); break;
+        case 12: WAIT_VM(12); break;
+        default: WAIT_VM(0); break;
+    }
+}
+
+typedef uint32_t u32x4a __attribute__((ext_vector_type(4)));
+
+// 16 bytes at an even LDS byte offset (realigned from 5 aligned dwords)
+__device__ __forceinline__ void lds16_u2(const uint8_t * base, uint32_t off, uint32_t (&o)[4]) {
+    const uint32_t * p = (const uint32_t *)(base + (off & ~3u));
+    const uint32_t sh = off & 3u;
+    uint32_t d[5];
+#pragma unroll
+    for (int i = 0; i < 5; ++i) d[i] = p[i];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = alignb(d[i + 1], d[i], sh);
+}
+
+template <int FMT, int NX, int D>
+__global__ __launch_bounds__(256) void k_dot_kstream(DotArgs a, uint32_t nr) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t sm[];
+    constexpr uint32_t B = KS<FMT>::BLK, WIN = KS<FMT>::WIN;
+    constexpr int NI = KS<FMT>::NI;
+    const uint32_t nsb = a.cols >> 8, nx = a.nx;
+    const uint64_t rb = (uint64_t)nsb * B;
+    const uint8_t * w = a.w + (a.id_slot ? (size_t)(*a.id_slot) * a.estride : 0);
+    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const uint32_t s = lane >> 2, c = lane & 3;
+
+    uint8_t * stages = sm;                                        // [4][D][WIN]
+    uint8_t * xr = sm + (size_t)4 * D * WIN;                      // [NX][nsb][4][80]
+    float * xd = (float *)(xr + (size_t)NX * nsb * 4 * XREC);     // [NX][nsb]
+    int * TI = (int *)(xd + (size_t)NX * nsb);                    // [nr][NX][nsb]
+    int * TM = TI + (size_t)nr * NX * nsb;                        // Q4_K only
+    uint32_t * TH = (uint32_t *)(FMT == FMT_Q4_K ? TM + (size_t)nr * NX * nsb : TM);   // [nr][nsb]
+    uint8_t * myst = stages + (size_t)wave * D * WIN;
+
+    // ---- activation records, once per workgroup
+    for (uint32_t i = tid; i < NX * nsb * 4; i += 256) {
+        const uint32_t p = i / (nsb * 4), rem = i % (nsb * 4), sb = rem >> 2, cc = rem & 3;
+        const uint32_t pp = p < nx ? p : 0;
+        const uint8_t * xb = (const uint8_t *)(a.x + (size_t)pp * a.xstride) + xqk_off(a.cols) + (size_t)sb * 292;
+        uint32_t * rec = (uint32_t *)(xr + (size_t)i * XREC);
+        int bs[4];
+        if constexpr (FMT == FMT_Q4_K) {
+            const uint32_t g0 = 2 * (cc >> 1), h = cc & 1;
+            const uint32_t gs[4] = {g0, g0 + 1, g0 + 4, g0 + 5};
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const u32x4 v = ld4(xb + 36 + 32 * gs[k] + 16 * h);
+                rec[4 * k + 0] = v.x; rec[4 * k + 1] = v.y; rec[4 * k + 2] = v.z; rec[4 * k + 3] = v.w;
+                bs[k] = *(const int16_t *)(xb + 4 + 2 * (2 * gs[k] + h));
+            }
+        } else {
+            const uint32_t hh = cc >> 1, bb = cc & 1;
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const u32x4 v = ld4(xb + 36 + 128 * hh + 32 * g + 16 * bb);
+                rec[4 * g + 0] = v.x; rec[4 * g + 1] = v.y; rec[4 * g + 2] = v.z; rec[4 * g + 3] = v.w;
+                bs[g] = 32 * (int)*(const int16_t *)(xb + 4 + 2 * (8 * hh + 2 * g + bb));
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) rec[16 + k] = (uint32_t)bs[k];
+        if (cc == 0) xd[p * nsb + sb] = (p < nx) ? *(const float *)xb : 0.f;
+    }
+    __syncthreads();
+
+    const uint32_t magic = (uint32_t)((0x100000000ull + nsb - 1) / nsb);   // f / nsb, f < 2^16
+    const uint32_t nbatch = (a.rows + nr - 1) / nr;
+    const uint32_t fk = tid & 3, fp = (tid >> 2) % NX, frl = tid / (4 * NX);
+
+    for (uint32_t bt = blockIdx.x; bt < nbatch; bt += gridDim.x) {
+        const uint32_t row0 = bt * nr;
+        const uint32_t nrow = min(nr, a.rows - row0);
+        const uint32_t nsbb = nrow * nsb;                       // superblocks in this batch
+        const uint32_t nch = (nsbb + 15) / 16;
+        const uint32_t nci = nch > wave ? (nch - wave + 3) / 4 : 0;   // this wave's chunks
+        const uint8_t * wb = w + (size_t)row0 * rb;
+        const bool fok = frl < nrow && fp < nx;
+        const float yold = a.y[(size_t)fp * a.ystride + row0 + (frl < nrow ? frl : nrow - 1)];
+        if (nci) {
+#pragma unroll
+            for (int j = 0; j < D; ++j) {
+                const uint32_t ci = (uint32_t)j < nci ? (uint32_t)j : nci - 1;
+                ks_issue<FMT>(wb, wave + 4 * ci, nsbb, myst + j * WIN, lane);
+            }
+        }
+        for (uint32_t i0 = 0; i0 < nci; i0 += D) {
+#pragma unroll
+            for (int j = 0; j < D; ++j) {
+                const uint32_t i = i0 + j;
+                if (i < nci) {
+                    // chunks issued after this one: D - 1 (refills keep the ring full)
+                    WAIT_VM(NI * (D - 1));
+                    const uint8_t * st = myst + j * WIN;
+                    const uint32_t f = (wave + 4 * i) * 16 + s;            // batch-local superblock
+                    const bool act = f < nsbb;
+                    const uint32_t ff = act ? f : nsbb - 1;
+                    const uint32_t rl = __umulhi(ff, magic);
+                    const uint32_t sb = ff - rl * nsb;
+                    const uint8_t * xrec = xr + ((size_t)sb * 4 + c) * XREC;
+                    int ia[NX], im[NX];
+                    uint32_t tag;
+                    if constexpr (FMT == FMT_Q4_K) {
+                        const u32x4a hd = *(const u32x4a *)(st + 144 * s);
+                        const u32x4a qa = *(const u32x4a *)(st + 144 * s + 16 + 16 * c);
+                        const u32x4a qb = *(const u32x4a *)(st + 144 * s + 80 + 16 * c);
+                        tag = hd.x;
+                        const uint32_t sclo = hd.y & 0x3F3F3F3Fu, mlo = hd.z & 0x3F3F3F3Fu;
+                        const uint32_t schi = (hd.w & 0x0F0F0F0Fu) | ((hd.y >> 2) & 0x30303030u);
+                        const uint32_t mhi = ((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u);
+                        const uint32_t sh = (c >> 1) * 16;
+                        const int sc[4] = {(int)((sclo >> sh) & 0xFF), (int)((sclo >> (sh + 8)) & 0xFF),
+                                           (int)((schi >> sh) & 0xFF), (int)((schi >> (sh + 8)) & 0xFF)};
+                        const int mn[4] = {(int)((mlo >> sh) & 0xFF), (int)((mlo >> (sh + 8)) & 0xFF),
+                                           (int)((mhi >> sh) & 0xFF), (int)((mhi >> (sh + 8)) & 0xFF)};
+                        const uint32_t q[2][4] = {{qa.x, qa.y, qa.z, qa.w}, {qb.x, qb.y, qb.z, qb.w}};
+                        int nib[4][4];
+#pragma unroll
+                        for (int k = 0; k < 4; ++k) {
+                            nib[0][k] = (int)(q[0][k] & 0x0F0F0F0Fu);
+                            nib[1][k] = (int)((q[0][k] >> 4) & 0x0F0F0F0Fu);
+                            nib[2][k] = (int)(q[1][k] & 0x0F0F0F0Fu);
+                            nib[3][k] = (int)((q[1][k] >> 4) & 0x0F0F0F0Fu);
+                        }
+#pragma unroll
+                        for (int p = 0; p < NX; ++p) {
+                            const uint8_t * xp = xrec + (size_t)p * nsb * 4 * XREC;
+                            int acc_i = 0, acc_m = 0;
+#pragma unroll
+                            for (int g = 0; g < 4; ++g) {
+                                const u32x4a xv = *(const u32x4a *)(xp + 16 * g);
+                                int d = 0;
+                                d = dot4(nib[g][0], (int)xv.x, d);
+                                d = dot4(nib[g][1], (int)xv.y, d);
+                                d = dot4(nib[g][2], (int)xv.z, d);
+                                d = dot4(nib[g][3], (int)xv.w, d);
+                                acc_i += sc[g] * d;
+                            }
+                            const u32x4a bsv = *(const u32x4a *)(xp + 64);
+                            acc_m = mn[0] * (int)bsv.x + mn[1] * (int)bsv.y + mn[2] * (int)bsv.z + mn[3] * (int)bsv.w;
+                            ia[p] = acc_i;
+                            im[p] = acc_m;
+                        }
+                    } else {
+                        const uint32_t so = (uint32_t)(((uintptr_t)(wb + (size_t)(wave + 4 * i) * 16 * B)) & 15u) + 210 * s;
+                        const uint32_t hh = c >> 1, bb = c & 1;
+                        uint32_t A[4], Bq[4], H[4], S[4];
+                        lds16_u2(st, so + 64 * hh + 16 * bb, A);
+                        lds16_u2(st, so + 64 * hh + 32 + 16 * bb, Bq);
+                        lds16_u2(st, so + 128 + 32 * hh + 16 * bb, H);
+                        lds16_u2(st, so + 192, S);
+                        const uint32_t dw = *(const uint32_t *)(st + ((so + 208) & ~3u));
+                        tag = ((so + 208) & 2u) ? (dw >> 16) : (dw & 0xFFFFu);
+                        const uint32_t sd0 = hh ? S[2] : S[0], sd1 = hh ? S[3] : S[1];
+                        const int sc[4] = {(int)(int8_t)(sd0 >> (8 * bb)), (int)(int8_t)(sd0 >> (8 * bb + 16)),
+                                           (int)(int8_t)(sd1 >> (8 * bb)), (int)(int8_t)(sd1 >> (8 * bb + 16))};
+                        int g6[4][4];
+#pragma unroll
+                        for (int k = 0; k < 4; ++k) {
+                            g6[0][k] = (int)((A[k] & 0x0F0F0F0Fu) | ((H[k] & 0x03030303u) << 4));
+                            g6[1][k] = (int)((Bq[k] & 0x0F0F0F0Fu) | ((H[k] << 2) & 0x30303030u));
+                            g6[2][k] = (int)(((A[k] >> 4) & 0x0F0F0F0Fu) | (H[k] & 0x30303030u));
+                            g6[3][k] = (int)(((Bq[k] >> 4) & 0x0F0F0F0Fu) | ((H[k] >> 2) & 0x30303030u));
+                        }
+#pragma unroll
+                        for (int p = 0; p < NX; ++p) {
+                            const uint8_t * xp = xrec + (size_t)p * nsb * 4 * XREC;
+                            const u32x4a bsv = *(const u32x4a *)(xp + 64);
+                            const int b32[4] = {(int)bsv.x, (int)bsv.y, (int)bsv.z, (int)bsv.w};
+                            int acc_i = 0;
+#pragma unroll
+                            for (int g = 0; g < 4; ++g) {
+                                const u32x4a xv = *(const u32x4a *)(xp + 16 * g);
+                                int d = 0;
+                                d = dot4(g6[g][0], (int)xv.x, d);
+                                d = dot4(g6[g][1], (int)xv.y, d);
+                                d = dot4(g6[g][2], (int)xv.z, d);
+                                d = dot4(g6[g][3], (int)xv.w, d);
+                                acc_i += sc[g] * (d - b32[g]);
+                            }
+                            ia[p] = acc_i;
+                            im[p] = 0;
+                        }
+                    }
+                    // all reads of this stage are done before it is refilled
+                    WAIT_LGKM0();
+                    const uint32_t inext = i + D < nci ? i + D : nci - 1;
+                    ks_issue<FMT>(wb, wave + 4 * inext, nsbb, myst + j * WIN, lane);
+#pragma unroll
+                    for (int p = 0; p < NX; ++p) {
+                        int x1 = ia[p];
+                        x1 += qx1(x1); x1 += qx2(x1);
+                        if (act && c == 0 && p < (int)nx) TI[(rl * NX + p) * nsb + sb] = x1;
+                        if constexpr (FMT == FMT_Q4_K) {
+                            int m1 = im[p];
+                            m1 += qx1(m1); m1 += qx2(m1);
+                            if (act && c == 0 && p < (int)nx) TM[(rl * NX + p) * nsb + sb] = m1;
+                        }
+                    }
+                    if (act && c == 0) TH[rl * nsb + sb] = tag;
+                }
+            }
+        }
+        WAIT_VM(0);
+        __syncthreads();
+        {
+            const uint32_t k = fk, p = fp, rl = frl;
+            float acc = 0.f;
+            if (fok) {
+                const int * ti = TI + (rl * NX + p) * nsb;
+                const int * tm = TM + (rl * NX + p) * nsb;
+                const uint32_t * th = TH + rl * nsb;
+                const float * xdp = xd + p * nsb;
+                for (uint32_t sbi = k; sbi < nsb; sbi += 4) {
+                    const float dk = xdp[sbi];
+                    if constexpr (FMT == FMT_Q4_K) {
+                        const float d = h2f(th[sbi] & 0xFFFFu), dmin = h2f(th[sbi] >> 16);
+                        acc = fmaf(d * dk, (float)ti[sbi], acc);
+                        acc = fmaf(-(dmin * dk), (float)tm[sbi], acc);
+                    } else {
+                        acc = fmaf(h2f(th[sbi]) * dk, (float)ti[sbi], acc);
+                    }
+                }
+            }
+            const float s01 = acc + qx1f(acc);
+            const float r = s01 + qx2f(s01);
+            if (fok && k == 0) a.y[(size_t)p * a.ystride + row0 + rl] = yold + r;
+        }
+        __syncthreads();
+    }
+}
+
+// ----------------------------------------------------------------- launch --
+struct KsTune { uint32_t wgs_per_cu, nr, D; };
+static KsTune ks_tune() {
+    static KsTune t = [] {
+        KsTune d{2, 0, 0};
+        if (const char * e = getenv("FLH_KS_TUNE")) {
+            unsigned x = 0, y = 0, z = 0;
+            if (sscanf(e, "%u,%u,%u", &x, &y, &z) == 3) d = KsTune{x, y, z};
+        }
+        return d;
+    }();
+    return t;
+}
+
+static size_t g_lds_limit = 0;
+size_t lds_limit() {
+    if (!g_lds_limit) {
+        int dev = 0;
+        (void)hipGetDevice(&dev);
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || v <= 0)
+            v = 65536;
+        g_lds_limit = (size_t)v;
+    }
+    return g_lds_limit;
+}
+
+template <int FMT, int NX, int D>
+static int ks_launch_d(const DotArgs & a, uint32_t nr, uint32_t grid, size_t smb, hipStream_t s) {
+    if (smb > 65536)
+        (void)hipFuncSetAttribute((const void *)k_dot_kstream<FMT, NX, D>,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)smb);
+    hipLaunchKernelGGL((k_dot_kstream<FMT, NX, D>), dim3(grid), dim3(256), smb, s, a, nr);
+    return hip_check(hipGetLastError(), "k_dot_kstream launch");
+}
+
+// Returns FLH_ERR_UNSUPPORTED (without launching) when the shape does not fit
+// this kernel's LDS plan; the caller then uses the register-resident kernel.
+template <int FMT, int NX>
+static int ks_launch(const DotArgs & a, hipStream_t s) {
+    const uint32_t nsb = a.cols >> 8;
+    const KsTune t = ks_tune();
+    const uint32_t wpc = t.wgs_per_cu ? t.wgs_per_cu : 2;
+    const uint32_t slots = (uint32_t)num_cus() * wpc;
+    uint32_t nr = t.nr ? t.nr : (a.rows + slots - 1) / slots;
+    if (nr < 1) nr = 1;
+    if (nr > 64u / NX) nr = 64u / NX;
+    int D = t.D ? (int)t.D : (FMT == FMT_Q4_K ? 4 : 3);
+    const size_t lim = lds_limit() / wpc > 65536 ? lds_limit() / wpc : 65536;
+    while (ks_smem_bytes<FMT>(nr, NX, nsb, D) > lim && nr > 1) nr >>= 1;
+    while (ks_smem_bytes<FMT>(nr, NX, nsb, D) > lim && D > 2) --D;
+    const size_t smb = ks_smem_bytes<FMT>(nr, NX, nsb, D);
+    if (smb > lds_limit()) return FLH_ERR_UNSUPPORTED;
+    const uint32_t nbatch = (a.rows + nr - 1) / nr;
+    const uint32_t grid = nbatch < slots ? nbatch : slots;
+    switch (D) {
+        case 2: return ks_launch_d<FMT, NX, 2>(a, nr, grid, smb, s);
+        case 3: return ks_launch_d<FMT, NX, 3>(a, nr, grid, smb, s);
+        default: return ks_launch_d<FMT, NX, 4>(a, nr, grid, smb, s);
+    }
+}
+
+int launch_dot_kstream(int fmt, const DotArgs & a, hipStream_t s) {
+    const uint32_t nsb = a.cols >> 8;
+    if (nsb == 0 || (a.cols & 255) || nsb > 64 || a.nx > 4) return FLH_ERR_UNSUPPORTED;
+    if ((uintptr_t)a.w & 15 || (a.estride & 15)) return FLH_ERR_UNSUPPORTED;
+    if (getenv("FLH_NO_KSTREAM")) return FLH_ERR_UNSUPPORTED;
+    if (fmt == FMT_Q4_K)
+        return a.nx == 1 ? ks_launch<FMT_Q4_K, 1>(a, s) : a.nx == 2 ? ks_launch<FMT_Q4_K, 2>(a, s)
+                                                                   : ks_launch<FMT_Q4_K, 4>(a, s);
+    if (fmt == FMT_Q6_K)
+        return a.nx == 1 ? ks_launch<FMT_Q6_K, 1>(a, s) : a.nx == 2 ? ks_launch<FMT_Q6_K, 2>(a, s)
+                                                                   : ks_launch<FMT_Q6_K, 4>(a, s);
+    return FLH_ERR_UNSUPPORTED;
+}
+
+}  // namespace flh

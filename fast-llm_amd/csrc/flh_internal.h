@@ -40,6 +40,9 @@ int num_cus();
 int launch_act_q8(float * x, void * y_q81, uint32_t cols, uint32_t nx,
                   uint32_t xstride, hipStream_t s);
 int launch_dot_i8k(int fmt, const DotArgs & a, hipStream_t s);    // Q4_K, Q6_K x q8_K
+// LDS-staged variant; FLH_ERR_UNSUPPORTED (nothing launched) if the shape
+// does not fit its plan
+int launch_dot_kstream(int fmt, const DotArgs & a, hipStream_t s);
 int launch_dot_i8_q8_0(const DotArgs & a, hipStream_t s);         // Q8_0 x q8_1
 int launch_dot_i8_k(int fmt, const DotArgs & a, hipStream_t s);   // Q4_K, Q6_K x q8_1
 int launch_dot_canonical(int fmt, const DotArgs & a, hipStream_t s);
