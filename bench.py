@@ -141,10 +141,10 @@ def main():
         y.zero(s)
 
     def issue_layer(l):
+        # ACT_Q8 + STREAM_DOT per matrix (one fused launch each, same bytes)
         for name, r, c in LAYER:
             x, st = xin[name]
-            flh.act_q8(x, c, s)
-            flh.stream_dot(Q4_K, W[name][l], r, c, x, yout[name], s)
+            flh.act_q8_stream_dot(Q4_K, W[name][l], r, c, x, yout[name], s)
 
     graphs = []
     for l in range(L):

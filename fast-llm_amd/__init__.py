@@ -153,6 +153,8 @@ _SIGS = {
     "flh_act_q8": (_I, [_P, _P, _U32, _U32, _U32, _P]),
     "flh_stream_dot": (_I, [_I, _P, _U64, _U32, _U32, _P, _P, _U32, _U32, _U32, _P, _U64,
                             _I, _U32, _U32, _P]),
+    "flh_act_q8_stream_dot": (_I, [_I, _P, _U64, _U32, _U32, _P, _P, _U32, _U32, _U32, _P, _U64,
+                                   _I, _U32, _U32, _P]),
     "flh_exec_tasks": (_I, [_P, _U32, _I, _U32, _U32, _P]),
     "flh_dequant": (_I, [_I, _P, _U32, _U32, _P, _P]),
     "flh_moe_dot": (_I, [_I, _P, _U64, _U32, _U32, _P, _U32, _U32, _U32, _P, _U32, _U32, _P,
@@ -337,6 +339,17 @@ def stream_dot(fmt: int, w, rows: int, cols: int, x, y, stream: Stream, nx: int 
     check(lib().flh_stream_dot(int(fmt), _p(w), w_bytes, rows, cols, _p(x), _p(y), nx,
                                xstride, ystride, _p(id_slot), estride, int(bool(fast)),
                                i8_mask, i8k_mask, stream.handle))
+
+
+def act_q8_stream_dot(fmt: int, w, rows: int, cols: int, x, y, stream: Stream, nx: int = 1,
+                      xstride: int = 0, ystride: int = 0, id_slot=None, estride: int = 0,
+                      fast: bool = True, i8_mask: int = I8_MASK_DEFAULT,
+                      i8k_mask: int = I8K_MASK_DEFAULT) -> None:
+    """ACT_Q8 + STREAM_DOT on the same activation (fused where possible)."""
+    w_bytes = rows * row_bytes(fmt, cols)
+    check(lib().flh_act_q8_stream_dot(int(fmt), _p(w), w_bytes, rows, cols, _p(x), _p(y), nx,
+                                      xstride, ystride, _p(id_slot), estride, int(bool(fast)),
+                                      i8_mask, i8k_mask, stream.handle))
 
 
 def exec_tasks(tasks, stream: Stream, fast: bool = True, i8_mask: int = I8_MASK_DEFAULT,

@@ -210,7 +210,7 @@ int flh_graph_capture_end(void * stream, void ** graph_exec) {
     if (int rc = hip_check(hipStreamEndCapture((hipStream_t)stream, &g), "hipStreamEndCapture")) return rc;
     hipGraphExec_t ge = nullptr;
     const int rc = hip_check(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0), "hipGraphInstantiate");
-    hipGraphDestroy(g);
+    (void)hipGraphDestroy(g);
     if (rc) return rc;
     *graph_exec = (void *)ge;
     return FLH_OK;
@@ -241,6 +241,27 @@ int flh_stream_dot(int fmt, const void * w, uint64_t w_bytes, uint32_t rows, uin
     if (int rc = need_init()) return rc;
     DotArgs a{(const uint8_t *)w, id_slot, estride, x, y, rows, cols, nx, xstride, ystride};
     return dispatch_dot(fmt, a, fast, i8_mask, i8k_mask, (hipStream_t)stream);
+}
+
+int flh_act_q8_stream_dot(int fmt, const void * w, uint64_t w_bytes, uint32_t rows, uint32_t cols,
+                          float * x, float * y, uint32_t nx, uint32_t xstride, uint32_t ystride,
+                          const uint32_t * id_slot, uint64_t estride, int fast, uint32_t i8_mask,
+                          uint32_t i8k_mask, void * stream) {
+    if (nx == 0) nx = 1;
+    if (int rc = validate_dot(fmt, w, w_bytes, rows, cols, x, y, nx, id_slot, estride)) return rc;
+    if (((uintptr_t)x & 15) || (nx > 1 && (xstride & 3)))
+        return set_error(FLH_ERR_ARG, "act_q8: x must be 16-byte aligned, xstride a multiple of 4");
+    if (int rc = need_init()) return rc;
+    hipStream_t s = (hipStream_t)stream;
+    DotArgs a{(const uint8_t *)w, id_slot, estride, x, y, rows, cols, nx, xstride, ystride};
+    // Fused when every workgroup re-reading the fp32 column is cheaper than a
+    // separate ACT_Q8 launch: up to 8192 columns (32 KiB of fp32 per column).
+    if (fast && cols <= 8192 && (fmt == FLH_FMT_Q4_K || fmt == FLH_FMT_Q6_K) && ((i8k_mask >> fmt) & 1u)) {
+        const int rc = launch_act_dot_kstream(fmt, a, s);
+        if (rc != FLH_ERR_UNSUPPORTED) return rc;
+    }
+    if (int rc = launch_act_q8(x, nullptr, cols, nx, xstride, s)) return rc;
+    return dispatch_dot(fmt, a, fast, i8_mask, i8k_mask, s);
 }
 
 int flh_dequant(int fmt, const void * w, uint32_t rows, uint32_t cols, float * out, void * stream) {
@@ -301,9 +322,26 @@ int flh_exec_tasks(const flh_task * t, uint32_t n, int fast, uint32_t i8_mask, u
                 rc = dispatch_dot(k.fmt, a, fast, i8_mask, i8k_mask, s);
                 break;
             }
-            case FLH_TASK_ACT_Q8:
+            case FLH_TASK_ACT_Q8: {
+                // ACT_Q8 whose next task is a single-column q8_K dot of the
+                // same activation: one fused launch (same appendix bytes,
+                // same outputs).
+                const flh_task * q = i + 1 < n ? &t[i + 1] : nullptr;
+                const bool canon_y = (const uint8_t *)k.y == (const uint8_t *)k.x + xq_off(k.cols);
+                if (q && canon_y && fast && k.cols <= 8192 && q->kind == FLH_TASK_STREAM_DOT && q->x == k.x &&
+                    q->cols == k.cols && (q->nx ? q->nx : 1u) == 1 &&
+                    (q->fmt == FLH_FMT_Q4_K || q->fmt == FLH_FMT_Q6_K) && ((i8k_mask >> q->fmt) & 1u)) {
+                    DotArgs a{(const uint8_t *)q->w, nullptr, 0, (const float *)q->x, (float *)q->y,
+                              q->rows, q->cols, 1u, q->xstride, q->ystride};
+                    rc = launch_act_dot_kstream(q->fmt, a, s);
+                    if (rc != FLH_ERR_UNSUPPORTED) {
+                        ++i;
+                        break;
+                    }
+                }
                 rc = launch_act_q8((float *)k.x, k.y, k.cols, 1, 0, s);
                 break;
+            }
             case FLH_TASK_MERGE:
                 rc = launch_merge((const float *)k.x, (float *)k.y, k.rows, k.cols, s);
                 break;

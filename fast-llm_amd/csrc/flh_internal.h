@@ -43,6 +43,10 @@ int launch_dot_i8k(int fmt, const DotArgs & a, hipStream_t s);    // Q4_K, Q6_K 
 // LDS-staged variant; FLH_ERR_UNSUPPORTED (nothing launched) if the shape
 // does not fit its plan
 int launch_dot_kstream(int fmt, const DotArgs & a, hipStream_t s);
+// ACT_Q8 fused into the kstream dot: quantises x (fp32) in-kernel, writes both
+// appendices (workgroup 0), then streams; same bytes and results as
+// launch_act_q8 followed by launch_dot_kstream
+int launch_act_dot_kstream(int fmt, const DotArgs & a, hipStream_t s);
 int launch_dot_i8_q8_0(const DotArgs & a, hipStream_t s);         // Q8_0 x q8_1
 int launch_dot_i8_k(int fmt, const DotArgs & a, hipStream_t s);   // Q4_K, Q6_K x q8_1
 int launch_dot_canonical(int fmt, const DotArgs & a, hipStream_t s);

@@ -186,6 +186,19 @@ int flh_stream_dot(int fmt, const void * w, uint64_t w_bytes, uint32_t rows,
                    uint64_t estride, int fast, uint32_t i8_mask,
                    uint32_t i8k_mask, void * stream);
 
+/* ACT_Q8 immediately followed by its STREAM_DOT consumer (the pair every
+ * int8 tile of the reference graph builder emits, src/model/decoder.cpp:
+ * 874-880,899-906), fused into one launch when the tile takes the q8_K path:
+ * the kernel quantises x itself, workgroup 0 still writes both appendices,
+ * and every output bit equals flh_act_q8 followed by flh_stream_dot (which is
+ * what runs for any other format / mode).  No reference counterpart: the
+ * reference always runs the two tasks separately. */
+int flh_act_q8_stream_dot(int fmt, const void * w, uint64_t w_bytes, uint32_t rows,
+                          uint32_t cols, float * x, float * y, uint32_t nx,
+                          uint32_t xstride, uint32_t ystride,
+                          const uint32_t * id_slot, uint64_t estride, int fast,
+                          uint32_t i8_mask, uint32_t i8k_mask, void * stream);
+
 /* Execute a task table in array order on one stream (replaces the persistent
  * executor's per-task dispatch, exec_task_block, src/runtime/gpu_exec.cu:
  * 64-140, for a topologically ordered table such as run_serial walks,
@@ -193,7 +206,9 @@ int flh_stream_dot(int fmt, const void * w, uint64_t w_bytes, uint32_t rows,
  * STREAM_DOT_IDX, ACT_Q8, MERGE, SIGNAL, ROUTER_SEL, SILU_MUL, WMERGE;
  * anything else -> FLH_ERR_UNSUPPORTED before any launch.  Consecutive
  * STREAM_DOT row tiles of one matrix (same fmt/cols/x/nx/strides, w and y
- * contiguous) are fused into one launch; results are unchanged. */
+ * contiguous) are fused into one launch, and an ACT_Q8 followed by its
+ * single-column q8_K consumer runs as flh_act_q8_stream_dot; results are
+ * unchanged. */
 int flh_exec_tasks(const flh_task * tasks, uint32_t n, int fast,
                    uint32_t i8_mask, uint32_t i8k_mask, void * stream);
 

@@ -284,3 +284,31 @@ def dequant_activation(orc, x, fmt):
     d = blk[:, 0:4].copy().view(np.float32).astype(np.float64)
     q = blk[:, 36:].view(np.int8).astype(np.float64)
     return (d * q).ravel()
+
+
+# ------------------------------------------------ fused ACT_Q8 + STREAM_DOT --
+@pytest.mark.parametrize("fmt", [Q4_K, Q6_K])
+@pytest.mark.parametrize("rows,cols,nx", [(37, 1024, 1), (300, 4096, 1), (64, 14336, 1),
+                                          (33, 2816, 3), (20, 4096, 4), (1, 256, 2)])
+def test_fused_act_q8_dot_bitwise(flh, orc, gpu, fmt, rows, cols, nx):
+    """flh_act_q8_stream_dot == ACT_Q8 then STREAM_DOT: same appendix bytes
+    in memory, bitwise-equal outputs (vs the oracle)."""
+    say("fused act+dot", fmt, rows, cols, nx)
+    rng = np.random.default_rng(rows + cols + nx + fmt)
+    w = sane_rows(fmt, rows, cols, rng)
+    xs = activations(nx, cols, rng, outliers=True)
+    st = col_stride_floats(cols)
+    dx, _ = dev_cols(flh, gpu, xs, st)
+    y0 = rng.standard_normal((nx - 1) * rows + rows).astype(np.float32)
+    dy = flh.DeviceBuffer.from_array(y0, gpu)
+    dw = flh.DeviceBuffer.from_array(w, gpu)
+    flh.act_q8_stream_dot(fmt, dw, rows, cols, dx, dy, gpu, nx=nx, xstride=st, ystride=rows)
+    got = dy.download(np.float32, y0.size, gpu)
+    xq = dx.download(np.float32, nx * st, gpu)
+    ref_x = orc.act_q8_cols(xs, st)
+    for p in range(nx):
+        n = x_alloc_bytes(cols) // 4
+        assert np.array_equal(xq[p * st:p * st + n].view(np.uint8), ref_x[p * st:p * st + n].view(np.uint8))
+    want = y0.copy()
+    orc.stream_dot(fmt, w, rows, cols, ref_x, want, nx=nx, xstride=st, ystride=rows, threads=8)
+    assert np.array_equal(bits(got), bits(want))
