@@ -134,19 +134,36 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// Columns of one kstream pass: x_p / y_p base pointers (p < nx <= NX).
+template <int NX>
+struct KsCols {
+    const float * x[NX];
+    float * y[NX];
+};
+// runtime column select without dynamic register indexing
+template <int NX, typename T>
+__device__ __forceinline__ T col_pick(T const (&v)[NX], uint32_t p) {
+    T r = v[0];
+#pragma unroll
+    for (int i = 1; i < NX; ++i) r = p == (uint32_t)i ? v[i] : r;
+    return r;
+}
+
+// One pass over rows [0, rows) of the matrix at w for nx <= NX columns; the
+// workgroup owns batches batch0, batch0 + G, ...  Ends with every weight DMA
+// drained, so the caller may start another pass on the same LDS.
 template <int FMT, int NX, int D, bool FUSE, bool XREG>
-__global__ __launch_bounds__(256) void k_dot_kstream(DotArgs a, uint32_t nr) {
-    extern __shared__ __attribute__((aligned(16))) uint8_t sm[];
+__device__ __forceinline__ void ks_body(const uint8_t * __restrict__ w, uint32_t rows, uint32_t cols,
+                                        const KsCols<NX> & C, uint32_t nx, uint32_t nr,
+                                        uint32_t batch0, uint32_t G, uint8_t * sm) {
     constexpr uint32_t B = KS<FMT>::BLK, WIN = KS<FMT>::WIN;
     constexpr int NI = KS<FMT>::NI;
-    const uint32_t nsb = a.cols >> 8, nx = a.nx;
+    const uint32_t nsb = cols >> 8;
     const uint64_t rb = (uint64_t)nsb * B;
-    const uint8_t * w = a.w + (a.id_slot ? (size_t)(*a.id_slot) * a.estride : 0);
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     // wave-uniform: keeps the chunk cursor and batch logic on the scalar unit
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t s = lane >> 2, c = lane & 3;
-    const uint32_t G = gridDim.x;
 
     uint8_t * stages = sm;                                        // [4][D][WIN]
     uint8_t * xr = sm + (size_t)4 * D * WIN;                      // [NX][nsb][4][80]
@@ -156,9 +173,9 @@ __global__ __launch_bounds__(256) void k_dot_kstream(DotArgs a, uint32_t nr) {
     uint32_t * TH = (uint32_t *)(FMT == FMT_Q4_K ? TM + (size_t)nr * NX * nsb : TM);   // [nr][nsb]
     uint8_t * myst = stages + (size_t)wave * D * WIN;
 
-    const uint32_t nbatch = (a.rows + nr - 1) / nr;
+    const uint32_t nbatch = (rows + nr - 1) / nr;
     auto nci_of = [&](uint32_t bt) -> uint32_t {                  // this wave's chunks in batch bt
-        const uint32_t nrow = min(nr, a.rows - bt * nr);
+        const uint32_t nrow = min(nr, rows - bt * nr);
         const uint32_t nch = (nrow * nsb + 15) / 16;
         return nch > wave ? (nch - wave + 3) / 4 : 0;
     };
@@ -166,7 +183,7 @@ __global__ __launch_bounds__(256) void k_dot_kstream(DotArgs a, uint32_t nr) {
     // Every call issues exactly NI loads (a repeat of the last real chunk once
     // the sequence is exhausted), so the count of loads behind any chunk is
     // always NI * (D - 1).
-    uint32_t qbt = blockIdx.x, qci = 0, qn = qbt < nbatch ? nci_of(qbt) : 0;
+    uint32_t qbt = batch0, qci = 0, qn = qbt < nbatch ? nci_of(qbt) : 0;
     const uint8_t * l_wb = w;            // a wave without chunks re-reads row 0 (valid, unused)
     uint32_t l_ch = 0, l_nsbb = nsb;
     auto issue_one = [&](uint8_t * stage) {
@@ -178,7 +195,7 @@ __global__ __launch_bounds__(256) void k_dot_kstream(DotArgs a, uint32_t nr) {
         if (qbt < nbatch) {
             l_wb = w + (size_t)qbt * nr * rb;
             l_ch = wave + 4 * qci;
-            l_nsbb = min(nr, a.rows - qbt * nr) * nsb;
+            l_nsbb = min(nr, rows - qbt * nr) * nsb;
             ++qci;
         }
         ks_issue<FMT>(l_wb, l_ch, l_nsbb, stage, lane);
@@ -208,7 +225,7 @@ __global__ __launch_bounds__(256) void k_dot_kstream(DotArgs a, uint32_t nr) {
             for (int q = 0; q < 4; ++q) {
                 const uint32_t i = base + 16 * q + 4 * wave + sub;
                 const uint32_t ii = i < nitem ? i : 0;
-                const float * src = a.x + (size_t)(ii / nsb) * a.xstride + 256 * (ii % nsb) + 16 * run;
+                const float * src = col_pick<NX>(C.x, ii / nsb) + 256 * (ii % nsb) + 16 * run;
 #pragma unroll
                 for (int k = 0; k < 4; ++k) raw[q][k] = *(const u32x4a *)(src + 4 * k);
             }
@@ -257,9 +274,9 @@ __global__ __launch_bounds__(256) void k_dot_kstream(DotArgs a, uint32_t nr) {
                     *(u32x4a *)(rec + 16 * kk) = u32x4a{pk[0], pk[1], pk[2], pk[3]};
                     *(int *)(rec + 64 + 4 * kk) = FMT == FMT_Q4_K ? sum : 32 * sum;
                     if (run == 0) xd[p * nsb + sb] = d;
-                    if (blockIdx.x == 0) {
-                        float * xc = (float *)(a.x + (size_t)p * a.xstride);
-                        uint8_t * q8k = (uint8_t *)xc + xqk_off(a.cols) + (size_t)sb * 292;
+                    if (batch0 == 0) {
+                        float * xc = (float *)col_pick<NX>(C.x, p);
+                        uint8_t * q8k = (uint8_t *)xc + xqk_off(cols) + (size_t)sb * 292;
                         uint32_t * dst = (uint32_t *)(q8k + 36 + 16 * run);
 #pragma unroll
                         for (int k = 0; k < 4; ++k) dst[k] = pk[k];
@@ -290,7 +307,7 @@ __global__ __launch_bounds__(256) void k_dot_kstream(DotArgs a, uint32_t nr) {
                             }
                         }
                         s1 += __shfl_xor(s1, 1);
-                        uint8_t * q81 = (uint8_t *)xc + xq_off(a.cols) + (size_t)(sb * 8 + (run >> 1)) * 36;
+                        uint8_t * q81 = (uint8_t *)xc + xq_off(cols) + (size_t)(sb * 8 + (run >> 1)) * 36;
                         uint32_t * d1p = (uint32_t *)(q81 + 4 + 16 * (run & 1));
 #pragma unroll
                         for (int k = 0; k < 4; ++k) d1p[k] = pk1[k];
@@ -309,7 +326,7 @@ __global__ __launch_bounds__(256) void k_dot_kstream(DotArgs a, uint32_t nr) {
         const uint32_t i = tid < NX * nsb * 4 ? tid : 0;
         const uint32_t p = i / (nsb * 4), rem = i % (nsb * 4), sb = rem >> 2, cc = rem & 3;
         const uint32_t pp = p < nx ? p : 0;
-        const uint8_t * xb = (const uint8_t *)(a.x + (size_t)pp * a.xstride) + xqk_off(a.cols) + (size_t)sb * 292;
+        const uint8_t * xb = (const uint8_t *)col_pick<NX>(C.x, pp) + xqk_off(cols) + (size_t)sb * 292;
         u32x4 v[4];
         int bs[4];
         float dk;
@@ -345,7 +362,7 @@ __global__ __launch_bounds__(256) void k_dot_kstream(DotArgs a, uint32_t nr) {
         for (uint32_t i = tid; i < NX * nsb * 4; i += 256) {
             const uint32_t p = i / (nsb * 4), rem = i % (nsb * 4), sb = rem >> 2, cc = rem & 3;
             const uint32_t pp = p < nx ? p : 0;
-            const uint8_t * xb = (const uint8_t *)(a.x + (size_t)pp * a.xstride) + xqk_off(a.cols) + (size_t)sb * 292;
+            const uint8_t * xb = (const uint8_t *)col_pick<NX>(C.x, pp) + xqk_off(cols) + (size_t)sb * 292;
             uint32_t * rec = (uint32_t *)(xr + (size_t)i * XREC);
             int bs[4];
             if constexpr (FMT == FMT_Q4_K) {
@@ -388,14 +405,15 @@ __global__ __launch_bounds__(256) void k_dot_kstream(DotArgs a, uint32_t nr) {
     const uint32_t fk = tid & 3, fp = (tid >> 2) % NX, frl = tid / (4 * NX);
     uint32_t slot = 0;                                            // ring stage of the next chunk
 
-    for (uint32_t bt = blockIdx.x; bt < nbatch; bt += G) {
+    for (uint32_t bt = batch0; bt < nbatch; bt += G) {
         const uint32_t row0 = bt * nr;
-        const uint32_t nrow = min(nr, a.rows - row0);
+        const uint32_t nrow = min(nr, rows - row0);
         const uint32_t nsbb = nrow * nsb;                       // superblocks in this batch
         const uint32_t nci = nci_of(bt);
         const uint8_t * wb = w + (size_t)row0 * rb;
         const bool fok = frl < nrow && fp < nx;
-        const float yold = a.y[(size_t)fp * a.ystride + row0 + (frl < nrow ? frl : nrow - 1)];
+        float * const ycol = col_pick<NX>(C.y, fp);
+        const float yold = ycol[row0 + (frl < nrow ? frl : nrow - 1)];
         for (uint32_t i = 0; i < nci; ++i) {
             // NI * (D - 1) loads were issued after this chunk's
             WAIT_VM(NI * (D - 1));
@@ -533,12 +551,60 @@ __global__ __launch_bounds__(256) void k_dot_kstream(DotArgs a, uint32_t nr) {
             }
             const float s01 = acc + qx1f(acc);
             const float r = s01 + qx2f(s01);
-            if (fok && k == 0) a.y[(size_t)p * a.ystride + row0 + rl] = yold + r;
+            if (fok && k == 0) ycol[row0 + rl] = yold + r;
         }
         __syncthreads();
     }
     // the trailing repeat loads still target this workgroup's LDS: drain them
     WAIT_VM(0);
+}
+
+template <int FMT, int NX, int D, bool FUSE, bool XREG>
+__global__ __launch_bounds__(256) void k_dot_kstream(DotArgs a, uint32_t nr) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t sm[];
+    const uint8_t * w = a.w + (a.id_slot ? (size_t)(*a.id_slot) * a.estride : 0);
+    KsCols<NX> C;
+#pragma unroll
+    for (int p = 0; p < NX; ++p) {
+        const uint32_t pp = p < (int)a.nx ? p : 0;
+        C.x[p] = a.x + (size_t)pp * a.xstride;
+        C.y[p] = a.y + (size_t)pp * a.ystride;
+    }
+    ks_body<FMT, NX, D, FUSE, XREG>(w, a.rows, a.cols, C, a.nx, nr, blockIdx.x, gridDim.x, sm);
+}
+
+// Grouped expert matvec: blockIdx.y = expert.  The workgroup collects the
+// routed (token, slot) pairs of its expert and streams that expert's weights
+// once per group of NX pairs; with no pair routed to it, it exits before any
+// weight byte is requested.
+template <int FMT, int NX, int D, bool XREG>
+__global__ __launch_bounds__(256) void k_moe_kstream(MoeArgs a, uint32_t nr) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t sm[];
+    __shared__ uint32_t pairs[256];
+    __shared__ uint32_t npairs;
+    const uint32_t e = blockIdx.y;
+    if (threadIdx.x == 0) {
+        uint32_t n = 0;
+        for (uint32_t i = 0; i < a.ntok * a.top_k && n < 256; ++i)
+            if (a.ids[i] == e) pairs[n++] = i;                    // i = tok * top_k + slot
+        npairs = n;
+    }
+    __syncthreads();
+    const uint32_t np = npairs;
+    const uint8_t * w = a.w + (size_t)e * a.estride;
+    for (uint32_t p0 = 0; p0 < np; p0 += NX) {
+        const uint32_t nx = min((uint32_t)NX, np - p0);
+        KsCols<NX> C;
+#pragma unroll
+        for (int p = 0; p < NX; ++p) {
+            const uint32_t ts = pairs[p0 + ((uint32_t)p < nx ? p : 0)];
+            const uint32_t xi = a.x_per_slot ? ts : ts / a.top_k;
+            C.x[p] = a.x + (size_t)xi * a.xstride;
+            C.y[p] = a.y + (size_t)ts * a.ystride;
+        }
+        ks_body<FMT, NX, D, false, XREG>(w, a.rows, a.cols, C, nx, nr, blockIdx.x, gridDim.x, sm);
+        __syncthreads();
+    }
 }
 
 // ----------------------------------------------------------------- launch --
@@ -585,21 +651,33 @@ static int ks_launch_d(const DotArgs & a, uint32_t nr, uint32_t grid, size_t smb
 
 // Returns FLH_ERR_UNSUPPORTED (without launching) when the shape does not fit
 // this kernel's LDS plan; the caller then uses the register-resident kernel.
+// LDS plan: at most 64 KiB per workgroup (two workgroups per CU); shrink the
+// batch first, then the ring depth; FLH_ERR_UNSUPPORTED if it cannot fit.
+template <int FMT>
+static int ks_plan(uint32_t rows, uint32_t nx_t, uint32_t nsb, uint32_t slots, int Ddef,
+                   uint32_t & nr, int & D, size_t & smb) {
+    const KsTune t = ks_tune();
+    nr = t.nr ? t.nr : (rows + slots - 1) / slots;
+    if (nr < 1) nr = 1;
+    if (nr > 64u / nx_t) nr = 64u / nx_t;
+    D = t.D ? (int)t.D : Ddef;
+    const size_t lim = lds_limit() < 65536 ? lds_limit() : 65536;
+    while (ks_smem_bytes<FMT>(nr, nx_t, nsb, D) > lim && nr > 4) nr >>= 1;
+    while (ks_smem_bytes<FMT>(nr, nx_t, nsb, D) > lim && D > 2) --D;
+    while (ks_smem_bytes<FMT>(nr, nx_t, nsb, D) > lim && nr > 1) nr >>= 1;
+    smb = ks_smem_bytes<FMT>(nr, nx_t, nsb, D);
+    return smb > lim ? FLH_ERR_UNSUPPORTED : FLH_OK;
+}
+
 template <int FMT, int NX, bool FUSE>
 static int ks_launch(const DotArgs & a, hipStream_t s) {
     const uint32_t nsb = a.cols >> 8;
     const KsTune t = ks_tune();
-    const uint32_t wpc = t.wgs_per_cu ? t.wgs_per_cu : 2;
-    const uint32_t slots = (uint32_t)num_cus() * wpc;
-    uint32_t nr = t.nr ? t.nr : (a.rows + slots - 1) / slots;
-    if (nr < 1) nr = 1;
-    if (nr > 64u / NX) nr = 64u / NX;
-    int D = t.D ? (int)t.D : (FMT == FMT_Q4_K ? 4 : 3);
-    const size_t lim = lds_limit() / wpc > 65536 ? lds_limit() / wpc : 65536;
-    while (ks_smem_bytes<FMT>(nr, NX, nsb, D) > lim && nr > 1) nr >>= 1;
-    while (ks_smem_bytes<FMT>(nr, NX, nsb, D) > lim && D > 2) --D;
-    const size_t smb = ks_smem_bytes<FMT>(nr, NX, nsb, D);
-    if (smb > lds_limit()) return FLH_ERR_UNSUPPORTED;
+    const uint32_t slots = (uint32_t)num_cus() * (t.wgs_per_cu ? t.wgs_per_cu : 2);
+    uint32_t nr;
+    int D;
+    size_t smb;
+    if (ks_plan<FMT>(a.rows, NX, nsb, slots, FMT == FMT_Q4_K ? 4 : 3, nr, D, smb)) return FLH_ERR_UNSUPPORTED;
     const uint32_t nbatch = (a.rows + nr - 1) / nr;
     const uint32_t grid = nbatch < slots ? nbatch : slots;
     switch (D) {
@@ -607,6 +685,57 @@ static int ks_launch(const DotArgs & a, hipStream_t s) {
         case 3: return ks_launch_d<FMT, NX, 3, FUSE>(a, nr, grid, smb, s);
         default: return ks_launch_d<FMT, NX, 4, FUSE>(a, nr, grid, smb, s);
     }
+}
+
+template <int FMT, int NX, int D, bool XREG>
+static int moe_launch_x(const MoeArgs & a, uint32_t nr, uint32_t gx, size_t smb, hipStream_t s) {
+    hipLaunchKernelGGL((k_moe_kstream<FMT, NX, D, XREG>), dim3(gx, a.n_expert), dim3(256), smb, s, a, nr);
+    return hip_check(hipGetLastError(), "k_moe_kstream launch");
+}
+template <int FMT, int NX, int D>
+static int moe_launch_d(const MoeArgs & a, uint32_t nr, uint32_t gx, size_t smb, hipStream_t s) {
+    const uint32_t nsb = a.cols >> 8;
+    if (16 % nsb == 0) return moe_launch_x<FMT, NX, D, true>(a, nr, gx, smb, s);
+    return moe_launch_x<FMT, NX, D, false>(a, nr, gx, smb, s);
+}
+template <int FMT, int NX>
+static int moe_launch(const MoeArgs & a, hipStream_t s) {
+    const uint32_t nsb = a.cols >> 8;
+    // experts that can be active at once share the chip
+    const uint32_t pairs = a.ntok * a.top_k;
+    const uint32_t active = pairs < a.n_expert ? pairs : a.n_expert;
+    const uint32_t gx = ((uint32_t)num_cus() * 2 + active - 1) / active;
+    uint32_t nr;
+    int D;
+    size_t smb;
+    if (ks_plan<FMT>(a.rows, NX, nsb, gx, FMT == FMT_Q4_K ? 4 : 3, nr, D, smb)) return FLH_ERR_UNSUPPORTED;
+    const uint32_t nbatch = (a.rows + nr - 1) / nr;
+    const uint32_t g = nbatch < gx ? nbatch : gx;
+    switch (D) {
+        case 2: return moe_launch_d<FMT, NX, 2>(a, nr, g, smb, s);
+        case 3: return moe_launch_d<FMT, NX, 3>(a, nr, g, smb, s);
+        default: return moe_launch_d<FMT, NX, 4>(a, nr, g, smb, s);
+    }
+}
+
+int launch_moe_kstream(int fmt, const MoeArgs & a, hipStream_t s) {
+    const uint32_t nsb = a.cols >> 8;
+    if (nsb == 0 || (a.cols & 255) || nsb > 64) return FLH_ERR_UNSUPPORTED;
+    if ((uintptr_t)a.w & 15 || (a.estride & 15) || getenv("FLH_NO_KSTREAM")) return FLH_ERR_UNSUPPORTED;
+    // columns per pass: the most pairs one expert can get, capped by what fits
+    const uint32_t pairs = a.ntok * a.top_k;
+    const uint32_t want = pairs < a.ntok ? pairs : a.ntok;     // an expert appears once per token
+    int rc = FLH_ERR_UNSUPPORTED;
+    if (fmt == FMT_Q4_K) {
+        if (want >= 4) rc = moe_launch<FMT_Q4_K, 4>(a, s);
+        if (rc == FLH_ERR_UNSUPPORTED && want >= 2) rc = moe_launch<FMT_Q4_K, 2>(a, s);
+        if (rc == FLH_ERR_UNSUPPORTED) rc = moe_launch<FMT_Q4_K, 1>(a, s);
+    } else if (fmt == FMT_Q6_K) {
+        if (want >= 4) rc = moe_launch<FMT_Q6_K, 4>(a, s);
+        if (rc == FLH_ERR_UNSUPPORTED && want >= 2) rc = moe_launch<FMT_Q6_K, 2>(a, s);
+        if (rc == FLH_ERR_UNSUPPORTED) rc = moe_launch<FMT_Q6_K, 1>(a, s);
+    }
+    return rc;
 }
 
 template <bool FUSE>

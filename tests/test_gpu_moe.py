@@ -1,0 +1,170 @@
+"""MoE decode path on the GPU: grouped expert matvec, router, silu*up, merge.
+
+The grouped kernel must reproduce, bit for bit, the per-(token, slot)
+STREAM_DOT_IDX tiles the reference emits (src/model/decoder.cpp:941-996),
+checked against the oracle.  The decode ops that call expf (router softmax,
+silu) use the device libm, so they are compared within float tolerance; the
+whole FFN layer is held to the north-star bar (1e-3 of max |y|).
+"""
+import numpy as np
+import pytest
+
+from oracle import Q4_K, Q6_K, col_stride_floats, row_bytes
+from util import sane_rows, activations
+
+pytestmark = pytest.mark.gpu
+
+
+def bits(a):
+    return np.ascontiguousarray(a).view(np.uint32)
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+
+
+def route(orc, ntok, E, K, rng):
+    logits = rng.standard_normal((ntok, E)).astype(np.float32)
+    ids = np.zeros((ntok, K), dtype=np.uint32)
+    gates = np.zeros((ntok, K), dtype=np.float32)
+    for t in range(ntok):
+        ids[t], gates[t] = orc.router_sel(logits[t], K, norm=1)
+    return logits, ids, gates
+
+
+@pytest.mark.parametrize("fmt", [Q4_K, Q6_K])
+@pytest.mark.parametrize("ntok,rows,cols,per_slot", [(1, 300, 1024, False), (3, 64, 2816, False),
+                                                     (8, 257, 4096, False), (8, 96, 2048, True),
+                                                     (5, 40, 14336, True)])
+def test_grouped_expert_dot_bitwise(flh, orc, gpu, fmt, ntok, rows, cols, per_slot):
+    say("moe_dot", fmt, ntok, rows, cols, per_slot)
+    rng = np.random.default_rng(ntok * 31 + rows + cols + fmt)
+    E, K = 8, 2
+    _, ids, _ = route(orc, ntok, E, K, rng)
+    rb = row_bytes(fmt, cols)
+    estride = rows * rb
+    w = sane_rows(fmt, rows * E, cols, rng)
+    nx = ntok * K if per_slot else ntok
+    xs = activations(nx, cols, rng, outliers=True)
+    st = col_stride_floats(cols)
+    buf = np.zeros(nx * st, dtype=np.float32)
+    for p in range(nx):
+        buf[p * st:p * st + cols] = xs[p]
+    dx = flh.DeviceBuffer.from_array(buf, gpu)
+    flh.act_q8(dx, cols, gpu, nx=nx, xstride=st)
+    ref_x = orc.act_q8_cols(xs, st)
+    y0 = rng.standard_normal(ntok * K * rows).astype(np.float32)
+    dy = flh.DeviceBuffer.from_array(y0, gpu)
+    dw = flh.DeviceBuffer.from_array(w, gpu)
+    di = flh.DeviceBuffer.from_array(ids.ravel(), gpu)
+    flh.moe_dot(fmt, dw, estride, rows, cols, di, ntok, K, E, dx, st, per_slot, dy, rows, gpu)
+    got = dy.download(np.float32, y0.size, gpu)
+    want = y0.copy()
+    for t in range(ntok):
+        for k in range(K):
+            i = t * K + k
+            xi = i if per_slot else t
+            yi = want[i * rows:(i + 1) * rows]
+            orc.stream_dot(fmt, w, rows, cols, ref_x[xi * st:(xi + 1) * st], yi,
+                           id_slot=int(ids[t, k]), estride=estride)
+            want[i * rows:(i + 1) * rows] = yi
+    assert np.array_equal(bits(got), bits(want))
+
+
+def test_router_matches_reference_order(flh, orc, gpu, golden):
+    """Top-k ids equal the reference's (ties -> lower id); gates to float tolerance."""
+    say("router")
+    for name, K, norm in (("router_kat_in", 3, 0), ("router_kat_in", 3, 1)):
+        lg = golden[name]
+        d_l = flh.DeviceBuffer.from_array(lg, gpu)
+        d_i = flh.DeviceBuffer(4 * K)
+        d_g = flh.DeviceBuffer(4 * K)
+        flh.router_sel(d_l, 1, lg.size, K, norm, 1.0, d_i, d_g, gpu)
+        ids = d_i.download(np.uint32, K, gpu)
+        g = d_g.download(np.float32, K, gpu)
+        assert list(ids) == list(golden[f"router_kat_ids_{norm}"])
+        assert np.allclose(g, golden[f"router_kat_gates_{norm}"], rtol=2e-6, atol=0)
+    lg = golden["router_in"]
+    d_l = flh.DeviceBuffer.from_array(lg, gpu)
+    d_i = flh.DeviceBuffer(4 * 2 * lg.shape[0])
+    d_g = flh.DeviceBuffer(4 * 2 * lg.shape[0])
+    flh.router_sel(d_l, lg.shape[0], 8, 2, 1, 1.0, d_i, d_g, gpu)
+    assert np.array_equal(d_i.download(np.uint32, 2 * lg.shape[0], gpu).reshape(-1, 2), golden["router_ids"])
+    assert np.allclose(d_g.download(np.float32, 2 * lg.shape[0], gpu).reshape(-1, 2),
+                       golden["router_gates"], rtol=2e-6, atol=0)
+
+
+def test_silu_mul_and_wmerge(flh, gpu, golden):
+    say("silu/wmerge")
+    g, u = golden["silu_g"], golden["silu_u"]
+    dg, du = flh.DeviceBuffer.from_array(g, gpu), flh.DeviceBuffer.from_array(u, gpu)
+    dh = flh.DeviceBuffer(g.nbytes)
+    flh.silu_mul(dg, du, dh, g.size, 1, 0, 0, gpu)
+    h = dh.download(np.float32, g.size, gpu)
+    assert np.allclose(h, golden["silu_h"], rtol=4e-7, atol=1e-30)
+    parts, gates, add1 = golden["wm_parts"], golden["wm_gates"], golden["wm_add1"]
+    dp = flh.DeviceBuffer.from_array(parts, gpu)
+    dgt = flh.DeviceBuffer.from_array(gates, gpu)
+    da = flh.DeviceBuffer.from_array(add1, gpu)
+    dy = flh.DeviceBuffer(add1.nbytes)
+    flh.wmerge(dp, dgt, da, None, dy, 1.0, 2, add1.size, 0, 1, 0, 0, gpu)
+    assert np.array_equal(bits(dy.download(np.float32, add1.size, gpu)), bits(golden["wm_y"]))
+
+
+@pytest.mark.parametrize("ntok", [1, 8])
+def test_moe_ffn_layer_end_to_end(flh, orc, gpu, ntok):
+    """router -> grouped gate/up -> silu*up -> ACT_Q8 -> grouped down ->
+    weighted merge + residual, against the oracle's per-token reference
+    sequence (decoder.cpp:941-1040), within 1e-3 of max |y|."""
+    say("moe ffn", ntok)
+    rng = np.random.default_rng(ntok)
+    E, K, D, F = 8, 2, 1024, 2048
+    logits, ids_ref, gates_ref = route(orc, ntok, E, K, rng)
+    wgu = flh.quantize_host(Q4_K, (rng.standard_normal((E * 2 * F, D)) * 0.02).astype(np.float32))
+    wdn = flh.quantize_host(Q4_K, (rng.standard_normal((E * D, F)) * 0.02).astype(np.float32))
+    gu_stride, dn_stride = 2 * F * row_bytes(Q4_K, D), D * row_bytes(Q4_K, F)
+    xs = activations(ntok, D, rng)
+    resid = rng.standard_normal((ntok, D)).astype(np.float32)
+    stD, stF = col_stride_floats(D), col_stride_floats(F)
+    # ---- device
+    xb = np.zeros(ntok * stD, dtype=np.float32)
+    for t in range(ntok):
+        xb[t * stD:t * stD + D] = xs[t]
+    dx = flh.DeviceBuffer.from_array(xb, gpu)
+    dlg = flh.DeviceBuffer.from_array(logits, gpu)
+    dids, dgat = flh.DeviceBuffer(4 * ntok * K), flh.DeviceBuffer(4 * ntok * K)
+    dgu_w, ddn_w = flh.DeviceBuffer.from_array(wgu, gpu), flh.DeviceBuffer.from_array(wdn, gpu)
+    ygu = flh.DeviceBuffer(4 * ntok * K * 2 * F)
+    ygu.zero(gpu)
+    h = flh.DeviceBuffer(4 * ntok * K * stF)
+    h.zero(gpu)
+    ydn = flh.DeviceBuffer(4 * ntok * K * D)
+    ydn.zero(gpu)
+    dres = flh.DeviceBuffer.from_array(resid, gpu)
+    yo = flh.DeviceBuffer(4 * ntok * D)
+    flh.act_q8(dx, D, gpu, nx=ntok, xstride=stD)
+    flh.router_sel(dlg, ntok, E, K, 1, 1.0, dids, dgat, gpu)
+    flh.moe_dot(Q4_K, dgu_w, gu_stride, 2 * F, D, dids, ntok, K, E, dx, stD, False, ygu, 2 * F, gpu)
+    flh.silu_mul(ygu, ygu.ptr + 4 * F, h, F, ntok * K, 2 * F, stF, gpu)
+    flh.act_q8(h, F, gpu, nx=ntok * K, xstride=stF)
+    flh.moe_dot(Q4_K, ddn_w, dn_stride, D, F, dids, ntok, K, E, h, stF, True, ydn, D, gpu)
+    flh.wmerge(ydn, dgat, dres, None, yo, 1.0, K, D, 0, ntok, K * D, D, gpu)
+    got = yo.download(np.float32, ntok * D, gpu).reshape(ntok, D)
+    assert np.array_equal(dids.download(np.uint32, ntok * K, gpu).reshape(ntok, K), ids_ref)
+    # ---- oracle, per token and slot as the reference graph runs it
+    want = np.zeros((ntok, D), dtype=np.float32)
+    for t in range(ntok):
+        xq = orc.act_q8_cols(xs[t:t + 1], stD)
+        parts = np.zeros((K, D), dtype=np.float32)
+        for k in range(K):
+            e = int(ids_ref[t, k])
+            yg = np.zeros(2 * F, dtype=np.float32)
+            orc.stream_dot(Q4_K, wgu, 2 * F, D, xq, yg, id_slot=e, estride=gu_stride)
+            hh = orc.silu_mul(yg[:F], yg[F:])
+            hq = orc.act_q8_cols(hh[None, :], stF)
+            yd = np.zeros(D, dtype=np.float32)
+            orc.stream_dot(Q4_K, wdn, D, F, hq, yd, id_slot=e, estride=dn_stride)
+            parts[k] = yd
+        want[t] = orc.wmerge(parts, gates_ref[t], add1=resid[t])
+    err = np.max(np.abs(got - want))
+    assert err <= 1e-3 * np.max(np.abs(want)), err
