@@ -115,6 +115,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-ops", action="store_true", help="headline only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--profile", action="store_true",
+                    help="counter-collection run: a 256 MiB device copy (calibration) and "
+                         "64 launches of the dominant kernel only, no JSON line")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the matvec shards by rows; "
@@ -128,6 +131,10 @@ def main():
     s = flh.Stream()
     B = Bench(flh, s)
     staging = B.buf(256 << 20)
+
+    if args.profile:
+        profile_run(flh, B, s, staging)
+        return
 
     # ------------------------------------------------ headline: layer step
     layer_bytes = sum(flh.row_bytes(Q4_K, c) * r for _, r, c in LAYER)
@@ -204,7 +211,8 @@ def main():
     result["roofline"] = {"bound": "hbm", "achieved": round(alg / gu["us"] / 1e3, 1),
                           "peak": HBM_PEAK_GBS, "unit": "GB/s",
                           "frac": round(alg / gu["us"] / 1e3 / HBM_PEAK_GBS, 4),
-                          "traffic": None, "kernel": "k_dot_i8k<Q4_K,1> gate/up 28672x4096",
+                          "traffic": traffic_from_profile(),
+                          "kernel": "k_dot_kstream<Q4_K> gate/up 28672x4096",
                           "alg_bytes_per_launch": alg, "us_per_launch": gu["us"]}
 
     if not args.no_ops:
@@ -246,6 +254,37 @@ def main():
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(flh, s, W, xin)
     print(json.dumps(result), flush=True)
+
+
+def profile_run(flh, B, s, staging):
+    """What the committed counter profiles were collected on: 5 device copies
+    of 256 MiB (known HBM bytes: read 256 MiB + write 256 MiB each) and 64
+    launches of the Q4_K gate/up matvec rotating over its weight copies."""
+    n = 256 << 20
+    src, dst = B.buf(n), B.buf(n)
+    src.zero(s)
+    for _ in range(5):
+        flh.copy(dst, src, n, s)
+    s.sync()
+    r, c = 28672, 4096
+    nb = r * flh.row_bytes(Q4_K, c)
+    ws = B.weights(Q4_K, r, c, copies_for(nb), seed=101 + r + 7 * c, staging=staging)
+    x, st = B.activation(c, 1, 12, outliers=True)
+    y = B.buf(r * 4)
+    for i in range(64):
+        flh.stream_dot(Q4_K, ws[i % len(ws)], r, c, x, y, s)
+    s.sync()
+
+
+def traffic_from_profile():
+    """HBM bytes per launch of the dominant kernel, from the committed
+    rocprofv3 --pmc summary (profiles/pmc_q4_K_gate_up_28672x4096.json)."""
+    f = os.path.join(ROOT, "profiles", "pmc_q4_K_gate_up_28672x4096.json")
+    try:
+        with open(f) as fh:
+            return json.load(fh).get("traffic_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
 
 
 def bench_moe(flh, B, s, staging):

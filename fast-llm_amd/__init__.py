@@ -139,6 +139,7 @@ _SIGS = {
     "flh_upload": (_I, [_P, _P, _SZ, _P]),
     "flh_download": (_I, [_P, _P, _SZ, _P]),
     "flh_zero": (_I, [_P, _SZ, _P]),
+    "flh_copy": (_I, [_P, _P, _SZ, _P]),
     "flh_stream_create": (_I, [C.POINTER(_P)]),
     "flh_stream_sync": (_I, [_P]),
     "flh_stream_destroy": (_I, [_P]),
@@ -324,6 +325,10 @@ class DeviceBuffer:
 
 
 # ---------------------------------------------------------------- ops --
+def copy(dst, src, n: int, stream: Stream) -> None:
+    check(lib().flh_copy(_p(dst), _p(src), n, stream.handle))
+
+
 def act_q8(x, cols: int, stream: Stream, nx: int = 1, xstride: int = 0, y_q81=None) -> None:
     """ACT_Q8 (fl_exec_act_q8, src/runtime/quants.h:404-416) on nx columns."""
     check(lib().flh_act_q8(_p(x), _p(y_q81), cols, nx, xstride, stream.handle))

@@ -174,6 +174,9 @@ int flh_download(void * dst, const void * src, size_t n, void * stream) {
     if (int rc = hip_check(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, (hipStream_t)stream), "download")) return rc;
     return hip_check(hipStreamSynchronize((hipStream_t)stream), "download sync");
 }
+int flh_copy(void * dst, const void * src, size_t n, void * stream) {
+    return hip_check(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToDevice, (hipStream_t)stream), "copy");
+}
 int flh_zero(void * dst, size_t n, void * stream) { return launch_zero(dst, n, (hipStream_t)stream); }
 
 // --------------------------------------------------------------- streams --

@@ -136,6 +136,8 @@ int flh_malloc(size_t bytes, void ** out);
 int flh_free(void * p);
 int flh_upload(void * dst_dev, const void * src_host, size_t n, void * stream);
 int flh_download(void * dst_host, const void * src_dev, size_t n, void * stream);
+/* device-to-device copy of n bytes on a stream (asynchronous) */
+int flh_copy(void * dst_dev, const void * src_dev, size_t n, void * stream);
 /* zero n bytes with a fill kernel (safe inside HIP graph capture) */
 int flh_zero(void * dst_dev, size_t n, void * stream);
 

@@ -1,0 +1,320 @@
+"""Pins the C oracle with checks that do not use the reference's code.
+
+The golden vectors (test_oracle_golden.py) pin the oracle to the reference's
+own outputs; these tests pin it to what the mathematics and the format
+definitions fix, each written independently of fl_oracle.c (numpy,
+vectorised, exact rational arithmetic), chosen so that a dropped term, a
+wrong shift / index or a swapped operand fails:
+  * half2float: all 65536 halves vs numpy float16;
+  * float2half: the reference KATs (tests/test_runtime.cpp:540-544) and
+    numpy's round-to-nearest-even on random floats;
+  * dequant: per-element transcription of the block layouts;
+  * ACT_Q8: bsums = per-16 sums, d = amax/127, round-half-away quantisation;
+  * int8 dots: integer partials from numpy int64, the reference fold order
+    replayed with exactly-rounded fmaf (Fractions);
+  * error budgets vs an f64 dot (tests/test_runtime.cpp:547-587, 687-723).
+"""
+from fractions import Fraction
+
+import numpy as np
+import pytest
+
+from oracle import Q8_0, Q4_K, Q6_K, row_bytes, xq_offset, xqk_offset
+from util import sane_rows
+
+
+# ------------------------------------------------------------- fp16 --
+def test_half2float_exhaustive(orc):
+    h = np.arange(65536, dtype=np.uint16)
+    want = h.view(np.float16).astype(np.float32)
+    got = np.array([orc.half2float(int(v)) for v in h], dtype=np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+def test_float2half_kats_and_rne(orc):
+    assert orc.float2half(1.0) == 0x3C00
+    assert orc.float2half(-2.0) == 0xC000
+    assert orc.float2half(65504.0) == 0x7BFF
+    assert orc.float2half(1e30) == 0x7C00
+    assert orc.float2half(5.96046448e-8) == 0x0001
+    rng = np.random.default_rng(1)
+    f = np.concatenate([(rng.standard_normal(20000) * 10.0 ** rng.integers(-9, 6, 20000)).astype(np.float32),
+                        rng.integers(0, 1 << 32, 20000, dtype=np.uint64).astype(np.uint32).view(np.float32)])
+    f = f[~np.isnan(f)]
+    with np.errstate(over="ignore"):
+        want = f.astype(np.float16).view(np.uint16)
+    got = np.array([orc.float2half(float(v)) for v in f], dtype=np.uint16)
+    assert np.array_equal(got, want)
+
+
+# ----------------------------------------------------------- dequant --
+def h16(b):
+    return b.copy().view(np.float16).astype(np.float32)
+
+
+def deq_reference_numpy(fmt, w, rows, cols):
+    """Vectorised per-element decode of the block layouts (quants.h:23-26)."""
+    if fmt == Q8_0:
+        B = w.reshape(rows * cols // 32, 34)
+        d = h16(B[:, 0:2])[:, 0]
+        q = B[:, 2:].view(np.int8).astype(np.float32)
+        return (d[:, None] * q).reshape(rows, cols)
+    if fmt == Q4_K:
+        B = w.reshape(rows * cols // 256, 144)
+        d, dmin = h16(B[:, 0:2])[:, 0], h16(B[:, 2:4])[:, 0]
+        s = B[:, 4:16].astype(np.uint32)
+        sc = np.empty((len(B), 8), np.uint32)
+        mn = np.empty((len(B), 8), np.uint32)
+        sc[:, :4], mn[:, :4] = s[:, 0:4] & 63, s[:, 4:8] & 63
+        sc[:, 4:] = (s[:, 8:12] & 0xF) | ((s[:, 0:4] >> 6) << 4)
+        mn[:, 4:] = (s[:, 8:12] >> 4) | ((s[:, 4:8] >> 6) << 4)
+        qs = B[:, 16:].reshape(-1, 4, 32)
+        nib = np.empty((len(B), 8, 32), np.float32)
+        nib[:, 0::2] = (qs & 0xF).astype(np.float32)
+        nib[:, 1::2] = (qs >> 4).astype(np.float32)
+        d1 = d[:, None] * sc.astype(np.float32)
+        m1 = dmin[:, None] * mn.astype(np.float32)
+        return (d1[:, :, None] * nib - m1[:, :, None]).reshape(rows, cols)
+    B = w.reshape(rows * cols // 256, 210)
+    d = h16(B[:, 208:210])[:, 0]
+    out = np.empty((len(B), 256), np.float32)
+    for h in range(2):
+        ql = B[:, 64 * h:64 * h + 64].astype(np.int32)
+        qh = B[:, 128 + 32 * h:128 + 32 * h + 32].astype(np.int32)
+        sc = B[:, 192 + 8 * h:200 + 8 * h].view(np.int8).astype(np.float32)
+        for g in range(4):
+            lb = ql[:, 32 * (g & 1):32 * (g & 1) + 32]
+            lo = (lb & 0xF) if g < 2 else (lb >> 4)
+            q6 = lo | (((qh >> (2 * g)) & 3) << 4)
+            s16 = np.repeat(sc[:, 2 * g:2 * g + 2], 16, axis=1)
+            out[:, 128 * h + 32 * g:128 * h + 32 * g + 32] = (d[:, None] * s16) * (q6 - 32).astype(np.float32)
+    return out.reshape(rows, cols)
+
+
+@pytest.mark.parametrize("fmt", [Q8_0, Q4_K, Q6_K])
+def test_dequant_matches_format_definition(orc, fmt):
+    rng = np.random.default_rng(fmt)
+    rows, cols = 7, 1024
+    w = sane_rows(fmt, rows, cols, rng)
+    got = orc.dequant(fmt, w, rows, cols)
+    want = deq_reference_numpy(fmt, w, rows, cols)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_q4k_scale_unpack_every_byte(orc):
+    """Each of the 8 (scale, min) pairs as a function of the 12 bytes: set one
+    byte at a time to every value and compare with the closed form."""
+    import ctypes as C
+    for pos in range(12):
+        for v in range(256):
+            s = np.zeros(12, np.uint8)
+            s[pos] = v
+            for j in range(8):
+                d, m = C.c_uint8(), C.c_uint8()
+                orc.q4k_scale_min(j, s.ctypes.data, C.byref(d), C.byref(m))
+                if j < 4:
+                    ed, em = s[j] & 63, s[j + 4] & 63
+                else:
+                    ed = (s[j + 4] & 0xF) | ((s[j - 4] >> 6) << 4)
+                    em = (s[j + 4] >> 4) | ((s[j] >> 6) << 4)
+                assert (d.value, m.value) == (ed, em)
+
+
+# ------------------------------------------------------------ ACT_Q8 --
+def round_half_away(v):
+    v = np.asarray(v, dtype=np.float64)
+    return np.sign(v) * np.floor(np.abs(v) + 0.5)
+
+
+def test_act_q8_invariants(orc):
+    rng = np.random.default_rng(5)
+    cols = 1024
+    x = rng.standard_normal(cols).astype(np.float32)
+    x[rng.random(cols) < 0.02] *= 30
+    x[256:512] = 0.0                                # an all-zero superblock
+    buf = orc.act_q8(x)
+    k = buf[xqk_offset(cols):xqk_offset(cols) + (cols // 256) * 292].reshape(-1, 292)
+    for sb in range(cols // 256):
+        xs = x[256 * sb:256 * sb + 256]
+        amax = np.float32(np.max(np.abs(xs)))
+        d = k[sb, 0:4].copy().view(np.float32)[0]
+        assert d == np.float32(amax / np.float32(127))
+        idv = np.float32(127) / amax if amax > 0 else np.float32(0)
+        q = np.clip(round_half_away((xs * idv).astype(np.float32)), -127, 127).astype(np.int8)
+        assert np.array_equal(k[sb, 36:].view(np.int8), q)
+        bs = k[sb, 4:36].copy().view(np.int16)
+        assert np.array_equal(bs, q.astype(np.int32).reshape(16, 16).sum(axis=1))
+    blk = buf[xq_offset(cols):xq_offset(cols) + (cols // 32) * 36].reshape(-1, 36)
+    for b in range(cols // 32):
+        xs = x[32 * b:32 * b + 32]
+        amax = np.float32(np.max(np.abs(xs)))
+        d = np.float32(amax / np.float32(127))
+        assert blk[b, 0:2].copy().view(np.float16)[0] == np.float16(d)
+        q = blk[b, 4:].view(np.int8).astype(np.float32)
+        assert np.all(np.abs(d * q - xs) <= amax / 127 + 1e-4 * max(amax, 1))
+
+
+# ------------------------------------------------ exact fmaf fold replay --
+def f32_round(fr: Fraction) -> np.float32:
+    """Round an exact rational to the nearest float32, ties to even."""
+    if fr == 0:
+        return np.float32(0.0)
+    c = np.float32(float(fr))                       # within one ulp of the answer
+    best = None
+    for cand in (np.nextafter(c, np.float32(-np.inf)), c, np.nextafter(c, np.float32(np.inf))):
+        if not np.isfinite(cand):
+            continue
+        err = abs(Fraction(float(cand)) - fr)
+        key = (err, int(np.float32(cand).view(np.uint32)) & 1)
+        if best is None or key < best[0]:
+            best = (key, cand)
+    return np.float32(best[1])
+
+
+def fmaf(a, b, c):
+    return f32_round(Fraction(float(a)) * Fraction(float(b)) + Fraction(float(c)))
+
+
+def fold4(a):
+    s01 = np.float32(a[0] + a[1])
+    s23 = np.float32(a[2] + a[3])
+    return np.float32(s01 + s23)
+
+
+def i8k_q4k_replay(row, xk, cols):
+    """fl_dot_i8k_q4_K's contract (quants.h:528-561) restated from scratch."""
+    nsb = cols // 256
+    B = row.reshape(nsb, 144)
+    X = xk.reshape(nsb, 292)
+    s = B[:, 4:16].astype(np.int64)
+    sc = np.concatenate([s[:, 0:4] & 63, (s[:, 8:12] & 0xF) | ((s[:, 0:4] >> 6) << 4)], axis=1)
+    mn = np.concatenate([s[:, 4:8] & 63, (s[:, 8:12] >> 4) | ((s[:, 4:8] >> 6) << 4)], axis=1)
+    qs = B[:, 16:].reshape(nsb, 4, 32).astype(np.int64)
+    nib = np.empty((nsb, 8, 32), np.int64)
+    nib[:, 0::2], nib[:, 1::2] = qs & 0xF, qs >> 4
+    xq = X[:, 36:].view(np.int8).astype(np.int64).reshape(nsb, 8, 32)
+    bs = X[:, 4:36].copy().view(np.int16).astype(np.int64).reshape(nsb, 8, 2).sum(axis=2)
+    iacc = (sc * (nib * xq).sum(axis=2)).sum(axis=1)
+    imin = (mn * bs).sum(axis=1)
+    d, dmin = h16(B[:, 0:2])[:, 0], h16(B[:, 2:4])[:, 0]
+    dk = X[:, 0:4].copy().view(np.float32)[:, 0]
+    a = [np.float32(0)] * 4
+    for sb in range(nsb):
+        a[sb & 3] = fmaf(np.float32(d[sb] * dk[sb]), np.float32(iacc[sb]), a[sb & 3])
+        a[sb & 3] = fmaf(-np.float32(dmin[sb] * dk[sb]), np.float32(imin[sb]), a[sb & 3])
+    return fold4(a)
+
+
+def i8k_q6k_replay(row, xk, cols):
+    """fl_dot_i8k_q6_K's contract (quants.h:563-594) restated from scratch."""
+    nsb = cols // 256
+    B = row.reshape(nsb, 210)
+    X = xk.reshape(nsb, 292)
+    q6 = np.empty((nsb, 256), np.int64)
+    for h in range(2):
+        ql = B[:, 64 * h:64 * h + 64].astype(np.int64)
+        qh = B[:, 128 + 32 * h:160 + 32 * h].astype(np.int64)
+        for g in range(4):
+            lb = ql[:, 32 * (g & 1):32 * (g & 1) + 32]
+            q6[:, 128 * h + 32 * g:128 * h + 32 * g + 32] = ((lb & 0xF) if g < 2 else (lb >> 4)) | (((qh >> (2 * g)) & 3) << 4)
+    xq = X[:, 36:].view(np.int8).astype(np.int64)
+    idot = (q6 * xq).reshape(nsb, 16, 16).sum(axis=2)
+    bs = X[:, 4:36].copy().view(np.int16).astype(np.int64)
+    sc = B[:, 192:208].view(np.int8).astype(np.int64)
+    iacc = (sc * (idot - 32 * bs)).sum(axis=1)
+    d = h16(B[:, 208:210])[:, 0]
+    dk = X[:, 0:4].copy().view(np.float32)[:, 0]
+    a = [np.float32(0)] * 4
+    for sb in range(nsb):
+        a[sb & 3] = fmaf(np.float32(d[sb] * dk[sb]), np.float32(iacc[sb]), a[sb & 3])
+    return fold4(a)
+
+
+def i8_q80_replay(row, xq, cols):
+    """fl_dot_i8_q8_0's contract (quants.h:438-447) restated from scratch."""
+    nb = cols // 32
+    B = row.reshape(nb, 34)
+    X = xq.reshape(nb, 36)
+    idot = (B[:, 2:].view(np.int8).astype(np.int64) * X[:, 4:].view(np.int8).astype(np.int64)).sum(axis=1)
+    dd = h16(B[:, 0:2])[:, 0] * h16(X[:, 0:2])[:, 0]
+    a = [np.float32(0)] * 4
+    for b in range(nb):
+        a[b & 3] = fmaf(np.float32(dd[b]), np.float32(idot[b]), a[b & 3])
+    return fold4(a)
+
+
+@pytest.mark.parametrize("fmt,cols", [(Q4_K, 512), (Q4_K, 2816), (Q6_K, 1024), (Q6_K, 2304),
+                                      (Q8_0, 512), (Q8_0, 1056)])
+def test_int8_dot_replay_bitwise(orc, fmt, cols):
+    rng = np.random.default_rng(fmt * 7 + cols)
+    rows = 5
+    w = sane_rows(fmt, rows, cols, rng)
+    x = rng.uniform(-1, 1, cols).astype(np.float32)
+    x[rng.random(cols) < 0.01] *= 20
+    buf = orc.act_q8(x)
+    xk = buf[xqk_offset(cols):xqk_offset(cols) + (cols // 256) * 292]
+    xq = buf[xq_offset(cols):xq_offset(cols) + (cols // 32) * 36]
+    rb = row_bytes(fmt, cols)
+    for r in range(rows):
+        row = w[r * rb:(r + 1) * rb]
+        if fmt == Q4_K:
+            got, want = orc.dot_i8k_q4_K(row.ctypes.data, xk.ctypes.data, cols), i8k_q4k_replay(row, xk, cols)
+        elif fmt == Q6_K:
+            got, want = orc.dot_i8k_q6_K(row.ctypes.data, xk.ctypes.data, cols), i8k_q6k_replay(row, xk, cols)
+        else:
+            got, want = orc.dot_i8_q8_0(row.ctypes.data, xq.ctypes.data, cols), i8_q80_replay(row, xq, cols)
+        assert np.float32(got).view(np.uint32) == np.float32(want).view(np.uint32), (r, got, want)
+
+
+# ------------------------------------------------------- error budgets --
+@pytest.mark.parametrize("fmt,i8k,max_gate", [(Q4_K, True, 3e-2), (Q6_K, True, 3e-2),
+                                             (Q8_0, False, 2.5e-2), (Q4_K, False, 2.5e-2),
+                                             (Q6_K, False, 2.5e-2)])
+def test_int8_error_budget_vs_f64(orc, fmt, i8k, max_gate):
+    """The reference's own budgets: x ~ U(-1,1), cols 512, 200 trials, error
+    normalised by ||w .* x||_2 (tests/test_runtime.cpp:547-587, 687-723)."""
+    rng = np.random.default_rng(100 + fmt + 10 * i8k)
+    cols, trials = 512, 200
+    mx = mean = mcn = 0.0
+    for _ in range(trials):
+        w = sane_rows(fmt, 1, cols, rng)
+        x = rng.uniform(-1, 1, cols).astype(np.float32)
+        xb = orc.act_q8_cols(x[None, :])
+        deq = orc.dequant(fmt, w, 1, cols)[0].astype(np.float64)
+        prod = deq * x.astype(np.float64)
+        ref, S = prod.sum(), max(1e-6, np.sqrt((prod ** 2).sum()))
+        y = np.zeros(1, np.float32)
+        orc.stream_dot(fmt, w, 1, cols, xb, y, i8_mask=0b11110, i8k_mask=0b11000 if i8k else 0)
+        yc = np.zeros(1, np.float32)
+        orc.stream_dot(fmt, w, 1, cols, xb, yc, fast=False)
+        e = abs(float(y[0]) - ref) / S
+        mx, mean = max(mx, e), mean + e / trials
+        mcn = max(mcn, abs(float(yc[0]) - ref) / S)
+    assert mx < max_gate and mean < 6e-3 and mcn < 1e-5, (mx, mean, mcn)
+
+
+def test_multicolumn_equals_single_columns(orc):
+    """fastllm.h:87-93: an nx-column tile equals nx single tiles, bitwise."""
+    rng = np.random.default_rng(11)
+    for fmt, cols in ((Q4_K, 1024), (Q6_K, 1024), (Q8_0, 1024)):
+        rows, nx = 9, 5
+        w = sane_rows(fmt, rows, cols, rng)
+        xs = rng.uniform(-1, 1, (nx, cols)).astype(np.float32)
+        xb = orc.act_q8_cols(xs)
+        st = xb.size // nx
+        y = np.zeros(nx * rows, np.float32)
+        orc.stream_dot(fmt, w, rows, cols, xb, y, nx=nx, xstride=st, ystride=rows)
+        for p in range(nx):
+            y1 = np.zeros(rows, np.float32)
+            orc.stream_dot(fmt, w, rows, cols, xb[p * st:(p + 1) * st], y1)
+            assert np.array_equal(y[p * rows:(p + 1) * rows].view(np.uint32), y1.view(np.uint32))
+
+
+def test_router_ties_and_norm(orc):
+    ids, g = orc.router_sel(np.array([1.0, 3.0, 3.0, 0.5, 3.0], np.float32), 3, norm=1)
+    assert list(ids) == [1, 2, 4]
+    assert abs(float(g.sum()) - 1.0) < 1e-6
+    ids, g = orc.router_sel(np.array([0.0, 0.0, 0.0, 0.0], np.float32), 2, norm=0, scale=2.0)
+    assert list(ids) == [0, 1] and np.allclose(g, [0.5, 0.5])
