@@ -36,6 +36,12 @@ namespace flh {
 #define WAIT_VM(n) __builtin_amdgcn_s_waitcnt(((n) & 0xF) | (0x7 << 4) | (0xF << 8) | (((n) >> 4) << 14))
 #define WAIT_LGKM0() __builtin_amdgcn_s_waitcnt(0xC07F)
 
+// Cache-policy bits of the weight-streaming DMA (2 = nontemporal: the weights
+// are read once per launch and should not displace the activation in L2).
+#ifndef FLH_KS_AUX
+#define FLH_KS_AUX 2
+#endif
+
 template <int FMT> struct KS;
 template <> struct KS<FMT_Q4_K> {
     static constexpr uint32_t BLK = 144;
@@ -70,9 +76,9 @@ __device__ __forceinline__ void ks_issue(const uint8_t * wb, uint32_t ch, uint32
         const uint8_t * g = wb + (size_t)f0 * B;
         const uint32_t last16 = nact * B - 16, last4 = nact * B - 4;
         const uint32_t o0 = 16 * lane, o1 = 1024 + 16 * lane, o2 = 2048 + 4 * lane;
-        __builtin_amdgcn_global_load_lds(GPTR(g + (o0 <= last16 ? o0 : last16)), LPTR(stage), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds(GPTR(g + (o1 <= last16 ? o1 : last16)), LPTR(stage + 1024), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds(GPTR(g + (o2 <= last4 ? o2 : last4)), LPTR(stage + 2048), 4, 0, 0);
+        __builtin_amdgcn_global_load_lds(GPTR(g + (o0 <= last16 ? o0 : last16)), LPTR(stage), 16, 0, FLH_KS_AUX);
+        __builtin_amdgcn_global_load_lds(GPTR(g + (o1 <= last16 ? o1 : last16)), LPTR(stage + 1024), 16, 0, FLH_KS_AUX);
+        __builtin_amdgcn_global_load_lds(GPTR(g + (o2 <= last4 ? o2 : last4)), LPTR(stage + 2048), 4, 0, FLH_KS_AUX);
     } else {
         const uintptr_t gs = (uintptr_t)(wb + (size_t)f0 * B);
         const uint8_t * g = (const uint8_t *)(gs & ~(uintptr_t)15);
@@ -80,7 +86,7 @@ __device__ __forceinline__ void ks_issue(const uint8_t * wb, uint32_t ch, uint32
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const uint32_t o = 1024 * i + 16 * lane;
-            __builtin_amdgcn_global_load_lds(GPTR(g + (o <= last16 ? o : last16)), LPTR(stage + 1024 * i), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(GPTR(g + (o <= last16 ? o : last16)), LPTR(stage + 1024 * i), 16, 0, FLH_KS_AUX);
         }
     }
 }
