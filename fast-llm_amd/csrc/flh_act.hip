@@ -10,38 +10,11 @@
 // One wave per 256-element chunk of one column: lane i owns elements
 // 4i..4i+3 (one 16-B load, one packed dword store per appendix); 8-lane
 // groups form the q8_1 blocks, 4-lane groups the q8_K 16-sums.
-#include "flh_common.h"
+#include "flh_kstream.h"
 #include "flh_internal.h"
 #include "flh_status.h"
 
 namespace flh {
-
-__device__ __forceinline__ float wave_max8(float v) {      // within 8 lanes
-    v = fmaxf(v, __shfl_xor(v, 1));
-    v = fmaxf(v, __shfl_xor(v, 2));
-    v = fmaxf(v, __shfl_xor(v, 4));
-    return v;
-}
-__device__ __forceinline__ int isum8(int v) {
-    v += __shfl_xor(v, 1);
-    v += __shfl_xor(v, 2);
-    v += __shfl_xor(v, 4);
-    return v;
-}
-
-__device__ __forceinline__ uint32_t quant4(const float (&v)[4], float id, int & sum) {
-    uint32_t packed = 0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        float q = roundf(v[j] * id);
-        if (q > 127.f) q = 127.f;
-        if (q < -127.f) q = -127.f;
-        const int qi = (int)q;
-        sum += qi;
-        packed |= ((uint32_t)qi & 0xFFu) << (8 * j);
-    }
-    return packed;
-}
 
 __global__ __launch_bounds__(64) void k_act_q8(float * x, uint8_t * yq, uint32_t cols,
                                                uint32_t xstride) {
@@ -53,40 +26,7 @@ __global__ __launch_bounds__(64) void k_act_q8(float * x, uint8_t * yq, uint32_t
     float v[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) v[j] = (e0 + j < cols) ? xc[e0 + j] : 0.f;
-    float am = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-
-    // q8_1: block of 32 = 8 lanes
-    {
-        const uint32_t blk = chunk * 8 + (lane >> 3);
-        const float amax = wave_max8(am);
-        const float d = amax / 127.f;
-        const float id = amax > 0.f ? 127.f / amax : 0.f;
-        int s = 0;
-        const uint32_t pk = quant4(v, id, s);
-        const int sum = isum8(s);
-        if ((blk + 1) * 32 <= cols) {
-            uint8_t * o = q81 + (size_t)blk * 36;
-            *(uint32_t *)(o + 4 + 4 * (lane & 7)) = pk;
-            if ((lane & 7) == 0) *(uint32_t *)o = f2h(d) | (f2h(d * (float)sum) << 16);
-        }
-    }
-    // q8_K: whole chunk
-    if ((chunk + 1) * 256 <= cols) {
-        float amax = wave_max8(am);
-        amax = fmaxf(amax, __shfl_xor(amax, 8));
-        amax = fmaxf(amax, __shfl_xor(amax, 16));
-        amax = fmaxf(amax, __shfl_xor(amax, 32));
-        const float d = amax / 127.f;
-        const float id = amax > 0.f ? 127.f / amax : 0.f;
-        int s = 0;
-        const uint32_t pk = quant4(v, id, s);
-        s += __shfl_xor(s, 1);
-        s += __shfl_xor(s, 2);
-        uint8_t * o = q8k + (size_t)chunk * 292;
-        *(uint32_t *)(o + 36 + 4 * lane) = pk;
-        if ((lane & 3) == 0) *(int16_t *)(o + 4 + 2 * (lane >> 2)) = (int16_t)s;
-        if (lane == 0) *(float *)o = d;
-    }
+    act_q8_lanes(v, lane, chunk, q81, q8k, cols);
 }
 
 int launch_act_q8(float * x, void * y_q81, uint32_t cols, uint32_t nx,
