@@ -54,7 +54,7 @@ BLK_BYTES = {Fmt.F32: 4, Fmt.Q8_0: 34, Fmt.Q5_0: 22, Fmt.Q4_K: 144, Fmt.Q6_K: 21
              Fmt.IQ2_XXS: 66, Fmt.IQ3_XXS: 98}
 MAX_DOT_COLS = 16
 
-OK, ERR_ARG, ERR_HIP, ERR_UNSUPPORTED, ERR_NOMEM, ERR_STATE, ERR_TIMEOUT = 0, -1, -2, -3, -4, -5, -6
+OK, ERR_ARG, ERR_HIP, ERR_UNSUPPORTED, ERR_NOMEM, ERR_STATE = 0, -1, -2, -3, -4, -5
 
 # reference CPU default masks (src/runtime/kernels.h:920,937)
 I8_MASK_DEFAULT = (1 << Fmt.Q8_0) | (1 << Fmt.Q5_0) | (1 << Fmt.Q4_K) | (1 << Fmt.Q6_K)
@@ -157,11 +157,6 @@ _SIGS = {
     "flh_act_q8_stream_dot": (_I, [_I, _P, _U64, _U32, _U32, _P, _P, _U32, _U32, _U32, _P, _U64,
                                    _I, _U32, _U32, _P]),
     "flh_exec_tasks": (_I, [_P, _U32, _I, _U32, _U32, _P]),
-    "flh_plan_create": (_I, [_P, _U32, _I, _U32, _U32, C.POINTER(_P)]),
-    "flh_plan_launch": (_I, [_P, _P]),
-    "flh_plan_status": (_I, [_P]),
-    "flh_plan_info": (_I, [_P, C.POINTER(_U32), C.POINTER(_U32), C.POINTER(_U32), C.POINTER(_SZ)]),
-    "flh_plan_destroy": (_I, [_P]),
     "flh_dequant": (_I, [_I, _P, _U32, _U32, _P, _P]),
     "flh_moe_dot": (_I, [_I, _P, _U64, _U32, _U32, _P, _U32, _U32, _U32, _P, _U32, _U32, _P,
                          _U32, _P]),
@@ -368,42 +363,6 @@ def exec_tasks(tasks, stream: Stream, fast: bool = True, i8_mask: int = I8_MASK_
     arr = (Task * len(tasks))(*tasks)
     check(lib().flh_exec_tasks(C.cast(arr, C.c_void_p), len(tasks), int(bool(fast)),
                                i8_mask, i8k_mask, stream.handle))
-
-
-class Plan:
-    """A task table compiled for the persistent plan executor: every launch
-    runs the whole table in one kernel (results equal exec_tasks')."""
-
-    def __init__(self, tasks, fast: bool = True, i8_mask: int = I8_MASK_DEFAULT,
-                 i8k_mask: int = I8K_MASK_DEFAULT):
-        arr = (Task * len(tasks))(*tasks)
-        h = C.c_void_p()
-        check(lib().flh_plan_create(C.cast(arr, C.c_void_p), len(tasks), int(bool(fast)), i8_mask,
-                                    i8k_mask, C.byref(h)))
-        self.handle = h.value
-
-    def launch(self, stream: Stream) -> None:
-        check(lib().flh_plan_launch(self.handle, stream.handle))
-
-    def status(self) -> None:
-        """Raise FlhError(ERR_TIMEOUT) if a launch gave up waiting (synchronises)."""
-        check(lib().flh_plan_status(self.handle))
-
-    def info(self) -> dict:
-        a, b, g, l = C.c_uint32(), C.c_uint32(), C.c_uint32(), C.c_size_t()
-        check(lib().flh_plan_info(self.handle, C.byref(a), C.byref(b), C.byref(g), C.byref(l)))
-        return {"ops": a.value, "items": b.value, "grid": g.value, "lds_bytes": l.value}
-
-    def close(self):
-        if self.handle:
-            lib().flh_plan_destroy(self.handle)
-            self.handle = None
-
-    def __del__(self):
-        try:
-            self.close()
-        except Exception:
-            pass
 
 
 def dequant(fmt: int, w, rows: int, cols: int, out, stream: Stream) -> None:

@@ -6,9 +6,8 @@
 #include <string.h>
 #include <string>
 #include <mutex>
-#include <vector>
 #include "../../include/fastllm_hip.h"
-#include "flh_kstream.h"
+#include "flh_common.h"
 #include "flh_internal.h"
 #include "flh_status.h"
 
@@ -424,283 +423,6 @@ int flh_quantize(int fmt, const float * src, uint32_t rows, uint32_t cols, void 
 }
 int flh_quantize_host(int fmt, const float * src, uint32_t rows, uint32_t cols, void * dst) {
     return quantize_host(fmt, src, rows, cols, (uint8_t *)dst);
-}
-
-}  // extern "C"
-
-// ------------------------------------------------------------------ plans --
-// Compile a frozen task table into ops for the persistent plan executor
-// (flh_plan.hip): fuse a matrix's consecutive row tiles into one DOT op, an
-// ACT_Q8 into the q8_K dot that follows it on the same activation
-// (cols <= 8192, as flh_exec_tasks does), a SILU_MUL into the ACT_Q8 of its
-// output; derive each op's producer ops from the tasks' consumer lists
-// (Graph::add, src/runtime/graph.cpp:25-47; SIGNAL tasks pass their
-// producers on); then size items and LDS for two resident workgroups per CU.
-struct flh_plan {
-    int fmt;
-    PlanOp * d_ops;
-    uint32_t * d_ctl;
-    PlanArgs args;
-    uint32_t grid;
-    size_t smb;
-};
-
-extern "C" {
-
-int flh_plan_create(const flh_task * t, uint32_t n, int fast, uint32_t i8_mask, uint32_t i8k_mask,
-                    flh_plan ** out) {
-    (void)i8_mask;
-    if (!out) return set_error(FLH_ERR_ARG, "null output pointer");
-    *out = nullptr;
-    if (int rc = validate_table(t, n)) return rc;
-    if (int rc = need_init()) return rc;
-    if (n == 0) return set_error(FLH_ERR_ARG, "empty task table");
-    if (!fast) return set_error(FLH_ERR_UNSUPPORTED, "plans run the fast (q8_K int8) path only");
-    std::vector<PlanOp> ops;
-    std::vector<int> op_of(n, -1);
-    int fmt = -1;
-    auto unsup = [](const char * m) { return set_error(FLH_ERR_UNSUPPORTED, m); };
-    int64_t prev = -1;                           // previous non-SIGNAL task (relays may sit between tiles)
-    for (uint32_t i = 0; i < n; ++i) {
-        const flh_task & k = t[i];
-        switch (k.kind) {
-            case FLH_TASK_STREAM_DOT: {
-                if ((k.nx ? k.nx : 1u) != 1) return unsup("plan: multi-column dot tiles are not supported");
-                if (k.fmt != FLH_FMT_Q4_K && k.fmt != FLH_FMT_Q6_K) return unsup("plan: only Q4_K / Q6_K dot tiles");
-                if (!((i8k_mask >> k.fmt) & 1u)) return unsup("plan: dot format not on the q8_K path (i8k mask)");
-                if (fmt >= 0 && k.fmt != fmt) return unsup("plan: one weight format per plan");
-                fmt = k.fmt;
-                if ((k.cols & 255) || (k.cols >> 8) > 64 || k.rows == 0)
-                    return unsup("plan: cols must be a multiple of 256, at most 16384");
-                if (((uintptr_t)k.w & 15) || ((uintptr_t)k.x & 15))
-                    return unsup("plan: weights and activation must be 16-byte aligned");
-                PlanOp * last = ops.empty() ? nullptr : &ops.back();
-                const bool extend = last && prev >= 0 && op_of[prev] == (int)ops.size() - 1 &&
-                                    t[prev].kind == FLH_TASK_STREAM_DOT && last->kind == PLOP_DOT &&
-                                    last->cols == k.cols && (const void *)last->x == k.x &&
-                                    (const uint8_t *)k.w == last->w + (uint64_t)last->rows * flh_row_bytes(k.fmt, k.cols) &&
-                                    (float *)k.y == last->y + last->rows;
-                if (extend) {
-                    last->rows += k.rows;
-                } else if (last && prev >= 0 && op_of[prev] == (int)ops.size() - 1 && t[prev].kind == FLH_TASK_ACT_Q8 &&
-                           last->kind == PLOP_DOT && last->rows == 0) {
-                    // the op opened by the preceding ACT_Q8 (fused quantisation)
-                    last->w = (const uint8_t *)k.w;
-                    last->y = (float *)k.y;
-                    last->rows = k.rows;
-                    last->cols = k.cols;
-                } else {
-                    PlanOp o{};
-                    o.kind = PLOP_DOT;
-                    o.w = (const uint8_t *)k.w;
-                    o.x = (const float *)k.x;
-                    o.y = (float *)k.y;
-                    o.rows = k.rows;
-                    o.cols = k.cols;
-                    ops.push_back(o);
-                }
-                op_of[i] = (int)ops.size() - 1;
-                break;
-            }
-            case FLH_TASK_ACT_Q8: {
-                if ((k.cols & 255) || k.cols == 0) return unsup("plan: ACT_Q8 cols must be a multiple of 256");
-                if ((const uint8_t *)k.y != (const uint8_t *)k.x + xq_off(k.cols))
-                    return unsup("plan: ACT_Q8 must write the canonical appendix");
-                uint32_t nx_i = i + 1;                   // next real task
-                while (nx_i < n && t[nx_i].kind == FLH_TASK_SIGNAL) ++nx_i;
-                const flh_task * q = nx_i < n ? &t[nx_i] : nullptr;
-                if (q && k.cols <= 8192 && q->kind == FLH_TASK_STREAM_DOT && q->x == k.x && q->cols == k.cols &&
-                    (q->nx ? q->nx : 1u) == 1 && (q->fmt == FLH_FMT_Q4_K || q->fmt == FLH_FMT_Q6_K) &&
-                    ((i8k_mask >> q->fmt) & 1u)) {
-                    PlanOp o{};                  // filled in by the dot that follows
-                    o.kind = PLOP_DOT;
-                    o.flags = PLF_FUSE;
-                    o.x = (const float *)k.x;
-                    ops.push_back(o);
-                } else if (!ops.empty() && prev >= 0 && t[prev].kind == FLH_TASK_SILU_MUL &&
-                           op_of[prev] == (int)ops.size() - 1 && (ops.back().flags & PLF_NOQ) &&
-                           (const void *)ops.back().y == k.x && ops.back().cols == k.cols) {
-                    ops.back().flags &= ~PLF_NOQ;       // quantise the SILU_MUL output in place
-                } else {
-                    PlanOp o{};
-                    o.kind = PLOP_ACT;
-                    o.x = o.y = (float *)k.x;
-                    o.cols = k.cols;
-                    ops.push_back(o);
-                }
-                op_of[i] = (int)ops.size() - 1;
-                break;
-            }
-            case FLH_TASK_SILU_MUL: {
-                const flh_silu_mul_p & p = *(const flh_silu_mul_p *)k.aux;
-                if ((p.n & 255) || p.n == 0) return unsup("plan: SILU_MUL n must be a multiple of 256");
-                if ((uintptr_t)p.h & 15) return unsup("plan: SILU_MUL output must be 16-byte aligned");
-                PlanOp o{};
-                o.kind = PLOP_ACT;
-                o.flags = PLF_SILU | PLF_NOQ;
-                o.x = p.gate;
-                o.u = p.up;
-                o.y = p.h;
-                o.cols = p.n;
-                ops.push_back(o);
-                op_of[i] = (int)ops.size() - 1;
-                break;
-            }
-            case FLH_TASK_SIGNAL:
-                break;
-            default:
-                return unsup("plan: task kind not supported by the plan executor (use flh_exec_tasks)");
-        }
-        if (ops.size() > (size_t)PLAN_MAX_OPS) return unsup("plan: more than 32 ops");
-        if (k.kind != FLH_TASK_SIGNAL) prev = i;
-    }
-    if (fmt < 0) return unsup("plan: no dot tile");
-    for (const PlanOp & o : ops)
-        if (o.kind == PLOP_DOT && o.rows == 0) return unsup("plan: ACT_Q8 fused without its dot");
-    // producer sets from the consumer lists: a Kahn traversal (relay SIGNALs
-    // may follow their consumers in the array) carrying, per task, the ops
-    // it stands for (its own op, or a SIGNAL's producers)
-    bool edges = false;
-    std::vector<uint32_t> incoming(n, 0), indeg(n, 0), ready;
-    for (uint32_t i = 0; i < n; ++i) {
-        if (t[i].n_consumers > 6) return set_error(FLH_ERR_ARG, "n_consumers exceeds kMaxConsumers (6)");
-        for (uint32_t c = 0; c < t[i].n_consumers; ++c) {
-            const uint32_t u = t[i].consumers[c];
-            if (u >= n || u == i) return set_error(FLH_ERR_ARG, "bad consumer index");
-            ++indeg[u];
-            edges = true;
-        }
-    }
-    for (uint32_t i = 0; i < n; ++i)
-        if (!indeg[i]) ready.push_back(i);
-    for (size_t r = 0; r < ready.size(); ++r) {
-        const uint32_t i = ready[r];
-        const uint32_t carry = op_of[i] >= 0 ? (1u << op_of[i]) : incoming[i];
-        for (uint32_t c = 0; c < t[i].n_consumers; ++c) {
-            const uint32_t u = t[i].consumers[c];
-            incoming[u] |= carry;
-            if (--indeg[u] == 0) ready.push_back(u);
-        }
-    }
-    if (ready.size() != n) return set_error(FLH_ERR_ARG, "task graph has a cycle");
-    for (uint32_t i = 0; i < n; ++i)
-        if (op_of[i] >= 0) ops[op_of[i]].prod |= incoming[i] & ~(1u << op_of[i]);
-    if (!edges)
-        for (size_t k = 1; k < ops.size(); ++k) ops[k].prod = 1u << (k - 1);
-    for (size_t k = 0; k < ops.size(); ++k)
-        if (ops[k].prod >> k) return unsup("plan: an op depends on a later op (table order is not topological)");
-    // items and LDS: two resident workgroups per CU if the LDS plan allows,
-    // each op's rows dealt as ~one item per workgroup
-    const uint32_t cus = (uint32_t)num_cus();
-    size_t smb = 0, term_off = 0;
-    uint32_t G = 0;
-    for (uint32_t occ = 2;; --occ) {
-        G = occ * cus;
-        size_t xrec = 0, term = 0;
-        for (PlanOp & o : ops) {
-            if (o.kind != PLOP_DOT) continue;
-            const uint32_t nsb = o.cols >> 8;
-            uint32_t nr = (o.rows + G - 1) / G;
-            nr = nr < 1 ? 1 : nr > 64 ? 64 : nr;
-            o.nr = nr;
-            o.flags = (o.flags & PLF_FUSE) | ((16 % nsb == 0) ? PLF_XREG : 0u);
-            const size_t xb = fmt == FLH_FMT_Q4_K ? ks_xrec_bytes<FMT_Q4_K>(1, nsb) : ks_xrec_bytes<FMT_Q6_K>(1, nsb);
-            const size_t tb = fmt == FLH_FMT_Q4_K ? ks_term_bytes<FMT_Q4_K>(nr, 1, nsb) : ks_term_bytes<FMT_Q6_K>(nr, 1, nsb);
-            xrec = xb > xrec ? xb : xrec;
-            term = tb > term ? tb : term;
-        }
-        term_off = plan_stage_bytes(fmt) + ((xrec + 15) & ~(size_t)15);
-        smb = term_off + term;
-        int nb = 0;
-        if (int rc = plan_occupancy(fmt, smb, &nb)) return rc;
-        if ((uint32_t)nb >= occ) break;
-        if (occ == 1) return unsup("plan: LDS plan does not fit one workgroup per CU");
-    }
-    uint32_t item = 0;
-    const uint8_t * wdummy = nullptr;
-    for (PlanOp & o : ops) {
-        o.item0 = item;
-        if (o.kind == PLOP_DOT) {
-            o.nitems = (o.rows + o.nr - 1) / o.nr;
-            if (!wdummy) wdummy = o.w;
-        } else {
-            o.nr = 4;
-            o.nitems = ((o.cols >> 8) + 3) / 4;
-        }
-        item += o.nitems;
-    }
-    flh_plan * p = new flh_plan{};
-    p->fmt = fmt;
-    p->smb = smb;
-    p->grid = item < G ? item : G;
-    PlanArgs & a = p->args;
-    a.nops = (uint32_t)ops.size();
-    a.nitems = item;
-    a.spin_limit = 1u << 16;                     // polls of ~1 us: a wait gives up after ~0.1 s
-    a.term_off = (uint32_t)term_off;
-    a.wdummy = wdummy;
-    if (hipMalloc((void **)&p->d_ops, ops.size() * sizeof(PlanOp)) != hipSuccess ||
-        hipMalloc((void **)&p->d_ctl, (2 + PLAN_MAX_OPS) * sizeof(uint32_t)) != hipSuccess) {
-        if (p->d_ops) (void)hipFree(p->d_ops);
-        delete p;
-        return set_error(FLH_ERR_NOMEM, "plan: hipMalloc failed");
-    }
-    int rc = hip_check(hipMemcpy(p->d_ops, ops.data(), ops.size() * sizeof(PlanOp), hipMemcpyHostToDevice),
-                       "plan: op upload");
-    if (!rc) rc = hip_check(hipMemset(p->d_ctl, 0, (2 + PLAN_MAX_OPS) * sizeof(uint32_t)), "plan: counter reset");
-    if (rc) {
-        (void)hipFree(p->d_ops);
-        (void)hipFree(p->d_ctl);
-        delete p;
-        return rc;
-    }
-    a.ops = p->d_ops;
-    a.ctl = p->d_ctl;
-#ifdef FLH_PLAN_TRACE
-    (void)hipMalloc((void **)&a.trace, (size_t)p->grid * 8 * 6 * sizeof(uint64_t));
-    (void)hipMemset(a.trace, 0, (size_t)p->grid * 8 * 6 * sizeof(uint64_t));
-#endif
-    *out = p;
-    return FLH_OK;
-}
-
-#ifdef FLH_PLAN_TRACE
-// diagnostic builds: device address of the plan's trace ([grid][8 items][6] u64)
-void * flh_plan_trace(flh_plan * p) { return p ? (void *)p->args.trace : nullptr; }
-#endif
-
-int flh_plan_launch(flh_plan * p, void * stream) {
-    if (!p) return set_error(FLH_ERR_ARG, "null plan");
-    if (int rc = need_init()) return rc;
-    return launch_plan(p->fmt, p->args, p->grid, p->smb, (hipStream_t)stream);
-}
-
-int flh_plan_status(flh_plan * p) {
-    if (!p) return set_error(FLH_ERR_ARG, "null plan");
-    uint32_t flag = 0;
-    if (int rc = hip_check(hipDeviceSynchronize(), "plan status: synchronize")) return rc;
-    if (int rc = hip_check(hipMemcpy(&flag, p->d_ctl + 1, 4, hipMemcpyDeviceToHost), "plan status: read")) return rc;
-    if (!flag) return FLH_OK;
-    const uint32_t zero = 0;
-    (void)hipMemcpy(p->d_ctl + 1, &zero, 4, hipMemcpyHostToDevice);
-    return set_error(FLH_ERR_TIMEOUT, "plan: a workgroup gave up waiting for a producer op (results invalid)");
-}
-
-int flh_plan_info(const flh_plan * p, uint32_t * n_ops, uint32_t * n_items, uint32_t * grid, size_t * lds_bytes) {
-    if (!p) return set_error(FLH_ERR_ARG, "null plan");
-    if (n_ops) *n_ops = p->args.nops;
-    if (n_items) *n_items = p->args.nitems;
-    if (grid) *grid = p->grid;
-    if (lds_bytes) *lds_bytes = p->smb;
-    return FLH_OK;
-}
-
-int flh_plan_destroy(flh_plan * p) {
-    if (!p) return FLH_OK;
-    (void)hipFree(p->d_ops);
-    (void)hipFree(p->d_ctl);
-    delete p;
-    return FLH_OK;
 }
 
 }  // extern "C"

@@ -73,36 +73,4 @@ int launch_fill_normal(float * dst, size_t n, uint64_t seed, float mean,
                        float stddev, float outlier_frac, float outlier_scale,
                        hipStream_t s);
 
-// ------------------------------------------------------------------ plans --
-// A frozen task table compiled into ops for the persistent plan executor
-// (flh_plan.hip).  Op k's work is split into nitems items with global
-// indices [item0, item0 + nitems); items are dealt to the resident
-// workgroups round-robin in index order, and an item starts its activation
-// reads only when every producer op (bitmask prod) has completed all items.
-constexpr int PLAN_MAX_OPS = 32;
-enum : uint32_t { PLOP_DOT = 0, PLOP_ACT = 1 };
-enum : uint32_t { PLF_FUSE = 1, PLF_XREG = 2, PLF_SILU = 4, PLF_NOQ = 8 };
-struct PlanOp {
-    const uint8_t * w;     // DOT: weights (16-byte aligned)
-    const float * x;       // DOT: activation column; ACT: input (SILU: gate)
-    float * y;             // DOT: output (+=); ACT: column quantised in place (SILU: h)
-    const float * u;       // ACT with SILU: up operand
-    uint32_t kind, flags;
-    uint32_t rows, cols;   // DOT: matrix shape; ACT: cols = elements
-    uint32_t nr;           // DOT: rows per item; ACT: 256-element chunks per item (4)
-    uint32_t item0, nitems;
-    uint32_t prod;         // producer ops
-};
-struct PlanArgs {
-    const PlanOp * ops;    // device copy, sorted by item0
-    uint32_t * ctl;        // [0] finished workgroups, [1] error flag, [2 + k] items done of op k
-    const uint8_t * wdummy;  // a valid weight address (re-read, unused, once a cursor is exhausted)
-    uint64_t * trace;        // per-item timestamps (diagnostic builds only; null otherwise)
-    uint32_t nops, nitems, spin_limit, term_off;
-};
-// the LDS plan of a plan launch
-size_t plan_stage_bytes(int fmt);
-int launch_plan(int fmt, const PlanArgs & a, uint32_t grid, size_t smb, hipStream_t s);
-int plan_occupancy(int fmt, size_t smb, int * blocks_per_cu);
-
 }  // namespace flh

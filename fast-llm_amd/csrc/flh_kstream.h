@@ -1,6 +1,6 @@
 // flh_kstream.h -- device building blocks of the LDS-staged int8 x q8_K
 // row-dot (Q4_K / Q6_K), shared by the single-matrix kernels
-// (flh_dot_kstream.hip) and the persistent plan executor (flh_plan.hip).
+// (flh_dot_kstream.hip) and their fused / grouped variants.
 //
 // Weight bytes go HBM -> LDS with direct-to-LDS dwordx4 loads
 // (global_load_lds_dwordx4) in one fully coalesced pass.  Work unit: a CHUNK

@@ -35,8 +35,7 @@ enum {
     FLH_ERR_HIP = -2,          /* HIP runtime error */
     FLH_ERR_UNSUPPORTED = -3,  /* task kind / format / shape not implemented */
     FLH_ERR_NOMEM = -4,        /* arena exhausted or hipMalloc failed */
-    FLH_ERR_STATE = -5,        /* flh_init not called / no device */
-    FLH_ERR_TIMEOUT = -6       /* a plan launch gave up waiting for a producer */
+    FLH_ERR_STATE = -5         /* flh_init not called / no device */
 };
 
 /* TaskKind values (include/fastllm/fastllm.h:19-45), stable. */
@@ -219,37 +218,6 @@ int flh_exec_tasks(const flh_task * tasks, uint32_t n, int fast,
  * (dequant_chunk, src/runtime/kernels.h:162-242). */
 int flh_dequant(int fmt, const void * w, uint32_t rows, uint32_t cols,
                 float * out, void * stream);
-
-/* -------------------------------------------------------------- plans -- */
-/* Persistent executor for a frozen task table: replaces the reference's
- * persistent GPU executor (src/runtime/gpu_exec.cu:156-344), which pops
- * ready tiles from unified-memory queues by dependency count (dep_init /
- * dep_count, include/fastllm/fastllm.h:65-97).  The table (topologically
- * ordered; consumers[] = indices of the dependent tasks, as Graph::add
- * records them, src/runtime/graph.cpp:25-47) is compiled once; every
- * flh_plan_launch then runs the whole table in ONE kernel launch.  A
- * workgroup starts an op's activation reads only after all its producer ops
- * completed, and streams the next op's weights while it waits.  Results are
- * bitwise those of flh_exec_tasks on the same table.  A table without any
- * consumer edge runs its ops strictly in order.
- * Supported: STREAM_DOT tiles of one K format (Q4_K or Q6_K) on the q8_K path
- * (fast = 1, format bit in i8k_mask), nx = 1, cols % 256 == 0, 16-byte
- * aligned w and x; ACT_Q8 (canonical appendix, cols % 256 == 0); SILU_MUL
- * (n % 256 == 0); SIGNAL.  Anything else -> FLH_ERR_UNSUPPORTED: run such a
- * table with flh_exec_tasks.  A plan keeps every CU busy for its duration:
- * two plans must not run concurrently on one device (their waits could
- * stall each other until the spin limit, see flh_plan_status). */
-typedef struct flh_plan flh_plan;
-int flh_plan_create(const flh_task * tasks, uint32_t n, int fast, uint32_t i8_mask,
-                    uint32_t i8k_mask, flh_plan ** out);
-int flh_plan_launch(flh_plan * plan, void * stream);
-/* Synchronises the device; FLH_OK, or FLH_ERR_TIMEOUT if a launch since the
- * last call gave up waiting for a producer (its outputs are invalid).
- * Clears the flag. */
-int flh_plan_status(flh_plan * plan);
-int flh_plan_info(const flh_plan * plan, uint32_t * n_ops, uint32_t * n_items,
-                  uint32_t * grid, size_t * lds_bytes);
-int flh_plan_destroy(flh_plan * plan);
 
 /* ------------------------------------------------------------------ MoE -- */
 /* Grouped expert matvec (the STREAM_DOT_IDX expert tiles of
