@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <string.h>
+#include <stdlib.h>
 #include <string>
 #include <mutex>
 #include "../../include/fastllm_hip.h"
@@ -66,6 +67,17 @@ static int validate_dot(int fmt, const void * w, uint64_t w_bytes, uint32_t rows
     if (((uintptr_t)w & 3) || (estride & 3) || ((uintptr_t)x & 3) || ((uintptr_t)y & 3))
         return set_error(FLH_ERR_ARG, "w, x, y and the expert stride must be 4-byte aligned");
     return FLH_OK;
+}
+
+// Widest activation fused into its dot (every workgroup quantises the whole
+// fp32 column itself); wider ones get a separate ACT_Q8 launch.  Override:
+// FLH_FUSE_MAX_COLS.
+static uint32_t fuse_max_cols() {
+    static const uint32_t v = [] {
+        const char * e = getenv("FLH_FUSE_MAX_COLS");
+        return e ? (uint32_t)strtoul(e, nullptr, 0) : 8192u;
+    }();
+    return v;
 }
 
 static int dispatch_dot(int fmt, const DotArgs & a, int fast, uint32_t i8_mask, uint32_t i8k_mask,
@@ -286,8 +298,8 @@ int flh_act_q8_stream_dot(int fmt, const void * w, uint64_t w_bytes, uint32_t ro
     hipStream_t s = (hipStream_t)stream;
     DotArgs a{(const uint8_t *)w, id_slot, estride, x, y, rows, cols, nx, xstride, ystride};
     // Fused when every workgroup re-reading the fp32 column is cheaper than a
-    // separate ACT_Q8 launch: up to 8192 columns (32 KiB of fp32 per column).
-    if (fast && cols <= 8192 && (fmt == FLH_FMT_Q4_K || fmt == FLH_FMT_Q6_K) && ((i8k_mask >> fmt) & 1u)) {
+    // separate ACT_Q8 launch.
+    if (fast && cols <= fuse_max_cols() && (fmt == FLH_FMT_Q4_K || fmt == FLH_FMT_Q6_K) && ((i8k_mask >> fmt) & 1u)) {
         const int rc = launch_act_dot_kstream(fmt, a, s);
         if (rc != FLH_ERR_UNSUPPORTED) return rc;
     }
@@ -336,7 +348,7 @@ int flh_exec_tasks(const flh_task * t, uint32_t n, int fast, uint32_t i8_mask, u
                 // same outputs).
                 const flh_task * q = i + 1 < n ? &t[i + 1] : nullptr;
                 const bool canon_y = (const uint8_t *)k.y == (const uint8_t *)k.x + xq_off(k.cols);
-                if (q && canon_y && fast && k.cols <= 8192 && q->kind == FLH_TASK_STREAM_DOT && q->x == k.x &&
+                if (q && canon_y && fast && k.cols <= fuse_max_cols() && q->kind == FLH_TASK_STREAM_DOT && q->x == k.x &&
                     q->cols == k.cols && (q->nx ? q->nx : 1u) == 1 &&
                     (q->fmt == FLH_FMT_Q4_K || q->fmt == FLH_FMT_Q6_K) && ((i8k_mask >> q->fmt) & 1u)) {
                     DotArgs a{(const uint8_t *)q->w, nullptr, 0, (const float *)q->x, (float *)q->y,

@@ -60,11 +60,12 @@ __device__ __forceinline__ void ks_body(const uint8_t * __restrict__ w, uint32_t
         return nch > wave ? (nch - wave + 3) / 4 : 0;
     };
     // Issue cursor over this wave's chunk sequence (batches blockIdx.x, +G, ...).
-    // Every call issues exactly NI loads (a repeat of the last real chunk once
-    // the sequence is exhausted), so the count of loads behind any chunk is
-    // always NI * (D - 1).
+    // Every call issues exactly NI loads, so the count of loads behind any
+    // chunk is always NI * (D - 1).  Once the sequence is exhausted the loads
+    // repeat the matrix's first chunk: every wave re-reads the same lines,
+    // which stay in L2, instead of adding HBM traffic.
     uint32_t qbt = batch0, qci = 0, qn = qbt < nbatch ? nci_of(qbt) : 0;
-    const uint8_t * l_wb = w;            // a wave without chunks re-reads row 0 (valid, unused)
+    const uint8_t * l_wb = w;
     uint32_t l_ch = 0, l_nsbb = nsb;
     auto issue_one = [&](uint8_t * stage) {
         while (qbt < nbatch && qci >= qn) {
@@ -77,6 +78,10 @@ __device__ __forceinline__ void ks_body(const uint8_t * __restrict__ w, uint32_t
             l_ch = wave + 4 * qci;
             l_nsbb = min(nr, rows - qbt * nr) * nsb;
             ++qci;
+        } else {
+            l_wb = w;
+            l_ch = 0;
+            l_nsbb = nsb;
         }
         ks_issue<FMT>(l_wb, l_ch, l_nsbb, stage, lane);
     };
@@ -261,7 +266,7 @@ static int ks_launch(const DotArgs & a, hipStream_t s) {
     uint32_t nr;
     int D;
     size_t smb;
-    if (ks_plan<FMT>(a.rows, NX, nsb, slots, FMT == FMT_Q4_K ? 4 : 3, nr, D, smb)) return FLH_ERR_UNSUPPORTED;
+    if (ks_plan<FMT>(a.rows, NX, nsb, slots, 2, nr, D, smb)) return FLH_ERR_UNSUPPORTED;
     const uint32_t nbatch = (a.rows + nr - 1) / nr;
     const uint32_t grid = nbatch < slots ? nbatch : slots;
     switch (D) {
@@ -292,7 +297,7 @@ static int moe_launch(const MoeArgs & a, hipStream_t s) {
     uint32_t nr;
     int D;
     size_t smb;
-    if (ks_plan<FMT>(a.rows, NX, nsb, gx, FMT == FMT_Q4_K ? 4 : 3, nr, D, smb)) return FLH_ERR_UNSUPPORTED;
+    if (ks_plan<FMT>(a.rows, NX, nsb, gx, 2, nr, D, smb)) return FLH_ERR_UNSUPPORTED;
     const uint32_t nbatch = (a.rows + nr - 1) / nr;
     const uint32_t g = nbatch < gx ? nbatch : gx;
     switch (D) {

@@ -176,10 +176,13 @@ __device__ __forceinline__ void ks_x_fuse(const KsCols<NX> & C, uint32_t nx, uin
     const uint32_t sub = lane >> 4, run = lane & 15;        // superblock in the pass, 16-run
     bool issued = false;
     for (uint32_t base = 0; base < nitem; base += 64) {
-        // 16 superblocks per wave-pass (4 per pass x 4 passes), loads first
+        // up to 64 superblocks per pass (16 per q-group, 4 per wave), loads
+        // first; only the q-groups that hold superblocks are loaded
+        const uint32_t nq = min(4u, (nitem - base + 15) / 16);
         u32x4a raw[4][4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
+            if ((uint32_t)q >= nq) break;
             const uint32_t i = base + 16 * q + 4 * wave + sub;
             const uint32_t ii = i < nitem ? i : 0;
             const float * src = col_pick<NX>(C.x, ii / nsb) + 256 * (ii % nsb) + 16 * run;
@@ -193,12 +196,13 @@ __device__ __forceinline__ void ks_x_fuse(const KsCols<NX> & C, uint32_t nx, uin
         if (tid < 64) amx[tid] = 0u;
         __syncthreads();
 #pragma unroll
-        for (int q = 0; q < 4; ++q) atomicMax(&amx[16 * q + 4 * wave + sub], __float_as_uint(ks_absmax16(raw[q])));
+        for (int q = 0; q < 4; ++q)
+            if ((uint32_t)q < nq) atomicMax(&amx[16 * q + 4 * wave + sub], __float_as_uint(ks_absmax16(raw[q])));
         __syncthreads();
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const uint32_t i = base + 16 * q + 4 * wave + sub;
-            if (i < nitem) {
+            if ((uint32_t)q < nq && i < nitem) {
                 const uint32_t p = i / nsb, sb = i % nsb;
                 const float amax = __uint_as_float(amx[16 * q + 4 * wave + sub]);
                 const float d = amax / 127.f;
