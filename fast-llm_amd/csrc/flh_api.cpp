@@ -86,7 +86,10 @@ static int dispatch_dot(int fmt, const DotArgs & a, int fast, uint32_t i8_mask, 
     if ((fmt == FLH_FMT_Q4_K || fmt == FLH_FMT_Q6_K) && ((i8k_mask >> fmt) & 1u))
         return launch_dot_i8k(fmt, a, s);
     if (fmt != FLH_FMT_F32 && ((i8_mask >> fmt) & 1u)) {
-        if (fmt == FLH_FMT_Q8_0) return launch_dot_i8_q8_0(a, s);
+        if (fmt == FLH_FMT_Q8_0) {
+            const int rc = launch_dot_kstream(fmt, a, s);     // LDS-staged; register kernel otherwise
+            return rc != FLH_ERR_UNSUPPORTED ? rc : launch_dot_i8_q8_0(a, s);
+        }
         return set_error(FLH_ERR_UNSUPPORTED,
                          "q8_1 int8 path is implemented for Q8_0 only (use the i8k mask for K formats)");
     }

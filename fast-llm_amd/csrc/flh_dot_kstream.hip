@@ -47,10 +47,11 @@ __device__ __forceinline__ void ks_body(const uint8_t * __restrict__ w, uint32_t
 
     uint8_t * stages = sm;                                        // [4][D][WIN]
     uint8_t * xr = sm + (size_t)4 * D * WIN;                      // [NX][nsb][4][80]
-    float * xd = (float *)(xr + (size_t)NX * nsb * 4 * XREC);     // [NX][nsb]
-    int * TI = (int *)(xd + (size_t)NX * nsb);                    // [nr][NX][nsb]
-    int * TM = TI + (size_t)nr * NX * nsb;                        // Q4_K only
-    uint32_t * TH = (uint32_t *)(FMT == FMT_Q4_K ? TM + (size_t)nr * NX * nsb : TM);   // [nr][nsb]
+    constexpr uint32_t TPS = ks_tps<FMT>();                      // fold terms per superblock
+    float * xd = (float *)(xr + (size_t)NX * nsb * 4 * XREC);     // [NX][nsb * TPS]
+    int * TI = (int *)(xd + (size_t)NX * nsb * TPS);              // [nr][NX][nsb * TPS]
+    int * TM = TI + (size_t)nr * NX * nsb * TPS;                  // Q4_K only
+    uint32_t * TH = (uint32_t *)(FMT == FMT_Q4_K ? TM + (size_t)nr * NX * nsb : TM);   // [nr][nsb * TPS]
     uint8_t * myst = stages + (size_t)wave * D * WIN;
 
     const uint32_t nbatch = (rows + nr - 1) / nr;
@@ -340,6 +341,11 @@ static int ks_dispatch(int fmt, const DotArgs & a, hipStream_t s) {
     if (fmt == FMT_Q6_K)
         return a.nx == 1 ? ks_launch<FMT_Q6_K, 1, FUSE>(a, s) : a.nx == 2 ? ks_launch<FMT_Q6_K, 2, FUSE>(a, s)
                                                                          : ks_launch<FMT_Q6_K, 4, FUSE>(a, s);
+    if constexpr (!FUSE) {                    // Q8_0 x q8_1 (ACT_Q8 runs separately)
+        if (fmt == FMT_Q8_0)
+            return a.nx == 1 ? ks_launch<FMT_Q8_0, 1, false>(a, s) : a.nx == 2 ? ks_launch<FMT_Q8_0, 2, false>(a, s)
+                                                                             : ks_launch<FMT_Q8_0, 4, false>(a, s);
+    }
     return FLH_ERR_UNSUPPORTED;
 }
 

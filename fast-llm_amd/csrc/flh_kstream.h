@@ -43,6 +43,15 @@ template <> struct KS<FMT_Q6_K> {
     static constexpr uint32_t WIN = 4096;            // 3360 B + realignment slack
     static constexpr int NI = 4;
 };
+// Q8_0: a "superblock" is a unit of 8 blocks (256 weights, 272 bytes, 16-byte
+// aligned in a row-major matrix whose rows hold a multiple of 256 weights)
+template <> struct KS<FMT_Q8_0> {
+    static constexpr uint32_t BLK = 272;
+    static constexpr uint32_t WIN = 4352;            // 16 units: 4 x 1024 B + 256 B
+    static constexpr int NI = 5;
+};
+// fold terms per superblock (Q8_0 folds per 32-weight block)
+template <int FMT> __host__ __device__ constexpr uint32_t ks_tps() { return FMT == FMT_Q8_0 ? 8 : 1; }
 
 constexpr uint32_t XREC = 80;                        // bytes per (sb, part) activation record
 
@@ -50,11 +59,11 @@ constexpr uint32_t XREC = 80;                        // bytes per (sb, part) act
 // of nr rows
 template <int FMT>
 __host__ __device__ inline size_t ks_xrec_bytes(uint32_t nx, uint32_t nsb) {
-    return (size_t)nx * nsb * 4 * XREC + (size_t)nx * nsb * 4;
+    return (size_t)nx * nsb * 4 * XREC + (size_t)nx * nsb * 4 * ks_tps<FMT>();
 }
 template <int FMT>
 __host__ __device__ inline size_t ks_term_bytes(uint32_t nr, uint32_t nx, uint32_t nsb) {
-    return (size_t)nr * nx * nsb * 4 * (FMT == FMT_Q4_K ? 2 : 1) + (size_t)nr * nsb * 4;
+    return ((size_t)nr * nx * nsb * 4 * (FMT == FMT_Q4_K ? 2 : 1) + (size_t)nr * nsb * 4) * ks_tps<FMT>();
 }
 template <int FMT>
 __host__ __device__ inline size_t ks_smem_bytes(uint32_t nr, uint32_t nx, uint32_t nsb, int D) {
@@ -76,6 +85,16 @@ __device__ __forceinline__ void ks_issue(const uint8_t * wb, uint32_t ch, uint32
         __builtin_amdgcn_global_load_lds(GPTR(g + (o0 <= last16 ? o0 : last16)), LPTR(stage), 16, 0, FLH_KS_AUX);
         __builtin_amdgcn_global_load_lds(GPTR(g + (o1 <= last16 ? o1 : last16)), LPTR(stage + 1024), 16, 0, FLH_KS_AUX);
         __builtin_amdgcn_global_load_lds(GPTR(g + (o2 <= last4 ? o2 : last4)), LPTR(stage + 2048), 4, 0, FLH_KS_AUX);
+    } else if constexpr (FMT == FMT_Q8_0) {
+        const uint8_t * g = wb + (size_t)f0 * B;
+        const uint32_t last16 = nact * B - 16, last4 = nact * B - 4;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t o = 1024 * i + 16 * lane;
+            __builtin_amdgcn_global_load_lds(GPTR(g + (o <= last16 ? o : last16)), LPTR(stage + 1024 * i), 16, 0, FLH_KS_AUX);
+        }
+        const uint32_t o4 = 4096 + 4 * lane;
+        __builtin_amdgcn_global_load_lds(GPTR(g + (o4 <= last4 ? o4 : last4)), LPTR(stage + 4096), 4, 0, FLH_KS_AUX);
     } else {
         const uintptr_t gs = (uintptr_t)(wb + (size_t)f0 * B);
         const uint8_t * g = (const uint8_t *)(gs & ~(uintptr_t)15);
@@ -250,10 +269,21 @@ __device__ __forceinline__ void ks_x_fuse(const KsCols<NX> & C, uint32_t nx, uin
     for (uint32_t i = tid; i < (NX - nx) * nsb; i += 256) xd[nx * nsb + i] = 0.f;
 }
 
-// Record (sb, part cc) of column p from the q8_K appendix at xb (superblock base).
+// Record (sb, part cc) of column p from its appendix at xb (the superblock's
+// base: q8_K for the K formats; for Q8_0, the unit's 8 q8_1 blocks, whose
+// scales go to bs[0..1] as raw halves).
 template <int FMT>
 __device__ __forceinline__ void ks_xrec_load(const uint8_t * xb, uint32_t cc, u32x4 (&v)[4], int (&bs)[4]) {
-    if constexpr (FMT == FMT_Q4_K) {
+    if constexpr (FMT == FMT_Q8_0) {
+        const uint8_t * b0 = xb + 72 * cc;                  // q8_1 blocks 2cc, 2cc + 1 (36 B each)
+        v[0] = ld4(b0 + 4);
+        v[1] = ld4(b0 + 20);
+        v[2] = ld4(b0 + 40);
+        v[3] = ld4(b0 + 56);
+        bs[0] = (int)*(const uint16_t *)b0;
+        bs[1] = (int)*(const uint16_t *)(b0 + 36);
+        bs[2] = bs[3] = 0;
+    } else if constexpr (FMT == FMT_Q4_K) {
         const uint32_t g0 = 2 * (cc >> 1), h = cc & 1;
         const uint32_t gs[4] = {g0, g0 + 1, g0 + 4, g0 + 5};
 #pragma unroll
@@ -271,7 +301,14 @@ __device__ __forceinline__ void ks_xrec_load(const uint8_t * xb, uint32_t cc, u3
     }
 }
 
-// Records from the q8_K appendices written by ACT_Q8.  after_loads() as above.
+// Base of superblock sb's activation in column x: its q8_K block (K formats)
+// or its 8 q8_1 blocks (Q8_0).
+template <int FMT>
+__device__ __forceinline__ const uint8_t * ks_xsb(const uint8_t * x, uint32_t cols, uint32_t sb) {
+    return FMT == FMT_Q8_0 ? x + xq_off(cols) + (size_t)sb * 288 : x + xqk_off(cols) + (size_t)sb * 292;
+}
+
+// Records from the appendices written by ACT_Q8.  after_loads() as above.
 template <int FMT, int NX, typename F>
 __device__ __forceinline__ void ks_x_app(const KsCols<NX> & C, uint32_t nx, uint32_t nsb, uint32_t cols,
                                          uint8_t * xr, float * xd, F && after_loads) {
@@ -281,11 +318,11 @@ __device__ __forceinline__ void ks_x_app(const KsCols<NX> & C, uint32_t nx, uint
         const uint32_t i = tid < NX * nsb * 4 ? tid : 0;
         const uint32_t p = i / (nsb * 4), rem = i % (nsb * 4), sb = rem >> 2, cc = rem & 3;
         const uint32_t pp = p < nx ? p : 0;
-        const uint8_t * xb = (const uint8_t *)col_pick<NX>(C.x, pp) + xqk_off(cols) + (size_t)sb * 292;
+        const uint8_t * xb = ks_xsb<FMT>((const uint8_t *)col_pick<NX>(C.x, pp), cols, sb);
         u32x4 v[4];
         int bs[4];
         ks_xrec_load<FMT>(xb, cc, v, bs);
-        const float dk = *(const float *)xb;
+        const float dk = FMT == FMT_Q8_0 ? 0.f : *(const float *)xb;
         after_loads();
         if (tid < NX * nsb * 4) {
             uint32_t * rec = (uint32_t *)(xr + (size_t)tid * XREC);
@@ -294,13 +331,18 @@ __device__ __forceinline__ void ks_x_app(const KsCols<NX> & C, uint32_t nx, uint
                 rec[4 * k + 0] = v[k].x; rec[4 * k + 1] = v[k].y; rec[4 * k + 2] = v[k].z; rec[4 * k + 3] = v[k].w;
                 rec[16 + k] = (uint32_t)bs[k];
             }
-            if (cc == 0) xd[p * nsb + sb] = (p < nx) ? dk : 0.f;
+            if constexpr (FMT == FMT_Q8_0) {
+                xd[(p * nsb + sb) * 8 + 2 * cc] = (p < nx) ? h2f((uint32_t)bs[0]) : 0.f;
+                xd[(p * nsb + sb) * 8 + 2 * cc + 1] = (p < nx) ? h2f((uint32_t)bs[1]) : 0.f;
+            } else if (cc == 0) {
+                xd[p * nsb + sb] = (p < nx) ? dk : 0.f;
+            }
         }
     } else {
         for (uint32_t i = tid; i < NX * nsb * 4; i += 256) {
             const uint32_t p = i / (nsb * 4), rem = i % (nsb * 4), sb = rem >> 2, cc = rem & 3;
             const uint32_t pp = p < nx ? p : 0;
-            const uint8_t * xb = (const uint8_t *)col_pick<NX>(C.x, pp) + xqk_off(cols) + (size_t)sb * 292;
+            const uint8_t * xb = ks_xsb<FMT>((const uint8_t *)col_pick<NX>(C.x, pp), cols, sb);
             uint32_t * rec = (uint32_t *)(xr + (size_t)i * XREC);
             u32x4 v[4];
             int bs[4];
@@ -310,7 +352,12 @@ __device__ __forceinline__ void ks_x_app(const KsCols<NX> & C, uint32_t nx, uint
                 rec[4 * k + 0] = v[k].x; rec[4 * k + 1] = v[k].y; rec[4 * k + 2] = v[k].z; rec[4 * k + 3] = v[k].w;
                 rec[16 + k] = (uint32_t)bs[k];
             }
-            if (cc == 0) xd[p * nsb + sb] = (p < nx) ? *(const float *)xb : 0.f;
+            if constexpr (FMT == FMT_Q8_0) {
+                xd[(p * nsb + sb) * 8 + 2 * cc] = (p < nx) ? h2f((uint32_t)bs[0]) : 0.f;
+                xd[(p * nsb + sb) * 8 + 2 * cc + 1] = (p < nx) ? h2f((uint32_t)bs[1]) : 0.f;
+            } else if (cc == 0) {
+                xd[p * nsb + sb] = (p < nx) ? *(const float *)xb : 0.f;
+            }
         }
         after_loads();
     }
@@ -324,7 +371,37 @@ template <int FMT, int NX, bool XREG>
 __device__ __forceinline__ void ks_chunk(const uint8_t * st, uint32_t mis, uint32_t s, uint32_t c,
                                          const uint8_t * xrec, uint32_t nsb, const u32x4a (&xregs)[NX][5],
                                          int (&ia)[NX], int (&im)[NX], uint32_t & tag) {
-    if constexpr (FMT == FMT_Q4_K) {
+    if constexpr (FMT == FMT_Q8_0) {
+        // blocks 2c, 2c + 1 of unit s: 68 bytes at a 4-byte aligned offset
+        const uint32_t * u = (const uint32_t *)(st + 272 * s + 68 * c);
+        uint32_t w[17];
+#pragma unroll
+        for (int i = 0; i < 17; ++i) w[i] = u[i];
+        tag = (w[0] & 0xFFFFu) | (w[8] & 0xFFFF0000u);       // d of block 2c | d of block 2c+1 << 16
+        int q0[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) q0[i] = (int)alignb(w[i + 1], w[i], 2);
+#pragma unroll
+        for (int p = 0; p < NX; ++p) {
+            const uint8_t * xp = xrec + (size_t)p * nsb * 4 * XREC;
+            u32x4a xv[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                if constexpr (XREG) xv[k] = xregs[p][k]; else xv[k] = *(const u32x4a *)(xp + 16 * k);
+            }
+            int d0 = 0, d1 = 0;
+            d0 = dot4(q0[0], (int)xv[0].x, d0); d0 = dot4(q0[1], (int)xv[0].y, d0);
+            d0 = dot4(q0[2], (int)xv[0].z, d0); d0 = dot4(q0[3], (int)xv[0].w, d0);
+            d0 = dot4(q0[4], (int)xv[1].x, d0); d0 = dot4(q0[5], (int)xv[1].y, d0);
+            d0 = dot4(q0[6], (int)xv[1].z, d0); d0 = dot4(q0[7], (int)xv[1].w, d0);
+            d1 = dot4((int)w[9], (int)xv[2].x, d1); d1 = dot4((int)w[10], (int)xv[2].y, d1);
+            d1 = dot4((int)w[11], (int)xv[2].z, d1); d1 = dot4((int)w[12], (int)xv[2].w, d1);
+            d1 = dot4((int)w[13], (int)xv[3].x, d1); d1 = dot4((int)w[14], (int)xv[3].y, d1);
+            d1 = dot4((int)w[15], (int)xv[3].z, d1); d1 = dot4((int)w[16], (int)xv[3].w, d1);
+            ia[p] = d0;
+            im[p] = d1;
+        }
+    } else if constexpr (FMT == FMT_Q4_K) {
         const u32x4a hd = *(const u32x4a *)(st + 144 * s);
         const u32x4a qa = *(const u32x4a *)(st + 144 * s + 16 + 16 * c);
         const u32x4a qb = *(const u32x4a *)(st + 144 * s + 80 + 16 * c);
@@ -417,6 +494,21 @@ template <int FMT, int NX>
 __device__ __forceinline__ void ks_park(int (&ia)[NX], int (&im)[NX], uint32_t tag, bool act, uint32_t c,
                                         uint32_t nx, uint32_t rl, uint32_t sb, uint32_t nsb,
                                         int * TI, int * TM, uint32_t * TH) {
+    if constexpr (FMT == FMT_Q8_0) {       // exact per-block sums, no reduction: every lane parks two
+        const uint32_t nb = nsb * 8, b = 8 * sb + 2 * c;
+#pragma unroll
+        for (int p = 0; p < NX; ++p) {
+            if (act && p < (int)nx) {
+                TI[(rl * NX + p) * nb + b] = ia[p];
+                TI[(rl * NX + p) * nb + b + 1] = im[p];
+            }
+        }
+        if (act) {
+            TH[rl * nb + b] = tag & 0xFFFFu;
+            TH[rl * nb + b + 1] = tag >> 16;
+        }
+        return;
+    }
 #pragma unroll
     for (int p = 0; p < NX; ++p) {
         int x1 = ia[p];
@@ -437,6 +529,17 @@ template <int FMT, int NX>
 __device__ __forceinline__ float ks_fold(const int * TI, const int * TM, const uint32_t * TH, const float * xd,
                                          uint32_t nsb, uint32_t k, uint32_t p, uint32_t rl, bool fok) {
     float acc = 0.f;
+    if constexpr (FMT == FMT_Q8_0) {       // acc[b & 3] over 32-weight blocks (fl_dot_i8_q8_0 order)
+        if (fok) {
+            const uint32_t nb = nsb * 8;
+            const int * ti = TI + (rl * NX + p) * nb;
+            const uint32_t * th = TH + rl * nb;
+            const float * xdp = xd + p * nb;
+            for (uint32_t b = k; b < nb; b += 4) acc = fmaf(h2f(th[b]) * xdp[b], (float)ti[b], acc);
+        }
+        const float s01 = acc + qx1f(acc);
+        return s01 + qx2f(s01);
+    }
     if (fok) {
         const int * ti = TI + (rl * NX + p) * nsb;
         const int * tm = TM + (rl * NX + p) * nsb;
