@@ -54,6 +54,16 @@ __global__ void k_dequant(int fmt, const uint8_t * __restrict__ w, uint32_t rows
         const uint8_t * b = w + (size_t)r * (cols / 32) * 34 + (size_t)j * 34;
         const float d = h2f(b[0] | (b[1] << 8));
         for (int i = 0; i < 32; ++i) o[32 * j + i] = d * (float)(int8_t)b[2 + i];
+    } else if (fmt == FMT_Q5_0) {
+        const uint8_t * b = w + (size_t)r * (cols / 32) * 22 + (size_t)j * 22;
+        const float d = h2f(b[0] | (b[1] << 8));
+        const uint32_t qh = b[2] | (b[3] << 8) | (b[4] << 16) | ((uint32_t)b[5] << 24);
+        for (int i = 0; i < 16; ++i) {
+            const uint32_t lo = (b[6 + i] & 0x0F) | (((qh >> i) << 4) & 0x10);
+            const uint32_t hi = (b[6 + i] >> 4) | ((qh >> (i + 12)) & 0x10);
+            o[32 * j + i] = d * (float)((int)lo - 16);
+            o[32 * j + 16 + i] = d * (float)((int)hi - 16);
+        }
     } else if (fmt == FMT_Q4_K) {
         const uint32_t sb = j >> 3, g = j & 7, c = g >> 1;   // group g of superblock sb
         const uint8_t * b = w + (size_t)r * (cols / 256) * 144 + (size_t)sb * 144;
@@ -86,7 +96,7 @@ __global__ void k_dequant(int fmt, const uint8_t * __restrict__ w, uint32_t rows
 
 int launch_dequant(int fmt, const uint8_t * w, uint32_t rows, uint32_t cols,
                    float * out, hipStream_t s) {
-    if (fmt != FMT_Q8_0 && fmt != FMT_Q4_K && fmt != FMT_Q6_K)
+    if (fmt != FMT_Q8_0 && fmt != FMT_Q5_0 && fmt != FMT_Q4_K && fmt != FMT_Q6_K)
         return set_error(FLH_ERR_UNSUPPORTED, "dequant: format not supported");
     const uint64_t units = (uint64_t)rows * (cols / 32);
     if (units == 0) return FLH_OK;

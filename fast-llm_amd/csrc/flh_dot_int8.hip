@@ -359,22 +359,28 @@ __global__ __launch_bounds__(256) void k_moe_i8k(MoeArgs a, uint32_t nr) {
     }
 }
 
-// ------------------------------------------------------------ Q8_0 x q8_1 --
-// One lane per 32-weight block; NK blocks per lane (row of up to 256*NK
+// ----------------------------------------------------- Q8_0 / Q5_0 x q8_1 --
+// One lane per 32-weight block (Q5_0: 5-bit values built in registers, the
+// -16 offset applied as 16 x the block's activation sum, fl_dot_i8_q5_0,
+// src/runtime/quants.h:449-466); NK blocks per lane (row of up to 256*NK
 // blocks).  Terms: idot per (row, column, block) and the weight scale bits
 // per (row, block); chain acc[b & 3] = fmaf(dw * dx, idot, .).
 __host__ __device__ inline size_t q8_smem_bytes(uint32_t nr, uint32_t nx_t, uint32_t P) {
     return 4 * ((size_t)nr * nx_t * P + (size_t)nr * P + (size_t)nx_t * P);
 }
 
-template <int NX, int NK>
-__global__ __launch_bounds__(256) void k_dot_i8_q8_0(DotArgs a, uint32_t nr) {
+// bit i of the 4-bit n -> bit 0 of byte i
+__device__ __forceinline__ uint32_t spread4(uint32_t n) { return (n * 0x00204081u) & 0x01010101u; }
+
+template <int FMT, int NX, int NK>
+__global__ __launch_bounds__(256) void k_dot_i8_b32(DotArgs a, uint32_t nr) {
     extern __shared__ int smem[];
     const uint8_t * w = a.w + (a.id_slot ? (size_t)(*a.id_slot) * a.estride : 0);
     const uint32_t nb = a.cols >> 5;
     const uint32_t lgP = ceil_log2(nb), P = 1u << lgP;   // P <= 256*NK
     const uint32_t rpi = NK == 1 ? (256u >> lgP) : 1u;
-    const uint64_t rb = (uint64_t)nb * 34;
+    constexpr uint32_t BB = FMT == FMT_Q5_0 ? 22 : 34;     // block bytes
+    const uint64_t rb = (uint64_t)nb * BB;
     const uint32_t tid = threadIdx.x;
     const uint32_t rsub = NK == 1 ? (tid >> lgP) : 0u;
     uint32_t bl[NK];
@@ -409,16 +415,35 @@ __global__ __launch_bounds__(256) void k_dot_i8_q8_0(DotArgs a, uint32_t nr) {
             X[p][k][0] = v0.x; X[p][k][1] = v0.y; X[p][k][2] = v0.z; X[p][k][3] = v0.w;
             X[p][k][4] = v1.x; X[p][k][5] = v1.y; X[p][k][6] = v1.z; X[p][k][7] = v1.w;
         }
+    // Q5_0: the block's activation sum (the -16 offset term), exact
+    int XS[NX][NK];
+#pragma unroll
+    for (int p = 0; p < NX; ++p)
+#pragma unroll
+        for (int k = 0; k < NK; ++k) {
+            int t = 0;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) t = dot4(0x01010101, X[p][k][j], t);
+            XS[p][k] = t;
+        }
 
+    // A block's bytes from the dword-aligned window at f (blocks are 2-byte
+    // aligned; nothing past the block's last byte is read).
     struct W8 { u32x4 d0, d1; uint32_t d8, sh; };
     auto wload = [&](uint32_t row, uint32_t b) -> W8 {
-        const uint8_t * blk = w + (size_t)row * rb + (size_t)b * 34;
+        const uint8_t * blk = w + (size_t)row * rb + (size_t)b * BB;
         const uintptr_t ba = (uintptr_t)blk;
         const uint8_t * f = (const uint8_t *)(ba & ~(uintptr_t)3);
         W8 r;
         r.sh = (uint32_t)(ba & 3);
-        r.d0 = ld4_nt(f); r.d1 = ld4_nt(f + 16);
-        r.d8 = ldh(f + 32) | (ldh(blk + 32) << 16);
+        r.d0 = ld4_nt(f);
+        if constexpr (FMT == FMT_Q5_0) {
+            r.d1 = u32x4{*(const uint32_t *)(f + 16), r.sh ? *(const uint32_t *)(f + 20) : ldh(f + 20), 0u, 0u};
+            r.d8 = 0;
+        } else {
+            r.d1 = ld4_nt(f + 16);
+            r.d8 = ldh(f + 32) | (ldh(blk + 32) << 16);
+        }
         return r;
     };
 
@@ -442,19 +467,38 @@ __global__ __launch_bounds__(256) void k_dot_i8_q8_0(DotArgs a, uint32_t nr) {
 #pragma unroll
             for (int k = 0; k < NK; ++k) {
                 const W8 & W = cur[k];
-                const uint32_t D[9] = {W.d0.x, W.d0.y, W.d0.z, W.d0.w,
-                                       W.d1.x, W.d1.y, W.d1.z, W.d1.w, W.d8};
-                const uint32_t dbits = W.sh ? (D[0] >> 16) : (D[0] & 0xFFFFu);
-                int qs[8];
-#pragma unroll
-                for (int j = 0; j < 8; ++j)
-                    qs[j] = (int)(W.sh ? D[j + 1] : alignb(D[j + 1], D[j], 2));
                 const bool wr = act[k] && rl < nrow && rl < nr;
+                uint32_t dbits;
+                int qs[8];
+                if constexpr (FMT == FMT_Q5_0) {
+                    // E = the block's bytes 0..21; d, qh, then 16 bytes of nibble pairs
+                    const uint32_t D[6] = {W.d0.x, W.d0.y, W.d0.z, W.d0.w, W.d1.x, W.d1.y};
+                    uint32_t E[6];
+#pragma unroll
+                    for (int i = 0; i < 5; ++i) E[i] = alignb(D[i + 1], D[i], W.sh);
+                    E[5] = D[5] >> (8 * W.sh);
+                    dbits = E[0] & 0xFFFFu;
+                    const uint32_t qh = (E[0] >> 16) | (E[1] << 16);
+#pragma unroll
+                    for (int k4 = 0; k4 < 4; ++k4) {
+                        const uint32_t q = alignb(E[2 + k4], E[1 + k4], 2);
+                        qs[k4] = (int)((q & 0x0F0F0F0Fu) | (spread4((qh >> (4 * k4)) & 0xFu) << 4));
+                        qs[4 + k4] = (int)(((q >> 4) & 0x0F0F0F0Fu) | (spread4((qh >> (16 + 4 * k4)) & 0xFu) << 4));
+                    }
+                } else {
+                    const uint32_t D[9] = {W.d0.x, W.d0.y, W.d0.z, W.d0.w,
+                                           W.d1.x, W.d1.y, W.d1.z, W.d1.w, W.d8};
+                    dbits = W.sh ? (D[0] >> 16) : (D[0] & 0xFFFFu);
+#pragma unroll
+                    for (int j = 0; j < 8; ++j)
+                        qs[j] = (int)(W.sh ? D[j + 1] : alignb(D[j + 1], D[j], 2));
+                }
 #pragma unroll
                 for (int p = 0; p < NX; ++p) {
                     int d = 0;
 #pragma unroll
                     for (int j = 0; j < 8; ++j) d = dot4(qs[j], X[p][k][j], d);
+                    if constexpr (FMT == FMT_Q5_0) d -= 16 * XS[p][k];     // (idot - 16 isum), quants.h:449-466
                     if (wr && p < (int)a.nx) TI[((rl * NX + p) << lgP) + bl[k]] = d;
                 }
                 if (wr) TH[(rl << lgP) + bl[k]] = dbits;
@@ -601,7 +645,7 @@ int launch_moe_i8k(int fmt, const MoeArgs & a, hipStream_t s) {
     return set_error(FLH_ERR_UNSUPPORTED, "moe i8k: format has no q8_K path");
 }
 
-template <int NX, int NK>
+template <int FMT, int NX, int NK>
 static int launch_q8(const DotArgs & a, hipStream_t s) {
     const uint32_t nb = a.cols >> 5;
     const uint32_t P = 1u << ceil_log2(nb);
@@ -612,14 +656,15 @@ static int launch_q8(const DotArgs & a, hipStream_t s) {
     const uint32_t nr = pick_nr(a.rows, rpi, nr_max);
     const size_t sm = q8_smem_bytes(nr, NX, P);
     const uint32_t grid = (a.rows + nr - 1) / nr;
-    hipLaunchKernelGGL((k_dot_i8_q8_0<NX, NK>), dim3(grid), dim3(256), sm, s, a, nr);
-    return hip_check(hipGetLastError(), "k_dot_i8_q8_0 launch");
+    hipLaunchKernelGGL((k_dot_i8_b32<FMT, NX, NK>), dim3(grid), dim3(256), sm, s, a, nr);
+    return hip_check(hipGetLastError(), "k_dot_i8_b32 launch");
 }
 
-int launch_dot_i8_q8_0(const DotArgs & a0, hipStream_t s) {
+template <int FMT>
+static int launch_i8_b32(const DotArgs & a0, hipStream_t s) {
     const uint32_t nb = a0.cols >> 5;
     if (nb == 0 || nb > 512 || (a0.cols & 31))
-        return set_error(FLH_ERR_UNSUPPORTED, "q8_0 dot: cols must be a multiple of 32, <= 16384");
+        return set_error(FLH_ERR_UNSUPPORTED, "32-block int8 dot: cols must be a multiple of 32, <= 16384");
     if (a0.rows == 0 || a0.nx == 0) return FLH_OK;
     for (uint32_t p0 = 0; p0 < a0.nx; p0 += 4) {
         DotArgs a = a0;
@@ -627,11 +672,14 @@ int launch_dot_i8_q8_0(const DotArgs & a0, hipStream_t s) {
         a.x = a0.x + (size_t)p0 * a0.xstride;
         a.y = a0.y + (size_t)p0 * a0.ystride;
         int rc;
-        if (nb <= 256) rc = a.nx == 1 ? launch_q8<1, 1>(a, s) : a.nx == 2 ? launch_q8<2, 1>(a, s) : launch_q8<4, 1>(a, s);
-        else           rc = a.nx == 1 ? launch_q8<1, 2>(a, s) : a.nx == 2 ? launch_q8<2, 2>(a, s) : launch_q8<4, 2>(a, s);
+        if (nb <= 256) rc = a.nx == 1 ? launch_q8<FMT, 1, 1>(a, s) : a.nx == 2 ? launch_q8<FMT, 2, 1>(a, s) : launch_q8<FMT, 4, 1>(a, s);
+        else           rc = a.nx == 1 ? launch_q8<FMT, 1, 2>(a, s) : a.nx == 2 ? launch_q8<FMT, 2, 2>(a, s) : launch_q8<FMT, 4, 2>(a, s);
         if (rc) return rc;
     }
     return FLH_OK;
 }
+
+int launch_dot_i8_q8_0(const DotArgs & a, hipStream_t s) { return launch_i8_b32<FMT_Q8_0>(a, s); }
+int launch_dot_i8_q5_0(const DotArgs & a, hipStream_t s) { return launch_i8_b32<FMT_Q5_0>(a, s); }
 
 }  // namespace flh

@@ -22,9 +22,23 @@ namespace flh {
 
 __device__ __forceinline__ uint32_t ld16u(const uint8_t * p) { return p[0] | (p[1] << 8); }
 
+// Q5_0 value of element j (0..31) of a block: 4 bits from qs, the 5th from
+// bit j of qh, minus 16 (src/runtime/kernels.h:169-180)
+__device__ __forceinline__ int q5v(const uint8_t * b, uint32_t qh, int j) {
+    if (j < 16) return (int)((b[6 + j] & 0x0F) | (((qh >> j) << 4) & 0x10)) - 16;
+    return (int)((b[6 + j - 16] >> 4) | ((qh >> (j - 4)) & 0x10)) - 16;
+}
+__device__ __forceinline__ uint32_t q5qh(const uint8_t * b) {
+    return b[2] | (b[3] << 8) | (b[4] << 16) | ((uint32_t)b[5] << 24);
+}
+
 __device__ void dq_block(int fmt, const uint8_t * b, float * o) {
-    // value formulas of dequant_chunk (src/runtime/kernels.h:182-240)
-    if (fmt == FMT_Q8_0) {
+    // value formulas of dequant_chunk (src/runtime/kernels.h:169-240)
+    if (fmt == FMT_Q5_0) {                 // one 32-element block
+        const float d = h2f(ld16u(b));
+        const uint32_t qh = q5qh(b);
+        for (int j = 0; j < 32; ++j) o[j] = d * (float)q5v(b, qh, j);
+    } else if (fmt == FMT_Q8_0) {
         const float d = h2f(ld16u(b));
         for (int j = 0; j < 32; ++j) o[j] = d * (float)(int8_t)b[2 + j];
     } else if (fmt == FMT_Q4_K) {
@@ -68,6 +82,13 @@ __device__ float canon_dot(int fmt, const uint8_t * row, const float * x, uint32
             const uint8_t * B = row + (size_t)b * 34;
             const float d = h2f(ld16u(B));
             for (int i = 0; i < 32; ++i) acc += d * (float)(int8_t)B[2 + i] * x[b * 32 + i];
+        }
+    } else if (fmt == FMT_Q5_0) {       // fl_dot_row_q5_0, src/runtime/quants.h:144-162
+        for (uint32_t b = 0; b < cols / 32; ++b) {
+            const uint8_t * B = row + (size_t)b * 22;
+            const float d = h2f(ld16u(B));
+            const uint32_t qh = q5qh(B);
+            for (int j = 0; j < 32; ++j) acc += d * (float)q5v(B, qh, j) * x[b * 32 + j];
         }
     } else if (fmt == FMT_Q4_K) {
         for (uint32_t sb = 0; sb < cols / 256; ++sb) {
@@ -138,12 +159,19 @@ __device__ float fast_dot(int fmt, const uint8_t * row, const float * x, uint32_
         }
         return tree16(L);
     }
-    const uint32_t bb = fmt == FMT_Q4_K ? 144 : 210;
+    // dot_row_fast_dequant (src/runtime/kernels.h:244-254): 256-element chunks
+    // (the last one shorter for Q5_0), each dequantised then dotted in the
+    // 16-lane order; chunk sums chained in order
     float acc = 0.f, buf[256];
     for (uint32_t e = 0; e < cols; e += 256) {
-        dq_block(fmt, row + (size_t)(e / 256) * bb, buf);
+        const uint32_t n = cols - e < 256 ? cols - e : 256;
+        if (fmt == FMT_Q5_0) {
+            for (uint32_t b = 0; b < n / 32; ++b) dq_block(fmt, row + (size_t)(e / 32 + b) * 22, buf + 32 * b);
+        } else {
+            dq_block(fmt, row + (size_t)(e / 256) * (fmt == FMT_Q4_K ? 144 : 210), buf);
+        }
         float L[16] = {0};
-        for (uint32_t k = 0; k < 256; k += 16)
+        for (uint32_t k = 0; k < n; k += 16)
             for (int j = 0; j < 16; ++j) L[j] += buf[k + j] * x[e + k + j];
         acc += tree16(L);
     }
@@ -158,6 +186,7 @@ __global__ void k_dot_f32(int fmt, DotArgs a) {
     const uint8_t * w = a.w + (a.id_slot ? (size_t)(*a.id_slot) * a.estride : 0);
     const uint64_t rb = fmt == FMT_F32 ? (uint64_t)a.cols * 4
                       : fmt == FMT_Q8_0 ? (uint64_t)(a.cols / 32) * 34
+                      : fmt == FMT_Q5_0 ? (uint64_t)(a.cols / 32) * 22
                       : (uint64_t)(a.cols / 256) * (fmt == FMT_Q4_K ? 144 : 210);
     const float * x = a.x + (size_t)p * a.xstride;
     const float v = FAST ? fast_dot(fmt, w + r * rb, x, a.cols) : canon_dot(fmt, w + r * rb, x, a.cols);
@@ -166,7 +195,7 @@ __global__ void k_dot_f32(int fmt, DotArgs a) {
 }
 
 static int launch_f32(bool fast, int fmt, const DotArgs & a, hipStream_t s) {
-    if (fmt != FMT_F32 && fmt != FMT_Q8_0 && fmt != FMT_Q4_K && fmt != FMT_Q6_K)
+    if (fmt != FMT_F32 && fmt != FMT_Q8_0 && fmt != FMT_Q5_0 && fmt != FMT_Q4_K && fmt != FMT_Q6_K)
         return set_error(FLH_ERR_UNSUPPORTED, "fp32 dot: format not supported");
     const uint64_t n = (uint64_t)a.rows * a.nx;
     if (n == 0) return FLH_OK;

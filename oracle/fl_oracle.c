@@ -117,6 +117,18 @@ static void dq_q4_K(const uint8_t * b, float * o) {
         for (int l = 0; l < 32; ++l) o[64 * c + 32 + l] = d2 * (float)(q[32 * c + l] >> 4) - mm2;
     }
 }
+/* Q5_0 element j of a block: 4 bits from qs, the 5th from qh (bit j) minus 16
+ * (src/runtime/kernels.h:169-180, quants.h:144-162) */
+static int q5_val(const uint8_t * b, int j) {
+    const uint32_t qh = (uint32_t)b[2] | ((uint32_t)b[3] << 8) | ((uint32_t)b[4] << 16) | ((uint32_t)b[5] << 24);
+    const uint8_t * qs = b + 6;
+    if (j < 16) return (int)((qs[j] & 0x0F) | (((qh >> j) << 4) & 0x10)) - 16;
+    return (int)((qs[j - 16] >> 4) | ((qh >> (j - 16 + 12)) & 0x10)) - 16;
+}
+static void dq_q5_0(const uint8_t * b, float * o) {
+    const float d = orc_half2float(rd16(b));
+    for (int j = 0; j < 32; ++j) o[j] = d * (float)q5_val(b, j);
+}
 /* the 6-bit value of Q6_K element (half h, group g in 0..3, position l) */
 static int q6_val(const uint8_t * b, int h, int g, int l) {
     const uint8_t * ql = b + 64 * h, * qh = b + 128 + 32 * h;
@@ -143,6 +155,7 @@ void orc_dequant_chunk(int fmt, const uint8_t * row, uint32_t elem0,
         const uint8_t * blk = bp + (size_t)b * bb;
         float * o = out + (size_t)b * be;
         if (fmt == ORC_Q8_0) dq_q8_0(blk, o);
+        else if (fmt == ORC_Q5_0) dq_q5_0(blk, o);
         else if (fmt == ORC_Q4_K) dq_q4_K(blk, o);
         else if (fmt == ORC_Q6_K) dq_q6_K(blk, o);
     }
@@ -162,6 +175,16 @@ static float dot_row_q8_0(const uint8_t * row, const float * x, uint32_t cols) {
         const uint8_t * B = row + (size_t)b * 34;
         const float d = orc_half2float(rd16(B));
         for (int i = 0; i < 32; ++i) acc += d * (float)(int8_t)B[2 + i] * x[b * 32 + i];
+    }
+    return acc;
+}
+/* src/runtime/quants.h:144-162: elements 0..15 (low nibbles) then 16..31 */
+static float dot_row_q5_0(const uint8_t * row, const float * x, uint32_t cols) {
+    float acc = 0.f;
+    for (uint32_t b = 0; b < cols / 32; ++b) {
+        const uint8_t * B = row + (size_t)b * 22;
+        const float d = orc_half2float(rd16(B));
+        for (int j = 0; j < 32; ++j) acc += d * (float)q5_val(B, j) * x[b * 32 + j];
     }
     return acc;
 }
@@ -207,6 +230,7 @@ float orc_dot_row(int fmt, const uint8_t * row, const float * x, uint32_t cols) 
             return acc;
         }
         case ORC_Q8_0: return dot_row_q8_0(row, x, cols);
+        case ORC_Q5_0: return dot_row_q5_0(row, x, cols);
         case ORC_Q4_K: return dot_row_q4_K(row, x, cols);
         case ORC_Q6_K: return dot_row_q6_K(row, x, cols);
     }
@@ -310,6 +334,22 @@ float orc_dot_i8_q8_0(const uint8_t * row, const uint8_t * xq, uint32_t cols) {
         for (int i = 0; i < 32; ++i) idot += (int)(int8_t)W[2 + i] * (int)(int8_t)X[4 + i];
         a[b & 3] = fmaf(orc_half2float(rd16(W)) * orc_half2float(rd16(X)),
                         (float)idot, a[b & 3]);
+    }
+    return fold4(a);
+}
+/* src/runtime/quants.h:449-466: per block idot over the 5-bit values
+ * (unshifted), isum over the activation; term (idot - 16 * isum) */
+float orc_dot_i8_q5_0(const uint8_t * row, const uint8_t * xq, uint32_t cols) {
+    float a[4] = {0.f, 0.f, 0.f, 0.f};
+    for (uint32_t b = 0; b < cols / 32; ++b) {
+        const uint8_t * W = row + (size_t)b * 22, * X = xq + (size_t)b * 36;
+        int idot = 0, isum = 0;
+        for (int i = 0; i < 32; ++i) {
+            idot += (q5_val(W, i) + 16) * (int)(int8_t)X[4 + i];
+            isum += (int)(int8_t)X[4 + i];
+        }
+        a[b & 3] = fmaf(orc_half2float(rd16(W)) * orc_half2float(rd16(X)),
+                        (float)(idot - 16 * isum), a[b & 3]);
     }
     return fold4(a);
 }
@@ -420,6 +460,7 @@ static float one_dot(int fmt, const uint8_t * row, const float * x, uint32_t col
         const uint8_t * xq = (const uint8_t *)x + orc_xq_offset(cols);
         switch (fmt) {
             case ORC_Q8_0: return orc_dot_i8_q8_0(row, xq, cols);
+            case ORC_Q5_0: return orc_dot_i8_q5_0(row, xq, cols);
             case ORC_Q4_K: return orc_dot_i8_q4_K(row, xq, cols);
             case ORC_Q6_K: return orc_dot_i8_q6_K(row, xq, cols);
             default: return 0.f;

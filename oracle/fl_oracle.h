@@ -65,6 +65,7 @@ void orc_quantize_q8_K_block(const float * x, uint8_t * o292);
 void orc_act_q8(float * x, uint32_t cols);
 
 float orc_dot_i8_q8_0(const uint8_t * row, const uint8_t * xq, uint32_t cols);
+float orc_dot_i8_q5_0(const uint8_t * row, const uint8_t * xq, uint32_t cols);
 float orc_dot_i8_q4_K(const uint8_t * row, const uint8_t * xq, uint32_t cols);
 float orc_dot_i8_q6_K(const uint8_t * row, const uint8_t * xq, uint32_t cols);
 float orc_dot_i8k_q4_K(const uint8_t * row, const uint8_t * xk, uint32_t cols);

@@ -20,7 +20,7 @@ ORACLE_SO = os.path.join(HERE, "liboracle.so")
 REF_SO = os.path.join(HERE, "_ref", "libflref.so")
 
 F32, Q8_0, Q5_0, Q4_K, Q6_K = 0, 1, 2, 3, 4
-BLK = {F32: (1, 4), Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}
+BLK = {F32: (1, 4), Q8_0: (32, 34), Q5_0: (32, 22), Q4_K: (256, 144), Q6_K: (256, 210)}
 
 
 def row_bytes(fmt, cols):
@@ -87,7 +87,8 @@ class Oracle:
             self._sdmt.restype = None
             self._sdmt.argtypes = [_I, _P, _U32, _U32, _P, _P, _U32, _U32, _U32, _I, _U32, _U32, _I]
             for n, args, res in [
-                ("orc_dot_i8_q8_0", [_P, _P, _U32], _F), ("orc_dot_i8k_q4_K", [_P, _P, _U32], _F),
+                ("orc_dot_i8_q8_0", [_P, _P, _U32], _F), ("orc_dot_i8_q5_0", [_P, _P, _U32], _F),
+                ("orc_dot_i8k_q4_K", [_P, _P, _U32], _F),
                 ("orc_dot_i8k_q6_K", [_P, _P, _U32], _F), ("orc_dot_i8_q4_K", [_P, _P, _U32], _F),
                 ("orc_dot_i8_q6_K", [_P, _P, _U32], _F), ("orc_dot_row", [_I, _P, _P, _U32], _F),
                 ("orc_q4k_scale_min", [_I, _P, _P, _P], None),

@@ -23,7 +23,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(os.path.dirname(HERE))
 sys.path.insert(0, os.path.join(ROOT, "oracle"))
-from oracle import Oracle, row_bytes, col_stride_floats, F32, Q8_0, Q4_K, Q6_K  # noqa: E402
+from oracle import Oracle, row_bytes, col_stride_floats, F32, Q8_0, Q5_0, Q4_K, Q6_K  # noqa: E402
 
 REF = "/root/reference"
 
@@ -31,7 +31,7 @@ REF = "/root/reference"
 def sane_rows(fmt, rows, cols, rng):
     """Random block bytes with finite fp16 scales (small positive halves)."""
     w = rng.integers(0, 256, size=rows * row_bytes(fmt, cols), dtype=np.uint8)
-    bb = {Q8_0: 34, Q4_K: 144, Q6_K: 210}[fmt]
+    bb = {Q8_0: 34, Q5_0: 22, Q4_K: 144, Q6_K: 210}[fmt]
     blocks = w.reshape(-1, bb)
     def half():
         return (0x2000 | (rng.integers(0, 1 << 16, size=blocks.shape[0]) & 0x0BFF)).astype(np.uint16)
@@ -171,6 +171,35 @@ def main():
     add1 = rng.standard_normal(4096).astype(np.float32)
     out.update({"wm_parts": parts, "wm_gates": gates, "wm_add1": add1,
                 "wm_y": ref.wmerge(parts, gates, add1=add1, scale=1.0)})
+
+    # ---- Q5_0 (own RNG stream, so the cases above keep their bytes): dequant
+    # and every STREAM_DOT routing mode; cols 1408 = 5.5 chunks of 256 also
+    # covers the fast path's partial last dequant chunk (kernels.h:244-254)
+    rng5 = np.random.default_rng(20261202)
+    w = sane_rows(Q5_0, 3, 1408, rng5)
+    out["dq5_w"], out["dq5_out"] = w, ref.dequant(Q5_0, w, 3, 1408)
+    n5 = 0
+    for cols in (512, 1408):
+        for mode in ("i8", "f32fast", "canon"):
+            for nx in (1, 3):
+                rows = 7
+                w = sane_rows(Q5_0, rows, cols, rng5)
+                xs = xs_for(cols, nx, rng5, outliers=(n5 % 2 == 0))
+                st = col_stride_floats(cols)
+                xbuf = np.zeros(nx * st, dtype=np.float32)
+                for p in range(nx):
+                    col = ref.act_q8(xs[p])
+                    xbuf[p * st:p * st + col.size // 4] = col.view(np.float32)
+                y0 = rng5.standard_normal(nx * rows).astype(np.float32)
+                y = y0.copy()
+                fast, i8, i8k = modes[mode]
+                ref.stream_dot(Q5_0, w, rows, cols, xbuf, y, nx=nx, xstride=st, ystride=rows,
+                               fast=fast, i8_mask=i8, i8k_mask=i8k)
+                key = f"q5dot{n5}"
+                out[key + "_meta"] = np.array([Q5_0, cols, rows, nx, st, fast, i8, i8k], dtype=np.int64)
+                out[key + "_w"], out[key + "_x"], out[key + "_y0"], out[key + "_y"] = w, xbuf, y0, y
+                n5 += 1
+    out["q5dot_count"] = np.array([n5])
 
     np.savez_compressed(os.path.join(HERE, "golden_ref.npz"), **out)
     with open(os.path.join(HERE, "task_layout.json"), "w") as fh:

@@ -48,6 +48,21 @@ def test_stream_dot_every_mode_matches_reference(orc, golden):
         assert np.array_equal(bits(y), bits(golden[f"dot{i}_y"])), (i, fmt, cols, nx, fast, i8, i8k)
 
 
+def test_q5_0_dequant_and_dots_match_reference(orc, golden):
+    """Q5_0: bit-exact dequant and every routing mode (q8_1 int8, fast fp32
+    with a partial last 256-chunk, canonical) vs the reference's own code."""
+    got = orc.dequant(2, golden["dq5_w"], 3, 1408)
+    assert np.array_equal(bits(got), bits(golden["dq5_out"]))
+    n = int(golden["q5dot_count"][0])
+    assert n == 12
+    for i in range(n):
+        fmt, cols, rows, nx, st, fast, i8, i8k = (int(v) for v in golden[f"q5dot{i}_meta"])
+        y = golden[f"q5dot{i}_y0"].copy()
+        orc.stream_dot(fmt, golden[f"q5dot{i}_w"], rows, cols, golden[f"q5dot{i}_x"], y, nx=nx,
+                       xstride=st, ystride=rows, fast=fast, i8_mask=i8, i8k_mask=i8k)
+        assert np.array_equal(bits(y), bits(golden[f"q5dot{i}_y"])), (i, cols, nx, fast, i8)
+
+
 def test_stream_dot_idx_matches_reference(orc, golden):
     from oracle import row_bytes
     y = np.zeros(5, dtype=np.float32)

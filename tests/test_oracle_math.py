@@ -19,7 +19,7 @@ from fractions import Fraction
 import numpy as np
 import pytest
 
-from oracle import Q8_0, Q4_K, Q6_K, row_bytes, xq_offset, xqk_offset
+from oracle import Q8_0, Q5_0, Q4_K, Q6_K, row_bytes, xq_offset, xqk_offset
 from util import sane_rows
 
 
@@ -61,6 +61,16 @@ def deq_reference_numpy(fmt, w, rows, cols):
         d = h16(B[:, 0:2])[:, 0]
         q = B[:, 2:].view(np.int8).astype(np.float32)
         return (d[:, None] * q).reshape(rows, cols)
+    if fmt == Q5_0:
+        B = w.reshape(rows * cols // 32, 22)
+        d = h16(B[:, 0:2])[:, 0]
+        qh = B[:, 2:6].copy().view("<u4")[:, 0].astype(np.uint64)
+        qs = B[:, 6:22].astype(np.uint64)
+        j = np.arange(16, dtype=np.uint64)
+        lo = (qs & 0xF) | (((qh[:, None] >> j) & 1) << 4)           # element j: bit j of qh
+        hi = (qs >> 4) | (((qh[:, None] >> (j + 16)) & 1) << 4)     # element 16 + j: bit 16 + j
+        q = np.concatenate([lo, hi], axis=1).astype(np.float32) - 16.0
+        return (d[:, None] * q).reshape(rows, cols)
     if fmt == Q4_K:
         B = w.reshape(rows * cols // 256, 144)
         d, dmin = h16(B[:, 0:2])[:, 0], h16(B[:, 2:4])[:, 0]
@@ -93,7 +103,7 @@ def deq_reference_numpy(fmt, w, rows, cols):
     return out.reshape(rows, cols)
 
 
-@pytest.mark.parametrize("fmt", [Q8_0, Q4_K, Q6_K])
+@pytest.mark.parametrize("fmt", [Q8_0, Q5_0, Q4_K, Q6_K])
 def test_dequant_matches_format_definition(orc, fmt):
     rng = np.random.default_rng(fmt)
     rows, cols = 7, 1024
@@ -245,8 +255,25 @@ def i8_q80_replay(row, xq, cols):
     return fold4(a)
 
 
+def i8_q50_replay(row, xq, cols):
+    """fl_dot_i8_q5_0's contract (quants.h:449-466) restated from scratch:
+    per block, the exact integer sum of (5-bit value - 16) * x, scaled by
+    d_w * d_x (exact product of two halves), chained with fmaf into a4[b & 3]."""
+    nb = cols // 32
+    B = row.reshape(nb, 22)
+    X = xq.reshape(nb, 36)
+    d = h16(B[:, 0:2])[:, 0]
+    q = deq_reference_numpy(Q5_0, row, 1, cols).reshape(nb, 32) / d[:, None]   # exact: q * d / d
+    t = (np.rint(q).astype(np.int64) * X[:, 4:].view(np.int8).astype(np.int64)).sum(axis=1)
+    dd = d * h16(X[:, 0:2])[:, 0]
+    a = [np.float32(0)] * 4
+    for b in range(nb):
+        a[b & 3] = fmaf(np.float32(dd[b]), np.float32(t[b]), a[b & 3])
+    return fold4(a)
+
+
 @pytest.mark.parametrize("fmt,cols", [(Q4_K, 512), (Q4_K, 2816), (Q6_K, 1024), (Q6_K, 2304),
-                                      (Q8_0, 512), (Q8_0, 1056)])
+                                      (Q8_0, 512), (Q8_0, 1056), (Q5_0, 512), (Q5_0, 1408)])
 def test_int8_dot_replay_bitwise(orc, fmt, cols):
     rng = np.random.default_rng(fmt * 7 + cols)
     rows = 5
@@ -263,6 +290,8 @@ def test_int8_dot_replay_bitwise(orc, fmt, cols):
             got, want = orc.dot_i8k_q4_K(row.ctypes.data, xk.ctypes.data, cols), i8k_q4k_replay(row, xk, cols)
         elif fmt == Q6_K:
             got, want = orc.dot_i8k_q6_K(row.ctypes.data, xk.ctypes.data, cols), i8k_q6k_replay(row, xk, cols)
+        elif fmt == Q5_0:
+            got, want = orc.dot_i8_q5_0(row.ctypes.data, xq.ctypes.data, cols), i8_q50_replay(row, xq, cols)
         else:
             got, want = orc.dot_i8_q8_0(row.ctypes.data, xq.ctypes.data, cols), i8_q80_replay(row, xq, cols)
         assert np.float32(got).view(np.uint32) == np.float32(want).view(np.uint32), (r, got, want)
