@@ -178,6 +178,82 @@ __device__ float fast_dot(int fmt, const uint8_t * row, const float * x, uint32_
     return acc;
 }
 
+// K formats on the q8_1 int8 path (i8 mask bit set, i8k bit clear):
+// fl_dot_i8_q4_K / fl_dot_i8_q6_K (src/runtime/quants.h:468-526), exact
+// integer group sums, two (Q4_K) or per-16 (Q6_K) fmaf terms per 32-element
+// block into acc[. & 3], fold (a0 + a1) + (a2 + a3).  The reference's default
+// masks never route here; one thread per (row, column), bitwise.
+__device__ float q81k_dot(int fmt, const uint8_t * row, const uint8_t * xq, uint32_t cols) {
+    float a[4] = {0.f, 0.f, 0.f, 0.f};
+    for (uint32_t sb = 0; sb < cols / 256; ++sb) {
+        if (fmt == FMT_Q4_K) {
+            const uint8_t * W = row + (size_t)sb * 144;
+            const float d = h2f(ld16u(W)), dmin = h2f(ld16u(W + 2));
+            const uint8_t * s = W + 4;
+            for (int g = 0; g < 8; ++g) {
+                uint32_t sc, mn;
+                if (g < 4) { sc = s[g] & 63; mn = s[g + 4] & 63; }
+                else { sc = (s[g + 4] & 0xF) | ((s[g - 4] >> 6) << 4); mn = (s[g + 4] >> 4) | ((s[g] >> 6) << 4); }
+                const uint8_t * q = W + 16 + (g / 2) * 32;
+                const uint8_t * X = xq + (size_t)(sb * 8 + g) * 36;
+                int idot = 0, isum = 0;
+                for (int i = 0; i < 32; ++i) {
+                    const int w4 = (g & 1) ? (q[i] >> 4) : (q[i] & 0xF);
+                    idot += w4 * (int8_t)X[4 + i];
+                    isum += (int8_t)X[4 + i];
+                }
+                const float dx = h2f(ld16u(X));
+                a[g & 3] = fmaf(d * (float)sc * dx, (float)idot, a[g & 3]);
+                a[g & 3] = fmaf(-(dmin * (float)mn) * dx, (float)isum, a[g & 3]);
+            }
+        } else {
+            const uint8_t * W = row + (size_t)sb * 210;
+            const float d = h2f(ld16u(W + 208));
+            const int8_t * sc = (const int8_t *)(W + 192);
+            for (int h = 0; h < 2; ++h)
+                for (int g = 0; g < 4; ++g) {
+                    const uint8_t * X = xq + (size_t)(sb * 8 + h * 4 + g) * 36;
+                    const float dx = h2f(ld16u(X));
+                    for (int k = 0; k < 2; ++k) {
+                        int idot = 0, isum = 0;
+                        for (int i = 0; i < 16; ++i) {
+                            const int e = 16 * k + i;
+                            const uint8_t lb = W[64 * h + e + 32 * (g & 1)];
+                            const int q6 = ((g < 2) ? (lb & 0xF) : (lb >> 4)) |
+                                           (((W[128 + 32 * h + e] >> (2 * g)) & 3) << 4);
+                            idot += q6 * (int8_t)X[4 + e];
+                            isum += (int8_t)X[4 + e];
+                        }
+                        const int t = (int)sc[8 * h + 2 * g + k] * (idot - 32 * isum);
+                        const int ti = 8 * h + 2 * g + k;
+                        a[ti & 3] = fmaf(d * dx, (float)t, a[ti & 3]);
+                    }
+                }
+        }
+    }
+    return (a[0] + a[1]) + (a[2] + a[3]);
+}
+
+__global__ void k_dot_q81k(int fmt, DotArgs a) {
+    const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= (uint64_t)a.rows * a.nx) return;
+    const uint32_t r = (uint32_t)(t % a.rows), p = (uint32_t)(t / a.rows);
+    const uint8_t * w = a.w + (a.id_slot ? (size_t)(*a.id_slot) * a.estride : 0);
+    const uint64_t rb = (uint64_t)(a.cols / 256) * (fmt == FMT_Q4_K ? 144 : 210);
+    const uint8_t * xq = (const uint8_t *)(a.x + (size_t)p * a.xstride) + xq_off(a.cols);
+    const float v = q81k_dot(fmt, w + r * rb, xq, a.cols);
+    float * y = a.y + (size_t)p * a.ystride + r;
+    *y = *y + v;
+}
+
+int launch_dot_i8_k(int fmt, const DotArgs & a, hipStream_t s) {
+    if (fmt != FMT_Q4_K && fmt != FMT_Q6_K) return set_error(FLH_ERR_UNSUPPORTED, "q8_1 K-format dot: Q4_K / Q6_K only");
+    const uint64_t n = (uint64_t)a.rows * a.nx;
+    if (n == 0) return FLH_OK;
+    hipLaunchKernelGGL(k_dot_q81k, dim3((uint32_t)((n + 63) / 64)), dim3(64), 0, s, fmt, a);
+    return hip_check(hipGetLastError(), "k_dot_q81k launch");
+}
+
 template <bool FAST>
 __global__ void k_dot_f32(int fmt, DotArgs a) {
     const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;

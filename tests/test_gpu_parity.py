@@ -206,8 +206,6 @@ def test_i8k_golden_vectors(flh, gpu, golden):
     for i in range(n):
         fmt, cols, rows, nx, st, fast, i8, i8k = (int(v) for v in golden[f"dot{i}_meta"])
         say("golden dot", i, fmt, cols, nx, fast, i8, i8k)
-        if fast and i8 and not i8k and fmt != Q8_0:
-            continue                  # q8_1 path for K formats: not implemented on the GPU
         xb = golden[f"dot{i}_x"]
         dx = flh.DeviceBuffer.from_array(xb, gpu)
         dw = flh.DeviceBuffer.from_array(golden[f"dot{i}_w"], gpu)
@@ -217,7 +215,20 @@ def test_i8k_golden_vectors(flh, gpu, golden):
         got = dy.download(np.float32, nx * rows, gpu)
         assert np.array_equal(bits(got), bits(golden[f"dot{i}_y"])), i
         done += 1
-    assert done >= 30
+    assert done == n
+
+
+@pytest.mark.parametrize("fmt", [Q4_K, Q6_K])
+@pytest.mark.parametrize("rows,cols,nx", [(7, 256, 1), (33, 2816, 1), (19, 4096, 3), (5, 14336, 2)])
+def test_k_formats_on_q8_1_path_bitwise(flh, orc, gpu, fmt, rows, cols, nx):
+    """Non-default masks (i8 bit without the i8k bit) route K formats to
+    fl_dot_i8_q4_K / fl_dot_i8_q6_K (src/runtime/quants.h:468-526)."""
+    say("q8_1 K path", fmt, rows, cols, nx)
+    rng = np.random.default_rng(fmt * 31 + cols + nx)
+    w = sane_rows(fmt, rows, cols, rng)
+    xs = activations(nx, cols, rng, outliers=True)
+    got, want = run_dot(flh, orc, gpu, fmt, w, rows, cols, xs, mode="q81")
+    assert np.array_equal(bits(got), bits(want))
 
 
 @pytest.mark.parametrize("mode", ["f32fast", "canon"])
