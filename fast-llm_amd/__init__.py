@@ -54,7 +54,8 @@ BLK_BYTES = {Fmt.F32: 4, Fmt.Q8_0: 34, Fmt.Q5_0: 22, Fmt.Q4_K: 144, Fmt.Q6_K: 21
              Fmt.IQ2_XXS: 66, Fmt.IQ3_XXS: 98}
 MAX_DOT_COLS = 16
 
-OK, ERR_ARG, ERR_HIP, ERR_UNSUPPORTED, ERR_NOMEM, ERR_STATE = 0, -1, -2, -3, -4, -5
+OK, ERR_ARG, ERR_HIP, ERR_UNSUPPORTED, ERR_NOMEM, ERR_STATE, ERR_IO, ERR_FORMAT = \
+    0, -1, -2, -3, -4, -5, -6, -7
 
 # reference CPU default masks (src/runtime/kernels.h:920,937)
 I8_MASK_DEFAULT = (1 << Fmt.Q8_0) | (1 << Fmt.Q5_0) | (1 << Fmt.Q4_K) | (1 << Fmt.Q6_K)
@@ -114,6 +115,22 @@ class WmergeP(C.Structure):
                 ("n_parts", C.c_uint32), ("n", C.c_uint32), ("n_full", C.c_uint32)]
 
 
+class GgufTensorInfo(C.Structure):
+    """flh_gguf_tensor (GgufTensor, src/model/gguf.h:19-27)."""
+    _fields_ = [("name", C.c_void_p), ("name_len", C.c_size_t), ("type", C.c_uint32),
+                ("fmt", C.c_int32), ("n_dims", C.c_int32), ("ne", C.c_uint64 * 4),
+                ("offset", C.c_uint64), ("nbytes", C.c_uint64), ("shard", C.c_int32),
+                ("data", C.c_void_p)]
+
+
+class WeightInfo(C.Structure):
+    """flh_weight (WTensor as DecoderImpl::load_tensor fills it,
+    src/model/decoder.cpp:186-206)."""
+    _fields_ = [("fmt", C.c_int32), ("rows", C.c_uint32), ("cols", C.c_uint32),
+                ("nexp", C.c_uint32), ("row_bytes", C.c_uint64), ("w_bytes", C.c_uint64),
+                ("estride", C.c_uint64), ("host", C.c_void_p), ("tensor", C.c_uint64)]
+
+
 class FlhError(RuntimeError):
     def __init__(self, code: int, msg: str):
         super().__init__(f"fastllm_hip error {code}: {msg}")
@@ -166,6 +183,24 @@ _SIGS = {
     "flh_fill_normal": (_I, [_P, _SZ, _U64, _F, _F, _F, _F, _P]),
     "flh_quantize": (_I, [_I, _P, _U32, _U32, _P, _P]),
     "flh_quantize_host": (_I, [_I, _P, _U32, _U32, _P]),
+    "flh_gguf_open": (_I, [C.c_char_p, C.POINTER(_P)]),
+    "flh_gguf_close": (_I, [_P]),
+    "flh_gguf_alignment": (_U32, [_P]),
+    "flh_gguf_n_shards": (_I, [_P]),
+    "flh_gguf_n_tensors": (_U64, [_P]),
+    "flh_gguf_tensor_info": (_I, [_P, _U64, C.POINTER(GgufTensorInfo)]),
+    "flh_gguf_find": (C.c_int64, [_P, C.c_char_p]),
+    "flh_gguf_fmt_of": (_I, [_U32]),
+    "flh_gguf_type_name": (C.c_char_p, [_U32]),
+    "flh_gguf_has": (_I, [_P, C.c_char_p]),
+    "flh_gguf_kv_i": (C.c_int64, [_P, C.c_char_p, C.c_int64]),
+    "flh_gguf_kv_f": (C.c_double, [_P, C.c_char_p, C.c_double]),
+    "flh_gguf_kv_s": (_P, [_P, C.c_char_p, C.c_char_p, C.POINTER(_SZ)]),
+    "flh_gguf_kv_sarr_len": (C.c_int64, [_P, C.c_char_p]),
+    "flh_gguf_kv_sarr_at": (_P, [_P, C.c_char_p, _U64, C.POINTER(_SZ)]),
+    "flh_gguf_weight": (_I, [_P, C.c_char_p, C.POINTER(WeightInfo)]),
+    "flh_gguf_upload": (_I, [_P, _U64, _P, _U64, _P]),
+    "flh_gguf_upload_all": (_I, [_P, _P, C.POINTER(_P), _P]),
 }
 
 
@@ -409,3 +444,160 @@ def quantize_host(fmt: int, w: np.ndarray) -> np.ndarray:
     out = np.zeros(rows * row_bytes(fmt, cols), dtype=np.uint8)
     check(lib().flh_quantize_host(int(fmt), w.ctypes.data, rows, cols, out.ctypes.data))
     return out
+
+
+# --------------------------------------------------------------- arena --
+class Arena:
+    """Device bump arena (flh_arena_*; Arena, src/runtime/arena.cpp:54-74)."""
+
+    def __init__(self, nbytes: int):
+        h = C.c_void_p()
+        check(lib().flh_arena_create(int(nbytes), C.byref(h)))
+        self.handle = h.value
+
+    def alloc(self, nbytes: int, align: int = 256) -> int:
+        p = C.c_void_p()
+        check(lib().flh_arena_alloc(self.handle, int(nbytes), int(align), C.byref(p)))
+        return p.value
+
+    @property
+    def used(self) -> int:
+        return lib().flh_arena_used(self.handle)
+
+    def close(self):
+        if self.handle:
+            check(lib().flh_arena_destroy(self.handle))
+            self.handle = None
+
+
+# ---------------------------------------------------------------- GGUF --
+class GgufTensor:
+    """One tensor info; `data` is a read-only uint8 view of the mapping."""
+
+    def __init__(self, g: "Gguf", index: int, ti: GgufTensorInfo):
+        self.index = index
+        self.name = C.string_at(ti.name, ti.name_len).decode("utf-8", "surrogateescape")
+        self.type = ti.type
+        self.fmt = ti.fmt
+        self.n_dims = ti.n_dims
+        self.ne = tuple(ti.ne)
+        self.offset = ti.offset
+        self.nbytes = ti.nbytes
+        self.shard = ti.shard
+        self.address = ti.data
+        self._g = g
+
+    @property
+    def data(self) -> np.ndarray:
+        if self.nbytes == 0:
+            return np.zeros(0, dtype=np.uint8)
+        buf = (C.c_uint8 * self.nbytes).from_address(self.address)
+        a = np.frombuffer(buf, dtype=np.uint8)
+        a.flags.writeable = False
+        return a
+
+
+class Gguf:
+    """GGUF reader over the C-ABI (fastllm::Gguf, src/model/gguf.h:28-79).
+
+    Same method names as the reference: open (the constructor), tensors,
+    find, data, alignment, n_shards, has, kv_i, kv_f, kv_s, kv_sarr, fmt_of,
+    type_name.  Errors raise FlhError (ERR_IO for a missing file or shard,
+    ERR_FORMAT for a malformed one) where the reference returns false or
+    aborts.  Parsing is host-only; upload / upload_all copy to the device.
+    """
+
+    def __init__(self, path: str):
+        h = C.c_void_p()
+        check(lib().flh_gguf_open(os.fsencode(path), C.byref(h)))
+        self.handle = h.value
+        L = lib()
+        self._tensors = []
+        for i in range(L.flh_gguf_n_tensors(self.handle)):
+            ti = GgufTensorInfo()
+            check(L.flh_gguf_tensor_info(self.handle, i, C.byref(ti)))
+            self._tensors.append(GgufTensor(self, i, ti))
+
+    def close(self):
+        if self.handle:
+            lib().flh_gguf_close(self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+        return False
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def tensors(self) -> list:
+        return list(self._tensors)
+
+    def find(self, name: str) -> GgufTensor | None:
+        i = lib().flh_gguf_find(self.handle, name.encode())
+        return None if i < 0 else self._tensors[i]
+
+    def data(self, t: GgufTensor) -> np.ndarray:
+        return t.data
+
+    def alignment(self) -> int:
+        return lib().flh_gguf_alignment(self.handle)
+
+    def n_shards(self) -> int:
+        return lib().flh_gguf_n_shards(self.handle)
+
+    def has(self, key: str) -> bool:
+        return bool(lib().flh_gguf_has(self.handle, key.encode()))
+
+    def kv_i(self, key: str, dflt: int) -> int:
+        return lib().flh_gguf_kv_i(self.handle, key.encode(), int(dflt))
+
+    def kv_f(self, key: str, dflt: float) -> float:
+        return lib().flh_gguf_kv_f(self.handle, key.encode(), float(dflt))
+
+    def kv_s(self, key: str, dflt: str = "") -> str:
+        n = C.c_size_t()
+        p = lib().flh_gguf_kv_s(self.handle, key.encode(), dflt.encode(), C.byref(n))
+        return C.string_at(p, n.value).decode("utf-8", "surrogateescape")
+
+    def kv_sarr(self, key: str) -> list | None:
+        L = lib()
+        n = L.flh_gguf_kv_sarr_len(self.handle, key.encode())
+        if n < 0:
+            return None
+        out, ln = [], C.c_size_t()
+        for i in range(n):
+            p = L.flh_gguf_kv_sarr_at(self.handle, key.encode(), i, C.byref(ln))
+            out.append(C.string_at(p, ln.value).decode("utf-8", "surrogateescape"))
+        return out
+
+    @staticmethod
+    def fmt_of(ggml_type: int) -> int | None:
+        f = lib().flh_gguf_fmt_of(ggml_type)
+        return None if f < 0 else f
+
+    @staticmethod
+    def type_name(ggml_type: int) -> str:
+        return lib().flh_gguf_type_name(ggml_type).decode()
+
+    def weight(self, name: str) -> WeightInfo:
+        w = WeightInfo()
+        check(lib().flh_gguf_weight(self.handle, name.encode(), C.byref(w)))
+        return w
+
+    def upload(self, t: GgufTensor, dst, stream: Stream, dst_bytes: int | None = None) -> None:
+        n = t.nbytes if dst_bytes is None else dst_bytes
+        check(lib().flh_gguf_upload(self.handle, t.index, _p(dst), n, stream.handle))
+
+    def upload_all(self, arena: Arena, stream: Stream) -> list:
+        """Device pointer per tensor (None where the payload size is unknown)."""
+        n = len(self._tensors)
+        ptrs = (C.c_void_p * max(n, 1))()
+        check(lib().flh_gguf_upload_all(self.handle, arena.handle, ptrs, stream.handle))
+        return [ptrs[i] for i in range(n)]

@@ -51,6 +51,7 @@ static int need_init() {
     if (g_device < 0) return set_error(FLH_ERR_STATE, "flh_init() has not been called");
     return FLH_OK;
 }
+int need_device() { return need_init(); }
 
 // freeze()-style validation of one dot tile (src/runtime/graph.cpp:84-90)
 static int validate_dot(int fmt, const void * w, uint64_t w_bytes, uint32_t rows, uint32_t cols,

@@ -10,4 +10,6 @@ int set_error(int code, const char * msg);
 // 0 when e == hipSuccess, else records "<what>: <hip error string>" and
 // returns FLH_ERR_HIP.
 int hip_check(hipError_t e, const char * what);
+// FLH_OK once flh_init has selected a device, else FLH_ERR_STATE.
+int need_device();
 }  // namespace flh

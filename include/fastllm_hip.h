@@ -35,7 +35,9 @@ enum {
     FLH_ERR_HIP = -2,          /* HIP runtime error */
     FLH_ERR_UNSUPPORTED = -3,  /* task kind / format / shape not implemented */
     FLH_ERR_NOMEM = -4,        /* arena exhausted or hipMalloc failed */
-    FLH_ERR_STATE = -5         /* flh_init not called / no device */
+    FLH_ERR_STATE = -5,        /* flh_init not called / no device */
+    FLH_ERR_IO = -6,           /* file missing or unreadable (GGUF) */
+    FLH_ERR_FORMAT = -7        /* malformed GGUF file */
 };
 
 /* TaskKind values (include/fastllm/fastllm.h:19-45), stable. */
@@ -249,6 +251,90 @@ int flh_wmerge(const float * parts, const float * gates, const float * add1,
                const float * add2, float * y, float scale, uint32_t n_parts,
                uint32_t n, uint32_t n_full, uint32_t ncol, uint32_t pstride,
                uint32_t ystride, void * stream);
+
+/* ---------------------------------------------------------------- GGUF -- */
+/* GGUF v2/v3 reader (replaces fastllm::Gguf, src/model/gguf.h:28-79,
+ * src/model/gguf.cpp:133-303).  The file is mmapped read-only; metadata and
+ * tensor infos are parsed at open.  Split models named
+ * "<stem>-NNNNN-of-MMMMM.gguf" map every shard: metadata comes from the shard
+ * named, tensors are merged in shard order, each with offsets relative to its
+ * own shard's data section; split.tensors.count, when present, must equal the
+ * tensors mapped.  Where Gguf::open aborts (bad magic / version / KV type /
+ * n_dims, truncation) this returns FLH_ERR_FORMAT; a missing file or shard
+ * gives FLH_ERR_IO (Gguf::open returns false).  Stricter than the reference:
+ * a tensor payload past the end of its file, an array of an unsized element
+ * type and a general.alignment that is not a power of two are FLH_ERR_FORMAT.
+ * Host-only: nothing before flh_gguf_upload* touches the GPU. */
+typedef struct flh_gguf flh_gguf;
+
+/* One tensor info (GgufTensor, src/model/gguf.h:19-27).  Pointers stay valid
+ * until flh_gguf_close. */
+typedef struct flh_gguf_tensor {
+    const char * name;
+    size_t name_len;
+    uint32_t type;             /* ggml_type id */
+    int32_t fmt;               /* FLH_FMT_* (Gguf::fmt_of), -1 if none */
+    int32_t n_dims;
+    uint64_t ne[4];            /* unused dims are 1 */
+    uint64_t offset;           /* relative to its shard's data section */
+    uint64_t nbytes;           /* payload bytes; 0 for types with no size */
+    int32_t shard;
+    const void * data;         /* host pointer into the mapping (Gguf::data) */
+} flh_gguf_tensor;
+
+/* A STREAM_DOT weight bound from a tensor (DecoderImpl::load_tensor,
+ * src/model/decoder.cpp:186-206): cols = ne[0], rows = ne[1], nexp = ne[2]
+ * for 3-D expert stacks (else 1), estride = rows*row_bytes when nexp > 1. */
+typedef struct flh_weight {
+    int32_t fmt;
+    uint32_t rows, cols, nexp;
+    uint64_t row_bytes, w_bytes, estride;
+    const void * host;         /* mapping pointer of expert 0 */
+    uint64_t tensor;           /* tensor index */
+} flh_weight;
+
+int flh_gguf_open(const char * path, flh_gguf ** out);
+int flh_gguf_close(flh_gguf * g);
+uint32_t flh_gguf_alignment(const flh_gguf * g);   /* of the named shard */
+int flh_gguf_n_shards(const flh_gguf * g);
+uint64_t flh_gguf_n_tensors(const flh_gguf * g);
+int flh_gguf_tensor_info(const flh_gguf * g, uint64_t i, flh_gguf_tensor * out);
+/* index of the first tensor of that name (Gguf::find), -1 if none */
+int64_t flh_gguf_find(const flh_gguf * g, const char * name);
+/* Gguf::fmt_of / Gguf::type_name (src/model/gguf.cpp:82-109) */
+int flh_gguf_fmt_of(uint32_t ggml_type);
+const char * flh_gguf_type_name(uint32_t ggml_type);
+/* Metadata (Gguf::has / kv_i / kv_f / kv_s / kv_sarr, gguf.cpp:267-293):
+ * integer kinds and bool read as int64, f32/f64 as double, each readable
+ * through the other getter; strings and string arrays verbatim (len
+ * receives the byte length, strings may hold NUL bytes).  Arrays of other
+ * element types are skipped.  kv_sarr_len is -1 for an absent key. */
+int flh_gguf_has(const flh_gguf * g, const char * key);
+int64_t flh_gguf_kv_i(const flh_gguf * g, const char * key, int64_t dflt);
+double flh_gguf_kv_f(const flh_gguf * g, const char * key, double dflt);
+const char * flh_gguf_kv_s(const flh_gguf * g, const char * key, const char * dflt,
+                           size_t * len);
+int64_t flh_gguf_kv_sarr_len(const flh_gguf * g, const char * key);
+const char * flh_gguf_kv_sarr_at(const flh_gguf * g, const char * key, uint64_t i,
+                                 size_t * len);
+/* FLH_ERR_ARG for a missing tensor, FLH_ERR_UNSUPPORTED for a type with no
+ * Fmt (the two failures of load_tensor). */
+int flh_gguf_weight(const flh_gguf * g, const char * name, flh_weight * out);
+
+/* Host -> device.  The reference reads the mapping in place through unified
+ * memory (decoder.cpp:203); here weights are copied into HBM once.  Bytes go
+ * through a ring of pinned staging buffers filled by host threads while the
+ * DMA engine drains the previous one; both calls return when every byte is
+ * on the device.  flh_gguf_upload copies tensor i to dst (dst_bytes >=
+ * nbytes).  flh_gguf_upload_all allocates, per shard, one 256-B aligned arena
+ * block for the span of its tensor payloads and copies that span as-is, so
+ * dev_ptrs[i] (n_tensors entries) = block + offset keeps the file's alignment;
+ * dev_ptrs[i] = NULL where nbytes = 0.  Uploads from several threads are
+ * serialised. */
+int flh_gguf_upload(const flh_gguf * g, uint64_t i, void * dst, uint64_t dst_bytes,
+                    void * stream);
+int flh_gguf_upload_all(const flh_gguf * g, flh_arena * arena, void ** dev_ptrs,
+                        void * stream);
 
 /* ----------------------------------------------------- synthetic inputs -- */
 /* dst[i] = mean + stddev * N(0,1) from a counter-based generator keyed by
