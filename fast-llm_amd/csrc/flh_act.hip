@@ -79,6 +79,15 @@ __global__ void k_dequant(int fmt, const uint8_t * __restrict__ w, uint32_t rows
             const uint32_t nib = (g & 1) ? (q[l] >> 4) : (q[l] & 0xF);
             oo[l] = d1 * (float)nib - m1;
         }
+    } else if (fmt == FMT_IQ2_XXS || fmt == FMT_IQ3_XXS) {
+        // group ib of superblock sb: db * (+-grid magnitude), the factor the
+        // reference's canonical IQ dots multiply x by (quants.h:252-254,
+        // 280-283); its dequant_chunk has no IQ case (kernels.h:215-221)
+        const uint32_t sb = j >> 3, ib = j & 7, bb = iq_block_bytes(fmt);
+        const uint8_t * b = w + (size_t)r * (cols / 256) * bb + (size_t)sb * bb;
+        const uint32_t w1 = iq_w1(fmt, b, ib);
+        const float db = iq_db(fmt, h2f(b[0] | (b[1] << 8)), w1);
+        for (int e = 0; e < 32; ++e) o[32 * j + e] = db * (float)iq_val(fmt, b, ib, w1, e);
     } else {  // Q6_K: group (h, gg) of superblock sb, positions l < 32
         const uint32_t sb = j >> 3, h = (j >> 2) & 1, gg = j & 3;
         const uint8_t * b = w + (size_t)r * (cols / 256) * 210 + (size_t)sb * 210;
@@ -96,7 +105,7 @@ __global__ void k_dequant(int fmt, const uint8_t * __restrict__ w, uint32_t rows
 
 int launch_dequant(int fmt, const uint8_t * w, uint32_t rows, uint32_t cols,
                    float * out, hipStream_t s) {
-    if (fmt != FMT_Q8_0 && fmt != FMT_Q5_0 && fmt != FMT_Q4_K && fmt != FMT_Q6_K)
+    if (fmt < FMT_Q8_0 || fmt > FMT_IQ3_XXS)
         return set_error(FLH_ERR_UNSUPPORTED, "dequant: format not supported");
     const uint64_t units = (uint64_t)rows * (cols / 32);
     if (units == 0) return FLH_OK;

@@ -93,7 +93,7 @@ static int dispatch_dot(int fmt, const DotArgs & a, int fast, uint32_t i8_mask, 
         }
         if (fmt == FLH_FMT_Q5_0) return launch_dot_i8_q5_0(a, s);
         if (fmt == FLH_FMT_Q4_K || fmt == FLH_FMT_Q6_K) return launch_dot_i8_k(fmt, a, s);
-        return set_error(FLH_ERR_UNSUPPORTED, "q8_1 int8 path: format without one (IQ formats)");
+        return launch_dot_i8_iq(fmt, a, s);      // IQ2_XXS, IQ3_XXS
     }
     return launch_dot_fast_f32(fmt, a, s);
 }

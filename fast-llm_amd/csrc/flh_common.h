@@ -7,11 +7,13 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <type_traits>
+#include "flh_iq_grids.h"
 
 namespace flh {
 
 // Fmt numeric values (reference include/fastllm/fastllm.h:56-57).
-enum : int { FMT_F32 = 0, FMT_Q8_0 = 1, FMT_Q5_0 = 2, FMT_Q4_K = 3, FMT_Q6_K = 4 };
+enum : int { FMT_F32 = 0, FMT_Q8_0 = 1, FMT_Q5_0 = 2, FMT_Q4_K = 3, FMT_Q6_K = 4,
+             FMT_IQ2_XXS = 5, FMT_IQ3_XXS = 6 };
 
 // Activation appendix offsets of one column (reference
 // src/runtime/quants.h:302-330): [f32 x cols][pad16][q8_1 x cols/32][pad16]
@@ -92,6 +94,56 @@ __device__ __forceinline__ u32x4 ld4_nt(const uint8_t * p) {
 #else
     return *(const u32x4 *)p;
 #endif
+}
+
+// bit i of the 4-bit n -> bit 0 of byte i
+__device__ __forceinline__ uint32_t spread4(uint32_t n) { return (n * 0x00204081u) & 0x01010101u; }
+
+// ---- IQ2_XXS / IQ3_XXS (reference src/runtime/quants.h:27-38, 231-290) ----
+// A 256-element superblock: f16 d, then per 32-element group ib a 32-bit
+// scale/sign word w1 (top nibble: scale s; four 7-bit sign fields) and the
+// grid indices of its 8-element runs (IQ2: 4 index bytes before w1, 8
+// magnitudes per entry; IQ3: 8 index bytes in a leading 64-byte array, 4 per
+// entry, w1 words after it).  Group scale db = (d * (0.5 + s)) * 0.25 (IQ2)
+// or * 0.5 (IQ3).  The 7-bit sign field of run l widens to a byte with an
+// even-parity top bit; bit j negates element 8l + j.
+static __device__ const uint64_t k_iq2_grid[256] = { FLH_IQ2XXS_GRID_VALUES };
+static __device__ const uint32_t k_iq3_grid[256] = { FLH_IQ3XXS_GRID_VALUES };
+
+__host__ __device__ constexpr uint32_t iq_block_bytes(int fmt) { return fmt == FMT_IQ2_XXS ? 66u : 98u; }
+__device__ __forceinline__ uint32_t iq_sign8(uint32_t s7) {
+    s7 &= 127u;
+    return s7 | (((uint32_t)__builtin_popcount(s7) & 1u) << 7);
+}
+// bytewise negate of the bytes of v whose mask byte is 0xFF; v's bytes are
+// grid magnitudes in [1, 127], so no byte borrows from its neighbour
+__device__ __forceinline__ uint32_t iq_apply(uint32_t v, uint32_t neg) {
+    return (v ^ neg) + (neg & 0x01010101u);
+}
+__device__ __forceinline__ uint32_t iq_neg4(uint32_t bits4) { return spread4(bits4 & 0xFu) * 0xFFu; }
+__device__ __forceinline__ uint32_t iq_ldu32(const uint8_t * p) {
+    return p[0] | (p[1] << 8) | (p[2] << 16) | ((uint32_t)p[3] << 24);
+}
+// scale/sign word of group ib of superblock b
+__device__ __forceinline__ uint32_t iq_w1(int fmt, const uint8_t * b, int ib) {
+    return fmt == FMT_IQ2_XXS ? iq_ldu32(b + 2 + 8 * ib + 4) : iq_ldu32(b + 66 + 4 * ib);
+}
+__device__ __forceinline__ float iq_db(int fmt, float d, uint32_t w1) {
+    return fmt == FMT_IQ2_XXS ? d * (0.5f + (float)(w1 >> 28)) * 0.25f
+                              : d * (0.5f + (float)(w1 >> 28)) * 0.5f;
+}
+// signed magnitude of element e (0..31) of group ib
+__device__ __forceinline__ int iq_val(int fmt, const uint8_t * b, int ib, uint32_t w1, int e) {
+    const int l = e >> 3, j = e & 7;
+    const uint32_t s = iq_sign8(w1 >> (7 * l));
+    int v;
+    if (fmt == FMT_IQ2_XXS) {
+        const uint32_t w0 = iq_ldu32(b + 2 + 8 * ib);
+        v = (int)((k_iq2_grid[(w0 >> (8 * l)) & 0xFFu] >> (8 * j)) & 0xFFu);
+    } else {
+        v = (int)((k_iq3_grid[b[2 + 8 * ib + 2 * l + (j >> 2)]] >> (8 * (j & 3))) & 0xFFu);
+    }
+    return (s >> j) & 1u ? -v : v;
 }
 
 }  // namespace flh

@@ -365,12 +365,10 @@ __global__ __launch_bounds__(256) void k_moe_i8k(MoeArgs a, uint32_t nr) {
 // src/runtime/quants.h:449-466); NK blocks per lane (row of up to 256*NK
 // blocks).  Terms: idot per (row, column, block) and the weight scale bits
 // per (row, block); chain acc[b & 3] = fmaf(dw * dx, idot, .).
+// terms, weight scales, activation scales, then the IQ codebook (2 KiB)
 __host__ __device__ inline size_t q8_smem_bytes(uint32_t nr, uint32_t nx_t, uint32_t P) {
-    return 4 * ((size_t)nr * nx_t * P + (size_t)nr * P + (size_t)nx_t * P);
+    return 4 * ((size_t)nr * nx_t * P + (size_t)nr * P + (size_t)nx_t * P) + 2048;
 }
-
-// bit i of the 4-bit n -> bit 0 of byte i
-__device__ __forceinline__ uint32_t spread4(uint32_t n) { return (n * 0x00204081u) & 0x01010101u; }
 
 template <int FMT, int NX, int NK>
 __global__ __launch_bounds__(256) void k_dot_i8_b32(DotArgs a, uint32_t nr) {
@@ -379,8 +377,10 @@ __global__ __launch_bounds__(256) void k_dot_i8_b32(DotArgs a, uint32_t nr) {
     const uint32_t nb = a.cols >> 5;
     const uint32_t lgP = ceil_log2(nb), P = 1u << lgP;   // P <= 256*NK
     const uint32_t rpi = NK == 1 ? (256u >> lgP) : 1u;
-    constexpr uint32_t BB = FMT == FMT_Q5_0 ? 22 : 34;     // block bytes
-    const uint64_t rb = (uint64_t)nb * BB;
+    constexpr bool IQ = FMT == FMT_IQ2_XXS || FMT == FMT_IQ3_XXS;
+    // block bytes (IQ: of a 256-element superblock holding 8 groups)
+    constexpr uint32_t BB = FMT == FMT_Q5_0 ? 22 : FMT == FMT_Q8_0 ? 34 : iq_block_bytes(FMT);
+    const uint64_t rb = IQ ? (uint64_t)(nb >> 3) * BB : (uint64_t)nb * BB;
     const uint32_t tid = threadIdx.x;
     const uint32_t rsub = NK == 1 ? (tid >> lgP) : 0u;
     uint32_t bl[NK];
@@ -394,6 +394,14 @@ __global__ __launch_bounds__(256) void k_dot_i8_b32(DotArgs a, uint32_t nr) {
     int * TI = smem;
     uint32_t * TH = (uint32_t *)(TI + (size_t)nr * NX * P);
     float * XD = (float *)(TH + (size_t)nr * P);
+    uint32_t * GR = (uint32_t *)(XD + (size_t)NX * P);   // IQ codebook, 2 KiB
+    if constexpr (FMT == FMT_IQ2_XXS) {
+        GR[2 * tid] = (uint32_t)k_iq2_grid[tid];
+        GR[2 * tid + 1] = (uint32_t)(k_iq2_grid[tid] >> 32);
+    } else if constexpr (FMT == FMT_IQ3_XXS) {
+        GR[tid] = k_iq3_grid[tid];
+    }
+    if constexpr (IQ) __syncthreads();
 
     const uint8_t * xq[NX];
 #pragma unroll
@@ -431,6 +439,26 @@ __global__ __launch_bounds__(256) void k_dot_i8_b32(DotArgs a, uint32_t nr) {
     // aligned; nothing past the block's last byte is read).
     struct W8 { u32x4 d0, d1; uint32_t d8, sh; };
     auto wload = [&](uint32_t row, uint32_t b) -> W8 {
+        if constexpr (IQ) {
+            // group b = (superblock b/8, group b%8); 2-byte aligned pieces:
+            // d, the 8 index bytes (IQ2: 4 indices + w1), IQ3's w1 word
+            const uint8_t * sbp = w + (size_t)row * rb + (size_t)(b >> 3) * BB;
+            const uint8_t * q = sbp + 2 + 8 * (b & 7);
+            const uintptr_t qa = (uintptr_t)q;
+            const uint8_t * f = (const uint8_t *)(qa & ~(uintptr_t)3);
+            W8 r;
+            r.sh = (uint32_t)(qa & 3);
+            const uint32_t A = *(const uint32_t *)f, B = *(const uint32_t *)(f + 4);
+            const uint32_t Cw = r.sh ? ldh(f + 8) : 0u;
+            r.d0 = u32x4{alignb(B, A, r.sh), alignb(Cw, B, r.sh), ldh(sbp), 0u};
+            if constexpr (FMT == FMT_IQ3_XXS) {
+                const uint8_t * sw = sbp + 66 + 4 * (b & 7);
+                r.d0.w = ldh(sw) | (ldh(sw + 2) << 16);
+            }
+            r.d1 = u32x4{0u, 0u, 0u, 0u};
+            r.d8 = 0;
+            return r;
+        }
         const uint8_t * blk = w + (size_t)row * rb + (size_t)b * BB;
         const uintptr_t ba = (uintptr_t)blk;
         const uint8_t * f = (const uint8_t *)(ba & ~(uintptr_t)3);
@@ -470,7 +498,29 @@ __global__ __launch_bounds__(256) void k_dot_i8_b32(DotArgs a, uint32_t nr) {
                 const bool wr = act[k] && rl < nrow && rl < nr;
                 uint32_t dbits;
                 int qs[8];
-                if constexpr (FMT == FMT_Q5_0) {
+                if constexpr (IQ) {
+                    // signed grid magnitudes of the group's 32 elements,
+                    // dword j = elements 4j..4j+3 (quants.h:237-290)
+                    const uint32_t w0 = W.d0.x;
+                    const uint32_t w1 = FMT == FMT_IQ2_XXS ? W.d0.y : W.d0.w;
+#pragma unroll
+                    for (int l = 0; l < 4; ++l) {
+                        const uint32_t sg = iq_sign8(w1 >> (7 * l));
+                        uint32_t lo, hi;
+                        if constexpr (FMT == FMT_IQ2_XXS) {
+                            const uint32_t gi = (w0 >> (8 * l)) & 0xFFu;
+                            lo = GR[2 * gi];
+                            hi = GR[2 * gi + 1];
+                        } else {
+                            const uint32_t ix = l < 2 ? w0 : W.d0.y;
+                            lo = GR[(ix >> (16 * (l & 1))) & 0xFFu];
+                            hi = GR[(ix >> (16 * (l & 1) + 8)) & 0xFFu];
+                        }
+                        qs[2 * l] = (int)iq_apply(lo, iq_neg4(sg));
+                        qs[2 * l + 1] = (int)iq_apply(hi, iq_neg4(sg >> 4));
+                    }
+                    dbits = __float_as_uint(iq_db(FMT, h2f(W.d0.z), w1));
+                } else if constexpr (FMT == FMT_Q5_0) {
                     // E = the block's bytes 0..21; d, qh, then 16 bytes of nibble pairs
                     const uint32_t D[6] = {W.d0.x, W.d0.y, W.d0.z, W.d0.w, W.d1.x, W.d1.y};
                     uint32_t E[6];
@@ -516,8 +566,10 @@ __global__ __launch_bounds__(256) void k_dot_i8_b32(DotArgs a, uint32_t nr) {
                 const int * ti = TI + ((rl * NX + p) << lgP);
                 const uint32_t * th = TH + (rl << lgP);
                 const float * xd = XD + (p << lgP);
-                for (uint32_t b = k; b < nb; b += 4)
-                    acc = fmaf(h2f(th[b]) * xd[b], (float)ti[b], acc);
+                for (uint32_t b = k; b < nb; b += 4) {
+                    const float ws = IQ ? __uint_as_float(th[b]) : h2f(th[b]);
+                    acc = fmaf(ws * xd[b], (float)ti[b], acc);
+                }
             }
             const float s01 = acc + qx1f(acc);
             const float r = s01 + qx2f(s01);
@@ -681,5 +733,11 @@ static int launch_i8_b32(const DotArgs & a0, hipStream_t s) {
 
 int launch_dot_i8_q8_0(const DotArgs & a, hipStream_t s) { return launch_i8_b32<FMT_Q8_0>(a, s); }
 int launch_dot_i8_q5_0(const DotArgs & a, hipStream_t s) { return launch_i8_b32<FMT_Q5_0>(a, s); }
+int launch_dot_i8_iq(int fmt, const DotArgs & a, hipStream_t s) {
+    if (a.cols & 255) return set_error(FLH_ERR_UNSUPPORTED, "IQ int8 dot: cols must be a multiple of 256");
+    if (fmt == FMT_IQ2_XXS) return launch_i8_b32<FMT_IQ2_XXS>(a, s);
+    if (fmt == FMT_IQ3_XXS) return launch_i8_b32<FMT_IQ3_XXS>(a, s);
+    return set_error(FLH_ERR_UNSUPPORTED, "IQ int8 dot: IQ2_XXS / IQ3_XXS only");
+}
 
 }  // namespace flh

@@ -33,8 +33,15 @@ __device__ __forceinline__ uint32_t q5qh(const uint8_t * b) {
 }
 
 __device__ void dq_block(int fmt, const uint8_t * b, float * o) {
-    // value formulas of dequant_chunk (src/runtime/kernels.h:169-240)
-    if (fmt == FMT_Q5_0) {                 // one 32-element block
+    // value formulas of dequant_chunk (src/runtime/kernels.h:169-240); IQ
+    // formats: db * (+-v), the factors of the canonical IQ dots
+    if (fmt == FMT_IQ2_XXS || fmt == FMT_IQ3_XXS) {
+        for (int ib = 0; ib < 8; ++ib) {
+            const uint32_t w1 = iq_w1(fmt, b, ib);
+            const float db = iq_db(fmt, h2f(ld16u(b)), w1);
+            for (int e = 0; e < 32; ++e) o[32 * ib + e] = db * (float)iq_val(fmt, b, ib, w1, e);
+        }
+    } else if (fmt == FMT_Q5_0) {                 // one 32-element block
         const float d = h2f(ld16u(b));
         const uint32_t qh = q5qh(b);
         for (int j = 0; j < 32; ++j) o[j] = d * (float)q5v(b, qh, j);
@@ -89,6 +96,33 @@ __device__ float canon_dot(int fmt, const uint8_t * row, const float * x, uint32
             const float d = h2f(ld16u(B));
             const uint32_t qh = q5qh(B);
             for (int j = 0; j < 32; ++j) acc += d * (float)q5v(B, qh, j) * x[b * 32 + j];
+        }
+    } else if (fmt == FMT_IQ2_XXS || fmt == FMT_IQ3_XXS) {
+        // fl_dot_row_iq2_xxs / fl_dot_row_iq3_xxs (src/runtime/quants.h:237-290):
+        // IQ2 ascending; IQ3 element 8l+j then 8l+j+4 for j = 0..3
+        const uint32_t bb = iq_block_bytes(fmt);
+        for (uint32_t sb = 0; sb < cols / 256; ++sb) {
+            const uint8_t * B = row + (size_t)sb * bb;
+            const float * xb = x + sb * 256;
+            const float d = h2f(ld16u(B));
+            for (int ib = 0; ib < 8; ++ib) {
+                const uint32_t w1 = iq_w1(fmt, B, ib);
+                const float db = iq_db(fmt, d, w1);
+                for (int l = 0; l < 4; ++l) {
+                    if (fmt == FMT_IQ2_XXS) {
+                        for (int j = 0; j < 8; ++j) {
+                            const int e = 8 * l + j;
+                            acc += db * (float)iq_val(fmt, B, ib, w1, e) * xb[32 * ib + e];
+                        }
+                    } else {
+                        for (int j = 0; j < 4; ++j) {
+                            const int e1 = 8 * l + j, e2 = e1 + 4;
+                            acc += db * (float)iq_val(fmt, B, ib, w1, e1) * xb[32 * ib + e1];
+                            acc += db * (float)iq_val(fmt, B, ib, w1, e2) * xb[32 * ib + e2];
+                        }
+                    }
+                }
+            }
         }
     } else if (fmt == FMT_Q4_K) {
         for (uint32_t sb = 0; sb < cols / 256; ++sb) {
@@ -168,7 +202,8 @@ __device__ float fast_dot(int fmt, const uint8_t * row, const float * x, uint32_
         if (fmt == FMT_Q5_0) {
             for (uint32_t b = 0; b < n / 32; ++b) dq_block(fmt, row + (size_t)(e / 32 + b) * 22, buf + 32 * b);
         } else {
-            dq_block(fmt, row + (size_t)(e / 256) * (fmt == FMT_Q4_K ? 144 : 210), buf);
+            const uint32_t bb = fmt == FMT_Q4_K ? 144 : fmt == FMT_Q6_K ? 210 : iq_block_bytes(fmt);
+            dq_block(fmt, row + (size_t)(e / 256) * bb, buf);
         }
         float L[16] = {0};
         for (uint32_t k = 0; k < n; k += 16)
@@ -263,7 +298,8 @@ __global__ void k_dot_f32(int fmt, DotArgs a) {
     const uint64_t rb = fmt == FMT_F32 ? (uint64_t)a.cols * 4
                       : fmt == FMT_Q8_0 ? (uint64_t)(a.cols / 32) * 34
                       : fmt == FMT_Q5_0 ? (uint64_t)(a.cols / 32) * 22
-                      : (uint64_t)(a.cols / 256) * (fmt == FMT_Q4_K ? 144 : 210);
+                      : (uint64_t)(a.cols / 256) * (fmt == FMT_Q4_K ? 144 : fmt == FMT_Q6_K ? 210
+                                                   : iq_block_bytes(fmt));
     const float * x = a.x + (size_t)p * a.xstride;
     const float v = FAST ? fast_dot(fmt, w + r * rb, x, a.cols) : canon_dot(fmt, w + r * rb, x, a.cols);
     float * y = a.y + (size_t)p * a.ystride + r;
@@ -271,7 +307,7 @@ __global__ void k_dot_f32(int fmt, DotArgs a) {
 }
 
 static int launch_f32(bool fast, int fmt, const DotArgs & a, hipStream_t s) {
-    if (fmt != FMT_F32 && fmt != FMT_Q8_0 && fmt != FMT_Q5_0 && fmt != FMT_Q4_K && fmt != FMT_Q6_K)
+    if (fmt < FMT_F32 || fmt > FMT_IQ3_XXS)
         return set_error(FLH_ERR_UNSUPPORTED, "fp32 dot: format not supported");
     const uint64_t n = (uint64_t)a.rows * a.nx;
     if (n == 0) return FLH_OK;

@@ -50,6 +50,7 @@ int launch_act_dot_kstream(int fmt, const DotArgs & a, hipStream_t s);
 int launch_dot_i8_q8_0(const DotArgs & a, hipStream_t s);         // Q8_0 x q8_1
 int launch_dot_i8_q5_0(const DotArgs & a, hipStream_t s);         // Q5_0 x q8_1
 int launch_dot_i8_k(int fmt, const DotArgs & a, hipStream_t s);   // Q4_K, Q6_K x q8_1
+int launch_dot_i8_iq(int fmt, const DotArgs & a, hipStream_t s);  // IQ2_XXS, IQ3_XXS x q8_1
 int launch_dot_canonical(int fmt, const DotArgs & a, hipStream_t s);
 int launch_dot_fast_f32(int fmt, const DotArgs & a, hipStream_t s);
 int launch_dequant(int fmt, const uint8_t * w, uint32_t rows, uint32_t cols,

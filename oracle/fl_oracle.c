@@ -15,6 +15,7 @@
  *   q8_K 292 B: d f32 @0, bsums[16] i16 @4, qs[256] @36 (quants.h:316)
  */
 #include "fl_oracle.h"
+#include "../fast-llm_amd/csrc/flh_iq_grids.h"
 #include <math.h>
 #include <string.h>
 #include <stdlib.h>
@@ -68,12 +69,55 @@ uint16_t orc_float2half(float f) {
 /* src/runtime/quants.h:76-99 */
 uint32_t orc_blk_elems(int fmt) {
     switch (fmt) { case ORC_Q8_0: case ORC_Q5_0: return 32;
-                   case ORC_Q4_K: case ORC_Q6_K: return 256; default: return 1; }
+                   case ORC_Q4_K: case ORC_Q6_K: case ORC_IQ2_XXS: case ORC_IQ3_XXS: return 256;
+                   default: return 1; }
 }
 uint32_t orc_blk_bytes(int fmt) {
     switch (fmt) { case ORC_Q8_0: return 34; case ORC_Q5_0: return 22;
                    case ORC_Q4_K: return 144; case ORC_Q6_K: return 210;
+                   case ORC_IQ2_XXS: return 66; case ORC_IQ3_XXS: return 98;
                    default: return 4; }
+}
+
+/* ---- IQ2_XXS / IQ3_XXS codebook formats (src/runtime/quants.h:27-38,
+ *      231-290).  Per 32-element group ib of a 256-element superblock: a
+ *      4-bit scale s (top nibble of the group's 32-bit sign/scale word w1)
+ *      gives db = (d * (0.5 + s)) * 0.25 (IQ2) or * 0.5 (IQ3); four 7-bit
+ *      sign fields of w1 widen to sign bytes with an even-parity top bit
+ *      (the format's sign table). */
+static const uint64_t iq2_grid[256] = { FLH_IQ2XXS_GRID_VALUES };
+static const uint32_t iq3_grid[256] = { FLH_IQ3XXS_GRID_VALUES };
+uint8_t orc_iq_signs(uint32_t s7) {
+    s7 &= 127u;
+    return (uint8_t)(s7 | ((uint32_t)__builtin_parity(s7) << 7));
+}
+uint64_t orc_iq2_grid(int i) { return iq2_grid[i & 255]; }
+uint32_t orc_iq3_grid(int i) { return iq3_grid[i & 255]; }
+static uint32_t rd32(const uint8_t * p) { uint32_t v; memcpy(&v, p, 4); return v; }
+/* group ib's scale-sign word and its grid magnitude of element e (0..31) */
+static uint32_t iq_w1(int fmt, const uint8_t * b, int ib) {
+    return fmt == ORC_IQ2_XXS ? rd32(b + 2 + 8 * ib + 4) : rd32(b + 2 + 64 + 4 * ib);
+}
+static float iq_db(int fmt, const uint8_t * b, uint32_t w1) {
+    const float d = orc_half2float(rd16(b));
+    return fmt == ORC_IQ2_XXS ? d * (0.5f + (float)(w1 >> 28)) * 0.25f
+                              : d * (0.5f + (float)(w1 >> 28)) * 0.5f;
+}
+/* signed magnitude of element e of group ib (grid byte, sign from the
+ * group's l-th sign byte; IQ3 entries 2l / 2l+1 take sign bits 0-3 / 4-7) */
+static int iq_val(int fmt, const uint8_t * b, int ib, int e) {
+    const uint32_t w1 = iq_w1(fmt, b, ib);
+    const int l = e >> 3, j = e & 7;
+    const uint8_t s = orc_iq_signs(w1 >> (7 * l));
+    int v;
+    if (fmt == ORC_IQ2_XXS) {
+        const uint32_t w0 = rd32(b + 2 + 8 * ib);
+        v = (int)(uint8_t)(iq2_grid[(w0 >> (8 * l)) & 0xFF] >> (8 * j));
+    } else {
+        const uint8_t * qs = b + 2;
+        v = (int)(uint8_t)(iq3_grid[qs[8 * ib + 2 * l + (j >> 2)]] >> (8 * (j & 3)));
+    }
+    return (s >> j) & 1 ? -v : v;
 }
 uint64_t orc_row_bytes(int fmt, uint32_t cols) {
     return (uint64_t)(cols / orc_blk_elems(fmt)) * orc_blk_bytes(fmt);
@@ -136,6 +180,19 @@ static int q6_val(const uint8_t * b, int h, int g, int l) {
     const int lo = (g < 2) ? (lb & 0xF) : (lb >> 4);
     return lo | (((qh[l] >> (2 * g)) & 3) << 4);
 }
+/* IQ dequant: element value db * (+-v), the factor fl_dot_row_iq2_xxs /
+ * fl_dot_row_iq3_xxs multiply x by (src/runtime/quants.h:252-254, 280-283).
+ * The reference's dequant_chunk has no IQ case (it zero-fills,
+ * src/runtime/kernels.h:215-221); this defines the fp32 values. */
+static void dq_iq(int fmt, const uint8_t * b, float * o) {
+    for (int ib = 0; ib < 8; ++ib) {
+        const float db = iq_db(fmt, b, iq_w1(fmt, b, ib));
+        for (int e = 0; e < 32; ++e) {
+            const int v = iq_val(fmt, b, ib, e);
+            o[32 * ib + e] = db * (float)v;
+        }
+    }
+}
 static void dq_q6_K(const uint8_t * b, float * o) {
     const float d = orc_half2float(rd16(b + 208));
     const int8_t * sc = (const int8_t *)(b + 192);
@@ -158,6 +215,7 @@ void orc_dequant_chunk(int fmt, const uint8_t * row, uint32_t elem0,
         else if (fmt == ORC_Q5_0) dq_q5_0(blk, o);
         else if (fmt == ORC_Q4_K) dq_q4_K(blk, o);
         else if (fmt == ORC_Q6_K) dq_q6_K(blk, o);
+        else if (fmt == ORC_IQ2_XXS || fmt == ORC_IQ3_XXS) dq_iq(fmt, blk, o);
     }
 }
 void orc_dequant_rows(int fmt, const uint8_t * w, uint32_t rows,
@@ -222,6 +280,37 @@ static float dot_row_q6_K(const uint8_t * row, const float * x, uint32_t cols) {
     }
     return acc;
 }
+/* fl_dot_row_iq2_xxs / fl_dot_row_iq3_xxs (src/runtime/quants.h:237-290):
+ * one accumulator; acc += (db * (+-v)) * x.  IQ2 walks elements ascending;
+ * IQ3 interleaves the two grid entries of each 8-element run (element
+ * 8l+j, then 8l+j+4, for j = 0..3). */
+static float dot_row_iq(int fmt, const uint8_t * row, const float * x, uint32_t cols) {
+    float acc = 0.f;
+    const uint32_t bb = orc_blk_bytes(fmt);
+    for (uint32_t sb = 0; sb < cols / 256; ++sb) {
+        const uint8_t * B = row + (size_t)sb * bb;
+        const float * xb = x + (size_t)sb * 256;
+        for (int ib = 0; ib < 8; ++ib) {
+            const float db = iq_db(fmt, B, iq_w1(fmt, B, ib));
+            for (int l = 0; l < 4; ++l) {
+                if (fmt == ORC_IQ2_XXS) {
+                    for (int j = 0; j < 8; ++j) {
+                        const int e = 8 * l + j;
+                        acc += db * (float)iq_val(fmt, B, ib, e) * xb[32 * ib + e];
+                    }
+                } else {
+                    for (int j = 0; j < 4; ++j) {
+                        const int e1 = 8 * l + j, e2 = 8 * l + j + 4;
+                        acc += db * (float)iq_val(fmt, B, ib, e1) * xb[32 * ib + e1];
+                        acc += db * (float)iq_val(fmt, B, ib, e2) * xb[32 * ib + e2];
+                    }
+                }
+            }
+        }
+    }
+    return acc;
+}
+
 float orc_dot_row(int fmt, const uint8_t * row, const float * x, uint32_t cols) {
     switch (fmt) {
         case ORC_F32: {
@@ -233,6 +322,7 @@ float orc_dot_row(int fmt, const uint8_t * row, const float * x, uint32_t cols) 
         case ORC_Q5_0: return dot_row_q5_0(row, x, cols);
         case ORC_Q4_K: return dot_row_q4_K(row, x, cols);
         case ORC_Q6_K: return dot_row_q6_K(row, x, cols);
+        case ORC_IQ2_XXS: case ORC_IQ3_XXS: return dot_row_iq(fmt, row, x, cols);
     }
     return 0.f;
 }
@@ -353,6 +443,27 @@ float orc_dot_i8_q5_0(const uint8_t * row, const uint8_t * xq, uint32_t cols) {
     }
     return fold4(a);
 }
+/* IQ2_XXS / IQ3_XXS x q8_1.  No reference CPU counterpart: the reference
+ * keeps codebook tiles off the CPU (fl_dot_i8_any returns 0 for them,
+ * src/runtime/quants.h:612-620) and runs them on its GPU int8 kernels
+ * (gdot_i8_iq2_xxs / gdot_i8_iq3_xxs, src/runtime/kernels_gpu.h:759-852),
+ * whose sums are q8_1 dot products scaled by db * dx per 32-element group.
+ * This build fixes the order the Q8_0 int8 dot uses: per group b the exact
+ * integer dot of the signed grid magnitudes with the q8_1 quants, folded
+ * acc[b & 3] = fmaf(db * dx, idot, .), then (a0 + a1) + (a2 + a3). */
+float orc_dot_i8_iq(int fmt, const uint8_t * row, const uint8_t * xq, uint32_t cols) {
+    float a[4] = {0.f, 0.f, 0.f, 0.f};
+    const uint32_t bb = orc_blk_bytes(fmt);
+    for (uint32_t b = 0; b < cols / 32; ++b) {
+        const uint8_t * B = row + (size_t)(b / 8) * bb, * X = xq + (size_t)b * 36;
+        const int ib = (int)(b & 7);
+        int idot = 0;
+        for (int e = 0; e < 32; ++e) idot += iq_val(fmt, B, ib, e) * (int)(int8_t)X[4 + e];
+        const float db = iq_db(fmt, B, iq_w1(fmt, B, ib));
+        a[b & 3] = fmaf(db * orc_half2float(rd16(X)), (float)idot, a[b & 3]);
+    }
+    return fold4(a);
+}
 float orc_dot_i8_q4_K(const uint8_t * row, const uint8_t * xq, uint32_t cols) {
     float a[4] = {0.f, 0.f, 0.f, 0.f};
     for (uint32_t sb = 0; sb < cols / 256; ++sb) {
@@ -463,6 +574,7 @@ static float one_dot(int fmt, const uint8_t * row, const float * x, uint32_t col
             case ORC_Q5_0: return orc_dot_i8_q5_0(row, xq, cols);
             case ORC_Q4_K: return orc_dot_i8_q4_K(row, xq, cols);
             case ORC_Q6_K: return orc_dot_i8_q6_K(row, xq, cols);
+            case ORC_IQ2_XXS: case ORC_IQ3_XXS: return orc_dot_i8_iq(fmt, row, xq, cols);
             default: return 0.f;
         }
     }

@@ -34,7 +34,8 @@ extern "C" {
 #endif
 
 /* Fmt numeric values: include/fastllm/fastllm.h:56-57 */
-enum { ORC_F32 = 0, ORC_Q8_0 = 1, ORC_Q5_0 = 2, ORC_Q4_K = 3, ORC_Q6_K = 4 };
+enum { ORC_F32 = 0, ORC_Q8_0 = 1, ORC_Q5_0 = 2, ORC_Q4_K = 3, ORC_Q6_K = 4,
+       ORC_IQ2_XXS = 5, ORC_IQ3_XXS = 6 };
 
 float    orc_half2float(uint16_t h);
 uint16_t orc_float2half(float f);
@@ -68,6 +69,11 @@ float orc_dot_i8_q8_0(const uint8_t * row, const uint8_t * xq, uint32_t cols);
 float orc_dot_i8_q5_0(const uint8_t * row, const uint8_t * xq, uint32_t cols);
 float orc_dot_i8_q4_K(const uint8_t * row, const uint8_t * xq, uint32_t cols);
 float orc_dot_i8_q6_K(const uint8_t * row, const uint8_t * xq, uint32_t cols);
+/* IQ formats: codebook accessors, the sign-byte widening, the q8_1 dot */
+uint64_t orc_iq2_grid(int i);
+uint32_t orc_iq3_grid(int i);
+uint8_t  orc_iq_signs(uint32_t s7);
+float orc_dot_i8_iq(int fmt, const uint8_t * row, const uint8_t * xq, uint32_t cols);
 float orc_dot_i8k_q4_K(const uint8_t * row, const uint8_t * xk, uint32_t cols);
 float orc_dot_i8k_q6_K(const uint8_t * row, const uint8_t * xk, uint32_t cols);
 

@@ -19,8 +19,9 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ORACLE_SO = os.path.join(HERE, "liboracle.so")
 REF_SO = os.path.join(HERE, "_ref", "libflref.so")
 
-F32, Q8_0, Q5_0, Q4_K, Q6_K = 0, 1, 2, 3, 4
-BLK = {F32: (1, 4), Q8_0: (32, 34), Q5_0: (32, 22), Q4_K: (256, 144), Q6_K: (256, 210)}
+F32, Q8_0, Q5_0, Q4_K, Q6_K, IQ2_XXS, IQ3_XXS = 0, 1, 2, 3, 4, 5, 6
+BLK = {F32: (1, 4), Q8_0: (32, 34), Q5_0: (32, 22), Q4_K: (256, 144), Q6_K: (256, 210),
+       IQ2_XXS: (256, 66), IQ3_XXS: (256, 98)}
 
 
 def row_bytes(fmt, cols):
@@ -88,6 +89,8 @@ class Oracle:
             self._sdmt.argtypes = [_I, _P, _U32, _U32, _P, _P, _U32, _U32, _U32, _I, _U32, _U32, _I]
             for n, args, res in [
                 ("orc_dot_i8_q8_0", [_P, _P, _U32], _F), ("orc_dot_i8_q5_0", [_P, _P, _U32], _F),
+                ("orc_dot_i8_iq", [_I, _P, _P, _U32], _F), ("orc_iq2_grid", [_I], C.c_uint64),
+                ("orc_iq3_grid", [_I], _U32), ("orc_iq_signs", [_U32], C.c_uint8),
                 ("orc_dot_i8k_q4_K", [_P, _P, _U32], _F),
                 ("orc_dot_i8k_q6_K", [_P, _P, _U32], _F), ("orc_dot_i8_q4_K", [_P, _P, _U32], _F),
                 ("orc_dot_i8_q6_K", [_P, _P, _U32], _F), ("orc_dot_row", [_I, _P, _P, _U32], _F),

@@ -96,6 +96,13 @@ void ref_stream_dot_canonical(int fmt, const void * w, uint32_t rows,
     exec_task_scalar_host(t);
 }
 
+// the reference's IQ codebooks and sign table (src/model/iq_tables.h), for
+// hashing: fixtures record only a digest of them, never the values
+void ref_iq_tables(uint64_t * g2, uint32_t * g3, uint8_t * signs) {
+    for (int i = 0; i < 256; ++i) { g2[i] = fl_kIq2xxsGrid(i); g3[i] = fl_kIq3xxsGrid(i); }
+    for (int i = 0; i < 128; ++i) signs[i] = fl_kIqSigns(i);
+}
+
 void ref_router_sel(const float * logits, uint32_t n_expert, uint32_t top_k,
                     uint32_t norm, float scale, uint32_t * ids, float * gates) {
     RouterP p{logits, ids, gates, n_expert, top_k, norm, scale};

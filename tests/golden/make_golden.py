@@ -201,6 +201,50 @@ def main():
                 n5 += 1
     out["q5dot_count"] = np.array([n5])
 
+    # ---- IQ2_XXS / IQ3_XXS: the reference runs them on its CPU only through
+    # the canonical chain (fl_dot_row_iq2_xxs / fl_dot_row_iq3_xxs,
+    # quants.h:237-290); its fast / int8 CPU routes have no codebook case.
+    # Canonical dots of random blocks (every grid index and sign pattern
+    # occurs), the reference KAT block (tests/test_runtime.cpp:979-993), and
+    # digests of the reference's codebooks and sign table.
+    rngq = np.random.default_rng(20261203)
+    nq = 0
+    for fmt, bb in ((5, 66), (6, 98)):
+        for cols, rows, nx in ((256, 64, 1), (2048, 9, 2), (512, 40, 3)):
+            w = rngq.integers(0, 256, size=rows * (cols // 256) * bb, dtype=np.uint8)
+            blocks = w.reshape(-1, bb)
+            blocks[:, 0:2] = (0x2000 | (rngq.integers(0, 1 << 16, blocks.shape[0]) & 0x0BFF)
+                              ).astype(np.uint16).view(np.uint8).reshape(-1, 2)
+            xs = xs_for(cols, nx, rngq, outliers=(nq % 2 == 1))
+            st = col_stride_floats(cols)
+            xbuf = np.zeros(nx * st, dtype=np.float32)
+            for p in range(nx):
+                xbuf[p * st:p * st + cols] = xs[p]
+            y0 = rngq.standard_normal(nx * rows).astype(np.float32)
+            y = y0.copy()
+            ref.stream_dot(fmt, w, rows, cols, xbuf, y, nx=nx, xstride=st, ystride=rows,
+                           fast=False, i8_mask=0, i8k_mask=0)
+            key = f"iqdot{nq}"
+            out[key + "_meta"] = np.array([fmt, cols, rows, nx, st, 0, 0, 0], dtype=np.int64)
+            out[key + "_w"], out[key + "_x"], out[key + "_y0"], out[key + "_y"] = w, xbuf, y0, y
+            nq += 1
+    out["iqdot_count"] = np.array([nq])
+    kat = np.zeros(66, dtype=np.uint8)
+    kat[0:2] = np.array([0x3C00], dtype=np.uint16).view(np.uint8)
+    xk = np.zeros(256, dtype=np.float32)
+    xk[3] = 2.0
+    yk = np.zeros(1, dtype=np.float32)
+    ref.stream_dot(5, kat, 1, 256, xk, yk, fast=False, i8_mask=0, i8k_mask=0)
+    out["iq_kat_w"], out["iq_kat_x"], out["iq_kat_y"] = kat, xk, yk
+    import hashlib
+    g2 = np.zeros(256, dtype=np.uint64)
+    g3 = np.zeros(256, dtype=np.uint32)
+    sg = np.zeros(128, dtype=np.uint8)
+    import ctypes
+    ref.lib.ref_iq_tables.argtypes = [ctypes.c_void_p] * 3
+    ref.lib.ref_iq_tables(g2.ctypes.data, g3.ctypes.data, sg.ctypes.data)
+    out["iq_sha256"] = np.array([hashlib.sha256(a.tobytes()).hexdigest() for a in (g2, g3, sg)])
+
     np.savez_compressed(os.path.join(HERE, "golden_ref.npz"), **out)
     with open(os.path.join(HERE, "task_layout.json"), "w") as fh:
         json.dump(task_layout(), fh, indent=1, sort_keys=True)

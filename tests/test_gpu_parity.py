@@ -43,7 +43,7 @@ def run_dot(flh, orc, gpu, fmt, w, rows, cols, xs, mode="int8", y0=None, id_slot
     st = col_stride_floats(cols)
     ys = rows if ystride is None else ystride
     fast, i8, i8k = {"int8": (1, I8, I8K), "q81": (1, I8, 0), "f32fast": (1, 0, 0),
-                     "canon": (0, 0, 0)}[mode]
+                     "canon": (0, 0, 0), "iq8": (1, 0b1100000, 0)}[mode]
     dx, hx = dev_cols(flh, gpu, xs, st)
     flh.act_q8(dx, cols, gpu, nx=nx, xstride=st)
     xq = dx.download(np.float32, nx * st, gpu)

@@ -91,3 +91,30 @@ def test_router_silu_wmerge_match_reference(orc, golden):
     assert np.array_equal(bits(h), bits(golden["silu_h"]))
     y = orc.wmerge(golden["wm_parts"], golden["wm_gates"], add1=golden["wm_add1"])
     assert np.array_equal(bits(y), bits(golden["wm_y"]))
+
+
+def test_iq_codebooks_match_reference(orc, golden):
+    """The IQ2_XXS / IQ3_XXS grids and the sign widening equal the
+    reference's tables (src/model/iq_tables.h), compared by SHA-256."""
+    import hashlib
+    g2 = np.array([orc.iq2_grid(i) for i in range(256)], dtype=np.uint64)
+    g3 = np.array([orc.iq3_grid(i) for i in range(256)], dtype=np.uint32)
+    sg = np.array([orc.iq_signs(i) for i in range(128)], dtype=np.uint8)
+    got = [hashlib.sha256(a.tobytes()).hexdigest() for a in (g2, g3, sg)]
+    assert got == [str(v) for v in golden["iq_sha256"]]
+
+
+def test_iq_canonical_dots_match_reference(orc, golden):
+    """fl_dot_row_iq2_xxs / fl_dot_row_iq3_xxs (quants.h:237-290) through the
+    canonical route, and the reference KAT block (test_runtime.cpp:979-993)."""
+    n = int(golden["iqdot_count"][0])
+    assert n == 6
+    for i in range(n):
+        fmt, cols, rows, nx, st, fast, i8, i8k = (int(v) for v in golden[f"iqdot{i}_meta"])
+        y = golden[f"iqdot{i}_y0"].copy()
+        orc.stream_dot(fmt, golden[f"iqdot{i}_w"], rows, cols, golden[f"iqdot{i}_x"], y, nx=nx,
+                       xstride=st, ystride=rows, fast=False)
+        assert np.array_equal(bits(y), bits(golden[f"iqdot{i}_y"])), (i, fmt, cols, nx)
+    y = np.zeros(1, dtype=np.float32)
+    orc.stream_dot(5, golden["iq_kat_w"], 1, 256, golden["iq_kat_x"], y, fast=False)
+    assert y[0] == golden["iq_kat_y"][0] == 2.0

@@ -19,7 +19,7 @@ from fractions import Fraction
 import numpy as np
 import pytest
 
-from oracle import Q8_0, Q5_0, Q4_K, Q6_K, row_bytes, xq_offset, xqk_offset
+from oracle import Q8_0, Q5_0, Q4_K, Q6_K, IQ2_XXS, IQ3_XXS, row_bytes, xq_offset, xqk_offset
 from util import sane_rows
 
 
@@ -347,3 +347,108 @@ def test_router_ties_and_norm(orc):
     assert abs(float(g.sum()) - 1.0) < 1e-6
     ids, g = orc.router_sel(np.array([0.0, 0.0, 0.0, 0.0], np.float32), 2, norm=0, scale=2.0)
     assert list(ids) == [0, 1] and np.allclose(g, [0.5, 0.5])
+
+
+# ----------------------------------------------------- IQ codebook formats --
+def iq_grids():
+    """The codebook values as written in the product header (their digest
+    is pinned to the reference's tables in test_oracle_golden.py)."""
+    import os
+    import re
+    src = open(os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
+                            "fast-llm_amd", "csrc", "flh_iq_grids.h")).read()
+    g2 = src.split("FLH_IQ2XXS_GRID_VALUES")[1].split("#define")[0]
+    g3 = src.split("FLH_IQ3XXS_GRID_VALUES")[1]
+    g2 = np.array([int(v, 16) for v in re.findall(r"0x([0-9a-f]+)ull", g2)], dtype=np.uint64)
+    g3 = np.array([int(v, 16) for v in re.findall(r"0x([0-9a-f]+)u", g3)], dtype=np.uint32)
+    assert g2.size == 256 and g3.size == 256
+    return g2, g3
+
+
+def iq_decode_numpy(fmt, row, cols):
+    """Per 32-element group: db (float32, as (d * (0.5 + s)) * 0.25 or 0.5)
+    and the 32 signed grid magnitudes (quants.h:237-290), vectorised."""
+    g2, g3 = iq_grids()
+    bb = 66 if fmt == IQ2_XXS else 98
+    B = row.reshape(cols // 256, bb)
+    d = h16(B[:, 0:2])[:, 0]
+    if fmt == IQ2_XXS:
+        W = B[:, 2:].reshape(-1, 8, 8)                       # [sb, group, 8 bytes]
+        idx = W[:, :, 0:4].astype(np.int64)                  # grid index of run l
+        w1 = W[:, :, 4:8].copy().view("<u4")[..., 0].astype(np.uint64)
+        mag = ((g2[idx][..., None] >> (8 * np.arange(8, dtype=np.uint64))) & 0xFF).astype(np.int64)
+        mag = mag.reshape(-1, 8, 32)                         # element 8l + j
+        scale = 0.25
+    else:
+        qs = B[:, 2:66].reshape(-1, 8, 8).astype(np.int64)   # [sb, group, 8 indices]
+        w1 = B[:, 66:98].copy().view("<u4").reshape(-1, 8).astype(np.uint64)
+        ent = ((g3[qs][..., None] >> (8 * np.arange(4, dtype=np.uint32))) & 0xFF).astype(np.int64)
+        mag = ent.reshape(-1, 8, 32)                         # entry 2l+h, byte j -> 8l + 4h + j
+        scale = 0.5
+    l = np.arange(32) // 8
+    j = np.arange(32) % 8
+    s7 = (w1[..., None] >> (7 * l).astype(np.uint64)) & 127
+    par = np.zeros_like(s7)
+    for b in range(7):
+        par ^= (s7 >> b) & 1
+    sgn = s7 | (par << 7)
+    neg = (sgn >> j.astype(np.uint64)) & 1
+    val = np.where(neg == 1, -mag, mag)
+    sc = (w1 >> 28).astype(np.float32)
+    db = (d[:, None] * (np.float32(0.5) + sc)) * np.float32(scale)
+    return db.reshape(-1).astype(np.float32), val.reshape(-1, 32)
+
+
+@pytest.mark.parametrize("fmt", [IQ2_XXS, IQ3_XXS])
+def test_iq_dequant_and_canonical_order(orc, fmt):
+    """dequant = db * (+-grid byte); the canonical dot is the single chain
+    acc += (db * v) * x in the element order of quants.h:237-290 (IQ3: 8l+j
+    then 8l+j+4), replayed in float32."""
+    rng = np.random.default_rng(40 + fmt)
+    rows, cols = 3, 512
+    w = sane_rows(fmt, rows, cols, rng)
+    x = rng.standard_normal(cols).astype(np.float32)
+    got = orc.dequant(fmt, w, rows, cols)
+    rb = row_bytes(fmt, cols)
+    order = [8 * l + j for l in range(4) for j in range(8)] if fmt == IQ2_XXS else \
+        [8 * l + j + 4 * h for l in range(4) for j in range(4) for h in range(2)]
+    for r in range(rows):
+        db, val = iq_decode_numpy(fmt, w[r * rb:(r + 1) * rb], cols)
+        want = (db[:, None] * val.astype(np.float32)).reshape(-1)
+        assert np.array_equal(got[r].view(np.uint32), want.view(np.uint32))
+        acc = np.float32(0)
+        for g in range(cols // 32):
+            for e in order:
+                acc = np.float32(acc + np.float32(np.float32(db[g] * np.float32(val[g, e])) * x[32 * g + e]))
+        y = np.zeros(1, np.float32)
+        orc.stream_dot(fmt, w[r * rb:(r + 1) * rb], 1, cols, x, y, fast=False)
+        assert y[0].view(np.uint32) == acc.view(np.uint32)
+
+
+@pytest.mark.parametrize("fmt", [IQ2_XXS, IQ3_XXS])
+def test_iq_int8_replay_and_budget(orc, fmt):
+    """q8_1 dot: exact integer group sums (numpy int64) folded with exactly
+    rounded fmaf into a[b & 3]; and its error against an f64 dot stays in the
+    budget the reference holds its q8_1 dots to (test_runtime.cpp:547-587)."""
+    rng = np.random.default_rng(50 + fmt)
+    cols = 1024
+    mx = 0.0
+    for t in range(60):
+        w = sane_rows(fmt, 1, cols, rng)
+        x = rng.uniform(-1, 1, cols).astype(np.float32)
+        buf = orc.act_q8(x)
+        xq = buf[xq_offset(cols):xq_offset(cols) + (cols // 32) * 36]
+        X = xq.reshape(-1, 36)
+        db, val = iq_decode_numpy(fmt, w, cols)
+        idot = (val * X[:, 4:].view(np.int8).astype(np.int64)).sum(axis=1)
+        dx = h16(X[:, 0:2])[:, 0]
+        a = [np.float32(0)] * 4
+        for b in range(cols // 32):
+            a[b & 3] = fmaf(np.float32(db[b] * dx[b]), np.float32(idot[b]), a[b & 3])
+        want = fold4(a)
+        got = orc.dot_i8_iq(fmt, w.ctypes.data, xq.ctypes.data, cols)
+        assert np.float32(got).view(np.uint32) == np.float32(want).view(np.uint32), t
+        prod = (db[:, None].astype(np.float64) * val).reshape(-1) * x.astype(np.float64)
+        S = max(1e-6, np.sqrt((prod ** 2).sum()))
+        mx = max(mx, abs(float(got) - prod.sum()) / S)
+    assert mx < 2.5e-2, mx

@@ -1,9 +1,9 @@
 """Input generators shared by the tests (not a checker: inputs only)."""
 import numpy as np
 
-from oracle import row_bytes, Q8_0, Q5_0, Q4_K, Q6_K
+from oracle import row_bytes, Q8_0, Q5_0, Q4_K, Q6_K, IQ2_XXS, IQ3_XXS
 
-BLOCK_BYTES = {Q8_0: 34, Q5_0: 22, Q4_K: 144, Q6_K: 210}
+BLOCK_BYTES = {Q8_0: 34, Q5_0: 22, Q4_K: 144, Q6_K: 210, IQ2_XXS: 66, IQ3_XXS: 98}
 
 
 def sane_rows(fmt, rows, cols, rng):
