@@ -28,14 +28,41 @@
 
 namespace flh {
 
+// Development timing probe (compiled only with -DFLH_TRACE): per workgroup,
+// s_memrealtime stamps at entry, after activation staging, at the first
+// landed chunk, after the last chunk and at exit.
+#ifdef FLH_TRACE
+__device__ uint64_t g_ks_trace[8192 * 6];
+#define KS_STAMP(k) do { if (threadIdx.x == 0 && blockIdx.x < 8192) { \
+    g_ks_trace[(size_t)blockIdx.x * 6 + (k)] = __builtin_amdgcn_s_memrealtime(); \
+    if ((k) == 0) g_ks_trace[(size_t)blockIdx.x * 6 + 5] = \
+        ((uint64_t)__builtin_amdgcn_s_getreg((20) | (0 << 6) | (3 << 11)) << 32) | \
+        (uint64_t)__builtin_amdgcn_s_getreg((4) | (0 << 6) | (31 << 11)); } } while (0)
+#else
+#define KS_STAMP(k) do { } while (0)
+#endif
+
+// Wait until at most `behind` chunks' DMAs (NI loads each) are outstanding;
+// behind < D is wave-uniform.
+template <int NI, int D>
+__device__ __forceinline__ void ks_wait_behind(uint32_t behind) {
+    if (D > 4 && behind >= 4) { WAIT_VM(NI * (D > 4 ? 4 : 0)); return; }
+    if (D > 3 && behind >= 3) { WAIT_VM(NI * (D > 3 ? 3 : 0)); return; }
+    if (D > 2 && behind >= 2) { WAIT_VM(NI * (D > 2 ? 2 : 0)); return; }
+    if (D > 1 && behind >= 1) { WAIT_VM(NI); return; }
+    WAIT_VM(0);
+}
 
 // One pass over rows [0, rows) of the matrix at w for nx <= NX columns; the
 // workgroup owns batches batch0, batch0 + G, ...  Ends with every weight DMA
 // drained, so the caller may start another pass on the same LDS.
 template <int FMT, int NX, int D, bool FUSE, bool XREG>
 __device__ __forceinline__ void ks_body(const uint8_t * __restrict__ w, uint32_t rows, uint32_t cols,
-                                        const KsCols<NX> & C, uint32_t nx, uint32_t nr,
+                                        const KsCols<NX> & C, uint32_t nx, uint32_t nrp,
                                         uint32_t batch0, uint32_t G, uint8_t * sm) {
+    // nrp: rows per batch | chunks issued by the prologue << 16 (0: D)
+    const uint32_t nr = nrp & 0xFFFF;
+    const uint32_t pro = (nrp >> 16) ? min(nrp >> 16, (uint32_t)D) : (uint32_t)D;
     constexpr uint32_t B = KS<FMT>::BLK, WIN = KS<FMT>::WIN;
     constexpr int NI = KS<FMT>::NI;
     const uint32_t nsb = cols >> 8;
@@ -52,8 +79,10 @@ __device__ __forceinline__ void ks_body(const uint8_t * __restrict__ w, uint32_t
     int * TI = (int *)(xd + (size_t)NX * nsb * TPS);              // [nr][NX][nsb * TPS]
     int * TM = TI + (size_t)nr * NX * nsb * TPS;                  // Q4_K only
     uint32_t * TH = (uint32_t *)(FMT == FMT_Q4_K ? TM + (size_t)nr * NX * nsb : TM);   // [nr][nsb * TPS]
+    float * ysm = (float *)(TH + (size_t)nr * nsb * TPS);          // [64] old y of the batch
     uint8_t * myst = stages + (size_t)wave * D * WIN;
 
+    KS_STAMP(0);
     const uint32_t nbatch = (rows + nr - 1) / nr;
     auto nci_of = [&](uint32_t bt) -> uint32_t {                  // this wave's chunks in batch bt
         const uint32_t nrow = min(nr, rows - bt * nr);
@@ -61,52 +90,62 @@ __device__ __forceinline__ void ks_body(const uint8_t * __restrict__ w, uint32_t
         return nch > wave ? (nch - wave + 3) / 4 : 0;
     };
     // Issue cursor over this wave's chunk sequence (batches blockIdx.x, +G, ...).
-    // Every call issues exactly NI loads, so the count of loads behind any
-    // chunk is always NI * (D - 1).  Once the sequence is exhausted the loads
-    // repeat the matrix's first chunk: every wave re-reads the same lines,
-    // which stay in L2, instead of adding HBM traffic.
+    // nissued counts the chunks whose DMA was issued; past the end of the
+    // sequence nothing is issued, and the wait before each chunk counts only
+    // the chunks really issued after it.
     uint32_t qbt = batch0, qci = 0, qn = qbt < nbatch ? nci_of(qbt) : 0;
-    const uint8_t * l_wb = w;
-    uint32_t l_ch = 0, l_nsbb = nsb;
-    auto issue_one = [&](uint8_t * stage) {
+    uint32_t nissued = 0, ncons = 0;
+    auto issue_one = [&]() {
+        uint8_t * stage = myst + (nissued % D) * WIN;
         while (qbt < nbatch && qci >= qn) {
             qbt += G;
             qci = 0;
             qn = qbt < nbatch ? nci_of(qbt) : 0;
         }
         if (qbt < nbatch) {
-            l_wb = w + (size_t)qbt * nr * rb;
-            l_ch = wave + 4 * qci;
-            l_nsbb = min(nr, rows - qbt * nr) * nsb;
+            ks_issue<FMT>(w + (size_t)qbt * nr * rb, wave + 4 * qci, min(nr, rows - qbt * nr) * nsb, stage, lane);
             ++qci;
-        } else {
-            l_wb = w;
-            l_ch = 0;
-            l_nsbb = nsb;
+            ++nissued;
         }
-        ks_issue<FMT>(l_wb, l_ch, l_nsbb, stage, lane);
     };
-    // The first D weight chunks are issued right after the activation loads
-    // (which are older, so waiting for them does not wait for the weights).
+    // The first D chunks of the sequence are issued right after the
+    // activation loads.
     auto prologue = [&]() {
 #pragma unroll
-        for (int j = 0; j < D; ++j) issue_one(myst + j * WIN);
+        for (int j = 0; j < D; ++j)
+            if ((uint32_t)j < pro) issue_one();
     };
+
+    // The batch's old y values (y += semantics) go to LDS by a DMA of wave 0:
+    // a register load would make the compiler wait for every weight DMA in
+    // flight before the fold.  The first batch's is issued before anything
+    // else, later ones right after the previous fold; y_at = chunks issued
+    // before it.
+    uint32_t y_at = 0;
+    auto issue_y = [&](uint32_t bt) {
+        if (wave == 0 && bt < nbatch) {
+            const uint32_t row0 = bt * nr, nrow = min(nr, rows - row0);
+            const uint32_t yr = lane / NX, yp = lane % NX;
+            const bool yv = yr < nrow && yp < nx;
+            const float * ya = yv ? col_pick<NX>(C.y, yp) + row0 + yr : C.y[0] + row0;
+            __builtin_amdgcn_global_load_lds(GPTR(ya), LPTR(ysm), 4, 0, 0);
+            y_at = nissued;
+        }
+    };
+    issue_y(batch0);
 
     // ---- activation records, once per workgroup (overlaps the first weight DMAs)
     if constexpr (FUSE) ks_x_fuse<FMT, NX>(C, nx, nsb, cols, xr, xd, batch0 == 0, prologue);
     else ks_x_app<FMT, NX>(C, nx, nsb, cols, xr, xd, prologue);
-    __syncthreads();
+    lds_barrier();
+    KS_STAMP(1);
 
     // XREG (16 % nsb == 0): a lane's superblock position within a row is the
     // same for every chunk, so its activation record stays in registers.
     u32x4a xregs[NX][5];
     if constexpr (XREG) {
 #pragma unroll
-        for (int p = 0; p < NX; ++p)
-#pragma unroll
-            for (int k = 0; k < 5; ++k)
-                xregs[p][k] = *(const u32x4a *)(xr + (((size_t)p * nsb + (s & (nsb - 1))) * 4 + c) * XREC + 16 * k);
+        for (int p = 0; p < NX; ++p) lds_ld_rec(xr + (((size_t)p * nsb + (s & (nsb - 1))) * 4 + c) * XREC, xregs[p]);
     }
     const uint32_t magic = (uint32_t)((0x100000000ull + nsb - 1) / nsb);   // f / nsb, f < 2^16
     const uint32_t fk = tid & 3, fp = (tid >> 2) % NX, frl = tid / (4 * NX);
@@ -120,10 +159,12 @@ __device__ __forceinline__ void ks_body(const uint8_t * __restrict__ w, uint32_t
         const uint8_t * wb = w + (size_t)row0 * rb;
         const bool fok = frl < nrow && fp < nx;
         float * const ycol = col_pick<NX>(C.y, fp);
-        const float yold = ycol[row0 + (frl < nrow ? frl : nrow - 1)];
+        if (bt != batch0) issue_y(bt);
         for (uint32_t i = 0; i < nci; ++i) {
-            // NI * (D - 1) loads were issued after this chunk's
-            WAIT_VM(NI * (D - 1));
+            // wait for this chunk's DMA: (nissued - 1 - ncons) chunks were issued after it
+            ks_wait_behind<NI, D>(nissued - 1 - ncons);
+            ++ncons;
+            if (i == 0 && bt == batch0) KS_STAMP(2);
             uint8_t * st = myst + slot * WIN;
             const uint32_t f = (wave + 4 * i) * 16 + s;            // batch-local superblock
             const bool act = f < nsbb;
@@ -136,17 +177,25 @@ __device__ __forceinline__ void ks_body(const uint8_t * __restrict__ w, uint32_t
             ks_chunk<FMT, NX, XREG>(st, mis, s, c, xr + ((size_t)sb * 4 + c) * XREC, nsb, xregs, ia, im, tag);
             // all reads of this stage are done before it is refilled
             WAIT_LGKM0();
-            issue_one(st);
+            // refill the ring to D chunks in flight (the prologue issued only pro)
+            issue_one();
+            if (ncons == 1)
+                for (int j = 1; j < D; ++j)
+                    if (nissued < ncons + D) issue_one();
             slot = slot + 1 == (uint32_t)D ? 0 : slot + 1;
             ks_park<FMT, NX>(ia, im, tag, act, c, nx, rl, sb, nsb, TI, TM, TH);
         }
-        __syncthreads();
+        // wave 0: chunks issued after the y DMA are the only loads that can be
+        // younger than it and still outstanding (at most D of them)
+        if (wave == 0) ks_wait_behind<NI, D + 1>(min(nissued - y_at, (uint32_t)D));
+        lds_barrier();
+        KS_STAMP(3);
         const float r = ks_fold<FMT, NX>(TI, TM, TH, xd, nsb, fk, fp, frl, fok);
-        if (fok && fk == 0) ycol[row0 + frl] = yold + r;
-        __syncthreads();
+        if (fok && fk == 0) ycol[row0 + frl] = ysm[frl * NX + fp] + r;
+        lds_barrier();
     }
-    // the trailing repeat loads still target this workgroup's LDS: drain them
     WAIT_VM(0);
+    KS_STAMP(4);
 }
 
 template <int FMT, int NX, int D, bool FUSE, bool XREG>
@@ -198,18 +247,24 @@ __global__ __launch_bounds__(256) void k_moe_kstream(MoeArgs a, uint32_t nr) {
 }
 
 // ----------------------------------------------------------------- launch --
-struct KsTune { uint32_t wgs_per_cu, nr, D; };
+struct KsTune { uint32_t wgs_per_cu, nr, D, pro; };
 static KsTune ks_tune() {
     static KsTune t = [] {
-        KsTune d{2, 0, 0};
+        KsTune d{2, 0, 0, 0};
         if (const char * e = getenv("FLH_KS_TUNE")) {
-            unsigned x = 0, y = 0, z = 0;
-            if (sscanf(e, "%u,%u,%u", &x, &y, &z) == 3) d = KsTune{x, y, z};
+            unsigned x = 0, y = 0, z = 0, q = 0;
+            if (sscanf(e, "%u,%u,%u,%u", &x, &y, &z, &q) >= 3) d = KsTune{x, y, z, q};
         }
         return d;
     }();
     return t;
 }
+
+// Chunks each wave requests before the activation is staged (the rest of its
+// ring is requested after its first chunk): a smaller launch-time burst lands
+// the first chunks sooner (measured: Q4_K 4096x4096 5.6 -> 5.3 us, others
+// unchanged).
+static uint32_t ks_pro() { return ks_tune().pro ? ks_tune().pro : 1u; }
 
 static size_t g_lds_limit = 0;
 size_t lds_limit() {
@@ -229,7 +284,7 @@ static int ks_launch_x(const DotArgs & a, uint32_t nr, uint32_t grid, size_t smb
     if (smb > 65536)
         (void)hipFuncSetAttribute((const void *)k_dot_kstream<FMT, NX, D, FUSE, XREG>,
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)smb);
-    hipLaunchKernelGGL((k_dot_kstream<FMT, NX, D, FUSE, XREG>), dim3(grid), dim3(256), smb, s, a, nr);
+    hipLaunchKernelGGL((k_dot_kstream<FMT, NX, D, FUSE, XREG>), dim3(grid), dim3(256), smb, s, a, nr | (ks_pro() << 16));
     return hip_check(hipGetLastError(), "k_dot_kstream launch");
 }
 template <int FMT, int NX, int D, bool FUSE>
@@ -279,7 +334,7 @@ static int ks_launch(const DotArgs & a, hipStream_t s) {
 
 template <int FMT, int NX, int D, bool XREG>
 static int moe_launch_x(const MoeArgs & a, uint32_t nr, uint32_t gx, size_t smb, hipStream_t s) {
-    hipLaunchKernelGGL((k_moe_kstream<FMT, NX, D, XREG>), dim3(gx, a.n_expert), dim3(256), smb, s, a, nr);
+    hipLaunchKernelGGL((k_moe_kstream<FMT, NX, D, XREG>), dim3(gx, a.n_expert), dim3(256), smb, s, a, nr | (ks_pro() << 16));
     return hip_check(hipGetLastError(), "k_moe_kstream launch");
 }
 template <int FMT, int NX, int D>
@@ -348,6 +403,12 @@ static int ks_dispatch(int fmt, const DotArgs & a, hipStream_t s) {
     }
     return FLH_ERR_UNSUPPORTED;
 }
+
+#ifdef FLH_TRACE
+extern "C" int flh_ks_trace(uint64_t * host, size_t n) {
+    return hipMemcpyFromSymbol(host, HIP_SYMBOL(g_ks_trace), n * 8, 0, hipMemcpyDeviceToHost) == hipSuccess ? 0 : -2;
+}
+#endif
 
 int launch_dot_kstream(int fmt, const DotArgs & a, hipStream_t s) { return ks_dispatch<false>(fmt, a, s); }
 int launch_act_dot_kstream(int fmt, const DotArgs & a, hipStream_t s) { return ks_dispatch<true>(fmt, a, s); }

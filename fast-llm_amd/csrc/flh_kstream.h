@@ -32,6 +32,44 @@ namespace flh {
 #define FLH_KS_AUX 2
 #endif
 
+// Workgroup barrier for LDS data only: waits for this wave's LDS operations,
+// not for its outstanding global loads, so the direct-to-LDS weight DMAs stay
+// in flight across it (each wave waits for its own stages explicitly).
+// __syncthreads() would also wait for every outstanding global load.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+typedef uint32_t u32x4a __attribute__((ext_vector_type(4)));
+
+// LDS offset of a pointer into __shared__ memory
+__device__ __forceinline__ uint32_t lds_off(const void * p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+// LDS accesses hidden from the compiler's wait-count pass.  A plain LDS access
+// issued while direct-to-LDS DMAs are in flight makes the compiler wait for
+// every outstanding global load (it cannot tell the LDS regions apart); these
+// wait only for the loads that produce their register operands.  Reads wait
+// for their own completion inside the asm.
+__device__ __forceinline__ void lds_st128(void * p, u32x4a v) {
+    asm volatile("ds_write_b128 %0, %1" :: "v"(lds_off(p)), "v"(v));
+}
+__device__ __forceinline__ void lds_st32(void * p, uint32_t v) {
+    asm volatile("ds_write_b32 %0, %1" :: "v"(lds_off(p)), "v"(v));
+}
+__device__ __forceinline__ void lds_max32(void * p, uint32_t v) {
+    asm volatile("ds_max_u32 %0, %1" :: "v"(lds_off(p)), "v"(v));
+}
+__device__ __forceinline__ uint32_t lds_ld32(const void * p) {
+    uint32_t v;
+    asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(lds_off(p)) : "memory");
+    return v;
+}
+// five consecutive 16-byte words (one 80-byte activation record)
+__device__ __forceinline__ void lds_ld_rec(const void * p, u32x4a (&v)[5]) {
+    asm volatile("ds_read_b128 %0, %5\n\tds_read_b128 %1, %5 offset:16\n\tds_read_b128 %2, %5 offset:32\n\t"
+                 "ds_read_b128 %3, %5 offset:48\n\tds_read_b128 %4, %5 offset:64\n\ts_waitcnt lgkmcnt(0)"
+                 : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]) : "v"(lds_off(p)) : "memory");
+}
+
 template <int FMT> struct KS;
 template <> struct KS<FMT_Q4_K> {
     static constexpr uint32_t BLK = 144;
@@ -67,7 +105,7 @@ __host__ __device__ inline size_t ks_term_bytes(uint32_t nr, uint32_t nx, uint32
 }
 template <int FMT>
 __host__ __device__ inline size_t ks_smem_bytes(uint32_t nr, uint32_t nx, uint32_t nsb, int D) {
-    return (size_t)4 * D * KS<FMT>::WIN + ks_xrec_bytes<FMT>(nx, nsb) + ks_term_bytes<FMT>(nr, nx, nsb);
+    return (size_t)4 * D * KS<FMT>::WIN + ks_xrec_bytes<FMT>(nx, nsb) + ks_term_bytes<FMT>(nr, nx, nsb) + 256;
 }
 
 // Issue the DMA of chunk `ch` (batch-local) into a stage.  Lanes past the
@@ -106,8 +144,6 @@ __device__ __forceinline__ void ks_issue(const uint8_t * wb, uint32_t ch, uint32
         }
     }
 }
-
-typedef uint32_t u32x4a __attribute__((ext_vector_type(4)));
 
 // 16 bytes at an even LDS byte offset (realigned from 5 aligned dwords)
 __device__ __forceinline__ void lds16_u2(const uint8_t * base, uint32_t off, uint32_t (&o)[4]) {
@@ -212,18 +248,18 @@ __device__ __forceinline__ void ks_x_fuse(const KsCols<NX> & C, uint32_t nx, uin
             after_loads();
             issued = true;
         }
-        if (tid < 64) amx[tid] = 0u;
-        __syncthreads();
+        if (tid < 64) lds_st32(&amx[tid], 0u);
+        lds_barrier();
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-            if ((uint32_t)q < nq) atomicMax(&amx[16 * q + 4 * wave + sub], __float_as_uint(ks_absmax16(raw[q])));
-        __syncthreads();
+            if ((uint32_t)q < nq) lds_max32(&amx[16 * q + 4 * wave + sub], __float_as_uint(ks_absmax16(raw[q])));
+        lds_barrier();
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const uint32_t i = base + 16 * q + 4 * wave + sub;
             if ((uint32_t)q < nq && i < nitem) {
                 const uint32_t p = i / nsb, sb = i % nsb;
-                const float amax = __uint_as_float(amx[16 * q + 4 * wave + sub]);
+                const float amax = __uint_as_float(lds_ld32(&amx[16 * q + 4 * wave + sub]));
                 const float d = amax / 127.f;
                 const float id = amax > 0.f ? 127.f / amax : 0.f;
                 uint32_t pk[4];
@@ -232,9 +268,9 @@ __device__ __forceinline__ void ks_x_fuse(const KsCols<NX> & C, uint32_t nx, uin
                 uint32_t cc, kk, t;
                 xrec_pos<FMT>(16 * run, cc, kk, t);
                 uint8_t * rec = xr + (((size_t)p * nsb + sb) * 4 + cc) * XREC;
-                *(u32x4a *)(rec + 16 * kk) = u32x4a{pk[0], pk[1], pk[2], pk[3]};
-                *(int *)(rec + 64 + 4 * kk) = FMT == FMT_Q4_K ? sum : 32 * sum;
-                if (run == 0) xd[p * nsb + sb] = d;
+                lds_st128(rec + 16 * kk, u32x4a{pk[0], pk[1], pk[2], pk[3]});
+                lds_st32(rec + 64 + 4 * kk, (uint32_t)(FMT == FMT_Q4_K ? sum : 32 * sum));
+                if (run == 0) lds_st32(&xd[p * nsb + sb], __float_as_uint(d));
                 if (write_app) {
                     float * xc = (float *)col_pick<NX>(C.x, p);
                     uint8_t * q8k = (uint8_t *)xc + xqk_off(cols) + (size_t)sb * 292;
@@ -260,7 +296,7 @@ __device__ __forceinline__ void ks_x_fuse(const KsCols<NX> & C, uint32_t nx, uin
                 }
             }
         }
-        __syncthreads();
+        lds_barrier();
     }
     if (!issued) after_loads();
     // columns p >= nx of the template width read zero records
@@ -325,17 +361,15 @@ __device__ __forceinline__ void ks_x_app(const KsCols<NX> & C, uint32_t nx, uint
         const float dk = FMT == FMT_Q8_0 ? 0.f : *(const float *)xb;
         after_loads();
         if (tid < NX * nsb * 4) {
-            uint32_t * rec = (uint32_t *)(xr + (size_t)tid * XREC);
+            uint8_t * rec = xr + (size_t)tid * XREC;
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                rec[4 * k + 0] = v[k].x; rec[4 * k + 1] = v[k].y; rec[4 * k + 2] = v[k].z; rec[4 * k + 3] = v[k].w;
-                rec[16 + k] = (uint32_t)bs[k];
-            }
+            for (int k = 0; k < 4; ++k) lds_st128(rec + 16 * k, u32x4a{v[k].x, v[k].y, v[k].z, v[k].w});
+            lds_st128(rec + 64, u32x4a{(uint32_t)bs[0], (uint32_t)bs[1], (uint32_t)bs[2], (uint32_t)bs[3]});
             if constexpr (FMT == FMT_Q8_0) {
-                xd[(p * nsb + sb) * 8 + 2 * cc] = (p < nx) ? h2f((uint32_t)bs[0]) : 0.f;
-                xd[(p * nsb + sb) * 8 + 2 * cc + 1] = (p < nx) ? h2f((uint32_t)bs[1]) : 0.f;
+                lds_st32(&xd[(p * nsb + sb) * 8 + 2 * cc], __float_as_uint((p < nx) ? h2f((uint32_t)bs[0]) : 0.f));
+                lds_st32(&xd[(p * nsb + sb) * 8 + 2 * cc + 1], __float_as_uint((p < nx) ? h2f((uint32_t)bs[1]) : 0.f));
             } else if (cc == 0) {
-                xd[p * nsb + sb] = (p < nx) ? dk : 0.f;
+                lds_st32(&xd[p * nsb + sb], __float_as_uint((p < nx) ? dk : 0.f));
             }
         }
     } else {
