@@ -54,12 +54,14 @@ __device__ __forceinline__ void ks_wait_behind(uint32_t behind) {
 }
 
 // One pass over rows [0, rows) of the matrix at w for nx <= NX columns; the
-// workgroup owns batches batch0, batch0 + G, ...  Ends with every weight DMA
+// workgroup g of G owns the contiguous rows [rows*g/G, rows*(g+1)/G) (an
+// even split: workgroups differ by at most one row), streamed in batches of at
+// most nr rows.  Ends with every weight DMA
 // drained, so the caller may start another pass on the same LDS.
 template <int FMT, int NX, int D, bool FUSE, bool XREG>
 __device__ __forceinline__ void ks_body(const uint8_t * __restrict__ w, uint32_t rows, uint32_t cols,
                                         const KsCols<NX> & C, uint32_t nx, uint32_t nrp,
-                                        uint32_t batch0, uint32_t G, uint8_t * sm) {
+                                        uint32_t g, uint32_t G, uint8_t * sm) {
     // nrp: rows per batch | chunks issued by the prologue << 16 (0: D)
     const uint32_t nr = nrp & 0xFFFF;
     const uint32_t pro = (nrp >> 16) ? min(nrp >> 16, (uint32_t)D) : (uint32_t)D;
@@ -83,9 +85,11 @@ __device__ __forceinline__ void ks_body(const uint8_t * __restrict__ w, uint32_t
     uint8_t * myst = stages + (size_t)wave * D * WIN;
 
     KS_STAMP(0);
-    const uint32_t nbatch = (rows + nr - 1) / nr;
+    const uint32_t rbeg = (uint32_t)((uint64_t)rows * g / G);
+    const uint32_t rend = (uint32_t)((uint64_t)rows * (g + 1) / G);
+    const uint32_t nbatch = (rend - rbeg + nr - 1) / nr;          // batches of this workgroup
     auto nci_of = [&](uint32_t bt) -> uint32_t {                  // this wave's chunks in batch bt
-        const uint32_t nrow = min(nr, rows - bt * nr);
+        const uint32_t nrow = min(nr, rend - rbeg - bt * nr);
         const uint32_t nch = (nrow * nsb + 15) / 16;
         return nch > wave ? (nch - wave + 3) / 4 : 0;
     };
@@ -93,17 +97,18 @@ __device__ __forceinline__ void ks_body(const uint8_t * __restrict__ w, uint32_t
     // nissued counts the chunks whose DMA was issued; past the end of the
     // sequence nothing is issued, and the wait before each chunk counts only
     // the chunks really issued after it.
-    uint32_t qbt = batch0, qci = 0, qn = qbt < nbatch ? nci_of(qbt) : 0;
+    uint32_t qbt = 0, qci = 0, qn = qbt < nbatch ? nci_of(qbt) : 0;
     uint32_t nissued = 0, ncons = 0;
     auto issue_one = [&]() {
         uint8_t * stage = myst + (nissued % D) * WIN;
         while (qbt < nbatch && qci >= qn) {
-            qbt += G;
+            ++qbt;
             qci = 0;
             qn = qbt < nbatch ? nci_of(qbt) : 0;
         }
         if (qbt < nbatch) {
-            ks_issue<FMT>(w + (size_t)qbt * nr * rb, wave + 4 * qci, min(nr, rows - qbt * nr) * nsb, stage, lane);
+            ks_issue<FMT>(w + (size_t)(rbeg + qbt * nr) * rb, wave + 4 * qci, min(nr, rend - rbeg - qbt * nr) * nsb,
+                          stage, lane);
             ++qci;
             ++nissued;
         }
@@ -124,7 +129,7 @@ __device__ __forceinline__ void ks_body(const uint8_t * __restrict__ w, uint32_t
     uint32_t y_at = 0;
     auto issue_y = [&](uint32_t bt) {
         if (wave == 0 && bt < nbatch) {
-            const uint32_t row0 = bt * nr, nrow = min(nr, rows - row0);
+            const uint32_t row0 = rbeg + bt * nr, nrow = min(nr, rend - row0);
             const uint32_t yr = lane / NX, yp = lane % NX;
             const bool yv = yr < nrow && yp < nx;
             const float * ya = yv ? col_pick<NX>(C.y, yp) + row0 + yr : C.y[0] + row0;
@@ -132,10 +137,10 @@ __device__ __forceinline__ void ks_body(const uint8_t * __restrict__ w, uint32_t
             y_at = nissued;
         }
     };
-    issue_y(batch0);
+    issue_y(0);
 
     // ---- activation records, once per workgroup (overlaps the first weight DMAs)
-    if constexpr (FUSE) ks_x_fuse<FMT, NX>(C, nx, nsb, cols, xr, xd, batch0 == 0, prologue);
+    if constexpr (FUSE) ks_x_fuse<FMT, NX>(C, nx, nsb, cols, xr, xd, g == 0, prologue);
     else ks_x_app<FMT, NX>(C, nx, nsb, cols, xr, xd, prologue);
     lds_barrier();
     KS_STAMP(1);
@@ -151,20 +156,20 @@ __device__ __forceinline__ void ks_body(const uint8_t * __restrict__ w, uint32_t
     const uint32_t fk = tid & 3, fp = (tid >> 2) % NX, frl = tid / (4 * NX);
     uint32_t slot = 0;                                            // ring stage of the next chunk
 
-    for (uint32_t bt = batch0; bt < nbatch; bt += G) {
-        const uint32_t row0 = bt * nr;
-        const uint32_t nrow = min(nr, rows - row0);
+    for (uint32_t bt = 0; bt < nbatch; ++bt) {
+        const uint32_t row0 = rbeg + bt * nr;
+        const uint32_t nrow = min(nr, rend - row0);
         const uint32_t nsbb = nrow * nsb;                       // superblocks in this batch
         const uint32_t nci = nci_of(bt);
         const uint8_t * wb = w + (size_t)row0 * rb;
         const bool fok = frl < nrow && fp < nx;
         float * const ycol = col_pick<NX>(C.y, fp);
-        if (bt != batch0) issue_y(bt);
+        if (bt != 0) issue_y(bt);
         for (uint32_t i = 0; i < nci; ++i) {
             // wait for this chunk's DMA: (nissued - 1 - ncons) chunks were issued after it
             ks_wait_behind<NI, D>(nissued - 1 - ncons);
             ++ncons;
-            if (i == 0 && bt == batch0) KS_STAMP(2);
+            if (i == 0 && bt == 0) KS_STAMP(2);
             uint8_t * st = myst + slot * WIN;
             const uint32_t f = (wave + 4 * i) * 16 + s;            // batch-local superblock
             const bool act = f < nsbb;
@@ -310,6 +315,10 @@ static int ks_plan(uint32_t rows, uint32_t nx_t, uint32_t nsb, uint32_t slots, i
     while (ks_smem_bytes<FMT>(nr, nx_t, nsb, D) > lim && nr > 4) nr >>= 1;
     while (ks_smem_bytes<FMT>(nr, nx_t, nsb, D) > lim && D > 2) --D;
     while (ks_smem_bytes<FMT>(nr, nx_t, nsb, D) > lim && nr > 1) nr >>= 1;
+    // equal batches: a workgroup's ceil(rows / slots) rows in the fewest batches
+    const uint32_t g = rows < slots ? rows : slots;
+    const uint32_t rpw = (rows + g - 1) / g, nb = (rpw + nr - 1) / nr;
+    nr = (rpw + nb - 1) / nb;
     smb = ks_smem_bytes<FMT>(nr, nx_t, nsb, D);
     return smb > lim ? FLH_ERR_UNSUPPORTED : FLH_OK;
 }
@@ -323,8 +332,7 @@ static int ks_launch(const DotArgs & a, hipStream_t s) {
     int D;
     size_t smb;
     if (ks_plan<FMT>(a.rows, NX, nsb, slots, 2, nr, D, smb)) return FLH_ERR_UNSUPPORTED;
-    const uint32_t nbatch = (a.rows + nr - 1) / nr;
-    const uint32_t grid = nbatch < slots ? nbatch : slots;
+    const uint32_t grid = a.rows < slots ? a.rows : slots;
     switch (D) {
         case 2: return ks_launch_d<FMT, NX, 2, FUSE>(a, nr, grid, smb, s);
         case 3: return ks_launch_d<FMT, NX, 3, FUSE>(a, nr, grid, smb, s);
@@ -354,8 +362,7 @@ static int moe_launch(const MoeArgs & a, hipStream_t s) {
     int D;
     size_t smb;
     if (ks_plan<FMT>(a.rows, NX, nsb, gx, 2, nr, D, smb)) return FLH_ERR_UNSUPPORTED;
-    const uint32_t nbatch = (a.rows + nr - 1) / nr;
-    const uint32_t g = nbatch < gx ? nbatch : gx;
+    const uint32_t g = a.rows < gx ? a.rows : gx;
     switch (D) {
         case 2: return moe_launch_d<FMT, NX, 2>(a, nr, g, smb, s);
         case 3: return moe_launch_d<FMT, NX, 3>(a, nr, g, smb, s);

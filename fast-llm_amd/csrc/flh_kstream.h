@@ -180,12 +180,19 @@ struct KsCols {
     float * y[NX];
 };
 // runtime column select without dynamic register indexing
+// (each candidate passes through an empty asm so that the compiler cannot fold
+// the select chain back into an indexed access of a stack array, which a
+// lane-varying p would turn into scratch memory)
 template <int NX, typename T>
 __device__ __forceinline__ T col_pick(T const (&v)[NX], uint32_t p) {
-    T r = v[0];
+    uint64_t r = (uint64_t)v[0];
 #pragma unroll
-    for (int i = 1; i < NX; ++i) r = p == (uint32_t)i ? v[i] : r;
-    return r;
+    for (int i = 1; i < NX; ++i) {
+        uint64_t vi = (uint64_t)v[i];
+        asm volatile("" : "+v"(vi));
+        r = p == (uint32_t)i ? vi : r;
+    }
+    return (T)r;
 }
 
 __device__ __forceinline__ uint32_t ks_quant16(const u32x4a (&raw)[4], float id, int & sum, uint32_t (&pk)[4]) {
