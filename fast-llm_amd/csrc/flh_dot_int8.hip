@@ -643,6 +643,25 @@ int launch_dot_i8k(int fmt, const DotArgs & a0, hipStream_t s) {
     if (nsb == 0 || nsb > 64 || (a0.cols & 255))
         return set_error(FLH_ERR_UNSUPPORTED, "i8k dot: cols must be a multiple of 256, <= 16384");
     if (a0.rows == 0 || a0.nx == 0) return FLH_OK;
+    // several Q4_K columns: the int8 matrix-core kernel, all columns in one
+    // pass when they fit its LDS plan, else in groups of 8 or 4
+    if (fmt == FMT_Q4_K && a0.nx >= mfma_min_cols(a0.cols)) {
+        for (uint32_t gs : {16u, 8u, 4u}) {
+            if (gs < 16 && a0.nx <= gs) continue;
+            int rc = FLH_OK;
+            for (uint32_t p0 = 0; p0 < a0.nx && rc == FLH_OK; p0 += gs) {
+                DotArgs a = a0;
+                a.nx = a0.nx - p0 < gs ? a0.nx - p0 : gs;
+                a.x = a0.x + (size_t)p0 * a0.xstride;
+                a.y = a0.y + (size_t)p0 * a0.ystride;
+                rc = launch_dot_mfma(fmt, a, s);
+                // the plan depends on the column count only through NC, so a
+                // later (narrower) group never fails where the first fitted
+                if (rc == FLH_ERR_UNSUPPORTED && p0 != 0) return set_error(rc, "mfma dot: group plan");
+            }
+            if (rc != FLH_ERR_UNSUPPORTED) return rc;
+        }
+    }
     for (uint32_t p0 = 0; p0 < a0.nx; p0 += 4) {
         DotArgs a = a0;
         a.nx = a0.nx - p0 < 4 ? a0.nx - p0 : 4;

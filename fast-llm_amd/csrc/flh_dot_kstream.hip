@@ -42,17 +42,6 @@ __device__ uint64_t g_ks_trace[8192 * 6];
 #define KS_STAMP(k) do { } while (0)
 #endif
 
-// Wait until at most `behind` chunks' DMAs (NI loads each) are outstanding;
-// behind < D is wave-uniform.
-template <int NI, int D>
-__device__ __forceinline__ void ks_wait_behind(uint32_t behind) {
-    if (D > 4 && behind >= 4) { WAIT_VM(NI * (D > 4 ? 4 : 0)); return; }
-    if (D > 3 && behind >= 3) { WAIT_VM(NI * (D > 3 ? 3 : 0)); return; }
-    if (D > 2 && behind >= 2) { WAIT_VM(NI * (D > 2 ? 2 : 0)); return; }
-    if (D > 1 && behind >= 1) { WAIT_VM(NI); return; }
-    WAIT_VM(0);
-}
-
 // One pass over rows [0, rows) of the matrix at w for nx <= NX columns; the
 // workgroup g of G owns the contiguous rows [rows*g/G, rows*(g+1)/G) (an
 // even split: workgroups differ by at most one row), streamed in batches of at

@@ -1,0 +1,443 @@
+// flh_dot_mfma.hip -- multi-column Q4_K x q8_K row-dots (speculative verify,
+// grouped MoE experts) on gfx950's int8 matrix cores.
+//
+// With several activation columns the per-lane VALU dot of the streaming
+// kernel (flh_dot_kstream.hip) becomes instruction-bound (about 300 wave
+// instructions per 2304-byte chunk at 4 columns).  Here the integer dot of
+// every 32-weight sub-block is one MFMA over a 16-row tile:
+//
+//   D[n][r] = sum_k x_n[k] * q_r[k]      v_mfma_i32_16x16x32_i8
+//             A = activations (16 columns x 32), B = weight nibbles (32 x 16 rows)
+//
+// so lane l owns weight row r = l % 16 and activation columns 4*(l/16) + i,
+// and decodes only its own row's 6-bit scales.  The scale-weighted sum
+// iacc = sum_g sc_g * D_g is exact integer VALU work; the min term
+// imins = sum_g m_g * (bsum[2g] + bsum[2g+1]) is a 16x16x8 product done as two
+// v_mfma_f32_16x16x4f32 whose operands and sums are integers below 2^24, so
+// it is exact too.  The (row, column, superblock) integer terms are parked in
+// LDS and folded in the reference order (acc[sb & 3], fl_dot_i8k_q4_K,
+// src/runtime/quants.h:538-561), so every output is bitwise equal to the
+// reference CPU path, as with the streaming kernel.
+//
+// Weights stream HBM -> LDS with direct-to-LDS loads in chunks of one
+// superblock of a 16-row tile (16 x 144 bytes); the chunks of a workgroup's
+// rows are dealt round-robin to its 8 waves, each with a D-deep ring.  The
+// activation columns are staged once per workgroup in the MFMA A layout.
+#include "flh_kstream.h"
+#include "flh_internal.h"
+#include "flh_status.h"
+#include <stdio.h>
+#include <stdlib.h>
+
+namespace flh {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// Development timing probe (-DFLH_TRACE): per workgroup, s_memrealtime at
+// entry, after activation staging, first chunk, last chunk and exit.
+#ifdef FLH_TRACE
+__device__ uint64_t g_mf_trace[8192 * 6];
+#define MF_STAMP(k) do { if (threadIdx.x == 0 && blockIdx.x < 8192) \
+    g_mf_trace[(size_t)blockIdx.x * 6 + (k)] = __builtin_amdgcn_s_memrealtime(); } while (0)
+extern "C" int flh_mf_trace(uint64_t * host, size_t n) {
+    return hipMemcpyFromSymbol(host, HIP_SYMBOL(g_mf_trace), n * 8, 0, hipMemcpyDeviceToHost) == hipSuccess ? 0 : -2;
+}
+#else
+#define MF_STAMP(k) do { } while (0)
+#endif
+
+// cache policy of the weight DMA (2 = nontemporal)
+#ifndef FLH_MF_AUX
+#define FLH_MF_AUX 2
+#endif
+
+constexpr uint32_t MF_WAVES = 8;
+constexpr uint32_t MF_CHUNK = 2304;          // 16 rows x one Q4_K superblock
+constexpr int MF_NI = 3;                     // DMA instructions per chunk
+
+// LDS: [waves][D][2304] ring | xr [NC][XS] raw q8_K appendices | TI, TM [nrb][NC][nsb]
+//      | TH [nrb][nsb] | ysm [nrb * NC]
+// XS: a column's appendix (292 bytes per superblock) padded so that XS / 4 is
+// 8 mod 32 (the 16 columns' reads of one k-slice fall in distinct banks).
+__host__ __device__ inline uint32_t mf_xs(uint32_t nsb) { return ((nsb * 292 + 127) & ~127u) + 32; }
+template <int NC>
+__host__ __device__ inline size_t mf_smem_bytes(uint32_t nrb, uint32_t nsb, int D) {
+    return (size_t)MF_WAVES * D * MF_CHUNK + (size_t)NC * mf_xs(nsb) + (size_t)nrb * NC * nsb * 8 +
+           (size_t)nrb * nsb * 4 + (size_t)nrb * NC * 4;
+}
+
+// Column sources of one pass: activation column p at x(p) (fp32 x followed by
+// its appendices), output column p at y(p).
+struct MfColsStrided {
+    const float * x0;
+    float * y0;
+    uint32_t xs, ys;
+    __device__ const float * x(uint32_t p) const { return x0 + (size_t)p * xs; }
+    __device__ float * y(uint32_t p) const { return y0 + (size_t)p * ys; }
+};
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Activation operands of one superblock from column r's raw q8_K block at xs:
+// xw[2c + h] = bytes 36 + 64c + 32h + 8j .. +7 (sub-block 2c + h, k-slice j),
+// bp = the bsum pairs of sub-blocks j and 4 + j.  Hidden from the compiler's
+// wait-count pass (a plain read of DMA-written LDS would wait for every
+// outstanding load); waits for its own reads.
+__device__ __forceinline__ void mf_ld_x(const uint8_t * xs, uint32_t j, u32x2 (&xw)[8], u32x2 & bp) {
+    const uint32_t a8 = lds_off(xs) + 8 * j, a4 = lds_off(xs) + 4 * j;
+    asm volatile(
+        "ds_read2_b32 %0, %9 offset0:9 offset1:10\n\t"
+        "ds_read2_b32 %1, %9 offset0:17 offset1:18\n\t"
+        "ds_read2_b32 %2, %9 offset0:25 offset1:26\n\t"
+        "ds_read2_b32 %3, %9 offset0:33 offset1:34\n\t"
+        "ds_read2_b32 %4, %9 offset0:41 offset1:42\n\t"
+        "ds_read2_b32 %5, %9 offset0:49 offset1:50\n\t"
+        "ds_read2_b32 %6, %9 offset0:57 offset1:58\n\t"
+        "ds_read2_b32 %7, %9 offset0:65 offset1:66\n\t"
+        "ds_read2_b32 %8, %10 offset0:1 offset1:5\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(xw[0]), "=&v"(xw[1]), "=&v"(xw[2]), "=&v"(xw[3]), "=&v"(xw[4]), "=&v"(xw[5]), "=&v"(xw[6]),
+          "=&v"(xw[7]), "=&v"(bp)
+        : "v"(a8), "v"(a4));
+}
+
+// Reference-order fold of row rl, column p (terms [sb][row][column]; the
+// q8_K scale read from the column's raw appendix at xp): lane k runs
+// accumulator k over superblocks k, k + 4, ... (loads of four steps issued
+// together); the quad then combines (a0 + a1) + (a2 + a3).  Same float
+// operations, in the same order, as ks_fold and fl_dot_i8k_q4_K.
+template <int NC>
+__device__ __forceinline__ float mf_fold(const int * TI, const int * TM, const uint32_t * TH, const uint8_t * xp,
+                                         uint32_t nsb, uint32_t nrb, uint32_t k, uint32_t p, uint32_t rl, bool fok) {
+    float acc = 0.f;
+    if (fok) {
+        auto step = [&](int ti, int tm, uint32_t th, float dk) {
+            const float d = h2f(th & 0xFFFFu), dmin = h2f(th >> 16);
+            acc = fmaf(d * dk, (float)ti, acc);
+            acc = fmaf(-(dmin * dk), (float)tm, acc);
+        };
+        uint32_t s = k;
+        for (; s + 12 < nsb; s += 16) {
+            int ti[4], tm[4];
+            uint32_t th[4];
+            float dk[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint32_t sq = s + 4 * q;
+                ti[q] = TI[((size_t)sq * nrb + rl) * NC + p];
+                tm[q] = TM[((size_t)sq * nrb + rl) * NC + p];
+                th[q] = TH[(size_t)sq * nrb + rl];
+                dk[q] = *(const float *)(xp + (size_t)sq * 292);
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) step(ti[q], tm[q], th[q], dk[q]);
+        }
+        for (; s < nsb; s += 4)
+            step(TI[((size_t)s * nrb + rl) * NC + p], TM[((size_t)s * nrb + rl) * NC + p], TH[(size_t)s * nrb + rl],
+                 *(const float *)(xp + (size_t)s * 292));
+    }
+    const float s01 = acc + qx1f(acc);
+    return s01 + qx2f(s01);
+}
+
+// One pass over the rows [rows*g/G, rows*(g+1)/G) for nx <= NC columns, in
+// batches of nrb rows (a multiple of 16).  A chunk is superblock sb of a
+// 16-row tile of the batch; the batch's chunks q = (tile, sb), tile-major, are
+// dealt to the waves round-robin.
+template <int NC, int D, typename COLS>
+__device__ __forceinline__ void mf_body(const uint8_t * __restrict__ w, uint32_t rows, uint32_t cols,
+                                        const COLS & C, uint32_t nx, uint32_t nrbp, uint32_t g, uint32_t G,
+                                        uint8_t * sm) {
+    // nrbp: rows per batch | chunks issued before the first is consumed << 16 (0: D)
+    const uint32_t nrb = nrbp & 0xFFFF;
+    const uint32_t pro = (nrbp >> 16) ? min(nrbp >> 16, (uint32_t)D) : (uint32_t)D;
+    const uint32_t nsb = cols >> 8;
+    const uint64_t rb = (uint64_t)nsb * 144;
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t r = lane & 15, j = lane >> 4;
+
+    uint8_t * myst = sm + (size_t)wave * D * MF_CHUNK;
+    const uint32_t XS = mf_xs(nsb);
+    uint8_t * xr = sm + (size_t)MF_WAVES * D * MF_CHUNK;
+    int * TI = (int *)(xr + (size_t)NC * XS);
+    int * TM = TI + (size_t)nrb * NC * nsb;
+    uint32_t * TH = (uint32_t *)(TM + (size_t)nrb * NC * nsb);
+    float * ysm = (float *)(TH + (size_t)nrb * nsb);
+
+    MF_STAMP(0);
+    const uint32_t rbeg = (uint32_t)((uint64_t)rows * g / G);
+    const uint32_t rend = (uint32_t)((uint64_t)rows * (g + 1) / G);
+    const uint32_t nbatch = (rend - rbeg + nrb - 1) / nrb;
+    auto nrow_of = [&](uint32_t bt) -> uint32_t { return min(nrb, rend - rbeg - bt * nrb); };
+
+    // ---- activations -> LDS by DMA, issued first (older than every weight
+    // DMA, so the wait before the first chunk covers them): each column's
+    // q8_K appendix copied as is, 1 KiB per instruction, the last 0-12 bytes
+    // by a dword instruction.  Columns past nx copy column 0 (their results
+    // are never stored).
+    {
+        const uint32_t L = nsb * 292, n16 = L >> 4, nti = (n16 + 63) >> 6;   // x4 instructions per column
+        const uint32_t tail = (L & 15) >> 2;                                  // trailing dwords
+        const uint32_t per = nti + (tail ? 1u : 0u);
+        for (uint32_t i = wave; i < NC * per; i += MF_WAVES) {
+            const uint32_t n = i / per, k = i % per;
+            const uint8_t * src = (const uint8_t *)C.x(n < nx ? n : 0) + xqk_off(cols);
+            uint8_t * dst = xr + (size_t)n * XS;
+            if (k < nti) {
+                const uint32_t pc = 64 * k + lane;
+                if (pc < n16) __builtin_amdgcn_global_load_lds(GPTR(src + 16 * pc), LPTR(dst + 1024 * k), 16, 0, 0);
+            } else if (lane < tail) {
+                __builtin_amdgcn_global_load_lds(GPTR(src + 16 * n16 + 4 * lane), LPTR(dst + 16 * n16), 4, 0, 0);
+            }
+        }
+    }
+
+    // ---- weight chunk stream.  Per-lane DMA pieces: piece p (16 bytes) of a
+    // chunk is row p / 9, bytes 16 (p % 9) of its superblock.
+    const uint32_t pr0 = lane / 9, pr1 = (64 + lane) / 9, pr2 = (128 + (lane >> 2)) / 9;
+    const uint32_t po0 = (lane % 9) * 16, po1 = ((64 + lane) % 9) * 16, po2 = ((128 + (lane >> 2)) % 9) * 16 + 4 * (lane & 3);
+    // issue cursor: batch qbt, tile qt, superblock qsb (q = wave + 8 i, tile-major)
+    uint32_t qbt = 0, qt = 0, qsb = wave, qnt = nbatch ? (nrow_of(0) + 15) >> 4 : 0;
+    while (qsb >= nsb) { qsb -= nsb; ++qt; }
+    uint32_t nissued = 0, ncons = 0;
+    auto issue_one = [&]() {
+        while (qbt < nbatch && qt >= qnt) {
+            ++qbt;
+            qt = 0;
+            qsb = wave;
+            while (qsb >= nsb) { qsb -= nsb; ++qt; }
+            qnt = qbt < nbatch ? (nrow_of(qbt) + 15) >> 4 : 0;
+        }
+        if (qbt < nbatch) {
+            const uint32_t tr0 = rbeg + qbt * nrb + 16 * qt;
+            const uint32_t nv1 = min(16u, rend - tr0) - 1;           // last valid row of the tile
+            const uint8_t * base = w + (size_t)tr0 * rb + (size_t)qsb * 144;
+            uint8_t * stage = myst + (nissued % D) * MF_CHUNK;
+            __builtin_amdgcn_global_load_lds(GPTR(base + (size_t)min(pr0, nv1) * rb + po0), LPTR(stage), 16, 0, FLH_MF_AUX);
+            __builtin_amdgcn_global_load_lds(GPTR(base + (size_t)min(pr1, nv1) * rb + po1), LPTR(stage + 1024), 16, 0,
+                                             FLH_MF_AUX);
+            __builtin_amdgcn_global_load_lds(GPTR(base + (size_t)min(pr2, nv1) * rb + po2), LPTR(stage + 2048), 4, 0,
+                                             FLH_MF_AUX);
+            ++nissued;
+            qsb += MF_WAVES;
+            while (qsb >= nsb) { qsb -= nsb; ++qt; }
+        }
+    };
+    // old y of a batch -> LDS (one 64-float DMA per wave; nrb * NC <= 512)
+    bool y_mine = false;
+    uint32_t y_at = 0;
+    auto issue_y = [&](uint32_t bt) {
+        const uint32_t row0 = rbeg + bt * nrb, nrow = nrow_of(bt);
+        y_mine = wave * 64 < nrow * NC;
+        if (y_mine) {
+            const uint32_t e = wave * 64 + lane, yr = e / NC, yp = e % NC;
+            const bool yv = yr < nrow && yp < nx;
+            const float * ya = yv ? C.y(yp) + row0 + yr : C.y(0) + row0;
+            __builtin_amdgcn_global_load_lds(GPTR(ya), LPTR(ysm + wave * 64), 4, 0, 0);
+            y_at = nissued;
+        }
+    };
+    if (nbatch) issue_y(0);
+    // the first pro chunks now (a smaller launch-time burst), the rest of the
+    // ring after the first chunk is consumed
+    for (uint32_t k = 0; k < pro; ++k) issue_one();
+    // the activation and y DMAs are older than the nissued chunks
+    ks_wait_behind<MF_NI, D + 1>(nissued);
+    lds_barrier();
+    MF_STAMP(1);
+
+    const uint32_t fk = tid & 3, fp = (tid >> 2) % NC, frl0 = tid / (4 * NC);
+    constexpr uint32_t FROWS = MF_WAVES * 64 / (4 * NC);         // rows folded per pass
+    uint32_t slot = 0;
+    for (uint32_t bt = 0; bt < nbatch; ++bt) {
+        const uint32_t row0 = rbeg + bt * nrb;
+        const uint32_t nrow = nrow_of(bt);
+        const uint32_t nt = (nrow + 15) >> 4;
+        if (bt != 0) issue_y(bt);
+        uint32_t ct = 0, csb = wave;                               // consume cursor
+        while (csb >= nsb) { csb -= nsb; ++ct; }
+        for (; ct < nt;) {
+            ks_wait_behind<MF_NI, D>(nissued - 1 - ncons);
+            ++ncons;
+            if (ncons == 1) MF_STAMP(2);
+            const uint32_t t = ct, sb = csb;
+            csb += MF_WAVES;
+            while (csb >= nsb) { csb -= nsb; ++ct; }
+            const uint8_t * rp = myst + slot * MF_CHUNK + 144 * r;
+            const u32x4a hd = *(const u32x4a *)rp;
+            uint32_t qw[4][2];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                qw[c][0] = *(const uint32_t *)(rp + 16 + 32 * c + 8 * j);
+                qw[c][1] = *(const uint32_t *)(rp + 20 + 32 * c + 8 * j);
+            }
+            // activation operands of this superblock (zero for lanes past NC):
+            // column r, bytes 32g + 8j .. +7 of sub-block g; sub-block sums
+            // bsum[2g] + bsum[2g + 1] for g = j and 4 + j
+            u32x2 xw[8] = {};
+            u32x2 bp = {};
+            if (r < NC) mf_ld_x(xr + (size_t)r * XS + (size_t)sb * 292, j, xw, bp);
+            const uint32_t bp0 = bp.x, bp1 = bp.y;
+            // every read of this stage is done before it is refilled
+            WAIT_LGKM0();
+            issue_one();
+            if (ncons == 1)
+                for (uint32_t k = 1; k < (uint32_t)D; ++k)
+                    if (nissued < ncons + D) issue_one();
+            slot = slot + 1 == (uint32_t)D ? 0 : slot + 1;
+
+            // scales / mins of row r (6-bit, SWAR as in fl_q4k_scale_min)
+            const uint32_t sclo = hd.y & 0x3F3F3F3Fu, mlo = hd.z & 0x3F3F3F3Fu;
+            const uint32_t schi = (hd.w & 0x0F0F0F0Fu) | ((hd.y >> 2) & 0x30303030u);
+            const uint32_t mhi = ((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u);
+            v4i acc[8];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const uint32_t lo0 = qw[c][0] & 0x0F0F0F0Fu, lo1 = qw[c][1] & 0x0F0F0F0Fu;
+                const uint32_t hi0 = (qw[c][0] >> 4) & 0x0F0F0F0Fu, hi1 = (qw[c][1] >> 4) & 0x0F0F0F0Fu;
+                const long blo = (long)(((uint64_t)lo1 << 32) | lo0), bhi = (long)(((uint64_t)hi1 << 32) | hi0);
+                const long alo = __builtin_bit_cast(long, xw[2 * c]);
+                const long ahi = __builtin_bit_cast(long, xw[2 * c + 1]);
+                acc[2 * c] = __builtin_amdgcn_mfma_i32_16x16x32_i8(alo, blo, v4i{0, 0, 0, 0}, 0, 0, 0);
+                acc[2 * c + 1] = __builtin_amdgcn_mfma_i32_16x16x32_i8(ahi, bhi, v4i{0, 0, 0, 0}, 0, 0, 0);
+            }
+            // min term: A = sub-block sums of column r (g = 4h + j), B = mins of row r
+            const float bsa0 = (float)((int)(int16_t)(bp0 & 0xFFFFu) + (int)(int16_t)(bp0 >> 16));
+            const float bsa1 = (float)((int)(int16_t)(bp1 & 0xFFFFu) + (int)(int16_t)(bp1 >> 16));
+            const float bm0 = (float)((mlo >> (8 * j)) & 0xFFu), bm1 = (float)((mhi >> (8 * j)) & 0xFFu);
+            v4f cm = __builtin_amdgcn_mfma_f32_16x16x4f32(bsa0, bm0, v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            cm = __builtin_amdgcn_mfma_f32_16x16x4f32(bsa1, bm1, cm, 0, 0, 0);
+            int sc[8];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                sc[k] = (int)((sclo >> (8 * k)) & 0xFFu);
+                sc[4 + k] = (int)((schi >> (8 * k)) & 0xFFu);
+            }
+            // park: terms [sb][row][column], the lane's 4 columns in one
+            // 16-byte store (rows past the batch and columns past nx hold
+            // values the fold never reads)
+            const uint32_t rl = 16 * t + r;                         // row within the batch
+            int ia[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                ia[i] = 0;
+#pragma unroll
+                for (int k = 0; k < 8; ++k) ia[i] += __mul24(sc[k], acc[k][i]);
+            }
+            if (4 * j < NC) {
+                const size_t e = ((size_t)sb * nrb + rl) * NC + 4 * j;
+                lds_st128(&TI[e], u32x4a{(uint32_t)ia[0], (uint32_t)ia[1], (uint32_t)ia[2], (uint32_t)ia[3]});
+                lds_st128(&TM[e], u32x4a{(uint32_t)(int)cm[0], (uint32_t)(int)cm[1], (uint32_t)(int)cm[2],
+                                          (uint32_t)(int)cm[3]});
+            }
+            if (j == 0) lds_st32(&TH[(size_t)sb * nrb + rl], hd.x);
+        }
+        if (y_mine) ks_wait_behind<MF_NI, D + 1>(min(nissued - y_at, (uint32_t)D));
+        lds_barrier();
+        MF_STAMP(3);
+        for (uint32_t frl = frl0; frl < nrow; frl += FROWS) {
+            const bool fok = fp < nx;
+            const float rr = mf_fold<NC>(TI, TM, TH, xr + (size_t)fp * XS, nsb, nrb, fk, fp, frl, fok);
+            if (fok && fk == 0) C.y(fp)[row0 + frl] = ysm[frl * NC + fp] + rr;
+        }
+        lds_barrier();
+    }
+    WAIT_VM(0);
+    MF_STAMP(4);
+}
+
+template <int NC, int D>
+__global__ __launch_bounds__(512) void k_dot_mfma(DotArgs a, uint32_t nrb) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t sm[];
+    const uint8_t * w = a.w + (a.id_slot ? (size_t)(*a.id_slot) * a.estride : 0);
+    const MfColsStrided C{a.x, a.y, a.xstride, a.ystride};
+    mf_body<NC, D>(w, a.rows, a.cols, C, a.nx, nrb, blockIdx.x, gridDim.x, sm);
+}
+
+// ----------------------------------------------------------------- launch --
+// chunks each wave requests before the activations are staged (the rest of
+// its ring after its first chunk); 0 = the whole ring (measured best here)
+static uint32_t mf_pro() {
+    static const uint32_t v = [] {
+        const char * e = getenv("FLH_MFMA_PRO");
+        return e ? (uint32_t)atoi(e) : 0u;            // 0: the whole ring
+    }();
+    return v;
+}
+template <int NC, int D>
+static int mf_launch_d(const DotArgs & a, uint32_t nrb, uint32_t grid, size_t smb, hipStream_t s) {
+    (void)hipFuncSetAttribute((const void *)k_dot_mfma<NC, D>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smb);
+    hipLaunchKernelGGL((k_dot_mfma<NC, D>), dim3(grid), dim3(MF_WAVES * 64), smb, s, a, nrb | (mf_pro() << 16));
+    return hip_check(hipGetLastError(), "k_dot_mfma launch");
+}
+
+size_t lds_limit();
+
+
+// LDS plan for NC columns: one workgroup per CU, batch of nrb rows (a multiple
+// of 16), ring depth D; FLH_ERR_UNSUPPORTED if it cannot fit.
+template <int NC>
+static int mf_plan(uint32_t rows, uint32_t nsb, uint32_t G, uint32_t & nrb, int & D, size_t & smb) {
+    const size_t lim = lds_limit();
+    const uint32_t rpw = (rows + G - 1) / G;
+    // a batch's old y values are one 64-float DMA per wave: nrb * NC <= 512
+    nrb = ((rpw + 15) / 16) * 16;
+    if (nrb > 512 / NC) nrb = 512 / NC;
+    // measured: a 2-deep ring with a full prologue beats deeper rings (N=4,
+    // 14336x4096: D=2 11.7 us, D=3 12.4 us, D=4 13.0 us)
+    D = 2;
+    if (const char * e = getenv("FLH_MFMA_TUNE")) {           // "D,nrb" (development sweeps)
+        unsigned d = 0, n = 0;
+        if (sscanf(e, "%u,%u", &d, &n) == 2) {
+            if (d >= 2 && d <= 4) D = (int)d;
+            if (n >= 16 && n % 16 == 0 && n <= 512 / NC) nrb = n;
+        }
+    }
+    while (mf_smem_bytes<NC>(nrb, nsb, D) > lim && nrb > 16) nrb -= 16;
+    while (mf_smem_bytes<NC>(nrb, nsb, D) > lim && D > 2) --D;
+    smb = mf_smem_bytes<NC>(nrb, nsb, D);
+    return smb > lim ? FLH_ERR_UNSUPPORTED : FLH_OK;
+}
+
+template <int NC>
+static int mf_launch(const DotArgs & a, hipStream_t s) {
+    const uint32_t nsb = a.cols >> 8;
+    const uint32_t G = a.rows < (uint32_t)num_cus() ? a.rows : (uint32_t)num_cus();
+    uint32_t nrb;
+    int D;
+    size_t smb;
+    if (mf_plan<NC>(a.rows, nsb, G, nrb, D, smb)) return FLH_ERR_UNSUPPORTED;
+    switch (D) {
+        case 2: return mf_launch_d<NC, 2>(a, nrb, G, smb, s);
+        case 3: return mf_launch_d<NC, 3>(a, nrb, G, smb, s);
+        default: return mf_launch_d<NC, 4>(a, nrb, G, smb, s);
+    }
+}
+
+// Fewest columns for which STREAM_DOT takes the matrix-core kernel (measured:
+// at 2 columns the streaming kernel is faster when a row's activation fits
+// its registers, cols <= 4096, and slower beyond).
+uint32_t mfma_min_cols(uint32_t cols) {
+    static const int v = [] {
+        const char * e = getenv("FLH_MFMA_MIN_COLS");
+        return e ? atoi(e) : 0;
+    }();
+    return v ? (uint32_t)v : (cols > 4096 ? 2u : 3u);
+}
+
+// Q4_K x q8_K with 1..16 columns; FLH_ERR_UNSUPPORTED (nothing launched) when
+// the shape does not fit (the caller then splits the columns).
+int launch_dot_mfma(int fmt, const DotArgs & a, hipStream_t s) {
+    const uint32_t nsb = a.cols >> 8;
+    if (fmt != FMT_Q4_K || nsb == 0 || (a.cols & 255) || nsb > 64 || a.nx < 1 || a.nx > 16)
+        return FLH_ERR_UNSUPPORTED;
+    if (((uintptr_t)a.w & 15) || (a.estride & 15) || ((uintptr_t)a.x & 3) || (a.xstride & 3) || getenv("FLH_NO_MFMA"))
+        return FLH_ERR_UNSUPPORTED;
+    if (a.nx <= 4) return mf_launch<4>(a, s);
+    if (a.nx <= 8) return mf_launch<8>(a, s);
+    return mf_launch<16>(a, s);
+}
+
+}  // namespace flh

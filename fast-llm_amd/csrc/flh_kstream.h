@@ -108,6 +108,17 @@ __host__ __device__ inline size_t ks_smem_bytes(uint32_t nr, uint32_t nx, uint32
     return (size_t)4 * D * KS<FMT>::WIN + ks_xrec_bytes<FMT>(nx, nsb) + ks_term_bytes<FMT>(nr, nx, nsb) + 256;
 }
 
+// Wait until at most `behind` chunks' DMAs (NI loads each) are outstanding;
+// behind < D is wave-uniform.
+template <int NI, int D>
+__device__ __forceinline__ void ks_wait_behind(uint32_t behind) {
+    if (D > 4 && behind >= 4) { WAIT_VM(NI * (D > 4 ? 4 : 0)); return; }
+    if (D > 3 && behind >= 3) { WAIT_VM(NI * (D > 3 ? 3 : 0)); return; }
+    if (D > 2 && behind >= 2) { WAIT_VM(NI * (D > 2 ? 2 : 0)); return; }
+    if (D > 1 && behind >= 1) { WAIT_VM(NI); return; }
+    WAIT_VM(0);
+}
+
 // Issue the DMA of chunk `ch` (batch-local) into a stage.  Lanes past the
 // chunk's valid bytes re-read the last valid 16 bytes (never out of bounds).
 template <int FMT>
@@ -586,7 +597,7 @@ __device__ __forceinline__ float ks_fold(const int * TI, const int * TM, const u
         const int * tm = TM + (rl * NX + p) * nsb;
         const uint32_t * th = TH + rl * nsb;
         const float * xdp = xd + p * nsb;
-        for (uint32_t sbi = k; sbi < nsb; sbi += 4) {
+        auto step = [&](uint32_t sbi) {
             const float dk = xdp[sbi];
             if constexpr (FMT == FMT_Q4_K) {
                 const float d = h2f(th[sbi] & 0xFFFFu), dmin = h2f(th[sbi] >> 16);
@@ -595,7 +606,14 @@ __device__ __forceinline__ float ks_fold(const int * TI, const int * TM, const u
             } else {
                 acc = fmaf(h2f(th[sbi]) * dk, (float)ti[sbi], acc);
             }
+        };
+        // four steps per iteration so their loads are issued together
+        uint32_t sbi = k;
+        for (; sbi + 12 < nsb; sbi += 16) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) step(sbi + 4 * q);
         }
+        for (; sbi < nsb; sbi += 4) step(sbi);
     }
     const float s01 = acc + qx1f(acc);
     return s01 + qx2f(s01);

@@ -1,0 +1,51 @@
+"""GPU parity of the multi-column Q4_K kernel on the int8 matrix cores
+(flh_dot_mfma.hip, used by STREAM_DOT for 2..16 Q4_K columns).
+
+Bar: bitwise against the oracle (the reference's fl_dot_i8k_q4_K per column,
+src/runtime/quants.h:538-561), at the speculative-verify shapes of the
+benchmark (14336x4096 and 4096x14336, N in {2, 4, 8}) and at shapes that
+exercise partial 16-row tiles, several row batches per workgroup, column
+groups (the 14336-column plan holds 4 columns) and the 16-column maximum.
+"""
+import os
+
+import numpy as np
+import pytest
+
+from oracle import Q4_K
+from util import sane_rows, activations
+from test_gpu_parity import run_dot, bits, say
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("rows,cols,nx", [
+    (14336, 4096, 2), (14336, 4096, 4), (14336, 4096, 8),
+    (4096, 14336, 2), (4096, 14336, 4), (4096, 14336, 8),
+    (20000, 512, 16), (300, 4096, 3), (17, 256, 2), (4100, 2048, 7), (40, 16384, 5),
+])
+def test_mfma_multicol_bitwise(flh, orc, gpu, rows, cols, nx):
+    say("mfma", rows, cols, nx)
+    rng = np.random.default_rng(rows + 7 * cols + nx)
+    w = sane_rows(Q4_K, rows, cols, rng)
+    xs = activations(nx, cols, rng, outliers=True)
+    got, want = run_dot(flh, orc, gpu, Q4_K, w, rows, cols, xs, ystride=rows + 1,
+                        y0=rng.standard_normal((nx - 1) * (rows + 1) + rows).astype(np.float32))
+    assert np.array_equal(bits(got), bits(want))
+
+
+def test_mfma_equals_streaming_kernel(flh, orc, gpu):
+    """Same bits with the matrix-core kernel switched off (streaming kernel)."""
+    say("mfma vs kstream")
+    rng = np.random.default_rng(3)
+    rows, cols, nx = 1000, 4096, 4
+    w = sane_rows(Q4_K, rows, cols, rng)
+    xs = activations(nx, cols, rng)
+    got, want = run_dot(flh, orc, gpu, Q4_K, w, rows, cols, xs)
+    os.environ["FLH_NO_MFMA"] = "1"
+    try:
+        got2, _ = run_dot(flh, orc, gpu, Q4_K, w, rows, cols, xs)
+    finally:
+        del os.environ["FLH_NO_MFMA"]
+    assert np.array_equal(bits(got), bits(want))
+    assert np.array_equal(bits(got2), bits(got))
