@@ -709,7 +709,9 @@ int launch_moe_i8k(int fmt, const MoeArgs & a, hipStream_t s) {
         return set_error(FLH_ERR_UNSUPPORTED, "moe i8k: cols must be a multiple of 256, <= 16384");
     if (a.rows == 0 || a.ntok == 0 || a.top_k == 0) return FLH_OK;
     if (a.ntok * a.top_k > 256) return set_error(FLH_ERR_UNSUPPORTED, "moe: ntok*top_k > 256");
-    const int rc = launch_moe_kstream(fmt, a, s);
+    int rc = launch_moe_mfma(fmt, a, s);
+    if (rc != FLH_ERR_UNSUPPORTED) return rc;
+    rc = launch_moe_kstream(fmt, a, s);
     if (rc != FLH_ERR_UNSUPPORTED) return rc;
     if (fmt == FMT_Q4_K) return launch_moe_t<FMT_Q4_K, 4>(a, s);
     if (fmt == FMT_Q6_K) return launch_moe_t<FMT_Q6_K, 4>(a, s);

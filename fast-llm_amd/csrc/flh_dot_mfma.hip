@@ -356,6 +356,50 @@ __global__ __launch_bounds__(512) void k_dot_mfma(DotArgs a, uint32_t nrb) {
     mf_body<NC, D>(w, a.rows, a.cols, C, a.nx, nrb, blockIdx.x, gridDim.x, sm);
 }
 
+// Grouped expert matvec (MoE): blockIdx.y = expert e.  The workgroup collects
+// the (token, slot) pairs routed to e and streams e's weights once per group
+// of NC pairs (the columns); with no pair routed to e it exits before any
+// weight byte is requested.  Column p's activation index and output index
+// sit in LDS tables read with the lane's own (lane-varying) p.
+struct MfColsMoe {
+    const float * x0;
+    float * y0;
+    uint32_t xs, ys;
+    const uint32_t * xi;                      // __shared__ [NC]
+    const uint32_t * yi;                      // __shared__ [NC]
+    __device__ const float * x(uint32_t p) const { return x0 + (size_t)lds_ld32(&xi[p]) * xs; }
+    __device__ float * y(uint32_t p) const { return y0 + (size_t)lds_ld32(&yi[p]) * ys; }
+};
+
+template <int NC, int D>
+__global__ __launch_bounds__(512) void k_moe_mfma(MoeArgs a, uint32_t nrbp) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t sm[];
+    __shared__ uint32_t pairs[256];
+    __shared__ uint32_t npairs;
+    __shared__ uint32_t cxi[NC], cyi[NC];
+    const uint32_t e = blockIdx.y, tid = threadIdx.x;
+    if (tid == 0) npairs = 0;
+    __syncthreads();
+    // pairs i = tok * top_k + slot routed to e (order free: every column's
+    // output is computed independently)
+    if (tid < a.ntok * a.top_k && a.ids[tid] == e) pairs[atomicAdd(&npairs, 1u)] = tid;
+    __syncthreads();
+    const uint32_t np = npairs;
+    const uint8_t * w = a.w + (size_t)e * a.estride;
+    for (uint32_t p0 = 0; p0 < np; p0 += NC) {
+        const uint32_t nx = min((uint32_t)NC, np - p0);
+        if (tid < NC) {
+            const uint32_t ts = pairs[p0 + (tid < nx ? tid : 0)];
+            cxi[tid] = a.x_per_slot ? ts : ts / a.top_k;
+            cyi[tid] = ts;
+        }
+        __syncthreads();
+        const MfColsMoe C{a.x, a.y, a.xstride, a.ystride, cxi, cyi};
+        mf_body<NC, D>(w, a.rows, a.cols, C, nx, nrbp, blockIdx.x, gridDim.x, sm);
+        __syncthreads();
+    }
+}
+
 // ----------------------------------------------------------------- launch --
 // chunks each wave requests before the activations are staged (the rest of
 // its ring after its first chunk); 0 = the whole ring (measured best here)
@@ -425,6 +469,52 @@ uint32_t mfma_min_cols(uint32_t cols) {
         return e ? atoi(e) : 0;
     }();
     return v ? (uint32_t)v : (cols > 4096 ? 2u : 3u);
+}
+
+uint32_t mfma_min_cols(uint32_t cols);
+
+template <int NC, int D>
+static int mf_moe_launch_d(const MoeArgs & a, uint32_t nrb, uint32_t gx, size_t smb, hipStream_t s) {
+    (void)hipFuncSetAttribute((const void *)k_moe_mfma<NC, D>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smb);
+    hipLaunchKernelGGL((k_moe_mfma<NC, D>), dim3(gx, a.n_expert), dim3(MF_WAVES * 64), smb, s, a,
+                       nrb | (mf_pro() << 16));
+    return hip_check(hipGetLastError(), "k_moe_mfma launch");
+}
+
+template <int NC>
+static int mf_moe_launch(const MoeArgs & a, hipStream_t s) {
+    const uint32_t nsb = a.cols >> 8;
+    // the experts that can be active at once share the CUs (one workgroup each)
+    const uint32_t pairs = a.ntok * a.top_k;
+    const uint32_t active = pairs < a.n_expert ? pairs : a.n_expert;
+    uint32_t gx = ((uint32_t)num_cus() + active - 1) / active;
+    if (gx > a.rows) gx = a.rows;
+    uint32_t nrb;
+    int D;
+    size_t smb;
+    if (mf_plan<NC>(a.rows, nsb, gx, nrb, D, smb)) return FLH_ERR_UNSUPPORTED;
+    switch (D) {
+        case 2: return mf_moe_launch_d<NC, 2>(a, nrb, gx, smb, s);
+        case 3: return mf_moe_launch_d<NC, 3>(a, nrb, gx, smb, s);
+        default: return mf_moe_launch_d<NC, 4>(a, nrb, gx, smb, s);
+    }
+}
+
+// Grouped Q4_K expert matvec on the matrix cores for token batches of at
+// least mfma_min_cols(cols) tokens; FLH_ERR_UNSUPPORTED (nothing launched)
+// otherwise or when the shape does not fit.
+int launch_moe_mfma(int fmt, const MoeArgs & a, hipStream_t s) {
+    const uint32_t nsb = a.cols >> 8;
+    if (fmt != FMT_Q4_K || nsb == 0 || (a.cols & 255) || nsb > 64 || a.ntok < mfma_min_cols(a.cols))
+        return FLH_ERR_UNSUPPORTED;
+    if (((uintptr_t)a.w & 15) || (a.estride & 15) || ((uintptr_t)a.x & 3) || (a.xstride & 3) || getenv("FLH_NO_MFMA") ||
+        a.ntok * a.top_k > 256)
+        return FLH_ERR_UNSUPPORTED;
+    // an expert gets at most one pair per token
+    int rc = FLH_ERR_UNSUPPORTED;
+    if (a.ntok > 4) rc = mf_moe_launch<8>(a, s);
+    if (rc == FLH_ERR_UNSUPPORTED) rc = mf_moe_launch<4>(a, s);
+    return rc;
 }
 
 // Q4_K x q8_K with 1..16 columns; FLH_ERR_UNSUPPORTED (nothing launched) when

@@ -50,6 +50,8 @@ int launch_act_dot_kstream(int fmt, const DotArgs & a, hipStream_t s);
 // Q4_K x q8_K, 1..16 columns, on the int8 matrix cores (flh_dot_mfma.hip);
 // FLH_ERR_UNSUPPORTED (nothing launched) if the shape does not fit its plan
 int launch_dot_mfma(int fmt, const DotArgs & a, hipStream_t s);
+// grouped expert variant (MoE, Q4_K, batches of several tokens)
+int launch_moe_mfma(int fmt, const MoeArgs & a, hipStream_t s);
 // fewest columns for which STREAM_DOT uses launch_dot_mfma
 uint32_t mfma_min_cols(uint32_t cols);
 int launch_dot_i8_q8_0(const DotArgs & a, hipStream_t s);         // Q8_0 x q8_1

@@ -35,7 +35,8 @@ def route(orc, ntok, E, K, rng):
 @pytest.mark.parametrize("fmt", [Q4_K, Q6_K])
 @pytest.mark.parametrize("ntok,rows,cols,per_slot", [(1, 300, 1024, False), (3, 64, 2816, False),
                                                      (8, 257, 4096, False), (8, 96, 2048, True),
-                                                     (5, 40, 14336, True)])
+                                                     (5, 40, 14336, True), (16, 1024, 4096, False),
+                                                     (8, 4096, 14336, True)])
 def test_grouped_expert_dot_bitwise(flh, orc, gpu, fmt, ntok, rows, cols, per_slot):
     say("moe_dot", fmt, ntok, rows, cols, per_slot)
     rng = np.random.default_rng(ntok * 31 + rows + cols + fmt)
