@@ -179,6 +179,7 @@ _SIGS = {
                          _U32, _P]),
     "flh_router_sel": (_I, [_P, _U32, _U32, _U32, _U32, _F, _P, _P, _P]),
     "flh_silu_mul": (_I, [_P, _P, _P, _U32, _U32, _U32, _U32, _P]),
+    "flh_silu_mul_act_q8": (_I, [_P, _P, _P, _U32, _U32, _U32, _U32, _P]),
     "flh_wmerge": (_I, [_P, _P, _P, _P, _P, _F, _U32, _U32, _U32, _U32, _U32, _U32, _P]),
     "flh_fill_normal": (_I, [_P, _SZ, _U64, _F, _F, _F, _F, _P]),
     "flh_quantize": (_I, [_I, _P, _U32, _U32, _P, _P]),
@@ -419,6 +420,11 @@ def router_sel(logits, ntok, n_expert, top_k, norm, scale, ids, gates, stream: S
 
 def silu_mul(gate, up, h, n, ncol, gstride, hstride, stream: Stream):
     check(lib().flh_silu_mul(_p(gate), _p(up), _p(h), n, ncol, gstride, hstride, stream.handle))
+
+
+def silu_mul_act_q8(gate, up, h, n, ncol, gstride, hstride, stream: Stream):
+    """SILU_MUL then ACT_Q8 of every h column (one launch, same bytes)."""
+    check(lib().flh_silu_mul_act_q8(_p(gate), _p(up), _p(h), n, ncol, gstride, hstride, stream.handle))
 
 
 def wmerge(parts, gates, add1, add2, y, scale, n_parts, n, n_full, ncol, pstride, ystride,

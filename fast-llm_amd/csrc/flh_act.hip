@@ -29,6 +29,37 @@ __global__ __launch_bounds__(64) void k_act_q8(float * x, uint8_t * yq, uint32_t
     act_q8_lanes(v, lane, chunk, q81, q8k, cols);
 }
 
+// SILU_MUL fused with the ACT_Q8 of its output (the MoE / FFN down input):
+// lane i of the wave for chunk `chunk` of column c computes h = silu(g) * u
+// for elements 4i..4i+3 with k_silu_mul's expression, stores h, and quantises
+// the same register values -- the bytes of k_silu_mul followed by k_act_q8.
+__global__ __launch_bounds__(64) void k_silu_act_q8(const float * gate, const float * up, float * h, uint32_t n,
+                                                    uint32_t gstride, uint32_t hstride) {
+    const uint32_t lane = threadIdx.x, chunk = blockIdx.x, col = blockIdx.y;
+    const float * gc = gate + (size_t)col * gstride;
+    const float * uc = up + (size_t)col * gstride;
+    float * hc = h + (size_t)col * hstride;
+    const uint32_t e0 = chunk * 256 + lane * 4;
+    float v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        v[j] = 0.f;
+        if (e0 + j < n) {
+            const float g = gc[e0 + j];
+            v[j] = (g / (1.0f + expf(-g))) * uc[e0 + j];
+            hc[e0 + j] = v[j];
+        }
+    }
+    act_q8_lanes(v, lane, chunk, (uint8_t *)hc + xq_off(n), (uint8_t *)hc + xqk_off(n), n);
+}
+
+int launch_silu_act_q8(const float * gate, const float * up, float * h, uint32_t n, uint32_t ncol,
+                       uint32_t gstride, uint32_t hstride, hipStream_t s) {
+    if (n == 0 || ncol == 0) return FLH_OK;
+    hipLaunchKernelGGL(k_silu_act_q8, dim3((n + 255) / 256, ncol), dim3(64), 0, s, gate, up, h, n, gstride, hstride);
+    return hip_check(hipGetLastError(), "k_silu_act_q8 launch");
+}
+
 int launch_act_q8(float * x, void * y_q81, uint32_t cols, uint32_t nx,
                   uint32_t xstride, hipStream_t s) {
     if (cols == 0 || nx == 0) return FLH_OK;

@@ -378,6 +378,15 @@ int flh_exec_tasks(const flh_task * t, uint32_t n, int fast, uint32_t i8_mask, u
             }
             case FLH_TASK_SILU_MUL: {
                 const flh_silu_mul_p & p = *(const flh_silu_mul_p *)k.aux;
+                // SILU_MUL followed by the ACT_Q8 of its output (the
+                // decoder's down-projection input): one fused launch
+                const flh_task * q = i + 1 < n ? &t[i + 1] : nullptr;
+                if (q && q->kind == FLH_TASK_ACT_Q8 && q->x == (void *)p.h && q->cols == p.n &&
+                    (const uint8_t *)q->y == (const uint8_t *)p.h + xq_off(p.n) && !((uintptr_t)p.h & 15)) {
+                    rc = launch_silu_act_q8(p.gate, p.up, p.h, p.n, 1, 0, 0, s);
+                    ++i;
+                    break;
+                }
                 rc = launch_silu_mul(p.gate, p.up, p.h, p.n, 1, 0, 0, s);
                 break;
             }
@@ -419,6 +428,13 @@ int flh_silu_mul(const float * gate, const float * up, float * h, uint32_t n, ui
                  uint32_t gstride, uint32_t hstride, void * stream) {
     if (int rc = need_init()) return rc;
     return launch_silu_mul(gate, up, h, n, ncol, gstride, hstride, (hipStream_t)stream);
+}
+int flh_silu_mul_act_q8(const float * gate, const float * up, float * h, uint32_t n, uint32_t ncol,
+                        uint32_t gstride, uint32_t hstride, void * stream) {
+    if (int rc = need_init()) return rc;
+    if (!gate || !up || !h || ((uintptr_t)h & 15) || (ncol > 1 && (hstride & 3)))
+        return set_error(FLH_ERR_ARG, "silu_mul_act_q8: h must be 16-byte aligned, hstride a multiple of 4");
+    return launch_silu_act_q8(gate, up, h, n, ncol, gstride, hstride, (hipStream_t)stream);
 }
 int flh_wmerge(const float * parts, const float * gates, const float * add1, const float * add2, float * y,
                float scale, uint32_t n_parts, uint32_t n, uint32_t n_full, uint32_t ncol, uint32_t pstride,

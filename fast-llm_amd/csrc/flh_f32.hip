@@ -349,6 +349,54 @@ __global__ void k_router_sel(const float * logits, uint32_t ntok, uint32_t n_exp
     }
 }
 
+// One wave per token (n_expert <= 64): lane i owns logit i; the same float
+// operations in the same order as k_router_sel / fl_op_router_sel (max; expf;
+// sum in ascending expert order; divide; top-k by first maximum; optional
+// renormalisation by the sum of the chosen weights; scale), without the
+// per-thread stack array.
+__global__ __launch_bounds__(64) void k_router_wave(const float * logits, uint32_t n_expert, uint32_t top_k,
+                                                    uint32_t norm, float scale, uint32_t * ids, float * gates) {
+    const uint32_t t = blockIdx.x, lane = threadIdx.x;
+    const float * lg = logits + (size_t)t * n_expert;
+    const float l = lane < n_expert ? lg[lane] : 0.f;
+    // max in ascending order (as the scalar loop: first strictly greater value wins)
+    float mx = -1e30f;
+    for (uint32_t i = 0; i < n_expert; ++i) {
+        const float li = __shfl(l, (int)i);
+        if (li > mx) mx = li;
+    }
+    float w = lane < n_expert ? expf(l - mx) : 0.f;
+    float sum = 0.f;
+    for (uint32_t i = 0; i < n_expert; ++i) sum += __shfl(w, (int)i);
+    w /= sum;
+    bool taken = lane >= n_expert;
+    float tsum = 0.f;
+    uint32_t id_k[8];
+    float gt_k[8];
+    for (uint32_t k = 0; k < top_k; ++k) {
+        // first lane holding the largest untaken weight (strict >, ascending)
+        float bw = -1.f;
+        uint32_t best = 0;
+        for (uint32_t i = 0; i < n_expert; ++i) {
+            const float wi = __shfl(w, (int)i);
+            const bool ti = __shfl((int)taken, (int)i) != 0;
+            if (!ti && wi > bw) { bw = wi; best = i; }
+        }
+        if (lane == best) taken = true;
+        if (k < 8) { id_k[k] = best; gt_k[k] = bw; }
+        tsum += bw;
+    }
+    if (lane == 0) {
+        for (uint32_t k = 0; k < top_k && k < 8; ++k) {
+            float g = gt_k[k];
+            if (norm) g /= tsum;
+            g *= scale;
+            ids[(size_t)t * top_k + k] = id_k[k];
+            gates[(size_t)t * top_k + k] = g;
+        }
+    }
+}
+
 __global__ void k_silu_mul(const float * gate, const float * up, float * h, uint32_t n,
                            uint32_t gstride, uint32_t hstride) {
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x, c = blockIdx.y;
@@ -393,6 +441,11 @@ int launch_router_sel(const float * logits, uint32_t ntok, uint32_t n_expert, ui
     if (n_expert == 0 || n_expert > 256 || top_k == 0 || top_k > n_expert)
         return set_error(FLH_ERR_ARG, "router_sel: need 0 < top_k <= n_expert <= 256");
     if (ntok == 0) return FLH_OK;
+    if (n_expert <= 64 && top_k <= 8) {
+        hipLaunchKernelGGL(k_router_wave, dim3(ntok), dim3(64), 0, s, logits, n_expert, top_k, norm, scale, ids,
+                           gates);
+        return hip_check(hipGetLastError(), "k_router_wave launch");
+    }
     hipLaunchKernelGGL(k_router_sel, dim3((ntok + 63) / 64), dim3(64), 0, s, logits, ntok,
                        n_expert, top_k, norm, scale, ids, gates);
     return hip_check(hipGetLastError(), "k_router_sel launch");

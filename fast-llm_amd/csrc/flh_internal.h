@@ -39,6 +39,9 @@ int num_cus();
 // Each returns hipSuccess-style 0 or a negative flh error code.
 int launch_act_q8(float * x, void * y_q81, uint32_t cols, uint32_t nx,
                   uint32_t xstride, hipStream_t s);
+// SILU_MUL over ncol columns followed by ACT_Q8 of h, in one launch
+int launch_silu_act_q8(const float * gate, const float * up, float * h, uint32_t n, uint32_t ncol,
+                       uint32_t gstride, uint32_t hstride, hipStream_t s);
 int launch_dot_i8k(int fmt, const DotArgs & a, hipStream_t s);    // Q4_K, Q6_K x q8_K
 // LDS-staged variant; FLH_ERR_UNSUPPORTED (nothing launched) if the shape
 // does not fit its plan

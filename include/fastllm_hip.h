@@ -244,6 +244,14 @@ int flh_router_sel(const float * logits, uint32_t ntok, uint32_t n_expert,
  * h[c*hstride + i] = silu(g[c*gstride + i]) * u[c*gstride + i]. */
 int flh_silu_mul(const float * gate, const float * up, float * h, uint32_t n,
                  uint32_t ncol, uint32_t gstride, uint32_t hstride, void * stream);
+/* SILU_MUL over ncol columns followed by ACT_Q8 of each h column, in one
+ * launch: h holds ACT_Q8 buffers (fp32 h, then its q8_1 and q8_K appendices,
+ * columns hstride floats apart, 16-byte aligned); the bytes written equal
+ * flh_silu_mul followed by flh_act_q8 (fl_op_silu_mul then fl_exec_act_q8,
+ * decode_params.h:267-272, quants.h:404-416; the decoder's down-projection
+ * input, decoder.cpp:874-880).  flh_exec_tasks fuses such a task pair itself. */
+int flh_silu_mul_act_q8(const float * gate, const float * up, float * h, uint32_t n,
+                        uint32_t ncol, uint32_t gstride, uint32_t hstride, void * stream);
 /* WMERGE over ncol columns (fl_op_wmerge, decode_params.h:274-295): column c
  * reads parts + c*pstride ([n_parts][n]), gates + c*n_parts, add1/add2 +
  * c*ystride, writes y + c*ystride. */

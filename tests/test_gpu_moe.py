@@ -169,3 +169,47 @@ def test_moe_ffn_layer_end_to_end(flh, orc, gpu, ntok):
         want[t] = orc.wmerge(parts, gates_ref[t], add1=resid[t])
     err = np.max(np.abs(got - want))
     assert err <= 1e-3 * np.max(np.abs(want)), err
+
+
+@pytest.mark.parametrize("n,ncol", [(14336, 3), (1000, 2), (256, 1)])
+def test_silu_mul_act_q8_fused_equals_separate(flh, gpu, n, ncol):
+    """The fused SILU_MUL+ACT_Q8 launch writes the bytes of SILU_MUL followed
+    by ACT_Q8 (h and both appendices of every column)."""
+    say("silu+act_q8", n, ncol)
+    from oracle import col_stride_floats, x_alloc_bytes
+    rng = np.random.default_rng(n + ncol)
+    gs = 2 * n + 5
+    gu = (rng.standard_normal(ncol * gs) * 3).astype(np.float32)
+    st = col_stride_floats(n)
+    dgu = flh.DeviceBuffer.from_array(gu, gpu)
+    h1 = flh.DeviceBuffer.from_array(np.zeros(ncol * st, np.float32), gpu)
+    h2 = flh.DeviceBuffer.from_array(np.zeros(ncol * st, np.float32), gpu)
+    flh.silu_mul(dgu, dgu.ptr + 4 * n, h1, n, ncol, gs, st, gpu)
+    flh.act_q8(h1, n, gpu, nx=ncol, xstride=st)
+    flh.silu_mul_act_q8(dgu, dgu.ptr + 4 * n, h2, n, ncol, gs, st, gpu)
+    a = h1.download(np.float32, ncol * st, gpu).view(np.uint8)
+    b = h2.download(np.float32, ncol * st, gpu).view(np.uint8)
+    for c in range(ncol):
+        lo = c * st * 4
+        assert np.array_equal(a[lo:lo + x_alloc_bytes(n)], b[lo:lo + x_alloc_bytes(n)]), f"column {c}"
+
+
+@pytest.mark.parametrize("E,K,norm", [(8, 2, 1), (64, 6, 0), (16, 4, 1), (100, 8, 1)])
+def test_router_ties_and_widths(flh, orc, gpu, E, K, norm):
+    """Equal weights resolve to the lower expert id (strict > in expert order,
+    decode_params.h:234-265); one-wave router (E <= 64) and per-thread router
+    (E > 64) both."""
+    say("router ties", E, K, norm)
+    rng = np.random.default_rng(E * 7 + K)
+    ntok = 5
+    lg = rng.integers(-3, 4, size=(ntok, E)).astype(np.float32) * 0.5   # many exact ties
+    d_l = flh.DeviceBuffer.from_array(lg.ravel(), gpu)
+    d_i = flh.DeviceBuffer(ntok * K * 4)
+    d_g = flh.DeviceBuffer(ntok * K * 4)
+    flh.router_sel(d_l, ntok, E, K, norm, 1.0, d_i, d_g, gpu)
+    ids = d_i.download(np.uint32, ntok * K, gpu).reshape(ntok, K)
+    g = d_g.download(np.float32, ntok * K, gpu).reshape(ntok, K)
+    for t in range(ntok):
+        wi, wg = orc.router_sel(lg[t], K, norm=norm)
+        assert list(ids[t]) == list(wi)
+        assert np.allclose(g[t], wg, rtol=2e-6, atol=0)
