@@ -116,9 +116,11 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-ops", action="store_true", help="headline only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--profile", action="store_true",
+    ap.add_argument("--profile", nargs="?", const="gate_up", choices=["gate_up", "verify8"],
                     help="counter-collection run: a 256 MiB device copy (calibration) and "
-                         "64 launches of the dominant kernel only, no JSON line")
+                         "64 launches of one kernel only (gate_up: the dominant Q4_K "
+                         "28672x4096 N=1 matvec; verify8: Q4_K 14336x4096 with 8 columns on "
+                         "the matrix-core kernel), no JSON line")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the matvec shards by rows; "
@@ -134,7 +136,7 @@ def main():
     staging = B.buf(256 << 20)
 
     if args.profile:
-        profile_run(flh, B, s, staging)
+        profile_run(flh, B, s, staging, args.profile)
         return
 
     # ------------------------------------------------ headline: layer step
@@ -268,23 +270,25 @@ def main():
     print(json.dumps(result), flush=True)
 
 
-def profile_run(flh, B, s, staging):
+def profile_run(flh, B, s, staging, which="gate_up"):
     """What the committed counter profiles were collected on: 5 device copies
     of 256 MiB (known HBM bytes: read 256 MiB + write 256 MiB each) and 64
-    launches of the Q4_K gate/up matvec rotating over its weight copies."""
+    launches of one matvec rotating over its weight copies: the Q4_K gate/up
+    28672x4096 at N=1 (gate_up) or the Q4_K 14336x4096 verify matvec with 8
+    activation columns (verify8)."""
     n = 256 << 20
     src, dst = B.buf(n), B.buf(n)
     src.zero(s)
     for _ in range(5):
         flh.copy(dst, src, n, s)
     s.sync()
-    r, c = 28672, 4096
+    r, c, nx = (28672, 4096, 1) if which == "gate_up" else (14336, 4096, 8)
     nb = r * flh.row_bytes(Q4_K, c)
     ws = B.weights(Q4_K, r, c, copies_for(nb), seed=101 + r + 7 * c, staging=staging)
-    x, st = B.activation(c, 1, 12, outliers=True)
-    y = B.buf(r * 4)
+    x, st = B.activation(c, nx, 12, outliers=True)
+    y = B.buf(nx * r * 4)
     for i in range(64):
-        flh.stream_dot(Q4_K, ws[i % len(ws)], r, c, x, y, s)
+        flh.stream_dot(Q4_K, ws[i % len(ws)], r, c, x, y, s, nx=nx, xstride=st, ystride=r)
     s.sync()
 
 
