@@ -38,6 +38,16 @@ def route(orc, ntok, E, K, rng):
                                                      (5, 40, 14336, True), (16, 1024, 4096, False),
                                                      (8, 4096, 14336, True)])
 def test_grouped_expert_dot_bitwise(flh, orc, gpu, fmt, ntok, rows, cols, per_slot):
+    grouped_dot_case(flh, orc, gpu, fmt, ntok, rows, cols, per_slot)
+
+
+def test_grouped_expert_dot_mixtral_gate_up_batch8(flh, orc, gpu):
+    """The benchmark's MoE shape: 8 experts of 28672x4096 Q4_K (fused gate/up),
+    8 tokens routed top-2 (matrix-core grouped kernel), bitwise."""
+    grouped_dot_case(flh, orc, gpu, Q4_K, 8, 28672, 4096, False)
+
+
+def grouped_dot_case(flh, orc, gpu, fmt, ntok, rows, cols, per_slot):
     say("moe_dot", fmt, ntok, rows, cols, per_slot)
     rng = np.random.default_rng(ntok * 31 + rows + cols + fmt)
     E, K = 8, 2
@@ -67,7 +77,7 @@ def test_grouped_expert_dot_bitwise(flh, orc, gpu, fmt, ntok, rows, cols, per_sl
             xi = i if per_slot else t
             yi = want[i * rows:(i + 1) * rows]
             orc.stream_dot(fmt, w, rows, cols, ref_x[xi * st:(xi + 1) * st], yi,
-                           id_slot=int(ids[t, k]), estride=estride)
+                           id_slot=int(ids[t, k]), estride=estride, threads=8)
             want[i * rows:(i + 1) * rows] = yi
     assert np.array_equal(bits(got), bits(want))
 
