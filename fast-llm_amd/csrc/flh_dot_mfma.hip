@@ -56,15 +56,29 @@ constexpr uint32_t MF_WAVES = 8;
 constexpr uint32_t MF_CHUNK = 2304;          // 16 rows x one Q4_K superblock
 constexpr int MF_NI = 3;                     // DMA instructions per chunk
 
-// LDS: [waves][D][2304] ring | xr [NC][XS] raw q8_K appendices | TI, TM [nrb][NC][nsb]
-//      | TH [nrb][nsb] | ysm [nrb * NC]
+// LDS: [waves][D][2304] ring | xr [NC][XS] raw q8_K appendices | TI, TM [nrb][NC][nl]
+//      | TH [nrb][nl] | ysm [nrb * NC] | (K halves) yph [nrb * NC], dkt [NC][nsb]
 // XS: a column's appendix (292 bytes per superblock) padded so that XS / 4 is
 // 8 mod 32 (the 16 columns' reads of one k-slice fall in distinct banks).
+//
+// K halves (KH): when NC columns of nsb superblocks do not fit, the superblocks
+// split by sb % 4 into half 0 ({0, 1}) and half 1 ({2, 3}); a batch streams
+// one half, folds accumulators 0-1 (resp. 2-3) of the reference's four, stages
+// the other half's activations and streams that.  nl = superblocks held at once.
 __host__ __device__ inline uint32_t mf_xs(uint32_t nsb) { return ((nsb * 292 + 127) & ~127u) + 32; }
-template <int NC>
+// K halves: pairs of superblocks at 592-byte pitch
+__host__ __device__ inline uint32_t mf_xs_h(uint32_t nl) { return ((((nl + 1) >> 1) * 592 + 127) & ~127u) + 32; }
+__host__ __device__ inline uint32_t mf_nsbh(uint32_t nsb, uint32_t h) {
+    const uint32_t r = nsb & 3;
+    return (nsb >> 2) * 2 + (h == 0 ? (r < 2 ? r : 2u) : (r > 2 ? r - 2 : 0u));
+}
+// superblock of local index li of half h
+__device__ __forceinline__ uint32_t mf_sbh(uint32_t li, uint32_t h) { return 4 * (li >> 1) + 2 * h + (li & 1); }
+template <int NC, bool KH>
 __host__ __device__ inline size_t mf_smem_bytes(uint32_t nrb, uint32_t nsb, int D) {
-    return (size_t)MF_WAVES * D * MF_CHUNK + (size_t)NC * mf_xs(nsb) + (size_t)nrb * NC * nsb * 8 +
-           (size_t)nrb * nsb * 4 + (size_t)nrb * NC * 4;
+    const uint32_t nl = KH ? mf_nsbh(nsb, 0) : nsb;
+    return (size_t)MF_WAVES * D * MF_CHUNK + (size_t)NC * (KH ? mf_xs_h(nl) : mf_xs(nl)) + (size_t)nrb * NC * nl * 8 +
+           (size_t)nrb * nl * 4 + (size_t)nrb * NC * 4 + (KH ? (size_t)nrb * NC * 4 + (size_t)NC * nsb * 4 : 0);
 }
 
 // Column sources of one pass: activation column p at x(p) (fp32 x followed by
@@ -141,11 +155,50 @@ __device__ __forceinline__ float mf_fold(const int * TI, const int * TM, const u
     return s01 + qx2f(s01);
 }
 
+// K halves: fold of half h (local superblocks li, terms [li][row][column]):
+// lane k < 2 runs accumulator 2h + k over li = k, k + 2, ... (superblocks in
+// increasing order); returns a_{2h} + a_{2h+1} in lane 0 of the quad.  The
+// q8_K scales come from dkt [column][sb].
+template <int NC>
+__device__ __forceinline__ float mf_fold_h(const int * TI, const int * TM, const uint32_t * TH, const float * dkt,
+                                           uint32_t nl, uint32_t nsb, uint32_t h, uint32_t nrb, uint32_t k,
+                                           uint32_t p, uint32_t rl, bool fok) {
+    float acc = 0.f;
+    if (fok && k < 2) {
+        auto step = [&](int ti, int tm, uint32_t th, float dk) {
+            const float d = h2f(th & 0xFFFFu), dmin = h2f(th >> 16);
+            acc = fmaf(d * dk, (float)ti, acc);
+            acc = fmaf(-(dmin * dk), (float)tm, acc);
+        };
+        uint32_t li = k;
+        for (; li + 6 < nl; li += 8) {
+            int ti[4], tm[4];
+            uint32_t th[4];
+            float dk[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint32_t lq = li + 2 * q;
+                ti[q] = TI[((size_t)lq * nrb + rl) * NC + p];
+                tm[q] = TM[((size_t)lq * nrb + rl) * NC + p];
+                th[q] = TH[(size_t)lq * nrb + rl];
+                dk[q] = dkt[p * nsb + mf_sbh(lq, h)];
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) step(ti[q], tm[q], th[q], dk[q]);
+        }
+        for (; li < nl; li += 2)
+            step(TI[((size_t)li * nrb + rl) * NC + p], TM[((size_t)li * nrb + rl) * NC + p], TH[(size_t)li * nrb + rl],
+                 dkt[p * nsb + mf_sbh(li, h)]);
+    }
+    return acc + qx1f(acc);
+}
+
 // One pass over the rows [rows*g/G, rows*(g+1)/G) for nx <= NC columns, in
 // batches of nrb rows (a multiple of 16).  A chunk is superblock sb of a
 // 16-row tile of the batch; the batch's chunks q = (tile, sb), tile-major, are
-// dealt to the waves round-robin.
-template <int NC, int D, typename COLS>
+// dealt to the waves round-robin (with K halves: per half, the first half of
+// batch bt being half bt & 1, whose activations are staged already).
+template <int NC, int D, bool KH, typename COLS>
 __device__ __forceinline__ void mf_body(const uint8_t * __restrict__ w, uint32_t rows, uint32_t cols,
                                         const COLS & C, uint32_t nx, uint32_t nrbp, uint32_t g, uint32_t G,
                                         uint8_t * sm) {
@@ -157,14 +210,20 @@ __device__ __forceinline__ void mf_body(const uint8_t * __restrict__ w, uint32_t
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t r = lane & 15, j = lane >> 4;
-
+    constexpr uint32_t NPH = KH ? 2 : 1;                          // phases (halves) per batch
+    auto half_of = [&](uint32_t bt, uint32_t ph) -> uint32_t { return KH ? ((bt & 1) ^ ph) : 0u; };
+    auto nl_of = [&](uint32_t h) -> uint32_t { return KH ? mf_nsbh(nsb, h) : nsb; };
+    auto sb_of = [&](uint32_t li, uint32_t h) -> uint32_t { return KH ? mf_sbh(li, h) : li; };
+    const uint32_t NL = nl_of(0);                                 // superblocks held at once
     uint8_t * myst = sm + (size_t)wave * D * MF_CHUNK;
-    const uint32_t XS = mf_xs(nsb);
+    const uint32_t XS = KH ? mf_xs_h(NL) : mf_xs(NL);
     uint8_t * xr = sm + (size_t)MF_WAVES * D * MF_CHUNK;
     int * TI = (int *)(xr + (size_t)NC * XS);
-    int * TM = TI + (size_t)nrb * NC * nsb;
-    uint32_t * TH = (uint32_t *)(TM + (size_t)nrb * NC * nsb);
-    float * ysm = (float *)(TH + (size_t)nrb * nsb);
+    int * TM = TI + (size_t)nrb * NC * NL;
+    uint32_t * TH = (uint32_t *)(TM + (size_t)nrb * NC * NL);
+    float * ysm = (float *)(TH + (size_t)nrb * NL);
+    float * yph = ysm + (size_t)nrb * NC;                         // KH: first half's sums
+    float * dkt = yph + (size_t)nrb * NC;                         // KH: q8_K scales [NC][nsb]
 
     MF_STAMP(0);
     const uint32_t rbeg = (uint32_t)((uint64_t)rows * g / G);
@@ -173,11 +232,51 @@ __device__ __forceinline__ void mf_body(const uint8_t * __restrict__ w, uint32_t
     auto nrow_of = [&](uint32_t bt) -> uint32_t { return min(nrb, rend - rbeg - bt * nrb); };
 
     // ---- activations -> LDS by DMA, issued first (older than every weight
-    // DMA, so the wait before the first chunk covers them): each column's
-    // q8_K appendix copied as is, 1 KiB per instruction, the last 0-12 bytes
-    // by a dword instruction.  Columns past nx copy column 0 (their results
-    // are never stored).
-    {
+    // DMA, so the wait before the first chunk covers them).  Whole: each
+    // column's q8_K appendix copied as is, 1 KiB per instruction, the last
+    // 0-12 bytes by a dword instruction.  K halves: the half's pairs of 292-byte
+    // blocks at a 592-byte pitch, 1 KiB per instruction, plus every
+    // superblock's scale into dkt.  Columns past nx copy column 0 (their results are never
+    // stored).
+    auto stage_half = [&](uint32_t h) {
+        // pairs (sb, sb + 1) of the half are contiguous in the appendix (584
+        // bytes): pair m -> LDS bytes 592 m, as 37 16-byte pieces (the last
+        // 8 bytes belong to the other half and are never read); pieces that
+        // would pass the appendix's end are copied by dword loads.
+        const uint32_t np = (nl_of(h) + 1) >> 1, npc = np * 37, nin = (npc + 63) >> 6;
+        const uint32_t aend = nsb * 292;
+        const uint32_t per = nin + 1;
+        for (uint32_t i = wave; i < NC * per; i += MF_WAVES) {
+            const uint32_t n = i / per, k = i % per;
+            const uint8_t * src = (const uint8_t *)C.x(n < nx ? n : 0) + xqk_off(cols);
+            uint8_t * dst = xr + (size_t)n * XS;
+            if (k < nin) {
+                const uint32_t pc = 64 * k + lane, m = pc / 37, o = pc - m * 37;
+                const uint32_t go = 1168 * m + 584 * h + 16 * o;
+                if (pc < npc && go + 16 <= aend)
+                    __builtin_amdgcn_global_load_lds(GPTR(src + go), LPTR(dst + 1024 * k), 16, 0, 0);
+            } else {
+                // the piece of the last pair that straddles the appendix's end
+                const uint32_t bl = 1168 * (np - 1) + 584 * h, rem = aend - bl;
+                if (aend > bl && rem < 592 && lane < ((rem & 15) >> 2)) {
+                    const uint32_t o = rem >> 4;
+                    __builtin_amdgcn_global_load_lds(GPTR(src + bl + 16 * o + 4 * lane),
+                                                     LPTR(dst + 16 * ((np - 1) * 37 + o)), 4, 0, 0);
+                }
+            }
+        }
+    };
+    if constexpr (KH) {
+        stage_half(0);
+        for (uint32_t i = wave; i < (NC * nsb + 63) / 64; i += MF_WAVES) {
+            const uint32_t e = 64 * i + lane;
+            if (e < NC * nsb) {
+                const uint32_t n = e / nsb, sb = e - n * nsb;
+                const uint8_t * src = (const uint8_t *)C.x(n < nx ? n : 0) + xqk_off(cols) + (size_t)sb * 292;
+                __builtin_amdgcn_global_load_lds(GPTR(src), LPTR(dkt + 64 * i), 4, 0, 0);
+            }
+        }
+    } else {
         const uint32_t L = nsb * 292, n16 = L >> 4, nti = (n16 + 63) >> 6;   // x4 instructions per column
         const uint32_t tail = (L & 15) >> 2;                                  // trailing dwords
         const uint32_t per = nti + (tail ? 1u : 0u);
@@ -198,22 +297,28 @@ __device__ __forceinline__ void mf_body(const uint8_t * __restrict__ w, uint32_t
     // chunk is row p / 9, bytes 16 (p % 9) of its superblock.
     const uint32_t pr0 = lane / 9, pr1 = (64 + lane) / 9, pr2 = (128 + (lane >> 2)) / 9;
     const uint32_t po0 = (lane % 9) * 16, po1 = ((64 + lane) % 9) * 16, po2 = ((128 + (lane >> 2)) % 9) * 16 + 4 * (lane & 3);
-    // issue cursor: batch qbt, tile qt, superblock qsb (q = wave + 8 i, tile-major)
-    uint32_t qbt = 0, qt = 0, qsb = wave, qnt = nbatch ? (nrow_of(0) + 15) >> 4 : 0;
-    while (qsb >= nsb) { qsb -= nsb; ++qt; }
+    // issue cursor: batch qbt, phase qph, tile qt, local superblock qsb
+    // (q = wave + 8 i over the phase's chunks, tile-major)
+    uint32_t qbt = 0, qph = 0, qt = 0, qsb = wave, qnl = nl_of(half_of(0, 0));
+    uint32_t qnt = nbatch ? (nrow_of(0) + 15) >> 4 : 0;
+    while (qsb >= qnl) { qsb -= qnl; ++qt; }
     uint32_t nissued = 0, ncons = 0;
     auto issue_one = [&]() {
         while (qbt < nbatch && qt >= qnt) {
-            ++qbt;
+            if (++qph == NPH) {
+                qph = 0;
+                ++qbt;
+                qnt = qbt < nbatch ? (nrow_of(qbt) + 15) >> 4 : 0;
+            }
             qt = 0;
             qsb = wave;
-            while (qsb >= nsb) { qsb -= nsb; ++qt; }
-            qnt = qbt < nbatch ? (nrow_of(qbt) + 15) >> 4 : 0;
+            qnl = nl_of(half_of(qbt, qph));
+            while (qsb >= qnl) { qsb -= qnl; ++qt; }
         }
         if (qbt < nbatch) {
             const uint32_t tr0 = rbeg + qbt * nrb + 16 * qt;
             const uint32_t nv1 = min(16u, rend - tr0) - 1;           // last valid row of the tile
-            const uint8_t * base = w + (size_t)tr0 * rb + (size_t)qsb * 144;
+            const uint8_t * base = w + (size_t)tr0 * rb + (size_t)sb_of(qsb, half_of(qbt, qph)) * 144;
             uint8_t * stage = myst + (nissued % D) * MF_CHUNK;
             __builtin_amdgcn_global_load_lds(GPTR(base + (size_t)min(pr0, nv1) * rb + po0), LPTR(stage), 16, 0, FLH_MF_AUX);
             __builtin_amdgcn_global_load_lds(GPTR(base + (size_t)min(pr1, nv1) * rb + po1), LPTR(stage + 1024), 16, 0,
@@ -222,7 +327,7 @@ __device__ __forceinline__ void mf_body(const uint8_t * __restrict__ w, uint32_t
                                              FLH_MF_AUX);
             ++nissued;
             qsb += MF_WAVES;
-            while (qsb >= nsb) { qsb -= nsb; ++qt; }
+            while (qsb >= qnl) { qsb -= qnl; ++qt; }
         }
     };
     // old y of a batch -> LDS (one 64-float DMA per wave; nrb * NC <= 512)
@@ -256,91 +361,117 @@ __device__ __forceinline__ void mf_body(const uint8_t * __restrict__ w, uint32_t
         const uint32_t nrow = nrow_of(bt);
         const uint32_t nt = (nrow + 15) >> 4;
         if (bt != 0) issue_y(bt);
-        uint32_t ct = 0, csb = wave;                               // consume cursor
-        while (csb >= nsb) { csb -= nsb; ++ct; }
-        for (; ct < nt;) {
-            ks_wait_behind<MF_NI, D>(nissued - 1 - ncons);
-            ++ncons;
-            if (ncons == 1) MF_STAMP(2);
-            const uint32_t t = ct, sb = csb;
-            csb += MF_WAVES;
-            while (csb >= nsb) { csb -= nsb; ++ct; }
-            const uint8_t * rp = myst + slot * MF_CHUNK + 144 * r;
-            const u32x4a hd = *(const u32x4a *)rp;
-            uint32_t qw[4][2];
+        for (uint32_t ph = 0; ph < NPH; ++ph) {
+            const uint32_t h = half_of(bt, ph), nl = nl_of(h);
+            uint32_t ct = 0, csb = wave;                           // consume cursor
+            while (csb >= nl) { csb -= nl; ++ct; }
+            for (; ct < nt;) {
+                ks_wait_behind<MF_NI, D>(nissued - 1 - ncons);
+                ++ncons;
+                if (ncons == 1) MF_STAMP(2);
+                const uint32_t t = ct, li = csb;
+                csb += MF_WAVES;
+                while (csb >= nl) { csb -= nl; ++ct; }
+                const uint8_t * rp = myst + slot * MF_CHUNK + 144 * r;
+                const u32x4a hd = *(const u32x4a *)rp;
+                uint32_t qw[4][2];
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                qw[c][0] = *(const uint32_t *)(rp + 16 + 32 * c + 8 * j);
-                qw[c][1] = *(const uint32_t *)(rp + 20 + 32 * c + 8 * j);
-            }
-            // activation operands of this superblock (zero for lanes past NC):
-            // column r, bytes 32g + 8j .. +7 of sub-block g; sub-block sums
-            // bsum[2g] + bsum[2g + 1] for g = j and 4 + j
-            u32x2 xw[8] = {};
-            u32x2 bp = {};
-            if (r < NC) mf_ld_x(xr + (size_t)r * XS + (size_t)sb * 292, j, xw, bp);
-            const uint32_t bp0 = bp.x, bp1 = bp.y;
-            // every read of this stage is done before it is refilled
-            WAIT_LGKM0();
-            issue_one();
-            if (ncons == 1)
-                for (uint32_t k = 1; k < (uint32_t)D; ++k)
-                    if (nissued < ncons + D) issue_one();
-            slot = slot + 1 == (uint32_t)D ? 0 : slot + 1;
+                for (int c = 0; c < 4; ++c) {
+                    qw[c][0] = *(const uint32_t *)(rp + 16 + 32 * c + 8 * j);
+                    qw[c][1] = *(const uint32_t *)(rp + 20 + 32 * c + 8 * j);
+                }
+                // activation operands of this superblock (zero for lanes past NC):
+                // column r, bytes 32g + 8j .. +7 of sub-block g; sub-block sums
+                // bsum[2g] + bsum[2g + 1] for g = j and 4 + j
+                u32x2 xw[8] = {};
+                u32x2 bp = {};
+                if (r < NC)
+                    mf_ld_x(xr + (size_t)r * XS + (KH ? (size_t)592 * (li >> 1) + 292 * (li & 1) : (size_t)li * 292), j, xw, bp);
+                const uint32_t bp0 = bp.x, bp1 = bp.y;
+                // every read of this stage is done before it is refilled
+                WAIT_LGKM0();
+                issue_one();
+                if (ncons == 1)
+                    for (uint32_t k = 1; k < (uint32_t)D; ++k)
+                        if (nissued < ncons + D) issue_one();
+                slot = slot + 1 == (uint32_t)D ? 0 : slot + 1;
 
-            // scales / mins of row r (6-bit, SWAR as in fl_q4k_scale_min)
-            const uint32_t sclo = hd.y & 0x3F3F3F3Fu, mlo = hd.z & 0x3F3F3F3Fu;
-            const uint32_t schi = (hd.w & 0x0F0F0F0Fu) | ((hd.y >> 2) & 0x30303030u);
-            const uint32_t mhi = ((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u);
-            v4i acc[8];
+                // scales / mins of row r (6-bit, SWAR as in fl_q4k_scale_min)
+                const uint32_t sclo = hd.y & 0x3F3F3F3Fu, mlo = hd.z & 0x3F3F3F3Fu;
+                const uint32_t schi = (hd.w & 0x0F0F0F0Fu) | ((hd.y >> 2) & 0x30303030u);
+                const uint32_t mhi = ((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u);
+                v4i acc[8];
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const uint32_t lo0 = qw[c][0] & 0x0F0F0F0Fu, lo1 = qw[c][1] & 0x0F0F0F0Fu;
-                const uint32_t hi0 = (qw[c][0] >> 4) & 0x0F0F0F0Fu, hi1 = (qw[c][1] >> 4) & 0x0F0F0F0Fu;
-                const long blo = (long)(((uint64_t)lo1 << 32) | lo0), bhi = (long)(((uint64_t)hi1 << 32) | hi0);
-                const long alo = __builtin_bit_cast(long, xw[2 * c]);
-                const long ahi = __builtin_bit_cast(long, xw[2 * c + 1]);
-                acc[2 * c] = __builtin_amdgcn_mfma_i32_16x16x32_i8(alo, blo, v4i{0, 0, 0, 0}, 0, 0, 0);
-                acc[2 * c + 1] = __builtin_amdgcn_mfma_i32_16x16x32_i8(ahi, bhi, v4i{0, 0, 0, 0}, 0, 0, 0);
-            }
-            // min term: A = sub-block sums of column r (g = 4h + j), B = mins of row r
-            const float bsa0 = (float)((int)(int16_t)(bp0 & 0xFFFFu) + (int)(int16_t)(bp0 >> 16));
-            const float bsa1 = (float)((int)(int16_t)(bp1 & 0xFFFFu) + (int)(int16_t)(bp1 >> 16));
-            const float bm0 = (float)((mlo >> (8 * j)) & 0xFFu), bm1 = (float)((mhi >> (8 * j)) & 0xFFu);
-            v4f cm = __builtin_amdgcn_mfma_f32_16x16x4f32(bsa0, bm0, v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-            cm = __builtin_amdgcn_mfma_f32_16x16x4f32(bsa1, bm1, cm, 0, 0, 0);
-            int sc[8];
+                for (int c = 0; c < 4; ++c) {
+                    const uint32_t lo0 = qw[c][0] & 0x0F0F0F0Fu, lo1 = qw[c][1] & 0x0F0F0F0Fu;
+                    const uint32_t hi0 = (qw[c][0] >> 4) & 0x0F0F0F0Fu, hi1 = (qw[c][1] >> 4) & 0x0F0F0F0Fu;
+                    const long blo = (long)(((uint64_t)lo1 << 32) | lo0), bhi = (long)(((uint64_t)hi1 << 32) | hi0);
+                    const long alo = __builtin_bit_cast(long, xw[2 * c]);
+                    const long ahi = __builtin_bit_cast(long, xw[2 * c + 1]);
+                    acc[2 * c] = __builtin_amdgcn_mfma_i32_16x16x32_i8(alo, blo, v4i{0, 0, 0, 0}, 0, 0, 0);
+                    acc[2 * c + 1] = __builtin_amdgcn_mfma_i32_16x16x32_i8(ahi, bhi, v4i{0, 0, 0, 0}, 0, 0, 0);
+                }
+                // min term: A = sub-block sums of column r (g = 4h + j), B = mins of row r
+                const float bsa0 = (float)((int)(int16_t)(bp0 & 0xFFFFu) + (int)(int16_t)(bp0 >> 16));
+                const float bsa1 = (float)((int)(int16_t)(bp1 & 0xFFFFu) + (int)(int16_t)(bp1 >> 16));
+                const float bm0 = (float)((mlo >> (8 * j)) & 0xFFu), bm1 = (float)((mhi >> (8 * j)) & 0xFFu);
+                v4f cm = __builtin_amdgcn_mfma_f32_16x16x4f32(bsa0, bm0, v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                cm = __builtin_amdgcn_mfma_f32_16x16x4f32(bsa1, bm1, cm, 0, 0, 0);
+                int sc[8];
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                sc[k] = (int)((sclo >> (8 * k)) & 0xFFu);
-                sc[4 + k] = (int)((schi >> (8 * k)) & 0xFFu);
-            }
-            // park: terms [sb][row][column], the lane's 4 columns in one
-            // 16-byte store (rows past the batch and columns past nx hold
-            // values the fold never reads)
-            const uint32_t rl = 16 * t + r;                         // row within the batch
-            int ia[4];
+                for (int k = 0; k < 4; ++k) {
+                    sc[k] = (int)((sclo >> (8 * k)) & 0xFFu);
+                    sc[4 + k] = (int)((schi >> (8 * k)) & 0xFFu);
+                }
+                // park: terms [li][row][column], the lane's 4 columns in one
+                // 16-byte store (rows past the batch and columns past nx hold
+                // values the fold never reads)
+                const uint32_t rl = 16 * t + r;                     // row within the batch
+                int ia[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                ia[i] = 0;
+                for (int i = 0; i < 4; ++i) {
+                    ia[i] = 0;
 #pragma unroll
-                for (int k = 0; k < 8; ++k) ia[i] += __mul24(sc[k], acc[k][i]);
+                    for (int k = 0; k < 8; ++k) ia[i] += __mul24(sc[k], acc[k][i]);
+                }
+                if (4 * j < NC) {
+                    const size_t e = ((size_t)li * nrb + rl) * NC + 4 * j;
+                    lds_st128(&TI[e], u32x4a{(uint32_t)ia[0], (uint32_t)ia[1], (uint32_t)ia[2], (uint32_t)ia[3]});
+                    lds_st128(&TM[e], u32x4a{(uint32_t)(int)cm[0], (uint32_t)(int)cm[1], (uint32_t)(int)cm[2],
+                                              (uint32_t)(int)cm[3]});
+                }
+                if (j == 0) lds_st32(&TH[(size_t)li * nrb + rl], hd.x);
             }
-            if (4 * j < NC) {
-                const size_t e = ((size_t)sb * nrb + rl) * NC + 4 * j;
-                lds_st128(&TI[e], u32x4a{(uint32_t)ia[0], (uint32_t)ia[1], (uint32_t)ia[2], (uint32_t)ia[3]});
-                lds_st128(&TM[e], u32x4a{(uint32_t)(int)cm[0], (uint32_t)(int)cm[1], (uint32_t)(int)cm[2],
-                                          (uint32_t)(int)cm[3]});
+            if constexpr (KH) {
+                if (ph == 0) {
+                    // every wave is done with this half's activations and
+                    // terms: stage the other half while folding this one
+                    lds_barrier();
+                    stage_half(h ^ 1);
+                    for (uint32_t frl = frl0; frl < nrow; frl += FROWS) {
+                        const float s0 = mf_fold_h<NC>(TI, TM, TH, dkt, nl, nsb, h, nrb, fk, fp, frl, fp < nx);
+                        if (fk == 0) lds_st32(&yph[frl * NC + fp], __float_as_uint(s0));
+                    }
+                    // the staging DMAs are the youngest loads (the batch's y too)
+                    WAIT_VM(0);
+                    lds_barrier();
+                }
             }
-            if (j == 0) lds_st32(&TH[(size_t)sb * nrb + rl], hd.x);
         }
-        if (y_mine) ks_wait_behind<MF_NI, D + 1>(min(nissued - y_at, (uint32_t)D));
+        if (!KH && y_mine) ks_wait_behind<MF_NI, D + 1>(min(nissued - y_at, (uint32_t)D));
         lds_barrier();
         MF_STAMP(3);
         for (uint32_t frl = frl0; frl < nrow; frl += FROWS) {
             const bool fok = fp < nx;
-            const float rr = mf_fold<NC>(TI, TM, TH, xr + (size_t)fp * XS, nsb, nrb, fk, fp, frl, fok);
-            if (fok && fk == 0) C.y(fp)[row0 + frl] = ysm[frl * NC + fp] + rr;
+            if constexpr (KH) {
+                // (a0 + a1) + (a2 + a3): the two halves' sums in either order
+                const uint32_t h1 = half_of(bt, 1);
+                const float s1 = mf_fold_h<NC>(TI, TM, TH, dkt, nl_of(h1), nsb, h1, nrb, fk, fp, frl, fok);
+                if (fok && fk == 0) C.y(fp)[row0 + frl] = ysm[frl * NC + fp] + (yph[frl * NC + fp] + s1);
+            } else {
+                const float rr = mf_fold<NC>(TI, TM, TH, xr + (size_t)fp * XS, nsb, nrb, fk, fp, frl, fok);
+                if (fok && fk == 0) C.y(fp)[row0 + frl] = ysm[frl * NC + fp] + rr;
+            }
         }
         lds_barrier();
     }
@@ -348,12 +479,12 @@ __device__ __forceinline__ void mf_body(const uint8_t * __restrict__ w, uint32_t
     MF_STAMP(4);
 }
 
-template <int NC, int D>
+template <int NC, int D, bool KH>
 __global__ __launch_bounds__(512) void k_dot_mfma(DotArgs a, uint32_t nrb) {
     extern __shared__ __attribute__((aligned(16))) uint8_t sm[];
     const uint8_t * w = a.w + (a.id_slot ? (size_t)(*a.id_slot) * a.estride : 0);
     const MfColsStrided C{a.x, a.y, a.xstride, a.ystride};
-    mf_body<NC, D>(w, a.rows, a.cols, C, a.nx, nrb, blockIdx.x, gridDim.x, sm);
+    mf_body<NC, D, KH>(w, a.rows, a.cols, C, a.nx, nrb, blockIdx.x, gridDim.x, sm);
 }
 
 // Grouped expert matvec (MoE): blockIdx.y = expert e.  The workgroup collects
@@ -371,7 +502,7 @@ struct MfColsMoe {
     __device__ float * y(uint32_t p) const { return y0 + (size_t)lds_ld32(&yi[p]) * ys; }
 };
 
-template <int NC, int D>
+template <int NC, int D, bool KH>
 __global__ __launch_bounds__(512) void k_moe_mfma(MoeArgs a, uint32_t nrbp) {
     extern __shared__ __attribute__((aligned(16))) uint8_t sm[];
     __shared__ uint32_t pairs[256];
@@ -395,7 +526,7 @@ __global__ __launch_bounds__(512) void k_moe_mfma(MoeArgs a, uint32_t nrbp) {
         }
         __syncthreads();
         const MfColsMoe C{a.x, a.y, a.xstride, a.ystride, cxi, cyi};
-        mf_body<NC, D>(w, a.rows, a.cols, C, nx, nrbp, blockIdx.x, gridDim.x, sm);
+        mf_body<NC, D, KH>(w, a.rows, a.cols, C, nx, nrbp, blockIdx.x, gridDim.x, sm);
         __syncthreads();
     }
 }
@@ -410,10 +541,10 @@ static uint32_t mf_pro() {
     }();
     return v;
 }
-template <int NC, int D>
+template <int NC, int D, bool KH>
 static int mf_launch_d(const DotArgs & a, uint32_t nrb, uint32_t grid, size_t smb, hipStream_t s) {
-    (void)hipFuncSetAttribute((const void *)k_dot_mfma<NC, D>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smb);
-    hipLaunchKernelGGL((k_dot_mfma<NC, D>), dim3(grid), dim3(MF_WAVES * 64), smb, s, a, nrb | (mf_pro() << 16));
+    (void)hipFuncSetAttribute((const void *)k_dot_mfma<NC, D, KH>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smb);
+    hipLaunchKernelGGL((k_dot_mfma<NC, D, KH>), dim3(grid), dim3(MF_WAVES * 64), smb, s, a, nrb | (mf_pro() << 16));
     return hip_check(hipGetLastError(), "k_dot_mfma launch");
 }
 
@@ -421,9 +552,11 @@ size_t lds_limit();
 
 
 // LDS plan for NC columns: one workgroup per CU, batch of nrb rows (a multiple
-// of 16), ring depth D; FLH_ERR_UNSUPPORTED if it cannot fit.
+// of 16), ring depth D, whole activations or K halves (kh) when the whole
+// activations do not fit with a 16-row batch; FLH_ERR_UNSUPPORTED if neither
+// fits.
 template <int NC>
-static int mf_plan(uint32_t rows, uint32_t nsb, uint32_t G, uint32_t & nrb, int & D, size_t & smb) {
+static int mf_plan_kh(uint32_t rows, uint32_t nsb, uint32_t G, uint32_t & nrb, int & D, bool & kh, size_t & smb) {
     const size_t lim = lds_limit();
     const uint32_t rpw = (rows + G - 1) / G;
     // a batch's old y values are one 64-float DMA per wave: nrb * NC <= 512
@@ -432,16 +565,22 @@ static int mf_plan(uint32_t rows, uint32_t nsb, uint32_t G, uint32_t & nrb, int 
     // measured: a 2-deep ring with a full prologue beats deeper rings (N=4,
     // 14336x4096: D=2 11.7 us, D=3 12.4 us, D=4 13.0 us)
     D = 2;
-    if (const char * e = getenv("FLH_MFMA_TUNE")) {           // "D,nrb" (development sweeps)
-        unsigned d = 0, n = 0;
-        if (sscanf(e, "%u,%u", &d, &n) == 2) {
-            if (d >= 2 && d <= 4) D = (int)d;
+    int force_kh = -1;
+    if (const char * e = getenv("FLH_MFMA_TUNE")) {           // "D,nrb[,kh]" (development sweeps)
+        unsigned d = 0, n = 0, k = 0;
+        const int got = sscanf(e, "%u,%u,%u", &d, &n, &k);
+        if (got >= 2) {
+            if (d >= 2 && d <= 3) D = (int)d;
             if (n >= 16 && n % 16 == 0 && n <= 512 / NC) nrb = n;
         }
+        if (got == 3) force_kh = (int)k;
     }
-    while (mf_smem_bytes<NC>(nrb, nsb, D) > lim && nrb > 16) nrb -= 16;
-    while (mf_smem_bytes<NC>(nrb, nsb, D) > lim && D > 2) --D;
-    smb = mf_smem_bytes<NC>(nrb, nsb, D);
+    kh = force_kh == 1 || (force_kh != 0 && mf_smem_bytes<NC, false>(16, nsb, 2) > lim);
+    if (kh && nsb < 8) kh = false;
+    auto bytes = [&]() { return kh ? mf_smem_bytes<NC, true>(nrb, nsb, D) : mf_smem_bytes<NC, false>(nrb, nsb, D); };
+    while (bytes() > lim && nrb > 16) nrb -= 16;
+    while (bytes() > lim && D > 2) --D;
+    smb = bytes();
     return smb > lim ? FLH_ERR_UNSUPPORTED : FLH_OK;
 }
 
@@ -451,13 +590,11 @@ static int mf_launch(const DotArgs & a, hipStream_t s) {
     const uint32_t G = a.rows < (uint32_t)num_cus() ? a.rows : (uint32_t)num_cus();
     uint32_t nrb;
     int D;
+    bool kh;
     size_t smb;
-    if (mf_plan<NC>(a.rows, nsb, G, nrb, D, smb)) return FLH_ERR_UNSUPPORTED;
-    switch (D) {
-        case 2: return mf_launch_d<NC, 2>(a, nrb, G, smb, s);
-        case 3: return mf_launch_d<NC, 3>(a, nrb, G, smb, s);
-        default: return mf_launch_d<NC, 4>(a, nrb, G, smb, s);
-    }
+    if (mf_plan_kh<NC>(a.rows, nsb, G, nrb, D, kh, smb)) return FLH_ERR_UNSUPPORTED;
+    if (kh) return D == 2 ? mf_launch_d<NC, 2, true>(a, nrb, G, smb, s) : mf_launch_d<NC, 3, true>(a, nrb, G, smb, s);
+    return D == 2 ? mf_launch_d<NC, 2, false>(a, nrb, G, smb, s) : mf_launch_d<NC, 3, false>(a, nrb, G, smb, s);
 }
 
 // Fewest columns for which STREAM_DOT takes the matrix-core kernel (measured:
@@ -473,10 +610,10 @@ uint32_t mfma_min_cols(uint32_t cols) {
 
 uint32_t mfma_min_cols(uint32_t cols);
 
-template <int NC, int D>
+template <int NC, int D, bool KH>
 static int mf_moe_launch_d(const MoeArgs & a, uint32_t nrb, uint32_t gx, size_t smb, hipStream_t s) {
-    (void)hipFuncSetAttribute((const void *)k_moe_mfma<NC, D>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smb);
-    hipLaunchKernelGGL((k_moe_mfma<NC, D>), dim3(gx, a.n_expert), dim3(MF_WAVES * 64), smb, s, a,
+    (void)hipFuncSetAttribute((const void *)k_moe_mfma<NC, D, KH>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smb);
+    hipLaunchKernelGGL((k_moe_mfma<NC, D, KH>), dim3(gx, a.n_expert), dim3(MF_WAVES * 64), smb, s, a,
                        nrb | (mf_pro() << 16));
     return hip_check(hipGetLastError(), "k_moe_mfma launch");
 }
@@ -491,13 +628,11 @@ static int mf_moe_launch(const MoeArgs & a, hipStream_t s) {
     if (gx > a.rows) gx = a.rows;
     uint32_t nrb;
     int D;
+    bool kh;
     size_t smb;
-    if (mf_plan<NC>(a.rows, nsb, gx, nrb, D, smb)) return FLH_ERR_UNSUPPORTED;
-    switch (D) {
-        case 2: return mf_moe_launch_d<NC, 2>(a, nrb, gx, smb, s);
-        case 3: return mf_moe_launch_d<NC, 3>(a, nrb, gx, smb, s);
-        default: return mf_moe_launch_d<NC, 4>(a, nrb, gx, smb, s);
-    }
+    if (mf_plan_kh<NC>(a.rows, nsb, gx, nrb, D, kh, smb)) return FLH_ERR_UNSUPPORTED;
+    if (kh) return D == 2 ? mf_moe_launch_d<NC, 2, true>(a, nrb, gx, smb, s) : mf_moe_launch_d<NC, 3, true>(a, nrb, gx, smb, s);
+    return D == 2 ? mf_moe_launch_d<NC, 2, false>(a, nrb, gx, smb, s) : mf_moe_launch_d<NC, 3, false>(a, nrb, gx, smb, s);
 }
 
 // Grouped Q4_K expert matvec on the matrix cores for token batches of at

@@ -34,6 +34,26 @@ def test_mfma_multicol_bitwise(flh, orc, gpu, rows, cols, nx):
     assert np.array_equal(bits(got), bits(want))
 
 
+@pytest.mark.parametrize("rows,cols,nx", [
+    (4096, 14336, 8), (20000, 2304, 8), (1000, 2560, 5), (333, 2816, 16), (4100, 4096, 3), (40, 16384, 7),
+])
+def test_mfma_k_halves_bitwise(flh, orc, gpu, rows, cols, nx):
+    """K halves forced (superblocks split by sb % 4 into two staged halves):
+    odd superblock counts, several row batches (the halves alternate), 16
+    columns, partial tiles."""
+    say("mfma k-halves", rows, cols, nx)
+    rng = np.random.default_rng(rows + 5 * cols + nx)
+    w = sane_rows(Q4_K, rows, cols, rng)
+    xs = activations(nx, cols, rng, outliers=True)
+    os.environ["FLH_MFMA_TUNE"] = "2,0,1"
+    try:
+        got, want = run_dot(flh, orc, gpu, Q4_K, w, rows, cols, xs, ystride=rows + 3,
+                            y0=rng.standard_normal((nx - 1) * (rows + 3) + rows).astype(np.float32))
+    finally:
+        del os.environ["FLH_MFMA_TUNE"]
+    assert np.array_equal(bits(got), bits(want))
+
+
 def test_mfma_equals_streaming_kernel(flh, orc, gpu):
     """Same bits with the matrix-core kernel switched off (streaming kernel)."""
     say("mfma vs kstream")
