@@ -556,7 +556,8 @@ size_t lds_limit();
 // activations do not fit with a 16-row batch; FLH_ERR_UNSUPPORTED if neither
 // fits.
 template <int NC>
-static int mf_plan_kh(uint32_t rows, uint32_t nsb, uint32_t G, uint32_t & nrb, int & D, bool & kh, size_t & smb) {
+static int mf_plan_kh(uint32_t rows, uint32_t nsb, uint32_t G, uint32_t & nrb, int & D, bool & kh, size_t & smb,
+                      bool allow_kh = true) {
     const size_t lim = lds_limit();
     const uint32_t rpw = (rows + G - 1) / G;
     // a batch's old y values are one 64-float DMA per wave: nrb * NC <= 512
@@ -576,7 +577,7 @@ static int mf_plan_kh(uint32_t rows, uint32_t nsb, uint32_t G, uint32_t & nrb, i
         if (got == 3) force_kh = (int)k;
     }
     kh = force_kh == 1 || (force_kh != 0 && mf_smem_bytes<NC, false>(16, nsb, 2) > lim);
-    if (kh && nsb < 8) kh = false;
+    if (kh && (nsb < 8 || (!allow_kh && force_kh != 1))) kh = false;
     auto bytes = [&]() { return kh ? mf_smem_bytes<NC, true>(nrb, nsb, D) : mf_smem_bytes<NC, false>(nrb, nsb, D); };
     while (bytes() > lim && nrb > 16) nrb -= 16;
     while (bytes() > lim && D > 2) --D;
@@ -619,7 +620,7 @@ static int mf_moe_launch_d(const MoeArgs & a, uint32_t nrb, uint32_t gx, size_t 
 }
 
 template <int NC>
-static int mf_moe_launch(const MoeArgs & a, hipStream_t s) {
+static int mf_moe_launch(const MoeArgs & a, hipStream_t s, bool allow_kh) {
     const uint32_t nsb = a.cols >> 8;
     // the experts that can be active at once share the CUs (one workgroup each)
     const uint32_t pairs = a.ntok * a.top_k;
@@ -630,7 +631,7 @@ static int mf_moe_launch(const MoeArgs & a, hipStream_t s) {
     int D;
     bool kh;
     size_t smb;
-    if (mf_plan_kh<NC>(a.rows, nsb, gx, nrb, D, kh, smb)) return FLH_ERR_UNSUPPORTED;
+    if (mf_plan_kh<NC>(a.rows, nsb, gx, nrb, D, kh, smb, allow_kh)) return FLH_ERR_UNSUPPORTED;
     if (kh) return D == 2 ? mf_moe_launch_d<NC, 2, true>(a, nrb, gx, smb, s) : mf_moe_launch_d<NC, 3, true>(a, nrb, gx, smb, s);
     return D == 2 ? mf_moe_launch_d<NC, 2, false>(a, nrb, gx, smb, s) : mf_moe_launch_d<NC, 3, false>(a, nrb, gx, smb, s);
 }
@@ -645,10 +646,15 @@ int launch_moe_mfma(int fmt, const MoeArgs & a, hipStream_t s) {
     if (((uintptr_t)a.w & 15) || (a.estride & 15) || ((uintptr_t)a.x & 3) || (a.xstride & 3) || getenv("FLH_NO_MFMA") ||
         a.ntok * a.top_k > 256)
         return FLH_ERR_UNSUPPORTED;
-    // an expert gets at most one pair per token
+    // an expert gets at most one pair per token.  K halves only as a last
+    // resort: most experts get few pairs, and 4-column passes that hold the
+    // whole activations beat an 8-column pass that restages them (Mixtral
+    // top-2 of 8, batch 8: 217 vs 253 us)
     int rc = FLH_ERR_UNSUPPORTED;
-    if (a.ntok > 4) rc = mf_moe_launch<8>(a, s);
-    if (rc == FLH_ERR_UNSUPPORTED) rc = mf_moe_launch<4>(a, s);
+    if (a.ntok > 4) rc = mf_moe_launch<8>(a, s, false);
+    if (rc == FLH_ERR_UNSUPPORTED) rc = mf_moe_launch<4>(a, s, false);
+    if (rc == FLH_ERR_UNSUPPORTED && a.ntok > 4) rc = mf_moe_launch<8>(a, s, true);
+    if (rc == FLH_ERR_UNSUPPORTED) rc = mf_moe_launch<4>(a, s, true);
     return rc;
 }
 
