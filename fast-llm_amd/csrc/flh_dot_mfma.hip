@@ -56,8 +56,8 @@ constexpr uint32_t MF_WAVES = 8;
 constexpr uint32_t MF_CHUNK = 2304;          // 16 rows x one Q4_K superblock
 constexpr int MF_NI = 3;                     // DMA instructions per chunk
 
-// LDS: [waves][D][2304] ring | xr [NC][XS] raw q8_K appendices | TI, TM [nrb][NC][nl]
-//      | TH [nrb][nl] | ysm [nrb * NC] | (K halves) yph [nrb * NC], dkt [NC][nsb]
+// LDS: [waves][D][2304] ring | xr [NC][XS] raw q8_K appendices | TI, TM [nl][nrb][NC]
+//      | TH [nl][nrb] | ysm [nrb * NC] | (K halves) yph [nrb * NC], dkt [NC][nsb]
 // XS: a column's appendix (292 bytes per superblock) padded so that XS / 4 is
 // 8 mod 32 (the 16 columns' reads of one k-slice fall in distinct banks).
 //
@@ -65,6 +65,12 @@ constexpr int MF_NI = 3;                     // DMA instructions per chunk
 // split by sb % 4 into half 0 ({0, 1}) and half 1 ({2, 3}); a batch streams
 // one half, folds accumulators 0-1 (resp. 2-3) of the reference's four, stages
 // the other half's activations and streams that.  nl = superblocks held at once.
+// Term strides per superblock, padded to 8 mod 32 words: the fold's four
+// accumulator lanes of a (row, column) read superblocks one apart, which would
+// otherwise fall in one LDS bank (nrb * NC is a multiple of 64).
+template <int NC>
+__host__ __device__ inline uint32_t mf_ts(uint32_t nrb) { return nrb * NC + 8; }
+__host__ __device__ inline uint32_t mf_ths(uint32_t nrb) { return nrb + 8; }
 __host__ __device__ inline uint32_t mf_xs(uint32_t nsb) { return ((nsb * 292 + 127) & ~127u) + 32; }
 // K halves: pairs of superblocks at 592-byte pitch
 __host__ __device__ inline uint32_t mf_xs_h(uint32_t nl) { return ((((nl + 1) >> 1) * 592 + 127) & ~127u) + 32; }
@@ -77,8 +83,8 @@ __device__ __forceinline__ uint32_t mf_sbh(uint32_t li, uint32_t h) { return 4 *
 template <int NC, bool KH>
 __host__ __device__ inline size_t mf_smem_bytes(uint32_t nrb, uint32_t nsb, int D) {
     const uint32_t nl = KH ? mf_nsbh(nsb, 0) : nsb;
-    return (size_t)MF_WAVES * D * MF_CHUNK + (size_t)NC * (KH ? mf_xs_h(nl) : mf_xs(nl)) + (size_t)nrb * NC * nl * 8 +
-           (size_t)nrb * nl * 4 + (size_t)nrb * NC * 4 + (KH ? (size_t)nrb * NC * 4 + (size_t)NC * nsb * 4 : 0);
+    return (size_t)MF_WAVES * D * MF_CHUNK + (size_t)NC * (KH ? mf_xs_h(nl) : mf_xs(nl)) + (size_t)mf_ts<NC>(nrb) * nl * 8 +
+           (size_t)mf_ths(nrb) * nl * 4 + (size_t)nrb * NC * 4 + (KH ? (size_t)nrb * NC * 4 + (size_t)NC * nsb * 4 : 0);
 }
 
 // Column sources of one pass: activation column p at x(p) (fp32 x followed by
@@ -139,16 +145,17 @@ __device__ __forceinline__ float mf_fold(const int * TI, const int * TM, const u
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const uint32_t sq = s + 4 * q;
-                ti[q] = TI[((size_t)sq * nrb + rl) * NC + p];
-                tm[q] = TM[((size_t)sq * nrb + rl) * NC + p];
-                th[q] = TH[(size_t)sq * nrb + rl];
+                ti[q] = TI[(size_t)sq * mf_ts<NC>(nrb) + rl * NC + p];
+                tm[q] = TM[(size_t)sq * mf_ts<NC>(nrb) + rl * NC + p];
+                th[q] = TH[(size_t)sq * mf_ths(nrb) + rl];
                 dk[q] = *(const float *)(xp + (size_t)sq * 292);
             }
 #pragma unroll
             for (int q = 0; q < 4; ++q) step(ti[q], tm[q], th[q], dk[q]);
         }
         for (; s < nsb; s += 4)
-            step(TI[((size_t)s * nrb + rl) * NC + p], TM[((size_t)s * nrb + rl) * NC + p], TH[(size_t)s * nrb + rl],
+            step(TI[(size_t)s * mf_ts<NC>(nrb) + rl * NC + p], TM[(size_t)s * mf_ts<NC>(nrb) + rl * NC + p],
+                 TH[(size_t)s * mf_ths(nrb) + rl],
                  *(const float *)(xp + (size_t)s * 292));
     }
     const float s01 = acc + qx1f(acc);
@@ -178,16 +185,17 @@ __device__ __forceinline__ float mf_fold_h(const int * TI, const int * TM, const
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const uint32_t lq = li + 2 * q;
-                ti[q] = TI[((size_t)lq * nrb + rl) * NC + p];
-                tm[q] = TM[((size_t)lq * nrb + rl) * NC + p];
-                th[q] = TH[(size_t)lq * nrb + rl];
+                ti[q] = TI[(size_t)lq * mf_ts<NC>(nrb) + rl * NC + p];
+                tm[q] = TM[(size_t)lq * mf_ts<NC>(nrb) + rl * NC + p];
+                th[q] = TH[(size_t)lq * mf_ths(nrb) + rl];
                 dk[q] = dkt[p * nsb + mf_sbh(lq, h)];
             }
 #pragma unroll
             for (int q = 0; q < 4; ++q) step(ti[q], tm[q], th[q], dk[q]);
         }
         for (; li < nl; li += 2)
-            step(TI[((size_t)li * nrb + rl) * NC + p], TM[((size_t)li * nrb + rl) * NC + p], TH[(size_t)li * nrb + rl],
+            step(TI[(size_t)li * mf_ts<NC>(nrb) + rl * NC + p], TM[(size_t)li * mf_ts<NC>(nrb) + rl * NC + p],
+                 TH[(size_t)li * mf_ths(nrb) + rl],
                  dkt[p * nsb + mf_sbh(li, h)]);
     }
     return acc + qx1f(acc);
@@ -219,9 +227,9 @@ __device__ __forceinline__ void mf_body(const uint8_t * __restrict__ w, uint32_t
     const uint32_t XS = KH ? mf_xs_h(NL) : mf_xs(NL);
     uint8_t * xr = sm + (size_t)MF_WAVES * D * MF_CHUNK;
     int * TI = (int *)(xr + (size_t)NC * XS);
-    int * TM = TI + (size_t)nrb * NC * NL;
-    uint32_t * TH = (uint32_t *)(TM + (size_t)nrb * NC * NL);
-    float * ysm = (float *)(TH + (size_t)nrb * NL);
+    int * TM = TI + (size_t)mf_ts<NC>(nrb) * NL;
+    uint32_t * TH = (uint32_t *)(TM + (size_t)mf_ts<NC>(nrb) * NL);
+    float * ysm = (float *)(TH + (size_t)mf_ths(nrb) * NL);
     float * yph = ysm + (size_t)nrb * NC;                         // KH: first half's sums
     float * dkt = yph + (size_t)nrb * NC;                         // KH: q8_K scales [NC][nsb]
 
@@ -435,12 +443,12 @@ __device__ __forceinline__ void mf_body(const uint8_t * __restrict__ w, uint32_t
                     for (int k = 0; k < 8; ++k) ia[i] += __mul24(sc[k], acc[k][i]);
                 }
                 if (4 * j < NC) {
-                    const size_t e = ((size_t)li * nrb + rl) * NC + 4 * j;
+                    const size_t e = (size_t)li * mf_ts<NC>(nrb) + rl * NC + 4 * j;
                     lds_st128(&TI[e], u32x4a{(uint32_t)ia[0], (uint32_t)ia[1], (uint32_t)ia[2], (uint32_t)ia[3]});
                     lds_st128(&TM[e], u32x4a{(uint32_t)(int)cm[0], (uint32_t)(int)cm[1], (uint32_t)(int)cm[2],
                                               (uint32_t)(int)cm[3]});
                 }
-                if (j == 0) lds_st32(&TH[(size_t)li * nrb + rl], hd.x);
+                if (j == 0) lds_st32(&TH[(size_t)li * mf_ths(nrb) + rl], hd.x);
             }
             if constexpr (KH) {
                 if (ph == 0) {
