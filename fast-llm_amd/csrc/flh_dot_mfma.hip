@@ -72,8 +72,12 @@ template <int NC>
 __host__ __device__ inline uint32_t mf_ts(uint32_t nrb) { return nrb * NC + 8; }
 __host__ __device__ inline uint32_t mf_ths(uint32_t nrb) { return nrb + 8; }
 __host__ __device__ inline uint32_t mf_xs(uint32_t nsb) { return ((nsb * 292 + 127) & ~127u) + 32; }
-// K halves: pairs of superblocks at 592-byte pitch
-__host__ __device__ inline uint32_t mf_xs_h(uint32_t nl) { return ((((nl + 1) >> 1) * 592 + 127) & ~127u) + 32; }
+// K halves: slot li holds its superblock's 292-byte block for each of the NC
+// columns at a 304-byte pitch ([li][NC][304]), the block at byte 12 of its
+// 304 (copied as 19 16-byte pieces starting 12 bytes before the block, which
+// stays inside the column's q8_1 appendix for superblock 0).  A 76-word
+// column pitch puts 8 columns' reads of a k-slice in distinct banks.
+constexpr uint32_t MF_XB = 304, MF_XO = 12;
 __host__ __device__ inline uint32_t mf_nsbh(uint32_t nsb, uint32_t h) {
     const uint32_t r = nsb & 3;
     return (nsb >> 2) * 2 + (h == 0 ? (r < 2 ? r : 2u) : (r > 2 ? r - 2 : 0u));
@@ -83,7 +87,8 @@ __device__ __forceinline__ uint32_t mf_sbh(uint32_t li, uint32_t h) { return 4 *
 template <int NC, bool KH>
 __host__ __device__ inline size_t mf_smem_bytes(uint32_t nrb, uint32_t nsb, int D) {
     const uint32_t nl = KH ? mf_nsbh(nsb, 0) : nsb;
-    return (size_t)MF_WAVES * D * MF_CHUNK + (size_t)NC * (KH ? mf_xs_h(nl) : mf_xs(nl)) + (size_t)mf_ts<NC>(nrb) * nl * 8 +
+    return (size_t)MF_WAVES * D * MF_CHUNK + (KH ? (size_t)nl * NC * MF_XB : (size_t)NC * mf_xs(nl)) +
+           (size_t)mf_ts<NC>(nrb) * nl * 8 +
            (size_t)mf_ths(nrb) * nl * 4 + (size_t)nrb * NC * 4 + (KH ? (size_t)nrb * NC * 4 + (size_t)NC * nsb * 4 : 0);
 }
 
@@ -162,6 +167,31 @@ __device__ __forceinline__ float mf_fold(const int * TI, const int * TM, const u
     return s01 + qx2f(s01);
 }
 
+// Wait until at most n of this wave's DMA instructions are outstanding
+// (n >= 15 waits for 15: more waiting, never less).
+__device__ __forceinline__ void mf_wait_vm(uint32_t n) {
+    // wave-uniform by construction; readfirstlane keeps the switch on the
+    // scalar unit (a divergent switch runs every case's wait)
+    switch (__builtin_amdgcn_readfirstlane(n)) {
+        case 0: WAIT_VM(0); break;
+        case 1: WAIT_VM(1); break;
+        case 2: WAIT_VM(2); break;
+        case 3: WAIT_VM(3); break;
+        case 4: WAIT_VM(4); break;
+        case 5: WAIT_VM(5); break;
+        case 6: WAIT_VM(6); break;
+        case 7: WAIT_VM(7); break;
+        case 8: WAIT_VM(8); break;
+        case 9: WAIT_VM(9); break;
+        case 10: WAIT_VM(10); break;
+        case 11: WAIT_VM(11); break;
+        case 12: WAIT_VM(12); break;
+        case 13: WAIT_VM(13); break;
+        case 14: WAIT_VM(14); break;
+        default: WAIT_VM(15); break;
+    }
+}
+
 // K halves: fold of half h (local superblocks li, terms [li][row][column]):
 // lane k < 2 runs accumulator 2h + k over li = k, k + 2, ... (superblocks in
 // increasing order); returns a_{2h} + a_{2h+1} in lane 0 of the quad.  The
@@ -224,9 +254,9 @@ __device__ __forceinline__ void mf_body(const uint8_t * __restrict__ w, uint32_t
     auto sb_of = [&](uint32_t li, uint32_t h) -> uint32_t { return KH ? mf_sbh(li, h) : li; };
     const uint32_t NL = nl_of(0);                                 // superblocks held at once
     uint8_t * myst = sm + (size_t)wave * D * MF_CHUNK;
-    const uint32_t XS = KH ? mf_xs_h(NL) : mf_xs(NL);
+    const uint32_t XS = KH ? 0u : mf_xs(NL);
     uint8_t * xr = sm + (size_t)MF_WAVES * D * MF_CHUNK;
-    int * TI = (int *)(xr + (size_t)NC * XS);
+    int * TI = (int *)(xr + (KH ? (size_t)NL * NC * MF_XB : (size_t)NC * XS));
     int * TM = TI + (size_t)mf_ts<NC>(nrb) * NL;
     uint32_t * TH = (uint32_t *)(TM + (size_t)mf_ts<NC>(nrb) * NL);
     float * ysm = (float *)(TH + (size_t)mf_ths(nrb) * NL);
@@ -242,40 +272,29 @@ __device__ __forceinline__ void mf_body(const uint8_t * __restrict__ w, uint32_t
     // ---- activations -> LDS by DMA, issued first (older than every weight
     // DMA, so the wait before the first chunk covers them).  Whole: each
     // column's q8_K appendix copied as is, 1 KiB per instruction, the last
-    // 0-12 bytes by a dword instruction.  K halves: the half's pairs of 292-byte
-    // blocks at a 592-byte pitch, 1 KiB per instruction, plus every
-    // superblock's scale into dkt.  Columns past nx copy column 0 (their results are never
-    // stored).
-    auto stage_half = [&](uint32_t h) {
-        // pairs (sb, sb + 1) of the half are contiguous in the appendix (584
-        // bytes): pair m -> LDS bytes 592 m, as 37 16-byte pieces (the last
-        // 8 bytes belong to the other half and are never read); pieces that
-        // would pass the appendix's end are copied by dword loads.
-        const uint32_t np = (nl_of(h) + 1) >> 1, npc = np * 37, nin = (npc + 63) >> 6;
-        const uint32_t aend = nsb * 292;
-        const uint32_t per = nin + 1;
-        for (uint32_t i = wave; i < NC * per; i += MF_WAVES) {
-            const uint32_t n = i / per, k = i % per;
-            const uint8_t * src = (const uint8_t *)C.x(n < nx ? n : 0) + xqk_off(cols);
-            uint8_t * dst = xr + (size_t)n * XS;
-            if (k < nin) {
-                const uint32_t pc = 64 * k + lane, m = pc / 37, o = pc - m * 37;
-                const uint32_t go = 1168 * m + 584 * h + 16 * o;
-                if (pc < npc && go + 16 <= aend)
-                    __builtin_amdgcn_global_load_lds(GPTR(src + go), LPTR(dst + 1024 * k), 16, 0, 0);
-            } else {
-                // the piece of the last pair that straddles the appendix's end
-                const uint32_t bl = 1168 * (np - 1) + 584 * h, rem = aend - bl;
-                if (aend > bl && rem < 592 && lane < ((rem & 15) >> 2)) {
-                    const uint32_t o = rem >> 4;
-                    __builtin_amdgcn_global_load_lds(GPTR(src + bl + 16 * o + 4 * lane),
-                                                     LPTR(dst + 16 * ((np - 1) * 37 + o)), 4, 0, 0);
-                }
+    // 0-12 bytes by a dword instruction.  K halves: the half's slots, 1 KiB
+    // per instruction, plus every superblock's scale into dkt.  Columns past
+    // nx copy column 0 (their results are never stored).
+    // K halves: DMA of slots [l0, l1) of half h (19 NC pieces per slot), the
+    // instructions dealt from wave w0 with stride ws; returns the number of
+    // instructions this wave issued (each has an active lane).
+    auto stage_slots = [&](uint32_t h, uint32_t l0, uint32_t l1, uint32_t w0, uint32_t ws) -> uint32_t {
+        const uint32_t e0 = l0 * 19 * NC, e1 = l1 * 19 * NC, nin = (e1 - e0 + 63) >> 6;
+        uint32_t cnt = 0;
+        for (uint32_t i = w0; i < nin; i += ws) {
+            const uint32_t e = e0 + 64 * i + lane;
+            if (e < e1) {
+                const uint32_t li = e / (19 * NC), rem = e - li * 19 * NC, n = rem / 19, o = rem - n * 19;
+                const uint8_t * src = (const uint8_t *)C.x(n < nx ? n : 0) + xqk_off(cols) +
+                                      (size_t)mf_sbh(li, h) * 292 + 16 * o - MF_XO;
+                __builtin_amdgcn_global_load_lds(GPTR(src), LPTR(xr + 16 * (size_t)(e0 + 64 * i)), 16, 0, 0);
             }
+            ++cnt;
         }
+        return cnt;
     };
     if constexpr (KH) {
-        stage_half(0);
+        stage_slots(0, 0, nl_of(0), wave, MF_WAVES);
         for (uint32_t i = wave; i < (NC * nsb + 63) / 64; i += MF_WAVES) {
             const uint32_t e = 64 * i + lane;
             if (e < NC * nsb) {
@@ -311,6 +330,29 @@ __device__ __forceinline__ void mf_body(const uint8_t * __restrict__ w, uint32_t
     uint32_t qnt = nbatch ? (nrow_of(0) + 15) >> 4 : 0;
     while (qsb >= qnl) { qsb -= qnl; ++qt; }
     uint32_t nissued = 0, ncons = 0;
+    // K halves: this wave's DMA instructions so far (vm), and that count right
+    // after each ring stage's chunk, the y DMA and the latest restaging: the
+    // restaging DMAs interleave with the chunks, so waits count instructions
+    uint32_t vm = 0, ce0 = 0, ce1 = 0, y_vm = 0, rs_vm = 0;
+    // one slot's restaging: per instruction i, this lane's piece (column, 16-byte
+    // offset) is fixed, so its source minus the superblock offset is kept
+    constexpr uint32_t NIR = (19 * NC + 63) / 64;                 // instructions per slot
+    const uint8_t * rsrc[NIR];
+#pragma unroll
+    for (uint32_t i = 0; i < NIR; ++i) {
+        const uint32_t pc = 64 * i + lane, n = pc / 19, o = pc - n * 19;
+        rsrc[i] = (const uint8_t *)C.x(n < nx && n < NC ? n : 0) + xqk_off(cols) + 16 * o - MF_XO;
+    }
+    auto restage_slot = [&](uint32_t h, uint32_t li) {
+        const size_t so = (size_t)mf_sbh(li, h) * 292;
+#pragma unroll
+        for (uint32_t i = 0; i < NIR; ++i)
+            if (64 * i + lane < 19 * NC)
+                __builtin_amdgcn_global_load_lds(GPTR(rsrc[i] + so), LPTR(xr + 16 * (size_t)li * 19 * NC + 1024 * i),
+                                                 16, 0, 0);
+        vm += NIR;
+    };
+    static_assert(!KH || D == 2, "K halves run a 2-deep ring");
     auto issue_one = [&]() {
         while (qbt < nbatch && qt >= qnt) {
             if (++qph == NPH) {
@@ -333,6 +375,11 @@ __device__ __forceinline__ void mf_body(const uint8_t * __restrict__ w, uint32_t
                                              FLH_MF_AUX);
             __builtin_amdgcn_global_load_lds(GPTR(base + (size_t)min(pr2, nv1) * rb + po2), LPTR(stage + 2048), 4, 0,
                                              FLH_MF_AUX);
+            if constexpr (KH) {
+                vm += MF_NI;
+                ce1 = (nissued & 1) ? vm : ce1;
+                ce0 = (nissued & 1) ? ce0 : vm;
+            }
             ++nissued;
             qsb += MF_WAVES;
             while (qsb >= qnl) { qsb -= qnl; ++qt; }
@@ -350,6 +397,7 @@ __device__ __forceinline__ void mf_body(const uint8_t * __restrict__ w, uint32_t
             const float * ya = yv ? C.y(yp) + row0 + yr : C.y(0) + row0;
             __builtin_amdgcn_global_load_lds(GPTR(ya), LPTR(ysm + wave * 64), 4, 0, 0);
             y_at = nissued;
+            y_vm = ++vm;
         }
     };
     if (nbatch) issue_y(0);
@@ -373,8 +421,22 @@ __device__ __forceinline__ void mf_body(const uint8_t * __restrict__ w, uint32_t
             const uint32_t h = half_of(bt, ph), nl = nl_of(h);
             uint32_t ct = 0, csb = wave;                           // consume cursor
             while (csb >= nl) { csb -= nl; ++ct; }
+            // K halves: a slot is restaged right after its last use when one
+            // wave consumes every chunk of that slot (one tile, or nl a
+            // multiple of the wave count); otherwise after the half
+            const bool early = nt == 1 || nl % MF_WAVES == 0;
+            if constexpr (KH) {
+                // slots of the other half that this half does not use are
+                // free now: stage them (waves by slot)
+                const uint32_t nlo = nl_of(h ^ 1);
+                for (uint32_t li = nl + wave; early && ph == 0 && li < nlo; li += MF_WAVES) {
+                    restage_slot(h ^ 1, li);
+                    rs_vm = vm;
+                }
+            }
             for (; ct < nt;) {
-                ks_wait_behind<MF_NI, D>(nissued - 1 - ncons);
+                if constexpr (KH) mf_wait_vm(vm - (((ncons & 1) ? ce1 : 0u) | ((ncons & 1) ? 0u : ce0)));
+                else ks_wait_behind<MF_NI, D>(nissued - 1 - ncons);
                 ++ncons;
                 if (ncons == 1) MF_STAMP(2);
                 const uint32_t t = ct, li = csb;
@@ -394,10 +456,20 @@ __device__ __forceinline__ void mf_body(const uint8_t * __restrict__ w, uint32_t
                 u32x2 xw[8] = {};
                 u32x2 bp = {};
                 if (r < NC)
-                    mf_ld_x(xr + (size_t)r * XS + (KH ? (size_t)592 * (li >> 1) + 292 * (li & 1) : (size_t)li * 292), j, xw, bp);
+                    mf_ld_x(KH ? xr + ((size_t)li * NC + r) * MF_XB + MF_XO : xr + (size_t)r * XS + (size_t)li * 292, j,
+                            xw, bp);
                 const uint32_t bp0 = bp.x, bp1 = bp.y;
                 // every read of this stage is done before it is refilled
                 WAIT_LGKM0();
+                if constexpr (KH) {
+                    // the slot's last use in this half: stage the other half's
+                    // block into it (ahead of the next chunk, so chunk waits
+                    // count it)
+                    if (early && ph == 0 && t == nt - 1 && li < nl_of(h ^ 1)) {
+                        restage_slot(h ^ 1, li);
+                        rs_vm = vm;
+                    }
+                }
                 issue_one();
                 if (ncons == 1)
                     for (uint32_t k = 1; k < (uint32_t)D; ++k)
@@ -452,21 +524,27 @@ __device__ __forceinline__ void mf_body(const uint8_t * __restrict__ w, uint32_t
             }
             if constexpr (KH) {
                 if (ph == 0) {
-                    // every wave is done with this half's activations and
-                    // terms: stage the other half while folding this one
+                    // this half's terms are complete and its activations read
                     lds_barrier();
-                    stage_half(h ^ 1);
+                    if (!early)
+                        for (uint32_t li = wave; li < nl_of(h ^ 1); li += MF_WAVES) {
+                            restage_slot(h ^ 1, li);
+                            rs_vm = vm;
+                        }
                     for (uint32_t frl = frl0; frl < nrow; frl += FROWS) {
                         const float s0 = mf_fold_h<NC>(TI, TM, TH, dkt, nl, nsb, h, nrb, fk, fp, frl, fp < nx);
                         if (fk == 0) lds_st32(&yph[frl * NC + fp], __float_as_uint(s0));
                     }
-                    // the staging DMAs are the youngest loads (the batch's y too)
-                    WAIT_VM(0);
+                    // this wave's restaging has landed (the fold ran while it
+                    // was in flight); the barrier publishes every wave's and
+                    // orders the fold before the next half's parks
+                    mf_wait_vm(vm - rs_vm);
                     lds_barrier();
                 }
             }
         }
         if (!KH && y_mine) ks_wait_behind<MF_NI, D + 1>(min(nissued - y_at, (uint32_t)D));
+        if (KH && y_mine) mf_wait_vm(vm - y_vm);
         lds_barrier();
         MF_STAMP(3);
         for (uint32_t frl = frl0; frl < nrow; frl += FROWS) {
@@ -552,7 +630,8 @@ static uint32_t mf_pro() {
 template <int NC, int D, bool KH>
 static int mf_launch_d(const DotArgs & a, uint32_t nrb, uint32_t grid, size_t smb, hipStream_t s) {
     (void)hipFuncSetAttribute((const void *)k_dot_mfma<NC, D, KH>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smb);
-    hipLaunchKernelGGL((k_dot_mfma<NC, D, KH>), dim3(grid), dim3(MF_WAVES * 64), smb, s, a, nrb | (mf_pro() << 16));
+    hipLaunchKernelGGL((k_dot_mfma<NC, D, KH>), dim3(grid), dim3(MF_WAVES * 64), smb, s, a,
+                       nrb | (mf_pro() << 16));
     return hip_check(hipGetLastError(), "k_dot_mfma launch");
 }
 
@@ -586,6 +665,7 @@ static int mf_plan_kh(uint32_t rows, uint32_t nsb, uint32_t G, uint32_t & nrb, i
     }
     kh = force_kh == 1 || (force_kh != 0 && mf_smem_bytes<NC, false>(16, nsb, 2) > lim);
     if (kh && (nsb < 8 || (!allow_kh && force_kh != 1))) kh = false;
+    if (kh) D = 2;                                            // the K-halves waits assume it
     auto bytes = [&]() { return kh ? mf_smem_bytes<NC, true>(nrb, nsb, D) : mf_smem_bytes<NC, false>(nrb, nsb, D); };
     while (bytes() > lim && nrb > 16) nrb -= 16;
     while (bytes() > lim && D > 2) --D;
@@ -602,7 +682,7 @@ static int mf_launch(const DotArgs & a, hipStream_t s) {
     bool kh;
     size_t smb;
     if (mf_plan_kh<NC>(a.rows, nsb, G, nrb, D, kh, smb)) return FLH_ERR_UNSUPPORTED;
-    if (kh) return D == 2 ? mf_launch_d<NC, 2, true>(a, nrb, G, smb, s) : mf_launch_d<NC, 3, true>(a, nrb, G, smb, s);
+    if (kh) return mf_launch_d<NC, 2, true>(a, nrb, G, smb, s);
     return D == 2 ? mf_launch_d<NC, 2, false>(a, nrb, G, smb, s) : mf_launch_d<NC, 3, false>(a, nrb, G, smb, s);
 }
 
@@ -640,7 +720,7 @@ static int mf_moe_launch(const MoeArgs & a, hipStream_t s, bool allow_kh) {
     bool kh;
     size_t smb;
     if (mf_plan_kh<NC>(a.rows, nsb, gx, nrb, D, kh, smb, allow_kh)) return FLH_ERR_UNSUPPORTED;
-    if (kh) return D == 2 ? mf_moe_launch_d<NC, 2, true>(a, nrb, gx, smb, s) : mf_moe_launch_d<NC, 3, true>(a, nrb, gx, smb, s);
+    if (kh) return mf_moe_launch_d<NC, 2, true>(a, nrb, gx, smb, s);
     return D == 2 ? mf_moe_launch_d<NC, 2, false>(a, nrb, gx, smb, s) : mf_moe_launch_d<NC, 3, false>(a, nrb, gx, smb, s);
 }
 
