@@ -304,8 +304,8 @@ def traffic_from_profile():
 
 
 def bench_moe(flh, B, s, staging):
-    """Mixtral-style MoE FFN: router -> grouped gate/up -> silu*up + ACT_Q8 (one
-    fused launch) -> grouped down -> weighted merge.  Two copies of the expert
+    """Mixtral-style MoE FFN: router + grouped gate/up (one launch) -> silu*up +
+    ACT_Q8 (one launch) -> grouped down -> weighted merge.  Two copies of the expert
     set alternate."""
     E, K, D, F = 8, 2, 4096, 14336
     gu_b = 2 * F * flh.row_bytes(Q4_K, D)
@@ -335,8 +335,9 @@ def bench_moe(flh, B, s, staging):
 
         def issue(i):
             c = i % copies
-            flh.router_sel(lbufs[c], ntok, E, K, 1, 1.0, ids, gates, s)
-            flh.moe_dot(Q4_K, gu[c], gu_b, 2 * F, D, ids, ntok, K, E, x, stD, False, ygu, 2 * F, s)
+            # router + grouped gate/up in one launch (same bits as router_sel, moe_dot)
+            flh.router_moe_dot(Q4_K, gu[c], gu_b, 2 * F, D, lbufs[c], ntok, E, K, 1, 1.0, ids, gates, x, stD,
+                               False, ygu, 2 * F, s)
             flh.silu_mul_act_q8(ygu, ygu.ptr + F * 4, h, F, ntok * K, 2 * F, stF, s)
             flh.moe_dot(Q4_K, dn[c], dn_b, D, F, ids, ntok, K, E, h, stF, True, ydn, D, s)
             flh.wmerge(ydn, gates, None, None, yo, 1.0, K, D, 0, ntok, K * D, D, s)

@@ -178,6 +178,8 @@ _SIGS = {
     "flh_moe_dot": (_I, [_I, _P, _U64, _U32, _U32, _P, _U32, _U32, _U32, _P, _U32, _U32, _P,
                          _U32, _P]),
     "flh_router_sel": (_I, [_P, _U32, _U32, _U32, _U32, _F, _P, _P, _P]),
+    "flh_router_moe_dot": (_I, [_I, _P, _U64, _U32, _U32, _P, _U32, _U32, _U32, _U32, _F, _P, _P, _P,
+                                _U32, _U32, _P, _U32, _P]),
     "flh_silu_mul": (_I, [_P, _P, _P, _U32, _U32, _U32, _U32, _P]),
     "flh_silu_mul_act_q8": (_I, [_P, _P, _P, _U32, _U32, _U32, _U32, _P]),
     "flh_wmerge": (_I, [_P, _P, _P, _P, _P, _F, _U32, _U32, _U32, _U32, _U32, _U32, _P]),
@@ -411,6 +413,15 @@ def moe_dot(fmt: int, w, estride: int, rows: int, cols: int, ids, ntok: int, top
     check(lib().flh_moe_dot(int(fmt), _p(w), estride, rows, cols, _p(ids), ntok, top_k,
                             n_expert, _p(x), xstride, int(bool(x_per_slot)), _p(y), ystride,
                             stream.handle))
+
+
+def router_moe_dot(fmt: int, w, estride: int, rows: int, cols: int, logits, ntok: int, n_expert: int,
+                   top_k: int, norm: int, scale: float, ids, gates, x, xstride: int, x_per_slot: bool, y,
+                   ystride: int, stream: Stream) -> None:
+    """ROUTER_SEL + grouped expert matvec in one launch (same bits as router_sel then moe_dot)."""
+    check(lib().flh_router_moe_dot(int(fmt), _p(w), estride, rows, cols, _p(logits), ntok, n_expert, top_k,
+                                   norm, scale, _p(ids), _p(gates), _p(x), xstride, int(bool(x_per_slot)),
+                                   _p(y), ystride, stream.handle))
 
 
 def router_sel(logits, ntok, n_expert, top_k, norm, scale, ids, gates, stream: Stream):

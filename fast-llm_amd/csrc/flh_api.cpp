@@ -419,6 +419,37 @@ int flh_moe_dot(int fmt, const void * w, uint64_t estride, uint32_t rows, uint32
     return launch_moe_i8k(fmt, a, (hipStream_t)stream);
 }
 
+int flh_router_moe_dot(int fmt, const void * w, uint64_t estride, uint32_t rows, uint32_t cols,
+                       const float * logits, uint32_t ntok, uint32_t n_expert, uint32_t top_k, uint32_t norm,
+                       float scale, uint32_t * ids, float * gates, const float * x, uint32_t xstride,
+                       uint32_t x_per_slot, float * y, uint32_t ystride, void * stream) {
+    if (int rc = need_init()) return rc;
+    if (fmt != FLH_FMT_Q4_K && fmt != FLH_FMT_Q6_K)
+        return set_error(FLH_ERR_UNSUPPORTED, "router_moe_dot: K formats (q8_K path) only");
+    if (cols % 256) return set_error(FLH_ERR_ARG, "router_moe_dot: cols not a multiple of 256");
+    if (!w || !logits || !ids || !gates || !x || !y || n_expert == 0 || top_k == 0 || top_k > n_expert)
+        return set_error(FLH_ERR_ARG, "router_moe_dot: null argument or top_k outside 1..n_expert");
+    if (estride < (uint64_t)rows * flh_row_bytes(fmt, cols) || (estride & 3) || ((uintptr_t)w & 3))
+        return set_error(FLH_ERR_ARG, "router_moe_dot: expert stride smaller than one expert or misaligned");
+    if (ntok == 0) return FLH_OK;
+    hipStream_t s = (hipStream_t)stream;
+    MoeArgs a{(const uint8_t *)w, estride, ids, x, y, rows, cols, ntok, top_k, n_expert, xstride, ystride,
+              x_per_slot};
+    // routing inside the grouped kernels (one launch) where they take it
+    if (n_expert <= 64 && top_k <= 8 && ntok * top_k <= 256) {
+        MoeArgs f = a;
+        f.rt_logits = logits;
+        f.rt_norm = norm;
+        f.rt_scale = scale;
+        f.rt_gates = gates;
+        int rc = launch_moe_mfma(fmt, f, s);
+        if (rc == FLH_ERR_UNSUPPORTED) rc = launch_moe_kstream(fmt, f, s);
+        if (rc != FLH_ERR_UNSUPPORTED) return rc;
+    }
+    if (int rc = launch_router_sel(logits, ntok, n_expert, top_k, norm, scale, ids, gates, s)) return rc;
+    return launch_moe_i8k(fmt, a, s);
+}
+
 int flh_router_sel(const float * logits, uint32_t ntok, uint32_t n_expert, uint32_t top_k, uint32_t norm,
                    float scale, uint32_t * ids, float * gates, void * stream) {
     if (int rc = need_init()) return rc;

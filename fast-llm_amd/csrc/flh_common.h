@@ -146,4 +146,52 @@ __device__ __forceinline__ int iq_val(int fmt, const uint8_t * b, int ib, uint32
     return (s >> j) & 1u ? -v : v;
 }
 
+// ROUTER_SEL of one token by one wave (n_expert <= 64, top_k <= 8): lane i
+// owns logit i; the same float operations in the same order as
+// fl_op_router_sel (src/runtime/decode_params.h:234-265): max in ascending
+// expert order (first strictly greater wins); expf; sum in ascending order;
+// divide; top-k by first maximum; optional renormalisation by the sum of the
+// chosen weights; scale.  Lane 0 writes ids[0..top_k) and, when gates is not
+// null, gates[0..top_k) (generic pointers: global or LDS).
+__device__ __forceinline__ void router_token_wave(const float * lg, uint32_t n_expert, uint32_t top_k,
+                                                  uint32_t norm, float scale, uint32_t lane, uint32_t * ids,
+                                                  float * gates) {
+    const float l = lane < n_expert ? lg[lane] : 0.f;
+    float mx = -1e30f;
+    for (uint32_t i = 0; i < n_expert; ++i) {
+        const float li = __shfl(l, (int)i);
+        if (li > mx) mx = li;
+    }
+    float w = lane < n_expert ? expf(l - mx) : 0.f;
+    float sum = 0.f;
+    for (uint32_t i = 0; i < n_expert; ++i) sum += __shfl(w, (int)i);
+    w /= sum;
+    bool taken = lane >= n_expert;
+    float tsum = 0.f;
+    uint32_t id_k[8];
+    float gt_k[8];
+    for (uint32_t k = 0; k < top_k; ++k) {
+        // first lane holding the largest untaken weight (strict >, ascending)
+        float bw = -1.f;
+        uint32_t best = 0;
+        for (uint32_t i = 0; i < n_expert; ++i) {
+            const float wi = __shfl(w, (int)i);
+            const bool ti = __shfl((int)taken, (int)i) != 0;
+            if (!ti && wi > bw) { bw = wi; best = i; }
+        }
+        if (lane == best) taken = true;
+        if (k < 8) { id_k[k] = best; gt_k[k] = bw; }
+        tsum += bw;
+    }
+    if (lane == 0) {
+        for (uint32_t k = 0; k < top_k && k < 8; ++k) {
+            float g = gt_k[k];
+            if (norm) g /= tsum;
+            g *= scale;
+            ids[k] = id_k[k];
+            if (gates) gates[k] = g;
+        }
+    }
+}
+
 }  // namespace flh

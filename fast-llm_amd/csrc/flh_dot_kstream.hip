@@ -206,7 +206,7 @@ __global__ __launch_bounds__(256) void k_dot_kstream(DotArgs a, uint32_t nr) {
     ks_body<FMT, NX, D, FUSE, XREG>(w, a.rows, a.cols, C, a.nx, nr, blockIdx.x, gridDim.x, sm);
 }
 
-// Grouped expert matvec: blockIdx.y = expert.  The workgroup collects the
+// Grouped expert matvec: blockIdx.y = the y-th routed expert.  The workgroup collects the
 // routed (token, slot) pairs of its expert and streams that expert's weights
 // once per group of NX pairs; with no pair routed to it, it exits before any
 // weight byte is requested.
@@ -214,12 +214,15 @@ template <int FMT, int NX, int D, bool XREG>
 __global__ __launch_bounds__(256) void k_moe_kstream(MoeArgs a, uint32_t nr) {
     extern __shared__ __attribute__((aligned(16))) uint8_t sm[];
     __shared__ uint32_t pairs[256];
+    __shared__ uint32_t rids[256];
     __shared__ uint32_t npairs;
-    const uint32_t e = blockIdx.y;
+    const uint32_t * ids = moe_route(a, rids);
+    const uint32_t e = moe_jth_expert(ids, a.ntok * a.top_k, a.n_expert, blockIdx.y);
+    if (e >= a.n_expert) return;
     if (threadIdx.x == 0) {
         uint32_t n = 0;
         for (uint32_t i = 0; i < a.ntok * a.top_k && n < 256; ++i)
-            if (a.ids[i] == e) pairs[n++] = i;                    // i = tok * top_k + slot
+            if (ids[i] == e) pairs[n++] = i;                      // i = tok * top_k + slot
         npairs = n;
     }
     __syncthreads();
@@ -331,7 +334,8 @@ static int ks_launch(const DotArgs & a, hipStream_t s) {
 
 template <int FMT, int NX, int D, bool XREG>
 static int moe_launch_x(const MoeArgs & a, uint32_t nr, uint32_t gx, size_t smb, hipStream_t s) {
-    hipLaunchKernelGGL((k_moe_kstream<FMT, NX, D, XREG>), dim3(gx, a.n_expert), dim3(256), smb, s, a, nr | (ks_pro() << 16));
+    if (moe_rows(a) == 0) return FLH_OK;
+    hipLaunchKernelGGL((k_moe_kstream<FMT, NX, D, XREG>), dim3(gx, moe_rows(a)), dim3(256), smb, s, a, nr | (ks_pro() << 16));
     return hip_check(hipGetLastError(), "k_moe_kstream launch");
 }
 template <int FMT, int NX, int D>

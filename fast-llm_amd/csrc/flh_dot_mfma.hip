@@ -573,7 +573,7 @@ __global__ __launch_bounds__(512) void k_dot_mfma(DotArgs a, uint32_t nrb) {
     mf_body<NC, D, KH>(w, a.rows, a.cols, C, a.nx, nrb, blockIdx.x, gridDim.x, sm);
 }
 
-// Grouped expert matvec (MoE): blockIdx.y = expert e.  The workgroup collects
+// Grouped expert matvec (MoE): blockIdx.y = the y-th routed expert e.  The workgroup collects
 // the (token, slot) pairs routed to e and streams e's weights once per group
 // of NC pairs (the columns); with no pair routed to e it exits before any
 // weight byte is requested.  Column p's activation index and output index
@@ -594,12 +594,15 @@ __global__ __launch_bounds__(512) void k_moe_mfma(MoeArgs a, uint32_t nrbp) {
     __shared__ uint32_t pairs[256];
     __shared__ uint32_t npairs;
     __shared__ uint32_t cxi[NC], cyi[NC];
-    const uint32_t e = blockIdx.y, tid = threadIdx.x;
+    const uint32_t tid = threadIdx.x;
+    __shared__ uint32_t rids[256];
     if (tid == 0) npairs = 0;
-    __syncthreads();
+    const uint32_t * ids = moe_route(a, rids);
+    const uint32_t e = moe_jth_expert(ids, a.ntok * a.top_k, a.n_expert, blockIdx.y);   // (barriers)
+    if (e >= a.n_expert) return;
     // pairs i = tok * top_k + slot routed to e (order free: every column's
     // output is computed independently)
-    if (tid < a.ntok * a.top_k && a.ids[tid] == e) pairs[atomicAdd(&npairs, 1u)] = tid;
+    if (tid < a.ntok * a.top_k && ids[tid] == e) pairs[atomicAdd(&npairs, 1u)] = tid;
     __syncthreads();
     const uint32_t np = npairs;
     const uint8_t * w = a.w + (size_t)e * a.estride;
@@ -645,7 +648,7 @@ size_t lds_limit();
 template <int NC>
 static int mf_plan_kh(uint32_t rows, uint32_t nsb, uint32_t G, uint32_t & nrb, int & D, bool & kh, size_t & smb,
                       bool allow_kh = true) {
-    const size_t lim = lds_limit();
+    const size_t lim = lds_limit() - 4096;                    // the MoE kernel's static tables
     const uint32_t rpw = (rows + G - 1) / G;
     // a batch's old y values are one 64-float DMA per wave: nrb * NC <= 512
     nrb = ((rpw + 15) / 16) * 16;
@@ -701,8 +704,9 @@ uint32_t mfma_min_cols(uint32_t cols);
 
 template <int NC, int D, bool KH>
 static int mf_moe_launch_d(const MoeArgs & a, uint32_t nrb, uint32_t gx, size_t smb, hipStream_t s) {
+    if (moe_rows(a) == 0) return FLH_OK;
     (void)hipFuncSetAttribute((const void *)k_moe_mfma<NC, D, KH>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smb);
-    hipLaunchKernelGGL((k_moe_mfma<NC, D, KH>), dim3(gx, a.n_expert), dim3(MF_WAVES * 64), smb, s, a,
+    hipLaunchKernelGGL((k_moe_mfma<NC, D, KH>), dim3(gx, moe_rows(a)), dim3(MF_WAVES * 64), smb, s, a,
                        nrb | (mf_pro() << 16));
     return hip_check(hipGetLastError(), "k_moe_mfma launch");
 }

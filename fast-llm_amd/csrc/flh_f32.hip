@@ -349,52 +349,13 @@ __global__ void k_router_sel(const float * logits, uint32_t ntok, uint32_t n_exp
     }
 }
 
-// One wave per token (n_expert <= 64): lane i owns logit i; the same float
-// operations in the same order as k_router_sel / fl_op_router_sel (max; expf;
-// sum in ascending expert order; divide; top-k by first maximum; optional
-// renormalisation by the sum of the chosen weights; scale), without the
-// per-thread stack array.
+// One wave per token (n_expert <= 64, top_k <= 8): router_token_wave, the
+// per-token form also run inside the fused router + grouped expert matvec.
 __global__ __launch_bounds__(64) void k_router_wave(const float * logits, uint32_t n_expert, uint32_t top_k,
                                                     uint32_t norm, float scale, uint32_t * ids, float * gates) {
-    const uint32_t t = blockIdx.x, lane = threadIdx.x;
-    const float * lg = logits + (size_t)t * n_expert;
-    const float l = lane < n_expert ? lg[lane] : 0.f;
-    // max in ascending order (as the scalar loop: first strictly greater value wins)
-    float mx = -1e30f;
-    for (uint32_t i = 0; i < n_expert; ++i) {
-        const float li = __shfl(l, (int)i);
-        if (li > mx) mx = li;
-    }
-    float w = lane < n_expert ? expf(l - mx) : 0.f;
-    float sum = 0.f;
-    for (uint32_t i = 0; i < n_expert; ++i) sum += __shfl(w, (int)i);
-    w /= sum;
-    bool taken = lane >= n_expert;
-    float tsum = 0.f;
-    uint32_t id_k[8];
-    float gt_k[8];
-    for (uint32_t k = 0; k < top_k; ++k) {
-        // first lane holding the largest untaken weight (strict >, ascending)
-        float bw = -1.f;
-        uint32_t best = 0;
-        for (uint32_t i = 0; i < n_expert; ++i) {
-            const float wi = __shfl(w, (int)i);
-            const bool ti = __shfl((int)taken, (int)i) != 0;
-            if (!ti && wi > bw) { bw = wi; best = i; }
-        }
-        if (lane == best) taken = true;
-        if (k < 8) { id_k[k] = best; gt_k[k] = bw; }
-        tsum += bw;
-    }
-    if (lane == 0) {
-        for (uint32_t k = 0; k < top_k && k < 8; ++k) {
-            float g = gt_k[k];
-            if (norm) g /= tsum;
-            g *= scale;
-            ids[(size_t)t * top_k + k] = id_k[k];
-            gates[(size_t)t * top_k + k] = g;
-        }
-    }
+    const uint32_t t = blockIdx.x;
+    router_token_wave(logits + (size_t)t * n_expert, n_expert, top_k, norm, scale, threadIdx.x,
+                      ids + (size_t)t * top_k, gates + (size_t)t * top_k);
 }
 
 __global__ void k_silu_mul(const float * gate, const float * up, float * h, uint32_t n,

@@ -32,9 +32,22 @@ struct MoeArgs {
     const float * x;
     float * y;
     uint32_t rows, cols, ntok, top_k, n_expert, xstride, ystride, x_per_slot;
+    // fused ROUTER_SEL (rt_logits not null; n_expert <= 64, top_k <= 8,
+    // ntok * top_k <= 256): every workgroup routes the tokens itself, and
+    // workgroup (0, 0) also writes ids (the ids field) and rt_gates
+    const float * rt_logits = nullptr;
+    uint32_t rt_norm = 0;
+    float rt_scale = 1.f;
+    float * rt_gates = nullptr;
 };
 
 int num_cus();
+
+// grid rows of a grouped expert matvec: the experts that can be active
+inline uint32_t moe_rows(const MoeArgs & a) {
+    const uint32_t pairs = a.ntok * a.top_k;
+    return pairs < a.n_expert ? pairs : a.n_expert;
+}
 
 // Each returns hipSuccess-style 0 or a negative flh error code.
 int launch_act_q8(float * x, void * y_q81, uint32_t cols, uint32_t nx,

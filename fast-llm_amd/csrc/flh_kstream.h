@@ -16,6 +16,7 @@
 // re-laid in LDS as 80-byte per-lane records (64 int8 + 4 int32 block sums).
 #pragma once
 #include "flh_common.h"
+#include "flh_internal.h"
 
 namespace flh {
 
@@ -686,6 +687,57 @@ __device__ __forceinline__ void act_q8_lanes(const float (&v)[4], uint32_t lane,
         if ((lane & 3) == 0) *(int16_t *)(o + 4 + 2 * (lane >> 2)) = (int16_t)s;
         if (lane == 0) *(float *)o = d;
     }
+}
+
+// Expert ids of the ntok * top_k routed pairs for a grouped expert matvec:
+// a.ids, or with a fused ROUTER_SEL (a.rt_logits) the ids this workgroup
+// computes into rids (LDS, ntok * top_k entries), one wave per token;
+// workgroup (0, 0) also publishes ids and gates.  Contains a barrier.
+__device__ __forceinline__ const uint32_t * moe_route(const MoeArgs & a, uint32_t * rids) {
+    if (!a.rt_logits) return a.ids;
+    const uint32_t lane = threadIdx.x & 63, nw = blockDim.x >> 6;
+    const bool pub = blockIdx.x == 0 && blockIdx.y == 0;
+    for (uint32_t t = threadIdx.x >> 6; t < a.ntok; t += nw)
+        router_token_wave(a.rt_logits + (size_t)t * a.n_expert, a.n_expert, a.top_k, a.rt_norm, a.rt_scale, lane,
+                          rids + (size_t)t * a.top_k, pub ? a.rt_gates + (size_t)t * a.top_k : nullptr);
+    __syncthreads();
+    if (pub)
+        for (uint32_t i = threadIdx.x; i < a.ntok * a.top_k; i += blockDim.x) ((uint32_t *)a.ids)[i] = rids[i];
+    return rids;
+}
+
+// Expert of grouped-matvec row j of the grid (blockIdx.y): the j-th smallest
+// distinct id among the nids routed pairs, or n_expert when fewer experts are
+// routed (the workgroup then has nothing to do).  The grid holds only as many
+// rows as experts can be active, so no workgroup waits for a CU only to find
+// its expert unrouted.  Contains barriers.
+__device__ __forceinline__ uint32_t moe_jth_expert(const uint32_t * ids, uint32_t nids, uint32_t n_expert,
+                                                   uint32_t j) {
+    __shared__ uint32_t em[8];
+    __shared__ uint32_t pick;
+    if (threadIdx.x < 8) em[threadIdx.x] = 0u;
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < nids; i += blockDim.x) {
+        const uint32_t e = ids[i];
+        if (e < n_expert && e < 256) atomicOr(&em[e >> 5], 1u << (e & 31));
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t k = j, r = n_expert;
+        for (uint32_t w = 0; w < 8 && r == n_expert; ++w) {
+            uint32_t m = em[w];
+            const uint32_t c = (uint32_t)__popc(m);
+            if (k < c) {
+                for (; k; --k) m &= m - 1;
+                r = 32 * w + (uint32_t)__ffs(m) - 1;
+            } else {
+                k -= c;
+            }
+        }
+        pick = r;
+    }
+    __syncthreads();
+    return pick;
 }
 
 }  // namespace flh

@@ -240,6 +240,19 @@ int flh_moe_dot(int fmt, const void * w, uint64_t estride, uint32_t rows,
 int flh_router_sel(const float * logits, uint32_t ntok, uint32_t n_expert,
                    uint32_t top_k, uint32_t norm, float scale, uint32_t * ids,
                    float * gates, void * stream);
+/* ROUTER_SEL followed by the grouped expert matvec of its routing, as one
+ * launch where the grouped kernels take it (n_expert <= 64, top_k <= 8,
+ * ntok*top_k <= 256; otherwise two): every workgroup routes the ntok tokens
+ * itself with the same float operations as flh_router_sel, one of them
+ * writes ids and gates.  Outputs (ids, gates, y) equal flh_router_sel then
+ * flh_moe_dot bit for bit.  Replaces the ROUTER_SEL task
+ * (src/runtime/decode_params.h:234-265) and the STREAM_DOT_IDX expert tiles
+ * it feeds (src/model/decoder.cpp:941-996) for one MoE layer. */
+int flh_router_moe_dot(int fmt, const void * w, uint64_t estride, uint32_t rows,
+                       uint32_t cols, const float * logits, uint32_t ntok,
+                       uint32_t n_expert, uint32_t top_k, uint32_t norm, float scale,
+                       uint32_t * ids, float * gates, const float * x, uint32_t xstride,
+                       uint32_t x_per_slot, float * y, uint32_t ystride, void * stream);
 /* SILU_MUL over ncol columns (fl_op_silu_mul, decode_params.h:267-272):
  * h[c*hstride + i] = silu(g[c*gstride + i]) * u[c*gstride + i]. */
 int flh_silu_mul(const float * gate, const float * up, float * h, uint32_t n,

@@ -223,3 +223,47 @@ def test_router_ties_and_widths(flh, orc, gpu, E, K, norm):
         wi, wg = orc.router_sel(lg[t], K, norm=norm)
         assert list(ids[t]) == list(wi)
         assert np.allclose(g[t], wg, rtol=2e-6, atol=0)
+
+
+@pytest.mark.parametrize("fmt,ntok,rows,cols,per_slot,norm,E,K", [
+    (Q4_K, 1, 1024, 4096, False, 1, 8, 2), (Q4_K, 8, 512, 4096, False, 1, 8, 2),
+    (Q4_K, 8, 256, 14336, True, 0, 8, 2), (Q6_K, 3, 300, 2048, False, 1, 8, 2),
+    (Q4_K, 5, 128, 1024, False, 1, 64, 8), (Q6_K, 32, 64, 512, True, 1, 16, 8),
+])
+def test_router_moe_dot_fused_equals_separate(flh, gpu, fmt, ntok, rows, cols, per_slot, norm, E, K):
+    """flh_router_moe_dot (routing inside the grouped kernels) writes the ids,
+    gates and y of flh_router_sel followed by flh_moe_dot, bit for bit, incl.
+    tied logits (lowest id wins), 64 experts and top-8."""
+    say("router+moe", fmt, ntok, rows, cols, per_slot, norm, E, K)
+    rng = np.random.default_rng(ntok * 7 + rows + cols + E)
+    logits = rng.standard_normal((ntok, E)).astype(np.float32)
+    logits[0, 1] = logits[0, 3] = np.max(logits[0]) + 0.5            # a tie for the top weight
+    rb = row_bytes(fmt, cols)
+    estride = rows * rb
+    w = sane_rows(fmt, rows * E, cols, rng)
+    nx = ntok * K if per_slot else ntok
+    xs = activations(nx, cols, rng, outliers=True)
+    st = col_stride_floats(cols)
+    buf = np.zeros(nx * st, dtype=np.float32)
+    for p in range(nx):
+        buf[p * st:p * st + cols] = xs[p]
+    dx = flh.DeviceBuffer.from_array(buf, gpu)
+    flh.act_q8(dx, cols, gpu, nx=nx, xstride=st)
+    dw = flh.DeviceBuffer.from_array(w, gpu)
+    dl = flh.DeviceBuffer.from_array(logits, gpu)
+    y0 = rng.standard_normal(ntok * K * rows).astype(np.float32)
+    outs = []
+    for fused in (False, True):
+        di, dg = flh.DeviceBuffer(4 * ntok * K), flh.DeviceBuffer(4 * ntok * K)
+        dy = flh.DeviceBuffer.from_array(y0, gpu)
+        if fused:
+            flh.router_moe_dot(fmt, dw, estride, rows, cols, dl, ntok, E, K, norm, 0.75, di, dg, dx, st,
+                               per_slot, dy, rows, gpu)
+        else:
+            flh.router_sel(dl, ntok, E, K, norm, 0.75, di, dg, gpu)
+            flh.moe_dot(fmt, dw, estride, rows, cols, di, ntok, K, E, dx, st, per_slot, dy, rows, gpu)
+        outs.append((di.download(np.uint32, ntok * K, gpu), bits(dg.download(np.float32, ntok * K, gpu)),
+                     bits(dy.download(np.float32, y0.size, gpu))))
+    assert list(outs[0][0][:2]) == [1, 3]                               # tie -> lower id first
+    for a, b in zip(outs[0], outs[1]):
+        assert np.array_equal(a, b)
