@@ -235,15 +235,14 @@ __device__ __forceinline__ float ks_absmax16(const u32x4a (&raw)[4]) {
 
 // ACT_Q8 fused into the dot: quantise the fp32 columns into the records
 // (16 lanes per superblock, each lane one 16-element run).  When write_app,
-// also write both appendices so the bytes in memory equal ACT_Q8's.  The
-// superblock absmax is an LDS atomic max over the lanes' partial maxima (bit
-// patterns of non-negative floats order like the floats).  after_loads() runs
+// also write both appendices so the bytes in memory equal ACT_Q8's.  A
+// superblock's 16 runs sit in 16 consecutive lanes of one wave, so its absmax
+// is a 4-step shuffle max (order-free), with no barrier.  after_loads() runs
 // once, right after the first activation loads are issued (the caller issues
 // its weight prologue there, behind the older activation loads).
 template <int FMT, int NX, typename F>
 __device__ __forceinline__ void ks_x_fuse(const KsCols<NX> & C, uint32_t nx, uint32_t nsb, uint32_t cols,
                                           uint8_t * xr, float * xd, bool write_app, F && after_loads) {
-    __shared__ uint32_t amx[64];
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t nitem = nx * nsb;
@@ -267,18 +266,23 @@ __device__ __forceinline__ void ks_x_fuse(const KsCols<NX> & C, uint32_t nx, uin
             after_loads();
             issued = true;
         }
-        if (tid < 64) lds_st32(&amx[tid], 0u);
-        lds_barrier();
+        // superblock absmax: its 16 runs are 16 consecutive lanes of this wave
+        float amq[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-            if ((uint32_t)q < nq) lds_max32(&amx[16 * q + 4 * wave + sub], __float_as_uint(ks_absmax16(raw[q])));
-        lds_barrier();
+        for (int q = 0; q < 4; ++q) {
+            if ((uint32_t)q >= nq) break;                   // wave-uniform
+            float m = ks_absmax16(raw[q]);
+            m = fmaxf(m, __shfl_xor(m, 1));
+            m = fmaxf(m, __shfl_xor(m, 2));
+            m = fmaxf(m, __shfl_xor(m, 4));
+            amq[q] = fmaxf(m, __shfl_xor(m, 8));
+        }
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const uint32_t i = base + 16 * q + 4 * wave + sub;
             if ((uint32_t)q < nq && i < nitem) {
                 const uint32_t p = i / nsb, sb = i % nsb;
-                const float amax = __uint_as_float(lds_ld32(&amx[16 * q + 4 * wave + sub]));
+                const float amax = amq[q];
                 const float d = amax / 127.f;
                 const float id = amax > 0.f ? 127.f / amax : 0.f;
                 uint32_t pk[4];
@@ -315,7 +319,6 @@ __device__ __forceinline__ void ks_x_fuse(const KsCols<NX> & C, uint32_t nx, uin
                 }
             }
         }
-        lds_barrier();
     }
     if (!issued) after_loads();
     // columns p >= nx of the template width read zero records
