@@ -8,7 +8,7 @@
 //
 // Work unit: a CHUNK of 16 consecutive superblocks of the row-major matrix
 // (rows are contiguous, so a chunk may straddle a row boundary).  A workgroup
-// (4 waves) owns a batch of nr whole rows; its chunks are dealt round-robin
+// (4 or 8 waves) owns a batch of nr whole rows; its chunks are dealt round-robin
 // to the waves, each wave keeping D chunks in flight in a private LDS ring.
 // Lane (slot s = lane/4, part c = lane%4) of a wave handles superblock s of
 // the chunk, quarter c, exactly as in flh_dot_int8.hip: integer partials,
@@ -47,7 +47,7 @@ __device__ uint64_t g_ks_trace[8192 * 6];
 // even split: workgroups differ by at most one row), streamed in batches of at
 // most nr rows.  Ends with every weight DMA
 // drained, so the caller may start another pass on the same LDS.
-template <int FMT, int NX, int D, bool FUSE, bool XREG>
+template <int FMT, int NX, int D, bool FUSE, bool XREG, int KW = 4>
 __device__ __forceinline__ void ks_body(const uint8_t * __restrict__ w, uint32_t rows, uint32_t cols,
                                         const KsCols<NX> & C, uint32_t nx, uint32_t nrp,
                                         uint32_t g, uint32_t G, uint8_t * sm) {
@@ -64,7 +64,7 @@ __device__ __forceinline__ void ks_body(const uint8_t * __restrict__ w, uint32_t
     const uint32_t s = lane >> 2, c = lane & 3;
 
     uint8_t * stages = sm;                                        // [4][D][WIN]
-    uint8_t * xr = sm + (size_t)4 * D * WIN;                      // [NX][nsb][4][80]
+    uint8_t * xr = sm + (size_t)KW * D * WIN;                     // [NX][nsb][4][80]
     constexpr uint32_t TPS = ks_tps<FMT>();                      // fold terms per superblock
     float * xd = (float *)(xr + (size_t)NX * nsb * 4 * XREC);     // [NX][nsb * TPS]
     int * TI = (int *)(xd + (size_t)NX * nsb * TPS);              // [nr][NX][nsb * TPS]
@@ -80,7 +80,7 @@ __device__ __forceinline__ void ks_body(const uint8_t * __restrict__ w, uint32_t
     auto nci_of = [&](uint32_t bt) -> uint32_t {                  // this wave's chunks in batch bt
         const uint32_t nrow = min(nr, rend - rbeg - bt * nr);
         const uint32_t nch = (nrow * nsb + 15) / 16;
-        return nch > wave ? (nch - wave + 3) / 4 : 0;
+        return nch > wave ? (nch - wave + KW - 1) / KW : 0;
     };
     // Issue cursor over this wave's chunk sequence (batches blockIdx.x, +G, ...).
     // nissued counts the chunks whose DMA was issued; past the end of the
@@ -96,7 +96,7 @@ __device__ __forceinline__ void ks_body(const uint8_t * __restrict__ w, uint32_t
             qn = qbt < nbatch ? nci_of(qbt) : 0;
         }
         if (qbt < nbatch) {
-            ks_issue<FMT>(w + (size_t)(rbeg + qbt * nr) * rb, wave + 4 * qci, min(nr, rend - rbeg - qbt * nr) * nsb,
+            ks_issue<FMT>(w + (size_t)(rbeg + qbt * nr) * rb, wave + KW * qci, min(nr, rend - rbeg - qbt * nr) * nsb,
                           stage, lane);
             ++qci;
             ++nissued;
@@ -129,7 +129,7 @@ __device__ __forceinline__ void ks_body(const uint8_t * __restrict__ w, uint32_t
     issue_y(0);
 
     // ---- activation records, once per workgroup (overlaps the first weight DMAs)
-    if constexpr (FUSE) ks_x_fuse<FMT, NX>(C, nx, nsb, cols, xr, xd, g == 0, prologue);
+    if constexpr (FUSE) ks_x_fuse<FMT, NX, KW>(C, nx, nsb, cols, xr, xd, g == 0, prologue);
     else ks_x_app<FMT, NX>(C, nx, nsb, cols, xr, xd, prologue);
     lds_barrier();
     KS_STAMP(1);
@@ -160,14 +160,14 @@ __device__ __forceinline__ void ks_body(const uint8_t * __restrict__ w, uint32_t
             ++ncons;
             if (i == 0 && bt == 0) KS_STAMP(2);
             uint8_t * st = myst + slot * WIN;
-            const uint32_t f = (wave + 4 * i) * 16 + s;            // batch-local superblock
+            const uint32_t f = (wave + KW * i) * 16 + s;           // batch-local superblock
             const bool act = f < nsbb;
             const uint32_t ff = act ? f : nsbb - 1;
             const uint32_t rl = __umulhi(ff, magic);
             const uint32_t sb = ff - rl * nsb;
             int ia[NX], im[NX];
             uint32_t tag;
-            const uint32_t mis = (uint32_t)(((uintptr_t)(wb + (size_t)(wave + 4 * i) * 16 * B)) & 15u);
+            const uint32_t mis = (uint32_t)(((uintptr_t)(wb + (size_t)(wave + KW * i) * 16 * B)) & 15u);
             ks_chunk<FMT, NX, XREG>(st, mis, s, c, xr + ((size_t)sb * 4 + c) * XREC, nsb, xregs, ia, im, tag);
             // all reads of this stage are done before it is refilled
             WAIT_LGKM0();
@@ -192,8 +192,8 @@ __device__ __forceinline__ void ks_body(const uint8_t * __restrict__ w, uint32_t
     KS_STAMP(4);
 }
 
-template <int FMT, int NX, int D, bool FUSE, bool XREG>
-__global__ __launch_bounds__(256) void k_dot_kstream(DotArgs a, uint32_t nr) {
+template <int FMT, int NX, int D, bool FUSE, bool XREG, int KW = 4>
+__global__ __launch_bounds__(64 * KW) void k_dot_kstream(DotArgs a, uint32_t nr) {
     extern __shared__ __attribute__((aligned(16))) uint8_t sm[];
     const uint8_t * w = a.w + (a.id_slot ? (size_t)(*a.id_slot) * a.estride : 0);
     KsCols<NX> C;
@@ -203,7 +203,7 @@ __global__ __launch_bounds__(256) void k_dot_kstream(DotArgs a, uint32_t nr) {
         C.x[p] = a.x + (size_t)pp * a.xstride;
         C.y[p] = a.y + (size_t)pp * a.ystride;
     }
-    ks_body<FMT, NX, D, FUSE, XREG>(w, a.rows, a.cols, C, a.nx, nr, blockIdx.x, gridDim.x, sm);
+    ks_body<FMT, NX, D, FUSE, XREG, KW>(w, a.rows, a.cols, C, a.nx, nr, blockIdx.x, gridDim.x, sm);
 }
 
 // Grouped expert matvec: blockIdx.y = the y-th routed expert.  The workgroup collects the
@@ -297,21 +297,22 @@ static int ks_launch_d(const DotArgs & a, uint32_t nr, uint32_t grid, size_t smb
 // batch first, then the ring depth; FLH_ERR_UNSUPPORTED if it cannot fit.
 template <int FMT>
 static int ks_plan(uint32_t rows, uint32_t nx_t, uint32_t nsb, uint32_t slots, int Ddef,
-                   uint32_t & nr, int & D, size_t & smb) {
+                   uint32_t & nr, int & D, size_t & smb, int KW = 4) {
     const KsTune t = ks_tune();
     nr = t.nr ? t.nr : (rows + slots - 1) / slots;
     if (nr < 1) nr = 1;
     if (nr > 64u / nx_t) nr = 64u / nx_t;
     D = t.D ? (int)t.D : Ddef;
-    const size_t lim = lds_limit() < 65536 ? lds_limit() : 65536;
-    while (ks_smem_bytes<FMT>(nr, nx_t, nsb, D) > lim && nr > 4) nr >>= 1;
-    while (ks_smem_bytes<FMT>(nr, nx_t, nsb, D) > lim && D > 2) --D;
-    while (ks_smem_bytes<FMT>(nr, nx_t, nsb, D) > lim && nr > 1) nr >>= 1;
+    const size_t cap = KW == 4 ? 65536 : 81920;                  // two workgroups per CU / one
+    const size_t lim = lds_limit() < cap ? lds_limit() : cap;
+    while (ks_smem_bytes<FMT>(nr, nx_t, nsb, D, KW) > lim && nr > 4) nr >>= 1;
+    while (ks_smem_bytes<FMT>(nr, nx_t, nsb, D, KW) > lim && D > 2) --D;
+    while (ks_smem_bytes<FMT>(nr, nx_t, nsb, D, KW) > lim && nr > 1) nr >>= 1;
     // equal batches: a workgroup's ceil(rows / slots) rows in the fewest batches
     const uint32_t g = rows < slots ? rows : slots;
     const uint32_t rpw = (rows + g - 1) / g, nb = (rpw + nr - 1) / nr;
     nr = (rpw + nb - 1) / nb;
-    smb = ks_smem_bytes<FMT>(nr, nx_t, nsb, D);
+    smb = ks_smem_bytes<FMT>(nr, nx_t, nsb, D, KW);
     return smb > lim ? FLH_ERR_UNSUPPORTED : FLH_OK;
 }
 
@@ -319,6 +320,35 @@ template <int FMT, int NX, bool FUSE>
 static int ks_launch(const DotArgs & a, hipStream_t s) {
     const uint32_t nsb = a.cols >> 8;
     const KsTune t = ks_tune();
+    if constexpr (NX == 1) {
+        // Two 8-wave workgroups per CU (16 waves) for single-column dots with
+        // a fused ACT_Q8 or more than 16 superblocks per row: measured, the
+        // Llama-3-8B layer step 41.8 -> 40.6 us (down 4096x14336 9.9 -> 9.2,
+        // the fused ops each a little); the unfused 4096-column shapes stay on
+        // 4-wave workgroups (O 4096x4096: 5.2 vs 5.4 us).  FLH_KS_W8 =
+        // "mode,wgs_per_cu" overrides (mode bits 1: fused, nsb > 16;
+        // 2: fused, nsb <= 16; 4: unfused, nsb > 16; 8: unfused, nsb <= 16).
+        unsigned w8a = 7, w8b = 2;
+        if (const char * w8 = getenv("FLH_KS_W8")) sscanf(w8, "%u,%u", &w8a, &w8b);
+        const unsigned bit = (FUSE ? 1u : 4u) << (nsb > 16 ? 0 : 1);
+        const bool use = (w8a & bit) != 0;
+        if (use) {
+            const uint32_t slots = (uint32_t)num_cus() * (w8b ? w8b : 1);
+            uint32_t nr;
+            int D;
+            size_t smb;
+            if (ks_plan<FMT>(a.rows, 1, nsb, slots, 2, nr, D, smb, 8) == FLH_OK && D == 2) {
+                const uint32_t grid = a.rows < slots ? a.rows : slots;
+                auto go = [&](auto kern) {
+                    (void)hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smb);
+                    hipLaunchKernelGGL(kern, dim3(grid), dim3(512), smb, s, a, nr | (ks_pro() << 16));
+                    return hip_check(hipGetLastError(), "k_dot_kstream launch");
+                };
+                if (16 % nsb == 0) return go(k_dot_kstream<FMT, 1, 2, FUSE, true, 8>);
+                return go(k_dot_kstream<FMT, 1, 2, FUSE, false, 8>);
+            }
+        }
+    }
     const uint32_t slots = (uint32_t)num_cus() * (t.wgs_per_cu ? t.wgs_per_cu : 2);
     uint32_t nr;
     int D;

@@ -105,8 +105,8 @@ __host__ __device__ inline size_t ks_term_bytes(uint32_t nr, uint32_t nx, uint32
     return ((size_t)nr * nx * nsb * 4 * (FMT == FMT_Q4_K ? 2 : 1) + (size_t)nr * nsb * 4) * ks_tps<FMT>();
 }
 template <int FMT>
-__host__ __device__ inline size_t ks_smem_bytes(uint32_t nr, uint32_t nx, uint32_t nsb, int D) {
-    return (size_t)4 * D * KS<FMT>::WIN + ks_xrec_bytes<FMT>(nx, nsb) + ks_term_bytes<FMT>(nr, nx, nsb) + 256;
+__host__ __device__ inline size_t ks_smem_bytes(uint32_t nr, uint32_t nx, uint32_t nsb, int D, int KW = 4) {
+    return (size_t)KW * D * KS<FMT>::WIN + ks_xrec_bytes<FMT>(nx, nsb) + ks_term_bytes<FMT>(nr, nx, nsb) + 256;
 }
 
 // Wait until at most `behind` chunks' DMAs (NI loads each) are outstanding;
@@ -240,7 +240,7 @@ __device__ __forceinline__ float ks_absmax16(const u32x4a (&raw)[4]) {
 // is a 4-step shuffle max (order-free), with no barrier.  after_loads() runs
 // once, right after the first activation loads are issued (the caller issues
 // its weight prologue there, behind the older activation loads).
-template <int FMT, int NX, typename F>
+template <int FMT, int NX, int KW = 4, typename F>
 __device__ __forceinline__ void ks_x_fuse(const KsCols<NX> & C, uint32_t nx, uint32_t nsb, uint32_t cols,
                                           uint8_t * xr, float * xd, bool write_app, F && after_loads) {
     const uint32_t tid = threadIdx.x, lane = tid & 63;
@@ -248,15 +248,15 @@ __device__ __forceinline__ void ks_x_fuse(const KsCols<NX> & C, uint32_t nx, uin
     const uint32_t nitem = nx * nsb;
     const uint32_t sub = lane >> 4, run = lane & 15;        // superblock in the pass, 16-run
     bool issued = false;
-    for (uint32_t base = 0; base < nitem; base += 64) {
-        // up to 64 superblocks per pass (16 per q-group, 4 per wave), loads
-        // first; only the q-groups that hold superblocks are loaded
-        const uint32_t nq = min(4u, (nitem - base + 15) / 16);
+    for (uint32_t base = 0; base < nitem; base += 16 * KW) {
+        // up to 16 KW superblocks per pass (4 KW per q-group, 4 per wave),
+        // loads first; only the q-groups that hold superblocks are loaded
+        const uint32_t nq = min(4u, (nitem - base + 4 * KW - 1) / (4 * KW));
         u32x4a raw[4][4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             if ((uint32_t)q >= nq) break;
-            const uint32_t i = base + 16 * q + 4 * wave + sub;
+            const uint32_t i = base + 4 * KW * q + 4 * wave + sub;
             const uint32_t ii = i < nitem ? i : 0;
             const float * src = col_pick<NX>(C.x, ii / nsb) + 256 * (ii % nsb) + 16 * run;
 #pragma unroll
@@ -279,7 +279,7 @@ __device__ __forceinline__ void ks_x_fuse(const KsCols<NX> & C, uint32_t nx, uin
         }
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            const uint32_t i = base + 16 * q + 4 * wave + sub;
+            const uint32_t i = base + 4 * KW * q + 4 * wave + sub;
             if ((uint32_t)q < nq && i < nitem) {
                 const uint32_t p = i / nsb, sb = i % nsb;
                 const float amax = amq[q];
