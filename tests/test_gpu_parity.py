@@ -7,6 +7,8 @@ order exactly).  Full BASELINE shapes are also checked bitwise; the
 north-star tolerance (max |dy| <= 1e-3 * max |y| vs an f64 dequant dot) is
 checked on top of that for the headline shapes.
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -323,3 +325,32 @@ def test_fused_act_q8_dot_bitwise(flh, orc, gpu, fmt, rows, cols, nx):
     want = y0.copy()
     orc.stream_dot(fmt, w, rows, cols, ref_x, want, nx=nx, xstride=st, ystride=rows, threads=8)
     assert np.array_equal(bits(got), bits(want))
+
+
+# ------------------------------------------- 8- and 4-wave streaming kernels --
+@pytest.mark.parametrize("w8", ["15,2", "15,1", "0,2"])
+@pytest.mark.parametrize("fmt,rows,cols", [(Q4_K, 1000, 4096), (Q6_K, 513, 14336), (Q4_K, 3, 2816),
+                                           (Q8_0, 700, 4096), (Q6_K, 300, 512)])
+def test_streaming_workgroup_shapes_bitwise(flh, orc, gpu, w8, fmt, rows, cols):
+    """Every workgroup shape of the single-column streaming kernel (4 or 8
+    waves, one or two per CU; FLH_KS_W8 = "mode bits,workgroups per CU"),
+    fused with ACT_Q8 or not, equals the oracle bit for bit."""
+    say("kstream shapes", w8, fmt, rows, cols)
+    rng = np.random.default_rng(rows + cols + fmt)
+    w = sane_rows(fmt, rows, cols, rng)
+    xs = activations(1, cols, rng, outliers=True)
+    os.environ["FLH_KS_W8"] = w8
+    try:
+        got, want = run_dot(flh, orc, gpu, fmt, w, rows, cols, xs, y0=rng.standard_normal(rows).astype(np.float32))
+        assert np.array_equal(bits(got), bits(want))
+        if fmt != Q8_0:
+            st = col_stride_floats(cols)
+            dx, _ = dev_cols(flh, gpu, xs, st)
+            dy = flh.DeviceBuffer.from_array(np.zeros(rows, np.float32), gpu)
+            dw = flh.DeviceBuffer.from_array(w, gpu)
+            flh.act_q8_stream_dot(fmt, dw, rows, cols, dx, dy, gpu)
+            want2 = np.zeros(rows, np.float32)
+            orc.stream_dot(fmt, w, rows, cols, orc.act_q8_cols(xs, st), want2, threads=8)
+            assert np.array_equal(bits(dy.download(np.float32, rows, gpu)), bits(want2))
+    finally:
+        del os.environ["FLH_KS_W8"]
