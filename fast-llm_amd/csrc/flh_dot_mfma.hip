@@ -127,44 +127,65 @@ __device__ __forceinline__ void mf_ld_x(const uint8_t * xs, uint32_t j, u32x2 (&
         : "v"(a8), "v"(a4));
 }
 
-// Reference-order fold of row rl, column p (terms [sb][row][column]; the
-// q8_K scale read from the column's raw appendix at xp): lane k runs
-// accumulator k over superblocks k, k + 4, ... (loads of four steps issued
-// together); the quad then combines (a0 + a1) + (a2 + a3).  Same float
-// operations, in the same order, as ks_fold and fl_dot_i8k_q4_K.
-template <int NC>
-__device__ __forceinline__ float mf_fold(const int * TI, const int * TM, const uint32_t * TH, const uint8_t * xp,
-                                         uint32_t nsb, uint32_t nrb, uint32_t k, uint32_t p, uint32_t rl, bool fok) {
-    float acc = 0.f;
+// Reference-order fold of column p for the rows rl0 + FR*i, i < R (terms
+// [sb][row][column]; the q8_K scale read from the column's raw appendix at
+// xp): lane k runs accumulator k over superblocks k, k + 4, ...; the quad
+// then combines (a0 + a1) + (a2 + a3).  Same float operations, in the same
+// order, as ks_fold and fl_dot_i8k_q4_K.  The R rows' loads of four steps
+// are issued together: a fold's time is its LDS round trips (~0.4 us each
+// here), so R rows per round instead of one.  Rows >= nrow fold row nrow - 1
+// again (their results are not stored).
+template <int NC, int R>
+__device__ __forceinline__ void mf_fold(const int * TI, const int * TM, const uint32_t * TH, const uint8_t * xp,
+                                        uint32_t nsb, uint32_t nrb, uint32_t k, uint32_t p, uint32_t rl0, uint32_t FR,
+                                        uint32_t nrow, bool fok, float (&res)[R]) {
+    float acc[R];
+    uint32_t rl[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+        acc[i] = 0.f;
+        rl[i] = min(rl0 + FR * i, nrow - 1);
+    }
     if (fok) {
-        auto step = [&](int ti, int tm, uint32_t th, float dk) {
+        auto step = [&](float & a, int ti, int tm, uint32_t th, float dk) {
             const float d = h2f(th & 0xFFFFu), dmin = h2f(th >> 16);
-            acc = fmaf(d * dk, (float)ti, acc);
-            acc = fmaf(-(dmin * dk), (float)tm, acc);
+            a = fmaf(d * dk, (float)ti, a);
+            a = fmaf(-(dmin * dk), (float)tm, a);
         };
         uint32_t s = k;
         for (; s + 12 < nsb; s += 16) {
-            int ti[4], tm[4];
-            uint32_t th[4];
+            int ti[R][4], tm[R][4];
+            uint32_t th[R][4];
             float dk[4];
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const uint32_t sq = s + 4 * q;
-                ti[q] = TI[(size_t)sq * mf_ts<NC>(nrb) + rl * NC + p];
-                tm[q] = TM[(size_t)sq * mf_ts<NC>(nrb) + rl * NC + p];
-                th[q] = TH[(size_t)sq * mf_ths(nrb) + rl];
                 dk[q] = *(const float *)(xp + (size_t)sq * 292);
+#pragma unroll
+                for (int i = 0; i < R; ++i) {
+                    ti[i][q] = TI[(size_t)sq * mf_ts<NC>(nrb) + rl[i] * NC + p];
+                    tm[i][q] = TM[(size_t)sq * mf_ts<NC>(nrb) + rl[i] * NC + p];
+                    th[i][q] = TH[(size_t)sq * mf_ths(nrb) + rl[i]];
+                }
             }
 #pragma unroll
-            for (int q = 0; q < 4; ++q) step(ti[q], tm[q], th[q], dk[q]);
+            for (int i = 0; i < R; ++i)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) step(acc[i], ti[i][q], tm[i][q], th[i][q], dk[q]);
         }
-        for (; s < nsb; s += 4)
-            step(TI[(size_t)s * mf_ts<NC>(nrb) + rl * NC + p], TM[(size_t)s * mf_ts<NC>(nrb) + rl * NC + p],
-                 TH[(size_t)s * mf_ths(nrb) + rl],
-                 *(const float *)(xp + (size_t)s * 292));
+        for (; s < nsb; s += 4) {
+            const float dk = *(const float *)(xp + (size_t)s * 292);
+#pragma unroll
+            for (int i = 0; i < R; ++i)
+                step(acc[i], TI[(size_t)s * mf_ts<NC>(nrb) + rl[i] * NC + p],
+                     TM[(size_t)s * mf_ts<NC>(nrb) + rl[i] * NC + p], TH[(size_t)s * mf_ths(nrb) + rl[i]], dk);
+        }
     }
-    const float s01 = acc + qx1f(acc);
-    return s01 + qx2f(s01);
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+        const float s01 = acc[i] + qx1f(acc[i]);
+        res[i] = s01 + qx2f(s01);
+    }
 }
 
 // Wait until at most n of this wave's DMA instructions are outstanding
@@ -547,16 +568,37 @@ __device__ __forceinline__ void mf_body(const uint8_t * __restrict__ w, uint32_t
         if (KH && y_mine) mf_wait_vm(vm - y_vm);
         lds_barrier();
         MF_STAMP(3);
-        for (uint32_t frl = frl0; frl < nrow; frl += FROWS) {
+        for (uint32_t frl = frl0; KH && frl < nrow; frl += FROWS) {
             const bool fok = fp < nx;
             if constexpr (KH) {
                 // (a0 + a1) + (a2 + a3): the two halves' sums in either order
                 const uint32_t h1 = half_of(bt, 1);
                 const float s1 = mf_fold_h<NC>(TI, TM, TH, dkt, nl_of(h1), nsb, h1, nrb, fk, fp, frl, fok);
                 if (fok && fk == 0) C.y(fp)[row0 + frl] = ysm[frl * NC + fp] + (yph[frl * NC + fp] + s1);
+            }
+        }
+        if constexpr (!KH) {
+            // every row of the batch in one call (nrow <= nrb <= 512 / NC = 4 FROWS)
+            const bool fok = fp < nx;
+            const uint8_t * xp = xr + (size_t)fp * XS;
+            auto fold_store = [&](auto & rr) {
+                constexpr int R = sizeof(rr) / sizeof(float);
+                mf_fold<NC, R>(TI, TM, TH, xp, nsb, nrb, fk, fp, frl0, FROWS, nrow, fok, rr);
+#pragma unroll
+                for (int i = 0; i < R; ++i) {
+                    const uint32_t frl = frl0 + FROWS * i;
+                    if (fok && fk == 0 && frl < nrow) C.y(fp)[row0 + frl] = ysm[frl * NC + fp] + rr[i];
+                }
+            };
+            if (nrow <= FROWS) {
+                float rr[1];
+                fold_store(rr);
+            } else if (nrow <= 2 * FROWS) {
+                float rr[2];
+                fold_store(rr);
             } else {
-                const float rr = mf_fold<NC>(TI, TM, TH, xr + (size_t)fp * XS, nsb, nrb, fk, fp, frl, fok);
-                if (fok && fk == 0) C.y(fp)[row0 + frl] = ysm[frl * NC + fp] + rr;
+                float rr[4];
+                fold_store(rr);
             }
         }
         lds_barrier();
