@@ -206,7 +206,7 @@ __global__ __launch_bounds__(64 * KW) void k_dot_kstream(DotArgs a, uint32_t nr)
     ks_body<FMT, NX, D, FUSE, XREG, KW>(w, a.rows, a.cols, C, a.nx, nr, blockIdx.x, gridDim.x, sm);
 }
 
-// Grouped expert matvec: blockIdx.y = the y-th routed expert.  The workgroup collects the
+// Grouped expert matvec: the routed experts share the grid (moe_assign).  The workgroup collects the
 // routed (token, slot) pairs of its expert and streams that expert's weights
 // once per group of NX pairs; with no pair routed to it, it exits before any
 // weight byte is requested.
@@ -217,7 +217,9 @@ __global__ __launch_bounds__(256) void k_moe_kstream(MoeArgs a, uint32_t nr) {
     __shared__ uint32_t rids[256];
     __shared__ uint32_t npairs;
     const uint32_t * ids = moe_route(a, rids);
-    const uint32_t e = moe_jth_expert(ids, a.ntok * a.top_k, a.n_expert, blockIdx.y);
+    uint32_t g, G;
+    const uint32_t e = moe_assign(ids, a.ntok * a.top_k, a.n_expert, blockIdx.y * gridDim.x + blockIdx.x,
+                                  gridDim.x * gridDim.y, g, G);
     if (e >= a.n_expert) return;
     if (threadIdx.x == 0) {
         uint32_t n = 0;
@@ -238,7 +240,7 @@ __global__ __launch_bounds__(256) void k_moe_kstream(MoeArgs a, uint32_t nr) {
             C.x[p] = a.x + (size_t)xi * a.xstride;
             C.y[p] = a.y + (size_t)ts * a.ystride;
         }
-        ks_body<FMT, NX, D, false, XREG>(w, a.rows, a.cols, C, nx, nr, blockIdx.x, gridDim.x, sm);
+        ks_body<FMT, NX, D, false, XREG>(w, a.rows, a.cols, C, nx, nr, g, G, sm);
         __syncthreads();
     }
 }

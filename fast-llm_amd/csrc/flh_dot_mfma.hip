@@ -615,7 +615,7 @@ __global__ __launch_bounds__(512) void k_dot_mfma(DotArgs a, uint32_t nrb) {
     mf_body<NC, D, KH>(w, a.rows, a.cols, C, a.nx, nrb, blockIdx.x, gridDim.x, sm);
 }
 
-// Grouped expert matvec (MoE): blockIdx.y = the y-th routed expert e.  The workgroup collects
+// Grouped expert matvec (MoE): the routed experts share the grid (moe_assign).  The workgroup collects
 // the (token, slot) pairs routed to e and streams e's weights once per group
 // of NC pairs (the columns); with no pair routed to e it exits before any
 // weight byte is requested.  Column p's activation index and output index
@@ -640,7 +640,9 @@ __global__ __launch_bounds__(512) void k_moe_mfma(MoeArgs a, uint32_t nrbp) {
     __shared__ uint32_t rids[256];
     if (tid == 0) npairs = 0;
     const uint32_t * ids = moe_route(a, rids);
-    const uint32_t e = moe_jth_expert(ids, a.ntok * a.top_k, a.n_expert, blockIdx.y);   // (barriers)
+    uint32_t g, G;
+    const uint32_t e = moe_assign(ids, a.ntok * a.top_k, a.n_expert, blockIdx.y * gridDim.x + blockIdx.x,
+                                  gridDim.x * gridDim.y, g, G);                 // (barriers)
     if (e >= a.n_expert) return;
     // pairs i = tok * top_k + slot routed to e (order free: every column's
     // output is computed independently)
@@ -657,7 +659,7 @@ __global__ __launch_bounds__(512) void k_moe_mfma(MoeArgs a, uint32_t nrbp) {
         }
         __syncthreads();
         const MfColsMoe C{a.x, a.y, a.xstride, a.ystride, cxi, cyi};
-        mf_body<NC, D, KH>(w, a.rows, a.cols, C, nx, nrbp, blockIdx.x, gridDim.x, sm);
+        mf_body<NC, D, KH>(w, a.rows, a.cols, C, nx, nrbp, g, G, sm);
         __syncthreads();
     }
 }

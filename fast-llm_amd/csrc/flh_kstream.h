@@ -709,13 +709,15 @@ __device__ __forceinline__ const uint32_t * moe_route(const MoeArgs & a, uint32_
     return rids;
 }
 
-// Expert of grouped-matvec row j of the grid (blockIdx.y): the j-th smallest
-// distinct id among the nids routed pairs, or n_expert when fewer experts are
-// routed (the workgroup then has nothing to do).  The grid holds only as many
-// rows as experts can be active, so no workgroup waits for a CU only to find
-// its expert unrouted.  Contains barriers.
-__device__ __forceinline__ uint32_t moe_jth_expert(const uint32_t * ids, uint32_t nids, uint32_t n_expert,
-                                                   uint32_t j) {
+// Work of grouped-matvec workgroup b of B (flattened grid): the n routed
+// experts (distinct ids among the nids pairs) share the B workgroups evenly,
+// expert j (the j-th smallest id) taking workgroups [ceil(jB/n),
+// ceil((j+1)B/n)); returns e = n_expert when nothing is routed, else e and
+// this workgroup's index g among its expert's G.  Every workgroup computes the
+// same split from the same ids, so none idles on an unrouted expert.
+// Contains barriers.
+__device__ __forceinline__ uint32_t moe_assign(const uint32_t * ids, uint32_t nids, uint32_t n_expert, uint32_t b,
+                                               uint32_t B, uint32_t & g, uint32_t & G) {
     __shared__ uint32_t em[8];
     __shared__ uint32_t pick;
     if (threadIdx.x < 8) em[threadIdx.x] = 0u;
@@ -725,9 +727,13 @@ __device__ __forceinline__ uint32_t moe_jth_expert(const uint32_t * ids, uint32_
         if (e < n_expert && e < 256) atomicOr(&em[e >> 5], 1u << (e & 31));
     }
     __syncthreads();
+    uint32_t n = 0;
+#pragma unroll
+    for (int w = 0; w < 8; ++w) n += (uint32_t)__popc(em[w]);
+    const uint32_t j = n ? b * n / B : 0u;                  // b * n < 2^32: B <= 2^20 workgroups
     if (threadIdx.x == 0) {
         uint32_t k = j, r = n_expert;
-        for (uint32_t w = 0; w < 8 && r == n_expert; ++w) {
+        for (uint32_t w = 0; w < 8 && r == n_expert && n; ++w) {
             uint32_t m = em[w];
             const uint32_t c = (uint32_t)__popc(m);
             if (k < c) {
@@ -740,6 +746,10 @@ __device__ __forceinline__ uint32_t moe_jth_expert(const uint32_t * ids, uint32_
         pick = r;
     }
     __syncthreads();
+    const uint32_t nn = n ? n : 1u;
+    const uint32_t s0 = (j * B + nn - 1) / nn, s1 = ((j + 1) * B + nn - 1) / nn;
+    g = b - s0;
+    G = s1 - s0;
     return pick;
 }
 
