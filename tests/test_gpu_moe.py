@@ -267,3 +267,15 @@ def test_router_moe_dot_fused_equals_separate(flh, gpu, fmt, ntok, rows, cols, p
     assert list(outs[0][0][:2]) == [1, 3]                               # tie -> lower id first
     for a, b in zip(outs[0], outs[1]):
         assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("ntok,rows,cols,per_slot", [(8, 300, 4096, False), (6, 130, 2816, True)])
+def test_grouped_expert_dot_k_halves_bitwise(flh, orc, gpu, ntok, rows, cols, per_slot):
+    """The grouped matrix-core kernel with K halves forced (the mode wide
+    expert inputs take when the whole activations do not fit LDS), bitwise."""
+    import os
+    os.environ["FLH_MFMA_TUNE"] = "2,0,1"
+    try:
+        grouped_dot_case(flh, orc, gpu, Q4_K, ntok, rows, cols, per_slot)
+    finally:
+        del os.environ["FLH_MFMA_TUNE"]
