@@ -58,6 +58,7 @@ constexpr int MF_NI = 3;                     // DMA instructions per chunk
 
 // LDS: [waves][D][2304] ring | xr [NC][XS] raw q8_K appendices | TI, TM [nl][nrb][NC]
 //      | TH [nl][nrb] | ysm [nrb * NC] | (K halves) yph [nrb * NC], dkt [NC][nsb]
+//      | (NC = 4) zr: 64 zero bytes
 // XS: a column's appendix (292 bytes per superblock) padded so that XS / 4 is
 // 8 mod 32 (the 16 columns' reads of one k-slice fall in distinct banks).
 //
@@ -89,7 +90,8 @@ __host__ __device__ inline size_t mf_smem_bytes(uint32_t nrb, uint32_t nsb, int 
     const uint32_t nl = KH ? mf_nsbh(nsb, 0) : nsb;
     return (size_t)MF_WAVES * D * MF_CHUNK + (KH ? (size_t)nl * NC * MF_XB : (size_t)NC * mf_xs(nl)) +
            (size_t)mf_ts<NC>(nrb) * nl * 8 +
-           (size_t)mf_ths(nrb) * nl * 4 + (size_t)nrb * NC * 4 + (KH ? (size_t)nrb * NC * 4 + (size_t)NC * nsb * 4 : 0);
+           (size_t)mf_ths(nrb) * nl * 4 + (size_t)nrb * NC * 4 + (KH ? (size_t)nrb * NC * 4 + (size_t)NC * nsb * 4 : 0) +
+           (NC == 4 ? 64 : 0);
 }
 
 // Column sources of one pass: activation column p at x(p) (fp32 x followed by
@@ -125,6 +127,38 @@ __device__ __forceinline__ void mf_ld_x(const uint8_t * xs, uint32_t j, u32x2 (&
         : "=&v"(xw[0]), "=&v"(xw[1]), "=&v"(xw[2]), "=&v"(xw[3]), "=&v"(xw[4]), "=&v"(xw[5]), "=&v"(xw[6]),
           "=&v"(xw[7]), "=&v"(bp)
         : "v"(a8), "v"(a4));
+}
+
+// NC = 4 (block-diagonal A): xw[4G + m] = bytes 36 + 64j + 32G + 8m .. +7 of
+// the block at byte address ax - 64j (sub-block 2j + G, k-slice m); lanes off
+// the diagonal pass ax = a zero region - 36.  bp = bsum pairs of sub-blocks j
+// and 4 + j of the block at ab - 4j.  Waits for its own reads, as mf_ld_x.
+__device__ __forceinline__ void mf_ld_x4(uint32_t ax, uint32_t ab, u32x2 (&xw)[8], u32x2 & bp) {
+    asm volatile(
+        "ds_read2_b32 %0, %9 offset0:9 offset1:10\n\t"
+        "ds_read2_b32 %1, %9 offset0:11 offset1:12\n\t"
+        "ds_read2_b32 %2, %9 offset0:13 offset1:14\n\t"
+        "ds_read2_b32 %3, %9 offset0:15 offset1:16\n\t"
+        "ds_read2_b32 %4, %9 offset0:17 offset1:18\n\t"
+        "ds_read2_b32 %5, %9 offset0:19 offset1:20\n\t"
+        "ds_read2_b32 %6, %9 offset0:21 offset1:22\n\t"
+        "ds_read2_b32 %7, %9 offset0:23 offset1:24\n\t"
+        "ds_read2_b32 %8, %10 offset0:1 offset1:5\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(xw[0]), "=&v"(xw[1]), "=&v"(xw[2]), "=&v"(xw[3]), "=&v"(xw[4]), "=&v"(xw[5]), "=&v"(xw[6]),
+          "=&v"(xw[7]), "=&v"(bp)
+        : "v"(ax), "v"(ab));
+}
+
+// Sum of v over the four 16-lane rows, transposed: lane row j gets
+// sum over rows of p[j] (two permlane32 swaps pair rows j, j + 2; one
+// permlane16 swap pairs rows j, j + 1).  Integer adds: exact in any order.
+__device__ __forceinline__ int mf_rowsum_t(const int (&p)[4]) {
+    const auto a = __builtin_amdgcn_permlane32_swap((uint32_t)p[0], (uint32_t)p[2], false, false);
+    const auto b = __builtin_amdgcn_permlane32_swap((uint32_t)p[1], (uint32_t)p[3], false, false);
+    const uint32_t u = a[0] + a[1], v = b[0] + b[1];
+    const auto c = __builtin_amdgcn_permlane16_swap(u, v, false, false);
+    return (int)(c[0] + c[1]);
 }
 
 // Reference-order fold of column p for the rows rl0 + FR*i, i < R (terms
@@ -283,6 +317,13 @@ __device__ __forceinline__ void mf_body(const uint8_t * __restrict__ w, uint32_t
     float * ysm = (float *)(TH + (size_t)mf_ths(nrb) * NL);
     float * yph = ysm + (size_t)nrb * NC;                         // KH: first half's sums
     float * dkt = yph + (size_t)nrb * NC;                         // KH: q8_K scales [NC][nsb]
+    uint8_t * zr = KH ? (uint8_t *)(dkt + (size_t)NC * nsb) : (uint8_t *)yph;   // NC = 4: zeros
+    // NC = 4: each MFMA's A is block-diagonal (rows 4g .. 4g + 3 = the four
+    // columns on k-slice g only), so one wave's 8 MFMAs give every lane row j
+    // the dots of sub-blocks 2j, 2j + 1 for the 4 columns: the scale-weighted
+    // sum is 8 products plus a cross-row sum, not 32 products
+    constexpr bool BD = NC == 4;
+    if constexpr (BD) if (tid < 16) lds_st32(zr + 4 * tid, 0u);
 
     MF_STAMP(0);
     const uint32_t rbeg = (uint32_t)((uint64_t)rows * g / G);
@@ -466,17 +507,28 @@ __device__ __forceinline__ void mf_body(const uint8_t * __restrict__ w, uint32_t
                 const uint8_t * rp = myst + slot * MF_CHUNK + 144 * r;
                 const u32x4a hd = *(const u32x4a *)rp;
                 uint32_t qw[4][2];
+                u32x4a qv[2];                                       // BD: qs bytes 32j .. 32j + 31
+                if constexpr (BD) {
+                    qv[0] = *(const u32x4a *)(rp + 16 + 32 * j);
+                    qv[1] = *(const u32x4a *)(rp + 32 + 32 * j);
+                } else {
 #pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    qw[c][0] = *(const uint32_t *)(rp + 16 + 32 * c + 8 * j);
-                    qw[c][1] = *(const uint32_t *)(rp + 20 + 32 * c + 8 * j);
+                    for (int c = 0; c < 4; ++c) {
+                        qw[c][0] = *(const uint32_t *)(rp + 16 + 32 * c + 8 * j);
+                        qw[c][1] = *(const uint32_t *)(rp + 20 + 32 * c + 8 * j);
+                    }
                 }
                 // activation operands of this superblock (zero for lanes past NC):
                 // column r, bytes 32g + 8j .. +7 of sub-block g; sub-block sums
                 // bsum[2g] + bsum[2g + 1] for g = j and 4 + j
                 u32x2 xw[8] = {};
                 u32x2 bp = {};
-                if (r < NC)
+                if constexpr (BD) {
+                    // column r & 3 (rows 4 .. 15 of the min term are never stored)
+                    const uint32_t ab = lds_off(KH ? xr + ((size_t)li * NC + (r & 3)) * MF_XB + MF_XO
+                                                   : xr + (size_t)(r & 3) * XS + (size_t)li * 292);
+                    mf_ld_x4((r >> 2) == j ? ab + 64 * j : lds_off(zr) - 36, ab + 4 * j, xw, bp);
+                } else if (r < NC)
                     mf_ld_x(KH ? xr + ((size_t)li * NC + r) * MF_XB + MF_XO : xr + (size_t)r * XS + (size_t)li * 292, j,
                             xw, bp);
                 const uint32_t bp0 = bp.x, bp1 = bp.y;
@@ -502,6 +554,19 @@ __device__ __forceinline__ void mf_body(const uint8_t * __restrict__ w, uint32_t
                 const uint32_t schi = (hd.w & 0x0F0F0F0Fu) | ((hd.y >> 2) & 0x30303030u);
                 const uint32_t mhi = ((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u);
                 v4i acc[8];
+                v4i a0 = {0, 0, 0, 0}, a1 = {0, 0, 0, 0};           // BD: sub-blocks 2j, 2j + 1
+                if constexpr (BD) {
+                    const uint32_t q[8] = {qv[0].x, qv[0].y, qv[0].z, qv[0].w, qv[1].x, qv[1].y, qv[1].z, qv[1].w};
+#pragma unroll
+                    for (int m = 0; m < 4; ++m) {
+                        const uint32_t lo0 = q[2 * m] & 0x0F0F0F0Fu, lo1 = q[2 * m + 1] & 0x0F0F0F0Fu;
+                        const uint32_t hi0 = (q[2 * m] >> 4) & 0x0F0F0F0Fu, hi1 = (q[2 * m + 1] >> 4) & 0x0F0F0F0Fu;
+                        a0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(__builtin_bit_cast(long, xw[m]),
+                                                                    (long)(((uint64_t)lo1 << 32) | lo0), a0, 0, 0, 0);
+                        a1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(__builtin_bit_cast(long, xw[4 + m]),
+                                                                    (long)(((uint64_t)hi1 << 32) | hi0), a1, 0, 0, 0);
+                    }
+                } else
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
                     const uint32_t lo0 = qw[c][0] & 0x0F0F0F0Fu, lo1 = qw[c][1] & 0x0F0F0F0Fu;
@@ -518,16 +583,30 @@ __device__ __forceinline__ void mf_body(const uint8_t * __restrict__ w, uint32_t
                 const float bm0 = (float)((mlo >> (8 * j)) & 0xFFu), bm1 = (float)((mhi >> (8 * j)) & 0xFFu);
                 v4f cm = __builtin_amdgcn_mfma_f32_16x16x4f32(bsa0, bm0, v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
                 cm = __builtin_amdgcn_mfma_f32_16x16x4f32(bsa1, bm1, cm, 0, 0, 0);
+                // park: terms [li][row][column]
+                const uint32_t rl = 16 * t + r;                     // row within the batch
+                if constexpr (BD) {
+                    const uint32_t wsc = j < 2 ? sclo : schi, sh = 16 * (j & 1);
+                    const int s0 = (int)((wsc >> sh) & 0xFFu), s1 = (int)((wsc >> (sh + 8)) & 0xFFu);
+                    int pr[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) pr[i] = __mul24(s0, a0[i]) + __mul24(s1, a1[i]);
+                    const size_t e = (size_t)li * mf_ts<NC>(nrb) + rl * NC;
+                    lds_st32(&TI[e + j], (uint32_t)mf_rowsum_t(pr));
+                    if (j == 0)
+                        lds_st128(&TM[e], u32x4a{(uint32_t)(int)cm[0], (uint32_t)(int)cm[1], (uint32_t)(int)cm[2],
+                                                  (uint32_t)(int)cm[3]});
+                    if (j == 0) lds_st32(&TH[(size_t)li * mf_ths(nrb) + rl], hd.x);
+                    continue;
+                }
                 int sc[8];
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
                     sc[k] = (int)((sclo >> (8 * k)) & 0xFFu);
                     sc[4 + k] = (int)((schi >> (8 * k)) & 0xFFu);
                 }
-                // park: terms [li][row][column], the lane's 4 columns in one
-                // 16-byte store (rows past the batch and columns past nx hold
-                // values the fold never reads)
-                const uint32_t rl = 16 * t + r;                     // row within the batch
+                // the lane's 4 columns in one 16-byte store (rows past the
+                // batch and columns past nx hold values the fold never reads)
                 int ia[4];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
