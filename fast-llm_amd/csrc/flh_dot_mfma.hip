@@ -58,7 +58,7 @@ constexpr int MF_NI = 3;                     // DMA instructions per chunk
 
 // LDS: [waves][D][2304] ring | xr [NC][XS] raw q8_K appendices | TI, TM [nl][nrb][NC]
 //      | TH [nl][nrb] | ysm [nrb * NC] | (K halves) yph [nrb * NC], dkt [NC][nsb]
-//      | (NC = 4) zr: 64 zero bytes
+//      | (NC = 4, 8) zr: 128 zero bytes
 // XS: a column's appendix (292 bytes per superblock) padded so that XS / 4 is
 // 8 mod 32 (the 16 columns' reads of one k-slice fall in distinct banks).
 //
@@ -91,7 +91,7 @@ __host__ __device__ inline size_t mf_smem_bytes(uint32_t nrb, uint32_t nsb, int 
     return (size_t)MF_WAVES * D * MF_CHUNK + (KH ? (size_t)nl * NC * MF_XB : (size_t)NC * mf_xs(nl)) +
            (size_t)mf_ts<NC>(nrb) * nl * 8 +
            (size_t)mf_ths(nrb) * nl * 4 + (size_t)nrb * NC * 4 + (KH ? (size_t)nrb * NC * 4 + (size_t)NC * nsb * 4 : 0) +
-           (NC == 4 ? 64 : 0);
+           (NC <= 8 ? 128 : 0);
 }
 
 // Column sources of one pass: activation column p at x(p) (fp32 x followed by
@@ -148,6 +148,31 @@ __device__ __forceinline__ void mf_ld_x4(uint32_t ax, uint32_t ab, u32x2 (&xw)[8
         : "=&v"(xw[0]), "=&v"(xw[1]), "=&v"(xw[2]), "=&v"(xw[3]), "=&v"(xw[4]), "=&v"(xw[5]), "=&v"(xw[6]),
           "=&v"(xw[7]), "=&v"(bp)
         : "v"(ax), "v"(ab));
+}
+
+// NC = 8 (block-diagonal A): xw[4cc + 2n + m] = bytes 36 + 128h + 64cc + 32n +
+// 16m + 8e .. +7 of the block at ax - 128h - 8e (h = j >> 1, e = j & 1: sub-block
+// 4h + 2cc + n, k-slice 2m + e); lanes off the diagonal pass ax = a zero region
+// - 36.  bp as mf_ld_x4.
+__device__ __forceinline__ void mf_ld_x8(uint32_t ax, uint32_t ab, u32x2 (&xw)[8], u32x2 & bp) {
+    asm volatile(
+        "ds_read2_b32 %0, %9 offset0:9 offset1:10\n\t"
+        "ds_read2_b32 %1, %9 offset0:13 offset1:14\n\t"
+        "ds_read2_b32 %2, %9 offset0:17 offset1:18\n\t"
+        "ds_read2_b32 %3, %9 offset0:21 offset1:22\n\t"
+        "ds_read2_b32 %4, %9 offset0:25 offset1:26\n\t"
+        "ds_read2_b32 %5, %9 offset0:29 offset1:30\n\t"
+        "ds_read2_b32 %6, %9 offset0:33 offset1:34\n\t"
+        "ds_read2_b32 %7, %9 offset0:37 offset1:38\n\t"
+        "ds_read2_b32 %8, %10 offset0:1 offset1:5\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(xw[0]), "=&v"(xw[1]), "=&v"(xw[2]), "=&v"(xw[3]), "=&v"(xw[4]), "=&v"(xw[5]), "=&v"(xw[6]),
+          "=&v"(xw[7]), "=&v"(bp)
+        : "v"(ax), "v"(ab));
+}
+
+__device__ __forceinline__ void lds_st64(void * p, u32x2 v) {
+    asm volatile("ds_write_b64 %0, %1" :: "v"(lds_off(p)), "v"(v));
 }
 
 // Sum of v over the four 16-lane rows, transposed: lane row j gets
@@ -317,13 +342,15 @@ __device__ __forceinline__ void mf_body(const uint8_t * __restrict__ w, uint32_t
     float * ysm = (float *)(TH + (size_t)mf_ths(nrb) * NL);
     float * yph = ysm + (size_t)nrb * NC;                         // KH: first half's sums
     float * dkt = yph + (size_t)nrb * NC;                         // KH: q8_K scales [NC][nsb]
-    uint8_t * zr = KH ? (uint8_t *)(dkt + (size_t)NC * nsb) : (uint8_t *)yph;   // NC = 4: zeros
+    uint8_t * zr = KH ? (uint8_t *)(dkt + (size_t)NC * nsb) : (uint8_t *)yph;   // NC <= 8: zeros
     // NC = 4: each MFMA's A is block-diagonal (rows 4g .. 4g + 3 = the four
     // columns on k-slice g only), so one wave's 8 MFMAs give every lane row j
     // the dots of sub-blocks 2j, 2j + 1 for the 4 columns: the scale-weighted
-    // sum is 8 products plus a cross-row sum, not 32 products
-    constexpr bool BD = NC == 4;
-    if constexpr (BD) if (tid < 16) lds_st32(zr + 4 * tid, 0u);
+    // sum is 8 products plus a cross-row sum, not 32 products.  NC = 8: rows
+    // 8h .. 8h + 7 on k-slices 2h, 2h + 1; lane rows 2h, 2h + 1 get sub-blocks
+    // 4h .. 4h + 3 (16 products, a sum over h)
+    constexpr bool BD = NC <= 8;
+    if constexpr (BD) if (tid < 32) lds_st32(zr + 4 * tid, 0u);
 
     MF_STAMP(0);
     const uint32_t rbeg = (uint32_t)((uint64_t)rows * g / G);
@@ -507,10 +534,14 @@ __device__ __forceinline__ void mf_body(const uint8_t * __restrict__ w, uint32_t
                 const uint8_t * rp = myst + slot * MF_CHUNK + 144 * r;
                 const u32x4a hd = *(const u32x4a *)rp;
                 uint32_t qw[4][2];
-                u32x4a qv[2];                                       // BD: qs bytes 32j .. 32j + 31
-                if constexpr (BD) {
+                u32x4a qv[2];                                       // NC = 4: qs bytes 32j .. 32j + 31
+                u32x2 qb[4];                                        // NC = 8: qs bytes 64h + 32cc + 16m + 8e
+                if constexpr (NC == 4) {
                     qv[0] = *(const u32x4a *)(rp + 16 + 32 * j);
                     qv[1] = *(const u32x4a *)(rp + 32 + 32 * j);
+                } else if constexpr (NC == 8) {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) qb[q] = *(const u32x2 *)(rp + 16 + 64 * (j >> 1) + 16 * q + 8 * (j & 1));
                 } else {
 #pragma unroll
                     for (int c = 0; c < 4; ++c) {
@@ -524,10 +555,14 @@ __device__ __forceinline__ void mf_body(const uint8_t * __restrict__ w, uint32_t
                 u32x2 xw[8] = {};
                 u32x2 bp = {};
                 if constexpr (BD) {
-                    // column r & 3 (rows 4 .. 15 of the min term are never stored)
-                    const uint32_t ab = lds_off(KH ? xr + ((size_t)li * NC + (r & 3)) * MF_XB + MF_XO
-                                                   : xr + (size_t)(r & 3) * XS + (size_t)li * 292);
-                    mf_ld_x4((r >> 2) == j ? ab + 64 * j : lds_off(zr) - 36, ab + 4 * j, xw, bp);
+                    // column r % NC (rows NC .. 15 of the min term are never stored)
+                    const uint32_t ab = lds_off(KH ? xr + ((size_t)li * NC + (r & (NC - 1))) * MF_XB + MF_XO
+                                                   : xr + (size_t)(r & (NC - 1)) * XS + (size_t)li * 292);
+                    if constexpr (NC == 4)
+                        mf_ld_x4((r >> 2) == j ? ab + 64 * j : lds_off(zr) - 36, ab + 4 * j, xw, bp);
+                    else
+                        mf_ld_x8((r >> 3) == (j >> 1) ? ab + 128 * (j >> 1) + 8 * (j & 1) : lds_off(zr) - 36, ab + 4 * j,
+                                 xw, bp);
                 } else if (r < NC)
                     mf_ld_x(KH ? xr + ((size_t)li * NC + r) * MF_XB + MF_XO : xr + (size_t)r * XS + (size_t)li * 292, j,
                             xw, bp);
@@ -554,8 +589,18 @@ __device__ __forceinline__ void mf_body(const uint8_t * __restrict__ w, uint32_t
                 const uint32_t schi = (hd.w & 0x0F0F0F0Fu) | ((hd.y >> 2) & 0x30303030u);
                 const uint32_t mhi = ((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u);
                 v4i acc[8];
-                v4i a0 = {0, 0, 0, 0}, a1 = {0, 0, 0, 0};           // BD: sub-blocks 2j, 2j + 1
-                if constexpr (BD) {
+                v4i a0 = {0, 0, 0, 0}, a1 = {0, 0, 0, 0};           // NC = 4: sub-blocks 2j, 2j + 1
+                v4i ab8[4] = {};                                    // NC = 8: sub-blocks 4h + sl
+                if constexpr (NC == 8) {
+#pragma unroll
+                    for (int q = 0; q < 8; ++q) {                   // q = 4cc + 2n + m
+                        const u32x2 b = qb[2 * (q >> 2) + (q & 1)];
+                        const uint32_t b0 = (q & 2) ? (b.x >> 4) & 0x0F0F0F0Fu : b.x & 0x0F0F0F0Fu;
+                        const uint32_t b1 = (q & 2) ? (b.y >> 4) & 0x0F0F0F0Fu : b.y & 0x0F0F0F0Fu;
+                        ab8[q >> 1] = __builtin_amdgcn_mfma_i32_16x16x32_i8(
+                            __builtin_bit_cast(long, xw[q]), (long)(((uint64_t)b1 << 32) | b0), ab8[q >> 1], 0, 0, 0);
+                    }
+                } else if constexpr (NC == 4) {
                     const uint32_t q[8] = {qv[0].x, qv[0].y, qv[0].z, qv[0].w, qv[1].x, qv[1].y, qv[1].z, qv[1].w};
 #pragma unroll
                     for (int m = 0; m < 4; ++m) {
@@ -585,7 +630,28 @@ __device__ __forceinline__ void mf_body(const uint8_t * __restrict__ w, uint32_t
                 cm = __builtin_amdgcn_mfma_f32_16x16x4f32(bsa1, bm1, cm, 0, 0, 0);
                 // park: terms [li][row][column]
                 const uint32_t rl = 16 * t + r;                     // row within the batch
-                if constexpr (BD) {
+                if constexpr (NC == 8) {
+                    const uint32_t wsc = j < 2 ? sclo : schi;
+                    const int s0 = (int)(wsc & 0xFFu), s1 = (int)((wsc >> 8) & 0xFFu);
+                    const int s2 = (int)((wsc >> 16) & 0xFFu), s3 = (int)(wsc >> 24);
+                    int pr[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        pr[i] = __mul24(s0, ab8[0][i]) + __mul24(s1, ab8[1][i]) + __mul24(s2, ab8[2][i]) +
+                                __mul24(s3, ab8[3][i]);
+                    // lane rows 2h + e hold columns 4e + i of half h; the sum over h
+                    // leaves columns 4e + 2h, 4e + 2h + 1 in lane row 2h + e
+                    const auto u = __builtin_amdgcn_permlane32_swap((uint32_t)pr[0], (uint32_t)pr[2], false, false);
+                    const auto v = __builtin_amdgcn_permlane32_swap((uint32_t)pr[1], (uint32_t)pr[3], false, false);
+                    const size_t e = (size_t)li * mf_ts<NC>(nrb) + rl * NC;
+                    lds_st64(&TI[e + 4 * (j & 1) + 2 * (j >> 1)], u32x2{u[0] + u[1], v[0] + v[1]});
+                    if (j < 2)
+                        lds_st128(&TM[e + 4 * j], u32x4a{(uint32_t)(int)cm[0], (uint32_t)(int)cm[1],
+                                                          (uint32_t)(int)cm[2], (uint32_t)(int)cm[3]});
+                    if (j == 0) lds_st32(&TH[(size_t)li * mf_ths(nrb) + rl], hd.x);
+                    continue;
+                }
+                if constexpr (NC == 4) {
                     const uint32_t wsc = j < 2 ? sclo : schi, sh = 16 * (j & 1);
                     const int s0 = (int)((wsc >> sh) & 0xFFu), s1 = (int)((wsc >> (sh + 8)) & 0xFFu);
                     int pr[4];
