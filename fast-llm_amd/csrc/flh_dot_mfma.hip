@@ -11,7 +11,12 @@
 //
 // so lane l owns weight row r = l % 16 and activation columns 4*(l/16) + i,
 // and decodes only its own row's 6-bit scales.  The scale-weighted sum
-// iacc = sum_g sc_g * D_g is exact integer VALU work; the min term
+// iacc = sum_g sc_g * D_g is exact integer VALU work.  With 4 or 8 columns
+// the A operand is block-diagonal instead (the column block of A rows 4g..
+// (resp. 8h..) sees only k-slice g (resp. 2h, 2h + 1), and lane row g's B
+// slice carries its own sub-blocks), so no output row is idle: a lane holds
+// whole sub-block dots of 2 (resp. 4) sub-blocks and iacc is 8 (resp. 16)
+// products plus an exact cross-lane integer sum (permlane swaps).  The min term
 // imins = sum_g m_g * (bsum[2g] + bsum[2g+1]) is a 16x16x8 product done as two
 // v_mfma_f32_16x16x4f32 whose operands and sums are integers below 2^24, so
 // it is exact too.  The (row, column, superblock) integer terms are parked in
