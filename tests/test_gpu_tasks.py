@@ -31,8 +31,7 @@ def mk(flh, kind, **kw):
     return t
 
 
-def build(flh, gpu, rng):
-    cols = 1024
+def build(flh, gpu, rng, cols=1024):
     st = col_stride_floats(cols)
     xs = activations(2, cols, rng, outliers=True)
     xb = np.zeros(2 * st, dtype=np.float32)
@@ -113,20 +112,24 @@ def read(d, gpu):
             d["y8"].download(np.float32, 140, gpu), d["merged"].download(np.float32, 40, gpu))
 
 
-def test_task_table_bitwise(flh, orc, gpu):
-    print("[case] task table eager", flush=True)
-    d = build(flh, gpu, np.random.default_rng(7))
+# 14336 columns: the ACT_Q8 is wider than the per-workgroup fusion takes, so
+# it runs as a launch of its own ahead of the tiles
+@pytest.mark.parametrize("cols", [1024, 14336])
+def test_task_table_bitwise(flh, orc, gpu, cols):
+    print("[case] task table eager", cols, flush=True)
+    d = build(flh, gpu, np.random.default_rng(7), cols)
     zero_outputs(d, gpu)
     flh.exec_tasks(table(flh, d), gpu)
     for g, w in zip(read(d, gpu), expected(orc, d)):
         assert np.array_equal(bits(g), bits(w))
 
 
-def test_task_table_graph_replays(flh, orc, gpu):
+@pytest.mark.parametrize("cols", [1024, 14336])
+def test_task_table_graph_replays(flh, orc, gpu, cols):
     """Capture the table (and the zeroing) once, replay it several times with
     eager work in between; every replay equals the eager result."""
-    print("[case] task table graph", flush=True)
-    d = build(flh, gpu, np.random.default_rng(8))
+    print("[case] task table graph", cols, flush=True)
+    d = build(flh, gpu, np.random.default_rng(8), cols)
     want = expected(orc, d)
     tasks = table(flh, d)
     with flh.Graph.capture(gpu) as g:
