@@ -23,6 +23,7 @@ pytestmark = pytest.mark.gpu
     (14336, 4096, 2), (14336, 4096, 4), (14336, 4096, 8),
     (4096, 14336, 2), (4096, 14336, 4), (4096, 14336, 8),
     (20000, 512, 16), (300, 4096, 3), (17, 256, 2), (4100, 2048, 7), (40, 16384, 5),
+    (4096, 14336, 13), (100, 12288, 6),
 ])
 def test_mfma_multicol_bitwise(flh, orc, gpu, rows, cols, nx):
     say("mfma", rows, cols, nx)
