@@ -90,13 +90,23 @@ __host__ __device__ inline uint32_t mf_nsbh(uint32_t nsb, uint32_t h) {
 }
 // superblock of local index li of half h
 __device__ __forceinline__ uint32_t mf_sbh(uint32_t li, uint32_t h) { return 4 * (li >> 1) + 2 * h + (li & 1); }
-template <int NC, bool KH>
+// Activations in the chunk (XC, one 16-row tile per workgroup): each chunk's
+// DMA also brings its superblock's NC activation blocks, at MF_CHUNK + [NC][304]
+// of the stage (the K-halves slot layout); no whole-activation staging.  With
+// one tile per workgroup every activation block is used by exactly one chunk,
+// so this moves the same bytes as staging them whole, and where NC columns do
+// not fit whole (8 columns x 56 superblocks are 131 KB) it replaces K halves
+// (no half boundary, no restaging); the fold reads the q8_K scales from dkt.
+template <int NC> __host__ __device__ constexpr uint32_t mf_xci() { return (19 * NC + 63) / 64; }
+template <int NC, bool XC> __host__ __device__ constexpr uint32_t mf_stg() { return XC ? MF_CHUNK + NC * MF_XB : MF_CHUNK; }
+template <int NC, bool XC> __host__ __device__ constexpr int mf_ni() { return XC ? MF_NI + (int)mf_xci<NC>() : MF_NI; }
+template <int NC, bool KH, bool XC = false>
 __host__ __device__ inline size_t mf_smem_bytes(uint32_t nrb, uint32_t nsb, int D) {
     const uint32_t nl = KH ? mf_nsbh(nsb, 0) : nsb;
-    return (size_t)MF_WAVES * D * MF_CHUNK + (KH ? (size_t)nl * NC * MF_XB : (size_t)NC * mf_xs(nl)) +
-           (size_t)mf_ts<NC>(nrb) * nl * 8 +
-           (size_t)mf_ths(nrb) * nl * 4 + (size_t)nrb * NC * 4 + (KH ? (size_t)nrb * NC * 4 + (size_t)NC * nsb * 4 : 0) +
-           (NC <= 8 ? 128 : 0);
+    return (size_t)MF_WAVES * D * mf_stg<NC, XC>() +
+           (KH ? (size_t)nl * NC * MF_XB : XC ? 0 : (size_t)NC * mf_xs(nl)) + (size_t)mf_ts<NC>(nrb) * nl * 8 +
+           (size_t)mf_ths(nrb) * nl * 4 + (size_t)nrb * NC * 4 + (KH ? (size_t)nrb * NC * 4 : 0) +
+           (KH || XC ? (size_t)NC * nsb * 4 : 0) + (NC <= 8 ? 128 : 0);
 }
 
 // Column sources of one pass: activation column p at x(p) (fp32 x followed by
@@ -202,7 +212,7 @@ __device__ __forceinline__ int mf_rowsum_t(const int (&p)[4]) {
 template <int NC, int R>
 __device__ __forceinline__ void mf_fold(const int * TI, const int * TM, const uint32_t * TH, const uint8_t * xp,
                                         uint32_t nsb, uint32_t nrb, uint32_t k, uint32_t p, uint32_t rl0, uint32_t FR,
-                                        uint32_t nrow, bool fok, float (&res)[R]) {
+                                        uint32_t nrow, bool fok, float (&res)[R], uint32_t xps = 292) {
     float acc[R];
     uint32_t rl[R];
 #pragma unroll
@@ -224,7 +234,7 @@ __device__ __forceinline__ void mf_fold(const int * TI, const int * TM, const ui
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const uint32_t sq = s + 4 * q;
-                dk[q] = *(const float *)(xp + (size_t)sq * 292);
+                dk[q] = *(const float *)(xp + (size_t)sq * xps);
 #pragma unroll
                 for (int i = 0; i < R; ++i) {
                     ti[i][q] = TI[(size_t)sq * mf_ts<NC>(nrb) + rl[i] * NC + p];
@@ -238,7 +248,7 @@ __device__ __forceinline__ void mf_fold(const int * TI, const int * TM, const ui
                 for (int q = 0; q < 4; ++q) step(acc[i], ti[i][q], tm[i][q], th[i][q], dk[q]);
         }
         for (; s < nsb; s += 4) {
-            const float dk = *(const float *)(xp + (size_t)s * 292);
+            const float dk = *(const float *)(xp + (size_t)s * xps);
 #pragma unroll
             for (int i = 0; i < R; ++i)
                 step(acc[i], TI[(size_t)s * mf_ts<NC>(nrb) + rl[i] * NC + p],
@@ -321,7 +331,7 @@ __device__ __forceinline__ float mf_fold_h(const int * TI, const int * TM, const
 // 16-row tile of the batch; the batch's chunks q = (tile, sb), tile-major, are
 // dealt to the waves round-robin (with K halves: per half, the first half of
 // batch bt being half bt & 1, whose activations are staged already).
-template <int NC, int D, bool KH, typename COLS>
+template <int NC, int D, bool KH, typename COLS, bool XC = false>
 __device__ __forceinline__ void mf_body(const uint8_t * __restrict__ w, uint32_t rows, uint32_t cols,
                                         const COLS & C, uint32_t nx, uint32_t nrbp, uint32_t g, uint32_t G,
                                         uint8_t * sm) {
@@ -338,16 +348,19 @@ __device__ __forceinline__ void mf_body(const uint8_t * __restrict__ w, uint32_t
     auto nl_of = [&](uint32_t h) -> uint32_t { return KH ? mf_nsbh(nsb, h) : nsb; };
     auto sb_of = [&](uint32_t li, uint32_t h) -> uint32_t { return KH ? mf_sbh(li, h) : li; };
     const uint32_t NL = nl_of(0);                                 // superblocks held at once
-    uint8_t * myst = sm + (size_t)wave * D * MF_CHUNK;
-    const uint32_t XS = KH ? 0u : mf_xs(NL);
-    uint8_t * xr = sm + (size_t)MF_WAVES * D * MF_CHUNK;
+    static_assert(!(KH && XC), "one activation mode");
+    constexpr uint32_t STG = mf_stg<NC, XC>();                   // ring stage bytes
+    constexpr int NI = mf_ni<NC, XC>();                           // DMA instructions per chunk
+    uint8_t * myst = sm + (size_t)wave * D * STG;
+    const uint32_t XS = KH || XC ? 0u : mf_xs(NL);
+    uint8_t * xr = sm + (size_t)MF_WAVES * D * STG;
     int * TI = (int *)(xr + (KH ? (size_t)NL * NC * MF_XB : (size_t)NC * XS));
     int * TM = TI + (size_t)mf_ts<NC>(nrb) * NL;
     uint32_t * TH = (uint32_t *)(TM + (size_t)mf_ts<NC>(nrb) * NL);
     float * ysm = (float *)(TH + (size_t)mf_ths(nrb) * NL);
     float * yph = ysm + (size_t)nrb * NC;                         // KH: first half's sums
-    float * dkt = yph + (size_t)nrb * NC;                         // KH: q8_K scales [NC][nsb]
-    uint8_t * zr = KH ? (uint8_t *)(dkt + (size_t)NC * nsb) : (uint8_t *)yph;   // NC <= 8: zeros
+    float * dkt = KH ? yph + (size_t)nrb * NC : yph;              // KH, XC: q8_K scales [NC][nsb]
+    uint8_t * zr = KH || XC ? (uint8_t *)(dkt + (size_t)NC * nsb) : (uint8_t *)yph;   // NC <= 8: zeros
     // NC = 4: each MFMA's A is block-diagonal (rows 4g .. 4g + 3 = the four
     // columns on k-slice g only), so one wave's 8 MFMAs give every lane row j
     // the dots of sub-blocks 2j, 2j + 1 for the 4 columns: the scale-weighted
@@ -387,8 +400,8 @@ __device__ __forceinline__ void mf_body(const uint8_t * __restrict__ w, uint32_t
         }
         return cnt;
     };
-    if constexpr (KH) {
-        stage_slots(0, 0, nl_of(0), wave, MF_WAVES);
+    if constexpr (KH || XC) {
+        if constexpr (KH) stage_slots(0, 0, nl_of(0), wave, MF_WAVES);
         for (uint32_t i = wave; i < (NC * nsb + 63) / 64; i += MF_WAVES) {
             const uint32_t e = 64 * i + lane;
             if (e < NC * nsb) {
@@ -463,12 +476,20 @@ __device__ __forceinline__ void mf_body(const uint8_t * __restrict__ w, uint32_t
             const uint32_t tr0 = rbeg + qbt * nrb + 16 * qt;
             const uint32_t nv1 = min(16u, rend - tr0) - 1;           // last valid row of the tile
             const uint8_t * base = w + (size_t)tr0 * rb + (size_t)sb_of(qsb, half_of(qbt, qph)) * 144;
-            uint8_t * stage = myst + (nissued % D) * MF_CHUNK;
+            uint8_t * stage = myst + (nissued % D) * STG;
             __builtin_amdgcn_global_load_lds(GPTR(base + (size_t)min(pr0, nv1) * rb + po0), LPTR(stage), 16, 0, FLH_MF_AUX);
             __builtin_amdgcn_global_load_lds(GPTR(base + (size_t)min(pr1, nv1) * rb + po1), LPTR(stage + 1024), 16, 0,
                                              FLH_MF_AUX);
             __builtin_amdgcn_global_load_lds(GPTR(base + (size_t)min(pr2, nv1) * rb + po2), LPTR(stage + 2048), 4, 0,
                                              FLH_MF_AUX);
+            if constexpr (XC) {
+                const size_t so = (size_t)sb_of(qsb, half_of(qbt, qph)) * 292;
+#pragma unroll
+                for (uint32_t i = 0; i < NIR; ++i)
+                    if (64 * i + lane < 19 * NC)
+                        __builtin_amdgcn_global_load_lds(GPTR(rsrc[i] + so), LPTR(stage + MF_CHUNK + 1024 * i), 16, 0,
+                                                         0);
+            }
             if constexpr (KH) {
                 vm += MF_NI;
                 ce1 = (nissued & 1) ? vm : ce1;
@@ -499,7 +520,7 @@ __device__ __forceinline__ void mf_body(const uint8_t * __restrict__ w, uint32_t
     // ring after the first chunk is consumed
     for (uint32_t k = 0; k < pro; ++k) issue_one();
     // the activation and y DMAs are older than the nissued chunks
-    ks_wait_behind<MF_NI, D + 1>(nissued);
+    ks_wait_behind<NI, D + 1>(nissued);
     lds_barrier();
     MF_STAMP(1);
 
@@ -530,13 +551,14 @@ __device__ __forceinline__ void mf_body(const uint8_t * __restrict__ w, uint32_t
             }
             for (; ct < nt;) {
                 if constexpr (KH) mf_wait_vm(vm - (((ncons & 1) ? ce1 : 0u) | ((ncons & 1) ? 0u : ce0)));
-                else ks_wait_behind<MF_NI, D>(nissued - 1 - ncons);
+                else ks_wait_behind<NI, D>(nissued - 1 - ncons);
                 ++ncons;
                 if (ncons == 1) MF_STAMP(2);
                 const uint32_t t = ct, li = csb;
                 csb += MF_WAVES;
                 while (csb >= nl) { csb -= nl; ++ct; }
-                const uint8_t * rp = myst + slot * MF_CHUNK + 144 * r;
+                const uint8_t * rp = myst + slot * STG + 144 * r;
+                const uint8_t * xs_c = myst + slot * STG + MF_CHUNK + MF_XO;   // XC: column blocks, 304 B apart
                 const u32x4a hd = *(const u32x4a *)rp;
                 uint32_t qw[4][2];
                 u32x4a qv[2];                                       // NC = 4: qs bytes 32j .. 32j + 31
@@ -561,16 +583,18 @@ __device__ __forceinline__ void mf_body(const uint8_t * __restrict__ w, uint32_t
                 u32x2 bp = {};
                 if constexpr (BD) {
                     // column r % NC (rows NC .. 15 of the min term are never stored)
-                    const uint32_t ab = lds_off(KH ? xr + ((size_t)li * NC + (r & (NC - 1))) * MF_XB + MF_XO
-                                                   : xr + (size_t)(r & (NC - 1)) * XS + (size_t)li * 292);
+                    const uint32_t ab = lds_off(XC ? xs_c + (size_t)(r & (NC - 1)) * MF_XB
+                                                : KH ? xr + ((size_t)li * NC + (r & (NC - 1))) * MF_XB + MF_XO
+                                                     : xr + (size_t)(r & (NC - 1)) * XS + (size_t)li * 292);
                     if constexpr (NC == 4)
                         mf_ld_x4((r >> 2) == j ? ab + 64 * j : lds_off(zr) - 36, ab + 4 * j, xw, bp);
                     else
                         mf_ld_x8((r >> 3) == (j >> 1) ? ab + 128 * (j >> 1) + 8 * (j & 1) : lds_off(zr) - 36, ab + 4 * j,
                                  xw, bp);
                 } else if (r < NC)
-                    mf_ld_x(KH ? xr + ((size_t)li * NC + r) * MF_XB + MF_XO : xr + (size_t)r * XS + (size_t)li * 292, j,
-                            xw, bp);
+                    mf_ld_x(XC ? xs_c + (size_t)r * MF_XB
+                               : KH ? xr + ((size_t)li * NC + r) * MF_XB + MF_XO : xr + (size_t)r * XS + (size_t)li * 292,
+                            j, xw, bp);
                 const uint32_t bp0 = bp.x, bp1 = bp.y;
                 // every read of this stage is done before it is refilled
                 WAIT_LGKM0();
@@ -714,7 +738,7 @@ __device__ __forceinline__ void mf_body(const uint8_t * __restrict__ w, uint32_t
                 }
             }
         }
-        if (!KH && y_mine) ks_wait_behind<MF_NI, D + 1>(min(nissued - y_at, (uint32_t)D));
+        if (!KH && y_mine) ks_wait_behind<NI, D + 1>(min(nissued - y_at, (uint32_t)D));
         if (KH && y_mine) mf_wait_vm(vm - y_vm);
         lds_barrier();
         MF_STAMP(3);
@@ -730,10 +754,10 @@ __device__ __forceinline__ void mf_body(const uint8_t * __restrict__ w, uint32_t
         if constexpr (!KH) {
             // every row of the batch in one call (nrow <= nrb <= 512 / NC = 4 FROWS)
             const bool fok = fp < nx;
-            const uint8_t * xp = xr + (size_t)fp * XS;
+            const uint8_t * xp = XC ? (const uint8_t *)(dkt + (size_t)fp * nsb) : xr + (size_t)fp * XS;
             auto fold_store = [&](auto & rr) {
                 constexpr int R = sizeof(rr) / sizeof(float);
-                mf_fold<NC, R>(TI, TM, TH, xp, nsb, nrb, fk, fp, frl0, FROWS, nrow, fok, rr);
+                mf_fold<NC, R>(TI, TM, TH, xp, nsb, nrb, fk, fp, frl0, FROWS, nrow, fok, rr, XC ? 4u : 292u);
 #pragma unroll
                 for (int i = 0; i < R; ++i) {
                     const uint32_t frl = frl0 + FROWS * i;
@@ -757,12 +781,12 @@ __device__ __forceinline__ void mf_body(const uint8_t * __restrict__ w, uint32_t
     MF_STAMP(4);
 }
 
-template <int NC, int D, bool KH>
+template <int NC, int D, bool KH, bool XC = false>
 __global__ __launch_bounds__(512) void k_dot_mfma(DotArgs a, uint32_t nrb) {
     extern __shared__ __attribute__((aligned(16))) uint8_t sm[];
     const uint8_t * w = a.w + (a.id_slot ? (size_t)(*a.id_slot) * a.estride : 0);
     const MfColsStrided C{a.x, a.y, a.xstride, a.ystride};
-    mf_body<NC, D, KH>(w, a.rows, a.cols, C, a.nx, nrb, blockIdx.x, gridDim.x, sm);
+    mf_body<NC, D, KH, MfColsStrided, XC>(w, a.rows, a.cols, C, a.nx, nrb, blockIdx.x, gridDim.x, sm);
 }
 
 // Grouped expert matvec (MoE): the routed experts share the grid (moe_assign).  The workgroup collects
@@ -824,10 +848,11 @@ static uint32_t mf_pro() {
     }();
     return v;
 }
-template <int NC, int D, bool KH>
+template <int NC, int D, bool KH, bool XC = false>
 static int mf_launch_d(const DotArgs & a, uint32_t nrb, uint32_t grid, size_t smb, hipStream_t s) {
-    (void)hipFuncSetAttribute((const void *)k_dot_mfma<NC, D, KH>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smb);
-    hipLaunchKernelGGL((k_dot_mfma<NC, D, KH>), dim3(grid), dim3(MF_WAVES * 64), smb, s, a,
+    (void)hipFuncSetAttribute((const void *)k_dot_mfma<NC, D, KH, XC>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)smb);
+    hipLaunchKernelGGL((k_dot_mfma<NC, D, KH, XC>), dim3(grid), dim3(MF_WAVES * 64), smb, s, a,
                        nrb | (mf_pro() << 16));
     return hip_check(hipGetLastError(), "k_dot_mfma launch");
 }
@@ -841,7 +866,7 @@ size_t lds_limit();
 // fits.
 template <int NC>
 static int mf_plan_kh(uint32_t rows, uint32_t nsb, uint32_t G, uint32_t & nrb, int & D, bool & kh, size_t & smb,
-                      bool allow_kh = true) {
+                      bool allow_kh = true, bool * xc = nullptr) {
     const size_t lim = lds_limit() - 4096;                    // the MoE kernel's static tables
     const uint32_t rpw = (rows + G - 1) / G;
     // a batch's old y values are one 64-float DMA per wave: nrb * NC <= 512
@@ -861,6 +886,17 @@ static int mf_plan_kh(uint32_t rows, uint32_t nsb, uint32_t G, uint32_t & nrb, i
         if (got == 3) force_kh = (int)k;
     }
     kh = force_kh == 1 || (force_kh != 0 && mf_smem_bytes<NC, false>(16, nsb, 2) > lim);
+    // one 16-row tile per workgroup: activations in the chunks instead of halves
+    // (FLH_MFMA_XC=0 disables)
+    static const bool xc_on = [] { const char * e = getenv("FLH_MFMA_XC"); return !e || atoi(e) != 0; }();
+    if (xc) *xc = false;
+    if (xc && kh && force_kh != 1 && xc_on && nrb == 16 && mf_smem_bytes<NC, false, true>(16, nsb, 2) <= lim) {
+        *xc = true;
+        kh = false;
+        D = 2;
+        smb = mf_smem_bytes<NC, false, true>(16, nsb, 2);
+        return FLH_OK;
+    }
     if (kh && (nsb < 8 || (!allow_kh && force_kh != 1))) kh = false;
     if (kh) D = 2;                                            // the K-halves waits assume it
     auto bytes = [&]() { return kh ? mf_smem_bytes<NC, true>(nrb, nsb, D) : mf_smem_bytes<NC, false>(nrb, nsb, D); };
@@ -878,7 +914,9 @@ static int mf_launch(const DotArgs & a, hipStream_t s) {
     int D;
     bool kh;
     size_t smb;
-    if (mf_plan_kh<NC>(a.rows, nsb, G, nrb, D, kh, smb)) return FLH_ERR_UNSUPPORTED;
+    bool xc;
+    if (mf_plan_kh<NC>(a.rows, nsb, G, nrb, D, kh, smb, true, &xc)) return FLH_ERR_UNSUPPORTED;
+    if (xc) return mf_launch_d<NC, 2, false, true>(a, nrb, G, smb, s);
     if (kh) return mf_launch_d<NC, 2, true>(a, nrb, G, smb, s);
     return D == 2 ? mf_launch_d<NC, 2, false>(a, nrb, G, smb, s) : mf_launch_d<NC, 3, false>(a, nrb, G, smb, s);
 }

@@ -5,7 +5,10 @@ Bar: bitwise against the oracle (the reference's fl_dot_i8k_q4_K per column,
 src/runtime/quants.h:538-561), at the speculative-verify shapes of the
 benchmark (14336x4096 and 4096x14336, N in {2, 4, 8}) and at shapes that
 exercise partial 16-row tiles, several row batches per workgroup, column
-groups (the 14336-column plan holds 4 columns) and the 16-column maximum.
+groups (the 14336-column plan holds 4 columns), the 16-column maximum, and
+one 16-row tile per workgroup with 5-8 columns of 48-64 superblocks, where each
+chunk's DMA carries its own activation blocks (4096x14336 N=8, 250x14336 N=7,
+100x12288 N=6, 40x16384 N=5).
 """
 import os
 
@@ -23,7 +26,7 @@ pytestmark = pytest.mark.gpu
     (14336, 4096, 2), (14336, 4096, 4), (14336, 4096, 8),
     (4096, 14336, 2), (4096, 14336, 4), (4096, 14336, 8),
     (20000, 512, 16), (300, 4096, 3), (17, 256, 2), (4100, 2048, 7), (40, 16384, 5),
-    (4096, 14336, 13), (100, 12288, 6),
+    (4096, 14336, 13), (100, 12288, 6), (250, 14336, 7),
 ])
 def test_mfma_multicol_bitwise(flh, orc, gpu, rows, cols, nx):
     say("mfma", rows, cols, nx)
