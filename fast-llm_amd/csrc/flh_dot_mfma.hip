@@ -888,9 +888,10 @@ static int mf_plan_kh(uint32_t rows, uint32_t nsb, uint32_t G, uint32_t & nrb, i
     kh = force_kh == 1 || (force_kh != 0 && mf_smem_bytes<NC, false>(16, nsb, 2) > lim);
     // one 16-row tile per workgroup: activations in the chunks instead of halves
     // (FLH_MFMA_XC=0 disables)
-    static const bool xc_on = [] { const char * e = getenv("FLH_MFMA_XC"); return !e || atoi(e) != 0; }();
+    static const int xc_mode = [] { const char * e = getenv("FLH_MFMA_XC"); return e ? atoi(e) : 1; }();
     if (xc) *xc = false;
-    if (xc && kh && force_kh != 1 && xc_on && nrb == 16 && mf_smem_bytes<NC, false, true>(16, nsb, 2) <= lim) {
+    if (xc && (kh || xc_mode == 2) && force_kh != 1 && xc_mode && nrb == 16 &&
+        mf_smem_bytes<NC, false, true>(16, nsb, 2) <= lim) {
         *xc = true;
         kh = false;
         D = 2;
