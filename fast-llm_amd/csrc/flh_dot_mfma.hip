@@ -887,16 +887,22 @@ static int mf_plan_kh(uint32_t rows, uint32_t nsb, uint32_t G, uint32_t & nrb, i
     }
     kh = force_kh == 1 || (force_kh != 0 && mf_smem_bytes<NC, false>(16, nsb, 2) > lim);
     // one 16-row tile per workgroup: activations in the chunks instead of halves
-    // (FLH_MFMA_XC=0 disables)
+    // (FLH_MFMA_XC: 0 off; 2 also where they fit whole; 3 also with several
+    // tiles per batch, re-fetching them per tile -- measured slower, kept for
+    // development sweeps)
     static const int xc_mode = [] { const char * e = getenv("FLH_MFMA_XC"); return e ? atoi(e) : 1; }();
     if (xc) *xc = false;
-    if (xc && (kh || xc_mode == 2) && force_kh != 1 && xc_mode && nrb == 16 &&
-        mf_smem_bytes<NC, false, true>(16, nsb, 2) <= lim) {
-        *xc = true;
-        kh = false;
-        D = 2;
-        smb = mf_smem_bytes<NC, false, true>(16, nsb, 2);
-        return FLH_OK;
+    if (xc && (kh || xc_mode >= 2) && force_kh != 1 && xc_mode && (nrb == 16 || xc_mode == 3)) {
+        uint32_t n = nrb;
+        while (mf_smem_bytes<NC, false, true>(n, nsb, 2) > lim && n > 16) n -= 16;
+        if (mf_smem_bytes<NC, false, true>(n, nsb, 2) <= lim) {
+            *xc = true;
+            kh = false;
+            D = 2;
+            nrb = n;
+            smb = mf_smem_bytes<NC, false, true>(n, nsb, 2);
+            return FLH_OK;
+        }
     }
     if (kh && (nsb < 8 || (!allow_kh && force_kh != 1))) kh = false;
     if (kh) D = 2;                                            // the K-halves waits assume it
