@@ -123,8 +123,8 @@ def main():
                          "the matrix-core kernel), no JSON line")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py: this build measures one GPU only (the matvec shards by rows; "
-              "see DESIGN.md); run with --gpus 1", file=sys.stderr)
+        print("bench.py: this build measures one GPU only (the matvec would shard by "
+              "rows across GPUs; no multi-GPU path is built); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
 
     import __graft_entry__ as ge
