@@ -67,6 +67,12 @@ __device__ __forceinline__ uint32_t alignb(uint32_t hi, uint32_t lo, uint32_t sh
     return __builtin_amdgcn_alignbyte(hi, lo, sh);
 }
 
+// floor(i / n) by multiply-high, exact for i < 2^16 and 1 <= n < 2^16:
+// m = div_magic(n) = ceil(2^32 / n), which does not fit 32 bits for n == 1
+// (stored as 0: the quotient is i itself).
+__host__ __device__ inline uint32_t div_magic(uint32_t n) { return (uint32_t)((0x100000000ull + n - 1) / n); }
+__device__ __forceinline__ uint32_t div_small(uint32_t i, uint32_t m) { return m ? __umulhi(i, m) : i; }
+
 // DPP quad permutations: exchange with lane^1 / lane^2 inside each quad.
 __device__ __forceinline__ int qx1(int v) {
     return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);   // [1,0,3,2]
@@ -76,6 +82,36 @@ __device__ __forceinline__ int qx2(int v) {
 }
 __device__ __forceinline__ float qx1f(float v) { return __int_as_float(qx1(__float_as_int(v))); }
 __device__ __forceinline__ float qx2f(float v) { return __int_as_float(qx2(__float_as_int(v))); }
+// DPP row mirrors: lane i <- lane 7-i inside each 8-lane half row, and lane
+// i <- lane 15-i inside each 16-lane row.
+__device__ __forceinline__ int hmir(int v) { return __builtin_amdgcn_mov_dpp(v, 0x141, 0xF, 0xF, false); }
+__device__ __forceinline__ int rmir(int v) { return __builtin_amdgcn_mov_dpp(v, 0x140, 0xF, 0xF, false); }
+
+// Cross-lane reductions on the VALU (DPP and readlane; ds_bpermute-based
+// shuffles go through the LDS pipe, which the weight DMA keeps busy).  The
+// max works on the bits of non-negative floats (same order, no NaN handling
+// needed); integer sums are exact.  Every lane of the group gets the result;
+// all 64 lanes must be active.
+__device__ __forceinline__ uint32_t umax8(uint32_t v) {
+    v = max(v, (uint32_t)qx1((int)v));
+    v = max(v, (uint32_t)qx2((int)v));
+    return max(v, (uint32_t)hmir((int)v));
+}
+__device__ __forceinline__ uint32_t umax64(uint32_t v) {
+    v = umax8(v);
+    v = max(v, (uint32_t)rmir((int)v));
+    const uint32_t a = max((uint32_t)__builtin_amdgcn_readlane((int)v, 0), (uint32_t)__builtin_amdgcn_readlane((int)v, 16));
+    const uint32_t b = max((uint32_t)__builtin_amdgcn_readlane((int)v, 32), (uint32_t)__builtin_amdgcn_readlane((int)v, 48));
+    return max(a, b);
+}
+__device__ __forceinline__ int sum4i(int v) {
+    v += qx1(v);
+    return v + qx2(v);
+}
+__device__ __forceinline__ int sum8i(int v) {
+    v = sum4i(v);
+    return v + hmir(v);
+}
 
 // Plain 4-byte-aligned global loads (dword alignment is all gfx950 needs
 // for multi-dword global loads).

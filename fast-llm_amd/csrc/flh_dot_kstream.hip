@@ -28,19 +28,6 @@
 
 namespace flh {
 
-// Development timing probe (compiled only with -DFLH_TRACE): per workgroup,
-// s_memrealtime stamps at entry, after activation staging, at the first
-// landed chunk, after the last chunk and at exit.
-#ifdef FLH_TRACE
-__device__ uint64_t g_ks_trace[8192 * 6];
-#define KS_STAMP(k) do { if (threadIdx.x == 0 && blockIdx.x < 8192) { \
-    g_ks_trace[(size_t)blockIdx.x * 6 + (k)] = __builtin_amdgcn_s_memrealtime(); \
-    if ((k) == 0) g_ks_trace[(size_t)blockIdx.x * 6 + 5] = \
-        ((uint64_t)__builtin_amdgcn_s_getreg((20) | (0 << 6) | (3 << 11)) << 32) | \
-        (uint64_t)__builtin_amdgcn_s_getreg((4) | (0 << 6) | (31 << 11)); } } while (0)
-#else
-#define KS_STAMP(k) do { } while (0)
-#endif
 
 // One pass over rows [0, rows) of the matrix at w for nx <= NX columns; the
 // workgroup g of G owns the contiguous rows [rows*g/G, rows*(g+1)/G) (an
@@ -88,26 +75,56 @@ __device__ __forceinline__ void ks_body(const uint8_t * __restrict__ w, uint32_t
     // the chunks really issued after it.
     uint32_t qbt = 0, qci = 0, qn = qbt < nbatch ? nci_of(qbt) : 0;
     uint32_t nissued = 0, ncons = 0;
-    auto issue_one = [&]() {
-        uint8_t * stage = myst + (nissued % D) * WIN;
+    // Next chunk of the sequence: its batch's weight base, batch-local chunk
+    // index and superblock count; false past the end.
+    auto next_chunk = [&](const uint8_t *& base, uint32_t & ch, uint32_t & nsbb) -> bool {
         while (qbt < nbatch && qci >= qn) {
             ++qbt;
             qci = 0;
             qn = qbt < nbatch ? nci_of(qbt) : 0;
         }
-        if (qbt < nbatch) {
-            ks_issue<FMT>(w + (size_t)(rbeg + qbt * nr) * rb, wave + KW * qci, min(nr, rend - rbeg - qbt * nr) * nsb,
-                          stage, lane);
+        if (qbt >= nbatch) return false;
+        base = w + (size_t)(rbeg + qbt * nr) * rb;
+        ch = wave + KW * qci;
+        nsbb = min(nr, rend - rbeg - qbt * nr) * nsb;
+        return true;
+    };
+    auto issue_one = [&]() {
+        const uint8_t * base;
+        uint32_t ch, nsbb;
+        if (next_chunk(base, ch, nsbb)) {
+            ks_issue<FMT>(base, ch, nsbb, myst + (nissued % D) * WIN, lane);
             ++qci;
             ++nissued;
         }
     };
     // The first D chunks of the sequence are issued right after the
-    // activation loads.
-    auto prologue = [&]() {
+    // activation loads.  The first DMA is issued unconditionally (a wave with
+    // no chunk re-reads the workgroup's first superblock into its idle stage),
+    // so the compiler knows exactly NI loads follow the activation loads and
+    // waits for the activation alone (vmcnt(NI)) instead of for the first
+    // weight chunk as well.
+    // Returns the number of chunk DMAs issued (the dummy counts: the caller
+    // waits for the loads issued before them).
+    auto prologue = [&]() -> uint32_t {
+        const uint8_t * base = w + (size_t)rbeg * rb;
+        uint32_t ch = 0, nsbb = 1;
+        const bool real = next_chunk(base, ch, nsbb);
+        ks_issue<FMT>(base, ch, nsbb, myst, lane);
+        uint32_t n = 1;
+        if (real) {
+            ++qci;
+            ++nissued;
 #pragma unroll
-        for (int j = 0; j < D; ++j)
-            if ((uint32_t)j < pro) issue_one();
+            for (int j = 1; j < D; ++j) {
+                if ((uint32_t)j < pro) {
+                    const uint32_t before = nissued;
+                    issue_one();
+                    n += nissued - before;
+                }
+            }
+        }
+        return n;
     };
 
     // The batch's old y values (y += semantics) go to LDS by a DMA of wave 0:
@@ -129,8 +146,8 @@ __device__ __forceinline__ void ks_body(const uint8_t * __restrict__ w, uint32_t
     issue_y(0);
 
     // ---- activation records, once per workgroup (overlaps the first weight DMAs)
-    if constexpr (FUSE) ks_x_fuse<FMT, NX, KW>(C, nx, nsb, cols, xr, xd, g == 0, prologue);
-    else ks_x_app<FMT, NX>(C, nx, nsb, cols, xr, xd, prologue);
+    if constexpr (FUSE) ks_x_fuse<FMT, NX, NI, D, KW>(C, nx, nsb, cols, xr, xd, g == 0, prologue);
+    else ks_x_app<FMT, NX, NI, D>(C, nx, nsb, cols, xr, xd, prologue);
     lds_barrier();
     KS_STAMP(1);
 
@@ -141,7 +158,7 @@ __device__ __forceinline__ void ks_body(const uint8_t * __restrict__ w, uint32_t
 #pragma unroll
         for (int p = 0; p < NX; ++p) lds_ld_rec(xr + (((size_t)p * nsb + (s & (nsb - 1))) * 4 + c) * XREC, xregs[p]);
     }
-    const uint32_t magic = (uint32_t)((0x100000000ull + nsb - 1) / nsb);   // f / nsb, f < 2^16
+    const uint32_t magic = div_magic(nsb);                        // f / nsb, f < 2^16
     const uint32_t fk = tid & 3, fp = (tid >> 2) % NX, frl = tid / (4 * NX);
     uint32_t slot = 0;                                            // ring stage of the next chunk
 
@@ -163,7 +180,7 @@ __device__ __forceinline__ void ks_body(const uint8_t * __restrict__ w, uint32_t
             const uint32_t f = (wave + KW * i) * 16 + s;           // batch-local superblock
             const bool act = f < nsbb;
             const uint32_t ff = act ? f : nsbb - 1;
-            const uint32_t rl = __umulhi(ff, magic);
+            const uint32_t rl = div_small(ff, magic);
             const uint32_t sb = ff - rl * nsb;
             int ia[NX], im[NX];
             uint32_t tag;
@@ -260,10 +277,12 @@ static KsTune ks_tune() {
 }
 
 // Chunks each wave requests before the activation is staged (the rest of its
-// ring is requested after its first chunk): a smaller launch-time burst lands
-// the first chunks sooner (measured: Q4_K 4096x4096 5.6 -> 5.3 us, others
-// unchanged).
-static uint32_t ks_pro() { return ks_tune().pro ? ks_tune().pro : 1u; }
+// ring is requested after its first chunk).  Reading a ready q8_K appendix
+// takes about as long as the first chunk, and a smaller launch-time burst
+// lands that chunk sooner: one (measured: Q4_K 4096x4096 5.6 -> 5.3 us).  A
+// fused ACT_Q8 keeps the waves busy quantising well after the first chunk
+// has landed: the whole ring (layer step 41.7 -> 40.3 us).
+static uint32_t ks_pro(bool fuse) { return ks_tune().pro ? ks_tune().pro : fuse ? 2u : 1u; }
 
 static size_t g_lds_limit = 0;
 size_t lds_limit() {
@@ -283,7 +302,7 @@ static int ks_launch_x(const DotArgs & a, uint32_t nr, uint32_t grid, size_t smb
     if (smb > 65536)
         (void)hipFuncSetAttribute((const void *)k_dot_kstream<FMT, NX, D, FUSE, XREG>,
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)smb);
-    hipLaunchKernelGGL((k_dot_kstream<FMT, NX, D, FUSE, XREG>), dim3(grid), dim3(256), smb, s, a, nr | (ks_pro() << 16));
+    hipLaunchKernelGGL((k_dot_kstream<FMT, NX, D, FUSE, XREG>), dim3(grid), dim3(256), smb, s, a, nr | (ks_pro(FUSE) << 16));
     return hip_check(hipGetLastError(), "k_dot_kstream launch");
 }
 template <int FMT, int NX, int D, bool FUSE>
@@ -343,7 +362,7 @@ static int ks_launch(const DotArgs & a, hipStream_t s) {
                 const uint32_t grid = a.rows < slots ? a.rows : slots;
                 auto go = [&](auto kern) {
                     (void)hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smb);
-                    hipLaunchKernelGGL(kern, dim3(grid), dim3(512), smb, s, a, nr | (ks_pro() << 16));
+                    hipLaunchKernelGGL(kern, dim3(grid), dim3(512), smb, s, a, nr | (ks_pro(FUSE) << 16));
                     return hip_check(hipGetLastError(), "k_dot_kstream launch");
                 };
                 if (16 % nsb == 0) return go(k_dot_kstream<FMT, 1, 2, FUSE, true, 8>);
@@ -367,7 +386,7 @@ static int ks_launch(const DotArgs & a, hipStream_t s) {
 template <int FMT, int NX, int D, bool XREG>
 static int moe_launch_x(const MoeArgs & a, uint32_t nr, uint32_t gx, size_t smb, hipStream_t s) {
     if (moe_rows(a) == 0) return FLH_OK;
-    hipLaunchKernelGGL((k_moe_kstream<FMT, NX, D, XREG>), dim3(gx, moe_rows(a)), dim3(256), smb, s, a, nr | (ks_pro() << 16));
+    hipLaunchKernelGGL((k_moe_kstream<FMT, NX, D, XREG>), dim3(gx, moe_rows(a)), dim3(256), smb, s, a, nr | (ks_pro(false) << 16));
     return hip_check(hipGetLastError(), "k_moe_kstream launch");
 }
 template <int FMT, int NX, int D>

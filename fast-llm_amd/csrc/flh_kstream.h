@@ -20,6 +20,22 @@
 
 namespace flh {
 
+// Development timing probe (compiled only with -DFLH_TRACE): per workgroup of
+// the streaming kernel, s_memrealtime stamps at entry (0), after activation
+// staging (1), at the first landed chunk (2), after the last chunk (3), at
+// exit (4), when the activation loads have landed (5), before the staging
+// barrier (6); slot 7 holds the hardware ids (XCC_ID << 32 | HW_ID).
+#ifdef FLH_TRACE
+__device__ uint64_t g_ks_trace[8192 * 16];
+#define KS_STAMP(k) do { if (threadIdx.x == 0 && blockIdx.x < 8192) { \
+    g_ks_trace[(size_t)blockIdx.x * 16 + (k)] = __builtin_amdgcn_s_memrealtime(); \
+    if ((k) == 0) g_ks_trace[(size_t)blockIdx.x * 16 + 15] = \
+        ((uint64_t)__builtin_amdgcn_s_getreg((20) | (0 << 6) | (3 << 11)) << 32) | \
+        (uint64_t)__builtin_amdgcn_s_getreg((4) | (0 << 6) | (31 << 11)); } } while (0)
+#else
+#define KS_STAMP(k) do { } while (0)
+#endif
+
 #define GPTR(p) ((const void __attribute__((address_space(1))) *)(p))
 #define LPTR(p) ((void __attribute__((address_space(3))) *)(p))
 
@@ -70,6 +86,36 @@ __device__ __forceinline__ void lds_ld_rec(const void * p, u32x4a (&v)[5]) {
                  "ds_read_b128 %3, %5 offset:48\n\tds_read_b128 %4, %5 offset:64\n\ts_waitcnt lgkmcnt(0)"
                  : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]) : "v"(lds_off(p)) : "memory");
 }
+
+// Activation loads hidden from the compiler's wait-count pass.  A register
+// load followed by direct-to-LDS DMAs makes the compiler wait for every DMA
+// (vmcnt(0)) before the loaded value is used, i.e. for the first weight
+// chunks as well.  These loads are issued before the weight prologue; the
+// caller then waits with ks_wait_behind for exactly the DMAs issued after them
+// and passes the values through xfence() before use (the fence orders the uses
+// after that wait; each value stays in the register the load wrote).
+__device__ __forceinline__ u32x4a gld_x4(const void * p) {
+    u32x4a r;
+    asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(r) : "v"(p) : "memory");
+    return r;
+}
+__device__ __forceinline__ uint32_t gld_x1(const void * p) {
+    uint32_t r;
+    asm volatile("global_load_dword %0, %1, off" : "=v"(r) : "v"(p) : "memory");
+    return r;
+}
+__device__ __forceinline__ uint32_t gld_xs16(const void * p) {      // sign-extended int16
+    uint32_t r;
+    asm volatile("global_load_sshort %0, %1, off" : "=v"(r) : "v"(p) : "memory");
+    return r;
+}
+__device__ __forceinline__ uint32_t gld_xu16(const void * p) {
+    uint32_t r;
+    asm volatile("global_load_ushort %0, %1, off" : "=v"(r) : "v"(p) : "memory");
+    return r;
+}
+__device__ __forceinline__ void xfence(u32x4a & v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void xfence(uint32_t & v) { asm volatile("" : "+v"(v)); }
 
 template <int FMT> struct KS;
 template <> struct KS<FMT_Q4_K> {
@@ -207,156 +253,175 @@ __device__ __forceinline__ T col_pick(T const (&v)[NX], uint32_t p) {
     return (T)r;
 }
 
-__device__ __forceinline__ uint32_t ks_quant16(const u32x4a (&raw)[4], float id, int & sum, uint32_t (&pk)[4]) {
+// ---------------------------------------------------------------- ACT_Q8 --
+// One wave quantises one 256-element chunk: lane i holds elements 4i..4i+3
+// in v.  Writes the chunk's q8_1 blocks (8-lane groups) and its q8_K block
+// with the bytes of fl_quantize_q8_1_block / fl_quantize_q8_K_block
+// (src/runtime/quants.h:360-402): amax is a max (order free), d = amax/127
+// and id = 127/amax are correctly rounded IEEE divisions, q = roundf(x*id)
+// clamped to +-127, sums are exact integers, halves are RNE.
+// q = roundf(y) clamped to [-127, 127] (the reference quantizers' step), as
+// an integer: for every float |y| <= 128.5, trunc(y + copysign(0.5 - 2^-25, y))
+// equals roundf(y) (checked exhaustively over all such floats; a CPU test
+// pins the cases near every integer and half-integer), v_cvt_i32_f32
+// truncates, and larger |y| saturate to +-127 either way.
+__device__ __forceinline__ int q8_round(float y) {
+    const float t = y + __builtin_copysignf(0.49999997f, y);
+    const int q = (int)t;
+    return q < -127 ? -127 : q > 127 ? 127 : q;
+}
+// four values quantised with scale id, packed little-endian as int8
+__device__ __forceinline__ uint32_t quant4(const float (&v)[4], float id) {
+    uint32_t packed = 0;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const uint32_t r4[4] = {raw[k].x, raw[k].y, raw[k].z, raw[k].w};
-        pk[k] = 0;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            float qv = roundf(__uint_as_float(r4[j]) * id);
-            if (qv > 127.f) qv = 127.f;
-            if (qv < -127.f) qv = -127.f;
-            sum += (int)qv;
-            pk[k] |= ((uint32_t)(int)qv & 0xFFu) << (8 * j);
+    for (int j = 0; j < 4; ++j) packed |= ((uint32_t)q8_round(v[j] * id) & 0xFFu) << (8 * j);
+    return packed;
+}
+// max |v_j| from 0 (NaN never wins, as in the reference's "if (a > amax)")
+__device__ __forceinline__ float absmax4(const float (&v)[4]) {
+    return fmaxf(fmaxf(fmaxf(fmaxf(0.f, fabsf(v[0])), fabsf(v[1])), fabsf(v[2])), fabsf(v[3]));
+}
+__device__ __forceinline__ void act_q8_lanes(const float (&v)[4], uint32_t lane, uint32_t chunk,
+                                             uint8_t * q81, uint8_t * q8k, uint32_t cols) {
+    const uint32_t am = __float_as_uint(absmax4(v));
+    // q8_1: block of 32 = 8 lanes
+    {
+        const uint32_t blk = chunk * 8 + (lane >> 3);
+        const float amax = __uint_as_float(umax8(am));
+        const float d = amax / 127.f;
+        const float id = amax > 0.f ? 127.f / amax : 0.f;
+        const uint32_t pk = quant4(v, id);
+        const int sum = sum8i(dot4((int)pk, 0x01010101, 0));
+        if ((blk + 1) * 32 <= cols) {
+            uint8_t * o = q81 + (size_t)blk * 36;
+            *(uint32_t *)(o + 4 + 4 * (lane & 7)) = pk;
+            if ((lane & 7) == 0) *(uint32_t *)o = f2h(d) | (f2h(d * (float)sum) << 16);
         }
     }
-    return 0;
+    // q8_K: whole chunk
+    if ((chunk + 1) * 256 <= cols) {
+        const float amax = __uint_as_float(umax64(am));
+        const float d = amax / 127.f;
+        const float id = amax > 0.f ? 127.f / amax : 0.f;
+        const uint32_t pk = quant4(v, id);
+        const int s = sum4i(dot4((int)pk, 0x01010101, 0));
+        uint8_t * o = q8k + (size_t)chunk * 292;
+        *(uint32_t *)(o + 36 + 4 * lane) = pk;
+        if ((lane & 3) == 0) *(int16_t *)(o + 4 + 2 * (lane >> 2)) = (int16_t)s;
+        if (lane == 0) *(float *)o = d;
+    }
 }
 
-__device__ __forceinline__ float ks_absmax16(const u32x4a (&raw)[4]) {
-    float m = 0.f;
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-        m = fmaxf(fmaxf(fmaxf(m, fabsf(__uint_as_float(raw[k].x))), fabsf(__uint_as_float(raw[k].y))),
-                  fmaxf(fabsf(__uint_as_float(raw[k].z)), fabsf(__uint_as_float(raw[k].w))));
-    return m;
-}
-
-// ACT_Q8 fused into the dot: quantise the fp32 columns into the records
-// (16 lanes per superblock, each lane one 16-element run).  When write_app,
-// also write both appendices so the bytes in memory equal ACT_Q8's.  A
-// superblock's 16 runs sit in 16 consecutive lanes of one wave, so its absmax
-// is a 4-step shuffle max (order-free), with no barrier.  after_loads() runs
-// once, right after the first activation loads are issued (the caller issues
-// its weight prologue there, behind the older activation loads).
-template <int FMT, int NX, int KW = 4, typename F>
+// ACT_Q8 fused into the dot: quantise the fp32 columns into the records.
+// Wave w takes superblocks (items i = p * nsb + sb) w, w + KW, ..., up to four
+// at a time with their loads in flight together; lane l holds elements
+// 4l..4l+3 of an item, so each load instruction reads one contiguous 1 KiB
+// (every workgroup reads the whole column: a lane-strided pattern asked L2
+// for four times the lines and made this prologue ~1 us slower).  The
+// superblock's absmax is a wave max (order free); the lane's four quantised
+// bytes form one dword of a record and a quad sum gives its 16-element block
+// sum.  When write_app, also write both appendices with k_act_q8's lane code,
+// so the bytes in memory equal ACT_Q8's.  after_loads() runs once, right after
+// the first activation loads are issued (the caller issues its weight
+// prologue there, behind the older activation loads).
+template <int FMT, int NX, int NI, int D, int KW = 4, typename F>
 __device__ __forceinline__ void ks_x_fuse(const KsCols<NX> & C, uint32_t nx, uint32_t nsb, uint32_t cols,
                                           uint8_t * xr, float * xd, bool write_app, F && after_loads) {
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t nitem = nx * nsb;
-    const uint32_t sub = lane >> 4, run = lane & 15;        // superblock in the pass, 16-run
-    bool issued = false;
-    for (uint32_t base = 0; base < nitem; base += 16 * KW) {
-        // up to 16 KW superblocks per pass (4 KW per q-group, 4 per wave),
-        // loads first; only the q-groups that hold superblocks are loaded
-        const uint32_t nq = min(4u, (nitem - base + 4 * KW - 1) / (4 * KW));
-        u32x4a raw[4][4];
+    // record slot of this lane's four elements (the same in every superblock)
+    uint32_t cc, kk, t;
+    xrec_pos<FMT>(4 * lane, cc, kk, t);
+    const uint32_t magic = div_magic(nsb);                        // i / nsb, i < 2^16
+    // Quantise items base + KW * j + wave (j < 4) from v: four superblock
+    // absmaxes (wave max of the non-negative float bits; the lane max starts
+    // at 0, so NaN never wins, as the reference's "if (a > amax)"), one
+    // division sequence for the four scales (lanes 0..3), records and scales
+    // to LDS, and the appendices when write_app.
+    auto quant_group = [&](uint32_t base, const float (&v)[4][4]) {
+        uint32_t am[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            if ((uint32_t)q >= nq) break;
-            const uint32_t i = base + 4 * KW * q + 4 * wave + sub;
-            const uint32_t ii = i < nitem ? i : 0;
-            const float * src = col_pick<NX>(C.x, ii / nsb) + 256 * (ii % nsb) + 16 * run;
+        for (int j = 0; j < 4; ++j)
+            if (base + KW * j + wave < nitem) am[j] = umax64(__float_as_uint(absmax4(v[j])));
+        const float al = __uint_as_float(lane == 0 ? am[0] : lane == 1 ? am[1] : lane == 2 ? am[2] : am[3]);
+        const float dl = al / 127.f;
+        const float idl = al > 0.f ? 127.f / al : 0.f;
 #pragma unroll
-            for (int k = 0; k < 4; ++k) raw[q][k] = *(const u32x4a *)(src + 4 * k);
-        }
-        if (!issued) {
-            after_loads();
-            issued = true;
-        }
-        // superblock absmax: its 16 runs are 16 consecutive lanes of this wave
-        float amq[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            if ((uint32_t)q >= nq) break;                   // wave-uniform
-            float m = ks_absmax16(raw[q]);
-            m = fmaxf(m, __shfl_xor(m, 1));
-            m = fmaxf(m, __shfl_xor(m, 2));
-            m = fmaxf(m, __shfl_xor(m, 4));
-            amq[q] = fmaxf(m, __shfl_xor(m, 8));
-        }
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const uint32_t i = base + 4 * KW * q + 4 * wave + sub;
-            if ((uint32_t)q < nq && i < nitem) {
-                const uint32_t p = i / nsb, sb = i % nsb;
-                const float amax = amq[q];
-                const float d = amax / 127.f;
-                const float id = amax > 0.f ? 127.f / amax : 0.f;
-                uint32_t pk[4];
-                int sum = 0;
-                ks_quant16(raw[q], id, sum, pk);
-                uint32_t cc, kk, t;
-                xrec_pos<FMT>(16 * run, cc, kk, t);
-                uint8_t * rec = xr + (((size_t)p * nsb + sb) * 4 + cc) * XREC;
-                lds_st128(rec + 16 * kk, u32x4a{pk[0], pk[1], pk[2], pk[3]});
-                lds_st32(rec + 64 + 4 * kk, (uint32_t)(FMT == FMT_Q4_K ? sum : 32 * sum));
-                if (run == 0) lds_st32(&xd[p * nsb + sb], __float_as_uint(d));
-                if (write_app) {
-                    float * xc = (float *)col_pick<NX>(C.x, p);
-                    uint8_t * q8k = (uint8_t *)xc + xqk_off(cols) + (size_t)sb * 292;
-                    uint32_t * dst = (uint32_t *)(q8k + 36 + 16 * run);
-#pragma unroll
-                    for (int k = 0; k < 4; ++k) dst[k] = pk[k];
-                    *(int16_t *)(q8k + 4 + 2 * run) = (int16_t)sum;
-                    if (run == 0) *(float *)q8k = d;
-                    // q8_1 block of 32 = this lane's run and its neighbour's
-                    float m2 = ks_absmax16(raw[q]);
-                    m2 = fmaxf(m2, __shfl_xor(m2, 1));
-                    const float d1 = m2 / 127.f;
-                    const float id1 = m2 > 0.f ? 127.f / m2 : 0.f;
-                    uint32_t pk1[4];
-                    int s1 = 0;
-                    ks_quant16(raw[q], id1, s1, pk1);
-                    s1 += __shfl_xor(s1, 1);
-                    uint8_t * q81 = (uint8_t *)xc + xq_off(cols) + (size_t)(sb * 8 + (run >> 1)) * 36;
-                    uint32_t * d1p = (uint32_t *)(q81 + 4 + 16 * (run & 1));
-#pragma unroll
-                    for (int k = 0; k < 4; ++k) d1p[k] = pk1[k];
-                    if ((run & 1) == 0) *(uint32_t *)q81 = f2h(d1) | (f2h(d1 * (float)s1) << 16);
-                }
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t i = base + KW * j + wave;
+            if (i >= nitem) break;                                       // wave-uniform
+            const uint32_t p = div_small(i, magic), sb = i - p * nsb;
+            const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dl), j));
+            const float id = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(idl), j));
+            const uint32_t pk = quant4(v[j], id);
+            const int sum = sum4i(dot4((int)pk, 0x01010101, 0));        // 16-element block sum
+            uint8_t * rec = xr + (((size_t)p * nsb + sb) * 4 + cc) * XREC;
+            lds_st32(rec + 16 * kk + t, pk);
+            if ((lane & 3) == 0) lds_st32(rec + 64 + 4 * kk, (uint32_t)(FMT == FMT_Q4_K ? sum : 32 * sum));
+            if (lane == 0) lds_st32(&xd[p * nsb + sb], __float_as_uint(d));
+            if (write_app) {
+                uint8_t * xc = (uint8_t *)col_pick<NX>(C.x, p);
+                act_q8_lanes(v[j], lane, sb, xc + xq_off(cols), xc + xqk_off(cols), cols);
             }
         }
-    }
-    if (!issued) after_loads();
-    // columns p >= nx of the template width read zero records
-    for (uint32_t i = tid; i < (NX - nx) * nsb * 4 * (XREC / 4); i += 256)
-        ((uint32_t *)(xr + (size_t)nx * nsb * 4 * XREC))[i] = 0u;
-    for (uint32_t i = tid; i < (NX - nx) * nsb; i += 256) xd[nx * nsb + i] = 0.f;
-}
-
-// Record (sb, part cc) of column p from its appendix at xb (the superblock's
-// base: q8_K for the K formats; for Q8_0, the unit's 8 q8_1 blocks, whose
-// scales go to bs[0..1] as raw halves).
-template <int FMT>
-__device__ __forceinline__ void ks_xrec_load(const uint8_t * xb, uint32_t cc, u32x4 (&v)[4], int (&bs)[4]) {
-    if constexpr (FMT == FMT_Q8_0) {
-        const uint8_t * b0 = xb + 72 * cc;                  // q8_1 blocks 2cc, 2cc + 1 (36 B each)
-        v[0] = ld4(b0 + 4);
-        v[1] = ld4(b0 + 20);
-        v[2] = ld4(b0 + 40);
-        v[3] = ld4(b0 + 56);
-        bs[0] = (int)*(const uint16_t *)b0;
-        bs[1] = (int)*(const uint16_t *)(b0 + 36);
-        bs[2] = bs[3] = 0;
-    } else if constexpr (FMT == FMT_Q4_K) {
-        const uint32_t g0 = 2 * (cc >> 1), h = cc & 1;
-        const uint32_t gs[4] = {g0, g0 + 1, g0 + 4, g0 + 5};
+    };
+    auto vload = [&](uint32_t i) -> const float * {
+        const uint32_t p = div_small(i, magic);
+        return col_pick<NX>(C.x, p) + 256 * (i - p * nsb) + 4 * lane;
+    };
+    if (nitem <= 8 * KW) {
+        // every item of this wave (at most 8) is loaded before the weight
+        // prologue, and only these loads are waited for
+        u32x4a r[8];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            v[k] = ld4(xb + 36 + 32 * gs[k] + 16 * h);
-            bs[k] = *(const int16_t *)(xb + 4 + 2 * (2 * gs[k] + h));
+        for (int j = 0; j < 8; ++j)
+            if (KW * j + wave < nitem) r[j] = gld_x4(vload(KW * j + wave));
+        ks_wait_behind<NI, D + 1>(after_loads());
+#pragma unroll
+        for (int j = 0; j < 8; ++j) xfence(r[j]);
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+            if (4 * KW * g >= nitem) break;
+            float v[4][4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                v[j][0] = __uint_as_float(r[4 * g + j].x); v[j][1] = __uint_as_float(r[4 * g + j].y);
+                v[j][2] = __uint_as_float(r[4 * g + j].z); v[j][3] = __uint_as_float(r[4 * g + j].w);
+            }
+            quant_group(4 * KW * g, v);
         }
     } else {
-        const uint32_t hh = cc >> 1, bb = cc & 1;
+        bool issued = false;
+        for (uint32_t base = 0; base < nitem; base += 4 * KW) {
+            u32x4a r[4] = {};
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            v[g] = ld4(xb + 36 + 128 * hh + 32 * g + 16 * bb);
-            bs[g] = 32 * (int)*(const int16_t *)(xb + 4 + 2 * (8 * hh + 2 * g + bb));
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t i = base + KW * j + wave;                 // wave-uniform
+                if (i < nitem) r[j] = gld_x4(vload(i));
+            }
+            if (!issued) {
+                after_loads();
+                issued = true;
+            }
+            WAIT_VM(0);
+            float v[4][4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                xfence(r[j]);
+                v[j][0] = __uint_as_float(r[j].x); v[j][1] = __uint_as_float(r[j].y);
+                v[j][2] = __uint_as_float(r[j].z); v[j][3] = __uint_as_float(r[j].w);
+            }
+            quant_group(base, v);
         }
+        if (!issued) after_loads();
     }
+    KS_STAMP(11);
+    // columns p >= nx of the template width read zero records
+    for (uint32_t i = tid; i < (NX - nx) * nsb * 4 * (XREC / 4); i += 64 * KW)
+        ((uint32_t *)(xr + (size_t)nx * nsb * 4 * XREC))[i] = 0u;
+    for (uint32_t i = tid; i < (NX - nx) * nsb; i += 64 * KW) xd[nx * nsb + i] = 0.f;
+    KS_STAMP(6);
 }
 
 // Base of superblock sb's activation in column x: its q8_K block (K formats)
@@ -367,52 +432,109 @@ __device__ __forceinline__ const uint8_t * ks_xsb(const uint8_t * x, uint32_t co
 }
 
 // Records from the appendices written by ACT_Q8.  after_loads() as above.
-template <int FMT, int NX, typename F>
+// Loads of record (sb, part cc) of a column from its appendix at xb (the
+// superblock's base: q8_K for the K formats; for Q8_0, the unit's 8 q8_1
+// blocks), hidden from the compiler (gld_x*): v = the record's 64 int8, bs =
+// its raw block sums (Q4_K / Q6_K: int16; Q8_0: the two q8_1 halves d), dk =
+// the q8_K f32 d bits.
+template <int FMT>
+__device__ __forceinline__ void ks_xrec_issue(const uint8_t * xb, uint32_t cc, u32x4a (&v)[4], uint32_t (&bs)[4],
+                                              uint32_t & dk) {
+    if constexpr (FMT == FMT_Q8_0) {
+        const uint8_t * b0 = xb + 72 * cc;
+        v[0] = gld_x4(b0 + 4);
+        v[1] = gld_x4(b0 + 20);
+        v[2] = gld_x4(b0 + 40);
+        v[3] = gld_x4(b0 + 56);
+        bs[0] = gld_xu16(b0);
+        bs[1] = gld_xu16(b0 + 36);
+        bs[2] = bs[3] = 0;
+        dk = 0;
+    } else if constexpr (FMT == FMT_Q4_K) {
+        const uint32_t g0 = 2 * (cc >> 1), h = cc & 1;
+        const uint32_t gs[4] = {g0, g0 + 1, g0 + 4, g0 + 5};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            v[k] = gld_x4(xb + 36 + 32 * gs[k] + 16 * h);
+            bs[k] = gld_xs16(xb + 4 + 2 * (2 * gs[k] + h));
+        }
+        dk = gld_x1(xb);
+    } else {
+        const uint32_t hh = cc >> 1, bb = cc & 1;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            v[g] = gld_x4(xb + 36 + 128 * hh + 32 * g + 16 * bb);
+            bs[g] = gld_xs16(xb + 4 + 2 * (8 * hh + 2 * g + bb));
+        }
+        dk = gld_x1(xb);
+    }
+}
+
+template <int FMT, int NX, int NI, int D, typename F>
 __device__ __forceinline__ void ks_x_app(const KsCols<NX> & C, uint32_t nx, uint32_t nsb, uint32_t cols,
                                          uint8_t * xr, float * xd, F && after_loads) {
     const uint32_t tid = threadIdx.x;
     if (NX * nsb * 4 <= 256) {
-        // one record per thread: load, run after_loads, then store
+        // one record per thread: load, run after_loads (the weight prologue),
+        // wait for the record loads alone, then store
         const uint32_t i = tid < NX * nsb * 4 ? tid : 0;
         const uint32_t p = i / (nsb * 4), rem = i % (nsb * 4), sb = rem >> 2, cc = rem & 3;
         const uint32_t pp = p < nx ? p : 0;
         const uint8_t * xb = ks_xsb<FMT>((const uint8_t *)col_pick<NX>(C.x, pp), cols, sb);
-        u32x4 v[4];
-        int bs[4];
-        ks_xrec_load<FMT>(xb, cc, v, bs);
-        const float dk = FMT == FMT_Q8_0 ? 0.f : *(const float *)xb;
-        after_loads();
+        u32x4a v[4];
+        uint32_t bs[4], dkb;
+        ks_xrec_issue<FMT>(xb, cc, v, bs, dkb);
+        ks_wait_behind<NI, D + 1>(after_loads());
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            xfence(v[k]);
+            xfence(bs[k]);
+        }
+        xfence(dkb);
+        if constexpr (FMT == FMT_Q6_K) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) bs[k] = (uint32_t)(32 * (int)bs[k]);
+        }
         if (tid < NX * nsb * 4) {
             uint8_t * rec = xr + (size_t)tid * XREC;
 #pragma unroll
-            for (int k = 0; k < 4; ++k) lds_st128(rec + 16 * k, u32x4a{v[k].x, v[k].y, v[k].z, v[k].w});
-            lds_st128(rec + 64, u32x4a{(uint32_t)bs[0], (uint32_t)bs[1], (uint32_t)bs[2], (uint32_t)bs[3]});
+            for (int k = 0; k < 4; ++k) lds_st128(rec + 16 * k, v[k]);
+            lds_st128(rec + 64, u32x4a{bs[0], bs[1], bs[2], bs[3]});
             if constexpr (FMT == FMT_Q8_0) {
-                lds_st32(&xd[(p * nsb + sb) * 8 + 2 * cc], __float_as_uint((p < nx) ? h2f((uint32_t)bs[0]) : 0.f));
-                lds_st32(&xd[(p * nsb + sb) * 8 + 2 * cc + 1], __float_as_uint((p < nx) ? h2f((uint32_t)bs[1]) : 0.f));
+                lds_st32(&xd[(p * nsb + sb) * 8 + 2 * cc], __float_as_uint((p < nx) ? h2f(bs[0]) : 0.f));
+                lds_st32(&xd[(p * nsb + sb) * 8 + 2 * cc + 1], __float_as_uint((p < nx) ? h2f(bs[1]) : 0.f));
             } else if (cc == 0) {
-                lds_st32(&xd[p * nsb + sb], __float_as_uint((p < nx) ? dk : 0.f));
+                lds_st32(&xd[p * nsb + sb], (p < nx) ? dkb : 0u);
             }
         }
     } else {
-        for (uint32_t i = tid; i < NX * nsb * 4; i += 256) {
+        for (uint32_t i = tid; i < NX * nsb * 4; i += blockDim.x) {
             const uint32_t p = i / (nsb * 4), rem = i % (nsb * 4), sb = rem >> 2, cc = rem & 3;
             const uint32_t pp = p < nx ? p : 0;
             const uint8_t * xb = ks_xsb<FMT>((const uint8_t *)col_pick<NX>(C.x, pp), cols, sb);
-            uint32_t * rec = (uint32_t *)(xr + (size_t)i * XREC);
-            u32x4 v[4];
-            int bs[4];
-            ks_xrec_load<FMT>(xb, cc, v, bs);
+            uint8_t * rec = xr + (size_t)i * XREC;
+            u32x4a v[4];
+            uint32_t bs[4], dkb;
+            ks_xrec_issue<FMT>(xb, cc, v, bs, dkb);
+            WAIT_VM(0);
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-                rec[4 * k + 0] = v[k].x; rec[4 * k + 1] = v[k].y; rec[4 * k + 2] = v[k].z; rec[4 * k + 3] = v[k].w;
-                rec[16 + k] = (uint32_t)bs[k];
+                xfence(v[k]);
+                xfence(bs[k]);
             }
+            xfence(dkb);
+            if constexpr (FMT == FMT_Q6_K) {
+#pragma unroll
+                for (int k = 0; k < 4; ++k) bs[k] = (uint32_t)(32 * (int)bs[k]);
+            }
+#pragma unroll
+            for (int k = 0; k < 4; ++k) lds_st128(rec + 16 * k, v[k]);
+            lds_st128(rec + 64, u32x4a{bs[0], bs[1], bs[2], bs[3]});
             if constexpr (FMT == FMT_Q8_0) {
-                xd[(p * nsb + sb) * 8 + 2 * cc] = (p < nx) ? h2f((uint32_t)bs[0]) : 0.f;
-                xd[(p * nsb + sb) * 8 + 2 * cc + 1] = (p < nx) ? h2f((uint32_t)bs[1]) : 0.f;
+                lds_st32(&xd[(p * nsb + sb) * 8 + 2 * cc], __float_as_uint((p < nx) ? h2f(bs[0]) : 0.f));
+                lds_st32(&xd[(p * nsb + sb) * 8 + 2 * cc + 1], __float_as_uint((p < nx) ? h2f(bs[1]) : 0.f));
             } else if (cc == 0) {
-                xd[p * nsb + sb] = (p < nx) ? *(const float *)xb : 0.f;
+                lds_st32(&xd[p * nsb + sb], (p < nx) ? dkb : 0u);
             }
         }
         after_loads();
@@ -621,75 +743,6 @@ __device__ __forceinline__ float ks_fold(const int * TI, const int * TM, const u
     }
     const float s01 = acc + qx1f(acc);
     return s01 + qx2f(s01);
-}
-
-// ---------------------------------------------------------------- ACT_Q8 --
-// One wave quantises one 256-element chunk: lane i holds elements 4i..4i+3
-// in v.  Writes the chunk's q8_1 blocks (8-lane groups) and its q8_K block
-// with the bytes of fl_quantize_q8_1_block / fl_quantize_q8_K_block
-// (src/runtime/quants.h:360-402): amax is a max (order free), d = amax/127
-// and id = 127/amax are correctly rounded IEEE divisions, q = roundf(x*id)
-// clamped to +-127, sums are exact integers, halves are RNE.
-__device__ __forceinline__ float wave_max8(float v) {      // within 8 lanes
-    v = fmaxf(v, __shfl_xor(v, 1));
-    v = fmaxf(v, __shfl_xor(v, 2));
-    v = fmaxf(v, __shfl_xor(v, 4));
-    return v;
-}
-__device__ __forceinline__ int isum8(int v) {
-    v += __shfl_xor(v, 1);
-    v += __shfl_xor(v, 2);
-    v += __shfl_xor(v, 4);
-    return v;
-}
-__device__ __forceinline__ uint32_t quant4(const float (&v)[4], float id, int & sum) {
-    uint32_t packed = 0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        float q = roundf(v[j] * id);
-        if (q > 127.f) q = 127.f;
-        if (q < -127.f) q = -127.f;
-        const int qi = (int)q;
-        sum += qi;
-        packed |= ((uint32_t)qi & 0xFFu) << (8 * j);
-    }
-    return packed;
-}
-__device__ __forceinline__ void act_q8_lanes(const float (&v)[4], uint32_t lane, uint32_t chunk,
-                                             uint8_t * q81, uint8_t * q8k, uint32_t cols) {
-    const float am = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-    // q8_1: block of 32 = 8 lanes
-    {
-        const uint32_t blk = chunk * 8 + (lane >> 3);
-        const float amax = wave_max8(am);
-        const float d = amax / 127.f;
-        const float id = amax > 0.f ? 127.f / amax : 0.f;
-        int s = 0;
-        const uint32_t pk = quant4(v, id, s);
-        const int sum = isum8(s);
-        if ((blk + 1) * 32 <= cols) {
-            uint8_t * o = q81 + (size_t)blk * 36;
-            *(uint32_t *)(o + 4 + 4 * (lane & 7)) = pk;
-            if ((lane & 7) == 0) *(uint32_t *)o = f2h(d) | (f2h(d * (float)sum) << 16);
-        }
-    }
-    // q8_K: whole chunk
-    if ((chunk + 1) * 256 <= cols) {
-        float amax = wave_max8(am);
-        amax = fmaxf(amax, __shfl_xor(amax, 8));
-        amax = fmaxf(amax, __shfl_xor(amax, 16));
-        amax = fmaxf(amax, __shfl_xor(amax, 32));
-        const float d = amax / 127.f;
-        const float id = amax > 0.f ? 127.f / amax : 0.f;
-        int s = 0;
-        const uint32_t pk = quant4(v, id, s);
-        s += __shfl_xor(s, 1);
-        s += __shfl_xor(s, 2);
-        uint8_t * o = q8k + (size_t)chunk * 292;
-        *(uint32_t *)(o + 36 + 4 * lane) = pk;
-        if ((lane & 3) == 0) *(int16_t *)(o + 4 + 2 * (lane >> 2)) = (int16_t)s;
-        if (lane == 0) *(float *)o = d;
-    }
 }
 
 // Expert ids of the ntok * top_k routed pairs for a grouped expert matvec:

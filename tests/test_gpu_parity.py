@@ -189,6 +189,23 @@ def test_multicol_bitwise_equals_single(flh, orc, gpu, fmt, nx):
         assert np.array_equal(bits(g1), bits(got[p * (rows + 3):p * (rows + 3) + rows]))
 
 
+@pytest.mark.parametrize("fmt", [Q8_0, Q4_K, Q6_K])
+@pytest.mark.parametrize("rows,nx", [(300, 2), (77, 3), (130, 4), (40, 8)])
+def test_one_superblock_rows_multicol_bitwise(flh, orc, gpu, fmt, rows, nx):
+    """Rows of a single 256-weight superblock with several columns: the
+    streaming kernel's row / superblock split of a batch-local index
+    (quotient by the superblocks per row, here 1) -- regression for a
+    multiply-high divisor that does not fit 32 bits when it is 1."""
+    say("one-superblock rows", fmt, rows, nx)
+    cols = 256
+    rng = np.random.default_rng(rows * 7 + nx + fmt)
+    w = sane_rows(fmt, rows, cols, rng)
+    xs = activations(nx, cols, rng, outliers=True)
+    got, want = run_dot(flh, orc, gpu, fmt, w, rows, cols, xs, ystride=rows,
+                        y0=rng.standard_normal((nx - 1) * rows + rows).astype(np.float32))
+    assert np.array_equal(bits(got), bits(want))
+
+
 @pytest.mark.parametrize("fmt", [Q4_K, Q6_K, Q8_0])
 def test_idx_dot_resolves_expert_on_device(flh, orc, gpu, fmt):
     say("idx", fmt)
@@ -301,7 +318,7 @@ def dequant_activation(orc, x, fmt):
 
 # ------------------------------------------------ fused ACT_Q8 + STREAM_DOT --
 @pytest.mark.parametrize("fmt", [Q4_K, Q6_K])
-@pytest.mark.parametrize("rows,cols,nx", [(37, 1024, 1), (300, 4096, 1), (64, 14336, 1),
+@pytest.mark.parametrize("rows,cols,nx", [(37, 1024, 1), (300, 4096, 1), (64, 14336, 1), (300, 256, 2), (77, 256, 4),
                                           (33, 2816, 3), (20, 4096, 4), (1, 256, 2)])
 def test_fused_act_q8_dot_bitwise(flh, orc, gpu, fmt, rows, cols, nx):
     """flh_act_q8_stream_dot == ACT_Q8 then STREAM_DOT: same appendix bytes

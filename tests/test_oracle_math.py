@@ -452,3 +452,33 @@ def test_iq_int8_replay_and_budget(orc, fmt):
         S = max(1e-6, np.sqrt((prod ** 2).sum()))
         mx = max(mx, abs(float(got) - prod.sum()) / S)
     assert mx < 2.5e-2, mx
+
+
+def test_device_round_half_away_identity():
+    """The device quantizers round y = x * id with trunc(y + copysign(0.5 -
+    2^-25, y)) (one add and a truncating convert) instead of roundf(y), then
+    clamp to +-127 (fl_quantize_q8_1_block / fl_quantize_q8_K_block,
+    src/runtime/quants.h:360-402).  Pinned here on every float within 2^13
+    ulps of each integer and each half-integer in [-129, 129] -- where a
+    wrong offset or a double rounding would show -- and on 2^20 random floats
+    in that range, against roundf(y) = sign(y) * floor(|y| + 0.5) computed
+    exactly in float64.  (Checked exhaustively over all floats with |y| <=
+    128.5 when the identity was adopted.)"""
+    c = np.float32(0.5) - np.float32(2.0 ** -25)
+    assert c == np.float32(0.49999997)
+    centers = np.concatenate([np.arange(0, 130, dtype=np.float32), np.arange(0, 129, dtype=np.float32) + 0.5])
+    k = np.arange(-(1 << 13), 1 << 13, dtype=np.int64)
+    ys = []
+    for m in centers:
+        b = np.int64(np.float32(m).view(np.int32)) + k
+        b = b[(b >= 0) & (b < 0x43020000)]
+        ys.append(b.astype(np.uint32).view(np.float32))
+    ys.append(np.random.default_rng(3).uniform(0, 129, 1 << 20).astype(np.float32))
+    y = np.concatenate(ys)
+    y = np.concatenate([y, -y])
+    with np.errstate(over="ignore"):
+        t = (y + np.copysign(c, y)).astype(np.float32)
+    got = np.clip(np.trunc(t).astype(np.int64), -127, 127)
+    y64 = y.astype(np.float64)
+    want = np.clip(np.sign(y64) * np.floor(np.abs(y64) + 0.5), -127, 127).astype(np.int64)
+    assert np.array_equal(got, want)
