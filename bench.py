@@ -213,20 +213,28 @@ def main():
         ops[name] = e
 
     REPS = 64
+    cpu_in = {}          # host copies of each config's bytes for the CPU baseline
     for name, r, c in LAYER:
         x, st = xin[name]
         nb = r * flh.row_bytes(Q4_K, c)
         us = B.time_graph(lambda i: flh.stream_dot(Q4_K, W[name][i % L], r, c, x, yout[name], s), REPS)
         op_entry(f"q4_K_{name}_{r}x{c}", us, nb)
-    # dominant kernel roofline: gate/up
+        if name != "down":
+            # the fused ACT_Q8 + STREAM_DOT launch the layer step runs
+            us = B.time_graph(lambda i: flh.act_q8_stream_dot(Q4_K, W[name][i % L], r, c, x, yout[name], s), REPS)
+            op_entry(f"q4_K_{name}_{r}x{c}_act_fused", us, nb)
+    # dominant kernel of the timed step: the fused ACT_Q8 + gate/up launch.
+    # Algorithmic bytes: weights + fp32 x read + both appendices written
+    # (by one workgroup) + y read and written.
     r, c = 28672, 4096
-    gu = ops[f"q4_K_gate_up_{r}x{c}"]
-    alg = r * flh.row_bytes(Q4_K, c) + (c // 256) * 292 + r * 8
+    gu = ops[f"q4_K_gate_up_{r}x{c}_act_fused"]
+    alg = r * flh.row_bytes(Q4_K, c) + 4 * c + (c // 32) * 36 + (c // 256) * 292 + r * 8
     result["roofline"] = {"bound": "hbm", "achieved": round(alg / gu["us"] / 1e3, 1),
                           "peak": HBM_PEAK_GBS, "unit": "GB/s",
                           "frac": round(alg / gu["us"] / 1e3 / HBM_PEAK_GBS, 4),
                           "traffic": traffic_from_profile(),
-                          "kernel": "k_dot_kstream<Q4_K> gate/up 28672x4096",
+                          "kernel": "k_dot_kstream<Q4_K,1,2,fused ACT_Q8,8 waves> gate/up 28672x4096 "
+                                    "(the step's dominant launch)",
                           "alg_bytes_per_launch": alg, "us_per_launch": gu["us"]}
 
     if not args.no_ops:
@@ -240,6 +248,7 @@ def main():
             us = B.time_graph(lambda i: flh.stream_dot(Q6_K, ws[i % len(ws)], r, c, x, y, s),
                               8 if r > 100000 else REPS)
             op_entry(f"q6_K_{name}_{r}x{c}", us, nb)
+            cpu_in[f"q6_K_{name}_{r}x{c}"] = host_case(flh, s, Q6_K, ws[0], r, c, x, st, 1)
             del ws
         # Q8_0
         r = c = 4096
@@ -249,6 +258,7 @@ def main():
         y = B.buf(r * 4)
         us = B.time_graph(lambda i: flh.stream_dot(Q8_0, ws[i % len(ws)], r, c, x, y, s), REPS)
         op_entry(f"q8_0_{r}x{c}", us, nb)
+        cpu_in[f"q8_0_{r}x{c}"] = host_case(flh, s, Q8_0, ws[0], r, c, x, st, 1)
         # spec-verify small N
         for r, c in [(14336, 4096), (4096, 14336)]:
             nb = r * flh.row_bytes(Q4_K, c)
@@ -259,14 +269,16 @@ def main():
                 us = B.time_graph(lambda i: flh.stream_dot(Q4_K, ws[i % len(ws)], r, c, x, y, s,
                                                            nx=n, xstride=st, ystride=r), REPS)
                 op_entry(f"q4_K_verify_n{n}_{r}x{c}", us, nb, {"n": n})
+                if n == 8:
+                    cpu_in[f"q4_K_verify_n8_{r}x{c}"] = host_case(flh, s, Q4_K, ws[0], r, c, x, st, n)
         # MoE decode: 8 experts, top-2, d_model 4096, d_ff 14336
-        result["moe"] = bench_moe(flh, B, s, staging)
+        result["moe"] = bench_moe(flh, B, s, staging, cpu_in)
         ops.update(result["moe"].pop("ops"))
     result["ops"] = ops
 
     # ------------------------------------------------------- CPU baseline
     if not args.no_cpu:
-        result["cpu_baseline"] = cpu_baseline(flh, s, W, xin)
+        result["cpu_baseline"] = cpu_baseline(flh, s, W, xin, cpu_in)
     print(json.dumps(result), flush=True)
 
 
@@ -303,7 +315,7 @@ def traffic_from_profile():
         return None
 
 
-def bench_moe(flh, B, s, staging):
+def bench_moe(flh, B, s, staging, cpu_in):
     """Mixtral-style MoE FFN: router + grouped gate/up (one launch) -> silu*up +
     ACT_Q8 (one launch) -> grouped down -> weighted merge.  Two copies of the expert
     set alternate."""
@@ -352,57 +364,101 @@ def bench_moe(flh, B, s, staging):
                 sel.update(np.argsort(-ll[t], kind="stable")[:K].tolist())
             distinct.append(len(sel))
         nb = int(np.mean(distinct) * (gu_b + dn_b))
+        if ntok == 1:
+            # CPU figure: the two routed experts' gate/up and down dots of copy 0
+            sel = np.argsort(-lg[0].reshape(ntok, E)[0], kind="stable")[:K].tolist()
+            hx = x.download(np.float32, stD, s)
+            hh = h.download(np.float32, stF, s)          # a down input with its appendices
+            cpu_in["moe_q4_K_top2of8_batch1"] = [
+                (Q4_K, gu[0].download(np.uint8, gu_b, s, offset=e * gu_b), 2 * F, D, hx, stD, 1) for e in sel] + [
+                (Q4_K, dn[0].download(np.uint8, dn_b, s, offset=e * dn_b), D, F, hh, stF, 1) for e in sel]
         out["ops"][f"moe_q4_K_top2of8_batch{ntok}"] = {
             "us": round(us, 3), "weight_bytes": nb, "distinct_experts": float(np.mean(distinct)),
             "GBs": round(nb / us / 1e3, 1), "pct_hbm": round(100 * nb / us / 1e3 / HBM_PEAK_GBS, 2)}
     return out
 
 
-def cpu_baseline(flh, s, W, xin):
-    """The reference CPU quantized-dot path on the host cores, same layer step
-    (4 Q4_K matvecs on the same bytes and appendices), rows split over T
-    threads like tools/membench.cu:276-300."""
+def host_case(flh, s, fmt, w, rows, cols, x, st, nx):
+    """Host copy of one matvec's bytes (weights, activation columns with their
+    appendices) for the CPU baseline."""
+    return [(fmt, w.download(np.uint8, rows * flh.row_bytes(fmt, cols), s), rows, cols,
+             x.download(np.float32, nx * st, s), st, nx)]
+
+
+def cpu_share():
+    """Host cores this process may use: its affinity set, capped by the
+    thread share the box gives it (OMP_NUM_THREADS)."""
+    n = len(os.sched_getaffinity(0))
+    cap = os.environ.get("OMP_NUM_THREADS", "")
+    return min(n, int(cap)) if cap.isdigit() and int(cap) > 0 else n
+
+
+def cpu_model():
+    """/proc/cpuinfo's model name with its family / model / stepping numbers
+    (a virtualised host may report only a short name)."""
+    info = {}
+    try:
+        for line in open("/proc/cpuinfo"):
+            if ":" in line:
+                k, v = line.split(":", 1)
+                info.setdefault(k.strip(), v.strip())
+            elif info:
+                break
+    except OSError:
+        return ""
+    return (f"{info.get('model name', '')} (family {info.get('cpu family', '?')}, model "
+            f"{info.get('model', '?')}, stepping {info.get('stepping', '?')})")
+
+
+def cpu_baseline(flh, s, W, xin, cpu_in):
+    """The reference CPU quantized-dot path (exec_task_cpu, int8 dots with the
+    CPU default masks) on the host cores: rows split over T threads as
+    tools/membench.cu:276-300 does.  value: the headline layer step (4 Q4_K
+    matvecs on the same bytes and appendices); configs: every other
+    BASELINE config on its own bytes.  Each figure repeats its work for about
+    1.5 s (the single-thread layer figure about 3 s)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     from oracle import Oracle, REF_SO
     kind = "reference" if os.path.exists(REF_SO) else "port"
     orc = Oracle(ref=(kind == "reference"))
-    T = min(16, os.cpu_count() or 1)
-    host = {}
+    T = cpu_share()
+    layer = []
     for name, r, c in LAYER:
-        w = W[name][0].download(np.uint8, r * flh.row_bytes(Q4_K, c), s)
         x, st = xin[name]
-        xb = x.download(np.float32, st, s)
-        host[name] = (w, xb, r, c)
-    nbytes = sum(w.size for w, _, _, _ in host.values())
+        layer += host_case(flh, s, Q4_K, W[name][0], r, c, x, st, 1)
 
-    def run(threads):
-        for name, (w, xb, r, c) in host.items():
-            y = np.zeros(r, dtype=np.float32)
-            orc.stream_dot(Q4_K, w, r, c, xb, y, fast=True, threads=threads)
-    res = {}
-    for threads in (T, 1):
-        run(threads)
+    def run(cases, threads):
+        for fmt, w, r, c, xb, st, nx in cases:
+            y = np.zeros(nx * r, dtype=np.float32)
+            orc.stream_dot(fmt, w, r, c, xb, y, nx=nx, xstride=st, ystride=r, fast=True, threads=threads)
+
+    def rate(cases, threads, secs):
+        nbytes = sum(w.size for _, w, _, _, _, _, _ in cases)
+        run(cases, threads)
         reps, t0 = 0, time.perf_counter()
         while True:
-            run(threads)
+            run(cases, threads)
             reps += 1
             el = time.perf_counter() - t0
-            if el > (6.0 if threads > 1 else 4.0) or reps >= 50:
+            if el > secs:
                 break
-        res[threads] = nbytes * reps / el / 1e9
-    cpu_model = ""
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                cpu_model = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
-    return {"value": round(res[T], 3), "unit": "GB/s", "cores": T, "kind": kind,
-            "value_1thread": round(res[1], 3), "cpu": cpu_model,
-            "sample": f"the same layer step (4 Q4_K matvecs, {nbytes} weight bytes) on the "
-                      f"host, i8k int8 path (exec_task_cpu, fast + default masks), repeated "
-                      f">= 4-6 s per thread count"}
+        return nbytes, reps, el
+
+    nb, reps, el = rate(layer, T, 1.5)
+    val = nb * reps / el / 1e9
+    nb1, reps1, el1 = rate(layer, 1, 3.0)
+    configs = {}
+    for name, cases in cpu_in.items():
+        cb, cr, ce = rate(cases, T, 1.5)
+        configs[name] = {"us": round(ce / cr * 1e6, 1), "GBs": round(cb * cr / ce / 1e9, 3),
+                         "weight_bytes": cb, "reps": cr}
+    return {"value": round(val, 3), "unit": "GB/s", "cores": T, "kind": kind,
+            "us_per_step": round(el / reps * 1e6, 1), "value_1thread": round(nb1 * reps1 / el1 / 1e9, 3),
+            "cpu": cpu_model(), "configs": configs,
+            "sample": f"layer step (4 Q4_K matvecs, {nb} weight bytes) repeated {reps} times in "
+                      f"{el:.2f} s on {T} threads (and {reps1} times in {el1:.2f} s on 1 thread); each "
+                      f"other config repeated for ~1.5 s on {T} threads (configs.*.reps); reference "
+                      f"exec_task_cpu int8 path (fast, CPU default masks), rows split over threads"}
 
 
 if __name__ == "__main__":

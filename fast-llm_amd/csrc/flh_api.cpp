@@ -3,6 +3,7 @@
 // reference's Graph::freeze() rules, per-task dispatch and row-tile fusion.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <stdio.h>
 #include <string.h>
 #include <stdlib.h>
 #include <string>
@@ -70,15 +71,38 @@ static int validate_dot(int fmt, const void * w, uint64_t w_bytes, uint32_t rows
     return FLH_OK;
 }
 
-// Widest activation fused into its dot (every workgroup quantises the whole
-// fp32 column itself); wider ones get a separate ACT_Q8 launch.  Override:
-// FLH_FUSE_MAX_COLS.
-static uint32_t fuse_max_cols() {
-    static const uint32_t v = [] {
-        const char * e = getenv("FLH_FUSE_MAX_COLS");
-        return e ? (uint32_t)strtoul(e, nullptr, 0) : 8192u;
-    }();
-    return v;
+static Tune g_tune;
+const Tune & tune() { return g_tune; }
+
+// Development overrides of the launch tuning (see struct Tune).
+void load_tune() {
+    Tune t;
+    if (const char * e = getenv("FLH_FUSE_MAX_COLS")) t.fuse_max_cols = (uint32_t)strtoul(e, nullptr, 0);
+    if (const char * e = getenv("FLH_KS_TUNE")) {
+        unsigned a = 0, b = 0, c = 0, d = 0;
+        if (sscanf(e, "%u,%u,%u,%u", &a, &b, &c, &d) >= 3) {
+            t.ks_wgs_per_cu = a; t.ks_nr = b; t.ks_D = c; t.ks_pro = d;
+        }
+    }
+    if (const char * e = getenv("FLH_KS_W8")) {
+        unsigned a = 0, b = 0;
+        if (sscanf(e, "%u,%u", &a, &b) == 2) { t.ks_w8_mode = a; t.ks_w8_wgs = b; }
+    }
+    if (const char * e = getenv("FLH_KQ_TUNE")) {
+        unsigned a = 0, b = 0, c = 0;
+        if (sscanf(e, "%u,%u,%u", &a, &b, &c) == 3) { t.kq_wgs_per_cu = a; t.kq_nr = b; t.kq_D = c; }
+    }
+    if (const char * e = getenv("FLH_MFMA_PRO")) t.mf_pro = (uint32_t)atoi(e);
+    if (const char * e = getenv("FLH_MFMA_TUNE")) {
+        unsigned d = 0, n = 0, k = 0;
+        const int got = sscanf(e, "%u,%u,%u", &d, &n, &k);
+        if (got >= 2) { t.mf_D = d; t.mf_nrb = n; }
+        if (got == 3) t.mf_kh = (int)k;
+    }
+    if (const char * e = getenv("FLH_MFMA_XC")) t.mf_xc = atoi(e) != 0;
+    if (const char * e = getenv("FLH_MFMA_MIN_COLS")) t.mf_min_cols = (uint32_t)atoi(e);
+    if (const char * e = getenv("FLH_NO_MFMA")) t.no_mfma = atoi(e) != 0;
+    g_tune = t;
 }
 
 static int dispatch_dot(int fmt, const DotArgs & a, int fast, uint32_t i8_mask, uint32_t i8k_mask,
@@ -149,6 +173,7 @@ int flh_init(int device) {
     if (int rc = hip_check(hipGetDeviceProperties(&p, device), "hipGetDeviceProperties")) return rc;
     g_cus = p.multiProcessorCount > 0 ? p.multiProcessorCount : 256;
     g_device = device;
+    load_tune();
     return FLH_OK;
 }
 
@@ -304,7 +329,7 @@ int flh_act_q8_stream_dot(int fmt, const void * w, uint64_t w_bytes, uint32_t ro
     DotArgs a{(const uint8_t *)w, id_slot, estride, x, y, rows, cols, nx, xstride, ystride};
     // Fused when every workgroup re-reading the fp32 column is cheaper than a
     // separate ACT_Q8 launch.
-    if (fast && cols <= fuse_max_cols() && (fmt == FLH_FMT_Q4_K || fmt == FLH_FMT_Q6_K) && ((i8k_mask >> fmt) & 1u)) {
+    if (fast && cols <= tune().fuse_max_cols && (fmt == FLH_FMT_Q4_K || fmt == FLH_FMT_Q6_K) && ((i8k_mask >> fmt) & 1u)) {
         const int rc = launch_act_dot_kstream(fmt, a, s);
         if (rc != FLH_ERR_UNSUPPORTED) return rc;
     }
@@ -353,7 +378,7 @@ int flh_exec_tasks(const flh_task * t, uint32_t n, int fast, uint32_t i8_mask, u
                 // same outputs).
                 const flh_task * q = i + 1 < n ? &t[i + 1] : nullptr;
                 const bool canon_y = (const uint8_t *)k.y == (const uint8_t *)k.x + xq_off(k.cols);
-                if (q && canon_y && fast && k.cols <= fuse_max_cols() && q->kind == FLH_TASK_STREAM_DOT && q->x == k.x &&
+                if (q && canon_y && fast && k.cols <= tune().fuse_max_cols && q->kind == FLH_TASK_STREAM_DOT && q->x == k.x &&
                     q->cols == k.cols && (q->nx ? q->nx : 1u) == 1 &&
                     (q->fmt == FLH_FMT_Q4_K || q->fmt == FLH_FMT_Q6_K) && ((i8k_mask >> q->fmt) & 1u)) {
                     DotArgs a{(const uint8_t *)q->w, nullptr, 0, (const float *)q->x, (float *)q->y,

@@ -588,17 +588,7 @@ __global__ __launch_bounds__(256) void k_dot_i8_b32(DotArgs a, uint32_t nr) {
 // D-deep weight pipeline.  FLH_KQ_TUNE="wgs_per_cu,nr,D" overrides the
 // defaults (development sweeps only).
 struct KqTune { uint32_t wgs_per_cu, nr, D; };
-static KqTune kq_tune() {
-    static KqTune t = [] {
-        KqTune d{4, 0, 2};
-        if (const char * e = getenv("FLH_KQ_TUNE")) {
-            unsigned a = 0, b = 0, c = 0;
-            if (sscanf(e, "%u,%u,%u", &a, &b, &c) == 3) d = KqTune{a, b, c};
-        }
-        return d;
-    }();
-    return t;
-}
+static KqTune kq_tune() { return KqTune{tune().kq_wgs_per_cu, tune().kq_nr, tune().kq_D}; }
 
 static uint32_t pick_nr(uint32_t rows, uint32_t rpi, uint32_t nr_max) {
     const uint32_t target = (uint32_t)num_cus() * 8u;

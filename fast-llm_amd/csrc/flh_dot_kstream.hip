@@ -263,26 +263,13 @@ __global__ __launch_bounds__(256) void k_moe_kstream(MoeArgs a, uint32_t nr) {
 }
 
 // ----------------------------------------------------------------- launch --
-struct KsTune { uint32_t wgs_per_cu, nr, D, pro; };
-static KsTune ks_tune() {
-    static KsTune t = [] {
-        KsTune d{2, 0, 0, 0};
-        if (const char * e = getenv("FLH_KS_TUNE")) {
-            unsigned x = 0, y = 0, z = 0, q = 0;
-            if (sscanf(e, "%u,%u,%u,%u", &x, &y, &z, &q) >= 3) d = KsTune{x, y, z, q};
-        }
-        return d;
-    }();
-    return t;
-}
-
 // Chunks each wave requests before the activation is staged (the rest of its
 // ring is requested after its first chunk).  Reading a ready q8_K appendix
 // takes about as long as the first chunk, and a smaller launch-time burst
 // lands that chunk sooner: one (measured: Q4_K 4096x4096 5.6 -> 5.3 us).  A
 // fused ACT_Q8 keeps the waves busy quantising well after the first chunk
 // has landed: the whole ring (layer step 41.7 -> 40.3 us).
-static uint32_t ks_pro(bool fuse) { return ks_tune().pro ? ks_tune().pro : fuse ? 2u : 1u; }
+static uint32_t ks_pro(bool fuse) { return tune().ks_pro ? tune().ks_pro : fuse ? 2u : 1u; }
 
 static size_t g_lds_limit = 0;
 size_t lds_limit() {
@@ -308,7 +295,7 @@ static int ks_launch_x(const DotArgs & a, uint32_t nr, uint32_t grid, size_t smb
 template <int FMT, int NX, int D, bool FUSE>
 static int ks_launch_d(const DotArgs & a, uint32_t nr, uint32_t grid, size_t smb, hipStream_t s) {
     const uint32_t nsb = a.cols >> 8;
-    if (16 % nsb == 0 && !getenv("FLH_NO_XREG")) return ks_launch_x<FMT, NX, D, FUSE, true>(a, nr, grid, smb, s);
+    if (16 % nsb == 0) return ks_launch_x<FMT, NX, D, FUSE, true>(a, nr, grid, smb, s);
     return ks_launch_x<FMT, NX, D, FUSE, false>(a, nr, grid, smb, s);
 }
 
@@ -319,11 +306,11 @@ static int ks_launch_d(const DotArgs & a, uint32_t nr, uint32_t grid, size_t smb
 template <int FMT>
 static int ks_plan(uint32_t rows, uint32_t nx_t, uint32_t nsb, uint32_t slots, int Ddef,
                    uint32_t & nr, int & D, size_t & smb, int KW = 4) {
-    const KsTune t = ks_tune();
-    nr = t.nr ? t.nr : (rows + slots - 1) / slots;
+    const Tune & t = tune();
+    nr = t.ks_nr ? t.ks_nr : (rows + slots - 1) / slots;
     if (nr < 1) nr = 1;
     if (nr > 64u / nx_t) nr = 64u / nx_t;
-    D = t.D ? (int)t.D : Ddef;
+    D = t.ks_D ? (int)t.ks_D : Ddef;
     const size_t cap = KW == 4 ? 65536 : 81920;                  // two workgroups per CU / one
     const size_t lim = lds_limit() < cap ? lds_limit() : cap;
     while (ks_smem_bytes<FMT>(nr, nx_t, nsb, D, KW) > lim && nr > 4) nr >>= 1;
@@ -340,17 +327,15 @@ static int ks_plan(uint32_t rows, uint32_t nx_t, uint32_t nsb, uint32_t slots, i
 template <int FMT, int NX, bool FUSE>
 static int ks_launch(const DotArgs & a, hipStream_t s) {
     const uint32_t nsb = a.cols >> 8;
-    const KsTune t = ks_tune();
+    const Tune & t = tune();
     if constexpr (NX == 1) {
         // Two 8-wave workgroups per CU (16 waves) for single-column dots with
         // a fused ACT_Q8 or more than 16 superblocks per row: measured, the
         // Llama-3-8B layer step 41.8 -> 40.6 us (down 4096x14336 9.9 -> 9.2,
         // the fused ops each a little); the unfused 4096-column shapes stay on
-        // 4-wave workgroups (O 4096x4096: 5.2 vs 5.4 us).  FLH_KS_W8 =
-        // "mode,wgs_per_cu" overrides (mode bits 1: fused, nsb > 16;
-        // 2: fused, nsb <= 16; 4: unfused, nsb > 16; 8: unfused, nsb <= 16).
-        unsigned w8a = 7, w8b = 2;
-        if (const char * w8 = getenv("FLH_KS_W8")) sscanf(w8, "%u,%u", &w8a, &w8b);
+        // 4-wave workgroups (O 4096x4096: 5.2 vs 5.4 us).  Tune::ks_w8_*
+        // overrides.
+        const unsigned w8a = t.ks_w8_mode, w8b = t.ks_w8_wgs;
         const unsigned bit = (FUSE ? 1u : 4u) << (nsb > 16 ? 0 : 1);
         const bool use = (w8a & bit) != 0;
         if (use) {
@@ -370,7 +355,7 @@ static int ks_launch(const DotArgs & a, hipStream_t s) {
             }
         }
     }
-    const uint32_t slots = (uint32_t)num_cus() * (t.wgs_per_cu ? t.wgs_per_cu : 2);
+    const uint32_t slots = (uint32_t)num_cus() * (t.ks_wgs_per_cu ? t.ks_wgs_per_cu : 2);
     uint32_t nr;
     int D;
     size_t smb;
@@ -417,7 +402,7 @@ static int moe_launch(const MoeArgs & a, hipStream_t s) {
 int launch_moe_kstream(int fmt, const MoeArgs & a, hipStream_t s) {
     const uint32_t nsb = a.cols >> 8;
     if (nsb == 0 || (a.cols & 255) || nsb > 64) return FLH_ERR_UNSUPPORTED;
-    if ((uintptr_t)a.w & 15 || (a.estride & 15) || getenv("FLH_NO_KSTREAM")) return FLH_ERR_UNSUPPORTED;
+    if ((uintptr_t)a.w & 15 || (a.estride & 15)) return FLH_ERR_UNSUPPORTED;
     // columns per pass: the most pairs one expert can get, capped by what fits
     const uint32_t pairs = a.ntok * a.top_k;
     const uint32_t want = pairs < a.ntok ? pairs : a.ntok;     // an expert appears once per token
@@ -440,7 +425,6 @@ static int ks_dispatch(int fmt, const DotArgs & a, hipStream_t s) {
     if (nsb == 0 || (a.cols & 255) || nsb > 64 || a.nx > 4) return FLH_ERR_UNSUPPORTED;
     if ((uintptr_t)a.w & 15 || (a.estride & 15)) return FLH_ERR_UNSUPPORTED;
     if (FUSE && (((uintptr_t)a.x & 15) || (a.xstride & 3))) return FLH_ERR_UNSUPPORTED;
-    if (getenv("FLH_NO_KSTREAM")) return FLH_ERR_UNSUPPORTED;
     if (fmt == FMT_Q4_K)
         return a.nx == 1 ? ks_launch<FMT_Q4_K, 1, FUSE>(a, s) : a.nx == 2 ? ks_launch<FMT_Q4_K, 2, FUSE>(a, s)
                                                                          : ks_launch<FMT_Q4_K, 4, FUSE>(a, s);

@@ -841,13 +841,7 @@ __global__ __launch_bounds__(512) void k_moe_mfma(MoeArgs a, uint32_t nrbp) {
 // ----------------------------------------------------------------- launch --
 // chunks each wave requests before the activations are staged (the rest of
 // its ring after its first chunk); 0 = the whole ring (measured best here)
-static uint32_t mf_pro() {
-    static const uint32_t v = [] {
-        const char * e = getenv("FLH_MFMA_PRO");
-        return e ? (uint32_t)atoi(e) : 0u;            // 0: the whole ring
-    }();
-    return v;
-}
+static uint32_t mf_pro() { return tune().mf_pro; }          // 0: the whole ring
 template <int NC, int D, bool KH, bool XC = false>
 static int mf_launch_d(const DotArgs & a, uint32_t nrb, uint32_t grid, size_t smb, hipStream_t s) {
     (void)hipFuncSetAttribute((const void *)k_dot_mfma<NC, D, KH, XC>, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -875,36 +869,26 @@ static int mf_plan_kh(uint32_t rows, uint32_t nsb, uint32_t G, uint32_t & nrb, i
     // measured: a 2-deep ring with a full prologue beats deeper rings (N=4,
     // 14336x4096: D=2 11.7 us, D=3 12.4 us, D=4 13.0 us)
     D = 2;
-    int force_kh = -1;
-    if (const char * e = getenv("FLH_MFMA_TUNE")) {           // "D,nrb[,kh]" (development sweeps)
-        unsigned d = 0, n = 0, k = 0;
-        const int got = sscanf(e, "%u,%u,%u", &d, &n, &k);
-        if (got >= 2) {
-            if (d >= 2 && d <= 3) D = (int)d;
-            if (n >= 16 && n % 16 == 0 && n <= 512 / NC) nrb = n;
-        }
-        if (got == 3) force_kh = (int)k;
-    }
+    const Tune & t = tune();
+    if (t.mf_D >= 2 && t.mf_D <= 3) D = (int)t.mf_D;          // development sweeps
+    if (t.mf_nrb >= 16 && t.mf_nrb % 16 == 0 && t.mf_nrb <= 512 / NC) nrb = t.mf_nrb;
+    const int force_kh = t.mf_kh;
     kh = force_kh == 1 || (force_kh != 0 && mf_smem_bytes<NC, false>(16, nsb, 2) > lim);
-    // one 16-row tile per workgroup: activations in the chunks instead of halves
-    // (FLH_MFMA_XC: 0 off; 2 also where they fit whole; 3 also with several
-    // tiles per batch, re-fetching them per tile -- measured slower, kept for
-    // development sweeps)
-    static const int xc_mode = [] { const char * e = getenv("FLH_MFMA_XC"); return e ? atoi(e) : 1; }();
+    // K halves need at least 8 superblocks per row, and the grouped (MoE)
+    // planner allows them only as a last resort
+    if (kh && (nsb < 8 || (!allow_kh && force_kh != 1))) kh = false;
+    // one 16-row tile per workgroup where K halves would be needed: the
+    // activations ride in the chunks instead (Tune::mf_xc = false: off)
     if (xc) *xc = false;
-    if (xc && (kh || xc_mode >= 2) && force_kh != 1 && xc_mode && (nrb == 16 || xc_mode == 3)) {
-        uint32_t n = nrb;
-        while (mf_smem_bytes<NC, false, true>(n, nsb, 2) > lim && n > 16) n -= 16;
-        if (mf_smem_bytes<NC, false, true>(n, nsb, 2) <= lim) {
+    if (xc && kh && force_kh != 1 && t.mf_xc && nrb == 16) {
+        if (mf_smem_bytes<NC, false, true>(16, nsb, 2) <= lim) {
             *xc = true;
             kh = false;
             D = 2;
-            nrb = n;
-            smb = mf_smem_bytes<NC, false, true>(n, nsb, 2);
+            smb = mf_smem_bytes<NC, false, true>(16, nsb, 2);
             return FLH_OK;
         }
     }
-    if (kh && (nsb < 8 || (!allow_kh && force_kh != 1))) kh = false;
     if (kh) D = 2;                                            // the K-halves waits assume it
     auto bytes = [&]() { return kh ? mf_smem_bytes<NC, true>(nrb, nsb, D) : mf_smem_bytes<NC, false>(nrb, nsb, D); };
     while (bytes() > lim && nrb > 16) nrb -= 16;
@@ -932,11 +916,7 @@ static int mf_launch(const DotArgs & a, hipStream_t s) {
 // at 2 columns the streaming kernel is faster when a row's activation fits
 // its registers, cols <= 4096, and slower beyond).
 uint32_t mfma_min_cols(uint32_t cols) {
-    static const int v = [] {
-        const char * e = getenv("FLH_MFMA_MIN_COLS");
-        return e ? atoi(e) : 0;
-    }();
-    return v ? (uint32_t)v : (cols > 4096 ? 2u : 3u);
+    return tune().mf_min_cols ? tune().mf_min_cols : (cols > 4096 ? 2u : 3u);
 }
 
 uint32_t mfma_min_cols(uint32_t cols);
@@ -974,7 +954,7 @@ int launch_moe_mfma(int fmt, const MoeArgs & a, hipStream_t s) {
     const uint32_t nsb = a.cols >> 8;
     if (fmt != FMT_Q4_K || nsb == 0 || (a.cols & 255) || nsb > 64 || a.ntok < mfma_min_cols(a.cols))
         return FLH_ERR_UNSUPPORTED;
-    if (((uintptr_t)a.w & 15) || (a.estride & 15) || ((uintptr_t)a.x & 3) || (a.xstride & 3) || getenv("FLH_NO_MFMA") ||
+    if (((uintptr_t)a.w & 15) || (a.estride & 15) || ((uintptr_t)a.x & 3) || (a.xstride & 3) || tune().no_mfma ||
         a.ntok * a.top_k > 256)
         return FLH_ERR_UNSUPPORTED;
     // an expert gets at most one pair per token.  K halves only as a last
@@ -1001,7 +981,7 @@ int launch_dot_mfma(int fmt, const DotArgs & a, hipStream_t s) {
     const uint32_t nsb = a.cols >> 8;
     if (fmt != FMT_Q4_K || nsb == 0 || (a.cols & 255) || nsb > 64 || a.nx < 1 || a.nx > 16)
         return FLH_ERR_UNSUPPORTED;
-    if (((uintptr_t)a.w & 15) || (a.estride & 15) || ((uintptr_t)a.x & 3) || (a.xstride & 3) || getenv("FLH_NO_MFMA"))
+    if (((uintptr_t)a.w & 15) || (a.estride & 15) || ((uintptr_t)a.x & 3) || (a.xstride & 3) || tune().no_mfma)
         return FLH_ERR_UNSUPPORTED;
     if (a.nx <= 4) return mf_launch<4>(a, s);
     if (a.nx <= 8) return mf_launch<8>(a, s);

@@ -58,6 +58,29 @@ int launch_silu_act_q8(const float * gate, const float * up, float * h, uint32_t
 int launch_dot_i8k(int fmt, const DotArgs & a, hipStream_t s);    // Q4_K, Q6_K x q8_K
 // LDS-staged variant; FLH_ERR_UNSUPPORTED (nothing launched) if the shape
 // does not fit its plan
+// Launch tuning.  The defaults are the measured-best settings; flh_init()
+// (every call) re-reads the development overrides from the environment, so a
+// launch never reads the environment itself.
+struct Tune {
+    uint32_t fuse_max_cols = 8192;      // FLH_FUSE_MAX_COLS: widest activation fused into its dot
+    // streaming kernel, FLH_KS_TUNE = "wgs_per_cu,nr,D[,pro]" (0 = default)
+    uint32_t ks_wgs_per_cu = 0, ks_nr = 0, ks_D = 0, ks_pro = 0;
+    // single-column 8-wave workgroups, FLH_KS_W8 = "mode,wgs_per_cu" (mode bits
+    // 1: fused, > 16 superblocks; 2: fused, <= 16; 4: unfused, > 16; 8: unfused, <= 16)
+    uint32_t ks_w8_mode = 7, ks_w8_wgs = 2;
+    // register kernel, FLH_KQ_TUNE = "wgs_per_cu,nr,D"
+    uint32_t kq_wgs_per_cu = 4, kq_nr = 0, kq_D = 2;
+    // matrix-core kernel
+    uint32_t mf_pro = 0;                // FLH_MFMA_PRO: chunks per wave before staging (0: the ring)
+    uint32_t mf_D = 0, mf_nrb = 0;      // FLH_MFMA_TUNE = "D,nrb[,kh]" (0: planned)
+    int mf_kh = -1;                     //   kh: 1 force K halves, 0 never, -1 planned
+    bool mf_xc = true;                  // FLH_MFMA_XC=0: no activations-in-chunk mode
+    uint32_t mf_min_cols = 0;           // FLH_MFMA_MIN_COLS (0: 2 above 4096 columns, else 3)
+    bool no_mfma = false;               // FLH_NO_MFMA=1: never the matrix-core kernels
+};
+const Tune & tune();
+void load_tune();
+
 int launch_dot_kstream(int fmt, const DotArgs & a, hipStream_t s);
 // ACT_Q8 fused into the kstream dot: quantises x (fp32) in-kernel, writes both
 // appendices (workgroup 0), then streams; same bytes and results as

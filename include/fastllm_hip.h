@@ -107,7 +107,10 @@ const char * flh_last_error(void);
 
 /* Select and initialise a device; must precede every call below that touches
  * the GPU.  Replaces the device setup inside gpu_start()
- * (src/runtime/gpu_exec.cu:457-496; prototype runtime_internal.h:292). */
+ * (src/runtime/gpu_exec.cu:457-496; prototype runtime_internal.h:292).
+ * Each call also (re-)reads the launch-tuning overrides FLH_* from the
+ * environment (development sweeps; the defaults are the measured best); no
+ * launch reads the environment itself. */
 int flh_init(int device);
 
 /* Device facts: compute units, HBM bytes, wave size, name. */

@@ -16,7 +16,7 @@ import numpy as np
 import pytest
 
 from oracle import Q4_K
-from util import sane_rows, activations
+from util import sane_rows, activations, tuned
 from test_gpu_parity import run_dot, bits, say
 
 pytestmark = pytest.mark.gpu
@@ -49,12 +49,9 @@ def test_mfma_k_halves_bitwise(flh, orc, gpu, rows, cols, nx):
     rng = np.random.default_rng(rows + 5 * cols + nx)
     w = sane_rows(Q4_K, rows, cols, rng)
     xs = activations(nx, cols, rng, outliers=True)
-    os.environ["FLH_MFMA_TUNE"] = "2,0,1"
-    try:
+    with tuned(flh, FLH_MFMA_TUNE="2,0,1"):
         got, want = run_dot(flh, orc, gpu, Q4_K, w, rows, cols, xs, ystride=rows + 3,
                             y0=rng.standard_normal((nx - 1) * (rows + 3) + rows).astype(np.float32))
-    finally:
-        del os.environ["FLH_MFMA_TUNE"]
     assert np.array_equal(bits(got), bits(want))
 
 
@@ -66,10 +63,24 @@ def test_mfma_equals_streaming_kernel(flh, orc, gpu):
     w = sane_rows(Q4_K, rows, cols, rng)
     xs = activations(nx, cols, rng)
     got, want = run_dot(flh, orc, gpu, Q4_K, w, rows, cols, xs)
-    os.environ["FLH_NO_MFMA"] = "1"
-    try:
+    with tuned(flh, FLH_NO_MFMA=1):
         got2, _ = run_dot(flh, orc, gpu, Q4_K, w, rows, cols, xs)
-    finally:
-        del os.environ["FLH_NO_MFMA"]
+    assert np.array_equal(bits(got), bits(want))
+    assert np.array_equal(bits(got2), bits(got))
+
+
+@pytest.mark.parametrize("rows,cols,nx", [(4096, 14336, 8), (250, 14336, 7)])
+def test_mfma_activations_in_chunk_equals_k_halves(flh, orc, gpu, rows, cols, nx):
+    """One 16-row tile per workgroup with activations too wide to stage
+    whole: the activations-in-chunk mode (default) and K halves (FLH_MFMA_XC=0)
+    give the same bits, and both equal the oracle."""
+    say("mfma xc vs kh", rows, cols, nx)
+    rng = np.random.default_rng(rows + 11 * cols + nx)
+    w = sane_rows(Q4_K, rows, cols, rng)
+    xs = activations(nx, cols, rng, outliers=True)
+    y0 = rng.standard_normal((nx - 1) * rows + rows).astype(np.float32)
+    got, want = run_dot(flh, orc, gpu, Q4_K, w, rows, cols, xs, y0=y0)
+    with tuned(flh, FLH_MFMA_XC=0):
+        got2, _ = run_dot(flh, orc, gpu, Q4_K, w, rows, cols, xs, y0=y0)
     assert np.array_equal(bits(got), bits(want))
     assert np.array_equal(bits(got2), bits(got))

@@ -273,9 +273,6 @@ def test_router_moe_dot_fused_equals_separate(flh, gpu, fmt, ntok, rows, cols, p
 def test_grouped_expert_dot_k_halves_bitwise(flh, orc, gpu, ntok, rows, cols, per_slot):
     """The grouped matrix-core kernel with K halves forced (the mode wide
     expert inputs take when the whole activations do not fit LDS), bitwise."""
-    import os
-    os.environ["FLH_MFMA_TUNE"] = "2,0,1"
-    try:
+    from util import tuned
+    with tuned(flh, FLH_MFMA_TUNE="2,0,1"):
         grouped_dot_case(flh, orc, gpu, Q4_K, ntok, rows, cols, per_slot)
-    finally:
-        del os.environ["FLH_MFMA_TUNE"]

@@ -14,7 +14,7 @@ import pytest
 
 from oracle import (Q8_0, Q4_K, Q6_K, col_stride_floats, row_bytes, x_alloc_bytes, xq_offset,
                     xqk_offset)
-from util import sane_rows, normal_weights, activations
+from util import tuned, sane_rows, normal_weights, activations
 
 pytestmark = pytest.mark.gpu
 
@@ -356,8 +356,7 @@ def test_streaming_workgroup_shapes_bitwise(flh, orc, gpu, w8, fmt, rows, cols):
     rng = np.random.default_rng(rows + cols + fmt)
     w = sane_rows(fmt, rows, cols, rng)
     xs = activations(1, cols, rng, outliers=True)
-    os.environ["FLH_KS_W8"] = w8
-    try:
+    with tuned(flh, FLH_KS_W8=w8):
         got, want = run_dot(flh, orc, gpu, fmt, w, rows, cols, xs, y0=rng.standard_normal(rows).astype(np.float32))
         assert np.array_equal(bits(got), bits(want))
         if fmt != Q8_0:
@@ -369,5 +368,3 @@ def test_streaming_workgroup_shapes_bitwise(flh, orc, gpu, w8, fmt, rows, cols):
             want2 = np.zeros(rows, np.float32)
             orc.stream_dot(fmt, w, rows, cols, orc.act_q8_cols(xs, st), want2, threads=8)
             assert np.array_equal(bits(dy.download(np.float32, rows, gpu)), bits(want2))
-    finally:
-        del os.environ["FLH_KS_W8"]

@@ -31,3 +31,29 @@ def activations(nx, cols, rng, outliers=False):
     if outliers:
         x[rng.random(x.shape) < 0.01] *= 20.0
     return x
+
+
+class tuned:
+    """Development tuning overrides for one block: sets the FLH_* variables,
+    re-reads them into the library (flh_init re-reads the environment), and
+    restores both afterwards."""
+
+    def __init__(self, flh, **env):
+        self.flh, self.env = flh, env
+
+    def __enter__(self):
+        import os
+        self.old = {k: os.environ.get(k) for k in self.env}
+        os.environ.update({k: str(v) for k, v in self.env.items()})
+        self.flh.init(0)
+        return self
+
+    def __exit__(self, *exc):
+        import os
+        for k, v in self.old.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+        self.flh.init(0)
+        return False
