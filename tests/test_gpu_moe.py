@@ -47,6 +47,14 @@ def test_grouped_expert_dot_mixtral_gate_up_batch8(flh, orc, gpu):
     grouped_dot_case(flh, orc, gpu, Q4_K, 8, 28672, 4096, False)
 
 
+@pytest.mark.parametrize("rows,cols,per_slot", [(28672, 4096, False), (4096, 14336, True)])
+def test_grouped_expert_dot_mixtral_batch1(flh, orc, gpu, rows, cols, per_slot):
+    """The benchmark's MoE batch-1 shapes (one token, top-2 of 8 experts):
+    the fused gate/up 28672x4096 and the down 4096x14336 per expert on the
+    grouped streaming kernel, bitwise."""
+    grouped_dot_case(flh, orc, gpu, Q4_K, 1, rows, cols, per_slot)
+
+
 def grouped_dot_case(flh, orc, gpu, fmt, ntok, rows, cols, per_slot):
     say("moe_dot", fmt, ntok, rows, cols, per_slot)
     rng = np.random.default_rng(ntok * 31 + rows + cols + fmt)

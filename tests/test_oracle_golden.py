@@ -118,3 +118,46 @@ def test_iq_canonical_dots_match_reference(orc, golden):
     y = np.zeros(1, dtype=np.float32)
     orc.stream_dot(5, golden["iq_kat_w"], 1, 256, golden["iq_kat_x"], y, fast=False)
     assert y[0] == golden["iq_kat_y"][0] == 2.0
+
+
+# ---- BASELINE widths (tests/golden/golden_wide.npz, inputs regenerated from seeds)
+def _wide():
+    import os
+    return np.load(os.path.join(os.path.dirname(__file__), "golden", "golden_wide.npz"))
+
+
+def test_wide_inputs_regenerate_bit_for_bit():
+    """The seeded generator still yields the bytes the reference saw."""
+    from wide_cases import WIDE_CASES, wide_case_inputs, digest
+    g = _wide()
+    assert int(g["wide_count"][0]) == len(WIDE_CASES)
+    for i, case in enumerate(WIDE_CASES):
+        assert list(g[f"w{i}_meta"]) == list(case)
+        w, xs, y0 = wide_case_inputs(*case)
+        assert bytes(g[f"w{i}_digest"]) == digest(w, xs, y0), i
+
+
+@pytest.mark.parametrize("i", range(11))
+def test_oracle_wide_dots_match_reference(orc, i):
+    """Int8 STREAM_DOT at the Llama-3-8B widths (4096 / 14336 columns, 1-8
+    columns): the oracle equals the reference bit for bit."""
+    from oracle import col_stride_floats
+    from wide_cases import WIDE_CASES, wide_case_inputs
+    g = _wide()
+    fmt, rows, cols, nx, seed = WIDE_CASES[i]
+    w, xs, y0 = wide_case_inputs(fmt, rows, cols, nx, seed)
+    st = col_stride_floats(cols)
+    y = y0.copy()
+    orc.stream_dot(fmt, w, rows, cols, orc.act_q8_cols(xs, st), y, nx=nx, xstride=st, ystride=rows, threads=8)
+    assert np.array_equal(bits(y), bits(g[f"w{i}_y"]))
+
+
+def test_q8_0_weight_quantizer_matches_reference_q8_1_blocks(flh):
+    """The library's Q8_0 weight quantizer (host path) writes the reference's
+    q8_1 block bytes without s (fl_quantize_q8_1_block, quants.h:360-378)."""
+    from wide_cases import Q8_0_QUANT
+    g = _wide()
+    rows, cols, seed = Q8_0_QUANT
+    wf = (np.random.default_rng(seed).standard_normal((rows, cols)) * 0.02).astype(np.float32)
+    got = flh.quantize_host(1, wf).reshape(rows, -1)
+    assert np.array_equal(got, g["q80_bytes"])
