@@ -116,11 +116,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-ops", action="store_true", help="headline only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--profile", nargs="?", const="gate_up", choices=["gate_up", "verify8"],
+    ap.add_argument("--profile", nargs="?", const="gate_up", choices=sorted(PROFILE_OPS),
                     help="counter-collection run: a 256 MiB device copy (calibration) and "
-                         "64 launches of one kernel only (gate_up: the dominant Q4_K "
-                         "28672x4096 N=1 matvec; verify8: Q4_K 14336x4096 with 8 columns on "
-                         "the matrix-core kernel), no JSON line")
+                         "64 launches of one operation only (see PROFILE_OPS), no JSON line")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the matvec would shard by "
@@ -282,32 +280,60 @@ def main():
     print(json.dumps(result), flush=True)
 
 
+# Operations a --profile run launches (64 times each, rotating over weight
+# copies > 3x the Infinity Cache): name -> (format, rows, cols, columns, kind)
+# kind: "dot" (STREAM_DOT on a ready appendix), "fused" (ACT_Q8 + STREAM_DOT
+# in one launch), "act" (ACT_Q8 alone), "dot_nomfma" (the streaming kernel
+# with the matrix-core kernel switched off).
+PROFILE_OPS = {
+    "gate_up": (Q4_K, 28672, 4096, 1, "dot"), "gate_up_fused": (Q4_K, 28672, 4096, 1, "fused"),
+    "qkv": (Q4_K, 6144, 4096, 1, "dot"), "qkv_fused": (Q4_K, 6144, 4096, 1, "fused"),
+    "o": (Q4_K, 4096, 4096, 1, "dot"), "o_fused": (Q4_K, 4096, 4096, 1, "fused"),
+    "down": (Q4_K, 4096, 14336, 1, "dot"), "act_down": (Q4_K, 4096, 14336, 1, "act"),
+    "q6k_vocab": (Q6_K, 128256, 4096, 1, "dot"), "q6k_down": (Q6_K, 4096, 14336, 1, "dot"),
+    "q8_0": (Q8_0, 4096, 4096, 1, "dot"),
+}
+for _n in (2, 4, 8):
+    for _r, _c in ((14336, 4096), (4096, 14336)):
+        PROFILE_OPS[f"verify{_n}_{_r}x{_c}"] = (Q4_K, _r, _c, _n, "dot")
+        PROFILE_OPS[f"verify{_n}_{_r}x{_c}_kstream"] = (Q4_K, _r, _c, _n, "dot_nomfma")
+PROFILE_OPS["verify8"] = PROFILE_OPS["verify8_14336x4096"]
+
+
 def profile_run(flh, B, s, staging, which="gate_up"):
     """What the committed counter profiles were collected on: 5 device copies
-    of 256 MiB (known HBM bytes: read 256 MiB + write 256 MiB each) and 64
-    launches of one matvec rotating over its weight copies: the Q4_K gate/up
-    28672x4096 at N=1 (gate_up) or the Q4_K 14336x4096 verify matvec with 8
-    activation columns (verify8)."""
+    of 256 MiB (known HBM bytes: read 256 MiB + write 256 MiB each), then 64
+    launches of one operation of PROFILE_OPS."""
     n = 256 << 20
     src, dst = B.buf(n), B.buf(n)
     src.zero(s)
     for _ in range(5):
         flh.copy(dst, src, n, s)
     s.sync()
-    r, c, nx = (28672, 4096, 1) if which == "gate_up" else (14336, 4096, 8)
-    nb = r * flh.row_bytes(Q4_K, c)
-    ws = B.weights(Q4_K, r, c, copies_for(nb), seed=101 + r + 7 * c, staging=staging)
-    x, st = B.activation(c, nx, 12, outliers=True)
+    fmt, r, c, nx, kind = PROFILE_OPS[which]
+    if kind == "dot_nomfma":
+        os.environ["FLH_NO_MFMA"] = "1"
+        flh.init(0)
+    nb = r * flh.row_bytes(fmt, c)
+    ws = B.weights(fmt, r, c, copies_for(nb), seed=101 + r + 7 * c, staging=staging)
+    x, st = B.activation(c, nx, 12, outliers=fmt == Q4_K)
     y = B.buf(nx * r * 4)
     for i in range(64):
-        flh.stream_dot(Q4_K, ws[i % len(ws)], r, c, x, y, s, nx=nx, xstride=st, ystride=r)
+        if kind == "fused":
+            flh.act_q8_stream_dot(fmt, ws[i % len(ws)], r, c, x, y, s)
+        elif kind == "act":
+            flh.act_q8(x, c, s)
+        else:
+            flh.stream_dot(fmt, ws[i % len(ws)], r, c, x, y, s, nx=nx, xstride=st, ystride=r)
     s.sync()
 
 
 def traffic_from_profile():
-    """HBM bytes per launch of the dominant kernel, from the committed
-    rocprofv3 --pmc summary (profiles/pmc_q4_K_gate_up_28672x4096.json)."""
-    f = os.path.join(ROOT, "profiles", "pmc_q4_K_gate_up_28672x4096.json")
+    """HBM bytes per launch of the step's dominant kernel (the fused ACT_Q8 +
+    gate/up launch), from the committed rocprofv3 --pmc summary
+    (profiles/pmc_q4_K_gate_up_28672x4096_fused.json; FETCH_SIZE and
+    WRITE_SIZE scaled by a 256 MiB copy's readings, profiles/q4_K_gate_up_28672x4096.md)."""
+    f = os.path.join(ROOT, "profiles", "pmc_q4_K_gate_up_28672x4096_fused.json")
     try:
         with open(f) as fh:
             return json.load(fh).get("traffic_bytes_per_launch")
