@@ -176,6 +176,7 @@ __device__ __forceinline__ void ks_body(const uint8_t * __restrict__ w, uint32_t
             ks_wait_behind<NI, D>(nissued - 1 - ncons);
             ++ncons;
             if (i == 0 && bt == 0) KS_STAMP(2);
+            if (i == 1 && bt == 0) KS_STAMP(7);
             uint8_t * st = myst + slot * WIN;
             const uint32_t f = (wave + KW * i) * 16 + s;           // batch-local superblock
             const bool act = f < nsbb;
@@ -196,12 +197,14 @@ __device__ __forceinline__ void ks_body(const uint8_t * __restrict__ w, uint32_t
             slot = slot + 1 == (uint32_t)D ? 0 : slot + 1;
             ks_park<FMT, NX>(ia, im, tag, act, c, nx, rl, sb, nsb, TI, TM, TH);
         }
+        KS_STAMP(12);
         // wave 0: chunks issued after the y DMA are the only loads that can be
         // younger than it and still outstanding (at most D of them)
         if (wave == 0) ks_wait_behind<NI, D + 1>(min(nissued - y_at, (uint32_t)D));
         lds_barrier();
         KS_STAMP(3);
         const float r = ks_fold<FMT, NX>(TI, TM, TH, xd, nsb, fk, fp, frl, fok);
+        KS_STAMP(8);
         if (fok && fk == 0) ycol[row0 + frl] = ysm[frl * NX + fp] + r;
         lds_barrier();
     }
@@ -328,6 +331,10 @@ template <int FMT, int NX, bool FUSE>
 static int ks_launch(const DotArgs & a, hipStream_t s) {
     const uint32_t nsb = a.cols >> 8;
     const Tune & t = tune();
+    if (FMT == FMT_Q4_K && NX == 1 && t.sbl) {
+        const int rc = launch_dot_sbl(FMT, a, FUSE, s);
+        if (rc != FLH_ERR_UNSUPPORTED) return rc;
+    }
     if constexpr (NX == 1) {
         // Two 8-wave workgroups per CU (16 waves) for single-column dots with
         // a fused ACT_Q8 or more than 16 superblocks per row: measured, the

@@ -1,0 +1,420 @@
+// flh_dot_sbl.hip -- single-column Q4_K x q8_K row-dots with one superblock
+// per lane.
+//
+// The streaming kernel of flh_dot_kstream.hip splits a superblock over four
+// lanes, which costs every quarter its own scale decode, a DPP reduction and
+// a parked term, and it folds each batch of rows after a workgroup barrier.
+// For one activation column the work per superblock is small enough that the
+// lane can take all of it:
+//
+//   * a CHUNK is rpc = floor(64 / nsb) whole rows (rpc * nsb superblocks,
+//     one per lane, row r = lane / nsb, position s = lane % nsb); its bytes
+//     go HBM -> LDS in 16-byte direct-to-LDS loads, each 1 KiB request of a
+//     wave fully coalesced;
+//   * a lane's activation superblock is the same for every chunk (position s),
+//     so its q8_K block (256 int8, 8 sub-block sums, d) lives in 73 VGPRs for
+//     the whole launch;
+//   * the lane computes the superblock's exact integer partials
+//     (iacc = sum_g sc_g * dot_g, imin = sum_g m_g * bsum_g) and the two
+//     reference factors d*dk and -(dmin*dk), parks them in a 1 KiB wave-local
+//     LDS area, and lanes (row, k) of the same wave fold accumulator k over
+//     positions k, k+4, ... with the reference's fmaf order, then
+//     (a0 + a1) + (a2 + a3) by DPP: bitwise fl_dot_i8k_q4_K
+//     (src/runtime/quants.h:538-561);
+//   * waves are independent after the activation is staged: no barrier per
+//     batch, each wave keeps two chunks in flight and refills a stage as soon
+//     as its reads are done.
+//
+// Chunks are dealt to workgroups first (chunk c -> workgroup c % G), so a
+// matrix with fewer chunks than waves still spreads over every CU.
+// With FUSE, the workgroup quantises the fp32 column itself (ACT_Q8,
+// src/runtime/quants.h:382-402): wave w takes superblocks w, w + W, ...; the
+// staged bytes are the q8_K block's, and workgroup 0 also writes both
+// appendices, so memory ends up as after a separate ACT_Q8 launch.
+#include "flh_kstream.h"
+#include "flh_internal.h"
+#include "flh_status.h"
+
+namespace flh {
+
+// Development timing probe (compiled only with -DFLH_TRACE): per wave of
+// the single-column kernel, s_memrealtime stamps at entry (0), after the
+// activation barrier (1), when the first chunk has landed (2), when the last
+// chunk has landed (3), at exit (4); slot 7 holds the chunk count.
+#ifdef FLH_TRACE
+__device__ uint64_t g_sbl_trace[4096 * 8 * 8];
+#define SBL_STAMP(k) do { if (lane == 0 && blockIdx.x < 4096) \
+    g_sbl_trace[((size_t)blockIdx.x * 8 + wave) * 8 + (k)] = __builtin_amdgcn_s_memrealtime(); } while (0)
+extern "C" int flh_sbl_trace(uint64_t * host, size_t n) {
+    return hipMemcpyFromSymbol(host, HIP_SYMBOL(g_sbl_trace), n * 8, 0, hipMemcpyDeviceToHost) == hipSuccess ? 0 : -2;
+}
+#else
+#define SBL_STAMP(k) do { } while (0)
+#endif
+
+namespace {
+
+constexpr uint32_t SBL_XS = 304;    // LDS bytes per staged q8_K block
+// A staged block is the 292-byte q8_K block placed 12 bytes into its 304-byte
+// slot: f32 d at +12, int16 bsums[16] at +16, int8 qs[256] at +48 (both
+// 16-byte aligned).  304 = 76 dwords: 16 consecutive blocks start in 16
+// distinct 4-bank groups, so lanes reading 16 positions do not conflict.
+
+// s_waitcnt vmcnt(n) for a wave-uniform run-time n (clamped to 31: waiting
+// for more loads than asked is always safe)
+__device__ __forceinline__ void wait_vm_dyn(uint32_t n) {
+    switch (n) {
+#define FLH_WV(k) case k: WAIT_VM(k); break;
+        FLH_WV(0) FLH_WV(1) FLH_WV(2) FLH_WV(3) FLH_WV(4) FLH_WV(5) FLH_WV(6) FLH_WV(7)
+        FLH_WV(8) FLH_WV(9) FLH_WV(10) FLH_WV(11) FLH_WV(12) FLH_WV(13) FLH_WV(14) FLH_WV(15)
+        FLH_WV(16) FLH_WV(17) FLH_WV(18) FLH_WV(19) FLH_WV(20) FLH_WV(21) FLH_WV(22) FLH_WV(23)
+        FLH_WV(24) FLH_WV(25) FLH_WV(26) FLH_WV(27) FLH_WV(28) FLH_WV(29) FLH_WV(30)
+#undef FLH_WV
+        default: WAIT_VM(31); break;
+    }
+}
+
+// the 144-byte Q4_K superblock at LDS address p as 9 x 16 bytes
+__device__ __forceinline__ void lds_ld_q4k(const void * p, u32x4a (&v)[9]) {
+    asm volatile("ds_read_b128 %0, %9\n\tds_read_b128 %1, %9 offset:16\n\tds_read_b128 %2, %9 offset:32\n\t"
+                 "ds_read_b128 %3, %9 offset:48\n\tds_read_b128 %4, %9 offset:64\n\tds_read_b128 %5, %9 offset:80\n\t"
+                 "ds_read_b128 %6, %9 offset:96\n\tds_read_b128 %7, %9 offset:112\n\tds_read_b128 %8, %9 offset:128\n\t"
+                 "s_waitcnt lgkmcnt(0)"
+                 : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]), "=&v"(v[6]),
+                   "=&v"(v[7]), "=&v"(v[8])
+                 : "v"(lds_off(p)) : "memory");
+}
+// 16 bytes at LDS address p; the caller waits (lds_wait4) before any use
+__device__ __forceinline__ u32x4a lds_ld128_nw(const void * p) {
+    u32x4a v;
+    asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(lds_off(p)) : "memory");
+    return v;
+}
+__device__ __forceinline__ void lds_wait4(u32x4a & a, u32x4a & b, u32x4a & c, u32x4a & d) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d) :: "memory");
+}
+__device__ __forceinline__ void lds_st16(void * p, uint32_t v) {
+    asm volatile("ds_write_b16 %0, %1" :: "v"(lds_off(p)), "v"(v));
+}
+// global store kept out of the compiler's wait-count bookkeeping (the wave
+// counts its own memory operations)
+__device__ __forceinline__ void gst_x1(float * p, uint32_t v) {
+    asm volatile("global_store_dword %0, %1, off" :: "v"(p), "v"(v) : "memory");
+}
+
+// A lane's activation superblock: 64 dwords of int8, the 8 sub-block sums
+// (bsums[2t] + bsums[2t+1]), and d.
+struct XQ4 {
+    u32x4a q[16];
+    int b[8];
+    float dk;
+};
+
+__device__ __forceinline__ void load_xq4(const uint8_t * xb, XQ4 & X) {
+    u32x4a bs0, bs1;
+    asm volatile("ds_read_b128 %0, %18 offset:48\n\tds_read_b128 %1, %18 offset:64\n\tds_read_b128 %2, %18 offset:80\n\t"
+                 "ds_read_b128 %3, %18 offset:96\n\tds_read_b128 %4, %18 offset:112\n\tds_read_b128 %5, %18 offset:128\n\t"
+                 "ds_read_b128 %6, %18 offset:144\n\tds_read_b128 %7, %18 offset:160\n\tds_read_b128 %8, %18 offset:176\n\t"
+                 "ds_read_b128 %9, %18 offset:192\n\tds_read_b128 %10, %18 offset:208\n\tds_read_b128 %11, %18 offset:224\n\t"
+                 "ds_read_b128 %12, %18 offset:240\n\tds_read_b128 %13, %18 offset:256\n\tds_read_b128 %14, %18 offset:272\n\t"
+                 "ds_read_b128 %15, %18 offset:288\n\tds_read_b128 %16, %18 offset:16\n\tds_read_b128 %17, %18 offset:32\n\t"
+                 "s_waitcnt lgkmcnt(0)"
+                 : "=&v"(X.q[0]), "=&v"(X.q[1]), "=&v"(X.q[2]), "=&v"(X.q[3]), "=&v"(X.q[4]), "=&v"(X.q[5]),
+                   "=&v"(X.q[6]), "=&v"(X.q[7]), "=&v"(X.q[8]), "=&v"(X.q[9]), "=&v"(X.q[10]), "=&v"(X.q[11]),
+                   "=&v"(X.q[12]), "=&v"(X.q[13]), "=&v"(X.q[14]), "=&v"(X.q[15]), "=&v"(bs0), "=&v"(bs1)
+                 : "v"(lds_off(xb)) : "memory");
+    X.dk = __uint_as_float(lds_ld32(xb + 12));
+    const uint32_t w[8] = {bs0.x, bs0.y, bs0.z, bs0.w, bs1.x, bs1.y, bs1.z, bs1.w};
+#pragma unroll
+    for (int t = 0; t < 8; ++t) X.b[t] = (int)(int16_t)(w[t] & 0xFFFFu) + (int)(int16_t)(w[t] >> 16);
+}
+
+// Exact integer partials of one Q4_K superblock against the lane's
+// activation: iacc = sum_t sc_t * dot_t, imin = sum_t m_t * bsum_t.  Sub-block
+// pair g holds sub-block 2g in the low nibbles of qs[32g..32g+31] and 2g+1 in
+// the high nibbles.  Every product fits 24 bits (sc, m < 64; |dot| <= 60960;
+// |bsum| <= 4064), so the multiplies are full-rate v_mul_i32_i24.
+__device__ __forceinline__ void sbl_q4k(const u32x4a (&w)[9], const XQ4 & X, int & ia, int & im) {
+    const u32x4a hd = w[0];
+    const uint32_t sclo = hd.y & 0x3F3F3F3Fu, mlo = hd.z & 0x3F3F3F3Fu;
+    const uint32_t schi = (hd.w & 0x0F0F0F0Fu) | ((hd.y >> 2) & 0x30303030u);
+    const uint32_t mhi = ((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u);
+    int acc = 0;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const u32x4a qa = w[1 + 2 * g], qb = w[2 + 2 * g];
+        const uint32_t Q[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+        const u32x4a xa = X.q[4 * g], xb = X.q[4 * g + 1], xc = X.q[4 * g + 2], xd = X.q[4 * g + 3];
+        const uint32_t XL[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+        const uint32_t XH[8] = {xc.x, xc.y, xc.z, xc.w, xd.x, xd.y, xd.z, xd.w};
+        int dl[2] = {0, 0}, dh[2] = {0, 0};                     // two chains each (exact sums)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            dl[i & 1] = dot4((int)(Q[i] & 0x0F0F0F0Fu), (int)XL[i], dl[i & 1]);
+            dh[i & 1] = dot4((int)((Q[i] >> 4) & 0x0F0F0F0Fu), (int)XH[i], dh[i & 1]);
+        }
+        const int dlo = dl[0] + dl[1], dhi = dh[0] + dh[1];
+        const uint32_t scw = g < 2 ? sclo : schi, sh = 16 * (g & 1);
+        acc += __mul24((int)((scw >> sh) & 0xFFu), dlo) + __mul24((int)((scw >> (sh + 8)) & 0xFFu), dhi);
+    }
+    int mi = 0;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) mi += __mul24((int)(((t < 4 ? mlo : mhi) >> (8 * (t & 3))) & 0xFFu), X.b[t]);
+    ia = acc;
+    im = mi;
+}
+
+}  // namespace
+
+// One pass over all rows for one column.  Launch: G workgroups of W waves,
+// dynamic LDS = W * 2 * slot (rings) + the staged activation (rounded to
+// 1 KiB) + W * 1280 bytes (fold terms and old y values).
+template <bool FUSE, int W>
+__global__ __launch_bounds__(64 * W) void k_dot_sbl(DotArgs a, uint32_t rpc, uint32_t ni, uint32_t slot, uint32_t pre) {
+    constexpr uint32_t B = 144;
+    extern __shared__ __attribute__((aligned(16))) uint8_t sm[];
+    const uint32_t nsb = a.cols >> 8, rows = a.rows, cols = a.cols;
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t G = gridDim.x, b = blockIdx.x;
+    const uint32_t C = (rows + rpc - 1) / rpc;                    // chunks of the matrix
+    const uint32_t first = b + G * wave, stride = G * W;          // this wave's chunks: first + stride * i
+    const uint32_t nck = first < C ? (C - first + stride - 1) / stride : 0u;
+    uint8_t * ring = sm + (size_t)wave * 2 * slot;
+    uint8_t * xs = sm + (size_t)W * 2 * slot;
+    const uint32_t xs_bytes = (nsb * SBL_XS + 1023u) & ~1023u;
+    uint8_t * T = xs + xs_bytes + wave * 1280u;                   // [64][16 B] fold terms of this wave
+    uint8_t * Y = T + 1024;                                       // [64] old y values of this wave
+    const uint8_t * w = a.w + (a.id_slot ? (size_t)(*a.id_slot) * a.estride : 0);
+    const uint64_t cb = (uint64_t)rpc * nsb * B;                  // bytes of a full chunk
+    const uint8_t * xk = (const uint8_t *)a.x + xqk_off(cols);
+    uint32_t ops = 0;                                             // memory operations issued by this wave
+    SBL_STAMP(0);
+
+    // Old y values (y += semantics) of up to ypc chunks go to Y by a DMA:
+    // word l holds row l % rpc of chunk l / rpc.  Issued first, so every
+    // later wait covers it.
+    const uint32_t ypc = 64u / rpc;
+    const uint32_t yi = lane / rpc, yr = lane - yi * rpc;
+    auto yload = [&](uint32_t grp) {
+        const uint32_t i = grp * ypc + yi;
+        const uint32_t row = (first + stride * i) * rpc + yr;
+        const bool v = yi < ypc && i < nck && row < rows;
+        __builtin_amdgcn_global_load_lds(GPTR(a.y + (v ? row : 0u)), LPTR(Y), 4, 0, 0);
+        ++ops;
+    };
+    yload(0);
+    uint32_t y_mark = ops;
+
+    // activation: DMA of the q8_K blocks into the staged layout, or (FUSE)
+    // of the fp32 superblocks w, w + W, ... of this wave into its second
+    // ring stage (its first chunk is requested after the quantisation)
+    const uint32_t nfi = FUSE ? (nsb > wave ? (nsb - wave + W - 1) / W : 0u) : 0u;   // <= 8 (host check)
+    if constexpr (FUSE) {
+        for (uint32_t j = 0; j < nfi; ++j) {
+            __builtin_amdgcn_global_load_lds(GPTR(a.x + 256 * (wave + W * j) + 4 * lane), LPTR(ring + slot + 1024 * j),
+                                             16, 0, 0);
+            ++ops;
+        }
+    } else {
+        const uint32_t P = nsb * 19, nxi = (P + 63) / 64;
+        for (uint32_t t = wave; t < nxi; t += W) {
+            const uint32_t j = 64 * t + lane, jj = j < P ? j : P - 1;
+            const uint32_t s = jj / 19, i = jj - 19 * s;
+            __builtin_amdgcn_global_load_lds(GPTR(xk + 292 * s + 16 * i - 12), LPTR(xs + 1024 * t), 16, 0, 0);
+            ++ops;
+        }
+    }
+    const uint32_t x_mark = ops;
+    // Every wave's activation requests enter the CU's memory queue before any
+    // weight request: served in order, they would otherwise wait behind the
+    // CU's whole initial weight burst (~150 KB, several us at a CU's share of
+    // HBM bandwidth), and no wave could start before the last one.
+    __builtin_amdgcn_s_barrier();
+
+    // weight prologue: chunks 0 and (unless the stage holds fp32 x) 1
+    uint32_t mark[2] = {0u, 0u};
+    auto issue = [&](uint32_t i, uint8_t * st) {
+        const uint32_t c = first + stride * i;
+        const uint8_t * g = w + (uint64_t)c * cb;
+        const uint32_t nrow = min(rpc, rows - c * rpc);
+        const uint32_t vb = nrow * nsb * B;                       // valid bytes (a multiple of 16)
+        for (uint32_t t = 0; t < ni; ++t) {
+            const uint32_t o = 1024 * t + 16 * lane;
+            __builtin_amdgcn_global_load_lds(GPTR(g + (o < vb ? o : vb - 16)), LPTR(st + 1024 * t), 16, 0, FLH_KS_AUX);
+        }
+        ops += ni;
+    };
+    // Only waves below `pre` request a chunk before the activation has
+    // landed: the activation's own requests queue chip-wide behind whatever
+    // the launch has asked for (a 37 MB initial burst delays them by ~4 us).
+    const bool early = wave < pre;
+    if (early && nck > 0) { issue(0, ring); mark[0] = ops; }
+
+#ifdef FLH_TRACE
+    wait_vm_dyn(ops - 1);                                         // diagnostic: the old y values alone
+    SBL_STAMP(5);
+#endif
+    // wait for this wave's activation loads alone
+    wait_vm_dyn(ops - x_mark);
+    if constexpr (FUSE) {
+        uint8_t * q81 = (uint8_t *)a.x + xq_off(cols);
+        uint8_t * q8k = (uint8_t *)a.x + xqk_off(cols);
+        const uint8_t * xf = ring + slot + 16 * lane;
+        // items j = 4h .. 4h+3: four absmaxes, one division sequence (lanes
+        // 0..3), then per item the bytes, block sums and d of the q8_K block
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            if ((uint32_t)(4 * h) >= nfi) break;                   // wave-uniform
+            float v[4][4];
+            uint32_t am[4] = {0u, 0u, 0u, 0u};
+            u32x4a rr[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) rr[j] = lds_ld128_nw(xf + 1024 * ((uint32_t)(4 * h + j) < nfi ? 4 * h + j : 0));
+            lds_wait4(rr[0], rr[1], rr[2], rr[3]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const u32x4a r = rr[j];
+                v[j][0] = __uint_as_float(r.x); v[j][1] = __uint_as_float(r.y);
+                v[j][2] = __uint_as_float(r.z); v[j][3] = __uint_as_float(r.w);
+                if ((uint32_t)(4 * h + j) < nfi) am[j] = umax64(__float_as_uint(absmax4(v[j])));
+            }
+            const float al = __uint_as_float(lane == 0 ? am[0] : lane == 1 ? am[1] : lane == 2 ? am[2] : am[3]);
+            const float dl = al / 127.f;
+            const float idl = al > 0.f ? 127.f / al : 0.f;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if ((uint32_t)(4 * h + j) >= nfi) break;
+                const uint32_t s = wave + W * (4 * h + j);
+                const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dl), j));
+                const float id = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(idl), j));
+                const uint32_t pk = quant4(v[j], id);
+                const int s16 = sum4i(dot4((int)pk, 0x01010101, 0));     // 16-element block sum
+                uint8_t * xb = xs + SBL_XS * s;
+                lds_st32(xb + 48 + 4 * lane, pk);
+                if ((lane & 3) == 0) lds_st16(xb + 16 + 2 * (lane >> 2), (uint32_t)s16);
+                if (lane == 0) lds_st32(xb + 12, __float_as_uint(d));
+                if (b == 0) act_q8_lanes(v[j], lane, s, q81, q8k, cols);
+            }
+        }
+    }
+    SBL_STAMP(6);
+    lds_barrier();
+    SBL_STAMP(1);
+    XQ4 X;
+    load_xq4(xs + SBL_XS * (lane % nsb), X);
+    // The rest of the prologue comes after the barrier: a request blocks its
+    // wave while the CU's memory queue is full, and a wave stuck there would
+    // hold the whole workgroup at the barrier.
+    if (!early && nck > 0) { issue(0, ring); mark[0] = ops; }
+    // (FUSE: the second stage's fp32 reads are done, lds_wait4)
+    if (nck > 1) { issue(1, ring + slot); mark[1] = ops; }
+
+    const uint32_t fr = lane >> 2, fk = lane & 3;                 // fold lane: row r0 + fr, accumulator fk
+    for (uint32_t i = 0; i < nck; ++i) {
+        const uint32_t sl = i & 1u;
+        uint8_t * st = ring + sl * slot;
+        const uint32_t il = i % ypc;
+        if (il == 0 && i != 0) {                                  // the next group's old y values
+            yload(i / ypc);                                       // (the previous group's reads are done)
+            y_mark = ops;
+        }
+        wait_vm_dyn(ops - mark[sl]);
+        if (i == 0) SBL_STAMP(2);
+        if (i + 1 == nck) SBL_STAMP(3);
+        u32x4a wv[9];
+        lds_ld_q4k(st + B * lane, wv);
+        int ia, im;
+        sbl_q4k(wv, X, ia, im);
+        if (i + 2 < nck) {                                        // refill this stage
+            issue(i + 2, st);
+            mark[sl] = ops;
+        }
+        const float f1 = h2f(wv[0].x & 0xFFFFu) * X.dk;
+        const float f2 = -(h2f(wv[0].x >> 16) * X.dk);
+        lds_st128(T + 16 * lane, u32x4a{__float_as_uint(f1), __float_as_uint((float)ia), __float_as_uint(f2),
+                                        __float_as_uint((float)im)});
+        // reference fold: accumulator fk of row r0 + fr over positions fk,
+        // fk + 4, ... (16 rows per pass)
+        if (il == 0) wait_vm_dyn(ops - y_mark);                   // this group's old y values have landed
+        for (uint32_t r0 = 0; r0 < rpc; r0 += 16) {
+            const uint32_t r = r0 + fr;
+            float acc = 0.f;
+            if (r < rpc) {
+                const uint8_t * tr = T + 16 * (r * nsb);
+                for (uint32_t j0 = fk; j0 < nsb; j0 += 16) {
+                    u32x4a t0 = lds_ld128_nw(tr + 16 * j0);
+                    u32x4a t1 = lds_ld128_nw(tr + 16 * (j0 + 4 < nsb ? j0 + 4 : j0));
+                    u32x4a t2 = lds_ld128_nw(tr + 16 * (j0 + 8 < nsb ? j0 + 8 : j0));
+                    u32x4a t3 = lds_ld128_nw(tr + 16 * (j0 + 12 < nsb ? j0 + 12 : j0));
+                    lds_wait4(t0, t1, t2, t3);
+                    const u32x4a tt[4] = {t0, t1, t2, t3};
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        if (j0 + 4 * q < nsb) {
+                            acc = fmaf(__uint_as_float(tt[q].x), __uint_as_float(tt[q].y), acc);
+                            acc = fmaf(__uint_as_float(tt[q].z), __uint_as_float(tt[q].w), acc);
+                        }
+                    }
+                }
+            }
+            const float s01 = acc + qx1f(acc);
+            const float tot = s01 + qx2f(s01);
+            const float yo = __uint_as_float(lds_ld32(Y + 4 * ((il * rpc + r) & 63u)));
+            const uint32_t row0 = (first + stride * i) * rpc + r0, row = row0 + fr;
+            if (r < rpc && fk == 0 && row < rows) gst_x1(a.y + row, __float_as_uint(yo + tot));
+            ops += row0 < rows ? 1u : 0u;                         // lane 0 stores iff row r0 exists
+        }
+    }
+    WAIT_VM(0);
+    SBL_STAMP(4);
+#ifdef FLH_TRACE
+    if (lane == 0 && blockIdx.x < 4096) g_sbl_trace[((size_t)blockIdx.x * 8 + wave) * 8 + 7] = nck;
+#endif
+}
+
+static size_t sbl_smem(uint32_t W, uint32_t slot, uint32_t nsb) {
+    return (size_t)W * 2 * slot + ((nsb * SBL_XS + 1023u) & ~1023u) + (size_t)W * 1280;
+}
+
+int launch_dot_sbl(int fmt, const DotArgs & a, bool fuse, hipStream_t s) {
+    if (fmt != FMT_Q4_K || a.nx != 1 || (a.cols & 255) || a.rows == 0) return FLH_ERR_UNSUPPORTED;
+    const uint32_t nsb = a.cols >> 8;
+    if (nsb < 1 || nsb > 64) return FLH_ERR_UNSUPPORTED;
+    if ((uintptr_t)a.w & 15 || (a.estride & 15)) return FLH_ERR_UNSUPPORTED;
+    if (fuse && ((uintptr_t)a.x & 15)) return FLH_ERR_UNSUPPORTED;
+    const Tune & t = tune();
+    const uint32_t rpc = 64 / nsb;
+    const uint32_t ni = (rpc * nsb * 144 + 1023) / 1024, slot = ni * 1024;
+    // Measured defaults (layer shapes, graph-replayed launches):
+    //  * fused: 8 waves (the quantisation is shared by more waves), 4 of
+    //    them requesting a chunk before the activation is ready; above 2^17
+    //    superblocks the four-lanes-per-superblock kernel is faster (gate/up
+    //    28672x4096: 14.0 vs 14.9 us) and this launcher declines;
+    //  * unfused, <= 16 superblocks per row: 4 waves, 2 early (O 4096x4096
+    //    5.37 -> 4.85 us, QKV 5.95 -> 5.49);
+    //  * unfused, wider rows: 8 waves, 4 early (down 4096x14336 9.78 -> 9.63).
+    if (fuse && !t.sbl_w && (uint64_t)a.rows * nsb > (1u << 17)) return FLH_ERR_UNSUPPORTED;
+    const uint32_t wdef = fuse || nsb > 16 ? 8 : 4;
+    uint32_t W = t.sbl_w ? t.sbl_w : wdef;
+    const uint32_t pre = t.sbl_pre == 0xFFu ? W : t.sbl_pre ? t.sbl_pre : W / 2;
+    while (W > 4 && sbl_smem(W, slot, nsb) > lds_limit()) W -= 2;
+    const size_t smb = sbl_smem(W, slot, nsb);
+    if (smb > lds_limit() || (W != 8 && W != 6 && W != 4)) return FLH_ERR_UNSUPPORTED;
+    if (fuse && (nsb + W - 1) / W > 8) return FLH_ERR_UNSUPPORTED;
+    const uint32_t C = (a.rows + rpc - 1) / rpc;
+    const uint32_t wpc = t.sbl_wpc ? t.sbl_wpc : 1;
+    uint32_t G = (uint32_t)num_cus() * wpc;
+    if (t.sbl_gmax && G > t.sbl_gmax) G = t.sbl_gmax;
+    if (G > C) G = C;
+    auto go = [&](auto kern) {
+        (void)hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smb);
+        hipLaunchKernelGGL(kern, dim3(G), dim3(64 * W), smb, s, a, rpc, ni, slot, pre);
+        return hip_check(hipGetLastError(), "k_dot_sbl launch");
+    };
+    if (W == 8) return fuse ? go(k_dot_sbl<true, 8>) : go(k_dot_sbl<false, 8>);
+    if (W == 6) return fuse ? go(k_dot_sbl<true, 6>) : go(k_dot_sbl<false, 6>);
+    return fuse ? go(k_dot_sbl<true, 4>) : go(k_dot_sbl<false, 4>);
+}
+
+}  // namespace flh

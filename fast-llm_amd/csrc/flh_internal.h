@@ -77,11 +77,21 @@ struct Tune {
     bool mf_xc = true;                  // FLH_MFMA_XC=0: no activations-in-chunk mode
     uint32_t mf_min_cols = 0;           // FLH_MFMA_MIN_COLS (0: 2 above 4096 columns, else 3)
     bool no_mfma = false;               // FLH_NO_MFMA=1: never the matrix-core kernels
+    // superblock-per-lane single-column kernel, FLH_SBL = "on,waves,wgs_per_cu,max_wgs,pre"
+    // (0 = default; max_wgs caps the grid, for tests of long per-wave chunk
+    // lists; pre = waves requesting a chunk before the activation lands, 0: half, 255: all)
+    uint32_t sbl = 1, sbl_w = 0, sbl_wpc = 0, sbl_gmax = 0, sbl_pre = 0;
 };
 const Tune & tune();
 void load_tune();
 
 int launch_dot_kstream(int fmt, const DotArgs & a, hipStream_t s);
+// Q4_K x q8_K, one column, one superblock per lane (flh_dot_sbl.hip); fuse:
+// ACT_Q8 of the fp32 column in the same launch.  FLH_ERR_UNSUPPORTED
+// (nothing launched) if the shape does not fit its plan.
+int launch_dot_sbl(int fmt, const DotArgs & a, bool fuse, hipStream_t s);
+// largest dynamic LDS of one workgroup on the current device
+size_t lds_limit();
 // ACT_Q8 fused into the kstream dot: quantises x (fp32) in-kernel, writes both
 // appendices (workgroup 0), then streams; same bytes and results as
 // launch_act_q8 followed by launch_dot_kstream

@@ -24,7 +24,9 @@ namespace flh {
 // the streaming kernel, s_memrealtime stamps at entry (0), after activation
 // staging (1), at the first landed chunk (2), after the last chunk (3), at
 // exit (4), when the activation loads have landed (5), before the staging
-// barrier (6); slot 7 holds the hardware ids (XCC_ID << 32 | HW_ID).
+// barrier (6), at the second landed chunk (7), after wave 0's last chunk of
+// the last batch (12), after the last fold (8), after the fused quantisation
+// (11); slot 15 holds the hardware ids (XCC_ID << 32 | HW_ID).
 #ifdef FLH_TRACE
 __device__ uint64_t g_ks_trace[8192 * 16];
 #define KS_STAMP(k) do { if (threadIdx.x == 0 && blockIdx.x < 8192) { \
@@ -485,6 +487,7 @@ __device__ __forceinline__ void ks_x_app(const KsCols<NX> & C, uint32_t nx, uint
         uint32_t bs[4], dkb;
         ks_xrec_issue<FMT>(xb, cc, v, bs, dkb);
         ks_wait_behind<NI, D + 1>(after_loads());
+        KS_STAMP(5);
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             xfence(v[k]);

@@ -351,12 +351,13 @@ def test_fused_act_q8_dot_bitwise(flh, orc, gpu, fmt, rows, cols, nx):
 def test_streaming_workgroup_shapes_bitwise(flh, orc, gpu, w8, fmt, rows, cols):
     """Every workgroup shape of the single-column streaming kernel (4 or 8
     waves, one or two per CU; FLH_KS_W8 = "mode bits,workgroups per CU"),
-    fused with ACT_Q8 or not, equals the oracle bit for bit."""
+    fused with ACT_Q8 or not, equals the oracle bit for bit (Q4_K with the
+    superblock-per-lane kernel switched off, so that this kernel runs)."""
     say("kstream shapes", w8, fmt, rows, cols)
     rng = np.random.default_rng(rows + cols + fmt)
     w = sane_rows(fmt, rows, cols, rng)
     xs = activations(1, cols, rng, outliers=True)
-    with tuned(flh, FLH_KS_W8=w8):
+    with tuned(flh, FLH_KS_W8=w8, FLH_SBL="0"):
         got, want = run_dot(flh, orc, gpu, fmt, w, rows, cols, xs, y0=rng.standard_normal(rows).astype(np.float32))
         assert np.array_equal(bits(got), bits(want))
         if fmt != Q8_0:

@@ -1,0 +1,86 @@
+"""GPU parity of the superblock-per-lane single-column Q4_K kernel
+(fast-llm_amd/csrc/flh_dot_sbl.hip), which serves every single-column Q4_K
+STREAM_DOT with at most 64 superblocks per row.
+
+Bar: bitwise against the oracle (fl_dot_i8k_q4_K, src/runtime/quants.h:538-561)
+for every chunk geometry (rows per chunk = 64 // superblocks per row, partial
+last chunks, idle lanes), both workgroup widths, one or two workgroups per CU,
+grids so small that a wave's chunk list outgrows one batch of preloaded old y
+values, any number of waves requesting a chunk before the activation is
+staged, with y += accumulation onto random y, and with ACT_Q8 fused (the
+appendix bytes in memory must equal ACT_Q8's).
+"""
+import numpy as np
+import pytest
+
+from oracle import Q4_K, col_stride_floats, x_alloc_bytes
+from util import tuned, sane_rows, normal_weights, activations
+from test_gpu_parity import bits, say, dev_cols, run_dot
+
+pytestmark = pytest.mark.gpu
+
+# (rows, cols): superblocks per row 1, 2, 3, 5, 11, 16, 56, 64; rows that
+# leave a partial last chunk
+SHAPES = [(7, 256), (33, 512), (41, 768), (29, 1280), (13, 2816), (1001, 4096), (9, 14336),
+          (70, 16384), (4096, 4096)]
+CONFIGS = ["1,8,1,0", "1,4,1,0", "1,6,1,0,255", "1,4,2,0", "1,8,1,3,1", "1,4,1,1,255", "1"]
+
+
+def fused_run(flh, orc, gpu, w, rows, cols, xs, y0):
+    st = col_stride_floats(cols)
+    dx, _ = dev_cols(flh, gpu, xs, st)
+    dy = flh.DeviceBuffer.from_array(y0, gpu)
+    dw = flh.DeviceBuffer.from_array(w, gpu)
+    flh.act_q8_stream_dot(Q4_K, dw, rows, cols, dx, dy, gpu)
+    got = dy.download(np.float32, rows, gpu)
+    xq = dx.download(np.float32, st, gpu)
+    ref_x = orc.act_q8_cols(xs, st)
+    n = x_alloc_bytes(cols) // 4
+    assert np.array_equal(xq[:n].view(np.uint8), ref_x[:n].view(np.uint8)), "appendix bytes"
+    want = y0.copy()
+    orc.stream_dot(Q4_K, w, rows, cols, ref_x, want, threads=8)
+    return got, want
+
+
+@pytest.mark.parametrize("cfg", CONFIGS)
+@pytest.mark.parametrize("rows,cols", SHAPES)
+def test_sbl_bitwise(flh, orc, gpu, cfg, rows, cols):
+    say("sbl", cfg, rows, cols)
+    rng = np.random.default_rng(rows * 3 + cols)
+    w = sane_rows(Q4_K, rows, cols, rng)
+    xs = activations(1, cols, rng, outliers=True)
+    y0 = rng.standard_normal(rows).astype(np.float32)
+    with tuned(flh, FLH_SBL=cfg):
+        got, want = run_dot(flh, orc, gpu, Q4_K, w, rows, cols, xs, y0=y0)
+        assert np.array_equal(bits(got), bits(want))
+        got, want = fused_run(flh, orc, gpu, w, rows, cols, xs, y0)
+        assert np.array_equal(bits(got), bits(want))
+
+
+@pytest.mark.parametrize("rows,cols", [(6144, 4096), (4096, 14336)])
+def test_sbl_layer_shapes_normal_weights(flh, orc, gpu, rows, cols):
+    """Quantized N(0, 0.02^2) weights (the benchmark's recipe) at layer shapes."""
+    say("sbl layer", rows, cols)
+    rng = np.random.default_rng(rows + cols)
+    w = flh.quantize_host(Q4_K, normal_weights(rows, cols, rng))
+    xs = activations(1, cols, rng, outliers=True)
+    y0 = np.zeros(rows, np.float32)
+    got, want = run_dot(flh, orc, gpu, Q4_K, w, rows, cols, xs, y0=y0)
+    assert np.array_equal(bits(got), bits(want))
+    got, want = fused_run(flh, orc, gpu, w, rows, cols, xs, y0)
+    assert np.array_equal(bits(got), bits(want))
+
+
+def test_sbl_matches_streaming_kernel(flh, orc, gpu):
+    """The two single-column kernels give the same bits (FLH_SBL=0 runs the
+    four-lanes-per-superblock streaming kernel)."""
+    rows, cols = 3000, 4096
+    rng = np.random.default_rng(11)
+    w = sane_rows(Q4_K, rows, cols, rng)
+    xs = activations(1, cols, rng)
+    y0 = rng.standard_normal(rows).astype(np.float32)
+    got1, want = run_dot(flh, orc, gpu, Q4_K, w, rows, cols, xs, y0=y0)
+    with tuned(flh, FLH_SBL="0"):
+        got0, _ = run_dot(flh, orc, gpu, Q4_K, w, rows, cols, xs, y0=y0)
+    assert np.array_equal(bits(got1), bits(got0))
+    assert np.array_equal(bits(got1), bits(want))
