@@ -146,7 +146,7 @@ __device__ __forceinline__ void ks_body(const uint8_t * __restrict__ w, uint32_t
     issue_y(0);
 
     // ---- activation records, once per workgroup (overlaps the first weight DMAs)
-    if constexpr (FUSE) ks_x_fuse<FMT, NX, NI, D, KW>(C, nx, nsb, cols, xr, xd, g == 0, prologue);
+    if constexpr (FUSE) ks_x_fuse<FMT, NX, NI, D, KW>(C, nx, nsb, cols, xr, xd, g, G, prologue);
     else ks_x_app<FMT, NX, NI, D>(C, nx, nsb, cols, xr, xd, prologue);
     lds_barrier();
     KS_STAMP(1);

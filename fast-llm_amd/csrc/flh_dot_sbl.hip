@@ -29,8 +29,10 @@
 // matrix with fewer chunks than waves still spreads over every CU.
 // With FUSE, the workgroup quantises the fp32 column itself (ACT_Q8,
 // src/runtime/quants.h:382-402): wave w takes superblocks w, w + W, ...; the
-// staged bytes are the q8_K block's, and workgroup 0 also writes both
-// appendices, so memory ends up as after a separate ACT_Q8 launch.
+// staged bytes are the q8_K block's, and workgroup s % G also writes both
+// appendices of superblock s, so memory ends up as after a separate ACT_Q8
+// launch (with every appendix store in workgroup 0, that workgroup finished
+// ~2 us after the others).
 #include "flh_kstream.h"
 #include "flh_internal.h"
 #include "flh_status.h"
@@ -294,7 +296,7 @@ __global__ __launch_bounds__(64 * W) void k_dot_sbl(DotArgs a, uint32_t rpc, uin
                 lds_st32(xb + 48 + 4 * lane, pk);
                 if ((lane & 3) == 0) lds_st16(xb + 16 + 2 * (lane >> 2), (uint32_t)s16);
                 if (lane == 0) lds_st32(xb + 12, __float_as_uint(d));
-                if (b == 0) act_q8_lanes(v[j], lane, s, q81, q8k, cols);
+                if (s % G == b) act_q8_lanes(v[j], lane, s, q81, q8k, cols);   // each block by one workgroup
             }
         }
     }

@@ -322,13 +322,16 @@ __device__ __forceinline__ void act_q8_lanes(const float (&v)[4], uint32_t lane,
 // for four times the lines and made this prologue ~1 us slower).  The
 // superblock's absmax is a wave max (order free); the lane's four quantised
 // bytes form one dword of a record and a quad sum gives its 16-element block
-// sum.  When write_app, also write both appendices with k_act_q8's lane code,
+// sum.  Workgroup app_g of app_G also writes both appendices of the items i
+// with i % app_G == app_g (every item by exactly one workgroup, so no single
+// workgroup carries all the stores) with k_act_q8's lane code,
 // so the bytes in memory equal ACT_Q8's.  after_loads() runs once, right after
 // the first activation loads are issued (the caller issues its weight
 // prologue there, behind the older activation loads).
 template <int FMT, int NX, int NI, int D, int KW = 4, typename F>
 __device__ __forceinline__ void ks_x_fuse(const KsCols<NX> & C, uint32_t nx, uint32_t nsb, uint32_t cols,
-                                          uint8_t * xr, float * xd, bool write_app, F && after_loads) {
+                                          uint8_t * xr, float * xd, uint32_t app_g, uint32_t app_G,
+                                          F && after_loads) {
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t nitem = nx * nsb;
@@ -340,7 +343,7 @@ __device__ __forceinline__ void ks_x_fuse(const KsCols<NX> & C, uint32_t nx, uin
     // absmaxes (wave max of the non-negative float bits; the lane max starts
     // at 0, so NaN never wins, as the reference's "if (a > amax)"), one
     // division sequence for the four scales (lanes 0..3), records and scales
-    // to LDS, and the appendices when write_app.
+    // to LDS, and this workgroup's share of the appendices.
     auto quant_group = [&](uint32_t base, const float (&v)[4][4]) {
         uint32_t am[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
@@ -362,7 +365,7 @@ __device__ __forceinline__ void ks_x_fuse(const KsCols<NX> & C, uint32_t nx, uin
             lds_st32(rec + 16 * kk + t, pk);
             if ((lane & 3) == 0) lds_st32(rec + 64 + 4 * kk, (uint32_t)(FMT == FMT_Q4_K ? sum : 32 * sum));
             if (lane == 0) lds_st32(&xd[p * nsb + sb], __float_as_uint(d));
-            if (write_app) {
+            if (i % app_G == app_g) {
                 uint8_t * xc = (uint8_t *)col_pick<NX>(C.x, p);
                 act_q8_lanes(v[j], lane, sb, xc + xq_off(cols), xc + xqk_off(cols), cols);
             }
