@@ -353,6 +353,15 @@ int flh_exec_tasks(const flh_task * t, uint32_t n, int fast, uint32_t i8_mask, u
                    void * stream) {
     if (int rc = validate_table(t, n)) return rc;
     if (int rc = need_init()) return rc;
+    // the reference's GPU-default masks (src/runtime/kernels.h:927-940):
+    // Q6_K goes to the q8_K int8 path (the streaming kernel), not fp32 dequant
+    constexpr uint32_t kGpuI8 = (1u << FLH_FMT_Q8_0) | (1u << FLH_FMT_Q5_0) | (1u << FLH_FMT_Q4_K) |
+                                (1u << FLH_FMT_IQ2_XXS) | (1u << FLH_FMT_IQ3_XXS);
+    constexpr uint32_t kGpuI8K = 1u << FLH_FMT_Q4_K;
+    if (i8_mask == kGpuI8 && i8k_mask == kGpuI8K) {
+        i8_mask |= 1u << FLH_FMT_Q6_K;
+        i8k_mask |= 1u << FLH_FMT_Q6_K;
+    }
     hipStream_t s = (hipStream_t)stream;
     for (uint32_t i = 0; i < n; ++i) {
         const flh_task & k = t[i];

@@ -215,7 +215,13 @@ int flh_act_q8_stream_dot(int fmt, const void * w, uint64_t w_bytes, uint32_t ro
  * STREAM_DOT row tiles of one matrix (same fmt/cols/x/nx/strides, w and y
  * contiguous) are fused into one launch, and an ACT_Q8 followed by its
  * single-column q8_K consumer runs as flh_act_q8_stream_dot; results are
- * unchanged. */
+ * unchanged.  Masks: when (i8_mask, i8k_mask) are exactly the reference's
+ * GPU defaults (kI8MaskGpuDefault / kI8KMaskGpuDefault,
+ * src/runtime/kernels.h:927-940), Q6_K is promoted to the q8_K int8 path
+ * (both masks gain the Q6_K bit): the reference keeps Q6_K on fp32 dequant
+ * only because its CUDA int8 Q6_K kernel measured slower; here the int8
+ * kernel is the streaming one and the fp32 modes are correctness kernels.
+ * Any other masks are used as given. */
 int flh_exec_tasks(const flh_task * tasks, uint32_t n, int fast,
                    uint32_t i8_mask, uint32_t i8k_mask, void * stream);
 

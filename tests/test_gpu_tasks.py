@@ -155,3 +155,30 @@ def test_unsupported_kind_launches_nothing(flh, gpu):
     assert e.value.code == flh.ERR_UNSUPPORTED
     gpu.sync()
     assert not np.any(d["y4"].download(np.float32, 600, gpu))
+
+
+def test_gpu_default_masks_take_q6k_int8(flh, orc, gpu):
+    """With the reference's GPU-default masks (kernels.h:927-940: Q6_K on fp32
+    dequant), the table runs Q6_K on the q8_K int8 path: every output equals
+    the CPU-default (i8k) result bit for bit.  Other masks are honoured: the
+    GPU i8 mask with a q8_K mask that also names Q6_K gives the same, and
+    dropping Q6_K from both masks still gives the fp32 dequant bits."""
+    print("[case] task table gpu masks", flush=True)
+    d = build(flh, gpu, np.random.default_rng(10), 1024)
+    want = expected(orc, d)
+    gpu_i8 = (1 << 1) | (1 << 2) | (1 << 3) | (1 << 5) | (1 << 6)
+    gpu_i8k = 1 << 3
+    zero_outputs(d, gpu)
+    flh.exec_tasks(table(flh, d), gpu, i8_mask=gpu_i8, i8k_mask=gpu_i8k)
+    for g, w in zip(read(d, gpu), want):
+        assert np.array_equal(bits(g), bits(w))
+    # a non-default mask without Q6_K anywhere: the Q6_K tiles use fp32 dequant
+    zero_outputs(d, gpu)
+    flh.exec_tasks(table(flh, d), gpu, i8_mask=gpu_i8 & ~(1 << 5), i8k_mask=gpu_i8k)
+    y6 = read(d, gpu)[1]
+    cols = d["cols"]
+    xq = orc.act_q8_cols(d["xs"], d["st"])
+    f6 = np.zeros(40, np.float32)
+    orc.stream_dot(Q6_K, d["w6"], 40, cols, xq[d["st"]:], f6, id_slot=2, estride=40 * row_bytes(Q6_K, cols),
+                   i8_mask=0, i8k_mask=0)
+    assert np.array_equal(bits(y6), bits(f6))
