@@ -167,11 +167,26 @@ bool skip_array(Reader & r) {
 // The tensor payload size for known types (src/model/gguf.cpp:248-256):
 // row bytes of ne[0] times the other dims; 2 bytes an element for F16; 0
 // (metadata only) for anything else.
+// The products are checked (a crafted header could make them wrap and slip
+// past the end-of-file check): kOverflow marks a size that does not fit, a
+// quantized row wider than 2^32 - 1 elements or not a whole number of blocks.
+constexpr uint64_t kOverflow = ~0ull;
 uint64_t payload_bytes(const Tensor & t) {
-    const uint64_t outer = t.ne[1] * t.ne[2] * t.ne[3];
+    uint64_t outer = 1;
+    for (int d = 1; d < 4; ++d)
+        if (__builtin_mul_overflow(outer, t.ne[d], &outer)) return kOverflow;
     const int f = fmt_of_type(t.type);
-    if (f >= 0) return flh_row_bytes(f, (uint32_t)t.ne[0]) * outer;
-    if (t.type == T_F16) return 2 * t.ne[0] * outer;
+    uint64_t n = 0;
+    if (f >= 0) {
+        const uint64_t be = f == FLH_FMT_F32 ? 1 : f == FLH_FMT_Q8_0 || f == FLH_FMT_Q5_0 ? 32 : 256;
+        if (t.ne[0] > 0xFFFFFFFFull || t.ne[0] % be) return kOverflow;
+        if (__builtin_mul_overflow(flh_row_bytes(f, (uint32_t)t.ne[0]), outer, &n)) return kOverflow;
+        return n;
+    }
+    if (t.type == T_F16) {
+        if ((t.ne[0] >> 62) || __builtin_mul_overflow(2 * t.ne[0], outer, &n)) return kOverflow;
+        return n;
+    }
     return 0;
 }
 
@@ -265,6 +280,7 @@ int map_file(flh_gguf * g, const std::string & path, bool keep_kv) {
         t.offset = r.get<uint64_t>();
         if (r.bad) break;
         t.nbytes = payload_bytes(t);
+        if (t.nbytes == kOverflow) return fmt_error(path, ("tensor " + t.name + " has an impossible size").c_str());
         t.shard = idx;
         g->tensors.push_back(std::move(t));
     }
@@ -535,6 +551,9 @@ int flh_gguf_weight(const flh_gguf * g, const char * name, flh_weight * out) {
         return set_error(FLH_ERR_UNSUPPORTED, (std::string("gguf: ") + name + " unsupported type " +
                                                flh_gguf_type_name(t.type)).c_str());
     const Shard & s = g->shards[t.shard];
+    if (t.ne[0] > 0xFFFFFFFFull || t.ne[1] > 0xFFFFFFFFull || (t.n_dims >= 3 && t.ne[2] > 0xFFFFFFFFull) ||
+        (t.n_dims == 4 && t.ne[3] != 1))
+        return set_error(FLH_ERR_UNSUPPORTED, (std::string("gguf: ") + name + " has dimensions a weight cannot take").c_str());
     out->fmt = f;
     out->cols = (uint32_t)t.ne[0];
     out->rows = (uint32_t)t.ne[1];
@@ -542,6 +561,9 @@ int flh_gguf_weight(const flh_gguf * g, const char * name, flh_weight * out) {
     out->row_bytes = flh_row_bytes(f, out->cols);
     out->w_bytes = out->row_bytes * out->rows;
     out->estride = out->nexp > 1 ? out->w_bytes : 0;
+    uint64_t all = 0;                                     // every expert lies inside the payload
+    if (__builtin_mul_overflow(out->w_bytes, (uint64_t)out->nexp, &all) || all > t.nbytes)
+        return set_error(FLH_ERR_UNSUPPORTED, (std::string("gguf: ") + name + " payload smaller than its experts").c_str());
     out->host = s.base + s.data_off + t.offset;
     out->tensor = (uint64_t)i;
     return FLH_OK;

@@ -184,3 +184,20 @@ def test_upload_needs_init(flh):
         t = g.find("t.q8")
         rc = flh.lib().flh_gguf_upload(g.handle, t.index, 4096, t.nbytes, None)
         assert rc == flh.ERR_STATE
+
+
+@pytest.mark.parametrize("dims,why", [((256, 1 << 32, 1 << 32, 1), "dims whose product wraps 64 bits"),
+                                      ((256, 1 << 62, 4), "byte count past 2^64"),
+                                      ((300, 4), "row not a whole number of superblocks"),
+                                      ((256 << 32, 1), "row wider than 2^32 - 1 elements")])
+def test_impossible_sizes_are_rejected(flh, tmp_path, dims, why):
+    """A header whose size arithmetic would wrap (and so slip past the
+    end-of-file check) or whose rows cannot be a Q4_K row is FLH_ERR_FORMAT
+    (the reference reader, src/model/gguf.cpp:248-256, multiplies unchecked)."""
+    g = GgufFile(3)
+    g.add_tensor("w", gw.GGML_Q4_K, dims, np.zeros(144, np.uint8))
+    p = tmp_path / "big.gguf"
+    g.write(str(p))
+    with pytest.raises(flh.FlhError) as e:
+        flh.Gguf(str(p))
+    assert e.value.code == flh.ERR_FORMAT, why
