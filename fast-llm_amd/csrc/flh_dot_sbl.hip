@@ -36,6 +36,7 @@
 #include "flh_kstream.h"
 #include "flh_internal.h"
 #include "flh_status.h"
+#include <type_traits>
 
 namespace flh {
 
@@ -94,6 +95,15 @@ __device__ __forceinline__ u32x4a lds_ld128_nw(const void * p) {
 }
 __device__ __forceinline__ void lds_wait4(u32x4a & a, u32x4a & b, u32x4a & c, u32x4a & d) {
     asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d) :: "memory");
+}
+typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ u32x2v lds_ld64_nw(const void * p) {
+    u32x2v v;
+    asm volatile("ds_read_b64 %0, %1" : "=v"(v) : "v"(lds_off(p)) : "memory");
+    return v;
+}
+__device__ __forceinline__ void lds_wait4x2(u32x2v (&t)[4]) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(t[0]), "+v"(t[1]), "+v"(t[2]), "+v"(t[3]) :: "memory");
 }
 __device__ __forceinline__ void lds_st16(void * p, uint32_t v) {
     asm volatile("ds_write_b16 %0, %1" :: "v"(lds_off(p)), "v"(v));
@@ -166,16 +176,84 @@ __device__ __forceinline__ void sbl_q4k(const u32x4a (&w)[9], const XQ4 & X, int
     im = mi;
 }
 
+// ---- Q8_0: a lane takes half of a 256-weight unit, 4 blocks of 34 bytes
+// (136 bytes, 8-byte aligned); the activation's q8_1 blocks are staged as
+// 48-byte slots (d at +12, the 32 int8 at +16, 16-byte aligned).
+constexpr uint32_t SBL_X8 = 48;
+typedef u32x2v u32x2a;
+
+// the lane's 136 bytes at LDS address p as 34 dwords
+__device__ __forceinline__ void lds_ld_q8h(const void * p, uint32_t (&d)[34]) {
+    u32x2a v[17];
+    asm volatile("ds_read_b64 %0, %17\n\tds_read_b64 %1, %17 offset:8\n\tds_read_b64 %2, %17 offset:16\n\t"
+                 "ds_read_b64 %3, %17 offset:24\n\tds_read_b64 %4, %17 offset:32\n\tds_read_b64 %5, %17 offset:40\n\t"
+                 "ds_read_b64 %6, %17 offset:48\n\tds_read_b64 %7, %17 offset:56\n\tds_read_b64 %8, %17 offset:64\n\t"
+                 "ds_read_b64 %9, %17 offset:72\n\tds_read_b64 %10, %17 offset:80\n\tds_read_b64 %11, %17 offset:88\n\t"
+                 "ds_read_b64 %12, %17 offset:96\n\tds_read_b64 %13, %17 offset:104\n\tds_read_b64 %14, %17 offset:112\n\t"
+                 "ds_read_b64 %15, %17 offset:120\n\tds_read_b64 %16, %17 offset:128\n\ts_waitcnt lgkmcnt(0)"
+                 : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]), "=&v"(v[6]),
+                   "=&v"(v[7]), "=&v"(v[8]), "=&v"(v[9]), "=&v"(v[10]), "=&v"(v[11]), "=&v"(v[12]), "=&v"(v[13]),
+                   "=&v"(v[14]), "=&v"(v[15]), "=&v"(v[16])
+                 : "v"(lds_off(p)) : "memory");
+#pragma unroll
+    for (int i = 0; i < 17; ++i) { d[2 * i] = v[i].x; d[2 * i + 1] = v[i].y; }
+}
+
+// A lane's four q8_1 blocks: 32 dwords of int8 and the four d.
+struct XQ8 {
+    u32x4a q[8];
+    float dx[4];
+};
+
+__device__ __forceinline__ void load_xq8(const uint8_t * xb, XQ8 & X) {
+    asm volatile("ds_read_b128 %0, %8 offset:16\n\tds_read_b128 %1, %8 offset:32\n\tds_read_b128 %2, %8 offset:64\n\t"
+                 "ds_read_b128 %3, %8 offset:80\n\tds_read_b128 %4, %8 offset:112\n\tds_read_b128 %5, %8 offset:128\n\t"
+                 "ds_read_b128 %6, %8 offset:160\n\tds_read_b128 %7, %8 offset:176\n\ts_waitcnt lgkmcnt(0)"
+                 : "=&v"(X.q[0]), "=&v"(X.q[1]), "=&v"(X.q[2]), "=&v"(X.q[3]), "=&v"(X.q[4]), "=&v"(X.q[5]),
+                   "=&v"(X.q[6]), "=&v"(X.q[7])
+                 : "v"(lds_off(xb)) : "memory");
+#pragma unroll
+    for (int m = 0; m < 4; ++m) X.dx[m] = h2f(lds_ld32(xb + SBL_X8 * m + 12) & 0xFFFFu);
+}
+
+// Exact block dots and reference factors (fl_dot_i8_q8_0,
+// src/runtime/quants.h:438-447: fmaf(d_w * d_x, (float)idot, a4[b & 3])) of
+// the lane's four blocks.  Block m starts at byte 34m: its d is the low half
+// of dword 0 (m = 0), the high half of dword 8, the low half of dword 17 or
+// the high half of dword 25; the int8 of blocks 1 and 3 are dword aligned,
+// those of blocks 0 and 2 start two bytes into a dword.
+__device__ __forceinline__ void sbl_q8_0(const uint32_t (&D)[34], const XQ8 & X, float (&f)[4], int (&id)[4]) {
+    const uint32_t dw[4] = {D[0] & 0xFFFFu, D[8] >> 16, D[17] & 0xFFFFu, D[25] >> 16};
+    const int q0[4] = {0, 9, 17, 26};
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        const u32x4a xa = X.q[2 * m], xb = X.q[2 * m + 1];
+        const uint32_t XV[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+        int s0 = 0, s1 = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t q = (m & 1) ? D[q0[m] + i] : alignb(D[q0[m] + i + 1], D[q0[m] + i], 2);
+            if (i & 1) s1 = dot4((int)q, (int)XV[i], s1); else s0 = dot4((int)q, (int)XV[i], s0);
+        }
+        id[m] = s0 + s1;
+        f[m] = h2f(dw[m]) * X.dx[m];
+    }
+}
+
 }  // namespace
 
 // One pass over all rows for one column.  Launch: G workgroups of W waves,
 // dynamic LDS = W * 2 * slot (rings) + the staged activation (rounded to
 // 1 KiB) + W * 1280 bytes (fold terms and old y values).
-template <bool FUSE, int W>
+template <int FMT, bool FUSE, int W>
 __global__ __launch_bounds__(64 * W) void k_dot_sbl(DotArgs a, uint32_t rpc, uint32_t ni, uint32_t slot, uint32_t pre) {
-    constexpr uint32_t B = 144;
+    static_assert(FMT == FMT_Q4_K || (FMT == FMT_Q8_0 && !FUSE), "Q4_K (fused or not) or Q8_0");
+    constexpr bool Q8 = FMT == FMT_Q8_0;
+    constexpr uint32_t B = Q8 ? 136 : 144;                        // bytes of a lane's weights
+    constexpr uint32_t TB = Q8 ? 2048 : 1024;                     // fold-term bytes of a wave
     extern __shared__ __attribute__((aligned(16))) uint8_t sm[];
     const uint32_t nsb = a.cols >> 8, rows = a.rows, cols = a.cols;
+    const uint32_t P = Q8 ? 2 * nsb : nsb;                        // lanes of a row
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t G = gridDim.x, b = blockIdx.x;
@@ -184,11 +262,11 @@ __global__ __launch_bounds__(64 * W) void k_dot_sbl(DotArgs a, uint32_t rpc, uin
     const uint32_t nck = first < C ? (C - first + stride - 1) / stride : 0u;
     uint8_t * ring = sm + (size_t)wave * 2 * slot;
     uint8_t * xs = sm + (size_t)W * 2 * slot;
-    const uint32_t xs_bytes = (nsb * SBL_XS + 1023u) & ~1023u;
-    uint8_t * T = xs + xs_bytes + wave * 1280u;                   // [64][16 B] fold terms of this wave
-    uint8_t * Y = T + 1024;                                       // [64] old y values of this wave
+    const uint32_t xs_bytes = ((Q8 ? nsb * 8 * SBL_X8 : nsb * SBL_XS) + 1023u) & ~1023u;
+    uint8_t * T = xs + xs_bytes + wave * (TB + 256);              // [64][TB / 64] fold terms of this wave
+    uint8_t * Y = T + TB;                                         // [64] old y values of this wave
     const uint8_t * w = a.w + (a.id_slot ? (size_t)(*a.id_slot) * a.estride : 0);
-    const uint64_t cb = (uint64_t)rpc * nsb * B;                  // bytes of a full chunk
+    const uint64_t cb = (uint64_t)rpc * P * B;                    // bytes of a full chunk
     const uint8_t * xk = (const uint8_t *)a.x + xqk_off(cols);
     uint32_t ops = 0;                                             // memory operations issued by this wave
     SBL_STAMP(0);
@@ -218,10 +296,21 @@ __global__ __launch_bounds__(64 * W) void k_dot_sbl(DotArgs a, uint32_t rpc, uin
                                              16, 0, 0);
             ++ops;
         }
-    } else {
-        const uint32_t P = nsb * 19, nxi = (P + 63) / 64;
+    } else if constexpr (Q8) {
+        // q8_1 block j as three 16-byte pieces starting 12 bytes early (the
+        // bytes before block 0 belong to the fp32 column): slot j of 48 bytes
+        const uint8_t * x1 = (const uint8_t *)a.x + xq_off(cols);
+        const uint32_t NP = nsb * 8 * 3, nxi = (NP + 63) / 64;
         for (uint32_t t = wave; t < nxi; t += W) {
-            const uint32_t j = 64 * t + lane, jj = j < P ? j : P - 1;
+            const uint32_t j = 64 * t + lane, jj = j < NP ? j : NP - 1;
+            const uint32_t blk = jj / 3, i = jj - 3 * blk;
+            __builtin_amdgcn_global_load_lds(GPTR(x1 + 36 * blk + 16 * i - 12), LPTR(xs + 1024 * t), 16, 0, 0);
+            ++ops;
+        }
+    } else {
+        const uint32_t NP = nsb * 19, nxi = (NP + 63) / 64;
+        for (uint32_t t = wave; t < nxi; t += W) {
+            const uint32_t j = 64 * t + lane, jj = j < NP ? j : NP - 1;
             const uint32_t s = jj / 19, i = jj - 19 * s;
             __builtin_amdgcn_global_load_lds(GPTR(xk + 292 * s + 16 * i - 12), LPTR(xs + 1024 * t), 16, 0, 0);
             ++ops;
@@ -240,7 +329,7 @@ __global__ __launch_bounds__(64 * W) void k_dot_sbl(DotArgs a, uint32_t rpc, uin
         const uint32_t c = first + stride * i;
         const uint8_t * g = w + (uint64_t)c * cb;
         const uint32_t nrow = min(rpc, rows - c * rpc);
-        const uint32_t vb = nrow * nsb * B;                       // valid bytes (a multiple of 16)
+        const uint32_t vb = nrow * P * B;                         // valid bytes (a multiple of 16)
         for (uint32_t t = 0; t < ni; ++t) {
             const uint32_t o = 1024 * t + 16 * lane;
             __builtin_amdgcn_global_load_lds(GPTR(g + (o < vb ? o : vb - 16)), LPTR(st + 1024 * t), 16, 0, FLH_KS_AUX);
@@ -303,8 +392,9 @@ __global__ __launch_bounds__(64 * W) void k_dot_sbl(DotArgs a, uint32_t rpc, uin
     SBL_STAMP(6);
     lds_barrier();
     SBL_STAMP(1);
-    XQ4 X;
-    load_xq4(xs + SBL_XS * (lane % nsb), X);
+    typename std::conditional<Q8, XQ8, XQ4>::type X;
+    if constexpr (Q8) load_xq8(xs + 4 * SBL_X8 * (lane % P), X);
+    else load_xq4(xs + SBL_XS * (lane % nsb), X);
     // The rest of the prologue comes after the barrier: a request blocks its
     // wave while the CU's memory queue is full, and a wave stuck there would
     // hold the whole workgroup at the barrier.
@@ -324,25 +414,53 @@ __global__ __launch_bounds__(64 * W) void k_dot_sbl(DotArgs a, uint32_t rpc, uin
         wait_vm_dyn(ops - mark[sl]);
         if (i == 0) SBL_STAMP(2);
         if (i + 1 == nck) SBL_STAMP(3);
-        u32x4a wv[9];
-        lds_ld_q4k(st + B * lane, wv);
-        int ia, im;
-        sbl_q4k(wv, X, ia, im);
-        if (i + 2 < nck) {                                        // refill this stage
-            issue(i + 2, st);
-            mark[sl] = ops;
+        if constexpr (Q8) {
+            uint32_t D[34];
+            lds_ld_q8h(st + B * lane, D);
+            float f[4];
+            int id[4];
+            sbl_q8_0(D, X, f, id);
+            if (i + 2 < nck) {                                    // refill this stage
+                issue(i + 2, st);
+                mark[sl] = ops;
+            }
+            lds_st128(T + 32 * lane, u32x4a{__float_as_uint(f[0]), __float_as_uint((float)id[0]),
+                                            __float_as_uint(f[1]), __float_as_uint((float)id[1])});
+            lds_st128(T + 32 * lane + 16, u32x4a{__float_as_uint(f[2]), __float_as_uint((float)id[2]),
+                                                 __float_as_uint(f[3]), __float_as_uint((float)id[3])});
+        } else {
+            u32x4a wv[9];
+            lds_ld_q4k(st + B * lane, wv);
+            int ia, im;
+            sbl_q4k(wv, X, ia, im);
+            if (i + 2 < nck) {                                    // refill this stage
+                issue(i + 2, st);
+                mark[sl] = ops;
+            }
+            const float f1 = h2f(wv[0].x & 0xFFFFu) * X.dk;
+            const float f2 = -(h2f(wv[0].x >> 16) * X.dk);
+            lds_st128(T + 16 * lane, u32x4a{__float_as_uint(f1), __float_as_uint((float)ia), __float_as_uint(f2),
+                                            __float_as_uint((float)im)});
         }
-        const float f1 = h2f(wv[0].x & 0xFFFFu) * X.dk;
-        const float f2 = -(h2f(wv[0].x >> 16) * X.dk);
-        lds_st128(T + 16 * lane, u32x4a{__float_as_uint(f1), __float_as_uint((float)ia), __float_as_uint(f2),
-                                        __float_as_uint((float)im)});
-        // reference fold: accumulator fk of row r0 + fr over positions fk,
-        // fk + 4, ... (16 rows per pass)
+        // reference fold: accumulator fk of row r0 + fr over its terms in
+        // order (Q4_K: positions fk, fk + 4, ...; Q8_0: block fk of every
+        // lane of the row), 16 rows per pass
         if (il == 0) wait_vm_dyn(ops - y_mark);                   // this group's old y values have landed
         for (uint32_t r0 = 0; r0 < rpc; r0 += 16) {
             const uint32_t r = r0 + fr;
             float acc = 0.f;
-            if (r < rpc) {
+            if (Q8 && r < rpc) {
+                const uint8_t * tr = T + 32 * (r * P) + 8 * fk;
+                for (uint32_t j0 = 0; j0 < P; j0 += 4) {
+                    u32x2a t[4];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) t[q] = lds_ld64_nw(tr + 32 * (j0 + q < P ? j0 + q : j0));
+                    lds_wait4x2(t);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        if (j0 + q < P) acc = fmaf(__uint_as_float(t[q].x), __uint_as_float(t[q].y), acc);
+                }
+            } else if (r < rpc) {
                 const uint8_t * tr = T + 16 * (r * nsb);
                 for (uint32_t j0 = fk; j0 < nsb; j0 += 16) {
                     u32x4a t0 = lds_ld128_nw(tr + 16 * j0);
@@ -375,19 +493,22 @@ __global__ __launch_bounds__(64 * W) void k_dot_sbl(DotArgs a, uint32_t rpc, uin
 #endif
 }
 
-static size_t sbl_smem(uint32_t W, uint32_t slot, uint32_t nsb) {
-    return (size_t)W * 2 * slot + ((nsb * SBL_XS + 1023u) & ~1023u) + (size_t)W * 1280;
+static size_t sbl_smem(bool q8, uint32_t W, uint32_t slot, uint32_t nsb) {
+    const size_t xs = ((q8 ? nsb * 8 * SBL_X8 : nsb * SBL_XS) + 1023u) & ~(size_t)1023;
+    return (size_t)W * 2 * slot + xs + (size_t)W * ((q8 ? 2048 : 1024) + 256);
 }
 
 int launch_dot_sbl(int fmt, const DotArgs & a, bool fuse, hipStream_t s) {
-    if (fmt != FMT_Q4_K || a.nx != 1 || (a.cols & 255) || a.rows == 0) return FLH_ERR_UNSUPPORTED;
-    const uint32_t nsb = a.cols >> 8;
-    if (nsb < 1 || nsb > 64) return FLH_ERR_UNSUPPORTED;
+    const bool q8 = fmt == FMT_Q8_0;
+    if ((fmt != FMT_Q4_K && !q8) || (q8 && fuse) || a.nx != 1 || (a.cols & 255) || a.rows == 0)
+        return FLH_ERR_UNSUPPORTED;
+    const uint32_t nsb = a.cols >> 8, P = q8 ? 2 * nsb : nsb, B = q8 ? 136 : 144;
+    if (nsb < 1 || P > 64) return FLH_ERR_UNSUPPORTED;
     if ((uintptr_t)a.w & 15 || (a.estride & 15)) return FLH_ERR_UNSUPPORTED;
-    if (fuse && ((uintptr_t)a.x & 15)) return FLH_ERR_UNSUPPORTED;
+    if ((fuse || q8) && ((uintptr_t)a.x & 15)) return FLH_ERR_UNSUPPORTED;
     const Tune & t = tune();
-    const uint32_t rpc = 64 / nsb;
-    const uint32_t ni = (rpc * nsb * 144 + 1023) / 1024, slot = ni * 1024;
+    const uint32_t rpc = 64 / P;
+    const uint32_t ni = (rpc * P * B + 1023) / 1024, slot = ni * 1024;
     // Measured defaults (layer shapes, graph-replayed launches):
     //  * fused: 8 waves (the quantisation is shared by more waves), 4 of
     //    them requesting a chunk before the activation is ready; above 2^17
@@ -395,13 +516,15 @@ int launch_dot_sbl(int fmt, const DotArgs & a, bool fuse, hipStream_t s) {
     //    28672x4096: 14.0 vs 14.9 us) and this launcher declines;
     //  * unfused, <= 16 superblocks per row: 4 waves, 2 early (O 4096x4096
     //    5.37 -> 4.85 us, QKV 5.95 -> 5.49);
-    //  * unfused, wider rows: 8 waves, 4 early (down 4096x14336 9.78 -> 9.63).
+    //  * unfused, wider rows: 8 waves, 4 early (down 4096x14336 9.78 -> 9.63);
+    //  * Q8_0: 4 waves, all early (4096x4096 7.65 -> 7.25 us; its cost is the
+    //    fold, 32 dependent steps per accumulator and row at 4096 columns).
     if (fuse && !t.sbl_w && (uint64_t)a.rows * nsb > (1u << 17)) return FLH_ERR_UNSUPPORTED;
     const uint32_t wdef = fuse || nsb > 16 ? 8 : 4;
     uint32_t W = t.sbl_w ? t.sbl_w : wdef;
-    const uint32_t pre = t.sbl_pre == 0xFFu ? W : t.sbl_pre ? t.sbl_pre : W / 2;
-    while (W > 4 && sbl_smem(W, slot, nsb) > lds_limit()) W -= 2;
-    const size_t smb = sbl_smem(W, slot, nsb);
+    const uint32_t pre = t.sbl_pre == 0xFFu ? W : t.sbl_pre ? t.sbl_pre : q8 ? W : W / 2;
+    while (W > 4 && sbl_smem(q8, W, slot, nsb) > lds_limit()) W -= 2;
+    const size_t smb = sbl_smem(q8, W, slot, nsb);
     if (smb > lds_limit() || (W != 8 && W != 6 && W != 4)) return FLH_ERR_UNSUPPORTED;
     if (fuse && (nsb + W - 1) / W > 8) return FLH_ERR_UNSUPPORTED;
     const uint32_t C = (a.rows + rpc - 1) / rpc;
@@ -414,9 +537,14 @@ int launch_dot_sbl(int fmt, const DotArgs & a, bool fuse, hipStream_t s) {
         hipLaunchKernelGGL(kern, dim3(G), dim3(64 * W), smb, s, a, rpc, ni, slot, pre);
         return hip_check(hipGetLastError(), "k_dot_sbl launch");
     };
-    if (W == 8) return fuse ? go(k_dot_sbl<true, 8>) : go(k_dot_sbl<false, 8>);
-    if (W == 6) return fuse ? go(k_dot_sbl<true, 6>) : go(k_dot_sbl<false, 6>);
-    return fuse ? go(k_dot_sbl<true, 4>) : go(k_dot_sbl<false, 4>);
+    if (q8) {
+        if (W == 8) return go(k_dot_sbl<FMT_Q8_0, false, 8>);
+        if (W == 6) return go(k_dot_sbl<FMT_Q8_0, false, 6>);
+        return go(k_dot_sbl<FMT_Q8_0, false, 4>);
+    }
+    if (W == 8) return fuse ? go(k_dot_sbl<FMT_Q4_K, true, 8>) : go(k_dot_sbl<FMT_Q4_K, false, 8>);
+    if (W == 6) return fuse ? go(k_dot_sbl<FMT_Q4_K, true, 6>) : go(k_dot_sbl<FMT_Q4_K, false, 6>);
+    return fuse ? go(k_dot_sbl<FMT_Q4_K, true, 4>) : go(k_dot_sbl<FMT_Q4_K, false, 4>);
 }
 
 }  // namespace flh

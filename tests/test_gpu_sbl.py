@@ -84,3 +84,23 @@ def test_sbl_matches_streaming_kernel(flh, orc, gpu):
         got0, _ = run_dot(flh, orc, gpu, Q4_K, w, rows, cols, xs, y0=y0)
     assert np.array_equal(bits(got1), bits(got0))
     assert np.array_equal(bits(got1), bits(want))
+
+
+Q8_0 = 1
+
+
+@pytest.mark.parametrize("cfg", ["1", "1,8,1,0", "1,4,2,0,255", "1,6,1,3,1"])
+@pytest.mark.parametrize("rows,cols", [(7, 256), (33, 512), (41, 768), (13, 2816), (1001, 4096), (70, 8192),
+                                       (4096, 4096)])
+def test_sbl_q8_0_bitwise(flh, orc, gpu, cfg, rows, cols):
+    """Q8_0 x q8_1 with half a 256-weight unit per lane: bitwise
+    fl_dot_i8_q8_0 (src/runtime/quants.h:438-447) for every unit count per
+    row up to 32 (8192 columns)."""
+    say("sbl q8_0", cfg, rows, cols)
+    rng = np.random.default_rng(rows * 5 + cols)
+    w = sane_rows(Q8_0, rows, cols, rng)
+    xs = activations(1, cols, rng, outliers=True)
+    y0 = rng.standard_normal(rows).astype(np.float32)
+    with tuned(flh, FLH_SBL=cfg):
+        got, want = run_dot(flh, orc, gpu, Q8_0, w, rows, cols, xs, y0=y0)
+        assert np.array_equal(bits(got), bits(want))
