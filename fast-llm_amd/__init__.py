@@ -96,6 +96,12 @@ class Task(C.Structure):
     ]
 
 
+class RmsNormP(C.Structure):
+    """RmsNormP (src/runtime/decode_params.h:23-29)."""
+    _fields_ = [("wnorm", C.c_void_p), ("x", C.c_void_p), ("y", C.c_void_p), ("eps", C.c_float),
+                ("n", C.c_uint32)]
+
+
 class RouterP(C.Structure):
     """RouterP (src/runtime/decode_params.h:68-75)."""
     _fields_ = [("logits", C.c_void_p), ("ids", C.c_void_p), ("gates", C.c_void_p),
@@ -182,6 +188,7 @@ _SIGS = {
                                 _U32, _U32, _P, _U32, _P]),
     "flh_silu_mul": (_I, [_P, _P, _P, _U32, _U32, _U32, _U32, _P]),
     "flh_silu_mul_act_q8": (_I, [_P, _P, _P, _U32, _U32, _U32, _U32, _P]),
+    "flh_rmsnorm_act_q8": (_I, [_P, _P, _P, _U32, C.c_float, _I, _P]),
     "flh_wmerge": (_I, [_P, _P, _P, _P, _P, _F, _U32, _U32, _U32, _U32, _U32, _U32, _P]),
     "flh_fill_normal": (_I, [_P, _SZ, _U64, _F, _F, _F, _F, _P]),
     "flh_quantize": (_I, [_I, _P, _U32, _U32, _P, _P]),
@@ -436,6 +443,12 @@ def silu_mul(gate, up, h, n, ncol, gstride, hstride, stream: Stream):
 def silu_mul_act_q8(gate, up, h, n, ncol, gstride, hstride, stream: Stream):
     """SILU_MUL then ACT_Q8 of every h column (one launch, same bytes)."""
     check(lib().flh_silu_mul_act_q8(_p(gate), _p(up), _p(h), n, ncol, gstride, hstride, stream.handle))
+
+
+def rmsnorm_act_q8(x, wnorm, y, n, eps, stream: Stream, write_app: bool = True):
+    """RMSNORM of one column (y = x * s * wnorm) and, with write_app, the
+    ACT_Q8 appendices of y, in one launch."""
+    check(lib().flh_rmsnorm_act_q8(_p(x), _p(wnorm), _p(y), n, eps, int(bool(write_app)), stream.handle))
 
 
 def wmerge(parts, gates, add1, add2, y, scale, n_parts, n, n_full, ncol, pstride, ystride,

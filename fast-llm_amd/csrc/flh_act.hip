@@ -53,6 +53,56 @@ __global__ __launch_bounds__(64) void k_silu_act_q8(const float * gate, const fl
     act_q8_lanes(v, lane, chunk, (uint8_t *)hc + xq_off(n), (uint8_t *)hc + xqk_off(n), n);
 }
 
+// RMSNORM of one column with (write_app) the ACT_Q8 of its output, one
+// workgroup of 16 waves: the sum of squares as thread partials (elements
+// 4t..4t+3, 4t+4096.. in order) -> wave DPP tree -> the 16 wave sums in
+// wave order; s = 1 / sqrtf(ss / n + eps) (correctly rounded sqrt and
+// division, as the reference's libm); then wave w quantises chunks w, w + 16,
+// ... with y = (x * s) * wnorm computed in the registers it quantises, so
+// the appendices hold ACT_Q8's bytes for the stored y.
+__global__ __launch_bounds__(1024) void k_rmsnorm_act_q8(const float * x, const float * wn, float * y, uint32_t n,
+                                                         float eps, int write_app) {
+    __shared__ float part[16];
+    __shared__ float sh_s;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    float ss = 0.f;
+    for (uint32_t e0 = 4 * tid; e0 < n; e0 += 4096)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (e0 + j < n) ss += x[e0 + j] * x[e0 + j];
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) ss += __shfl_xor(ss, o);
+    if (lane == 0) part[wave] = ss;
+    __syncthreads();
+    if (tid == 0) {
+        float t = 0.f;
+        for (int w = 0; w < 16; ++w) t += part[w];
+        sh_s = 1.0f / sqrtf(t / (float)n + eps);
+    }
+    __syncthreads();
+    const float s = sh_s;
+    uint8_t * q81 = (uint8_t *)y + xq_off(n);
+    uint8_t * q8k = (uint8_t *)y + xqk_off(n);
+    for (uint32_t c = wave; c * 256 < n; c += 16) {
+        const uint32_t e0 = c * 256 + 4 * lane;
+        float v[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            v[j] = 0.f;
+            if (e0 + j < n) {
+                v[j] = x[e0 + j] * s * wn[e0 + j];
+                y[e0 + j] = v[j];
+            }
+        }
+        if (write_app) act_q8_lanes(v, lane, c, q81, q8k, n);
+    }
+}
+int launch_rmsnorm_act_q8(const float * x, const float * wnorm, float * y, uint32_t n, float eps, bool app,
+                          hipStream_t s) {
+    if (n == 0) return FLH_OK;
+    hipLaunchKernelGGL(k_rmsnorm_act_q8, dim3(1), dim3(1024), 0, s, x, wnorm, y, n, eps, app ? 1 : 0);
+    return hip_check(hipGetLastError(), "k_rmsnorm_act_q8 launch");
+}
 int launch_silu_act_q8(const float * gate, const float * up, float * h, uint32_t n, uint32_t ncol,
                        uint32_t gstride, uint32_t hstride, hipStream_t s) {
     if (n == 0 || ncol == 0) return FLH_OK;

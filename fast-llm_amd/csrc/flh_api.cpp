@@ -146,7 +146,7 @@ static int validate_table(const flh_task * t, uint32_t n) {
                 if (!k.x || ((uintptr_t)k.x & 15)) return set_error(FLH_ERR_ARG, "ACT_Q8: x must be 16-byte aligned");
                 break;
             case FLH_TASK_MERGE: case FLH_TASK_SIGNAL: break;
-            case FLH_TASK_ROUTER_SEL: case FLH_TASK_SILU_MUL: case FLH_TASK_WMERGE:
+            case FLH_TASK_ROUTER_SEL: case FLH_TASK_SILU_MUL: case FLH_TASK_WMERGE: case FLH_TASK_RMSNORM:
                 if (!k.aux) return set_error(FLH_ERR_ARG, "decode op without aux param block");
                 break;
             default:
@@ -411,6 +411,18 @@ int flh_exec_tasks(const flh_task * t, uint32_t n, int fast, uint32_t i8_mask, u
                 rc = launch_merge((const float *)k.x, (float *)k.y, k.rows, k.cols, s);
                 break;
             case FLH_TASK_SIGNAL: break;
+            case FLH_TASK_RMSNORM: {
+                const flh_rmsnorm_p & p = *(const flh_rmsnorm_p *)k.aux;
+                // RMSNORM followed by the ACT_Q8 of its output (the decoder's
+                // norm -> quant chain): one launch
+                const flh_task * q = i + 1 < n ? &t[i + 1] : nullptr;
+                const bool fuse = q && q->kind == FLH_TASK_ACT_Q8 && q->x == (const void *)p.y && q->cols == p.n &&
+                                  (const uint8_t *)q->y == (const uint8_t *)p.y + xq_off(p.n) &&
+                                  !((uintptr_t)p.y & 15);
+                rc = launch_rmsnorm_act_q8(p.x, p.wnorm, p.y, p.n, p.eps, fuse, s);
+                if (fuse) ++i;
+                break;
+            }
             case FLH_TASK_ROUTER_SEL: {
                 const flh_router_p & p = *(const flh_router_p *)k.aux;
                 rc = launch_router_sel(p.logits, 1, p.n_expert, p.top_k, p.norm, p.scale, p.ids, p.gates, s);
@@ -500,6 +512,14 @@ int flh_silu_mul(const float * gate, const float * up, float * h, uint32_t n, ui
     if (int rc = need_init()) return rc;
     return launch_silu_mul(gate, up, h, n, ncol, gstride, hstride, (hipStream_t)stream);
 }
+int flh_rmsnorm_act_q8(const float * x, const float * wnorm, float * y, uint32_t n, float eps, int write_app,
+                       void * stream) {
+    if (int rc = need_init()) return rc;
+    if (!x || !wnorm || !y || ((uintptr_t)x & 3) || ((uintptr_t)wnorm & 3) || ((uintptr_t)y & (write_app ? 15 : 3)))
+        return set_error(FLH_ERR_ARG, "rmsnorm: x, wnorm, y non-null and aligned (y 16 bytes with ACT_Q8)");
+    return launch_rmsnorm_act_q8(x, wnorm, y, n, eps, write_app != 0, (hipStream_t)stream);
+}
+
 int flh_silu_mul_act_q8(const float * gate, const float * up, float * h, uint32_t n, uint32_t ncol,
                         uint32_t gstride, uint32_t hstride, void * stream) {
     if (int rc = need_init()) return rc;

@@ -52,6 +52,9 @@ inline uint32_t moe_rows(const MoeArgs & a) {
 // Each returns hipSuccess-style 0 or a negative flh error code.
 int launch_act_q8(float * x, void * y_q81, uint32_t cols, uint32_t nx,
                   uint32_t xstride, hipStream_t s);
+// RMSNORM of one column, with the ACT_Q8 of its output when app
+int launch_rmsnorm_act_q8(const float * x, const float * wnorm, float * y, uint32_t n, float eps, bool app,
+                          hipStream_t s);
 // SILU_MUL over ncol columns followed by ACT_Q8 of h, in one launch
 int launch_silu_act_q8(const float * gate, const float * up, float * h, uint32_t n, uint32_t ncol,
                        uint32_t gstride, uint32_t hstride, hipStream_t s);

@@ -87,8 +87,11 @@ typedef struct __attribute__((aligned(128))) flh_task {
     uint32_t nx, xstride, ystride;
 } flh_task;
 
-/* Decode-op param blocks, layouts of RouterP / SiluMulP / WmergeP
- * (src/runtime/decode_params.h:68-97). */
+/* Decode-op param blocks, layouts of RmsNormP / RouterP / SiluMulP / WmergeP
+ * (src/runtime/decode_params.h:23-29, 68-97). */
+typedef struct flh_rmsnorm_p {
+    const float * wnorm; const float * x; float * y; float eps; uint32_t n;
+} flh_rmsnorm_p;
 typedef struct flh_router_p {
     const float * logits; uint32_t * ids; float * gates;
     uint32_t n_expert, top_k, norm; float scale;
@@ -210,7 +213,9 @@ int flh_act_q8_stream_dot(int fmt, const void * w, uint64_t w_bytes, uint32_t ro
  * executor's per-task dispatch, exec_task_block, src/runtime/gpu_exec.cu:
  * 64-140, for a topologically ordered table such as run_serial walks,
  * src/runtime/graph.cpp:116-148).  Supported kinds: STREAM_DOT,
- * STREAM_DOT_IDX, ACT_Q8, MERGE, SIGNAL, ROUTER_SEL, SILU_MUL, WMERGE;
+ * STREAM_DOT_IDX, ACT_Q8, MERGE, SIGNAL, RMSNORM, ROUTER_SEL, SILU_MUL,
+ * WMERGE (an RMSNORM followed by the ACT_Q8 of its output is one
+ * flh_rmsnorm_act_q8 launch);
  * anything else -> FLH_ERR_UNSUPPORTED before any launch.  Consecutive
  * STREAM_DOT row tiles of one matrix (same fmt/cols/x/nx/strides, w and y
  * contiguous) are fused into one launch, and an ACT_Q8 followed by its
@@ -274,6 +279,18 @@ int flh_silu_mul(const float * gate, const float * up, float * h, uint32_t n,
  * input, decoder.cpp:874-880).  flh_exec_tasks fuses such a task pair itself. */
 int flh_silu_mul_act_q8(const float * gate, const float * up, float * h, uint32_t n,
                         uint32_t ncol, uint32_t gstride, uint32_t hstride, void * stream);
+/* RMSNORM of one column (fl_op_rmsnorm, decode_params.h:101-106:
+ * y = (x * s) * wnorm, s = 1 / sqrtf(mean(x^2) + eps)) with, when write_app,
+ * the ACT_Q8 of y in the same launch (y is then an ACT_Q8 buffer, 16-byte
+ * aligned, and its appendices get the bytes flh_act_q8 would write from
+ * these y values: the decoder's norm -> quant chain, decoder.cpp:874-880).
+ * The reference (CPU-only op) sums the squares strictly in order; here the
+ * 16 waves of one workgroup sum them as a tree (lane partials over its
+ * elements in order, wave and workgroup trees in a fixed order), so s
+ * and y agree with the reference to float rounding, not bit for bit (the
+ * tests bound it); everything after s is the reference's arithmetic. */
+int flh_rmsnorm_act_q8(const float * x, const float * wnorm, float * y, uint32_t n, float eps,
+                       int write_app, void * stream);
 /* WMERGE over ncol columns (fl_op_wmerge, decode_params.h:274-295): column c
  * reads parts + c*pstride ([n_parts][n]), gates + c*n_parts, add1/add2 +
  * c*ystride, writes y + c*ystride. */

@@ -649,6 +649,17 @@ void orc_router_sel(const float * logits, uint32_t n_expert, uint32_t top_k,
         gates[k] *= scale;
     }
 }
+// RMSNORM (src/runtime/decode_params.h:101-106): the sum of squares in
+// ascending order, one product and one add per element, each rounded (the
+// reference builds with -ffp-contract=off); s = 1 / sqrtf(mean + eps) with a
+// correctly rounded sqrtf and division; y = (x * s) * w.
+void orc_rmsnorm(const float * wnorm, const float * x, float * y, float eps, uint32_t n) {
+    float ss = 0.f;
+    for (uint32_t i = 0; i < n; ++i) ss += x[i] * x[i];
+    const float s = 1.0f / sqrtf(ss / (float)n + eps);
+    for (uint32_t i = 0; i < n; ++i) y[i] = x[i] * s * wnorm[i];
+}
+
 void orc_silu_mul(const float * gate, const float * up, float * h, uint32_t n) {
     for (uint32_t i = 0; i < n; ++i) { const float g = gate[i]; h[i] = (g / (1.0f + expf(-g))) * up[i]; }
 }

@@ -94,6 +94,7 @@ void orc_stream_dot_mt(int fmt, const uint8_t * w, uint32_t rows, uint32_t cols,
 void orc_router_sel(const float * logits, uint32_t n_expert, uint32_t top_k,
                     uint32_t norm, float scale, uint32_t * ids, float * gates);
 void orc_silu_mul(const float * gate, const float * up, float * h, uint32_t n);
+void orc_rmsnorm(const float * wnorm, const float * x, float * y, float eps, uint32_t n);
 void orc_wmerge(const float * parts, const float * gates, const float * add1,
                 const float * add2, float * y, float scale, uint32_t n_parts,
                 uint32_t n, uint32_t n_full);

@@ -100,6 +100,9 @@ class Oracle:
                 f = getattr(L, n)
                 f.restype, f.argtypes = res, args
                 setattr(self, n[4:], f)
+        self._rmsnorm = getattr(L, pre + "rmsnorm")
+        self._rmsnorm.restype = None
+        self._rmsnorm.argtypes = [_P, _P, _P, _F, _U32]
         for n in ("router_sel", "silu_mul", "wmerge"):
             setattr(self, "_" + n, getattr(L, pre + n))
         self._router_sel.restype = None
@@ -183,6 +186,13 @@ class Oracle:
         gates = np.zeros(top_k, dtype=np.float32)
         self._router_sel(_ptr(logits), logits.size, top_k, norm, scale, _ptr(ids), _ptr(gates))
         return ids, gates
+
+    def rmsnorm(self, x, wnorm, eps):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        wnorm = np.ascontiguousarray(wnorm, dtype=np.float32)
+        y = np.empty_like(x)
+        self._rmsnorm(_ptr(wnorm), _ptr(x), _ptr(y), eps, x.size)
+        return y
 
     def silu_mul(self, gate, up):
         gate = np.ascontiguousarray(gate, dtype=np.float32)

@@ -109,6 +109,10 @@ void ref_router_sel(const float * logits, uint32_t n_expert, uint32_t top_k,
     RouterP p{logits, ids, gates, n_expert, top_k, norm, scale};
     fl_op_router_sel(p);
 }
+void ref_rmsnorm(const float * wnorm, const float * x, float * y, float eps, uint32_t n) {
+    RmsNormP p{wnorm, x, y, eps, n};
+    fl_op_rmsnorm(p);
+}
 void ref_silu_mul(const float * gate, const float * up, float * h, uint32_t n) {
     SiluMulP p{gate, up, h, n};
     fl_op_silu_mul(p);

@@ -1,0 +1,83 @@
+"""RMSNORM -> ACT_Q8 on the device (flh_rmsnorm_act_q8, and RMSNORM + ACT_Q8
+task pairs in flh_exec_tasks) against the oracle's fl_op_rmsnorm
+(src/runtime/decode_params.h:101-106; oracle pinned to the reference in
+tests/test_oracle_math.py).
+
+Bar: the reference sums the squares strictly in order on the CPU; the kernel
+sums them as a tree, so y may differ from the reference by the rounding of
+that sum: |y - y_ref| <= n * 2^-24 * |y_ref| + 2 ulp (the worst-case relative
+error of an n-term sequential float sum, which bounds both orders).  Every
+step after the sum is the reference's arithmetic, and the fused quantisation
+is exact: the appendices equal ACT_Q8 of the y the kernel stored, byte for
+byte; a STREAM_DOT of them equals the oracle's bit for bit."""
+import ctypes
+
+import numpy as np
+import pytest
+
+from oracle import Q4_K, col_stride_floats, x_alloc_bytes
+from util import sane_rows
+
+pytestmark = pytest.mark.gpu
+
+
+def bits(a):
+    return np.ascontiguousarray(a).view(np.uint32)
+
+
+def check_y(y, want, n):
+    ulp = np.spacing(np.abs(want).astype(np.float32))
+    assert np.all(np.abs(y - want) <= n * 2.0 ** -24 * np.abs(want) + 2 * ulp)
+
+
+@pytest.mark.parametrize("n", [256, 768, 4096, 5120, 14336])
+def test_rmsnorm_act_q8(flh, orc, gpu, n):
+    print("[case] rmsnorm", n, flush=True)
+    rng = np.random.default_rng(n)
+    x = (rng.standard_normal(n) * 3).astype(np.float32)
+    wn = (1 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+    st = col_stride_floats(n)
+    dx = flh.DeviceBuffer.from_array(x, gpu)
+    dw = flh.DeviceBuffer.from_array(wn, gpu)
+    dy = flh.DeviceBuffer.from_array(np.zeros(st, np.float32), gpu)
+    flh.rmsnorm_act_q8(dx, dw, dy, n, 1e-5, gpu)
+    yb = dy.download(np.float32, st, gpu)
+    y = yb[:n].copy()
+    check_y(y, orc.rmsnorm(x, wn, 1e-5), n)
+    nb = x_alloc_bytes(n)
+    assert np.array_equal(yb.view(np.uint8)[:nb], orc.act_q8(y)[:nb]), "appendices == ACT_Q8(y)"
+
+
+def test_rmsnorm_task_pair_fuses(flh, orc, gpu):
+    """RMSNORM, ACT_Q8 of its output, a Q4_K STREAM_DOT of it: the table gives
+    the bits of flh_rmsnorm_act_q8 followed by flh_stream_dot, and the dot
+    equals the oracle's on the quantised y."""
+    n, rows = 4096, 300
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal(n).astype(np.float32)
+    wn = (1 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+    w = sane_rows(Q4_K, rows, n, rng)
+    st = col_stride_floats(n)
+    dx = flh.DeviceBuffer.from_array(x, gpu)
+    dwn = flh.DeviceBuffer.from_array(wn, gpu)
+    dy = flh.DeviceBuffer.from_array(np.zeros(st, np.float32), gpu)
+    dw = flh.DeviceBuffer.from_array(w, gpu)
+    out = flh.DeviceBuffer.from_array(np.zeros(rows, np.float32), gpu)
+    p = flh.RmsNormP(dwn.ptr, dx.ptr, dy.ptr, 1e-5, n)
+    T = flh.TaskKind
+    t0 = flh.Task(); t0.kind = int(T.RMSNORM); t0.aux = ctypes.addressof(p)
+    t1 = flh.Task(); t1.kind = int(T.ACT_Q8); t1.x = dy.ptr; t1.y = dy.ptr + flh.xq_offset(n); t1.rows = n // 32
+    t1.cols = n
+    t2 = flh.Task(); t2.kind = int(T.STREAM_DOT); t2.fmt = Q4_K; t2.w = dw.ptr; t2.w_bytes = w.size; t2.x = dy.ptr
+    t2.y = out.ptr; t2.rows = rows; t2.cols = n
+    flh.exec_tasks([t0, t1, t2], gpu)
+    yb = dy.download(np.float32, st, gpu)
+    got = out.download(np.float32, rows, gpu)
+    check_y(yb[:n], orc.rmsnorm(x, wn, 1e-5), n)
+    want = np.zeros(rows, np.float32)
+    orc.stream_dot(Q4_K, w, rows, n, yb, want)
+    assert np.array_equal(bits(got), bits(want))
+    # the same through the direct entry points
+    dy2 = flh.DeviceBuffer.from_array(np.zeros(st, np.float32), gpu)
+    flh.rmsnorm_act_q8(dx, dwn, dy2, n, 1e-5, gpu)
+    assert np.array_equal(bits(dy2.download(np.float32, st, gpu)), bits(yb))

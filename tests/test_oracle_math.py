@@ -482,3 +482,20 @@ def test_device_round_half_away_identity():
     y64 = y.astype(np.float64)
     want = np.clip(np.sign(y64) * np.floor(np.abs(y64) + 0.5), -127, 127).astype(np.int64)
     assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("n", [256, 4096, 14336])
+def test_rmsnorm_oracle_pinned(n):
+    """orc_rmsnorm restates fl_op_rmsnorm (decode_params.h:101-106): the
+    squares summed in order with one rounding each (numpy's float32 cumsum is
+    that sequential sum), s = 1 / sqrt(mean + eps) correctly rounded, y =
+    (x * s) * w -- bit for bit."""
+    from oracle import Oracle
+    o = Oracle()
+    rng = np.random.default_rng(n + 1)
+    x = (rng.standard_normal(n) * 3).astype(np.float32)
+    w = rng.standard_normal(n).astype(np.float32)
+    ss = np.cumsum((x * x).astype(np.float32), dtype=np.float32)[-1]
+    s = np.float32(1.0) / np.sqrt(np.float32(ss / np.float32(n) + np.float32(1e-5)), dtype=np.float32)
+    want = ((x * s).astype(np.float32) * w).astype(np.float32)
+    assert np.array_equal(o.rmsnorm(x, w, 1e-5).view(np.uint32), want.view(np.uint32))
