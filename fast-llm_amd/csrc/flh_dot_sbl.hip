@@ -403,6 +403,8 @@ __global__ __launch_bounds__(64 * W) void k_dot_sbl(DotArgs a, uint32_t rpc, uin
     if (nck > 1) { issue(1, ring + slot); mark[1] = ops; }
 
     const uint32_t fr = lane >> 2, fk = lane & 3;                 // fold lane: row r0 + fr, accumulator fk
+    // Q4_K rows of 4, 8 or 16 superblocks fold in registers (DPP)
+    const bool dppf = !Q8 && (nsb == 4 || nsb == 8 || nsb == 16);
     for (uint32_t i = 0; i < nck; ++i) {
         const uint32_t sl = i & 1u;
         uint8_t * st = ring + sl * slot;
@@ -439,6 +441,28 @@ __global__ __launch_bounds__(64 * W) void k_dot_sbl(DotArgs a, uint32_t rpc, uin
             }
             const float f1 = h2f(wv[0].x & 0xFFFFu) * X.dk;
             const float f2 = -(h2f(wv[0].x >> 16) * X.dk);
+            if (dppf) {
+                // Rows of 4, 8 or 16 lanes sit inside one 16-lane DPP row:
+                // accumulator k runs down positions k, k + 4, ... by shifting
+                // the partial chain four lanes per step; after nsb / 4 steps
+                // the row's last four lanes hold a0..a3.
+                const float fi = (float)ia, fm = (float)im;
+                float acc = fmaf(f2, fm, fmaf(f1, fi, 0.f));
+                for (uint32_t q = 4; q < nsb; q += 4) {
+                    const float prev = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(acc), 0x114,
+                                                                                  0xF, 0xF, false));
+                    acc = fmaf(f2, fm, fmaf(f1, fi, prev));
+                }
+                const float s01 = acc + qx1f(acc);
+                const float tot = s01 + qx2f(s01);
+                if (il == 0) wait_vm_dyn(ops - y_mark);           // this group's old y values have landed
+                const uint32_t r = lane / nsb;
+                const float yo = __uint_as_float(lds_ld32(Y + 4 * ((il * rpc + r) & 63u)));
+                const uint32_t row0 = (first + stride * i) * rpc, row = row0 + r;
+                if (lane - r * nsb == nsb - 4 && row < rows) gst_x1(a.y + row, __float_as_uint(yo + tot));
+                ++ops;                                            // lane nsb - 4 (row 0 of the chunk) stores
+                continue;
+            }
             lds_st128(T + 16 * lane, u32x4a{__float_as_uint(f1), __float_as_uint((float)ia), __float_as_uint(f2),
                                             __float_as_uint((float)im)});
         }

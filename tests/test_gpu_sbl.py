@@ -21,7 +21,7 @@ pytestmark = pytest.mark.gpu
 
 # (rows, cols): superblocks per row 1, 2, 3, 5, 11, 16, 56, 64; rows that
 # leave a partial last chunk
-SHAPES = [(7, 256), (33, 512), (41, 768), (29, 1280), (13, 2816), (1001, 4096), (9, 14336),
+SHAPES = [(7, 256), (33, 512), (41, 768), (37, 1024), (29, 1280), (19, 2048), (13, 2816), (1001, 4096), (9, 14336),
           (70, 16384), (4096, 4096)]
 CONFIGS = ["1,8,1,0", "1,4,1,0", "1,6,1,0,255", "1,4,2,0", "1,8,1,3,1", "1,4,1,1,255", "1"]
 
