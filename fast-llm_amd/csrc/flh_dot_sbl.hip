@@ -114,6 +114,18 @@ __device__ __forceinline__ void gst_x1(float * p, uint32_t v) {
     asm volatile("global_store_dword %0, %1, off" :: "v"(p), "v"(v) : "memory");
 }
 
+__device__ __forceinline__ u32x4a lds_ld128(const void * p) {
+    u32x4a v;
+    asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(lds_off(p)) : "memory");
+    return v;
+}
+// ACT_Q8's appendix bytes of one 256-element chunk (k_act_q8's lane code),
+// (inlined once: the item loop stays rolled); one workgroup in G takes each chunk
+__device__ __forceinline__ void write_appendices(const float (&v)[4], uint32_t lane, uint32_t chunk,
+                                                           uint8_t * q81, uint8_t * q8k, uint32_t cols) {
+    act_q8_lanes(v, lane, chunk, q81, q8k, cols);
+}
+
 // A lane's activation superblock: 64 dwords of int8, the 8 sub-block sums
 // (bsums[2t] + bsums[2t+1]), and d.
 struct XQ4 {
@@ -342,51 +354,34 @@ __global__ __launch_bounds__(64 * W) void k_dot_sbl(DotArgs a, uint32_t rpc, uin
     const bool early = wave < pre;
     if (early && nck > 0) { issue(0, ring); mark[0] = ops; }
 
-#ifdef FLH_TRACE
-    wait_vm_dyn(ops - 1);                                         // diagnostic: the old y values alone
-    SBL_STAMP(5);
-#endif
     // wait for this wave's activation loads alone
     wait_vm_dyn(ops - x_mark);
+    SBL_STAMP(5);
     if constexpr (FUSE) {
         uint8_t * q81 = (uint8_t *)a.x + xq_off(cols);
         uint8_t * q8k = (uint8_t *)a.x + xqk_off(cols);
         const uint8_t * xf = ring + slot + 16 * lane;
-        // items j = 4h .. 4h+3: four absmaxes, one division sequence (lanes
-        // 0..3), then per item the bytes, block sums and d of the q8_K block
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            if ((uint32_t)(4 * h) >= nfi) break;                   // wave-uniform
-            float v[4][4];
-            uint32_t am[4] = {0u, 0u, 0u, 0u};
-            u32x4a rr[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) rr[j] = lds_ld128_nw(xf + 1024 * ((uint32_t)(4 * h + j) < nfi ? 4 * h + j : 0));
-            lds_wait4(rr[0], rr[1], rr[2], rr[3]);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const u32x4a r = rr[j];
-                v[j][0] = __uint_as_float(r.x); v[j][1] = __uint_as_float(r.y);
-                v[j][2] = __uint_as_float(r.z); v[j][3] = __uint_as_float(r.w);
-                if ((uint32_t)(4 * h + j) < nfi) am[j] = umax64(__float_as_uint(absmax4(v[j])));
-            }
-            const float al = __uint_as_float(lane == 0 ? am[0] : lane == 1 ? am[1] : lane == 2 ? am[2] : am[3]);
-            const float dl = al / 127.f;
-            const float idl = al > 0.f ? 127.f / al : 0.f;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                if ((uint32_t)(4 * h + j) >= nfi) break;
-                const uint32_t s = wave + W * (4 * h + j);
-                const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dl), j));
-                const float id = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(idl), j));
-                const uint32_t pk = quant4(v[j], id);
-                const int s16 = sum4i(dot4((int)pk, 0x01010101, 0));     // 16-element block sum
-                uint8_t * xb = xs + SBL_XS * s;
-                lds_st32(xb + 48 + 4 * lane, pk);
-                if ((lane & 3) == 0) lds_st16(xb + 16 + 2 * (lane >> 2), (uint32_t)s16);
-                if (lane == 0) lds_st32(xb + 12, __float_as_uint(d));
-                if (s % G == b) act_q8_lanes(v[j], lane, s, q81, q8k, cols);   // each block by one workgroup
-            }
+        // One item at a time, loop kept rolled (unrolled over 8 items with the
+        // appendix writer inlined it was ~16 KB of code, run once per wave).
+        // Its cost, ~1 us at 4096 columns, is VALU throughput: every
+        // workgroup quantises the whole column, 2 waves per SIMD x 2 items x
+        // ~75 instructions.
+#pragma unroll 1
+        for (uint32_t j = 0; j < nfi; ++j) {
+            const uint32_t s = wave + W * j;
+            const u32x4a r = lds_ld128(xf + 1024 * j);
+            const float v[4] = {__uint_as_float(r.x), __uint_as_float(r.y), __uint_as_float(r.z),
+                                __uint_as_float(r.w)};
+            const float amax = __uint_as_float(umax64(__float_as_uint(absmax4(v))));
+            const float d = amax / 127.f;
+            const float id = amax > 0.f ? 127.f / amax : 0.f;
+            const uint32_t pk = quant4(v, id);
+            const int s16 = sum4i(dot4((int)pk, 0x01010101, 0));     // 16-element block sum
+            uint8_t * xb = xs + SBL_XS * s;
+            lds_st32(xb + 48 + 4 * lane, pk);
+            if ((lane & 3) == 0) lds_st16(xb + 16 + 2 * (lane >> 2), (uint32_t)s16);
+            if (lane == 0) lds_st32(xb + 12, __float_as_uint(d));
+            if (s % G == b) write_appendices(v, lane, s, q81, q8k, cols);   // each block by one workgroup
         }
     }
     SBL_STAMP(6);
