@@ -38,7 +38,8 @@ HBM_PEAK_GBS = 8000.0
 MALL_BYTES = 256 << 20
 METRIC = "Q4_K/Q6_K matvec GB/s (% of HBM peak) + us/op at Llama-3-8B shapes, N=1"
 
-Q8_0, Q4_K, Q6_K = 1, 3, 4
+Q8_0, Q5_0, Q4_K, Q6_K, IQ2_XXS, IQ3_XXS = 1, 2, 3, 4, 5, 6
+BLOCK = {Q5_0: (32, 22), IQ2_XXS: (256, 66), IQ3_XXS: (256, 98)}
 LAYER = [("qkv", 6144, 4096), ("o", 4096, 4096), ("gate_up", 28672, 4096), ("down", 4096, 14336)]
 
 
@@ -69,6 +70,22 @@ class Bench:
                 flh.fill_normal(staging, nr * cols, seed * 1000003 + c * 7919 + r0, self.s, std=0.02)
                 flh.quantize(fmt, staging, nr, cols, w.ptr + r0 * rb, self.s)
             out.append(w)
+        self.s.sync()
+        return out
+
+    def weights_random(self, fmt, rows, cols, copies, seed):
+        """`copies` device copies of one matrix of random block bytes whose
+        fp16 scale d (bytes 0-1 of each block) is finite, as the reference
+        tests build them (tests/test_quants.cpp:109-128); the formats
+        flh_quantize does not produce (Q5_0, IQ2_XXS, IQ3_XXS)."""
+        rng = np.random.default_rng(seed)
+        n, bb = BLOCK[fmt]
+        w = rng.integers(0, 256, size=rows * (cols // n) * bb, dtype=np.uint8)
+        blocks = w.reshape(-1, bb)
+        d = (0x2000 | (rng.integers(0, 1 << 16, size=blocks.shape[0]) & 0x0BFF)).astype(np.uint16)
+        blocks[:, 0:2] = d.view(np.uint8).reshape(-1, 2)
+        out = [self.flh.DeviceBuffer.from_array(w, self.s) for _ in range(copies)]
+        self.bufs.extend(out)
         self.s.sync()
         return out
 
@@ -257,6 +274,23 @@ def main():
         us = B.time_graph(lambda i: flh.stream_dot(Q8_0, ws[i % len(ws)], r, c, x, y, s), REPS)
         op_entry(f"q8_0_{r}x{c}", us, nb)
         cpu_in[f"q8_0_{r}x{c}"] = host_case(flh, s, Q8_0, ws[0], r, c, x, st, 1)
+        del ws
+        # the other 32-weight-block formats on the same kernel: Q5_0 and the
+        # IQ codebook formats at an attention and an FFN shape (random
+        # block bytes; the reference CPU path has no IQ int8 dot, so only
+        # Q5_0 gets a CPU figure)
+        for fmt, fname in ((Q5_0, "q5_0"), (IQ2_XXS, "iq2_xxs"), (IQ3_XXS, "iq3_xxs")):
+            for r, c in ((4096, 4096), (14336, 4096)):
+                nb = r * flh.row_bytes(fmt, c)
+                ws = B.weights_random(fmt, r, c, copies_for(nb), seed=60 + fmt + r)
+                y = B.buf(r * 4)
+                # int8 dots for the IQ formats too (the reference's GPU default mask)
+                m8 = flh.I8_MASK_DEFAULT | (1 << IQ2_XXS) | (1 << IQ3_XXS)
+                us = B.time_graph(lambda i: flh.stream_dot(fmt, ws[i % len(ws)], r, c, x, y, s, i8_mask=m8), REPS)
+                op_entry(f"{fname}_{r}x{c}", us, nb)
+                if fmt == Q5_0 and r == 4096:
+                    cpu_in[f"q5_0_{r}x{c}"] = host_case(flh, s, Q5_0, ws[0], r, c, x, st, 1)
+                del ws
         # spec-verify small N
         for r, c in [(14336, 4096), (4096, 14336)]:
             nb = r * flh.row_bytes(Q4_K, c)
@@ -292,6 +326,9 @@ PROFILE_OPS = {
     "down": (Q4_K, 4096, 14336, 1, "dot"), "act_down": (Q4_K, 4096, 14336, 1, "act"),
     "q6k_vocab": (Q6_K, 128256, 4096, 1, "dot"), "q6k_down": (Q6_K, 4096, 14336, 1, "dot"),
     "q8_0": (Q8_0, 4096, 4096, 1, "dot"),
+    "q5_0": (Q5_0, 4096, 4096, 1, "dot"), "q5_0_ffn": (Q5_0, 14336, 4096, 1, "dot"),
+    "iq2_xxs": (IQ2_XXS, 4096, 4096, 1, "dot"), "iq2_xxs_ffn": (IQ2_XXS, 14336, 4096, 1, "dot"),
+    "iq3_xxs": (IQ3_XXS, 4096, 4096, 1, "dot"), "iq3_xxs_ffn": (IQ3_XXS, 14336, 4096, 1, "dot"),
 }
 for _n in (2, 4, 8):
     for _r, _c in ((14336, 4096), (4096, 14336)):
@@ -315,16 +352,20 @@ def profile_run(flh, B, s, staging, which="gate_up"):
         os.environ["FLH_NO_MFMA"] = "1"
         flh.init(0)
     nb = r * flh.row_bytes(fmt, c)
-    ws = B.weights(fmt, r, c, copies_for(nb), seed=101 + r + 7 * c, staging=staging)
+    if fmt in BLOCK:
+        ws = B.weights_random(fmt, r, c, copies_for(nb), seed=101 + r + 7 * c)
+    else:
+        ws = B.weights(fmt, r, c, copies_for(nb), seed=101 + r + 7 * c, staging=staging)
     x, st = B.activation(c, nx, 12, outliers=fmt == Q4_K)
     y = B.buf(nx * r * 4)
+    m8 = flh.I8_MASK_DEFAULT | (1 << IQ2_XXS) | (1 << IQ3_XXS)
     for i in range(64):
         if kind == "fused":
             flh.act_q8_stream_dot(fmt, ws[i % len(ws)], r, c, x, y, s)
         elif kind == "act":
             flh.act_q8(x, c, s)
         else:
-            flh.stream_dot(fmt, ws[i % len(ws)], r, c, x, y, s, nx=nx, xstride=st, ystride=r)
+            flh.stream_dot(fmt, ws[i % len(ws)], r, c, x, y, s, nx=nx, xstride=st, ystride=r, i8_mask=m8)
     s.sync()
 
 

@@ -121,9 +121,15 @@ static int dispatch_dot(int fmt, const DotArgs & a, int fast, uint32_t i8_mask, 
             const int rc = launch_dot_kstream(fmt, a, s);     // LDS-staged; register kernel otherwise
             return rc != FLH_ERR_UNSUPPORTED ? rc : launch_dot_i8_q8_0(a, s);
         }
-        if (fmt == FLH_FMT_Q5_0) return launch_dot_i8_q5_0(a, s);
         if (fmt == FLH_FMT_Q4_K || fmt == FLH_FMT_Q6_K) return launch_dot_i8_k(fmt, a, s);
-        return launch_dot_i8_iq(fmt, a, s);      // IQ2_XXS, IQ3_XXS
+        // Q5_0, IQ2_XXS, IQ3_XXS: one column on the LDS-staged kernel where its
+        // shape fits, the register kernel otherwise
+        if (tune().sbl) {
+            const int rc = launch_dot_sbl(fmt, a, false, s);
+            if (rc != FLH_ERR_UNSUPPORTED) return rc;
+        }
+        if (fmt == FLH_FMT_Q5_0) return launch_dot_i8_q5_0(a, s);
+        return launch_dot_i8_iq(fmt, a, s);
     }
     return launch_dot_fast_f32(fmt, a, s);
 }

@@ -1,5 +1,6 @@
-// flh_dot_sbl.hip -- single-column Q4_K x q8_K row-dots with one superblock
-// per lane.
+// flh_dot_sbl.hip -- single-column row-dots with one superblock (Q4_K x
+// q8_K) or four 32-weight blocks (Q8_0, Q5_0, IQ2_XXS, IQ3_XXS x q8_1) per
+// lane.
 //
 // The streaming kernel of flh_dot_kstream.hip splits a superblock over four
 // lanes, which costs every quarter its own scale decode, a DPP reduction and
@@ -24,6 +25,15 @@
 //   * waves are independent after the activation is staged: no barrier per
 //     batch, each wave keeps two chunks in flight and refills a stage as soon
 //     as its reads are done.
+//
+// The 32-weight-block formats fold as fl_dot_i8_q8_0 (src/runtime/quants.h:
+// 438-466): block b of a row goes to accumulator b & 3, so a lane holding
+// blocks 4p .. 4p + 3 (position p; P = 2 * nsb lanes per row) contributes one
+// term to each accumulator.  Terms are parked so that each (row,
+// accumulator) chain is contiguous, and a fold lane reads 16 of them per LDS
+// round trip.  Q5_0 lanes take 88 contiguous bytes; IQ lanes take half a
+// superblock (its d, the half's group data and, for IQ3, its sign words),
+// and the codebook is staged in LDS once per workgroup.
 //
 // Chunks are dealt to workgroups first (chunk c -> workgroup c % G), so a
 // matrix with fewer chunks than waves still spreads over every CU.
@@ -97,13 +107,19 @@ __device__ __forceinline__ void lds_wait4(u32x4a & a, u32x4a & b, u32x4a & c, u3
     asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d) :: "memory");
 }
 typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ u32x2v lds_ld64_nw(const void * p) {
-    u32x2v v;
-    asm volatile("ds_read_b64 %0, %1" : "=v"(v) : "v"(lds_off(p)) : "memory");
-    return v;
+__device__ __forceinline__ void lds_wait8(u32x4a (&t)[8]) {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(t[0]), "+v"(t[1]), "+v"(t[2]), "+v"(t[3]), "+v"(t[4]), "+v"(t[5]), "+v"(t[6]), "+v"(t[7])
+                 :: "memory");
 }
-__device__ __forceinline__ void lds_wait4x2(u32x2v (&t)[4]) {
-    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(t[0]), "+v"(t[1]), "+v"(t[2]), "+v"(t[3]) :: "memory");
+__device__ __forceinline__ void lds_wait16(u32x4a (&t)[16]) {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(t[0]), "+v"(t[1]), "+v"(t[2]), "+v"(t[3]), "+v"(t[4]), "+v"(t[5]), "+v"(t[6]), "+v"(t[7]),
+                   "+v"(t[8]), "+v"(t[9]), "+v"(t[10]), "+v"(t[11]), "+v"(t[12]), "+v"(t[13]), "+v"(t[14]), "+v"(t[15])
+                 :: "memory");
+}
+__device__ __forceinline__ void lds_st64(void * p, u32x2v v) {
+    asm volatile("ds_write_b64 %0, %1" :: "v"(lds_off(p)), "v"(v));
 }
 __device__ __forceinline__ void lds_st16(void * p, uint32_t v) {
     asm volatile("ds_write_b16 %0, %1" :: "v"(lds_off(p)), "v"(v));
@@ -252,17 +268,185 @@ __device__ __forceinline__ void sbl_q8_0(const uint32_t (&D)[34], const XQ8 & X,
     }
 }
 
+// ---- Q5_0: a lane takes 4 blocks of 22 bytes (88 bytes, 8-byte aligned).
+__device__ __forceinline__ void lds_ld_q5h(const void * p, uint32_t (&d)[22]) {
+    u32x2a v[11];
+    asm volatile("ds_read_b64 %0, %11\n\tds_read_b64 %1, %11 offset:8\n\tds_read_b64 %2, %11 offset:16\n\t"
+                 "ds_read_b64 %3, %11 offset:24\n\tds_read_b64 %4, %11 offset:32\n\tds_read_b64 %5, %11 offset:40\n\t"
+                 "ds_read_b64 %6, %11 offset:48\n\tds_read_b64 %7, %11 offset:56\n\tds_read_b64 %8, %11 offset:64\n\t"
+                 "ds_read_b64 %9, %11 offset:72\n\tds_read_b64 %10, %11 offset:80\n\ts_waitcnt lgkmcnt(0)"
+                 : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]), "=&v"(v[6]),
+                   "=&v"(v[7]), "=&v"(v[8]), "=&v"(v[9]), "=&v"(v[10])
+                 : "v"(lds_off(p)) : "memory");
+#pragma unroll
+    for (int i = 0; i < 11; ++i) { d[2 * i] = v[i].x; d[2 * i + 1] = v[i].y; }
+}
+
+// Block dots of fl_dot_i8_q5_0 (src/runtime/quants.h:449-466): the unshifted
+// 5-bit values (0..31) against the q8_1 quants, minus 16 x the block's
+// activation sum; factor d_w * d_x.  Block m starts at byte 22m: blocks 0 and
+// 2 at a dword boundary (d, then qh 2 bytes into it, nibbles 6 bytes in),
+// blocks 1 and 3 two bytes into dword 5 / 16 (qh and the nibbles aligned).
+__device__ __forceinline__ void sbl_q5_0(const uint32_t (&D)[22], const XQ8 & X, const int (&xsum)[4], float (&f)[4],
+                                         int (&id)[4]) {
+    const int o[4] = {0, 5, 11, 16};
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        const bool odd = m & 1;
+        const uint32_t db = odd ? D[o[m]] >> 16 : D[o[m]] & 0xFFFFu;
+        const uint32_t qh = odd ? D[o[m] + 1] : alignb(D[o[m] + 1], D[o[m]], 2);
+        const u32x4a xa = X.q[2 * m], xb = X.q[2 * m + 1];
+        const uint32_t XV[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+        int s0 = 0, s1 = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t q = odd ? D[o[m] + 2 + k] : alignb(D[o[m] + 2 + k], D[o[m] + 1 + k], 2);
+            const uint32_t lo = (q & 0x0F0F0F0Fu) | (spread4((qh >> (4 * k)) & 0xFu) << 4);
+            const uint32_t hi = ((q >> 4) & 0x0F0F0F0Fu) | (spread4((qh >> (16 + 4 * k)) & 0xFu) << 4);
+            s0 = dot4((int)lo, (int)XV[k], s0);
+            s1 = dot4((int)hi, (int)XV[4 + k], s1);
+        }
+        id[m] = s0 + s1 - 16 * xsum[m];
+        f[m] = h2f(db) * X.dx[m];
+    }
+}
+
+// ---- IQ2_XXS / IQ3_XXS: a lane takes half a superblock, groups 4h .. 4h + 3
+// (h = lane & 1) of superblock lane >> 1.  Its bytes are not contiguous:
+// d at the superblock's start, the half's 32 bytes of group data at +2 + 32h
+// (IQ2: per group 4 grid indices and the scale/sign word w1; IQ3: 8 grid
+// indices per group) and, for IQ3, the half's four w1 words at +66 + 16h.
+// Superblocks are 66 / 98 bytes, so these pieces are 2-byte aligned: they
+// are read as dwords from the aligned address below and shifted into place.
+template <int FMT>
+__device__ __forceinline__ void lds_ld_iqh(const uint8_t * st, uint32_t lane, uint32_t & db, uint32_t (&G)[8],
+                                           uint32_t (&S)[4]) {
+    constexpr uint32_t BB = iq_block_bytes(FMT);
+    const uint32_t base = lds_off(st) + BB * (lane >> 1), h = lane & 1u;
+    const uint32_t A = base + 2 + 32 * h, a4 = A & ~3u, sh = A & 3u;
+    u32x2a r0, r1, r2, r3;
+    uint32_t r4, dv;
+    asm volatile("ds_read_u16 %5, %6\n\tds_read2_b32 %0, %7 offset1:1\n\tds_read2_b32 %1, %7 offset0:2 offset1:3\n\t"
+                 "ds_read2_b32 %2, %7 offset0:4 offset1:5\n\tds_read2_b32 %3, %7 offset0:6 offset1:7\n\t"
+                 "ds_read_b32 %4, %7 offset:32\n\ts_waitcnt lgkmcnt(0)"
+                 : "=&v"(r0), "=&v"(r1), "=&v"(r2), "=&v"(r3), "=&v"(r4), "=&v"(dv)
+                 : "v"(base), "v"(a4) : "memory");
+    const uint32_t w[9] = {r0.x, r0.y, r1.x, r1.y, r2.x, r2.y, r3.x, r3.y, r4};
+#pragma unroll
+    for (int k = 0; k < 8; ++k) G[k] = alignb(w[k + 1], w[k], sh);
+    db = dv;
+    if constexpr (FMT == FMT_IQ3_XXS) {
+        const uint32_t s4 = (A + 64 - 16 * h) & ~3u;              // same alignment as A
+        u32x2a t0, t1;
+        uint32_t t2;
+        asm volatile("ds_read2_b32 %0, %3 offset1:1\n\tds_read2_b32 %1, %3 offset0:2 offset1:3\n\t"
+                     "ds_read_b32 %2, %3 offset:16\n\ts_waitcnt lgkmcnt(0)"
+                     : "=&v"(t0), "=&v"(t1), "=&v"(t2) : "v"(s4) : "memory");
+        const uint32_t u[5] = {t0.x, t0.y, t1.x, t1.y, t2};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) S[k] = alignb(u[k + 1], u[k], sh);
+    }
+}
+
+// Grid entries (magnitude bytes) of the lane's four groups, all requested in
+// one LDS round trip: E[4m + l] = run l of group m as (elements 0-3,
+// elements 4-7).  IQ2: one 8-byte entry per index byte of w0 (G[2m]); IQ3:
+// one 4-byte entry per index byte of G[2m], G[2m + 1].
+template <int FMT>
+__device__ __forceinline__ void iq_runs(uint32_t grid, const uint32_t (&G)[8], u32x2a (&E)[16]) {
+    if constexpr (FMT == FMT_IQ2_XXS) {
+        uint32_t ad[16];
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+#pragma unroll
+            for (int l = 0; l < 4; ++l) ad[4 * m + l] = grid + 8 * ((G[2 * m] >> (8 * l)) & 0xFFu);
+        asm volatile("ds_read_b64 %0, %16\n\tds_read_b64 %1, %17\n\tds_read_b64 %2, %18\n\tds_read_b64 %3, %19\n\t"
+                     "ds_read_b64 %4, %20\n\tds_read_b64 %5, %21\n\tds_read_b64 %6, %22\n\tds_read_b64 %7, %23\n\t"
+                     "ds_read_b64 %8, %24\n\tds_read_b64 %9, %25\n\tds_read_b64 %10, %26\n\tds_read_b64 %11, %27\n\t"
+                     "ds_read_b64 %12, %28\n\tds_read_b64 %13, %29\n\tds_read_b64 %14, %30\n\tds_read_b64 %15, %31\n\t"
+                     "s_waitcnt lgkmcnt(0)"
+                     : "=&v"(E[0]), "=&v"(E[1]), "=&v"(E[2]), "=&v"(E[3]), "=&v"(E[4]), "=&v"(E[5]), "=&v"(E[6]),
+                       "=&v"(E[7]), "=&v"(E[8]), "=&v"(E[9]), "=&v"(E[10]), "=&v"(E[11]), "=&v"(E[12]), "=&v"(E[13]),
+                       "=&v"(E[14]), "=&v"(E[15])
+                     : "v"(ad[0]), "v"(ad[1]), "v"(ad[2]), "v"(ad[3]), "v"(ad[4]), "v"(ad[5]), "v"(ad[6]), "v"(ad[7]),
+                       "v"(ad[8]), "v"(ad[9]), "v"(ad[10]), "v"(ad[11]), "v"(ad[12]), "v"(ad[13]), "v"(ad[14]),
+                       "v"(ad[15])
+                     : "memory");
+    } else {
+        uint32_t ad[32], v[32];
+#pragma unroll
+        for (int b = 0; b < 32; ++b) ad[b] = grid + 4 * ((G[b >> 2] >> (8 * (b & 3))) & 0xFFu);
+        asm volatile("ds_read_b32 %0, %32\n\tds_read_b32 %1, %33\n\tds_read_b32 %2, %34\n\tds_read_b32 %3, %35\n\t"
+                     "ds_read_b32 %4, %36\n\tds_read_b32 %5, %37\n\tds_read_b32 %6, %38\n\tds_read_b32 %7, %39\n\t"
+                     "ds_read_b32 %8, %40\n\tds_read_b32 %9, %41\n\tds_read_b32 %10, %42\n\tds_read_b32 %11, %43\n\t"
+                     "ds_read_b32 %12, %44\n\tds_read_b32 %13, %45\n\tds_read_b32 %14, %46\n\tds_read_b32 %15, %47\n\t"
+                     "ds_read_b32 %16, %48\n\tds_read_b32 %17, %49\n\tds_read_b32 %18, %50\n\tds_read_b32 %19, %51\n\t"
+                     "ds_read_b32 %20, %52\n\tds_read_b32 %21, %53\n\tds_read_b32 %22, %54\n\tds_read_b32 %23, %55\n\t"
+                     "ds_read_b32 %24, %56\n\tds_read_b32 %25, %57\n\tds_read_b32 %26, %58\n\tds_read_b32 %27, %59\n\t"
+                     "ds_read_b32 %28, %60\n\tds_read_b32 %29, %61\n\tds_read_b32 %30, %62\n\tds_read_b32 %31, %63\n\t"
+                     "s_waitcnt lgkmcnt(0)"
+                     : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]), "=&v"(v[6]),
+                       "=&v"(v[7]), "=&v"(v[8]), "=&v"(v[9]), "=&v"(v[10]), "=&v"(v[11]), "=&v"(v[12]), "=&v"(v[13]),
+                       "=&v"(v[14]), "=&v"(v[15]), "=&v"(v[16]), "=&v"(v[17]), "=&v"(v[18]), "=&v"(v[19]),
+                       "=&v"(v[20]), "=&v"(v[21]), "=&v"(v[22]), "=&v"(v[23]), "=&v"(v[24]), "=&v"(v[25]),
+                       "=&v"(v[26]), "=&v"(v[27]), "=&v"(v[28]), "=&v"(v[29]), "=&v"(v[30]), "=&v"(v[31])
+                     : "v"(ad[0]), "v"(ad[1]), "v"(ad[2]), "v"(ad[3]), "v"(ad[4]), "v"(ad[5]), "v"(ad[6]), "v"(ad[7]),
+                       "v"(ad[8]), "v"(ad[9]), "v"(ad[10]), "v"(ad[11]), "v"(ad[12]), "v"(ad[13]), "v"(ad[14]),
+                       "v"(ad[15]), "v"(ad[16]), "v"(ad[17]), "v"(ad[18]), "v"(ad[19]), "v"(ad[20]), "v"(ad[21]),
+                       "v"(ad[22]), "v"(ad[23]), "v"(ad[24]), "v"(ad[25]), "v"(ad[26]), "v"(ad[27]), "v"(ad[28]),
+                       "v"(ad[29]), "v"(ad[30]), "v"(ad[31])
+                     : "memory");
+#pragma unroll
+        for (int k = 0; k < 16; ++k) E[k] = u32x2a{v[2 * k], v[2 * k + 1]};
+    }
+}
+
+// Group dots of the codebook formats: the signed grid magnitudes (run l takes
+// sign field l of w1, bit j negating element 8l + j) against the q8_1 quants;
+// factor db * d_x with db = (d * (0.5 + s)) * 0.25 (IQ2) or * 0.5 (IQ3), s =
+// w1 >> 28 (kernels_gpu.h:759-852; fold as fl_dot_i8_q8_0).
+template <int FMT>
+__device__ __forceinline__ void sbl_iq(const uint8_t * st, uint32_t lane, uint32_t grid, const XQ8 & X, float (&f)[4],
+                                       int (&id)[4]) {
+    uint32_t dbits, G[8], S[4];
+    lds_ld_iqh<FMT>(st, lane, dbits, G, S);
+    u32x2a E[16];
+    iq_runs<FMT>(grid, G, E);
+    const float d = h2f(dbits);
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        const uint32_t w1 = FMT == FMT_IQ2_XXS ? G[2 * m + 1] : S[m];
+        const u32x4a xa = X.q[2 * m], xb = X.q[2 * m + 1];
+        const uint32_t XV[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+        int s0 = 0, s1 = 0;
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+            const uint32_t sg = iq_sign8(w1 >> (7 * l));
+            s0 = dot4((int)iq_apply(E[4 * m + l].x, iq_neg4(sg)), (int)XV[2 * l], s0);
+            s1 = dot4((int)iq_apply(E[4 * m + l].y, iq_neg4(sg >> 4)), (int)XV[2 * l + 1], s1);
+        }
+        id[m] = s0 + s1;
+        f[m] = iq_db(FMT, d, w1) * X.dx[m];
+    }
+}
+
 }  // namespace
 
 // One pass over all rows for one column.  Launch: G workgroups of W waves,
 // dynamic LDS = W * 2 * slot (rings) + the staged activation (rounded to
-// 1 KiB) + W * 1280 bytes (fold terms and old y values).
+// 1 KiB) + W * (TB + 256) bytes (fold terms and old y values) + the IQ
+// codebook (2 KiB).
 template <int FMT, bool FUSE, int W>
 __global__ __launch_bounds__(64 * W) void k_dot_sbl(DotArgs a, uint32_t rpc, uint32_t ni, uint32_t slot, uint32_t pre) {
-    static_assert(FMT == FMT_Q4_K || (FMT == FMT_Q8_0 && !FUSE), "Q4_K (fused or not) or Q8_0");
-    constexpr bool Q8 = FMT == FMT_Q8_0;
-    constexpr uint32_t B = Q8 ? 136 : 144;                        // bytes of a lane's weights
-    constexpr uint32_t TB = Q8 ? 2048 : 1024;                     // fold-term bytes of a wave
+    static_assert(FMT == FMT_Q4_K || !FUSE, "only Q4_K fuses the quantisation");
+    static_assert(FMT == FMT_Q4_K || FMT == FMT_Q8_0 || FMT == FMT_Q5_0 || FMT == FMT_IQ2_XXS ||
+                  FMT == FMT_IQ3_XXS, "Q4_K or a 32-weight-block format");
+    constexpr bool Q8 = FMT != FMT_Q4_K;                          // 4 blocks of 32 weights per lane
+    constexpr bool IQ = FMT == FMT_IQ2_XXS || FMT == FMT_IQ3_XXS;
+    // bytes of a lane's weights (IQ: half a superblock's share)
+    constexpr uint32_t B = FMT == FMT_Q4_K ? 144 : FMT == FMT_Q8_0 ? 136 : FMT == FMT_Q5_0 ? 88
+                                                 : iq_block_bytes(FMT) / 2;
+    constexpr uint32_t TB = Q8 ? 4096 : 1024;                     // fold-term bytes of a wave
     extern __shared__ __attribute__((aligned(16))) uint8_t sm[];
     const uint32_t nsb = a.cols >> 8, rows = a.rows, cols = a.cols;
     const uint32_t P = Q8 ? 2 * nsb : nsb;                        // lanes of a row
@@ -275,8 +459,9 @@ __global__ __launch_bounds__(64 * W) void k_dot_sbl(DotArgs a, uint32_t rpc, uin
     uint8_t * ring = sm + (size_t)wave * 2 * slot;
     uint8_t * xs = sm + (size_t)W * 2 * slot;
     const uint32_t xs_bytes = ((Q8 ? nsb * 8 * SBL_X8 : nsb * SBL_XS) + 1023u) & ~1023u;
-    uint8_t * T = xs + xs_bytes + wave * (TB + 256);              // [64][TB / 64] fold terms of this wave
+    uint8_t * T = xs + xs_bytes + wave * (TB + 256);              // fold terms of this wave
     uint8_t * Y = T + TB;                                         // [64] old y values of this wave
+    const uint32_t grid = lds_off(xs + xs_bytes + W * (TB + 256)); // IQ codebook (2 KiB)
     const uint8_t * w = a.w + (a.id_slot ? (size_t)(*a.id_slot) * a.estride : 0);
     const uint64_t cb = (uint64_t)rpc * P * B;                    // bytes of a full chunk
     const uint8_t * xk = (const uint8_t *)a.x + xqk_off(cols);
@@ -297,6 +482,19 @@ __global__ __launch_bounds__(64 * W) void k_dot_sbl(DotArgs a, uint32_t rpc, uin
     };
     yload(0);
     uint32_t y_mark = ops;
+    if constexpr (IQ) {
+        // the codebook (IQ2 2 KiB, IQ3 1 KiB) by wave 0, covered by its
+        // activation wait and the barrier after it
+        constexpr uint32_t GB = FMT == FMT_IQ2_XXS ? 2048 : 1024;
+        const uint8_t * gsrc = FMT == FMT_IQ2_XXS ? (const uint8_t *)k_iq2_grid : (const uint8_t *)k_iq3_grid;
+        if (wave == 0) {
+            for (uint32_t t = 0; t < GB / 1024; ++t) {
+                __builtin_amdgcn_global_load_lds(GPTR(gsrc + 1024 * t + 16 * lane),
+                                                 LPTR(xs + xs_bytes + W * (TB + 256) + 1024 * t), 16, 0, 0);
+                ++ops;
+            }
+        }
+    }
 
     // activation: DMA of the q8_K blocks into the staged layout, or (FUSE)
     // of the fp32 superblocks w, w + W, ... of this wave into its second
@@ -388,8 +586,21 @@ __global__ __launch_bounds__(64 * W) void k_dot_sbl(DotArgs a, uint32_t rpc, uin
     lds_barrier();
     SBL_STAMP(1);
     typename std::conditional<Q8, XQ8, XQ4>::type X;
+    int xsum[4] = {0, 0, 0, 0};                                   // Q5_0: the blocks' activation sums
     if constexpr (Q8) load_xq8(xs + 4 * SBL_X8 * (lane % P), X);
     else load_xq4(xs + SBL_XS * (lane % nsb), X);
+    if constexpr (FMT == FMT_Q5_0) {
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const u32x4a xa = X.q[2 * m], xb = X.q[2 * m + 1];
+            int t = 0;
+            t = dot4(0x01010101, (int)xa.x, t); t = dot4(0x01010101, (int)xa.y, t);
+            t = dot4(0x01010101, (int)xa.z, t); t = dot4(0x01010101, (int)xa.w, t);
+            t = dot4(0x01010101, (int)xb.x, t); t = dot4(0x01010101, (int)xb.y, t);
+            t = dot4(0x01010101, (int)xb.z, t); t = dot4(0x01010101, (int)xb.w, t);
+            xsum[m] = t;
+        }
+    }
     // The rest of the prologue comes after the barrier: a request blocks its
     // wave while the CU's memory queue is full, and a wave stuck there would
     // hold the whole workgroup at the barrier.
@@ -412,19 +623,32 @@ __global__ __launch_bounds__(64 * W) void k_dot_sbl(DotArgs a, uint32_t rpc, uin
         if (i == 0) SBL_STAMP(2);
         if (i + 1 == nck) SBL_STAMP(3);
         if constexpr (Q8) {
-            uint32_t D[34];
-            lds_ld_q8h(st + B * lane, D);
             float f[4];
             int id[4];
-            sbl_q8_0(D, X, f, id);
+            if constexpr (FMT == FMT_Q8_0) {
+                uint32_t D[34];
+                lds_ld_q8h(st + B * lane, D);
+                sbl_q8_0(D, X, f, id);
+            } else if constexpr (FMT == FMT_Q5_0) {
+                uint32_t D[22];
+                lds_ld_q5h(st + B * lane, D);
+                sbl_q5_0(D, X, xsum, f, id);
+            } else {
+                sbl_iq<FMT>(st, lane, grid, X, f, id);
+            }
             if (i + 2 < nck) {                                    // refill this stage
                 issue(i + 2, st);
                 mark[sl] = ops;
             }
-            lds_st128(T + 32 * lane, u32x4a{__float_as_uint(f[0]), __float_as_uint((float)id[0]),
-                                            __float_as_uint(f[1]), __float_as_uint((float)id[1])});
-            lds_st128(T + 32 * lane + 16, u32x4a{__float_as_uint(f[2]), __float_as_uint((float)id[2]),
-                                                 __float_as_uint(f[3]), __float_as_uint((float)id[3])});
+            // chain (row r, accumulator k) = its P terms in position order,
+            // CS bytes per chain (16 bytes of padding spread the fold
+            // lanes' reads over the banks)
+            const uint32_t r = lane / P, pos = lane - r * P, CS = 8 * P + 16;
+            if (r < rpc) {
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    lds_st64(T + (4 * r + k) * CS + 8 * pos, u32x2a{__float_as_uint(f[k]), __float_as_uint((float)id[k])});
+            }
         } else {
             u32x4a wv[9];
             lds_ld_q4k(st + B * lane, wv);
@@ -458,8 +682,15 @@ __global__ __launch_bounds__(64 * W) void k_dot_sbl(DotArgs a, uint32_t rpc, uin
                 ++ops;                                            // lane nsb - 4 (row 0 of the chunk) stores
                 continue;
             }
-            lds_st128(T + 16 * lane, u32x4a{__float_as_uint(f1), __float_as_uint((float)ia), __float_as_uint(f2),
-                                            __float_as_uint((float)im)});
+            // one row per chunk (more than 32 superblocks): accumulator k's
+            // terms (positions k, k + 4, ...) contiguous; else lane order
+            const u32x4a tv{__float_as_uint(f1), __float_as_uint((float)ia), __float_as_uint(f2),
+                            __float_as_uint((float)im)};
+            if (rpc == 1) {
+                if (lane < nsb) lds_st128(T + (lane & 3) * (16 * ((nsb + 3) >> 2)) + 16 * (lane >> 2), tv);
+            } else {
+                lds_st128(T + 16 * lane, tv);
+            }
         }
         // reference fold: accumulator fk of row r0 + fr over its terms in
         // order (Q4_K: positions fk, fk + 4, ...; Q8_0: block fk of every
@@ -469,15 +700,36 @@ __global__ __launch_bounds__(64 * W) void k_dot_sbl(DotArgs a, uint32_t rpc, uin
             const uint32_t r = r0 + fr;
             float acc = 0.f;
             if (Q8 && r < rpc) {
-                const uint8_t * tr = T + 32 * (r * P) + 8 * fk;
-                for (uint32_t j0 = 0; j0 < P; j0 += 4) {
-                    u32x2a t[4];
+                // 16 terms (8 x 16 bytes) per LDS round trip; P is even
+                const uint8_t * tr = T + (4 * r + fk) * (8 * P + 16);
+                for (uint32_t j0 = 0; j0 < P; j0 += 16) {
+                    u32x4a t[8];
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) t[q] = lds_ld64_nw(tr + 32 * (j0 + q < P ? j0 + q : j0));
-                    lds_wait4x2(t);
+                    for (int q = 0; q < 8; ++q) t[q] = lds_ld128_nw(tr + 8 * (j0 + 2 * q < P ? j0 + 2 * q : j0));
+                    lds_wait8(t);
 #pragma unroll
-                    for (int q = 0; q < 4; ++q)
-                        if (j0 + q < P) acc = fmaf(__uint_as_float(t[q].x), __uint_as_float(t[q].y), acc);
+                    for (int q = 0; q < 8; ++q) {
+                        if (j0 + 2 * q < P) {
+                            acc = fmaf(__uint_as_float(t[q].x), __uint_as_float(t[q].y), acc);
+                            acc = fmaf(__uint_as_float(t[q].z), __uint_as_float(t[q].w), acc);
+                        }
+                    }
+                }
+            } else if (rpc == 1) {
+                if (lane < 4) {                                   // one LDS round trip (<= 16 terms)
+                    const uint32_t nk = (nsb - fk + 3) >> 2;      // nsb > 32: 9 .. 16 terms
+                    const uint8_t * tr = T + fk * (16 * ((nsb + 3) >> 2));
+                    u32x4a t[16];
+#pragma unroll
+                    for (int q = 0; q < 16; ++q) t[q] = lds_ld128_nw(tr + 16 * (q < (int)nk ? q : 0));
+                    lds_wait16(t);
+#pragma unroll
+                    for (int q = 0; q < 16; ++q) {
+                        if (q < (int)nk) {
+                            acc = fmaf(__uint_as_float(t[q].x), __uint_as_float(t[q].y), acc);
+                            acc = fmaf(__uint_as_float(t[q].z), __uint_as_float(t[q].w), acc);
+                        }
+                    }
                 }
             } else if (r < rpc) {
                 const uint8_t * tr = T + 16 * (r * nsb);
@@ -512,17 +764,22 @@ __global__ __launch_bounds__(64 * W) void k_dot_sbl(DotArgs a, uint32_t rpc, uin
 #endif
 }
 
-static size_t sbl_smem(bool q8, uint32_t W, uint32_t slot, uint32_t nsb) {
+static size_t sbl_smem(bool q8, bool iq, uint32_t W, uint32_t slot, uint32_t nsb) {
     const size_t xs = ((q8 ? nsb * 8 * SBL_X8 : nsb * SBL_XS) + 1023u) & ~(size_t)1023;
-    return (size_t)W * 2 * slot + xs + (size_t)W * ((q8 ? 2048 : 1024) + 256);
+    return (size_t)W * 2 * slot + xs + (size_t)W * ((q8 ? 4096 : 1024) + 256) + (iq ? 2048 : 0);
 }
 
 int launch_dot_sbl(int fmt, const DotArgs & a, bool fuse, hipStream_t s) {
-    const bool q8 = fmt == FMT_Q8_0;
+    const bool iq = fmt == FMT_IQ2_XXS || fmt == FMT_IQ3_XXS;
+    const bool q8 = fmt == FMT_Q8_0 || fmt == FMT_Q5_0 || iq;     // 32-weight blocks
     if ((fmt != FMT_Q4_K && !q8) || (q8 && fuse) || a.nx != 1 || (a.cols & 255) || a.rows == 0)
         return FLH_ERR_UNSUPPORTED;
-    const uint32_t nsb = a.cols >> 8, P = q8 ? 2 * nsb : nsb, B = q8 ? 136 : 144;
+    const uint32_t nsb = a.cols >> 8, P = q8 ? 2 * nsb : nsb;
+    const uint32_t B = fmt == FMT_Q4_K ? 144 : fmt == FMT_Q8_0 ? 136 : fmt == FMT_Q5_0 ? 88
+                                              : iq_block_bytes(fmt) / 2;
     if (nsb < 1 || P > 64) return FLH_ERR_UNSUPPORTED;
+    // chunks are whole rows moved in 16-byte pieces (IQ rows: nsb % 8 == 0)
+    if ((P * B) & 15) return FLH_ERR_UNSUPPORTED;
     if ((uintptr_t)a.w & 15 || (a.estride & 15)) return FLH_ERR_UNSUPPORTED;
     if ((fuse || q8) && ((uintptr_t)a.x & 15)) return FLH_ERR_UNSUPPORTED;
     const Tune & t = tune();
@@ -536,14 +793,17 @@ int launch_dot_sbl(int fmt, const DotArgs & a, bool fuse, hipStream_t s) {
     //  * unfused, <= 16 superblocks per row: 4 waves, 2 early (O 4096x4096
     //    5.37 -> 4.85 us, QKV 5.95 -> 5.49);
     //  * unfused, wider rows: 8 waves, 4 early (down 4096x14336 9.78 -> 9.63);
-    //  * Q8_0: 4 waves, all early (4096x4096 7.65 -> 7.25 us; its cost is the
-    //    fold, 32 dependent steps per accumulator and row at 4096 columns).
+    //  * Q8_0: 4 waves, all early (4096x4096 6.98 -> 6.31 us, 14336x4096
+    //    13.53 -> 13.27 against 8 waves);
+    //  * Q5_0 and the IQ formats, more VALU work per byte: 8 waves, all
+    //    early (14336x4096 Q5_0 15.2 -> 11.9 us, IQ2_XXS 16.6 -> 12.2,
+    //    IQ3_XXS 18.3 -> 13.5 against 4 waves).
     if (fuse && !t.sbl_w && (uint64_t)a.rows * nsb > (1u << 17)) return FLH_ERR_UNSUPPORTED;
-    const uint32_t wdef = fuse || nsb > 16 ? 8 : 4;
+    const uint32_t wdef = fuse || nsb > 16 || (q8 && fmt != FMT_Q8_0) ? 8 : 4;
     uint32_t W = t.sbl_w ? t.sbl_w : wdef;
     const uint32_t pre = t.sbl_pre == 0xFFu ? W : t.sbl_pre ? t.sbl_pre : q8 ? W : W / 2;
-    while (W > 4 && sbl_smem(q8, W, slot, nsb) > lds_limit()) W -= 2;
-    const size_t smb = sbl_smem(q8, W, slot, nsb);
+    while (W > 4 && sbl_smem(q8, iq, W, slot, nsb) > lds_limit()) W -= 2;
+    const size_t smb = sbl_smem(q8, iq, W, slot, nsb);
     if (smb > lds_limit() || (W != 8 && W != 6 && W != 4)) return FLH_ERR_UNSUPPORTED;
     if (fuse && (nsb + W - 1) / W > 8) return FLH_ERR_UNSUPPORTED;
     const uint32_t C = (a.rows + rpc - 1) / rpc;
@@ -556,14 +816,23 @@ int launch_dot_sbl(int fmt, const DotArgs & a, bool fuse, hipStream_t s) {
         hipLaunchKernelGGL(kern, dim3(G), dim3(64 * W), smb, s, a, rpc, ni, slot, pre);
         return hip_check(hipGetLastError(), "k_dot_sbl launch");
     };
-    if (q8) {
-        if (W == 8) return go(k_dot_sbl<FMT_Q8_0, false, 8>);
-        if (W == 6) return go(k_dot_sbl<FMT_Q8_0, false, 6>);
-        return go(k_dot_sbl<FMT_Q8_0, false, 4>);
+    auto unfused = [&](auto fmt_tag) {
+        constexpr int F = decltype(fmt_tag)::value;
+        if (W == 8) return go(k_dot_sbl<F, false, 8>);
+        if (W == 6) return go(k_dot_sbl<F, false, 6>);
+        return go(k_dot_sbl<F, false, 4>);
+    };
+    switch (fmt) {
+        case FMT_Q8_0: return unfused(std::integral_constant<int, FMT_Q8_0>());
+        case FMT_Q5_0: return unfused(std::integral_constant<int, FMT_Q5_0>());
+        case FMT_IQ2_XXS: return unfused(std::integral_constant<int, FMT_IQ2_XXS>());
+        case FMT_IQ3_XXS: return unfused(std::integral_constant<int, FMT_IQ3_XXS>());
+        default: break;
     }
-    if (W == 8) return fuse ? go(k_dot_sbl<FMT_Q4_K, true, 8>) : go(k_dot_sbl<FMT_Q4_K, false, 8>);
-    if (W == 6) return fuse ? go(k_dot_sbl<FMT_Q4_K, true, 6>) : go(k_dot_sbl<FMT_Q4_K, false, 6>);
-    return fuse ? go(k_dot_sbl<FMT_Q4_K, true, 4>) : go(k_dot_sbl<FMT_Q4_K, false, 4>);
+    if (!fuse) return unfused(std::integral_constant<int, FMT_Q4_K>());
+    if (W == 8) return go(k_dot_sbl<FMT_Q4_K, true, 8>);
+    if (W == 6) return go(k_dot_sbl<FMT_Q4_K, true, 6>);
+    return go(k_dot_sbl<FMT_Q4_K, true, 4>);
 }
 
 }  // namespace flh

@@ -104,3 +104,63 @@ def test_sbl_q8_0_bitwise(flh, orc, gpu, cfg, rows, cols):
     with tuned(flh, FLH_SBL=cfg):
         got, want = run_dot(flh, orc, gpu, Q8_0, w, rows, cols, xs, y0=y0)
         assert np.array_equal(bits(got), bits(want))
+
+
+Q5_0, IQ2_XXS, IQ3_XXS = 2, 5, 6
+B32_MODE = {Q5_0: "int8", IQ2_XXS: "iq8", IQ3_XXS: "iq8"}
+
+
+@pytest.mark.parametrize("cfg", ["1", "1,8,1,0", "1,4,2,0,255", "1,6,1,3,1"])
+@pytest.mark.parametrize("rows,cols", [(7, 256), (33, 512), (41, 768), (13, 2816), (1001, 4096), (70, 8192),
+                                       (4096, 4096)])
+def test_sbl_q5_0_bitwise(flh, orc, gpu, cfg, rows, cols):
+    """Q5_0 x q8_1 with 4 blocks (88 bytes) per lane: bitwise fl_dot_i8_q5_0
+    (src/runtime/quants.h:449-466) for every lane count per row up to 64."""
+    say("sbl q5_0", cfg, rows, cols)
+    rng = np.random.default_rng(rows * 7 + cols)
+    w = sane_rows(Q5_0, rows, cols, rng)
+    xs = activations(1, cols, rng, outliers=True)
+    y0 = rng.standard_normal(rows).astype(np.float32)
+    with tuned(flh, FLH_SBL=cfg):
+        got, want = run_dot(flh, orc, gpu, Q5_0, w, rows, cols, xs, y0=y0)
+        assert np.array_equal(bits(got), bits(want))
+
+
+@pytest.mark.parametrize("fmt", [IQ2_XXS, IQ3_XXS])
+@pytest.mark.parametrize("cfg", ["1", "1,8,1,0", "1,4,2,0,255", "1,6,1,3,1"])
+@pytest.mark.parametrize("rows,cols", [(5, 2048), (33, 2048), (1001, 4096), (70, 8192), (4096, 4096)])
+def test_sbl_iq_bitwise(flh, orc, gpu, fmt, cfg, rows, cols):
+    """IQ2_XXS / IQ3_XXS x q8_1 with half a superblock per lane (2-byte
+    aligned pieces, codebook staged in LDS): bitwise against the oracle's
+    group order (fmaf(db * dx, idot, a[b & 3]))."""
+    say("sbl iq", fmt, cfg, rows, cols)
+    rng = np.random.default_rng(rows * 11 + cols + fmt)
+    w = sane_rows(fmt, rows, cols, rng)
+    xs = activations(1, cols, rng, outliers=True)
+    y0 = rng.standard_normal(rows).astype(np.float32)
+    with tuned(flh, FLH_SBL=cfg):
+        got, want = run_dot(flh, orc, gpu, fmt, w, rows, cols, xs, mode="iq8", y0=y0)
+        assert np.array_equal(bits(got), bits(want))
+
+
+@pytest.mark.parametrize("fmt", [Q5_0, IQ2_XXS, IQ3_XXS])
+def test_sbl_b32_matches_register_kernel(flh, orc, gpu, fmt):
+    """The LDS-staged and register kernels give the same bits (and both the
+    oracle's) on a 14336x4096 matrix and on an expert picked by an id slot."""
+    say("sbl b32 vs register", fmt)
+    rng = np.random.default_rng(900 + fmt)
+    rows, cols = 14336, 4096
+    w = sane_rows(fmt, rows, cols, rng)
+    xs = activations(1, cols, rng, outliers=True)
+    outs = []
+    for cfg in ("1", "0"):
+        with tuned(flh, FLH_SBL=cfg):
+            got, want = run_dot(flh, orc, gpu, fmt, w, rows, cols, xs, mode=B32_MODE[fmt])
+            assert np.array_equal(bits(got), bits(want)), cfg
+            outs.append(got)
+    assert np.array_equal(bits(outs[0]), bits(outs[1]))
+    r, ne = 96, 3
+    we = sane_rows(fmt, r * ne, cols, rng)
+    got, want = run_dot(flh, orc, gpu, fmt, we, r, cols, xs, mode=B32_MODE[fmt], id_slot=1,
+                        estride=r * flh.row_bytes(fmt, cols))
+    assert np.array_equal(bits(got), bits(want))
