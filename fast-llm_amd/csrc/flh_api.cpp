@@ -500,7 +500,9 @@ int flh_router_moe_dot(int fmt, const void * w, uint64_t estride, uint32_t rows,
         f.rt_norm = norm;
         f.rt_scale = scale;
         f.rt_gates = gates;
-        int rc = launch_moe_mfma(fmt, f, s);
+        int rc = FLH_ERR_UNSUPPORTED;
+        if (ntok == 1 && tune().sbl) rc = launch_moe_sbl(fmt, f, s);
+        if (rc == FLH_ERR_UNSUPPORTED) rc = launch_moe_mfma(fmt, f, s);
         if (rc == FLH_ERR_UNSUPPORTED) rc = launch_moe_kstream(fmt, f, s);
         if (rc != FLH_ERR_UNSUPPORTED) return rc;
     }

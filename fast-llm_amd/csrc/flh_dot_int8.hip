@@ -699,7 +699,10 @@ int launch_moe_i8k(int fmt, const MoeArgs & a, hipStream_t s) {
         return set_error(FLH_ERR_UNSUPPORTED, "moe i8k: cols must be a multiple of 256, <= 16384");
     if (a.rows == 0 || a.ntok == 0 || a.top_k == 0) return FLH_OK;
     if (a.ntok * a.top_k > 256) return set_error(FLH_ERR_UNSUPPORTED, "moe: ntok*top_k > 256");
-    int rc = launch_moe_mfma(fmt, a, s);
+    int rc = FLH_ERR_UNSUPPORTED;
+    if (a.ntok == 1 && tune().sbl) rc = launch_moe_sbl(fmt, a, s);     // one token: superblock per lane
+    if (rc != FLH_ERR_UNSUPPORTED) return rc;
+    rc = launch_moe_mfma(fmt, a, s);
     if (rc != FLH_ERR_UNSUPPORTED) return rc;
     rc = launch_moe_kstream(fmt, a, s);
     if (rc != FLH_ERR_UNSUPPORTED) return rc;

@@ -436,9 +436,17 @@ __device__ __forceinline__ void sbl_iq(const uint8_t * st, uint32_t lane, uint32
 // dynamic LDS = W * 2 * slot (rings) + the staged activation (rounded to
 // 1 KiB) + W * (TB + 256) bytes (fold terms and old y values) + the IQ
 // codebook (2 KiB).
-template <int FMT, bool FUSE, int W>
-__global__ __launch_bounds__(64 * W) void k_dot_sbl(DotArgs a, uint32_t rpc, uint32_t ni, uint32_t slot, uint32_t pre) {
+//
+// MOE: one token's routed experts (ROUTER_SEL fused or ids given):
+// blockIdx.y is the (token, slot) pair p, whose y is m.y + p * ystride and
+// whose activation is column p (per-slot x) or the token's; the pair's
+// expert is known only after routing, so its weight requests wait for that,
+// while the y and activation DMAs go out first.
+template <int FMT, bool FUSE, int W, bool MOE = false>
+__global__ __launch_bounds__(64 * W) void k_dot_sbl(DotArgs a, uint32_t rpc, uint32_t ni, uint32_t slot, uint32_t pre,
+                                                    MoeArgs m) {
     static_assert(FMT == FMT_Q4_K || !FUSE, "only Q4_K fuses the quantisation");
+    static_assert(!MOE || !FUSE, "the routed launch reads a ready appendix");
     static_assert(FMT == FMT_Q4_K || FMT == FMT_Q8_0 || FMT == FMT_Q5_0 || FMT == FMT_IQ2_XXS ||
                   FMT == FMT_IQ3_XXS, "Q4_K or a 32-weight-block format");
     constexpr bool Q8 = FMT != FMT_Q4_K;                          // 4 blocks of 32 weights per lane
@@ -462,7 +470,12 @@ __global__ __launch_bounds__(64 * W) void k_dot_sbl(DotArgs a, uint32_t rpc, uin
     uint8_t * T = xs + xs_bytes + wave * (TB + 256);              // fold terms of this wave
     uint8_t * Y = T + TB;                                         // [64] old y values of this wave
     const uint32_t grid = lds_off(xs + xs_bytes + W * (TB + 256)); // IQ codebook (2 KiB)
-    const uint8_t * w = a.w + (a.id_slot ? (size_t)(*a.id_slot) * a.estride : 0);
+    if constexpr (MOE) {
+        const uint32_t p = blockIdx.y;
+        a.x = m.x + (size_t)(m.x_per_slot ? p : p / m.top_k) * m.xstride;
+        a.y = m.y + (size_t)p * m.ystride;
+    }
+    const uint8_t * w = MOE ? m.w : a.w + (a.id_slot ? (size_t)(*a.id_slot) * a.estride : 0);
     const uint64_t cb = (uint64_t)rpc * P * B;                    // bytes of a full chunk
     const uint8_t * xk = (const uint8_t *)a.x + xqk_off(cols);
     uint32_t ops = 0;                                             // memory operations issued by this wave
@@ -527,6 +540,18 @@ __global__ __launch_bounds__(64 * W) void k_dot_sbl(DotArgs a, uint32_t rpc, uin
         }
     }
     const uint32_t x_mark = ops;
+    if constexpr (MOE) {
+        // the pair's expert (routing waits for every load issued so far,
+        // which the activation wait below needs anyway)
+        __shared__ uint32_t rids[8];
+        const uint32_t * ids = moe_route(m, rids);
+        const uint32_t e = ids[blockIdx.y];
+        if (e >= m.n_expert) {                                    // nothing routed to this pair
+            WAIT_VM(0);                                           // no DMA may land after exit
+            return;
+        }
+        w += (size_t)e * m.estride;
+    }
     // Every wave's activation requests enter the CU's memory queue before any
     // weight request: served in order, they would otherwise wait behind the
     // CU's whole initial weight burst (~150 KB, several us at a CU's share of
@@ -813,7 +838,7 @@ int launch_dot_sbl(int fmt, const DotArgs & a, bool fuse, hipStream_t s) {
     if (G > C) G = C;
     auto go = [&](auto kern) {
         (void)hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smb);
-        hipLaunchKernelGGL(kern, dim3(G), dim3(64 * W), smb, s, a, rpc, ni, slot, pre);
+        hipLaunchKernelGGL(kern, dim3(G), dim3(64 * W), smb, s, a, rpc, ni, slot, pre, MoeArgs{});
         return hip_check(hipGetLastError(), "k_dot_sbl launch");
     };
     auto unfused = [&](auto fmt_tag) {
@@ -833,6 +858,49 @@ int launch_dot_sbl(int fmt, const DotArgs & a, bool fuse, hipStream_t s) {
     if (W == 8) return go(k_dot_sbl<FMT_Q4_K, true, 8>);
     if (W == 6) return go(k_dot_sbl<FMT_Q4_K, true, 6>);
     return go(k_dot_sbl<FMT_Q4_K, true, 4>);
+}
+
+// One token's top-k experts (Q4_K, ready q8_K appendix): grid (Gx, top_k),
+// the dense launch's workgroups shared evenly by the pairs.  Measured at
+// Mixtral shapes (8 experts, top 2, batch 1) against the four-lanes-per-
+// superblock grouped kernel: gate/up 2 x 28672x4096 with ROUTER_SEL fused
+// 26.5 -> 25.0 us, down 2 x 4096x14336 16.2 -> 15.8 us.  The routed gate/up
+// still trails a dense 57344x4096 launch (22.3 us) by the routing itself:
+// no weight request can leave before the logits are loaded and ranked.
+int launch_moe_sbl(int fmt, const MoeArgs & m, hipStream_t s) {
+    if (fmt != FMT_Q4_K || m.ntok != 1 || m.top_k == 0 || m.top_k > 8 || (m.cols & 255) || m.rows == 0)
+        return FLH_ERR_UNSUPPORTED;
+    const uint32_t nsb = m.cols >> 8;
+    if (nsb < 1 || nsb > 64) return FLH_ERR_UNSUPPORTED;
+    if ((uintptr_t)m.w & 15 || (m.estride & 15)) return FLH_ERR_UNSUPPORTED;
+    const Tune & t = tune();
+    const uint32_t P = nsb, B = 144, rpc = 64 / P;
+    const uint32_t ni = (rpc * P * B + 1023) / 1024, slot = ni * 1024;
+    uint32_t W = t.sbl_w ? t.sbl_w : nsb > 16 ? 8 : 4;
+    const uint32_t pre = t.sbl_pre == 0xFFu ? W : t.sbl_pre ? t.sbl_pre : W / 2;
+    const size_t lim = lds_limit() - 64;                          // the routed ids (static LDS)
+    while (W > 4 && sbl_smem(false, false, W, slot, nsb) > lim) W -= 2;
+    const size_t smb = sbl_smem(false, false, W, slot, nsb);
+    if (smb > lim || (W != 8 && W != 6 && W != 4)) return FLH_ERR_UNSUPPORTED;
+    const uint32_t C = (m.rows + rpc - 1) / rpc;
+    const uint32_t wpc = t.sbl_wpc ? t.sbl_wpc : 1;
+    uint32_t G = (uint32_t)num_cus() * wpc;
+    if (t.sbl_gmax && G > t.sbl_gmax) G = t.sbl_gmax;
+    uint32_t gx = (G + m.top_k - 1) / m.top_k;
+    if (gx > C) gx = C;
+    DotArgs a{};
+    a.w = m.w;
+    a.rows = m.rows;
+    a.cols = m.cols;
+    a.nx = 1;
+    auto go = [&](auto kern) {
+        (void)hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smb);
+        hipLaunchKernelGGL(kern, dim3(gx, m.top_k), dim3(64 * W), smb, s, a, rpc, ni, slot, pre, m);
+        return hip_check(hipGetLastError(), "k_dot_sbl (moe) launch");
+    };
+    if (W == 8) return go(k_dot_sbl<FMT_Q4_K, false, 8, true>);
+    if (W == 6) return go(k_dot_sbl<FMT_Q4_K, false, 6, true>);
+    return go(k_dot_sbl<FMT_Q4_K, false, 4, true>);
 }
 
 }  // namespace flh

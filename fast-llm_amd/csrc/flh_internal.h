@@ -117,6 +117,7 @@ int launch_dequant(int fmt, const uint8_t * w, uint32_t rows, uint32_t cols,
 int launch_moe_i8k(int fmt, const MoeArgs & a, hipStream_t s);
 // LDS-staged grouped expert kernel; FLH_ERR_UNSUPPORTED if it does not fit
 int launch_moe_kstream(int fmt, const MoeArgs & a, hipStream_t s);
+int launch_moe_sbl(int fmt, const MoeArgs & a, hipStream_t s);
 int launch_router_sel(const float * logits, uint32_t ntok, uint32_t n_expert,
                       uint32_t top_k, uint32_t norm, float scale,
                       uint32_t * ids, float * gates, hipStream_t s);

@@ -284,3 +284,47 @@ def test_grouped_expert_dot_k_halves_bitwise(flh, orc, gpu, ntok, rows, cols, pe
     from util import tuned
     with tuned(flh, FLH_MFMA_TUNE="2,0,1"):
         grouped_dot_case(flh, orc, gpu, Q4_K, ntok, rows, cols, per_slot)
+
+
+@pytest.mark.parametrize("cfg", ["1", "1,8,1,0", "1,4,2,0,255"])
+@pytest.mark.parametrize("rows,cols,per_slot,E,K", [(300, 1024, False, 8, 2), (97, 14336, True, 8, 2),
+                                                    (1001, 4096, False, 64, 8), (64, 2048, True, 16, 4)])
+def test_moe_one_token_superblock_kernel(flh, orc, gpu, cfg, rows, cols, per_slot, E, K):
+    """One token (the superblock-per-lane routed launch, one workgroup row per
+    pair): bitwise against the oracle and against the grouped streaming kernel
+    (FLH_SBL=0); a pair whose id is out of range leaves its y untouched."""
+    from util import tuned
+    say("moe one token", cfg, rows, cols, per_slot, E, K)
+    rng = np.random.default_rng(rows + cols + E * K)
+    ids = rng.choice(E, size=K, replace=False).astype(np.uint32)
+    ids[K - 1] = E + 3                                   # not routed
+    rb = row_bytes(Q4_K, cols)
+    estride = rows * rb
+    w = sane_rows(Q4_K, rows * E, cols, rng)
+    nx = K if per_slot else 1
+    xs = activations(nx, cols, rng, outliers=True)
+    st = col_stride_floats(cols)
+    buf = np.zeros(nx * st, dtype=np.float32)
+    for p in range(nx):
+        buf[p * st:p * st + cols] = xs[p]
+    dx = flh.DeviceBuffer.from_array(buf, gpu)
+    flh.act_q8(dx, cols, gpu, nx=nx, xstride=st)
+    ref_x = orc.act_q8_cols(xs, st)
+    y0 = rng.standard_normal(K * rows).astype(np.float32)
+    want = y0.copy()
+    for k in range(K - 1):
+        xi = k if per_slot else 0
+        yk = want[k * rows:(k + 1) * rows]
+        orc.stream_dot(Q4_K, w, rows, cols, ref_x[xi * st:(xi + 1) * st], yk, id_slot=int(ids[k]),
+                       estride=estride, threads=8)
+        want[k * rows:(k + 1) * rows] = yk
+    dw = flh.DeviceBuffer.from_array(w, gpu)
+    di = flh.DeviceBuffer.from_array(ids, gpu)
+    outs = []
+    for c in (cfg, "0"):
+        with tuned(flh, FLH_SBL=c):
+            dy = flh.DeviceBuffer.from_array(y0, gpu)
+            flh.moe_dot(Q4_K, dw, estride, rows, cols, di, 1, K, E, dx, st, per_slot, dy, rows, gpu)
+            outs.append(dy.download(np.float32, y0.size, gpu))
+    assert np.array_equal(bits(outs[0]), bits(want))
+    assert np.array_equal(bits(outs[1]), bits(want))
