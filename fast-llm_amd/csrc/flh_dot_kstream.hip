@@ -331,7 +331,7 @@ template <int FMT, int NX, bool FUSE>
 static int ks_launch(const DotArgs & a, hipStream_t s) {
     const uint32_t nsb = a.cols >> 8;
     const Tune & t = tune();
-    if ((FMT == FMT_Q4_K || (FMT == FMT_Q8_0 && !FUSE)) && NX == 1 && t.sbl) {
+    if ((FMT == FMT_Q4_K || ((FMT == FMT_Q8_0 || FMT == FMT_Q6_K) && !FUSE)) && NX == 1 && t.sbl) {
         const int rc = launch_dot_sbl(FMT, a, FUSE, s);
         if (rc != FLH_ERR_UNSUPPORTED) return rc;
     }

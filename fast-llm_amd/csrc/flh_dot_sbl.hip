@@ -204,6 +204,98 @@ __device__ __forceinline__ void sbl_q4k(const u32x4a (&w)[9], const XQ4 & X, int
     im = mi;
 }
 
+// ---- Q6_K: a lane takes one 210-byte superblock (ql[128], qh[64], int8
+// scales[16], d), 2-byte aligned in LDS: 54 dwords are read from the aligned
+// address below and shifted into place (W[i] = bytes 4i .. 4i + 3).
+__device__ __forceinline__ void lds_ld_q6k(uint32_t p, uint32_t (&W)[53]) {
+    const uint32_t a4 = p & ~3u, sh = p & 3u;
+    u32x2v R[27];
+    asm volatile("ds_read2_b32 %0, %27 offset1:1\n\tds_read2_b32 %1, %27 offset0:2 offset1:3\n\t"
+                 "ds_read2_b32 %2, %27 offset0:4 offset1:5\n\tds_read2_b32 %3, %27 offset0:6 offset1:7\n\t"
+                 "ds_read2_b32 %4, %27 offset0:8 offset1:9\n\tds_read2_b32 %5, %27 offset0:10 offset1:11\n\t"
+                 "ds_read2_b32 %6, %27 offset0:12 offset1:13\n\tds_read2_b32 %7, %27 offset0:14 offset1:15\n\t"
+                 "ds_read2_b32 %8, %27 offset0:16 offset1:17\n\tds_read2_b32 %9, %27 offset0:18 offset1:19\n\t"
+                 "ds_read2_b32 %10, %27 offset0:20 offset1:21\n\tds_read2_b32 %11, %27 offset0:22 offset1:23\n\t"
+                 "ds_read2_b32 %12, %27 offset0:24 offset1:25\n\tds_read2_b32 %13, %27 offset0:26 offset1:27\n\t"
+                 "ds_read2_b32 %14, %27 offset0:28 offset1:29\n\tds_read2_b32 %15, %27 offset0:30 offset1:31\n\t"
+                 "ds_read2_b32 %16, %27 offset0:32 offset1:33\n\tds_read2_b32 %17, %27 offset0:34 offset1:35\n\t"
+                 "ds_read2_b32 %18, %27 offset0:36 offset1:37\n\tds_read2_b32 %19, %27 offset0:38 offset1:39\n\t"
+                 "ds_read2_b32 %20, %27 offset0:40 offset1:41\n\tds_read2_b32 %21, %27 offset0:42 offset1:43\n\t"
+                 "ds_read2_b32 %22, %27 offset0:44 offset1:45\n\tds_read2_b32 %23, %27 offset0:46 offset1:47\n\t"
+                 "ds_read2_b32 %24, %27 offset0:48 offset1:49\n\tds_read2_b32 %25, %27 offset0:50 offset1:51\n\t"
+                 "ds_read2_b32 %26, %27 offset0:52 offset1:53\n\ts_waitcnt lgkmcnt(0)"
+                 : "=&v"(R[0]), "=&v"(R[1]), "=&v"(R[2]), "=&v"(R[3]), "=&v"(R[4]), "=&v"(R[5]), "=&v"(R[6]),
+                   "=&v"(R[7]), "=&v"(R[8]), "=&v"(R[9]), "=&v"(R[10]), "=&v"(R[11]), "=&v"(R[12]), "=&v"(R[13]),
+                   "=&v"(R[14]), "=&v"(R[15]), "=&v"(R[16]), "=&v"(R[17]), "=&v"(R[18]), "=&v"(R[19]),
+                   "=&v"(R[20]), "=&v"(R[21]), "=&v"(R[22]), "=&v"(R[23]), "=&v"(R[24]), "=&v"(R[25]), "=&v"(R[26])
+                 : "v"(a4) : "memory");
+#pragma unroll
+    for (int i = 0; i < 53; ++i) {
+        const uint32_t lo = (i & 1) ? R[i >> 1].y : R[i >> 1].x;
+        const uint32_t hi = ((i + 1) & 1) ? R[(i + 1) >> 1].y : R[(i + 1) >> 1].x;
+        W[i] = alignb(hi, lo, sh);
+    }
+}
+
+// A lane's activation superblock for Q6_K: 64 dwords of int8, the 16
+// sub-block sums (int16 bsums), and d.
+struct XQ6 {
+    u32x4a q[16];
+    int bs[16];
+    float dk;
+};
+
+__device__ __forceinline__ void load_xq6(const uint8_t * xb, XQ6 & X) {
+    XQ4 t;
+    load_xq4(xb, t);                                              // the int8 and d
+#pragma unroll
+    for (int i = 0; i < 16; ++i) X.q[i] = t.q[i];
+    X.dk = t.dk;
+    const u32x4a b0 = lds_ld128(xb + 16), b1 = lds_ld128(xb + 32);
+    const uint32_t w[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+    for (int t2 = 0; t2 < 8; ++t2) {
+        X.bs[2 * t2] = (int)(int16_t)(w[t2] & 0xFFFFu);
+        X.bs[2 * t2 + 1] = (int)(int16_t)(w[t2] >> 16);
+    }
+}
+
+// Exact iacc of one Q6_K superblock (fl_dot_i8k_q6_K, src/runtime/quants.h:
+// 563-594): sum over the 16 sub-blocks of sc_i * (idot_i - 32 * bsum_i), as
+// sum sc_i * idot_i - 32 * sum sc_i * bsum_i.  Element 128h + 32g + l takes
+// the low (g < 2) or high nibble of ql[64h + 32(g & 1) + l] and bits 2g, 2g + 1
+// of qh[32h + l]; every product fits 24 bits (|idot| <= 16 * 63 * 128).
+__device__ __forceinline__ int sbl_q6k(const uint32_t (&W)[53], const XQ6 & X) {
+    int dsum[16];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                int sa = 0;
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj) {
+                    const int j = 4 * k + jj;
+                    const uint32_t ql = W[16 * h + 8 * (g & 1) + j], qh = W[32 + 8 * h + j];
+                    const uint32_t v = ((g < 2 ? ql : ql >> 4) & 0x0F0F0F0Fu) | (((qh >> (2 * g)) & 0x03030303u) << 4);
+                    const int xi = 32 * h + 8 * g + j;
+                    const u32x4a xq = X.q[xi >> 2];
+                    const uint32_t xv = (xi & 3) == 0 ? xq.x : (xi & 3) == 1 ? xq.y : (xi & 3) == 2 ? xq.z : xq.w;
+                    sa = dot4((int)v, (int)xv, sa);
+                }
+                dsum[8 * h + 2 * g + k] = sa;
+            }
+    int acc = 0, bacc = 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int sc = (int)(int8_t)((W[48 + (i >> 2)] >> (8 * (i & 3))) & 0xFFu);
+        acc += __mul24(sc, dsum[i]);
+        bacc += __mul24(sc, X.bs[i]);
+    }
+    return acc - 32 * bacc;
+}
+
 // ---- Q8_0: a lane takes half of a 256-weight unit, 4 blocks of 34 bytes
 // (136 bytes, 8-byte aligned); the activation's q8_1 blocks are staged as
 // 48-byte slots (d at +12, the 32 int8 at +16, 16-byte aligned).
@@ -446,13 +538,15 @@ template <int FMT, bool FUSE, int W, bool MOE = false>
 __global__ __launch_bounds__(64 * W) void k_dot_sbl(DotArgs a, uint32_t rpc, uint32_t ni, uint32_t slot, uint32_t pre,
                                                     MoeArgs m) {
     static_assert(FMT == FMT_Q4_K || !FUSE, "only Q4_K fuses the quantisation");
+    static_assert(FMT != FMT_Q6_K || !MOE, "the routed launch is Q4_K");
     static_assert(!MOE || !FUSE, "the routed launch reads a ready appendix");
-    static_assert(FMT == FMT_Q4_K || FMT == FMT_Q8_0 || FMT == FMT_Q5_0 || FMT == FMT_IQ2_XXS ||
-                  FMT == FMT_IQ3_XXS, "Q4_K or a 32-weight-block format");
-    constexpr bool Q8 = FMT != FMT_Q4_K;                          // 4 blocks of 32 weights per lane
+    static_assert(FMT == FMT_Q4_K || FMT == FMT_Q6_K || FMT == FMT_Q8_0 || FMT == FMT_Q5_0 ||
+                  FMT == FMT_IQ2_XXS || FMT == FMT_IQ3_XXS, "a K format or a 32-weight-block format");
+    constexpr bool Q6 = FMT == FMT_Q6_K;
+    constexpr bool Q8 = FMT != FMT_Q4_K && !Q6;                   // 4 blocks of 32 weights per lane
     constexpr bool IQ = FMT == FMT_IQ2_XXS || FMT == FMT_IQ3_XXS;
     // bytes of a lane's weights (IQ: half a superblock's share)
-    constexpr uint32_t B = FMT == FMT_Q4_K ? 144 : FMT == FMT_Q8_0 ? 136 : FMT == FMT_Q5_0 ? 88
+    constexpr uint32_t B = FMT == FMT_Q4_K ? 144 : Q6 ? 210 : FMT == FMT_Q8_0 ? 136 : FMT == FMT_Q5_0 ? 88
                                                  : iq_block_bytes(FMT) / 2;
     constexpr uint32_t TB = Q8 ? 4096 : 1024;                     // fold-term bytes of a wave
     extern __shared__ __attribute__((aligned(16))) uint8_t sm[];
@@ -610,9 +704,10 @@ __global__ __launch_bounds__(64 * W) void k_dot_sbl(DotArgs a, uint32_t rpc, uin
     SBL_STAMP(6);
     lds_barrier();
     SBL_STAMP(1);
-    typename std::conditional<Q8, XQ8, XQ4>::type X;
+    typename std::conditional<Q8, XQ8, typename std::conditional<Q6, XQ6, XQ4>::type>::type X;
     int xsum[4] = {0, 0, 0, 0};                                   // Q5_0: the blocks' activation sums
     if constexpr (Q8) load_xq8(xs + 4 * SBL_X8 * (lane % P), X);
+    else if constexpr (Q6) load_xq6(xs + SBL_XS * (lane % nsb), X);
     else load_xq4(xs + SBL_XS * (lane % nsb), X);
     if constexpr (FMT == FMT_Q5_0) {
 #pragma unroll
@@ -634,7 +729,7 @@ __global__ __launch_bounds__(64 * W) void k_dot_sbl(DotArgs a, uint32_t rpc, uin
     if (nck > 1) { issue(1, ring + slot); mark[1] = ops; }
 
     const uint32_t fr = lane >> 2, fk = lane & 3;                 // fold lane: row r0 + fr, accumulator fk
-    // Q4_K rows of 4, 8 or 16 superblocks fold in registers (DPP)
+    // K-format rows of 4, 8 or 16 superblocks fold in registers (DPP)
     const bool dppf = !Q8 && (nsb == 4 || nsb == 8 || nsb == 16);
     for (uint32_t i = 0; i < nck; ++i) {
         const uint32_t sl = i & 1u;
@@ -675,27 +770,39 @@ __global__ __launch_bounds__(64 * W) void k_dot_sbl(DotArgs a, uint32_t rpc, uin
                     lds_st64(T + (4 * r + k) * CS + 8 * pos, u32x2a{__float_as_uint(f[k]), __float_as_uint((float)id[k])});
             }
         } else {
-            u32x4a wv[9];
-            lds_ld_q4k(st + B * lane, wv);
-            int ia, im;
-            sbl_q4k(wv, X, ia, im);
+            // Q4_K: terms (d * dk) * iacc and -(dmin * dk) * imin; Q6_K:
+            // (d * dk) * iacc, its second product -0.0 * 0 (adding it leaves
+            // every value, signed zeros included, unchanged)
+            int ia, im = 0;
+            float f1, f2 = -0.f;
+            if constexpr (Q6) {
+                uint32_t W6[53];
+                lds_ld_q6k(lds_off(st) + B * lane, W6);
+                ia = sbl_q6k(W6, X);
+                f1 = h2f(W6[52] & 0xFFFFu) * X.dk;
+            } else {
+                u32x4a wv[9];
+                lds_ld_q4k(st + B * lane, wv);
+                sbl_q4k(wv, X, ia, im);
+                f1 = h2f(wv[0].x & 0xFFFFu) * X.dk;
+                f2 = -(h2f(wv[0].x >> 16) * X.dk);
+            }
             if (i + 2 < nck) {                                    // refill this stage
                 issue(i + 2, st);
                 mark[sl] = ops;
             }
-            const float f1 = h2f(wv[0].x & 0xFFFFu) * X.dk;
-            const float f2 = -(h2f(wv[0].x >> 16) * X.dk);
             if (dppf) {
                 // Rows of 4, 8 or 16 lanes sit inside one 16-lane DPP row:
                 // accumulator k runs down positions k, k + 4, ... by shifting
                 // the partial chain four lanes per step; after nsb / 4 steps
                 // the row's last four lanes hold a0..a3.
                 const float fi = (float)ia, fm = (float)im;
-                float acc = fmaf(f2, fm, fmaf(f1, fi, 0.f));
+                auto term = [&](float prev) { return Q6 ? fmaf(f1, fi, prev) : fmaf(f2, fm, fmaf(f1, fi, prev)); };
+                float acc = term(0.f);
                 for (uint32_t q = 4; q < nsb; q += 4) {
                     const float prev = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(acc), 0x114,
                                                                                   0xF, 0xF, false));
-                    acc = fmaf(f2, fm, fmaf(f1, fi, prev));
+                    acc = term(prev);
                 }
                 const float s01 = acc + qx1f(acc);
                 const float tot = s01 + qx2f(s01);
@@ -797,10 +904,11 @@ static size_t sbl_smem(bool q8, bool iq, uint32_t W, uint32_t slot, uint32_t nsb
 int launch_dot_sbl(int fmt, const DotArgs & a, bool fuse, hipStream_t s) {
     const bool iq = fmt == FMT_IQ2_XXS || fmt == FMT_IQ3_XXS;
     const bool q8 = fmt == FMT_Q8_0 || fmt == FMT_Q5_0 || iq;     // 32-weight blocks
-    if ((fmt != FMT_Q4_K && !q8) || (q8 && fuse) || a.nx != 1 || (a.cols & 255) || a.rows == 0)
+    const bool q6 = fmt == FMT_Q6_K;
+    if ((fmt != FMT_Q4_K && !q6 && !q8) || ((q8 || q6) && fuse) || a.nx != 1 || (a.cols & 255) || a.rows == 0)
         return FLH_ERR_UNSUPPORTED;
     const uint32_t nsb = a.cols >> 8, P = q8 ? 2 * nsb : nsb;
-    const uint32_t B = fmt == FMT_Q4_K ? 144 : fmt == FMT_Q8_0 ? 136 : fmt == FMT_Q5_0 ? 88
+    const uint32_t B = fmt == FMT_Q4_K ? 144 : q6 ? 210 : fmt == FMT_Q8_0 ? 136 : fmt == FMT_Q5_0 ? 88
                                               : iq_block_bytes(fmt) / 2;
     if (nsb < 1 || P > 64) return FLH_ERR_UNSUPPORTED;
     // chunks are whole rows moved in 16-byte pieces (IQ rows: nsb % 8 == 0)
@@ -824,6 +932,12 @@ int launch_dot_sbl(int fmt, const DotArgs & a, bool fuse, hipStream_t s) {
     //    early (14336x4096 Q5_0 15.2 -> 11.9 us, IQ2_XXS 16.6 -> 12.2,
     //    IQ3_XXS 18.3 -> 13.5 against 4 waves).
     if (fuse && !t.sbl_w && (uint64_t)a.rows * nsb > (1u << 17)) return FLH_ERR_UNSUPPORTED;
+    // Q6_K: its 6-bit decode is VALU-heavy and a 12-14 KB chunk leaves room
+    // for 4 waves only, so the four-lanes-per-superblock kernel stays faster
+    // unless the matrix is large enough for the streaming rate to dominate
+    // (measured: vocab 128256x4096 66.3 vs 68.6 us; 14336x4096 12.0 vs 10.8,
+    // 4096x14336 13.9 vs 12.1, 4096x4096 5.8 either way)
+    if (q6 && !t.sbl_w && (uint64_t)a.rows * nsb < (1u << 20)) return FLH_ERR_UNSUPPORTED;
     const uint32_t wdef = fuse || nsb > 16 || (q8 && fmt != FMT_Q8_0) ? 8 : 4;
     uint32_t W = t.sbl_w ? t.sbl_w : wdef;
     const uint32_t pre = t.sbl_pre == 0xFFu ? W : t.sbl_pre ? t.sbl_pre : q8 ? W : W / 2;
@@ -848,6 +962,7 @@ int launch_dot_sbl(int fmt, const DotArgs & a, bool fuse, hipStream_t s) {
         return go(k_dot_sbl<F, false, 4>);
     };
     switch (fmt) {
+        case FMT_Q6_K: return unfused(std::integral_constant<int, FMT_Q6_K>());
         case FMT_Q8_0: return unfused(std::integral_constant<int, FMT_Q8_0>());
         case FMT_Q5_0: return unfused(std::integral_constant<int, FMT_Q5_0>());
         case FMT_IQ2_XXS: return unfused(std::integral_constant<int, FMT_IQ2_XXS>());

@@ -164,3 +164,49 @@ def test_sbl_b32_matches_register_kernel(flh, orc, gpu, fmt):
     got, want = run_dot(flh, orc, gpu, fmt, we, r, cols, xs, mode=B32_MODE[fmt], id_slot=1,
                         estride=r * flh.row_bytes(fmt, cols))
     assert np.array_equal(bits(got), bits(want))
+
+
+Q6_K = 4
+
+
+# (explicit wave counts: by default the launcher leaves Q6_K below vocab size
+# to the streaming kernel)
+@pytest.mark.parametrize("cfg", ["1,4,1,0", "1,8,1,0", "1,4,2,0,255", "1,6,1,3,1"])
+@pytest.mark.parametrize("rows,cols", [(7, 2048), (33, 4096), (1001, 4096), (41, 6144), (13, 10240), (9, 14336),
+                                       (70, 16384), (4096, 4096)])
+def test_sbl_q6_k_bitwise(flh, orc, gpu, cfg, rows, cols):
+    """Q6_K x q8_K with one 210-byte superblock per lane (2-byte aligned in
+    LDS): bitwise fl_dot_i8k_q6_K (src/runtime/quants.h:563-594) for rows of
+    8 and 16 superblocks (folded by DPP), 24 (parked in lane order) and 40,
+    56, 64 (one row per chunk, chains parked contiguously)."""
+    say("sbl q6_K", cfg, rows, cols)
+    rng = np.random.default_rng(rows * 3 + cols)
+    w = sane_rows(Q6_K, rows, cols, rng)
+    xs = activations(1, cols, rng, outliers=True)
+    y0 = rng.standard_normal(rows).astype(np.float32)
+    with tuned(flh, FLH_SBL=cfg):
+        got, want = run_dot(flh, orc, gpu, Q6_K, w, rows, cols, xs, y0=y0)
+        assert np.array_equal(bits(got), bits(want))
+
+
+def test_sbl_q6_k_matches_streaming_kernel(flh, orc, gpu):
+    """Vocab-head Q6_K 65536x4096 (large enough for the default launch to
+    take the superblock-per-lane kernel): it and the four-lanes-per-superblock
+    kernel give the oracle's bits; and a zero activation gives +0.0 exactly
+    (the parked second product adds nothing)."""
+    say("sbl q6_K vs kstream")
+    rng = np.random.default_rng(66)
+    rows, cols = 65536, 4096
+    w = sane_rows(Q6_K, rows, cols, rng)
+    xs = activations(1, cols, rng, outliers=True)
+    outs = []
+    for cfg in ("1", "0"):
+        with tuned(flh, FLH_SBL=cfg):
+            got, want = run_dot(flh, orc, gpu, Q6_K, w, rows, cols, xs)
+            assert np.array_equal(bits(got), bits(want)), cfg
+            outs.append(got)
+    assert np.array_equal(bits(outs[0]), bits(outs[1]))
+    with tuned(flh, FLH_SBL="1,4,1,0"):
+        got, want = run_dot(flh, orc, gpu, Q6_K, w[:9 * flh.row_bytes(Q6_K, cols)], 9, cols,
+                            np.zeros((1, cols), np.float32))
+        assert np.array_equal(bits(got), bits(want))
