@@ -678,20 +678,15 @@ __global__ __launch_bounds__(64 * W) void k_dot_sbl(DotArgs a, uint32_t rpc, uin
         uint8_t * q81 = (uint8_t *)a.x + xq_off(cols);
         uint8_t * q8k = (uint8_t *)a.x + xqk_off(cols);
         const uint8_t * xf = ring + slot + 16 * lane;
-        // One item at a time, loop kept rolled (unrolled over 8 items with the
-        // appendix writer inlined it was ~16 KB of code, run once per wave).
-        // Its cost, ~1 us at 4096 columns, is VALU throughput: every
-        // workgroup quantises the whole column, 2 waves per SIMD x 2 items x
-        // ~75 instructions.
-#pragma unroll 1
-        for (uint32_t j = 0; j < nfi; ++j) {
-            const uint32_t s = wave + W * j;
-            const u32x4a r = lds_ld128(xf + 1024 * j);
-            const float v[4] = {__uint_as_float(r.x), __uint_as_float(r.y), __uint_as_float(r.z),
-                                __uint_as_float(r.w)};
-            const float amax = __uint_as_float(umax64(__float_as_uint(absmax4(v))));
-            const float d = amax / 127.f;
-            const float id = amax > 0.f ? 127.f / amax : 0.f;
+        // Two items per pass, loop kept rolled (unrolled with the appendix
+        // writer inlined it was ~16 KB of code, run once per wave).  The two
+        // items' maxima share one reduction: v_permlane32_swap leaves item
+        // a's partials in lanes 0-31 and item b's in lanes 32-63, DPP and
+        // v_permlane16_swap finish both, and one division sequence gives both
+        // scales (each lane's values are computed exactly as for one item).
+        // Every workgroup quantises the whole column: VALU throughput, 2
+        // waves per SIMD x 2 items at 4096 columns.
+        auto store_item = [&](const float (&v)[4], uint32_t s, float d, float id) {
             const uint32_t pk = quant4(v, id);
             const int s16 = sum4i(dot4((int)pk, 0x01010101, 0));     // 16-element block sum
             uint8_t * xb = xs + SBL_XS * s;
@@ -699,6 +694,31 @@ __global__ __launch_bounds__(64 * W) void k_dot_sbl(DotArgs a, uint32_t rpc, uin
             if ((lane & 3) == 0) lds_st16(xb + 16 + 2 * (lane >> 2), (uint32_t)s16);
             if (lane == 0) lds_st32(xb + 12, __float_as_uint(d));
             if (s % G == b) write_appendices(v, lane, s, q81, q8k, cols);   // each block by one workgroup
+        };
+#pragma unroll 1
+        for (uint32_t j = 0; j < nfi; j += 2) {
+            const bool two = j + 1 < nfi;                         // wave-uniform
+            const uint32_t sa = wave + W * j;
+            u32x4a ra = lds_ld128_nw(xf + 1024 * j), rb = lds_ld128_nw(xf + 1024 * (two ? j + 1 : j));
+            u32x4a r2 = ra, r3 = rb;
+            lds_wait4(ra, rb, r2, r3);
+            const float va[4] = {__uint_as_float(ra.x), __uint_as_float(ra.y), __uint_as_float(ra.z),
+                                 __uint_as_float(ra.w)};
+            const float vb[4] = {__uint_as_float(rb.x), __uint_as_float(rb.y), __uint_as_float(rb.z),
+                                 __uint_as_float(rb.w)};
+            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(absmax4(va)), __float_as_uint(absmax4(vb)),
+                                                             false, false);
+            uint32_t m = umax8(max((uint32_t)sw[0], (uint32_t)sw[1]));
+            m = max(m, (uint32_t)rmir((int)m));                   // each 16-lane row
+            const auto rs = __builtin_amdgcn_permlane16_swap(m, m, false, false);
+            const float amax = __uint_as_float(max((uint32_t)rs[0], (uint32_t)rs[1]));   // a: lanes 0-31, b: 32-63
+            const float dv = amax / 127.f;
+            const float iv = amax > 0.f ? 127.f / amax : 0.f;
+            store_item(va, sa, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dv), 0)),
+                       __int_as_float(__builtin_amdgcn_readlane(__float_as_int(iv), 0)));
+            if (two)
+                store_item(vb, sa + W, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dv), 32)),
+                           __int_as_float(__builtin_amdgcn_readlane(__float_as_int(iv), 32)));
         }
     }
     SBL_STAMP(6);
