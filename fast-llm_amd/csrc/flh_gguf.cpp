@@ -36,6 +36,7 @@
 #include <vector>
 #include "../../include/fastllm_hip.h"
 #include "flh_status.h"
+#include "flh_internal.h"
 
 using flh::set_error;
 using flh::hip_check;
@@ -334,13 +335,11 @@ struct Stager {
 };
 Stager g_stage;
 
+// host threads copying a tensor into the pinned staging ring (FLH_GGUF_THREADS,
+// read at flh_init; 0: the hardware's, at most 16)
 unsigned copy_threads() {
-    static const unsigned n = [] {
-        const char * e = getenv("FLH_GGUF_THREADS");
-        unsigned v = e ? (unsigned)strtoul(e, nullptr, 0) : std::thread::hardware_concurrency();
-        return std::max(1u, std::min(v, 16u));
-    }();
-    return n;
+    const unsigned v = flh::tune().gguf_threads ? flh::tune().gguf_threads : std::thread::hardware_concurrency();
+    return std::max(1u, std::min(v, 16u));
 }
 
 // memcpy of n bytes split over the copy threads (each part faults its own

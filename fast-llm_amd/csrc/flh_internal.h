@@ -84,14 +84,16 @@ struct Tune {
     // (0 = default; max_wgs caps the grid, for tests of long per-wave chunk
     // lists; pre = waves requesting a chunk before the activation lands, 0: half, 255: all)
     uint32_t sbl = 1, sbl_w = 0, sbl_wpc = 0, sbl_gmax = 0, sbl_pre = 0;
+    uint32_t gguf_threads = 0;          // FLH_GGUF_THREADS: host copy threads of an upload (0: all, <= 16)
 };
 const Tune & tune();
 void load_tune();
 
 int launch_dot_kstream(int fmt, const DotArgs & a, hipStream_t s);
-// Q4_K x q8_K, one column, one superblock per lane (flh_dot_sbl.hip); fuse:
-// ACT_Q8 of the fp32 column in the same launch.  FLH_ERR_UNSUPPORTED
-// (nothing launched) if the shape does not fit its plan.
+// One column, one superblock (K formats) or four 32-weight blocks per lane
+// (flh_dot_sbl.hip): Q4_K (fuse: ACT_Q8 of the fp32 column in the same
+// launch), Q6_K, Q8_0, Q5_0, IQ2_XXS, IQ3_XXS.  FLH_ERR_UNSUPPORTED (nothing
+// launched) if the shape does not fit its plan or another kernel is faster.
 int launch_dot_sbl(int fmt, const DotArgs & a, bool fuse, hipStream_t s);
 // largest dynamic LDS of one workgroup on the current device
 size_t lds_limit();
