@@ -493,6 +493,29 @@ __device__ __forceinline__ void iq_runs(uint32_t grid, const uint32_t (&G)[8], u
     }
 }
 
+// Negation masks of the lane's 16 runs (sign field l of group m's w1) from
+// the 128-entry table at LDS address tab (entry s7: the byte masks of
+// iq_sign8(s7)'s bits 0-3 and 4-7), in one LDS round trip.
+__device__ __forceinline__ void iq_negs(uint32_t tab, const uint32_t (&w1)[4], u32x2a (&N)[16]) {
+    uint32_t ad[16];
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+        for (int l = 0; l < 4; ++l) ad[4 * m + l] = tab + 8 * ((w1[m] >> (7 * l)) & 127u);
+    asm volatile("ds_read_b64 %0, %16\n\tds_read_b64 %1, %17\n\tds_read_b64 %2, %18\n\tds_read_b64 %3, %19\n\t"
+                 "ds_read_b64 %4, %20\n\tds_read_b64 %5, %21\n\tds_read_b64 %6, %22\n\tds_read_b64 %7, %23\n\t"
+                 "ds_read_b64 %8, %24\n\tds_read_b64 %9, %25\n\tds_read_b64 %10, %26\n\tds_read_b64 %11, %27\n\t"
+                 "ds_read_b64 %12, %28\n\tds_read_b64 %13, %29\n\tds_read_b64 %14, %30\n\tds_read_b64 %15, %31\n\t"
+                 "s_waitcnt lgkmcnt(0)"
+                 : "=&v"(N[0]), "=&v"(N[1]), "=&v"(N[2]), "=&v"(N[3]), "=&v"(N[4]), "=&v"(N[5]), "=&v"(N[6]),
+                   "=&v"(N[7]), "=&v"(N[8]), "=&v"(N[9]), "=&v"(N[10]), "=&v"(N[11]), "=&v"(N[12]), "=&v"(N[13]),
+                   "=&v"(N[14]), "=&v"(N[15])
+                 : "v"(ad[0]), "v"(ad[1]), "v"(ad[2]), "v"(ad[3]), "v"(ad[4]), "v"(ad[5]), "v"(ad[6]), "v"(ad[7]),
+                   "v"(ad[8]), "v"(ad[9]), "v"(ad[10]), "v"(ad[11]), "v"(ad[12]), "v"(ad[13]), "v"(ad[14]),
+                   "v"(ad[15])
+                 : "memory");
+}
+
 // Group dots of the codebook formats: the signed grid magnitudes (run l takes
 // sign field l of w1, bit j negating element 8l + j) against the q8_1 quants;
 // factor db * d_x with db = (d * (0.5 + s)) * 0.25 (IQ2) or * 0.5 (IQ3), s =
@@ -502,20 +525,23 @@ __device__ __forceinline__ void sbl_iq(const uint8_t * st, uint32_t lane, uint32
                                        int (&id)[4]) {
     uint32_t dbits, G[8], S[4];
     lds_ld_iqh<FMT>(st, lane, dbits, G, S);
-    u32x2a E[16];
+    uint32_t w1s[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) w1s[m] = FMT == FMT_IQ2_XXS ? G[2 * m + 1] : S[m];
+    u32x2a E[16], N[16];
     iq_runs<FMT>(grid, G, E);
+    iq_negs(grid + 2048, w1s, N);
     const float d = h2f(dbits);
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
-        const uint32_t w1 = FMT == FMT_IQ2_XXS ? G[2 * m + 1] : S[m];
+        const uint32_t w1 = w1s[m];
         const u32x4a xa = X.q[2 * m], xb = X.q[2 * m + 1];
         const uint32_t XV[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
         int s0 = 0, s1 = 0;
 #pragma unroll
         for (int l = 0; l < 4; ++l) {
-            const uint32_t sg = iq_sign8(w1 >> (7 * l));
-            s0 = dot4((int)iq_apply(E[4 * m + l].x, iq_neg4(sg)), (int)XV[2 * l], s0);
-            s1 = dot4((int)iq_apply(E[4 * m + l].y, iq_neg4(sg >> 4)), (int)XV[2 * l + 1], s1);
+            s0 = dot4((int)iq_apply(E[4 * m + l].x, N[4 * m + l].x), (int)XV[2 * l], s0);
+            s1 = dot4((int)iq_apply(E[4 * m + l].y, N[4 * m + l].y), (int)XV[2 * l + 1], s1);
         }
         id[m] = s0 + s1;
         f[m] = iq_db(FMT, d, w1) * X.dx[m];
@@ -563,7 +589,7 @@ __global__ __launch_bounds__(64 * W) void k_dot_sbl(DotArgs a, uint32_t rpc, uin
     const uint32_t xs_bytes = ((Q8 ? nsb * 8 * SBL_X8 : nsb * SBL_XS) + 1023u) & ~1023u;
     uint8_t * T = xs + xs_bytes + wave * (TB + 256);              // fold terms of this wave
     uint8_t * Y = T + TB;                                         // [64] old y values of this wave
-    const uint32_t grid = lds_off(xs + xs_bytes + W * (TB + 256)); // IQ codebook (2 KiB)
+    const uint32_t grid = lds_off(xs + xs_bytes + W * (TB + 256)); // IQ codebook (2 KiB), sign masks (1 KiB)
     if constexpr (MOE) {
         const uint32_t p = blockIdx.y;
         a.x = m.x + (size_t)(m.x_per_slot ? p : p / m.top_k) * m.xstride;
@@ -600,6 +626,11 @@ __global__ __launch_bounds__(64 * W) void k_dot_sbl(DotArgs a, uint32_t rpc, uin
                                                  LPTR(xs + xs_bytes + W * (TB + 256) + 1024 * t), 16, 0, 0);
                 ++ops;
             }
+        }
+        // sign-mask table after it (published by the staging barrier)
+        if (tid < 128) {
+            const uint32_t sg = iq_sign8(tid);
+            lds_st64(xs + xs_bytes + W * (TB + 256) + 2048 + 8 * tid, u32x2a{iq_neg4(sg), iq_neg4(sg >> 4)});
         }
     }
 
@@ -918,7 +949,7 @@ __global__ __launch_bounds__(64 * W) void k_dot_sbl(DotArgs a, uint32_t rpc, uin
 
 static size_t sbl_smem(bool q8, bool iq, uint32_t W, uint32_t slot, uint32_t nsb) {
     const size_t xs = ((q8 ? nsb * 8 * SBL_X8 : nsb * SBL_XS) + 1023u) & ~(size_t)1023;
-    return (size_t)W * 2 * slot + xs + (size_t)W * ((q8 ? 4096 : 1024) + 256) + (iq ? 2048 : 0);
+    return (size_t)W * 2 * slot + xs + (size_t)W * ((q8 ? 4096 : 1024) + 256) + (iq ? 3072 : 0);
 }
 
 int launch_dot_sbl(int fmt, const DotArgs & a, bool fuse, hipStream_t s) {
