@@ -188,19 +188,20 @@ __device__ __forceinline__ int iq_val(int fmt, const uint8_t * b, int ib, uint32
 // expert order (first strictly greater wins); expf; sum in ascending order;
 // divide; top-k by first maximum; optional renormalisation by the sum of the
 // chosen weights; scale.  Lane 0 writes ids[0..top_k) and, when gates is not
-// null, gates[0..top_k) (generic pointers: global or LDS).
+// null, gates[0..top_k) (generic pointers: global or LDS).  Every broadcast
+// reads one uniformly indexed lane: v_readlane (scalar), not an LDS permute.
 __device__ __forceinline__ void router_token_wave(const float * lg, uint32_t n_expert, uint32_t top_k,
                                                   uint32_t norm, float scale, uint32_t lane, uint32_t * ids,
                                                   float * gates) {
     const float l = lane < n_expert ? lg[lane] : 0.f;
     float mx = -1e30f;
     for (uint32_t i = 0; i < n_expert; ++i) {
-        const float li = __shfl(l, (int)i);
+        const float li = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(l), (int)i));
         if (li > mx) mx = li;
     }
     float w = lane < n_expert ? expf(l - mx) : 0.f;
     float sum = 0.f;
-    for (uint32_t i = 0; i < n_expert; ++i) sum += __shfl(w, (int)i);
+    for (uint32_t i = 0; i < n_expert; ++i) sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), (int)i));
     w /= sum;
     bool taken = lane >= n_expert;
     float tsum = 0.f;
@@ -211,8 +212,8 @@ __device__ __forceinline__ void router_token_wave(const float * lg, uint32_t n_e
         float bw = -1.f;
         uint32_t best = 0;
         for (uint32_t i = 0; i < n_expert; ++i) {
-            const float wi = __shfl(w, (int)i);
-            const bool ti = __shfl((int)taken, (int)i) != 0;
+            const float wi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), (int)i));
+            const bool ti = __builtin_amdgcn_readlane((int)taken, (int)i) != 0;
             if (!ti && wi > bw) { bw = wi; best = i; }
         }
         if (lane == best) taken = true;
