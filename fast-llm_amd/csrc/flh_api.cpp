@@ -135,6 +135,20 @@ static int dispatch_dot(int fmt, const DotArgs & a, int fast, uint32_t i8_mask, 
     return launch_dot_fast_f32(fmt, a, s);
 }
 
+// Grouped expert dots of the 32-weight-block formats (Q8_0, Q5_0, IQ2_XXS,
+// IQ3_XXS x q8_1): the routed superblock-per-lane launch, one workgroup row
+// per (token, slot) pair (the reference runs these per pair too,
+// src/model/decoder.cpp:941-996).
+static int launch_moe_b32(int fmt, const MoeArgs & a, hipStream_t s) {
+    if (a.rows == 0 || a.ntok == 0 || a.top_k == 0) return FLH_OK;
+    if (a.ntok * a.top_k > 256) return set_error(FLH_ERR_UNSUPPORTED, "moe: ntok*top_k > 256");
+    const int rc = launch_moe_sbl(fmt, a, s);
+    if (rc == FLH_ERR_UNSUPPORTED)
+        return set_error(rc, "moe: this format needs 16-byte aligned weights, x and expert stride, and rows of "
+                             "at most 8192 columns (IQ: a multiple of 2048)");
+    return rc;
+}
+
 // freeze()-style validation of a whole task table (nothing is launched on error)
 static int validate_table(const flh_task * t, uint32_t n) {
     if (n && !t) return set_error(FLH_ERR_ARG, "null task table");
@@ -467,15 +481,16 @@ int flh_moe_dot(int fmt, const void * w, uint64_t estride, uint32_t rows, uint32
                 const float * x, uint32_t xstride, uint32_t x_per_slot, float * y, uint32_t ystride,
                 void * stream) {
     if (int rc = need_init()) return rc;
-    if (fmt != FLH_FMT_Q4_K && fmt != FLH_FMT_Q6_K)
-        return set_error(FLH_ERR_UNSUPPORTED, "moe_dot: K formats (q8_K path) only");
+    if (fmt < FLH_FMT_Q8_0 || fmt > FLH_FMT_IQ3_XXS)
+        return set_error(FLH_ERR_UNSUPPORTED, "moe_dot: quantized weight formats only");
     if (cols % 256) return set_error(FLH_ERR_ARG, "moe_dot: cols not a multiple of 256");
     if (!w || !ids || !x || !y || n_expert == 0) return set_error(FLH_ERR_ARG, "moe_dot: null argument");
     if (estride < (uint64_t)rows * flh_row_bytes(fmt, cols) || (estride & 3) || ((uintptr_t)w & 3))
         return set_error(FLH_ERR_ARG, "moe_dot: expert stride smaller than one expert or misaligned");
     MoeArgs a{(const uint8_t *)w, estride, ids, x, y, rows, cols, ntok, top_k, n_expert, xstride, ystride,
               x_per_slot};
-    return launch_moe_i8k(fmt, a, (hipStream_t)stream);
+    if (fmt == FLH_FMT_Q4_K || fmt == FLH_FMT_Q6_K) return launch_moe_i8k(fmt, a, (hipStream_t)stream);
+    return launch_moe_b32(fmt, a, (hipStream_t)stream);
 }
 
 int flh_router_moe_dot(int fmt, const void * w, uint64_t estride, uint32_t rows, uint32_t cols,
@@ -483,8 +498,9 @@ int flh_router_moe_dot(int fmt, const void * w, uint64_t estride, uint32_t rows,
                        float scale, uint32_t * ids, float * gates, const float * x, uint32_t xstride,
                        uint32_t x_per_slot, float * y, uint32_t ystride, void * stream) {
     if (int rc = need_init()) return rc;
-    if (fmt != FLH_FMT_Q4_K && fmt != FLH_FMT_Q6_K)
-        return set_error(FLH_ERR_UNSUPPORTED, "router_moe_dot: K formats (q8_K path) only");
+    if (fmt < FLH_FMT_Q8_0 || fmt > FLH_FMT_IQ3_XXS)
+        return set_error(FLH_ERR_UNSUPPORTED, "router_moe_dot: quantized weight formats only");
+    const bool kf = fmt == FLH_FMT_Q4_K || fmt == FLH_FMT_Q6_K;
     if (cols % 256) return set_error(FLH_ERR_ARG, "router_moe_dot: cols not a multiple of 256");
     if (!w || !logits || !ids || !gates || !x || !y || n_expert == 0 || top_k == 0 || top_k > n_expert)
         return set_error(FLH_ERR_ARG, "router_moe_dot: null argument or top_k outside 1..n_expert");
@@ -502,13 +518,13 @@ int flh_router_moe_dot(int fmt, const void * w, uint64_t estride, uint32_t rows,
         f.rt_scale = scale;
         f.rt_gates = gates;
         int rc = FLH_ERR_UNSUPPORTED;
-        if (ntok == 1 && tune().sbl) rc = launch_moe_sbl(fmt, f, s);
-        if (rc == FLH_ERR_UNSUPPORTED) rc = launch_moe_mfma(fmt, f, s);
-        if (rc == FLH_ERR_UNSUPPORTED) rc = launch_moe_kstream(fmt, f, s);
+        if ((ntok == 1 || !kf) && tune().sbl) rc = launch_moe_sbl(fmt, f, s);
+        if (rc == FLH_ERR_UNSUPPORTED && kf) rc = launch_moe_mfma(fmt, f, s);
+        if (rc == FLH_ERR_UNSUPPORTED && kf) rc = launch_moe_kstream(fmt, f, s);
         if (rc != FLH_ERR_UNSUPPORTED) return rc;
     }
     if (int rc = launch_router_sel(logits, ntok, n_expert, top_k, norm, scale, ids, gates, s)) return rc;
-    return launch_moe_i8k(fmt, a, s);
+    return kf ? launch_moe_i8k(fmt, a, s) : launch_moe_b32(fmt, a, s);
 }
 
 int flh_router_sel(const float * logits, uint32_t ntok, uint32_t n_expert, uint32_t top_k, uint32_t norm,

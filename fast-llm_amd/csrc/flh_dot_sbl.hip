@@ -564,7 +564,7 @@ template <int FMT, bool FUSE, int W, bool MOE = false>
 __global__ __launch_bounds__(64 * W) void k_dot_sbl(DotArgs a, uint32_t rpc, uint32_t ni, uint32_t slot, uint32_t pre,
                                                     MoeArgs m) {
     static_assert(FMT == FMT_Q4_K || !FUSE, "only Q4_K fuses the quantisation");
-    static_assert(FMT != FMT_Q6_K || !MOE, "the routed launch is Q4_K");
+    static_assert(FMT != FMT_Q6_K || !MOE, "Q6_K experts run on the grouped streaming kernel");
     static_assert(!MOE || !FUSE, "the routed launch reads a ready appendix");
     static_assert(FMT == FMT_Q4_K || FMT == FMT_Q6_K || FMT == FMT_Q8_0 || FMT == FMT_Q5_0 ||
                   FMT == FMT_IQ2_XXS || FMT == FMT_IQ3_XXS, "a K format or a 32-weight-block format");
@@ -668,7 +668,7 @@ __global__ __launch_bounds__(64 * W) void k_dot_sbl(DotArgs a, uint32_t rpc, uin
     if constexpr (MOE) {
         // the pair's expert (routing waits for every load issued so far,
         // which the activation wait below needs anyway)
-        __shared__ uint32_t rids[8];
+        __shared__ uint32_t rids[256];
         const uint32_t * ids = moe_route(m, rids);
         const uint32_t e = ids[blockIdx.y];
         if (e >= m.n_expert) {                                    // nothing routed to this pair
@@ -1026,33 +1026,41 @@ int launch_dot_sbl(int fmt, const DotArgs & a, bool fuse, hipStream_t s) {
     return go(k_dot_sbl<FMT_Q4_K, true, 4>);
 }
 
-// One token's top-k experts (Q4_K, ready q8_K appendix): grid (Gx, top_k),
-// the dense launch's workgroups shared evenly by the pairs.  Measured at
-// Mixtral shapes (8 experts, top 2, batch 1) against the four-lanes-per-
-// superblock grouped kernel: gate/up 2 x 28672x4096 with ROUTER_SEL fused
-// 26.5 -> 25.0 us, down 2 x 4096x14336 16.2 -> 15.8 us.  The routed gate/up
-// still trails a dense 57344x4096 launch (22.3 us) by the routing itself:
-// no weight request can leave before the logits are loaded and ranked.
+// Routed expert dots, one workgroup row per (token, slot) pair, the dense
+// launch's workgroups shared evenly by the pairs: Q4_K for one token (more
+// tokens share experts on the grouped kernels), the 32-weight-block formats
+// for any batch (no grouping; ntok * top_k <= 256).  Measured at Mixtral
+// shapes (8 experts, top 2, batch 1) against the four-lanes-per-superblock
+// grouped kernel: gate/up 2 x 28672x4096 with ROUTER_SEL fused 26.5 -> 25.0
+// us, down 2 x 4096x14336 16.2 -> 15.8 us.  The routed gate/up still trails a
+// dense 57344x4096 launch (22.3 us) by the routing itself: no weight request
+// can leave before the logits are loaded and ranked.
 int launch_moe_sbl(int fmt, const MoeArgs & m, hipStream_t s) {
-    if (fmt != FMT_Q4_K || m.ntok != 1 || m.top_k == 0 || m.top_k > 8 || (m.cols & 255) || m.rows == 0)
+    const bool iq = fmt == FMT_IQ2_XXS || fmt == FMT_IQ3_XXS;
+    const bool q8 = fmt == FMT_Q8_0 || fmt == FMT_Q5_0 || iq;     // 32-weight blocks
+    const uint32_t pairs = m.ntok * m.top_k;
+    if ((fmt != FMT_Q4_K && !q8) || (fmt == FMT_Q4_K && m.ntok != 1) || pairs == 0 || pairs > 256 ||
+        (m.cols & 255) || m.rows == 0)
         return FLH_ERR_UNSUPPORTED;
-    const uint32_t nsb = m.cols >> 8;
-    if (nsb < 1 || nsb > 64) return FLH_ERR_UNSUPPORTED;
+    const uint32_t nsb = m.cols >> 8, P = q8 ? 2 * nsb : nsb;
+    const uint32_t B = fmt == FMT_Q4_K ? 144 : fmt == FMT_Q8_0 ? 136 : fmt == FMT_Q5_0 ? 88 : iq_block_bytes(fmt) / 2;
+    if (nsb < 1 || P > 64 || ((P * B) & 15)) return FLH_ERR_UNSUPPORTED;
     if ((uintptr_t)m.w & 15 || (m.estride & 15)) return FLH_ERR_UNSUPPORTED;
+    if (q8 && (((uintptr_t)m.x & 15) || (m.xstride & 3))) return FLH_ERR_UNSUPPORTED;
     const Tune & t = tune();
-    const uint32_t P = nsb, B = 144, rpc = 64 / P;
+    const uint32_t rpc = 64 / P;
     const uint32_t ni = (rpc * P * B + 1023) / 1024, slot = ni * 1024;
-    uint32_t W = t.sbl_w ? t.sbl_w : nsb > 16 ? 8 : 4;
-    const uint32_t pre = t.sbl_pre == 0xFFu ? W : t.sbl_pre ? t.sbl_pre : W / 2;
-    const size_t lim = lds_limit() - 64;                          // the routed ids (static LDS)
-    while (W > 4 && sbl_smem(false, false, W, slot, nsb) > lim) W -= 2;
-    const size_t smb = sbl_smem(false, false, W, slot, nsb);
+    uint32_t W = t.sbl_w ? t.sbl_w : nsb > 16 || (q8 && fmt != FMT_Q8_0) ? 8 : 4;
+    const uint32_t pre = t.sbl_pre == 0xFFu ? W : t.sbl_pre ? t.sbl_pre : q8 ? W : W / 2;
+    const size_t lim = lds_limit() - 1088;                        // the routed ids (static LDS)
+    while (W > 4 && sbl_smem(q8, iq, W, slot, nsb) > lim) W -= 2;
+    const size_t smb = sbl_smem(q8, iq, W, slot, nsb);
     if (smb > lim || (W != 8 && W != 6 && W != 4)) return FLH_ERR_UNSUPPORTED;
     const uint32_t C = (m.rows + rpc - 1) / rpc;
     const uint32_t wpc = t.sbl_wpc ? t.sbl_wpc : 1;
     uint32_t G = (uint32_t)num_cus() * wpc;
     if (t.sbl_gmax && G > t.sbl_gmax) G = t.sbl_gmax;
-    uint32_t gx = (G + m.top_k - 1) / m.top_k;
+    uint32_t gx = (G + pairs - 1) / pairs;
     if (gx > C) gx = C;
     DotArgs a{};
     a.w = m.w;
@@ -1061,12 +1069,22 @@ int launch_moe_sbl(int fmt, const MoeArgs & m, hipStream_t s) {
     a.nx = 1;
     auto go = [&](auto kern) {
         (void)hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smb);
-        hipLaunchKernelGGL(kern, dim3(gx, m.top_k), dim3(64 * W), smb, s, a, rpc, ni, slot, pre, m);
+        hipLaunchKernelGGL(kern, dim3(gx, pairs), dim3(64 * W), smb, s, a, rpc, ni, slot, pre, m);
         return hip_check(hipGetLastError(), "k_dot_sbl (moe) launch");
     };
-    if (W == 8) return go(k_dot_sbl<FMT_Q4_K, false, 8, true>);
-    if (W == 6) return go(k_dot_sbl<FMT_Q4_K, false, 6, true>);
-    return go(k_dot_sbl<FMT_Q4_K, false, 4, true>);
+    auto routed = [&](auto fmt_tag) {
+        constexpr int F = decltype(fmt_tag)::value;
+        if (W == 8) return go(k_dot_sbl<F, false, 8, true>);
+        if (W == 6) return go(k_dot_sbl<F, false, 6, true>);
+        return go(k_dot_sbl<F, false, 4, true>);
+    };
+    switch (fmt) {
+        case FMT_Q8_0: return routed(std::integral_constant<int, FMT_Q8_0>());
+        case FMT_Q5_0: return routed(std::integral_constant<int, FMT_Q5_0>());
+        case FMT_IQ2_XXS: return routed(std::integral_constant<int, FMT_IQ2_XXS>());
+        case FMT_IQ3_XXS: return routed(std::integral_constant<int, FMT_IQ3_XXS>());
+        default: return routed(std::integral_constant<int, FMT_Q4_K>());
+    }
 }
 
 }  // namespace flh

@@ -241,8 +241,11 @@ int flh_dequant(int fmt, const void * w, uint32_t rows, uint32_t cols,
  * i = tok*top_k + slot with e = ids[i],
  *   y[i*ystride + r] += dot(W_e[r], x + xi*xstride),  W_e = w + e*estride,
  * xi = tok (x_per_slot = 0) or i (x_per_slot = 1).  Each expert's weights
- * are streamed once for all of its pairs; every output is bitwise equal to
- * the per-pair STREAM_DOT_IDX tile.  q8_K path (K formats). */
+ * are streamed once for all of its pairs (Q4_K, Q6_K: the q8_K int8 path);
+ * Q8_0, Q5_0, IQ2_XXS and IQ3_XXS run the q8_1 int8 path one pair at a time,
+ * as the reference's per-pair tiles do (16-byte aligned w, x and estride;
+ * cols a multiple of 256, at most 8192; IQ: a multiple of 2048).  Every
+ * output is bitwise equal to the per-pair STREAM_DOT_IDX tile. */
 int flh_moe_dot(int fmt, const void * w, uint64_t estride, uint32_t rows,
                 uint32_t cols, const uint32_t * ids, uint32_t ntok,
                 uint32_t top_k, uint32_t n_expert, const float * x,

@@ -328,3 +328,56 @@ def test_moe_one_token_superblock_kernel(flh, orc, gpu, cfg, rows, cols, per_slo
             outs.append(dy.download(np.float32, y0.size, gpu))
     assert np.array_equal(bits(outs[0]), bits(want))
     assert np.array_equal(bits(outs[1]), bits(want))
+
+
+Q8_0, Q5_0, IQ2_XXS, IQ3_XXS = 1, 2, 5, 6
+
+
+@pytest.mark.parametrize("fmt", [Q8_0, Q5_0, IQ2_XXS, IQ3_XXS])
+@pytest.mark.parametrize("ntok,per_slot,fused", [(1, False, False), (3, True, False), (5, False, True),
+                                                 (2, True, True)])
+def test_moe_block32_formats(flh, orc, gpu, fmt, ntok, per_slot, fused):
+    """Expert dots of the 32-weight-block formats (one workgroup row per
+    routed pair): every pair's y equals the oracle's STREAM_DOT_IDX tile on
+    the q8_1 int8 path, bit for bit, with the routing given as ids or fused
+    (ids then equal the reference router's; gates within the expf tolerance)."""
+    say("moe block32", fmt, ntok, per_slot, fused)
+    rng = np.random.default_rng(fmt * 11 + ntok * 3 + fused)
+    E, K, rows, cols = 8, 2, 200, 2048
+    logits, ids, gates = route(orc, ntok, E, K, rng)
+    estride = rows * row_bytes(fmt, cols)
+    w = sane_rows(fmt, rows * E, cols, rng)
+    nx = ntok * K if per_slot else ntok
+    xs = activations(nx, cols, rng, outliers=True)
+    st = col_stride_floats(cols)
+    buf = np.zeros(nx * st, dtype=np.float32)
+    for p in range(nx):
+        buf[p * st:p * st + cols] = xs[p]
+    dx = flh.DeviceBuffer.from_array(buf, gpu)
+    flh.act_q8(dx, cols, gpu, nx=nx, xstride=st)
+    ref_x = orc.act_q8_cols(xs, st)
+    y0 = rng.standard_normal(ntok * K * rows).astype(np.float32)
+    dy = flh.DeviceBuffer.from_array(y0, gpu)
+    dw = flh.DeviceBuffer.from_array(w, gpu)
+    if fused:
+        dl = flh.DeviceBuffer.from_array(logits, gpu)
+        di, dg = flh.DeviceBuffer(4 * ntok * K), flh.DeviceBuffer(4 * ntok * K)
+        flh.router_moe_dot(fmt, dw, estride, rows, cols, dl, ntok, E, K, 1, 1.0, di, dg, dx, st, per_slot, dy, rows,
+                           gpu)
+        assert np.array_equal(di.download(np.uint32, ntok * K, gpu), ids.ravel())
+        assert np.allclose(dg.download(np.float32, ntok * K, gpu), gates.ravel(), rtol=2e-6, atol=0)   # expf
+    else:
+        di = flh.DeviceBuffer.from_array(ids.ravel(), gpu)
+        flh.moe_dot(fmt, dw, estride, rows, cols, di, ntok, K, E, dx, st, per_slot, dy, rows, gpu)
+    got = dy.download(np.float32, y0.size, gpu)
+    want = y0.copy()
+    i8 = 0b11110 | (1 << IQ2_XXS) | (1 << IQ3_XXS)
+    for t in range(ntok):
+        for k in range(K):
+            i = t * K + k
+            xi = i if per_slot else t
+            yi = want[i * rows:(i + 1) * rows]
+            orc.stream_dot(fmt, w, rows, cols, ref_x[xi * st:(xi + 1) * st], yi, id_slot=int(ids[t, k]),
+                           estride=estride, i8_mask=i8, threads=8)
+            want[i * rows:(i + 1) * rows] = yi
+    assert np.array_equal(bits(got), bits(want))
