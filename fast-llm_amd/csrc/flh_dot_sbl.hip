@@ -1,6 +1,6 @@
-// flh_dot_sbl.hip -- single-column row-dots with one superblock (Q4_K x
-// q8_K) or four 32-weight blocks (Q8_0, Q5_0, IQ2_XXS, IQ3_XXS x q8_1) per
-// lane.
+// flh_dot_sbl.hip -- single-column row-dots with one superblock (Q4_K, Q6_K
+// x q8_K) or four 32-weight blocks (Q8_0, Q5_0, IQ2_XXS, IQ3_XXS x q8_1) per
+// lane, and the routed (MoE) form of the same launch.
 //
 // The streaming kernel of flh_dot_kstream.hip splits a superblock over four
 // lanes, which costs every quarter its own scale decode, a DPP reduction and
@@ -8,36 +8,37 @@
 // For one activation column the work per superblock is small enough that the
 // lane can take all of it:
 //
-//   * a CHUNK is rpc = floor(64 / nsb) whole rows (rpc * nsb superblocks,
-//     one per lane, row r = lane / nsb, position s = lane % nsb); its bytes
-//     go HBM -> LDS in 16-byte direct-to-LDS loads, each 1 KiB request of a
-//     wave fully coalesced;
-//   * a lane's activation superblock is the same for every chunk (position s),
-//     so its q8_K block (256 int8, 8 sub-block sums, d) lives in 73 VGPRs for
-//     the whole launch;
-//   * the lane computes the superblock's exact integer partials
-//     (iacc = sum_g sc_g * dot_g, imin = sum_g m_g * bsum_g) and the two
-//     reference factors d*dk and -(dmin*dk), parks them in a 1 KiB wave-local
-//     LDS area, and lanes (row, k) of the same wave fold accumulator k over
-//     positions k, k+4, ... with the reference's fmaf order, then
-//     (a0 + a1) + (a2 + a3) by DPP: bitwise fl_dot_i8k_q4_K
-//     (src/runtime/quants.h:538-561);
+//   * a CHUNK is rpc = floor(64 / P) whole rows (P lanes per row: nsb for the
+//     K formats, 2 nsb for 32-weight blocks; row r = lane / P, position
+//     lane % P); its bytes go HBM -> LDS in 16-byte direct-to-LDS loads, each
+//     1 KiB request of a wave fully coalesced;
+//   * a lane's activation block is the same for every chunk (its position),
+//     so it is read once from the workgroup's staged copy into registers
+//     (Q4_K: 256 int8, 8 sub-block sums, d: 73 VGPRs);
+//   * the lane computes its superblock's exact integer partials and the
+//     reference factors (Q4_K: iacc, imin with d*dk and -(dmin*dk),
+//     fl_dot_i8k_q4_K, src/runtime/quants.h:538-561; Q6_K: iacc with d*dk,
+//     :563-594); rows of 4, 8 or 16 superblocks fold in registers (the
+//     accumulator chains run down the row's lanes by DPP row shifts), other
+//     rows park the terms in a wave-local LDS area where lanes (row, k) run
+//     accumulator k over its terms in the reference's fmaf order; then
+//     (a0 + a1) + (a2 + a3) by DPP;
 //   * waves are independent after the activation is staged: no barrier per
 //     batch, each wave keeps two chunks in flight and refills a stage as soon
-//     as its reads are done.
+//     as its bytes are in registers.
 //
 // The 32-weight-block formats fold as fl_dot_i8_q8_0 (src/runtime/quants.h:
 // 438-466): block b of a row goes to accumulator b & 3, so a lane holding
-// blocks 4p .. 4p + 3 (position p; P = 2 * nsb lanes per row) contributes one
-// term to each accumulator.  Terms are parked so that each (row,
-// accumulator) chain is contiguous, and a fold lane reads 16 of them per LDS
-// round trip.  Q5_0 lanes take 88 contiguous bytes; IQ lanes take half a
-// superblock (its d, the half's group data and, for IQ3, its sign words),
-// and the codebook is staged in LDS once per workgroup.
+// blocks 4p .. 4p + 3 (position p) contributes one term to each accumulator.
+// Terms are parked so that each (row, accumulator) chain is contiguous, and a
+// fold lane reads 16 of them per LDS round trip.  Q5_0 lanes take 88
+// contiguous bytes; IQ lanes take half a superblock (its d, the half's group
+// data and, for IQ3, its sign words), with the codebook and a sign-mask table
+// staged in LDS once per workgroup.
 //
 // Chunks are dealt to workgroups first (chunk c -> workgroup c % G), so a
 // matrix with fewer chunks than waves still spreads over every CU.
-// With FUSE, the workgroup quantises the fp32 column itself (ACT_Q8,
+// With FUSE (Q4_K), the workgroup quantises the fp32 column itself (ACT_Q8,
 // src/runtime/quants.h:382-402): wave w takes superblocks w, w + W, ...; the
 // staged bytes are the q8_K block's, and workgroup s % G also writes both
 // appendices of superblock s, so memory ends up as after a separate ACT_Q8
