@@ -62,6 +62,10 @@ __device__ uint64_t g_sbl_trace[4096 * 8 * 8];
 extern "C" int flh_sbl_trace(uint64_t * host, size_t n) {
     return hipMemcpyFromSymbol(host, HIP_SYMBOL(g_sbl_trace), n * 8, 0, hipMemcpyDeviceToHost) == hipSuccess ? 0 : -2;
 }
+extern "C" int flh_sbl_trace_clear(void) {
+    static uint64_t zeros[4096 * 8 * 8];
+    return hipMemcpyToSymbol(HIP_SYMBOL(g_sbl_trace), zeros, sizeof(zeros), 0, hipMemcpyHostToDevice) == hipSuccess ? 0 : -2;
+}
 #else
 #define SBL_STAMP(k) do { } while (0)
 #endif
