@@ -15,7 +15,9 @@ Also reported (same JSON line):
   ops      -- per-op us and GB/s for every BASELINE config: Q8_0 4096^2,
               each Q4_K layer shape, Q6_K vocab head and down, spec-verify
               N in {2,4,8}, MoE top-2 of 8 at batch 1 and 8 (graph of R
-              launches rotating over weight copies, HIP events);
+              launches rotating over weight copies, HIP events); also Q5_0 /
+              IQ2_XXS / IQ3_XXS matvecs and the activation quantisers
+              (ACT_Q8 14336, RMSNORM -> ACT_Q8 4096);
   roofline -- the dominant kernel (Q4_K gate/up): algorithmic bytes per
               launch / average launch time vs the 8 TB/s HBM peak;
   cpu_baseline -- the reference CPU path on the host cores (oracle/_ref,
@@ -291,6 +293,20 @@ def main():
                 if fmt == Q5_0 and r == 4096:
                     cpu_in[f"q5_0_{r}x{c}"] = host_case(flh, s, Q5_0, ws[0], r, c, x, st, 1)
                 del ws
+        # the activation quantisers on their own (row f1): ACT_Q8 of the
+        # down projection's 14336-wide input (its own launch in the layer
+        # step) and RMSNORM -> ACT_Q8 of a 4096-wide hidden state in one launch
+        xq, _ = B.activation(14336, 1, 70, outliers=False)
+        us = B.time_graph(lambda i: flh.act_q8(xq, 14336, s), REPS)
+        op_entry("act_q8_14336", us, 14336 * 4 + 14336 // 32 * 36 + 14336 // 256 * 292,
+                 {"bytes": "fp32 x read + both appendices written (no weights)"})
+        xr, _ = B.activation(4096, 1, 71, outliers=False)
+        wn = B.buf(4096 * 4)
+        flh.fill_normal(wn, 4096, 72, s, mean=1.0, std=0.1)
+        yr, _ = B.activation(4096, 1, 73, outliers=False)
+        us = B.time_graph(lambda i: flh.rmsnorm_act_q8(xr, wn, yr, 4096, 1e-5, s), REPS)
+        op_entry("rmsnorm_act_q8_4096", us, 3 * 4096 * 4 + 4096 // 32 * 36 + 4096 // 256 * 292,
+                 {"bytes": "x and norm weight read, y and both appendices written (no matrix)"})
         # spec-verify small N
         for r, c in [(14336, 4096), (4096, 14336)]:
             nb = r * flh.row_bytes(Q4_K, c)
