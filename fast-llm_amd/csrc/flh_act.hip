@@ -55,11 +55,12 @@ __global__ __launch_bounds__(64) void k_silu_act_q8(const float * gate, const fl
 
 // RMSNORM of one column with (write_app) the ACT_Q8 of its output, one
 // workgroup of 16 waves: the sum of squares as thread partials (elements
-// 4t..4t+3, 4t+4096.. in order) -> wave DPP tree -> the 16 wave sums in
-// wave order; s = 1 / sqrtf(ss / n + eps) (correctly rounded sqrt and
-// division, as the reference's libm); then wave w quantises chunks w, w + 16,
-// ... with y = (x * s) * wnorm computed in the registers it quantises, so
-// the appendices hold ACT_Q8's bytes for the stored y.
+// 4t..4t+3, 4t+4096.. in order) -> a wave butterfly (every lane ends with the
+// same sum) -> the 16 wave sums in wave order; s = 1 / sqrtf(ss / n + eps)
+// (correctly rounded sqrt and division, as the reference's libm); then wave w
+// quantises chunks w, w + 16, ... with y = (x * s) * wnorm computed in the
+// registers it quantises, so the appendices hold ACT_Q8's bytes for the
+// stored y.
 __global__ __launch_bounds__(1024) void k_rmsnorm_act_q8(const float * x, const float * wn, float * y, uint32_t n,
                                                          float eps, int write_app) {
     __shared__ float part[16];
@@ -97,10 +98,67 @@ __global__ __launch_bounds__(1024) void k_rmsnorm_act_q8(const float * x, const 
         if (write_app) act_q8_lanes(v, lane, c, q81, q8k, n);
     }
 }
+// The same for n <= 16384, n % 4 == 0: thread t's elements (4t..4t+3,
+// 4t+4096.., the chunks wave, wave + 16, ... of the loop above) and their
+// norm weights come in as 16-B loads issued together, stay in registers
+// through the reduction, and every thread sums the 16 wave partials itself
+// (same order, so all hold the same s): one load round trip and one barrier.
+__global__ __launch_bounds__(1024) void k_rmsnorm_act_q8_reg(const float * x, const float * wn, float * y, uint32_t n,
+                                                             float eps, int write_app) {
+    __shared__ float part[16];
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    float4 xv[4], wv[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t e0 = 4 * tid + 4096 * k;
+        if (e0 < n) {
+            xv[k] = *(const float4 *)(x + e0);
+            wv[k] = *(const float4 *)(wn + e0);
+        }
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        if (4 * tid + 4096 * k < n) {
+            ss += xv[k].x * xv[k].x;
+            ss += xv[k].y * xv[k].y;
+            ss += xv[k].z * xv[k].z;
+            ss += xv[k].w * xv[k].w;
+        }
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) ss += __shfl_xor(ss, o);
+    if (lane == 0) part[wave] = ss;
+    __syncthreads();
+    float t = 0.f;
+#pragma unroll
+    for (int w = 0; w < 16; ++w) t += part[w];
+    const float s = 1.0f / sqrtf(t / (float)n + eps);
+    uint8_t * q81 = (uint8_t *)y + xq_off(n);
+    uint8_t * q8k = (uint8_t *)y + xqk_off(n);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t c = wave + 16 * k, e0 = c * 256 + 4 * lane;
+        if (c * 256 >= n) break;
+        float v[4] = {0.f, 0.f, 0.f, 0.f};
+        if (e0 < n) {
+            v[0] = xv[k].x * s * wv[k].x;
+            v[1] = xv[k].y * s * wv[k].y;
+            v[2] = xv[k].z * s * wv[k].z;
+            v[3] = xv[k].w * s * wv[k].w;
+            *(float4 *)(y + e0) = make_float4(v[0], v[1], v[2], v[3]);
+        }
+        if (write_app) act_q8_lanes(v, lane, c, q81, q8k, n);
+    }
+}
 int launch_rmsnorm_act_q8(const float * x, const float * wnorm, float * y, uint32_t n, float eps, bool app,
                           hipStream_t s) {
     if (n == 0) return FLH_OK;
-    hipLaunchKernelGGL(k_rmsnorm_act_q8, dim3(1), dim3(1024), 0, s, x, wnorm, y, n, eps, app ? 1 : 0);
+    const bool reg = n <= 16384 && n % 4 == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)wnorm & 15) == 0 &&
+                     ((uintptr_t)y & 15) == 0;
+    if (reg)
+        hipLaunchKernelGGL(k_rmsnorm_act_q8_reg, dim3(1), dim3(1024), 0, s, x, wnorm, y, n, eps, app ? 1 : 0);
+    else
+        hipLaunchKernelGGL(k_rmsnorm_act_q8, dim3(1), dim3(1024), 0, s, x, wnorm, y, n, eps, app ? 1 : 0);
     return hip_check(hipGetLastError(), "k_rmsnorm_act_q8 launch");
 }
 int launch_silu_act_q8(const float * gate, const float * up, float * h, uint32_t n, uint32_t ncol,
