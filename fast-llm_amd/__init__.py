@@ -151,6 +151,7 @@ _SIGS = {
     "flh_init": (_I, [_I]),
     "flh_device_info": (_I, [C.POINTER(_I), C.POINTER(_SZ), C.POINTER(_I), C.c_char_p, _SZ]),
     "flh_default_masks": (None, [C.POINTER(_U32), C.POINTER(_U32)]),
+    "flh_mfma_plan": (_I, [_U32, _U32, _U32, C.POINTER(_U32)]),
     "flh_row_bytes": (_U64, [_I, _U32]),
     "flh_x_alloc_bytes": (_SZ, [_U32]),
     "flh_arena_create": (_I, [_SZ, C.POINTER(_P)]),
@@ -258,6 +259,18 @@ def device_info() -> dict:
     check(lib().flh_device_info(C.byref(cus), C.byref(hbm), C.byref(ws), name, 128))
     return {"num_cus": cus.value, "hbm_bytes": hbm.value, "wave_size": ws.value,
             "arch": name.value.decode()}
+
+
+def mfma_plan(rows: int, cols: int, nx: int):
+    """The multi-column matrix-core kernel's plan for a Q4_K rows x cols
+    matrix with nx columns: {"kh", "xc", "nrb", "D"}, or None when that kernel
+    does not take the shape."""
+    out = (_U32 * 4)()
+    rc = lib().flh_mfma_plan(rows, cols, nx, out)
+    if rc == ERR_UNSUPPORTED:
+        return None
+    check(rc)
+    return {"kh": bool(out[0]), "xc": bool(out[1]), "nrb": out[2], "D": out[3]}
 
 
 class Stream:

@@ -218,6 +218,12 @@ int flh_device_info(int * num_cus, size_t * hbm_bytes, int * wave_size, char * n
     return FLH_OK;
 }
 
+int flh_mfma_plan(uint32_t rows, uint32_t cols, uint32_t nx, uint32_t * out) {
+    if (int rc = need_init()) return rc;
+    if (!out) return set_error(FLH_ERR_ARG, "null plan output");
+    return mfma_plan(rows, cols, nx, out);
+}
+
 void flh_default_masks(uint32_t * i8_mask, uint32_t * i8k_mask) {
     // kI8MaskCpuDefault / kI8KMaskCpuDefault (src/runtime/kernels.h:920,937)
     if (i8_mask) *i8_mask = (1u << FLH_FMT_Q8_0) | (1u << FLH_FMT_Q5_0) | (1u << FLH_FMT_Q4_K) | (1u << FLH_FMT_Q6_K);

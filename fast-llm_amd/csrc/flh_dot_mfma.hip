@@ -897,6 +897,27 @@ static int mf_plan_kh(uint32_t rows, uint32_t nsb, uint32_t G, uint32_t & nrb, i
     return smb > lim ? FLH_ERR_UNSUPPORTED : FLH_OK;
 }
 
+// The plan mf_launch<NC> takes for rows x cols with nx columns (NC as in
+// launch_dot_mfma): out = {K halves, activations in the chunk, nrb, D}.
+int mfma_plan(uint32_t rows, uint32_t cols, uint32_t nx, uint32_t * out) {
+    const uint32_t nsb = cols >> 8;
+    if (nsb == 0 || (cols & 255) || nsb > 64 || nx < 1 || nx > 16 || rows == 0) return FLH_ERR_UNSUPPORTED;
+    const uint32_t G = rows < (uint32_t)num_cus() ? rows : (uint32_t)num_cus();
+    uint32_t nrb;
+    int D;
+    bool kh, xc;
+    size_t smb;
+    const int rc = nx <= 4 ? mf_plan_kh<4>(rows, nsb, G, nrb, D, kh, smb, true, &xc)
+                 : nx <= 8 ? mf_plan_kh<8>(rows, nsb, G, nrb, D, kh, smb, true, &xc)
+                           : mf_plan_kh<16>(rows, nsb, G, nrb, D, kh, smb, true, &xc);
+    if (rc) return FLH_ERR_UNSUPPORTED;
+    out[0] = kh;
+    out[1] = xc;
+    out[2] = nrb;
+    out[3] = (uint32_t)D;
+    return FLH_OK;
+}
+
 template <int NC>
 static int mf_launch(const DotArgs & a, hipStream_t s) {
     const uint32_t nsb = a.cols >> 8;

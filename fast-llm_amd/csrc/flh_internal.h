@@ -108,6 +108,7 @@ int launch_dot_mfma(int fmt, const DotArgs & a, hipStream_t s);
 int launch_moe_mfma(int fmt, const MoeArgs & a, hipStream_t s);
 // fewest columns for which STREAM_DOT uses launch_dot_mfma
 uint32_t mfma_min_cols(uint32_t cols);
+int mfma_plan(uint32_t rows, uint32_t cols, uint32_t nx, uint32_t * out);
 int launch_dot_i8_q8_0(const DotArgs & a, hipStream_t s);         // Q8_0 x q8_1
 int launch_dot_i8_q5_0(const DotArgs & a, hipStream_t s);         // Q5_0 x q8_1
 int launch_dot_i8_k(int fmt, const DotArgs & a, hipStream_t s);   // Q4_K, Q6_K x q8_1

@@ -120,6 +120,14 @@ int flh_init(int device);
 int flh_device_info(int * num_cus, size_t * hbm_bytes, int * wave_size,
                     char * name, size_t name_len);
 
+/* Launch plan of the multi-column matrix-core dot for a Q4_K matrix of
+ * rows x cols with nx activation columns on this device: out[0] = K halves,
+ * out[1] = activations carried in the chunk DMA, out[2] = rows per batch,
+ * out[3] = ring depth.  FLH_ERR_UNSUPPORTED if that kernel does not take the
+ * shape.  No counterpart in the reference (whose multi-column kernel has one
+ * plan): a query for tests and tuning, launches nothing. */
+int flh_mfma_plan(uint32_t rows, uint32_t cols, uint32_t nx, uint32_t * out);
+
 /* Reference default dispatch masks for the CPU int8 path this backend
  * matches (src/runtime/kernels.h:920,937). */
 void flh_default_masks(uint32_t * i8_mask, uint32_t * i8k_mask);

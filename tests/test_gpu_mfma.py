@@ -60,6 +60,8 @@ def test_mfma_equals_streaming_kernel(flh, orc, gpu):
     say("mfma vs kstream")
     rng = np.random.default_rng(3)
     rows, cols, nx = 1000, 4096, 4
+    plan = flh.mfma_plan(rows, cols, nx)
+    assert not plan["xc"] and not plan["kh"], plan          # the activations fit whole
     w = sane_rows(Q4_K, rows, cols, rng)
     xs = activations(nx, cols, rng)
     got, want = run_dot(flh, orc, gpu, Q4_K, w, rows, cols, xs)
@@ -73,14 +75,19 @@ def test_mfma_equals_streaming_kernel(flh, orc, gpu):
 def test_mfma_activations_in_chunk_equals_k_halves(flh, orc, gpu, rows, cols, nx):
     """One 16-row tile per workgroup with activations too wide to stage
     whole: the activations-in-chunk mode (default) and K halves (FLH_MFMA_XC=0)
-    give the same bits, and both equal the oracle."""
+    give the same bits, and both equal the oracle.  The plan query confirms
+    which mode each run took."""
     say("mfma xc vs kh", rows, cols, nx)
+    plan = flh.mfma_plan(rows, cols, nx)
+    assert plan["xc"] and not plan["kh"] and plan["nrb"] == 16, plan
     rng = np.random.default_rng(rows + 11 * cols + nx)
     w = sane_rows(Q4_K, rows, cols, rng)
     xs = activations(nx, cols, rng, outliers=True)
     y0 = rng.standard_normal((nx - 1) * rows + rows).astype(np.float32)
     got, want = run_dot(flh, orc, gpu, Q4_K, w, rows, cols, xs, y0=y0)
     with tuned(flh, FLH_MFMA_XC=0):
+        plan = flh.mfma_plan(rows, cols, nx)
+        assert plan["kh"] and not plan["xc"], plan
         got2, _ = run_dot(flh, orc, gpu, Q4_K, w, rows, cols, xs, y0=y0)
     assert np.array_equal(bits(got), bits(want))
     assert np.array_equal(bits(got2), bits(got))
