@@ -118,6 +118,13 @@ static int dispatch_dot(int fmt, const DotArgs & a, int fast, uint32_t i8_mask, 
     if ((fmt == FLH_FMT_Q4_K || fmt == FLH_FMT_Q6_K) && ((i8k_mask >> fmt) & 1u))
         return launch_dot_i8k(fmt, a, s);
     if (fmt != FLH_FMT_F32 && ((i8_mask >> fmt) & 1u)) {
+        // 2..8 columns of the 32-weight-block formats: one weight pass on the
+        // superblock-per-lane layout where its LDS plan fits
+        if (a.nx >= 2 && tune().sbl &&
+            (fmt == FLH_FMT_Q8_0 || fmt == FLH_FMT_Q5_0 || fmt == FLH_FMT_IQ2_XXS || fmt == FLH_FMT_IQ3_XXS)) {
+            const int rc = launch_dot_sbl_nx(fmt, a, s);
+            if (rc != FLH_ERR_UNSUPPORTED) return rc;
+        }
         if (fmt == FLH_FMT_Q8_0) {
             const int rc = launch_dot_kstream(fmt, a, s);     // LDS-staged; register kernel otherwise
             return rc != FLH_ERR_UNSUPPORTED ? rc : launch_dot_i8_q8_0(a, s);

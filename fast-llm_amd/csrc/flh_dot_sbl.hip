@@ -952,6 +952,280 @@ __global__ __launch_bounds__(64 * W) void k_dot_sbl(DotArgs a, uint32_t rpc, uin
 #endif
 }
 
+// LDS of the several-column kernel: quants [NX][8 nsb][32], d words [NX][8 nsb]
+// (each rounded to 1 KiB: the staging DMAs write whole 1 KiB / 256 B rows),
+// per wave CG * rpc * 4 parked chains of 8 P + 16 bytes and 2 x 64 old y values
+__host__ __device__ inline uint32_t sbl_nx_xq_bytes(uint32_t NX, uint32_t nsb) { return (NX * nsb * 256 + 1023) & ~1023u; }
+__host__ __device__ inline uint32_t sbl_nx_xd_bytes(uint32_t NX, uint32_t nsb) { return (NX * nsb * 32 + 1023) & ~1023u; }
+__host__ __device__ inline uint32_t sbl_nx_tw(uint32_t CG, uint32_t rpc, uint32_t P) { return CG * rpc * 4 * (8 * P + 16) + 512; }
+
+// ---- several activation columns (32-weight-block formats) -----------------
+//
+// The lane layout of the single-column kernel (4 blocks of a row per lane),
+// with the weights decoded once per chunk into 32 int8 words and 4 weight
+// factors, then dotted with each column in turn.  The columns' q8_1 blocks
+// are staged as quants [NX][8][P][16 B] (piece q = 2 m + h of position
+// pos: half h of block 4 pos + m, so the lanes' reads of one piece are
+// adjacent and conflict-free) and the (d, s) words [NX][8 nsb]; a lane reads
+// its 128 quant bytes and 4 d of a column with one LDS round trip.  Terms (f, (float) idot) are parked per (column, row,
+// accumulator) chain for up to 4 columns at a time and folded as in the
+// single-column kernel: every column's output is the single-column result,
+// bit for bit (fl_dot_i8_q8_0 / _q5_0, src/runtime/quants.h:438-466; the IQ
+// factors of kernels_gpu.h:759-852).
+
+// Weights of the lane's 4 blocks as int8 words Q[8m + i] (the element order
+// of the q8_1 quants they meet) and factors wf[m] (the fp16 scale, or the IQ
+// group scale); Q5_0 values are the unshifted 5-bit ones (0..31).
+template <int FMT>
+__device__ __forceinline__ void nx_decode(const uint8_t * st, uint32_t lane, uint32_t grid, uint32_t (&Q)[32],
+                                          float (&wf)[4]) {
+    if constexpr (FMT == FMT_Q8_0) {
+        uint32_t D[34];
+        lds_ld_q8h(st + 136 * lane, D);
+        const uint32_t dw[4] = {D[0] & 0xFFFFu, D[8] >> 16, D[17] & 0xFFFFu, D[25] >> 16};
+        const int q0[4] = {0, 9, 17, 26};
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                Q[8 * m + i] = (m & 1) ? D[q0[m] + i] : alignb(D[q0[m] + i + 1], D[q0[m] + i], 2);
+            wf[m] = h2f(dw[m]);
+        }
+    } else if constexpr (FMT == FMT_Q5_0) {
+        uint32_t D[22];
+        lds_ld_q5h(st + 88 * lane, D);
+        const int o[4] = {0, 5, 11, 16};
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const bool odd = m & 1;
+            const uint32_t db = odd ? D[o[m]] >> 16 : D[o[m]] & 0xFFFFu;
+            const uint32_t qh = odd ? D[o[m] + 1] : alignb(D[o[m] + 1], D[o[m]], 2);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t q = odd ? D[o[m] + 2 + k] : alignb(D[o[m] + 2 + k], D[o[m] + 1 + k], 2);
+                Q[8 * m + k] = (q & 0x0F0F0F0Fu) | (spread4((qh >> (4 * k)) & 0xFu) << 4);
+                Q[8 * m + 4 + k] = ((q >> 4) & 0x0F0F0F0Fu) | (spread4((qh >> (16 + 4 * k)) & 0xFu) << 4);
+            }
+            wf[m] = h2f(db);
+        }
+    } else {
+        uint32_t dbits, G[8], S[4];
+        lds_ld_iqh<FMT>(st, lane, dbits, G, S);
+        uint32_t w1s[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) w1s[m] = FMT == FMT_IQ2_XXS ? G[2 * m + 1] : S[m];
+        u32x2a E[16], N[16];
+        iq_runs<FMT>(grid, G, E);
+        iq_negs(grid + 2048, w1s, N);
+        const float d = h2f(dbits);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+#pragma unroll
+            for (int l = 0; l < 4; ++l) {
+                Q[8 * m + 2 * l] = iq_apply(E[4 * m + l].x, N[4 * m + l].x);
+                Q[8 * m + 2 * l + 1] = iq_apply(E[4 * m + l].y, N[4 * m + l].y);
+            }
+            wf[m] = iq_db(FMT, d, w1s[m]);
+        }
+    }
+}
+
+// one column's quants of the lane (8 pieces of 16 bytes, piece q at
+// xq + q * qs) and its 4 d words (at xd), in one LDS round trip
+__device__ __forceinline__ void nx_load_col(const uint8_t * xq, uint32_t qs, const uint8_t * xd, u32x4a (&q)[8],
+                                            u32x4a & dv) {
+    const uint32_t a0 = lds_off(xq);
+    asm volatile("ds_read_b128 %0, %9\n\tds_read_b128 %1, %10\n\tds_read_b128 %2, %11\n\tds_read_b128 %3, %12\n\t"
+                 "ds_read_b128 %4, %13\n\tds_read_b128 %5, %14\n\tds_read_b128 %6, %15\n\tds_read_b128 %7, %16\n\t"
+                 "ds_read_b128 %8, %17\n\ts_waitcnt lgkmcnt(0)"
+                 : "=&v"(q[0]), "=&v"(q[1]), "=&v"(q[2]), "=&v"(q[3]), "=&v"(q[4]), "=&v"(q[5]), "=&v"(q[6]),
+                   "=&v"(q[7]), "=&v"(dv)
+                 : "v"(a0), "v"(a0 + qs), "v"(a0 + 2 * qs), "v"(a0 + 3 * qs), "v"(a0 + 4 * qs), "v"(a0 + 5 * qs),
+                   "v"(a0 + 6 * qs), "v"(a0 + 7 * qs), "v"(lds_off(xd))
+                 : "memory");
+}
+
+template <int FMT, int W, int CG>
+__global__ __launch_bounds__(64 * W) void k_dot_sbl_nx(DotArgs a, uint32_t rpc, uint32_t ni, uint32_t slot, uint32_t pre,
+                                                       uint32_t NX) {
+    static_assert(FMT == FMT_Q8_0 || FMT == FMT_Q5_0 || FMT == FMT_IQ2_XXS || FMT == FMT_IQ3_XXS,
+                  "a 32-weight-block format");
+    constexpr bool IQ = FMT == FMT_IQ2_XXS || FMT == FMT_IQ3_XXS;
+    constexpr uint32_t B = FMT == FMT_Q8_0 ? 136 : FMT == FMT_Q5_0 ? 88 : iq_block_bytes(FMT) / 2;
+    extern __shared__ __attribute__((aligned(16))) uint8_t sm[];
+    const uint32_t nsb = a.cols >> 8, rows = a.rows, cols = a.cols, nx = a.nx;
+    const uint32_t P = 2 * nsb, NB = 8 * nsb;                     // lanes of a row, q8_1 blocks of a column
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t G = gridDim.x, b = blockIdx.x;
+    const uint32_t C = (rows + rpc - 1) / rpc;
+    const uint32_t first = b + G * wave, stride = G * W;
+    const uint32_t nck = first < C ? (C - first + stride - 1) / stride : 0u;
+    uint8_t * ring = sm + (size_t)wave * 2 * slot;
+    uint8_t * xq = sm + (size_t)W * 2 * slot;
+    const uint32_t xqb = sbl_nx_xq_bytes(NX, nsb);
+    uint8_t * xd = xq + xqb;
+    const uint32_t CS = 8 * P + 16;                               // bytes per parked chain
+    const uint32_t TW = sbl_nx_tw(CG, rpc, P);
+    uint8_t * base = xd + sbl_nx_xd_bytes(NX, nsb);
+    uint8_t * T = base + (size_t)wave * TW;
+    uint8_t * Y = T + (size_t)CG * rpc * 4 * CS;                  // [2][64] old y values
+    const uint32_t grid = lds_off(base + (size_t)W * TW);         // IQ codebook (2 KiB), sign masks (1 KiB)
+    const uint64_t cb = (uint64_t)rpc * P * B;
+    const uint8_t * w = a.w + (a.id_slot ? (size_t)(*a.id_slot) * a.estride : 0);
+    auto x1 = [&](uint32_t p) -> const uint8_t * {
+        return (const uint8_t *)(a.x + (size_t)(p < nx ? p : 0) * a.xstride) + xq_off(cols);
+    };
+    uint32_t ops = 0;
+
+    // old y values of chunk i: word p * rpc + r = row r of column p (NX * rpc <= 64)
+    uint32_t y_mark[2] = {0u, 0u};
+    auto yload = [&](uint32_t i) {
+        const uint32_t p = lane / rpc, r = lane - p * rpc;
+        const uint32_t row = (first + stride * i) * rpc + r;
+        const bool v = p < nx && row < rows;
+        __builtin_amdgcn_global_load_lds(GPTR(v ? a.y + (size_t)p * a.ystride + row : a.y), LPTR(Y + 256 * (i & 1)),
+                                         4, 0, 0);
+        y_mark[i & 1] = ++ops;
+    };
+    if (nck > 0) yload(0);
+    if constexpr (IQ) {
+        constexpr uint32_t GB = FMT == FMT_IQ2_XXS ? 2048 : 1024;
+        const uint8_t * gsrc = FMT == FMT_IQ2_XXS ? (const uint8_t *)k_iq2_grid : (const uint8_t *)k_iq3_grid;
+        if (wave == 0) {
+            for (uint32_t t = 0; t < GB / 1024; ++t) {
+                __builtin_amdgcn_global_load_lds(GPTR(gsrc + 1024 * t + 16 * lane), LPTR(base + (size_t)W * TW + 1024 * t),
+                                                 16, 0, 0);
+                ++ops;
+            }
+        }
+        if (tid < 128) {
+            const uint32_t sg = iq_sign8(tid);
+            lds_st64(base + (size_t)W * TW + 2048 + 8 * tid, u32x2a{iq_neg4(sg), iq_neg4(sg >> 4)});
+        }
+    }
+    // activations: piece e = (p * 8 + q) * P + pos of the quants is half
+    // q & 1 (16 bytes from byte 4 of the 36-byte q8_1 block) of column p's
+    // block 4 pos + (q >> 1); the (d, s) word of block j at xd + 4 (p NB + j)
+    {
+        const uint32_t NQ = NX * NB * 2, nqi = (NQ + 63) / 64;
+        for (uint32_t t = wave; t < nqi; t += W) {
+            const uint32_t e = 64 * t + lane;
+            if (e < NQ) {
+                const uint32_t pq = e / P, pos = e - pq * P, p = pq >> 3, q = pq & 7u;
+                __builtin_amdgcn_global_load_lds(GPTR(x1(p) + 36 * (4 * pos + (q >> 1)) + 4 + 16 * (q & 1)),
+                                                 LPTR(xq + 1024 * t), 16, 0, 0);
+            }
+            ++ops;
+        }
+        const uint32_t ND = NX * NB, ndi = (ND + 63) / 64;
+        for (uint32_t t = wave; t < ndi; t += W) {
+            const uint32_t e = 64 * t + lane;
+            if (e < ND) {
+                const uint32_t p = e / NB;
+                __builtin_amdgcn_global_load_lds(GPTR(x1(p) + 36 * (e - p * NB)), LPTR(xd + 256 * t), 4, 0, 0);
+            }
+            ++ops;
+        }
+    }
+    const uint32_t x_mark = ops;
+    __builtin_amdgcn_s_barrier();
+
+    uint32_t mark[2] = {0u, 0u};
+    auto issue = [&](uint32_t i, uint8_t * st) {
+        const uint32_t c = first + stride * i;
+        const uint8_t * g = w + (uint64_t)c * cb;
+        const uint32_t nrow = min(rpc, rows - c * rpc);
+        const uint32_t vb = nrow * P * B;                         // valid bytes (a multiple of 16)
+        for (uint32_t t = 0; t < ni; ++t) {
+            const uint32_t o = 1024 * t + 16 * lane;
+            __builtin_amdgcn_global_load_lds(GPTR(g + (o < vb ? o : vb - 16)), LPTR(st + 1024 * t), 16, 0, FLH_KS_AUX);
+        }
+        ops += ni;
+    };
+    const bool early = wave < pre;
+    if (early && nck > 0) { issue(0, ring); mark[0] = ops; }
+    wait_vm_dyn(ops - x_mark);                                    // this wave's activation loads
+    lds_barrier();                                                // everyone's
+    if (!early && nck > 0) { issue(0, ring); mark[0] = ops; }
+    if (nck > 1) { issue(1, ring + slot); mark[1] = ops; }
+
+    const uint32_t r = lane / P, pos = lane - r * P;              // the lane's row in a chunk, its position
+    for (uint32_t i = 0; i < nck; ++i) {
+        const uint32_t sl = i & 1u;
+        uint8_t * st = ring + sl * slot;
+        wait_vm_dyn(ops - mark[sl]);
+        if (i + 1 < nck) yload(i + 1);
+        uint32_t Q[32];
+        float wf[4];
+        nx_decode<FMT>(st, lane, grid, Q, wf);
+        if (i + 2 < nck) {                                        // refill this stage
+            issue(i + 2, st);
+            mark[sl] = ops;
+        }
+        const uint32_t row0 = (first + stride * i) * rpc;
+        // columns g0 .. g0 + CG - 1 parked, then folded
+        for (uint32_t g0 = 0; g0 < nx; g0 += CG) {
+            if (r < rpc) {
+#pragma unroll
+                for (uint32_t pl = 0; pl < CG; ++pl) {
+                    const size_t blk = (size_t)(g0 + pl) * NB + 4 * pos;
+                    u32x4a q[8], dv;
+                    nx_load_col(xq + 16 * ((size_t)(g0 + pl) * 8 * P + pos), 16 * P, xd + 4 * blk, q, dv);
+                    const uint32_t dw[4] = {dv.x, dv.y, dv.z, dv.w};
+#pragma unroll
+                    for (int m = 0; m < 4; ++m) {
+                        const uint32_t XV[8] = {q[2 * m].x, q[2 * m].y, q[2 * m].z, q[2 * m].w,
+                                                q[2 * m + 1].x, q[2 * m + 1].y, q[2 * m + 1].z, q[2 * m + 1].w};
+                        int s = 0, xs = 0;
+#pragma unroll
+                        for (int k = 0; k < 8; ++k) {
+                            s = dot4((int)Q[8 * m + k], (int)XV[k], s);
+                            if constexpr (FMT == FMT_Q5_0) xs = dot4(0x01010101, (int)XV[k], xs);
+                        }
+                        if constexpr (FMT == FMT_Q5_0) s -= 16 * xs;
+                        const float f = wf[m] * h2f(dw[m] & 0xFFFFu);
+                        lds_st64(T + ((pl * rpc + r) * 4 + m) * CS + 8 * pos,
+                                 u32x2a{__float_as_uint(f), __float_as_uint((float)s)});
+                    }
+                }
+            }
+            if (g0 == 0) wait_vm_dyn(ops - y_mark[i & 1]);        // this chunk's old y values have landed
+            // chain c = (pl * rpc + rr) * 4 + k: accumulator k of row rr,
+            // column g0 + pl, over its P terms in position order
+            const uint32_t nch = CG * rpc * 4;
+            for (uint32_t c0 = 0; c0 < nch; c0 += 64) {
+                const uint32_t c = c0 + lane, ch = c < nch ? c : nch - 1;
+                const uint8_t * tr = T + ch * CS;
+                float acc = 0.f;
+                for (uint32_t j0 = 0; j0 < P; j0 += 16) {
+                    u32x4a t[8];
+#pragma unroll
+                    for (int q = 0; q < 8; ++q) t[q] = lds_ld128_nw(tr + 8 * (j0 + 2 * q < P ? j0 + 2 * q : j0));
+                    lds_wait8(t);
+#pragma unroll
+                    for (int q = 0; q < 8; ++q) {
+                        if (j0 + 2 * q < P) {
+                            acc = fmaf(__uint_as_float(t[q].x), __uint_as_float(t[q].y), acc);
+                            acc = fmaf(__uint_as_float(t[q].z), __uint_as_float(t[q].w), acc);
+                        }
+                    }
+                }
+                const float s01 = acc + qx1f(acc);
+                const float tot = s01 + qx2f(s01);
+                const uint32_t pl = ch / (4 * rpc), rr = (ch >> 2) - pl * rpc, p = g0 + pl, row = row0 + rr;
+                const bool ok = c < nch && (c & 3u) == 0 && p < nx && row < rows;
+                if (ok) {
+                    const float yo = __uint_as_float(lds_ld32(Y + 256 * (i & 1) + 4 * (p * rpc + rr)));
+                    gst_x1(a.y + (size_t)p * a.ystride + row, __float_as_uint(yo + tot));
+                }
+                if (__ballot(ok) != 0) ++ops;                     // counted only when some lane stores
+            }
+        }
+    }
+    WAIT_VM(0);
+}
+
 static size_t sbl_smem(bool q8, bool iq, uint32_t W, uint32_t slot, uint32_t nsb) {
     const size_t xs = ((q8 ? nsb * 8 * SBL_X8 : nsb * SBL_XS) + 1023u) & ~(size_t)1023;
     return (size_t)W * 2 * slot + xs + (size_t)W * ((q8 ? 4096 : 1024) + 256) + (iq ? 3072 : 0);
@@ -1029,6 +1303,70 @@ int launch_dot_sbl(int fmt, const DotArgs & a, bool fuse, hipStream_t s) {
     if (W == 8) return go(k_dot_sbl<FMT_Q4_K, true, 8>);
     if (W == 6) return go(k_dot_sbl<FMT_Q4_K, true, 6>);
     return go(k_dot_sbl<FMT_Q4_K, true, 4>);
+}
+
+// Several activation columns (2..8) of a 32-weight-block format: one pass
+// over the weights for up to 8 columns (capacity 2, 4 or 8; columns past nx
+// read column 0 and store nothing).  FLH_ERR_UNSUPPORTED (nothing launched)
+// when a row spans more than 64 lanes (over 8192 columns), a chunk's rows
+// would need more than 64 old-y words, or the LDS plan does not fit.
+int launch_dot_sbl_nx(int fmt, const DotArgs & a, hipStream_t s) {
+    const bool iq = fmt == FMT_IQ2_XXS || fmt == FMT_IQ3_XXS;
+    if ((fmt != FMT_Q8_0 && fmt != FMT_Q5_0 && !iq) || a.nx < 2 || a.nx > 8 || (a.cols & 255) || a.rows == 0)
+        return FLH_ERR_UNSUPPORTED;
+    const uint32_t nsb = a.cols >> 8, P = 2 * nsb;
+    const uint32_t B = fmt == FMT_Q8_0 ? 136 : fmt == FMT_Q5_0 ? 88 : iq_block_bytes(fmt) / 2;
+    if (P > 64 || ((P * B) & 15) || ((uintptr_t)a.w & 15) || (a.estride & 15) || ((uintptr_t)a.x & 3))
+        return FLH_ERR_UNSUPPORTED;
+    const uint32_t NX = a.nx <= 2 ? 2 : a.nx <= 4 ? 4 : 8;
+    const uint32_t rpc = 64 / P;
+    if (NX * rpc > 64) return FLH_ERR_UNSUPPORTED;
+    const uint32_t ni = (rpc * P * B + 1023) / 1024, slot = ni * 1024;
+    const Tune & t = tune();
+    // plan: 8 waves where the LDS holds them with at least 2 columns parked
+    // at once (two waves per SIMD hide the per-column LDS round trips:
+    // 14336x4096 x 8 columns IQ2_XXS 33.2 -> 24.6 us, IQ3_XXS 35.1 -> 31.0;
+    // with one column parked at a time Q5_0 lost, 36.6 -> 43.5), else 4
+    // waves with the most columns parked at once
+    auto smem = [&](uint32_t W, uint32_t cg) {
+        return (size_t)W * 2 * slot + sbl_nx_xq_bytes(NX, nsb) + sbl_nx_xd_bytes(NX, nsb) +
+               (size_t)W * sbl_nx_tw(cg, rpc, P) + (iq ? 3072 : 0);
+    };
+    uint32_t W = 0, CG = 0;
+    for (uint32_t w : {8u, 4u}) {
+        if (t.sbl_w && t.sbl_w != w) continue;
+        for (uint32_t cg = NX < 4 ? NX : 4; cg >= (w == 8 && !t.sbl_w ? 2u : 1u) && !W; cg >>= 1)
+            if (smem(w, cg) <= lds_limit()) { W = w; CG = cg; }
+        if (W) break;
+    }
+    if (!W) return FLH_ERR_UNSUPPORTED;
+    const size_t smb = smem(W, CG);
+    const uint32_t pre = t.sbl_pre == 0xFFu ? W : t.sbl_pre ? t.sbl_pre : W;
+    const uint32_t C = (a.rows + rpc - 1) / rpc;
+    uint32_t G = (uint32_t)num_cus() * (t.sbl_wpc ? t.sbl_wpc : 1);
+    if (t.sbl_gmax && G > t.sbl_gmax) G = t.sbl_gmax;
+    if (G > C) G = C;
+    auto go = [&](auto kern) {
+        (void)hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smb);
+        hipLaunchKernelGGL(kern, dim3(G), dim3(64 * W), smb, s, a, rpc, ni, slot, pre, NX);
+        return hip_check(hipGetLastError(), "k_dot_sbl_nx launch");
+    };
+    auto by_cg = [&](auto fmt_tag, auto w_tag) {
+        constexpr int F = decltype(fmt_tag)::value, WW = decltype(w_tag)::value;
+        if (CG == 4) return go(k_dot_sbl_nx<F, WW, 4>);
+        if (CG == 2) return go(k_dot_sbl_nx<F, WW, 2>);
+        return go(k_dot_sbl_nx<F, WW, 1>);
+    };
+    auto by_w = [&](auto fmt_tag) {
+        if (W == 8) return by_cg(fmt_tag, std::integral_constant<int, 8>());
+        return by_cg(fmt_tag, std::integral_constant<int, 4>());
+    };
+    switch (fmt) {
+        case FMT_Q8_0: return by_w(std::integral_constant<int, FMT_Q8_0>());
+        case FMT_Q5_0: return by_w(std::integral_constant<int, FMT_Q5_0>());
+        case FMT_IQ2_XXS: return by_w(std::integral_constant<int, FMT_IQ2_XXS>());
+        default: return by_w(std::integral_constant<int, FMT_IQ3_XXS>());
+    }
 }
 
 // Routed expert dots, one workgroup row per (token, slot) pair, the dense
