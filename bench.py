@@ -16,7 +16,8 @@ Also reported (same JSON line):
               each Q4_K layer shape, Q6_K vocab head and down, spec-verify
               N in {2,4,8}, MoE top-2 of 8 at batch 1 and 8 (graph of R
               launches rotating over weight copies, HIP events); also Q5_0 /
-              IQ2_XXS / IQ3_XXS matvecs and the activation quantisers
+              IQ2_XXS / IQ3_XXS matvecs, 2/4/8-column dots of those formats
+              and Q8_0 at 14336x4096, and the activation quantisers
               (ACT_Q8 14336, RMSNORM -> ACT_Q8 4096);
   roofline -- the dominant kernel (Q4_K gate/up): algorithmic bytes per
               launch / average launch time vs the 8 TB/s HBM peak;
@@ -293,6 +294,24 @@ def main():
                 if fmt == Q5_0 and r == 4096:
                     cpu_in[f"q5_0_{r}x{c}"] = host_case(flh, s, Q5_0, ws[0], r, c, x, st, 1)
                 del ws
+        # several activation columns of the 32-weight-block formats (a
+        # speculative-verify batch on a Q8_0 / Q5_0 / IQ model): 14336x4096
+        # with 2, 4, 8 columns, one weight pass per launch
+        for fmt, fname in ((Q8_0, "q8_0"), (Q5_0, "q5_0"), (IQ2_XXS, "iq2_xxs"), (IQ3_XXS, "iq3_xxs")):
+            r, c = 14336, 4096
+            nb = r * flh.row_bytes(fmt, c)
+            if fmt == Q8_0:
+                ws = B.weights(fmt, r, c, copies_for(nb), seed=80 + r, staging=staging)
+            else:
+                ws = B.weights_random(fmt, r, c, copies_for(nb), seed=80 + fmt + r)
+            m8 = flh.I8_MASK_DEFAULT | (1 << IQ2_XXS) | (1 << IQ3_XXS)
+            for n in (2, 4, 8):
+                xn, stn = B.activation(c, n, 90 + n, outliers=False)
+                y = B.buf(n * r * 4)
+                us = B.time_graph(lambda i: flh.stream_dot(fmt, ws[i % len(ws)], r, c, xn, y, s, nx=n, xstride=stn,
+                                                           ystride=r, i8_mask=m8), REPS)
+                op_entry(f"{fname}_verify_n{n}_{r}x{c}", us, nb, {"n": n})
+            del ws
         # the activation quantisers on their own (row f1): ACT_Q8 of the
         # down projection's 14336-wide input (its own launch in the layer
         # step) and RMSNORM -> ACT_Q8 of a 4096-wide hidden state in one launch
@@ -351,6 +370,9 @@ for _n in (2, 4, 8):
         PROFILE_OPS[f"verify{_n}_{_r}x{_c}"] = (Q4_K, _r, _c, _n, "dot")
         PROFILE_OPS[f"verify{_n}_{_r}x{_c}_kstream"] = (Q4_K, _r, _c, _n, "dot_nomfma")
 PROFILE_OPS["verify8"] = PROFILE_OPS["verify8_14336x4096"]
+for _f, _name in ((Q8_0, "q8_0"), (Q5_0, "q5_0"), (IQ2_XXS, "iq2_xxs"), (IQ3_XXS, "iq3_xxs")):
+    for _n in (2, 4, 8):
+        PROFILE_OPS[f"{_name}_verify{_n}"] = (_f, 14336, 4096, _n, "dot")
 
 
 def profile_run(flh, B, s, staging, which="gate_up"):
