@@ -1031,18 +1031,25 @@ __device__ __forceinline__ void nx_decode(const uint8_t * st, uint32_t lane, uin
 }
 
 // one column's quants of the lane (8 pieces of 16 bytes, piece q at
-// xq + q * qs) and its 4 d words (at xd), in one LDS round trip
-__device__ __forceinline__ void nx_load_col(const uint8_t * xq, uint32_t qs, const uint8_t * xd, u32x4a (&q)[8],
-                                            u32x4a & dv) {
+// xq + q * qs) and its 4 d words (at xd), requested together; nx_wait_col
+// waits for them (the registers stay untouched in between)
+__device__ __forceinline__ void nx_issue_col(const uint8_t * xq, uint32_t qs, const uint8_t * xd, u32x4a (&q)[8],
+                                             u32x4a & dv) {
     const uint32_t a0 = lds_off(xq);
     asm volatile("ds_read_b128 %0, %9\n\tds_read_b128 %1, %10\n\tds_read_b128 %2, %11\n\tds_read_b128 %3, %12\n\t"
                  "ds_read_b128 %4, %13\n\tds_read_b128 %5, %14\n\tds_read_b128 %6, %15\n\tds_read_b128 %7, %16\n\t"
-                 "ds_read_b128 %8, %17\n\ts_waitcnt lgkmcnt(0)"
+                 "ds_read_b128 %8, %17"
                  : "=&v"(q[0]), "=&v"(q[1]), "=&v"(q[2]), "=&v"(q[3]), "=&v"(q[4]), "=&v"(q[5]), "=&v"(q[6]),
                    "=&v"(q[7]), "=&v"(dv)
                  : "v"(a0), "v"(a0 + qs), "v"(a0 + 2 * qs), "v"(a0 + 3 * qs), "v"(a0 + 4 * qs), "v"(a0 + 5 * qs),
                    "v"(a0 + 6 * qs), "v"(a0 + 7 * qs), "v"(lds_off(xd))
                  : "memory");
+}
+__device__ __forceinline__ void nx_wait_col(u32x4a (&q)[8], u32x4a & dv) {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(q[0]), "+v"(q[1]), "+v"(q[2]), "+v"(q[3]), "+v"(q[4]), "+v"(q[5]), "+v"(q[6]), "+v"(q[7]),
+                   "+v"(dv)
+                 :: "memory");
 }
 
 template <int FMT, int W, int CG>
@@ -1167,11 +1174,22 @@ __global__ __launch_bounds__(64 * W) void k_dot_sbl_nx(DotArgs a, uint32_t rpc, 
         // columns g0 .. g0 + CG - 1 parked, then folded
         for (uint32_t g0 = 0; g0 < nx; g0 += CG) {
             if (r < rpc) {
+                // column pl + 1's pieces are requested before column pl's dots
+                u32x4a qa[8], da, qb[8], db;
+                auto issue_col = [&](uint32_t pl, u32x4a (&q)[8], u32x4a & dv) {
+                    nx_issue_col(xq + 16 * ((size_t)(g0 + pl) * 8 * P + pos), 16 * P,
+                                 xd + 4 * ((size_t)(g0 + pl) * NB + 4 * pos), q, dv);
+                };
+                issue_col(0, qa, da);
 #pragma unroll
                 for (uint32_t pl = 0; pl < CG; ++pl) {
-                    const size_t blk = (size_t)(g0 + pl) * NB + 4 * pos;
-                    u32x4a q[8], dv;
-                    nx_load_col(xq + 16 * ((size_t)(g0 + pl) * 8 * P + pos), 16 * P, xd + 4 * blk, q, dv);
+                    u32x4a (&q)[8] = (pl & 1) ? qb : qa;
+                    u32x4a & dv = (pl & 1) ? db : da;
+                    nx_wait_col(q, dv);
+                    if (pl + 1 < CG) {
+                        if (pl & 1) issue_col(pl + 1, qa, da);
+                        else issue_col(pl + 1, qb, db);
+                    }
                     const uint32_t dw[4] = {dv.x, dv.y, dv.z, dv.w};
 #pragma unroll
                     for (int m = 0; m < 4; ++m) {
@@ -1305,15 +1323,35 @@ int launch_dot_sbl(int fmt, const DotArgs & a, bool fuse, hipStream_t s) {
     return go(k_dot_sbl<FMT_Q4_K, true, 4>);
 }
 
-// Several activation columns (2..8) of a 32-weight-block format: one pass
+// Several activation columns (2..16) of a 32-weight-block format: one pass
 // over the weights for up to 8 columns (capacity 2, 4 or 8; columns past nx
-// read column 0 and store nothing).  FLH_ERR_UNSUPPORTED (nothing launched)
+// read column 0 and store nothing), two passes for 9..16.  FLH_ERR_UNSUPPORTED (nothing launched)
 // when a row spans more than 64 lanes (over 8192 columns), a chunk's rows
 // would need more than 64 old-y words, or the LDS plan does not fit.
-int launch_dot_sbl_nx(int fmt, const DotArgs & a, hipStream_t s) {
+static int sbl_nx_go(int fmt, const DotArgs & a, hipStream_t s, bool dry);
+int launch_dot_sbl_nx(int fmt, const DotArgs & a, hipStream_t s) { return sbl_nx_go(fmt, a, s, false); }
+
+// dry: FLH_OK when the launch would go ahead, launching nothing
+static int sbl_nx_go(int fmt, const DotArgs & a, hipStream_t s, bool dry) {
     const bool iq = fmt == FMT_IQ2_XXS || fmt == FMT_IQ3_XXS;
-    if ((fmt != FMT_Q8_0 && fmt != FMT_Q5_0 && !iq) || a.nx < 2 || a.nx > 8 || (a.cols & 255) || a.rows == 0)
+    if ((fmt != FMT_Q8_0 && fmt != FMT_Q5_0 && !iq) || a.nx < 2 || a.nx > 16 || (a.cols & 255) || a.rows == 0)
         return FLH_ERR_UNSUPPORTED;
+    if (a.nx > 8) {
+        // 9..16 columns: a pass of up to 8 and one of the rest (at least 2;
+        // each column's result is its own, so the split changes no bits).
+        // Nothing is launched unless both plans fit (the caller's fallback
+        // must not add to y twice).
+        DotArgs lo = a, hi = a;
+        lo.nx = a.nx - 8 >= 2 ? 8 : a.nx - 2;
+        hi.nx = a.nx - lo.nx;
+        hi.x = a.x + (size_t)lo.nx * a.xstride;
+        hi.y = a.y + (size_t)lo.nx * a.ystride;
+        if (sbl_nx_go(fmt, lo, s, true) != FLH_OK || sbl_nx_go(fmt, hi, s, true) != FLH_OK)
+            return FLH_ERR_UNSUPPORTED;
+        if (dry) return FLH_OK;
+        const int rc = sbl_nx_go(fmt, lo, s, false);
+        return rc != FLH_OK ? rc : sbl_nx_go(fmt, hi, s, false);
+    }
     const uint32_t nsb = a.cols >> 8, P = 2 * nsb;
     const uint32_t B = fmt == FMT_Q8_0 ? 136 : fmt == FMT_Q5_0 ? 88 : iq_block_bytes(fmt) / 2;
     if (P > 64 || ((P * B) & 15) || ((uintptr_t)a.w & 15) || (a.estride & 15) || ((uintptr_t)a.x & 3))
@@ -1340,6 +1378,7 @@ int launch_dot_sbl_nx(int fmt, const DotArgs & a, hipStream_t s) {
         if (W) break;
     }
     if (!W) return FLH_ERR_UNSUPPORTED;
+    if (dry) return FLH_OK;
     const size_t smb = smem(W, CG);
     const uint32_t pre = t.sbl_pre == 0xFFu ? W : t.sbl_pre ? t.sbl_pre : W;
     const uint32_t C = (a.rows + rpc - 1) / rpc;

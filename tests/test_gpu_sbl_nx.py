@@ -5,7 +5,8 @@ Q8_0, Q5_0, IQ2_XXS and IQ3_XXS x q8_1 in one pass over the weights.
 Bar: bitwise against the oracle's per-column dots (fl_dot_i8_q8_0 /
 fl_dot_i8_q5_0, src/runtime/quants.h:438-466; the IQ group order of
 kernels_gpu.h:759-852) with y += accumulation onto random y, for every column
-count up to the 8-column capacity (idle capacity columns store nothing), row
+count up to the 8-column capacity (idle capacity columns store nothing) and
+9..16 columns in two passes, row
 geometries with partial last chunks and idle lanes, widths where 8 columns do
 not fit (8192: the register kernel takes them), wave counts, grids small
 enough that every wave streams many chunks, an expert picked by an id slot,
@@ -43,6 +44,17 @@ def case(flh, orc, gpu, fmt, rows, cols, nx, seed, cfg="1"):
 def test_sbl_nx_bitwise(flh, orc, gpu, fmt, nx, rows, cols):
     say("sbl nx", fmt, nx, rows, cols)
     case(flh, orc, gpu, fmt, rows, cols, nx, rows * 13 + cols + 7 * nx + fmt)
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("nx", [9, 12, 16])
+@pytest.mark.parametrize("rows,cols", [(1001, 4096), (70, 8192)])
+def test_sbl_nx_two_passes(flh, orc, gpu, fmt, nx, rows, cols):
+    """9..16 columns: two passes (8 + the rest, 7 + 2 for 9); at 8192 columns
+    the 8-column pass does not fit and the whole tile takes the register
+    kernel (no column is added twice)."""
+    say("sbl nx passes", fmt, nx, rows, cols)
+    case(flh, orc, gpu, fmt, rows, cols, nx, rows + cols + 17 * nx + fmt)
 
 
 @pytest.mark.parametrize("fmt", FMTS)
