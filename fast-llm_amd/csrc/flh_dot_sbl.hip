@@ -1268,9 +1268,12 @@ int launch_dot_sbl(int fmt, const DotArgs & a, bool fuse, hipStream_t s) {
     const uint32_t ni = (rpc * P * B + 1023) / 1024, slot = ni * 1024;
     // Measured defaults (layer shapes, graph-replayed launches):
     //  * fused: 8 waves (the quantisation is shared by more waves), 4 of
-    //    them requesting a chunk before the activation is ready; above 2^17
-    //    superblocks the four-lanes-per-superblock kernel is faster (gate/up
-    //    28672x4096: 14.0 vs 14.9 us) and this launcher declines;
+    //    them requesting a chunk before the activation is ready; above 2^18
+    //    superblocks the four-lanes-per-superblock kernel is faster and this
+    //    launcher declines (fused, us, this kernel vs that one: 10240x4096
+    //    7.62 vs 9.10, 14336x4096 9.14 vs 9.61, 16384x4096 9.91 vs 10.28,
+    //    6144x8192 10.48 vs 10.61; 20480x4096 11.37 vs 11.11, gate/up
+    //    28672x4096 14.74 vs 13.47, 12288x8192 16.09 vs 13.34);
     //  * unfused, <= 16 superblocks per row: 4 waves, 2 early (O 4096x4096
     //    5.37 -> 4.85 us, QKV 5.95 -> 5.49);
     //  * unfused, wider rows: 8 waves, 4 early (down 4096x14336 9.78 -> 9.63);
@@ -1279,7 +1282,7 @@ int launch_dot_sbl(int fmt, const DotArgs & a, bool fuse, hipStream_t s) {
     //  * Q5_0 and the IQ formats, more VALU work per byte: 8 waves, all
     //    early (14336x4096 Q5_0 15.2 -> 11.9 us, IQ2_XXS 16.6 -> 12.2,
     //    IQ3_XXS 18.3 -> 13.5 against 4 waves).
-    if (fuse && !t.sbl_w && (uint64_t)a.rows * nsb > (1u << 17)) return FLH_ERR_UNSUPPORTED;
+    if (fuse && !t.sbl_w && (uint64_t)a.rows * nsb > (1u << 18)) return FLH_ERR_UNSUPPORTED;
     // Q6_K: its 6-bit decode is VALU-heavy and a 12-14 KB chunk leaves room
     // for 4 waves only, so the four-lanes-per-superblock kernel stays faster
     // unless the matrix is large enough for the streaming rate to dominate

@@ -57,7 +57,7 @@ def test_sbl_bitwise(flh, orc, gpu, cfg, rows, cols):
         assert np.array_equal(bits(got), bits(want))
 
 
-@pytest.mark.parametrize("rows,cols", [(6144, 4096), (4096, 14336)])
+@pytest.mark.parametrize("rows,cols", [(6144, 4096), (4096, 14336), (16384, 4096), (6144, 8192)])
 def test_sbl_layer_shapes_normal_weights(flh, orc, gpu, rows, cols):
     """Quantized N(0, 0.02^2) weights (the benchmark's recipe) at layer shapes."""
     say("sbl layer", rows, cols)
