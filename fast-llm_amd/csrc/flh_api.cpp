@@ -102,6 +102,7 @@ void load_tune() {
     if (const char * e = getenv("FLH_MFMA_XC")) t.mf_xc = atoi(e) != 0;
     if (const char * e = getenv("FLH_MFMA_MIN_COLS")) t.mf_min_cols = (uint32_t)atoi(e);
     if (const char * e = getenv("FLH_NO_MFMA")) t.no_mfma = atoi(e) != 0;
+    if (const char * e = getenv("FLH_SBL_NX_DEP")) t.sbl_nx_dep = (uint32_t)atoi(e);
     if (const char * e = getenv("FLH_GGUF_THREADS")) t.gguf_threads = (uint32_t)strtoul(e, nullptr, 0);
     if (const char * e = getenv("FLH_SBL")) {
         unsigned on = 1, w = 0, g = 0, m = 0, pre = 0;

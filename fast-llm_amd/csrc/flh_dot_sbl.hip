@@ -1054,7 +1054,7 @@ __device__ __forceinline__ void nx_wait_col(u32x4a (&q)[8], u32x4a & dv) {
 
 template <int FMT, int W, int CG>
 __global__ __launch_bounds__(64 * W) void k_dot_sbl_nx(DotArgs a, uint32_t rpc, uint32_t ni, uint32_t slot, uint32_t pre,
-                                                       uint32_t NX) {
+                                                       uint32_t NX, uint32_t dep) {
     static_assert(FMT == FMT_Q8_0 || FMT == FMT_Q5_0 || FMT == FMT_IQ2_XXS || FMT == FMT_IQ3_XXS,
                   "a 32-weight-block format");
     constexpr bool IQ = FMT == FMT_IQ2_XXS || FMT == FMT_IQ3_XXS;
@@ -1068,8 +1068,10 @@ __global__ __launch_bounds__(64 * W) void k_dot_sbl_nx(DotArgs a, uint32_t rpc, 
     const uint32_t C = (rows + rpc - 1) / rpc;
     const uint32_t first = b + G * wave, stride = G * W;
     const uint32_t nck = first < C ? (C - first + stride - 1) / stride : 0u;
-    uint8_t * ring = sm + (size_t)wave * 2 * slot;
-    uint8_t * xq = sm + (size_t)W * 2 * slot;
+    // ring of dep (1 or 2) stages: a stage is free again once the lane's
+    // decode has its bytes in registers
+    uint8_t * ring = sm + (size_t)wave * dep * slot;
+    uint8_t * xq = sm + (size_t)W * dep * slot;
     const uint32_t xqb = sbl_nx_xq_bytes(NX, nsb);
     uint8_t * xd = xq + xqb;
     const uint32_t CS = 8 * P + 16;                               // bytes per parked chain
@@ -1155,19 +1157,19 @@ __global__ __launch_bounds__(64 * W) void k_dot_sbl_nx(DotArgs a, uint32_t rpc, 
     wait_vm_dyn(ops - x_mark);                                    // this wave's activation loads
     lds_barrier();                                                // everyone's
     if (!early && nck > 0) { issue(0, ring); mark[0] = ops; }
-    if (nck > 1) { issue(1, ring + slot); mark[1] = ops; }
+    if (dep == 2 && nck > 1) { issue(1, ring + slot); mark[1] = ops; }
 
     const uint32_t r = lane / P, pos = lane - r * P;              // the lane's row in a chunk, its position
     for (uint32_t i = 0; i < nck; ++i) {
-        const uint32_t sl = i & 1u;
+        const uint32_t sl = dep == 2 ? (i & 1u) : 0u;
         uint8_t * st = ring + sl * slot;
         wait_vm_dyn(ops - mark[sl]);
         if (i + 1 < nck) yload(i + 1);
         uint32_t Q[32];
         float wf[4];
         nx_decode<FMT>(st, lane, grid, Q, wf);
-        if (i + 2 < nck) {                                        // refill this stage
-            issue(i + 2, st);
+        if (i + dep < nck) {                                      // refill this stage
+            issue(i + dep, st);
             mark[sl] = ops;
         }
         const uint32_t row0 = (first + stride * i) * rpc;
@@ -1364,25 +1366,30 @@ static int sbl_nx_go(int fmt, const DotArgs & a, hipStream_t s, bool dry) {
     if (NX * rpc > 64) return FLH_ERR_UNSUPPORTED;
     const uint32_t ni = (rpc * P * B + 1023) / 1024, slot = ni * 1024;
     const Tune & t = tune();
-    // plan: 8 waves where the LDS holds them with at least 2 columns parked
-    // at once (two waves per SIMD hide the per-column LDS round trips:
-    // 14336x4096 x 8 columns IQ2_XXS 33.2 -> 24.6 us, IQ3_XXS 35.1 -> 31.0;
-    // with one column parked at a time Q5_0 lost, 36.6 -> 43.5), else 4
-    // waves with the most columns parked at once
-    auto smem = [&](uint32_t W, uint32_t cg) {
-        return (size_t)W * 2 * slot + sbl_nx_xq_bytes(NX, nsb) + sbl_nx_xd_bytes(NX, nsb) +
+    // plan: 8 waves with a 1-stage ring (refilled right after the decode)
+    // and at least 2 columns parked at once, else 4 waves with 2 stages and
+    // the most columns parked at once.  Measured at 14336x4096 (us, N = 2 /
+    // 4 / 8): 8 waves x 1 stage Q8_0 14.0 / 18.5 / 27.6, Q5_0 15.4 / 18.4 /
+    // 27.6, IQ2_XXS 13.5 / 16.1 / 23.2, IQ3_XXS 15.4 / 17.9 / 25.1; with 2
+    // stages (8 waves where they fit, else 4) Q8_0 18.1 / 21.8 / 33.0, Q5_0
+    // 15.3 / 21.3 / 37.0, IQ3_XXS 15.4 / 17.9 / 29.1 (two waves per SIMD hide
+    // the per-column LDS round trips; one column parked at a time loses)
+    auto smem = [&](uint32_t W, uint32_t d, uint32_t cg) {
+        return (size_t)W * d * slot + sbl_nx_xq_bytes(NX, nsb) + sbl_nx_xd_bytes(NX, nsb) +
                (size_t)W * sbl_nx_tw(cg, rpc, P) + (iq ? 3072 : 0);
     };
-    uint32_t W = 0, CG = 0;
-    for (uint32_t w : {8u, 4u}) {
-        if (t.sbl_w && t.sbl_w != w) continue;
+    uint32_t W = 0, CG = 0, dep = 0;
+    const uint32_t plans[3][2] = {{8, 1}, {4, 2}, {8, 2}};   // the last: forced 8 waves x 2 stages
+    for (const auto & pl : plans) {
+        const uint32_t w = pl[0], d = pl[1];
+        if ((t.sbl_w && t.sbl_w != w) || (t.sbl_nx_dep && t.sbl_nx_dep != d)) continue;
         for (uint32_t cg = NX < 4 ? NX : 4; cg >= (w == 8 && !t.sbl_w ? 2u : 1u) && !W; cg >>= 1)
-            if (smem(w, cg) <= lds_limit()) { W = w; CG = cg; }
+            if (smem(w, d, cg) <= lds_limit()) { W = w; CG = cg; dep = d; }
         if (W) break;
     }
     if (!W) return FLH_ERR_UNSUPPORTED;
     if (dry) return FLH_OK;
-    const size_t smb = smem(W, CG);
+    const size_t smb = smem(W, dep, CG);
     const uint32_t pre = t.sbl_pre == 0xFFu ? W : t.sbl_pre ? t.sbl_pre : W;
     const uint32_t C = (a.rows + rpc - 1) / rpc;
     uint32_t G = (uint32_t)num_cus() * (t.sbl_wpc ? t.sbl_wpc : 1);
@@ -1390,7 +1397,7 @@ static int sbl_nx_go(int fmt, const DotArgs & a, hipStream_t s, bool dry) {
     if (G > C) G = C;
     auto go = [&](auto kern) {
         (void)hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smb);
-        hipLaunchKernelGGL(kern, dim3(G), dim3(64 * W), smb, s, a, rpc, ni, slot, pre, NX);
+        hipLaunchKernelGGL(kern, dim3(G), dim3(64 * W), smb, s, a, rpc, ni, slot, pre, NX, dep);
         return hip_check(hipGetLastError(), "k_dot_sbl_nx launch");
     };
     auto by_cg = [&](auto fmt_tag, auto w_tag) {

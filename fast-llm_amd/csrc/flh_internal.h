@@ -84,6 +84,7 @@ struct Tune {
     // (0 = default; max_wgs caps the grid, for tests of long per-wave chunk
     // lists; pre = waves requesting a chunk before the activation lands, 0: half, 255: all)
     uint32_t sbl = 1, sbl_w = 0, sbl_wpc = 0, sbl_gmax = 0, sbl_pre = 0;
+    uint32_t sbl_nx_dep = 0;            // FLH_SBL_NX_DEP: ring stages of the several-column kernel (0: planned)
     uint32_t gguf_threads = 0;          // FLH_GGUF_THREADS: host copy threads of an upload (0: all, <= 16)
 };
 const Tune & tune();

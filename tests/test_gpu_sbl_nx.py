@@ -82,3 +82,22 @@ def test_sbl_nx_matches_register_kernel(flh, orc, gpu, fmt):
     got, want = run_dot(flh, orc, gpu, fmt, we, r, cols, xs, mode=MODE[fmt], id_slot=2,
                         estride=r * flh.row_bytes(fmt, cols))
     assert np.array_equal(bits(got), bits(want))
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("env", [{"FLH_SBL_NX_DEP": "2"}, {"FLH_SBL": "1,8", "FLH_SBL_NX_DEP": "2"},
+                                 {"FLH_SBL": "1,8", "FLH_SBL_NX_DEP": "1"}])
+def test_sbl_nx_ring_depth_keeps_bits(flh, orc, gpu, fmt, env):
+    """FLH_SBL_NX_DEP: 2-stage rings (4 waves, or 8 where they fit) give the
+    planned 1-stage run's bits, and the oracle's."""
+    say("sbl nx ring depth", fmt, env)
+    rows, cols, nx = 1001, 4096, 5
+    base = case(flh, orc, gpu, fmt, rows, cols, nx, 77 + fmt)
+    rng = np.random.default_rng(77 + fmt)
+    w = sane_rows(fmt, rows, cols, rng)
+    xs = activations(nx, cols, rng, outliers=True)
+    y0 = rng.standard_normal(nx * rows).astype(np.float32)
+    with tuned(flh, **env):
+        got, want = run_dot(flh, orc, gpu, fmt, w, rows, cols, xs, mode=MODE[fmt], y0=y0)
+    assert np.array_equal(bits(got), bits(want))
+    assert np.array_equal(bits(got), bits(base))
