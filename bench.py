@@ -17,8 +17,9 @@ Also reported (same JSON line):
               N in {2,4,8}, MoE top-2 of 8 at batch 1 and 8 (graph of R
               launches rotating over weight copies, HIP events); also Q5_0 /
               IQ2_XXS / IQ3_XXS matvecs, 2/4/8-column dots of those formats
-              and Q8_0 at 14336x4096, and the activation quantisers
-              (ACT_Q8 14336, RMSNORM -> ACT_Q8 4096);
+              and Q8_0 at 14336x4096, the activation quantisers
+              (ACT_Q8 14336, RMSNORM -> ACT_Q8 4096) and RMSNORM -> QKV /
+              gate/up in one launch against two;
   roofline -- the dominant kernel (Q4_K gate/up): algorithmic bytes per
               launch / average launch time vs the 8 TB/s HBM peak;
   cpu_baseline -- the reference CPU path on the host cores (oracle/_ref,
@@ -326,6 +327,24 @@ def main():
         us = B.time_graph(lambda i: flh.rmsnorm_act_q8(xr, wn, yr, 4096, 1e-5, s), REPS)
         op_entry("rmsnorm_act_q8_4096", us, 3 * 4096 * 4 + 4096 // 32 * 36 + 4096 // 256 * 292,
                  {"bytes": "x and norm weight read, y and both appendices written (no matrix)"})
+        # the decoder's norm -> quant -> matvec chain (attention norm -> QKV,
+        # FFN norm -> gate/up): one launch (flh_rmsnorm_stream_dot) against
+        # RMSNORM+ACT_Q8 and the dot as two launches
+        for name, r, c in (("qkv", 6144, 4096), ("gate_up", 28672, 4096)):
+            nb = r * flh.row_bytes(Q4_K, c)
+            ws = B.weights(Q4_K, r, c, copies_for(nb), seed=74 + r, staging=staging)
+            y = B.buf(r * 4)
+            us = B.time_graph(lambda i: flh.rmsnorm_stream_dot(Q4_K, ws[i % len(ws)], r, c, xr, wn, 1e-5, yr, y, s),
+                              REPS)
+            op_entry(f"rmsnorm_q4_K_{name}_{r}x{c}_one_launch", us, nb)
+
+            def two(i):
+                flh.rmsnorm_act_q8(xr, wn, yr, c, 1e-5, s)
+                flh.stream_dot(Q4_K, ws[i % len(ws)], r, c, yr, y, s)
+
+            us = B.time_graph(two, REPS)
+            op_entry(f"rmsnorm_q4_K_{name}_{r}x{c}_two_launches", us, nb)
+            del ws
         # spec-verify small N
         for r, c in [(14336, 4096), (4096, 14336)]:
             nb = r * flh.row_bytes(Q4_K, c)

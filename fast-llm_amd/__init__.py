@@ -190,6 +190,7 @@ _SIGS = {
     "flh_silu_mul": (_I, [_P, _P, _P, _U32, _U32, _U32, _U32, _P]),
     "flh_silu_mul_act_q8": (_I, [_P, _P, _P, _U32, _U32, _U32, _U32, _P]),
     "flh_rmsnorm_act_q8": (_I, [_P, _P, _P, _U32, C.c_float, _I, _P]),
+    "flh_rmsnorm_stream_dot": (_I, [_I, _P, _U64, _U32, _U32, _P, _P, C.c_float, _P, _P, _I, _U32, _U32, _P]),
     "flh_wmerge": (_I, [_P, _P, _P, _P, _P, _F, _U32, _U32, _U32, _U32, _U32, _U32, _P]),
     "flh_fill_normal": (_I, [_P, _SZ, _U64, _F, _F, _F, _F, _P]),
     "flh_quantize": (_I, [_I, _P, _U32, _U32, _P, _P]),
@@ -462,6 +463,17 @@ def rmsnorm_act_q8(x, wnorm, y, n, eps, stream: Stream, write_app: bool = True):
     """RMSNORM of one column (y = x * s * wnorm) and, with write_app, the
     ACT_Q8 appendices of y, in one launch."""
     check(lib().flh_rmsnorm_act_q8(_p(x), _p(wnorm), _p(y), n, eps, int(bool(write_app)), stream.handle))
+
+
+def rmsnorm_stream_dot(fmt: int, w, rows: int, cols: int, x, wnorm, eps: float, xn, y, stream: Stream,
+                       fast: bool = True, i8_mask: int = I8_MASK_DEFAULT,
+                       i8k_mask: int = I8K_MASK_DEFAULT) -> None:
+    """RMSNORM of x into xn (with its ACT_Q8 appendices), then y += W xn
+    (one launch where the kernel takes it; the bits of rmsnorm_act_q8 followed
+    by stream_dot either way)."""
+    w_bytes = rows * row_bytes(fmt, cols)
+    check(lib().flh_rmsnorm_stream_dot(int(fmt), _p(w), w_bytes, rows, cols, _p(x), _p(wnorm), eps, _p(xn),
+                                       _p(y), int(bool(fast)), i8_mask, i8k_mask, stream.handle))
 
 
 def wmerge(parts, gates, add1, add2, y, scale, n_parts, n, n_full, ncol, pstride, ystride,

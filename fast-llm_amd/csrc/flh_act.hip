@@ -55,8 +55,8 @@ __global__ __launch_bounds__(64) void k_silu_act_q8(const float * gate, const fl
 
 // RMSNORM of one column with (write_app) the ACT_Q8 of its output, one
 // workgroup of 16 waves: the sum of squares as thread partials (elements
-// 4t..4t+3, 4t+4096.. in order) -> a wave butterfly (every lane ends with the
-// same sum) -> the 16 wave sums in wave order; s = 1 / sqrtf(ss / n + eps)
+// 4t..4t+3, 4t+4096.. in order) -> a wave butterfly (xor_lane exchanges;
+// every lane ends with the same sum) -> the 16 wave sums in wave order; s = 1 / sqrtf(ss / n + eps)
 // (correctly rounded sqrt and division, as the reference's libm); then wave w
 // quantises chunks w, w + 16, ... with y = (x * s) * wnorm computed in the
 // registers it quantises, so the appendices hold ACT_Q8's bytes for the
@@ -72,7 +72,7 @@ __global__ __launch_bounds__(1024) void k_rmsnorm_act_q8(const float * x, const 
         for (int j = 0; j < 4; ++j)
             if (e0 + j < n) ss += x[e0 + j] * x[e0 + j];
 #pragma unroll
-    for (int o = 1; o < 64; o <<= 1) ss += __shfl_xor(ss, o);
+    for (int o = 1; o < 64; o <<= 1) ss += xor_lane(ss, o, lane);
     if (lane == 0) part[wave] = ss;
     __syncthreads();
     if (tid == 0) {
@@ -126,7 +126,7 @@ __global__ __launch_bounds__(1024) void k_rmsnorm_act_q8_reg(const float * x, co
             ss += xv[k].w * xv[k].w;
         }
 #pragma unroll
-    for (int o = 1; o < 64; o <<= 1) ss += __shfl_xor(ss, o);
+    for (int o = 1; o < 64; o <<= 1) ss += xor_lane(ss, o, lane);
     if (lane == 0) part[wave] = ss;
     __syncthreads();
     float t = 0.f;

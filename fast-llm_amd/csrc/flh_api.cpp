@@ -378,6 +378,36 @@ int flh_act_q8_stream_dot(int fmt, const void * w, uint64_t w_bytes, uint32_t ro
     return dispatch_dot(fmt, a, fast, i8_mask, i8k_mask, s);
 }
 
+// RMSNORM -> ACT_Q8 -> one-column dot in one launch where the superblock-per-
+// lane kernel takes it (Q4_K on the int8 path), else the two calls.
+static int rmsnorm_dot(int fmt, const DotArgs & a, const NormArgs & nm, int fast, uint32_t i8_mask,
+                       uint32_t i8k_mask, hipStream_t s) {
+    const float * xb = nm.x, * xe = nm.x + a.cols;
+    const float * yb = a.x, * ye = (const float *)((const uint8_t *)a.x + x_alloc_bytes(a.cols));
+    const bool overlap = xb < ye && yb < xe;
+    if (fast && !overlap && fmt == FLH_FMT_Q4_K && ((i8k_mask >> fmt) & 1u) && a.cols <= 8192 && tune().sbl) {
+        const int rc = launch_dot_sbl(fmt, a, true, s, &nm);
+        if (rc != FLH_ERR_UNSUPPORTED) return rc;
+    }
+    if (int rc = launch_rmsnorm_act_q8(nm.x, nm.wn, (float *)a.x, a.cols, nm.eps, true, s)) return rc;
+    return dispatch_dot(fmt, a, fast, i8_mask, i8k_mask, s);
+}
+
+int flh_rmsnorm_stream_dot(int fmt, const void * w, uint64_t w_bytes, uint32_t rows, uint32_t cols, const float * x,
+                           const float * wnorm, float eps, float * xn, float * y, int fast, uint32_t i8_mask,
+                           uint32_t i8k_mask, void * stream) {
+    if (int rc = validate_dot(fmt, w, w_bytes, rows, cols, xn, y, 1, nullptr, 0)) return rc;
+    if (!x || !wnorm || ((uintptr_t)x & 15) || ((uintptr_t)wnorm & 15) || ((uintptr_t)xn & 15))
+        return set_error(FLH_ERR_ARG, "rmsnorm dot: x, wnorm, xn non-null and 16-byte aligned");
+    if (cols % 256) return set_error(FLH_ERR_ARG, "rmsnorm dot: cols must be a multiple of 256 (the q8_K appendix)");
+    if (int rc = need_init()) return rc;
+    const float * xe = x + cols;
+    const float * ye = (const float *)((const uint8_t *)xn + x_alloc_bytes(cols));
+    if (x < ye && xn < xe) return set_error(FLH_ERR_ARG, "rmsnorm dot: xn overlaps x");
+    DotArgs a{(const uint8_t *)w, nullptr, 0, xn, y, rows, cols, 1u, 0, 0};
+    return rmsnorm_dot(fmt, a, NormArgs{x, wnorm, eps}, fast, i8_mask, i8k_mask, (hipStream_t)stream);
+}
+
 int flh_dequant(int fmt, const void * w, uint32_t rows, uint32_t cols, float * out, void * stream) {
     if (int rc = need_init()) return rc;
     if (cols % blk_elems(fmt)) return set_error(FLH_ERR_ARG, "dequant: cols not a multiple of the block size");
@@ -454,6 +484,17 @@ int flh_exec_tasks(const flh_task * t, uint32_t n, int fast, uint32_t i8_mask, u
                 const bool fuse = q && q->kind == FLH_TASK_ACT_Q8 && q->x == (const void *)p.y && q->cols == p.n &&
                                   (const uint8_t *)q->y == (const uint8_t *)p.y + xq_off(p.n) &&
                                   !((uintptr_t)p.y & 15);
+                // ... and a single-column dot of that activation: one launch
+                const flh_task * d = fuse && i + 2 < n ? &t[i + 2] : nullptr;
+                if (d && d->kind == FLH_TASK_STREAM_DOT && d->x == (const void *)p.y && d->cols == p.n &&
+                    (d->nx ? d->nx : 1u) == 1 && p.n % 256 == 0 && !((uintptr_t)p.x & 15) &&
+                    !((uintptr_t)p.wnorm & 15)) {
+                    DotArgs a{(const uint8_t *)d->w, nullptr, 0, (const float *)d->x, (float *)d->y, d->rows, d->cols,
+                              1u, d->xstride, d->ystride};
+                    rc = rmsnorm_dot(d->fmt, a, NormArgs{p.x, p.wnorm, p.eps}, fast, i8_mask, i8k_mask, s);
+                    i += 2;
+                    break;
+                }
                 rc = launch_rmsnorm_act_q8(p.x, p.wnorm, p.y, p.n, p.eps, fuse, s);
                 if (fuse) ++i;
                 break;

@@ -82,6 +82,30 @@ __device__ __forceinline__ int qx2(int v) {
 }
 __device__ __forceinline__ float qx1f(float v) { return __int_as_float(qx1(__float_as_int(v))); }
 __device__ __forceinline__ float qx2f(float v) { return __int_as_float(qx2(__float_as_int(v))); }
+// The value of lane ^ o (o = 1, 2, 4, 8, 16, 32) in the calling lane: the data
+// __shfl_xor(v, o) returns, moved by DPP (quad permutations, row shifts by 4,
+// row rotation by 8) and the gfx950 permlane swaps (rows of 16, halves of
+// 32) instead of an LDS permute.  o must be a compile-time constant.
+__device__ __forceinline__ float xor_lane(float v, int o, uint32_t lane) {
+    const int x = __float_as_int(v);
+    if (o == 1) return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, false));
+    if (o == 2) return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, false));
+    if (o == 4) {
+        const int l4 = __builtin_amdgcn_mov_dpp(x, 0x104, 0xF, 0xF, false);   // row_shl:4 (lane + 4)
+        const int r4 = __builtin_amdgcn_mov_dpp(x, 0x114, 0xF, 0xF, false);   // row_shr:4 (lane - 4)
+        return __int_as_float((lane & 4) ? r4 : l4);
+    }
+    if (o == 8) return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0x128, 0xF, 0xF, false));   // row_ror:8
+    if (o == 16) {
+        // odd rows of the first operand <-> even rows of the second
+        const auto sw = __builtin_amdgcn_permlane16_swap((uint32_t)x, (uint32_t)x, false, false);
+        return __uint_as_float((lane & 16) ? sw[0] : sw[1]);
+    }
+    // upper half of the first operand <-> lower half of the second
+    const auto sw = __builtin_amdgcn_permlane32_swap((uint32_t)x, (uint32_t)x, false, false);
+    return __uint_as_float((lane & 32) ? sw[0] : sw[1]);
+}
+
 // DPP row mirrors: lane i <- lane 7-i inside each 8-lane half row, and lane
 // i <- lane 15-i inside each 16-lane row.
 __device__ __forceinline__ int hmir(int v) { return __builtin_amdgcn_mov_dpp(v, 0x141, 0xF, 0xF, false); }

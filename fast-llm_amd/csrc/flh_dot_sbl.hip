@@ -565,9 +565,10 @@ __device__ __forceinline__ void sbl_iq(const uint8_t * st, uint32_t lane, uint32
 // whose activation is column p (per-slot x) or the token's; the pair's
 // expert is known only after routing, so its weight requests wait for that,
 // while the y and activation DMAs go out first.
-template <int FMT, bool FUSE, int W, bool MOE = false>
+template <int FMT, bool FUSE, int W, bool MOE = false, bool NORM = false>
 __global__ __launch_bounds__(64 * W) void k_dot_sbl(DotArgs a, uint32_t rpc, uint32_t ni, uint32_t slot, uint32_t pre,
-                                                    MoeArgs m) {
+                                                    MoeArgs m, NormArgs nm) {
+    static_assert(!NORM || (FUSE && (W == 4 || W == 8)), "RMSNORM rides on the fused quantisation, 16 % W == 0");
     static_assert(FMT == FMT_Q4_K || !FUSE, "only Q4_K fuses the quantisation");
     static_assert(FMT != FMT_Q6_K || !MOE, "Q6_K experts run on the grouped streaming kernel");
     static_assert(!MOE || !FUSE, "the routed launch reads a ready appendix");
@@ -644,10 +645,18 @@ __global__ __launch_bounds__(64 * W) void k_dot_sbl(DotArgs a, uint32_t rpc, uin
     // ring stage (its first chunk is requested after the quantisation)
     const uint32_t nfi = FUSE ? (nsb > wave ? (nsb - wave + W - 1) / W : 0u) : 0u;   // <= 8 (host check)
     if constexpr (FUSE) {
+        // NORM: the input column instead, and the norm weights of the same
+        // superblocks after it (nfi <= 4, host check)
+        const float * xsrc = NORM ? nm.x : a.x;
         for (uint32_t j = 0; j < nfi; ++j) {
-            __builtin_amdgcn_global_load_lds(GPTR(a.x + 256 * (wave + W * j) + 4 * lane), LPTR(ring + slot + 1024 * j),
+            __builtin_amdgcn_global_load_lds(GPTR(xsrc + 256 * (wave + W * j) + 4 * lane), LPTR(ring + slot + 1024 * j),
                                              16, 0, 0);
             ++ops;
+            if constexpr (NORM) {
+                __builtin_amdgcn_global_load_lds(GPTR(nm.wn + 256 * (wave + W * j) + 4 * lane),
+                                                 LPTR(ring + slot + 1024 * (4 + j)), 16, 0, 0);
+                ++ops;
+            }
         }
     } else if constexpr (Q8) {
         // q8_1 block j as three 16-byte pieces starting 12 bytes early (the
@@ -729,7 +738,65 @@ __global__ __launch_bounds__(64 * W) void k_dot_sbl(DotArgs a, uint32_t rpc, uin
             lds_st32(xb + 48 + 4 * lane, pk);
             if ((lane & 3) == 0) lds_st16(xb + 16 + 2 * (lane >> 2), (uint32_t)s16);
             if (lane == 0) lds_st32(xb + 12, __float_as_uint(d));
-            if (s % G == b) write_appendices(v, lane, s, q81, q8k, cols);   // each block by one workgroup
+            if (s % G == b) {                                     // each block by one workgroup
+                if constexpr (NORM) *(float4 *)((float *)a.x + 256 * s + 4 * lane) = make_float4(v[0], v[1], v[2], v[3]);
+                write_appendices(v, lane, s, q81, q8k, cols);
+            }
+        };
+        // NORM: the sum of squares in k_rmsnorm_act_q8_reg's order.  Its
+        // thread (v, l) sums elements 4l .. 4l + 3 of superblocks v, v + 16,
+        // ... in turn, a butterfly makes the 64-lane total of "wave" v, and
+        // every thread adds the 16 totals in order.  Here superblock s sits in
+        // wave s % W (W divides 16), so wave w holds the partials of v = w +
+        // W q, q < 16 / W, for its items j = q, q + 16 / W, ... (nfi <= 4).
+        float nrm_s = 0.f;
+        if constexpr (NORM) {
+            __shared__ __attribute__((aligned(16))) float nparts[16];
+            constexpr uint32_t NQ = 16 / W;
+            float ss[NQ];
+#pragma unroll
+            for (uint32_t q = 0; q < NQ; ++q) ss[q] = 0.f;
+#pragma unroll
+            for (uint32_t j = 0; j < 4; ++j) {
+                if (j < nfi) {
+                    const u32x4a r = lds_ld128(xf + 1024 * j);
+                    const float x0 = __uint_as_float(r.x), x1 = __uint_as_float(r.y);
+                    const float x2 = __uint_as_float(r.z), x3 = __uint_as_float(r.w);
+                    float & t = ss[j % NQ];
+                    t += x0 * x0;
+                    t += x1 * x1;
+                    t += x2 * x2;
+                    t += x3 * x3;
+                }
+            }
+            // the butterfly ss += (value of lane ^ o), o = 1, 2, ..., 32
+            // (xor_lane: the values of __shfl_xor without LDS round trips)
+#pragma unroll
+            for (uint32_t q = 0; q < NQ; ++q) {
+#pragma unroll
+                for (int o = 1; o < 64; o <<= 1) ss[q] += xor_lane(ss[q], o, lane);
+                if (lane == 0) lds_st32(&nparts[wave + W * q], __float_as_uint(ss[q]));
+            }
+            lds_barrier();                                        // (no wait for the weight DMAs)
+            u32x4a p0 = lds_ld128_nw(&nparts[0]), p1 = lds_ld128_nw(&nparts[4]);
+            u32x4a p2 = lds_ld128_nw(&nparts[8]), p3 = lds_ld128_nw(&nparts[12]);
+            lds_wait4(p0, p1, p2, p3);                            // one LDS round trip for the 16 totals
+            const uint32_t pv[16] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w,
+                                     p2.x, p2.y, p2.z, p2.w, p3.x, p3.y, p3.z, p3.w};
+            float tn = 0.f;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) tn += __uint_as_float(pv[v]);
+            nrm_s = 1.0f / sqrtf(tn / (float)cols + nm.eps);
+        }
+        // y = (x * s) * wn of the lane's 4 elements (NORM), in place
+        auto normed = [&](float (&v)[4], uint32_t j) {
+            if constexpr (NORM) {
+                const u32x4a wr = lds_ld128(xf + 1024 * (4 + j));
+                const float wv[4] = {__uint_as_float(wr.x), __uint_as_float(wr.y), __uint_as_float(wr.z),
+                                     __uint_as_float(wr.w)};
+#pragma unroll
+                for (int k = 0; k < 4; ++k) v[k] = v[k] * nrm_s * wv[k];
+            }
         };
 #pragma unroll 1
         for (uint32_t j = 0; j < nfi; j += 2) {
@@ -738,10 +805,10 @@ __global__ __launch_bounds__(64 * W) void k_dot_sbl(DotArgs a, uint32_t rpc, uin
             u32x4a ra = lds_ld128_nw(xf + 1024 * j), rb = lds_ld128_nw(xf + 1024 * (two ? j + 1 : j));
             u32x4a r2 = ra, r3 = rb;
             lds_wait4(ra, rb, r2, r3);
-            const float va[4] = {__uint_as_float(ra.x), __uint_as_float(ra.y), __uint_as_float(ra.z),
-                                 __uint_as_float(ra.w)};
-            const float vb[4] = {__uint_as_float(rb.x), __uint_as_float(rb.y), __uint_as_float(rb.z),
-                                 __uint_as_float(rb.w)};
+            float va[4] = {__uint_as_float(ra.x), __uint_as_float(ra.y), __uint_as_float(ra.z), __uint_as_float(ra.w)};
+            float vb[4] = {__uint_as_float(rb.x), __uint_as_float(rb.y), __uint_as_float(rb.z), __uint_as_float(rb.w)};
+            normed(va, j);
+            normed(vb, two ? j + 1 : j);
             const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(absmax4(va)), __float_as_uint(absmax4(vb)),
                                                              false, false);
             uint32_t m = umax8(max((uint32_t)sw[0], (uint32_t)sw[1]));
@@ -1251,7 +1318,7 @@ static size_t sbl_smem(bool q8, bool iq, uint32_t W, uint32_t slot, uint32_t nsb
     return (size_t)W * 2 * slot + xs + (size_t)W * ((q8 ? 4096 : 1024) + 256) + (iq ? 3072 : 0);
 }
 
-int launch_dot_sbl(int fmt, const DotArgs & a, bool fuse, hipStream_t s) {
+int launch_dot_sbl(int fmt, const DotArgs & a, bool fuse, hipStream_t s, const NormArgs * norm) {
     const bool iq = fmt == FMT_IQ2_XXS || fmt == FMT_IQ3_XXS;
     const bool q8 = fmt == FMT_Q8_0 || fmt == FMT_Q5_0 || iq;     // 32-weight blocks
     const bool q6 = fmt == FMT_Q6_K;
@@ -1284,7 +1351,10 @@ int launch_dot_sbl(int fmt, const DotArgs & a, bool fuse, hipStream_t s) {
     //  * Q5_0 and the IQ formats, more VALU work per byte: 8 waves, all
     //    early (14336x4096 Q5_0 15.2 -> 11.9 us, IQ2_XXS 16.6 -> 12.2,
     //    IQ3_XXS 18.3 -> 13.5 against 4 waves).
-    if (fuse && !t.sbl_w && (uint64_t)a.rows * nsb > (1u << 18)) return FLH_ERR_UNSUPPORTED;
+    // (NORM: against an RMSNORM launch of its own, at every size)
+    if (fuse && !norm && !t.sbl_w && (uint64_t)a.rows * nsb > (1u << 18)) return FLH_ERR_UNSUPPORTED;
+    if (norm && (fmt != FMT_Q4_K || !fuse || ((uintptr_t)norm->x & 15) || ((uintptr_t)norm->wn & 15)))
+        return FLH_ERR_UNSUPPORTED;
     // Q6_K: its 6-bit decode is VALU-heavy and a 12-14 KB chunk leaves room
     // for 4 waves only, so the four-lanes-per-superblock kernel stays faster
     // unless the matrix is large enough for the streaming rate to dominate
@@ -1298,6 +1368,8 @@ int launch_dot_sbl(int fmt, const DotArgs & a, bool fuse, hipStream_t s) {
     const size_t smb = sbl_smem(q8, iq, W, slot, nsb);
     if (smb > lds_limit() || (W != 8 && W != 6 && W != 4)) return FLH_ERR_UNSUPPORTED;
     if (fuse && (nsb + W - 1) / W > 8) return FLH_ERR_UNSUPPORTED;
+    // NORM: the items' fp32 x and norm weights share the second ring stage
+    if (norm && ((W != 8 && W != 4) || (nsb + W - 1) / W > 4 || 8 * 1024 > slot)) return FLH_ERR_UNSUPPORTED;
     const uint32_t C = (a.rows + rpc - 1) / rpc;
     const uint32_t wpc = t.sbl_wpc ? t.sbl_wpc : 1;
     uint32_t G = (uint32_t)num_cus() * wpc;
@@ -1305,7 +1377,8 @@ int launch_dot_sbl(int fmt, const DotArgs & a, bool fuse, hipStream_t s) {
     if (G > C) G = C;
     auto go = [&](auto kern) {
         (void)hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smb);
-        hipLaunchKernelGGL(kern, dim3(G), dim3(64 * W), smb, s, a, rpc, ni, slot, pre, MoeArgs{});
+        hipLaunchKernelGGL(kern, dim3(G), dim3(64 * W), smb, s, a, rpc, ni, slot, pre, MoeArgs{},
+                           norm ? *norm : NormArgs{});
         return hip_check(hipGetLastError(), "k_dot_sbl launch");
     };
     auto unfused = [&](auto fmt_tag) {
@@ -1323,6 +1396,7 @@ int launch_dot_sbl(int fmt, const DotArgs & a, bool fuse, hipStream_t s) {
         default: break;
     }
     if (!fuse) return unfused(std::integral_constant<int, FMT_Q4_K>());
+    if (norm) return W == 8 ? go(k_dot_sbl<FMT_Q4_K, true, 8, false, true>) : go(k_dot_sbl<FMT_Q4_K, true, 4, false, true>);
     if (W == 8) return go(k_dot_sbl<FMT_Q4_K, true, 8>);
     if (W == 6) return go(k_dot_sbl<FMT_Q4_K, true, 6>);
     return go(k_dot_sbl<FMT_Q4_K, true, 4>);
@@ -1461,7 +1535,7 @@ int launch_moe_sbl(int fmt, const MoeArgs & m, hipStream_t s) {
     a.nx = 1;
     auto go = [&](auto kern) {
         (void)hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smb);
-        hipLaunchKernelGGL(kern, dim3(gx, pairs), dim3(64 * W), smb, s, a, rpc, ni, slot, pre, m);
+        hipLaunchKernelGGL(kern, dim3(gx, pairs), dim3(64 * W), smb, s, a, rpc, ni, slot, pre, m, NormArgs{});
         return hip_check(hipGetLastError(), "k_dot_sbl (moe) launch");
     };
     auto routed = [&](auto fmt_tag) {

@@ -20,6 +20,16 @@ struct DotArgs {
     uint32_t rows, cols, nx, xstride, ystride;
 };
 
+// RMSNORM in front of a fused ACT_Q8 dot: the activation buffer of the dot
+// (DotArgs::x) receives y = (x * s) * wn and its appendices, with
+// s = 1 / sqrtf(sum(x^2) / n + eps) over the column x (fl_op_rmsnorm,
+// src/runtime/decode_params.h:101-106).
+struct NormArgs {
+    const float * x;
+    const float * wn;
+    float eps;
+};
+
 // Grouped expert launch (MoE): for every expert e with at least one routed
 // (token, slot) pair, the columns are those pairs:
 //   y[(tok*top_k + slot)*ystride + r] += dot(W_e[r], x + xcol(tok,slot)*xstride)
@@ -95,7 +105,7 @@ int launch_dot_kstream(int fmt, const DotArgs & a, hipStream_t s);
 // (flh_dot_sbl.hip): Q4_K (fuse: ACT_Q8 of the fp32 column in the same
 // launch), Q6_K, Q8_0, Q5_0, IQ2_XXS, IQ3_XXS.  FLH_ERR_UNSUPPORTED (nothing
 // launched) if the shape does not fit its plan or another kernel is faster.
-int launch_dot_sbl(int fmt, const DotArgs & a, bool fuse, hipStream_t s);
+int launch_dot_sbl(int fmt, const DotArgs & a, bool fuse, hipStream_t s, const NormArgs * norm = nullptr);
 // 2..8 activation columns of Q8_0 / Q5_0 / IQ2_XXS / IQ3_XXS on the
 // superblock-per-lane layout (FLH_ERR_UNSUPPORTED: nothing launched)
 int launch_dot_sbl_nx(int fmt, const DotArgs & a, hipStream_t s);

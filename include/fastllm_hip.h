@@ -217,13 +217,28 @@ int flh_act_q8_stream_dot(int fmt, const void * w, uint64_t w_bytes, uint32_t ro
                           const uint32_t * id_slot, uint64_t estride, int fast,
                           uint32_t i8_mask, uint32_t i8k_mask, void * stream);
 
+/* RMSNORM of the column x (fl_op_rmsnorm, src/runtime/decode_params.h:101-106)
+ * into xn -- fp32 y followed by its ACT_Q8 appendices, as flh_rmsnorm_act_q8
+ * writes them with write_app = 1 -- then the single-column dot of it,
+ * y[r] += dot(W[r], ACT_Q8(xn)) as flh_stream_dot: the decoder's
+ * norm -> quant -> matvec chain (src/model/decoder.cpp:874-880; the tasks
+ * RMSNORM, ACT_Q8, STREAM_DOT).  A Q4_K dot on the int8 path with at most
+ * 8192 columns runs all three in one launch; anything else runs
+ * flh_rmsnorm_act_q8 then flh_stream_dot.  The results are those of the two
+ * calls, bit for bit.  x, wnorm and xn 16-byte aligned; xn must not overlap x. */
+int flh_rmsnorm_stream_dot(int fmt, const void * w, uint64_t w_bytes, uint32_t rows,
+                           uint32_t cols, const float * x, const float * wnorm, float eps,
+                           float * xn, float * y, int fast, uint32_t i8_mask,
+                           uint32_t i8k_mask, void * stream);
+
 /* Execute a task table in array order on one stream (replaces the persistent
  * executor's per-task dispatch, exec_task_block, src/runtime/gpu_exec.cu:
  * 64-140, for a topologically ordered table such as run_serial walks,
  * src/runtime/graph.cpp:116-148).  Supported kinds: STREAM_DOT,
  * STREAM_DOT_IDX, ACT_Q8, MERGE, SIGNAL, RMSNORM, ROUTER_SEL, SILU_MUL,
  * WMERGE (an RMSNORM followed by the ACT_Q8 of its output is one
- * flh_rmsnorm_act_q8 launch);
+ * flh_rmsnorm_act_q8 launch, and with a single-column STREAM_DOT of that
+ * activation after them, one flh_rmsnorm_stream_dot);
  * anything else -> FLH_ERR_UNSUPPORTED before any launch.  Consecutive
  * STREAM_DOT row tiles of one matrix (same fmt/cols/x/nx/strides, w and y
  * contiguous) are fused into one launch, and an ACT_Q8 followed by its

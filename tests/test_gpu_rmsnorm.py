@@ -16,7 +16,7 @@ import numpy as np
 import pytest
 
 from oracle import Q4_K, col_stride_floats, x_alloc_bytes
-from util import sane_rows
+from util import sane_rows, tuned
 
 pytestmark = pytest.mark.gpu
 
@@ -81,3 +81,42 @@ def test_rmsnorm_task_pair_fuses(flh, orc, gpu):
     dy2 = flh.DeviceBuffer.from_array(np.zeros(st, np.float32), gpu)
     flh.rmsnorm_act_q8(dx, dwn, dy2, n, 1e-5, gpu)
     assert np.array_equal(bits(dy2.download(np.float32, st, gpu)), bits(yb))
+
+
+@pytest.mark.parametrize("cfg", ["1", "1,4", "1,8,1,5,2"])
+@pytest.mark.parametrize("rows,n", [(5, 256), (9, 1024), (50, 2048), (300, 4096), (6144, 4096), (28672, 4096),
+                                    (77, 8192), (33, 14336)])
+def test_rmsnorm_stream_dot(flh, orc, gpu, cfg, rows, n):
+    """RMSNORM -> ACT_Q8 -> Q4_K dot in one launch (flh_rmsnorm_stream_dot;
+    14336 columns take the two-launch path): the normalised column, its
+    appendices and y += W xn equal rmsnorm_act_q8 followed by stream_dot bit
+    for bit, y is within the sequential-sum bound of the reference, and the
+    dot equals the oracle's on the stored column."""
+    print("[case] rmsnorm dot", cfg, rows, n, flush=True)
+    rng = np.random.default_rng(rows + n)
+    x = (rng.standard_normal(n) * 3).astype(np.float32)
+    wn = (1 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+    w = sane_rows(Q4_K, rows, n, rng)
+    y0 = rng.standard_normal(rows).astype(np.float32)
+    st = col_stride_floats(n)
+    dx = flh.DeviceBuffer.from_array(x, gpu)
+    dwn = flh.DeviceBuffer.from_array(wn, gpu)
+    dw = flh.DeviceBuffer.from_array(w, gpu)
+    outs = []
+    for fused in (True, False):
+        dxn = flh.DeviceBuffer.from_array(np.zeros(st, np.float32), gpu)
+        dy = flh.DeviceBuffer.from_array(y0, gpu)
+        with tuned(flh, FLH_SBL=cfg):
+            if fused:
+                flh.rmsnorm_stream_dot(Q4_K, dw, rows, n, dx, dwn, 1e-5, dxn, dy, gpu)
+            else:
+                flh.rmsnorm_act_q8(dx, dwn, dxn, n, 1e-5, gpu)
+                flh.stream_dot(Q4_K, dw, rows, n, dxn, dy, gpu)
+        outs.append((dxn.download(np.float32, st, gpu), dy.download(np.float32, rows, gpu)))
+    (xa, ya), (xb, yb) = outs
+    assert np.array_equal(bits(xa), bits(xb)), "normalised column and appendices"
+    assert np.array_equal(bits(ya), bits(yb)), "dot"
+    check_y(xa[:n], orc.rmsnorm(x, wn, 1e-5), n)
+    want = y0.copy()
+    orc.stream_dot(Q4_K, w, rows, n, xa, want)
+    assert np.array_equal(bits(ya), bits(want))
