@@ -19,7 +19,8 @@ Also reported (same JSON line):
               IQ2_XXS / IQ3_XXS matvecs, 2/4/8-column dots of those formats
               and Q8_0 at 14336x4096, the activation quantisers
               (ACT_Q8 14336, RMSNORM -> ACT_Q8 4096) and RMSNORM -> QKV /
-              gate/up in one launch against two;
+              gate/up in one launch against two, and the decoder's whole
+              norm -> matvec chain of a layer (5 launches);
   roofline -- the dominant kernel (Q4_K gate/up): algorithmic bytes per
               launch / average launch time vs the 8 TB/s HBM peak;
   cpu_baseline -- the reference CPU path on the host cores (oracle/_ref,
@@ -233,6 +234,32 @@ def main():
 
     REPS = 64
     cpu_in = {}          # host copies of each config's bytes for the CPU baseline
+    # The decoder's own chain over the same matrices (not the headline): the
+    # attention norm + QKV in one launch, ACT_Q8 + O, the FFN norm + gate/up
+    # in one launch, SILU_MUL + ACT_Q8 of the down input, down: 5 launches,
+    # each depending on nothing but the previous in stream order.
+    D_, F_ = 4096, 14336
+    x0, _ = B.activation(D_, 1, 80, outliers=True)
+    wn1, wn2 = B.buf(D_ * 4), B.buf(D_ * 4)
+    flh.fill_normal(wn1, D_, 81, s, mean=1.0, std=0.1)
+    flh.fill_normal(wn2, D_, 82, s, mean=1.0, std=0.1)
+    xn1, _ = B.activation(D_, 1, 83, outliers=False)
+    xn2, _ = B.activation(D_, 1, 84, outliers=False)
+    h, _ = B.activation(F_, 1, 85, outliers=False)
+    gu = yout["gate_up"]
+
+    def chain(i):
+        l = i % L
+        flh.rmsnorm_stream_dot(Q4_K, W["qkv"][l], 6144, D_, x0, wn1, 1e-5, xn1, yout["qkv"], s)
+        flh.act_q8_stream_dot(Q4_K, W["o"][l], D_, D_, xin["o"][0], yout["o"], s)
+        flh.rmsnorm_stream_dot(Q4_K, W["gate_up"][l], 2 * F_, D_, x0, wn2, 1e-5, xn2, gu, s)
+        flh.silu_mul_act_q8(gu, gu.ptr + F_ * 4, h, F_, 1, 2 * F_, col_stride(flh, F_), s)
+        flh.stream_dot(Q4_K, W["down"][l], D_, F_, h, yout["down"], s)
+
+    us = B.time_graph(chain, REPS)
+    op_entry("decoder_chain_q4_K_layer", us, layer_bytes,
+             {"launches": 5, "ops": "RMSNORM->ACT_Q8->QKV, ACT_Q8->O, RMSNORM->ACT_Q8->gate/up, "
+                                    "SILU_MUL->ACT_Q8, down (one launch per arrow chain)"})
     for name, r, c in LAYER:
         x, st = xin[name]
         nb = r * flh.row_bytes(Q4_K, c)
