@@ -120,3 +120,75 @@ def test_rmsnorm_stream_dot(flh, orc, gpu, cfg, rows, n):
     want = y0.copy()
     orc.stream_dot(Q4_K, w, rows, n, xa, want)
     assert np.array_equal(bits(ya), bits(want))
+
+
+@pytest.mark.parametrize("fmt", [1, 4])          # Q8_0, Q6_K: the two-launch path
+def test_rmsnorm_stream_dot_other_formats(flh, orc, gpu, fmt):
+    """Formats the one-launch kernel does not take give the separate calls' bits."""
+    print("[case] rmsnorm dot fmt", fmt, flush=True)
+    rows, n = 200, 4096
+    rng = np.random.default_rng(fmt)
+    x = rng.standard_normal(n).astype(np.float32)
+    wn = (1 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+    w = sane_rows(fmt, rows, n, rng)
+    st = col_stride_floats(n)
+    dx, dwn, dw = (flh.DeviceBuffer.from_array(a, gpu) for a in (x, wn, w))
+    outs = []
+    for fused in (True, False):
+        dxn = flh.DeviceBuffer.from_array(np.zeros(st, np.float32), gpu)
+        dy = flh.DeviceBuffer.from_array(np.zeros(rows, np.float32), gpu)
+        if fused:
+            flh.rmsnorm_stream_dot(fmt, dw, rows, n, dx, dwn, 1e-5, dxn, dy, gpu)
+        else:
+            flh.rmsnorm_act_q8(dx, dwn, dxn, n, 1e-5, gpu)
+            flh.stream_dot(fmt, dw, rows, n, dxn, dy, gpu)
+        outs.append((dxn.download(np.float32, st, gpu), dy.download(np.float32, rows, gpu)))
+    assert np.array_equal(bits(outs[0][0]), bits(outs[1][0]))
+    assert np.array_equal(bits(outs[0][1]), bits(outs[1][1]))
+
+
+def test_rmsnorm_stream_dot_rejects_overlap(flh, gpu):
+    """xn overlapping x is an argument error (the launch would read x while
+    other workgroups write y); nothing is launched."""
+    n, rows = 4096, 16
+    st = col_stride_floats(n)
+    buf = flh.DeviceBuffer.from_array(np.ones(2 * st, np.float32), gpu)
+    wn = flh.DeviceBuffer.from_array(np.ones(n, np.float32), gpu)
+    w = flh.DeviceBuffer.from_array(sane_rows(Q4_K, rows, n, np.random.default_rng(0)), gpu)
+    y = flh.DeviceBuffer.from_array(np.zeros(rows, np.float32), gpu)
+    with pytest.raises(flh.FlhError):
+        flh.rmsnorm_stream_dot(Q4_K, w, rows, n, buf, wn, 1e-5, buf.ptr + 1024, y, gpu)
+
+
+def test_rmsnorm_dot_triple_in_graph(flh, orc, gpu):
+    """RMSNORM + ACT_Q8 + STREAM_DOT in a HIP graph: every replay (with eager
+    work and synchronisations in between) gives the eager run's bits."""
+    n, rows = 4096, 6144
+    rng = np.random.default_rng(21)
+    x = rng.standard_normal(n).astype(np.float32)
+    wn = (1 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+    w = sane_rows(Q4_K, rows, n, rng)
+    st = col_stride_floats(n)
+    dx, dwn, dw = (flh.DeviceBuffer.from_array(a, gpu) for a in (x, wn, w))
+    dxn = flh.DeviceBuffer.from_array(np.zeros(st, np.float32), gpu)
+    dy = flh.DeviceBuffer.from_array(np.zeros(rows, np.float32), gpu)
+    p = flh.RmsNormP(dwn.ptr, dx.ptr, dxn.ptr, 1e-5, n)
+    T = flh.TaskKind
+    t0 = flh.Task(); t0.kind = int(T.RMSNORM); t0.aux = ctypes.addressof(p)
+    t1 = flh.Task(); t1.kind = int(T.ACT_Q8); t1.x = dxn.ptr; t1.y = dxn.ptr + flh.xq_offset(n); t1.rows = n // 32
+    t1.cols = n
+    t2 = flh.Task(); t2.kind = int(T.STREAM_DOT); t2.fmt = Q4_K; t2.w = dw.ptr; t2.w_bytes = w.size; t2.x = dxn.ptr
+    t2.y = dy.ptr; t2.rows = rows; t2.cols = n
+    tasks = [t0, t1, t2]
+    flh.exec_tasks(tasks, gpu)
+    ref = dy.download(np.float32, rows, gpu).copy()
+    refx = dxn.download(np.float32, st, gpu).copy()
+    with flh.Graph.capture(gpu) as g:
+        flh.exec_tasks(tasks, gpu)
+    for k in range(3):
+        dy.zero(gpu)
+        g.launch()
+        gpu.sync()
+        assert np.array_equal(bits(dy.download(np.float32, rows, gpu)), bits(ref)), k
+        assert np.array_equal(bits(dxn.download(np.float32, st, gpu)), bits(refx)), k
+    g.close()
