@@ -385,8 +385,12 @@ static int rmsnorm_dot(int fmt, const DotArgs & a, const NormArgs & nm, int fast
     const float * xb = nm.x, * xe = nm.x + a.cols;
     const float * yb = a.x, * ye = (const float *)((const uint8_t *)a.x + x_alloc_bytes(a.cols));
     const bool overlap = xb < ye && yb < xe;
-    if (fast && !overlap && fmt == FLH_FMT_Q4_K && ((i8k_mask >> fmt) & 1u) && a.cols <= 8192 && tune().sbl) {
-        const int rc = launch_dot_sbl(fmt, a, true, s, &nm);
+    if (fast && !overlap && fmt == FLH_FMT_Q4_K && ((i8k_mask >> fmt) & 1u) && a.cols <= 8192) {
+        // the kernel the plain fused ACT_Q8 dot takes at this size (above 2^18
+        // superblocks the four-lanes one)
+        int rc = FLH_ERR_UNSUPPORTED;
+        if ((uint64_t)a.rows * (a.cols >> 8) > (1u << 18) || !tune().sbl) rc = launch_norm_dot_kstream(a, nm, s);
+        if (rc == FLH_ERR_UNSUPPORTED && tune().sbl) rc = launch_dot_sbl(fmt, a, true, s, &nm);
         if (rc != FLH_ERR_UNSUPPORTED) return rc;
     }
     if (int rc = launch_rmsnorm_act_q8(nm.x, nm.wn, (float *)a.x, a.cols, nm.eps, true, s)) return rc;

@@ -34,10 +34,10 @@ namespace flh {
 // even split: workgroups differ by at most one row), streamed in batches of at
 // most nr rows.  Ends with every weight DMA
 // drained, so the caller may start another pass on the same LDS.
-template <int FMT, int NX, int D, bool FUSE, bool XREG, int KW = 4>
+template <int FMT, int NX, int D, bool FUSE, bool XREG, int KW = 4, bool NORM = false>
 __device__ __forceinline__ void ks_body(const uint8_t * __restrict__ w, uint32_t rows, uint32_t cols,
                                         const KsCols<NX> & C, uint32_t nx, uint32_t nrp,
-                                        uint32_t g, uint32_t G, uint8_t * sm) {
+                                        uint32_t g, uint32_t G, uint8_t * sm, const NormArgs & nm = NormArgs{}) {
     // nrp: rows per batch | chunks issued by the prologue << 16 (0: D)
     const uint32_t nr = nrp & 0xFFFF;
     const uint32_t pro = (nrp >> 16) ? min(nrp >> 16, (uint32_t)D) : (uint32_t)D;
@@ -146,7 +146,7 @@ __device__ __forceinline__ void ks_body(const uint8_t * __restrict__ w, uint32_t
     issue_y(0);
 
     // ---- activation records, once per workgroup (overlaps the first weight DMAs)
-    if constexpr (FUSE) ks_x_fuse<FMT, NX, NI, D, KW>(C, nx, nsb, cols, xr, xd, g, G, prologue);
+    if constexpr (FUSE) ks_x_fuse<FMT, NX, NI, D, KW, NORM>(C, nx, nsb, cols, xr, xd, g, G, prologue, nm);
     else ks_x_app<FMT, NX, NI, D>(C, nx, nsb, cols, xr, xd, prologue);
     lds_barrier();
     KS_STAMP(1);
@@ -212,8 +212,8 @@ __device__ __forceinline__ void ks_body(const uint8_t * __restrict__ w, uint32_t
     KS_STAMP(4);
 }
 
-template <int FMT, int NX, int D, bool FUSE, bool XREG, int KW = 4>
-__global__ __launch_bounds__(64 * KW) void k_dot_kstream(DotArgs a, uint32_t nr) {
+template <int FMT, int NX, int D, bool FUSE, bool XREG, int KW = 4, bool NORM = false>
+__global__ __launch_bounds__(64 * KW) void k_dot_kstream(DotArgs a, uint32_t nr, NormArgs nm) {
     extern __shared__ __attribute__((aligned(16))) uint8_t sm[];
     const uint8_t * w = a.w + (a.id_slot ? (size_t)(*a.id_slot) * a.estride : 0);
     KsCols<NX> C;
@@ -223,7 +223,7 @@ __global__ __launch_bounds__(64 * KW) void k_dot_kstream(DotArgs a, uint32_t nr)
         C.x[p] = a.x + (size_t)pp * a.xstride;
         C.y[p] = a.y + (size_t)pp * a.ystride;
     }
-    ks_body<FMT, NX, D, FUSE, XREG, KW>(w, a.rows, a.cols, C, a.nx, nr, blockIdx.x, gridDim.x, sm);
+    ks_body<FMT, NX, D, FUSE, XREG, KW, NORM>(w, a.rows, a.cols, C, a.nx, nr, blockIdx.x, gridDim.x, sm, nm);
 }
 
 // Grouped expert matvec: the routed experts share the grid (moe_assign).  The workgroup collects the
@@ -292,7 +292,8 @@ static int ks_launch_x(const DotArgs & a, uint32_t nr, uint32_t grid, size_t smb
     if (smb > 65536)
         (void)hipFuncSetAttribute((const void *)k_dot_kstream<FMT, NX, D, FUSE, XREG>,
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)smb);
-    hipLaunchKernelGGL((k_dot_kstream<FMT, NX, D, FUSE, XREG>), dim3(grid), dim3(256), smb, s, a, nr | (ks_pro(FUSE) << 16));
+    hipLaunchKernelGGL((k_dot_kstream<FMT, NX, D, FUSE, XREG>), dim3(grid), dim3(256), smb, s, a, nr | (ks_pro(FUSE) << 16),
+                       NormArgs{});
     return hip_check(hipGetLastError(), "k_dot_kstream launch");
 }
 template <int FMT, int NX, int D, bool FUSE>
@@ -354,7 +355,7 @@ static int ks_launch(const DotArgs & a, hipStream_t s) {
                 const uint32_t grid = a.rows < slots ? a.rows : slots;
                 auto go = [&](auto kern) {
                     (void)hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smb);
-                    hipLaunchKernelGGL(kern, dim3(grid), dim3(512), smb, s, a, nr | (ks_pro(FUSE) << 16));
+                    hipLaunchKernelGGL(kern, dim3(grid), dim3(512), smb, s, a, nr | (ks_pro(FUSE) << 16), NormArgs{});
                     return hip_check(hipGetLastError(), "k_dot_kstream launch");
                 };
                 if (16 % nsb == 0) return go(k_dot_kstream<FMT, 1, 2, FUSE, true, 8>);
@@ -404,6 +405,31 @@ static int moe_launch(const MoeArgs & a, hipStream_t s) {
         case 3: return moe_launch_d<FMT, NX, 3>(a, nr, g, smb, s);
         default: return moe_launch_d<FMT, NX, 4>(a, nr, g, smb, s);
     }
+}
+
+// RMSNORM -> ACT_Q8 -> Q4_K one-column dot on this kernel: 8-wave
+// workgroups (the plan of its fused single-column launches), at most 8
+// superblocks per wave (<= 16384 columns); FLH_ERR_UNSUPPORTED (nothing
+// launched) when the plan does not fit.
+int launch_norm_dot_kstream(const DotArgs & a, const NormArgs & nm, hipStream_t s) {
+    const uint32_t nsb = a.cols >> 8;
+    if (nsb == 0 || (a.cols & 255) || nsb > 64 || a.nx != 1 || ((uintptr_t)a.w & 15) || (a.estride & 15) ||
+        ((uintptr_t)a.x & 15) || ((uintptr_t)nm.x & 15) || ((uintptr_t)nm.wn & 15))
+        return FLH_ERR_UNSUPPORTED;
+    const Tune & t = tune();
+    const uint32_t slots = (uint32_t)num_cus() * (t.ks_w8_wgs ? t.ks_w8_wgs : 1);
+    uint32_t nr;
+    int D;
+    size_t smb;
+    if (ks_plan<FMT_Q4_K>(a.rows, 1, nsb, slots, 2, nr, D, smb, 8) != FLH_OK || D != 2) return FLH_ERR_UNSUPPORTED;
+    const uint32_t grid = a.rows < slots ? a.rows : slots;
+    auto go = [&](auto kern) {
+        (void)hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smb);
+        hipLaunchKernelGGL(kern, dim3(grid), dim3(512), smb, s, a, nr | (ks_pro(true) << 16), nm);
+        return hip_check(hipGetLastError(), "k_dot_kstream launch");
+    };
+    if (16 % nsb == 0) return go(k_dot_kstream<FMT_Q4_K, 1, 2, true, true, 8, true>);
+    return go(k_dot_kstream<FMT_Q4_K, 1, 2, true, false, 8, true>);
 }
 
 int launch_moe_kstream(int fmt, const MoeArgs & a, hipStream_t s) {

@@ -109,6 +109,9 @@ int launch_dot_sbl(int fmt, const DotArgs & a, bool fuse, hipStream_t s, const N
 // 2..8 activation columns of Q8_0 / Q5_0 / IQ2_XXS / IQ3_XXS on the
 // superblock-per-lane layout (FLH_ERR_UNSUPPORTED: nothing launched)
 int launch_dot_sbl_nx(int fmt, const DotArgs & a, hipStream_t s);
+// RMSNORM -> ACT_Q8 -> Q4_K one-column dot on the four-lanes-per-superblock
+// kernel (FLH_ERR_UNSUPPORTED: nothing launched)
+int launch_norm_dot_kstream(const DotArgs & a, const NormArgs & nm, hipStream_t s);
 // largest dynamic LDS of one workgroup on the current device
 size_t lds_limit();
 // ACT_Q8 fused into the kstream dot: quantises x (fp32) in-kernel, writes both

@@ -328,10 +328,19 @@ __device__ __forceinline__ void act_q8_lanes(const float (&v)[4], uint32_t lane,
 // so the bytes in memory equal ACT_Q8's.  after_loads() runs once, right after
 // the first activation loads are issued (the caller issues its weight
 // prologue there, behind the older activation loads).
-template <int FMT, int NX, int NI, int D, int KW = 4, typename F>
+//
+// NORM (one column, at most 8 items per wave, KW dividing 16): the items come
+// from nm.x with their norm weights, the column is first normalised exactly
+// as k_rmsnorm_act_q8_reg does it (that kernel's thread (v, l) sums elements
+// 4l..4l+3 of superblocks v, v + 16, ... in turn; superblock s sits in wave
+// s % KW here, which holds the partials of v = wave + KW q in the same
+// order), y = (x * s) * wn is quantised, and the workgroup that writes a
+// superblock's appendices also stores its y into C.x.
+template <int FMT, int NX, int NI, int D, int KW = 4, bool NORM = false, typename F>
 __device__ __forceinline__ void ks_x_fuse(const KsCols<NX> & C, uint32_t nx, uint32_t nsb, uint32_t cols,
                                           uint8_t * xr, float * xd, uint32_t app_g, uint32_t app_G,
-                                          F && after_loads) {
+                                          F && after_loads, const NormArgs & nm = NormArgs{}) {
+    static_assert(!NORM || (NX == 1 && (KW == 4 || KW == 8)), "RMSNORM: one column, 16 % KW == 0");
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t nitem = nx * nsb;
@@ -367,24 +376,76 @@ __device__ __forceinline__ void ks_x_fuse(const KsCols<NX> & C, uint32_t nx, uin
             if (lane == 0) lds_st32(&xd[p * nsb + sb], __float_as_uint(d));
             if (i % app_G == app_g) {
                 uint8_t * xc = (uint8_t *)col_pick<NX>(C.x, p);
+                if constexpr (NORM)
+                    *(float4 *)((float *)xc + 256 * sb + 4 * lane) = make_float4(v[j][0], v[j][1], v[j][2], v[j][3]);
                 act_q8_lanes(v[j], lane, sb, xc + xq_off(cols), xc + xqk_off(cols), cols);
             }
         }
     };
     auto vload = [&](uint32_t i) -> const float * {
+        if constexpr (NORM) return nm.x + 256 * i + 4 * lane;
         const uint32_t p = div_small(i, magic);
         return col_pick<NX>(C.x, p) + 256 * (i - p * nsb) + 4 * lane;
     };
     if (nitem <= 8 * KW) {
         // every item of this wave (at most 8) is loaded before the weight
         // prologue, and only these loads are waited for
-        u32x4a r[8];
+        u32x4a r[8], rw[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j)
-            if (KW * j + wave < nitem) r[j] = gld_x4(vload(KW * j + wave));
+            if (KW * j + wave < nitem) {
+                r[j] = gld_x4(vload(KW * j + wave));
+                if constexpr (NORM) rw[j] = gld_x4(nm.wn + 256 * (KW * j + wave) + 4 * lane);
+            }
         ks_wait_behind<NI, D + 1>(after_loads());
 #pragma unroll
-        for (int j = 0; j < 8; ++j) xfence(r[j]);
+        for (int j = 0; j < 8; ++j) {
+            xfence(r[j]);
+            if constexpr (NORM) xfence(rw[j]);
+        }
+        if constexpr (NORM) {
+            __shared__ __attribute__((aligned(16))) float nparts[16];
+            constexpr uint32_t NQ = 16 / KW;
+            float ss[NQ];
+#pragma unroll
+            for (uint32_t q = 0; q < NQ; ++q) ss[q] = 0.f;
+#pragma unroll
+            for (uint32_t j = 0; j < 8; ++j) {
+                if (KW * j + wave < nitem) {
+                    const float x0 = __uint_as_float(r[j].x), x1 = __uint_as_float(r[j].y);
+                    const float x2 = __uint_as_float(r[j].z), x3 = __uint_as_float(r[j].w);
+                    float & t = ss[j % NQ];
+                    t += x0 * x0;
+                    t += x1 * x1;
+                    t += x2 * x2;
+                    t += x3 * x3;
+                }
+            }
+#pragma unroll
+            for (uint32_t q = 0; q < NQ; ++q) {
+#pragma unroll
+                for (int o = 1; o < 64; o <<= 1) ss[q] += xor_lane(ss[q], o, lane);
+                if (lane == 0) lds_st32(&nparts[wave + KW * q], __float_as_uint(ss[q]));
+            }
+            lds_barrier();
+            u32x4a p0, p1, p2, p3;                                // the 16 totals in one LDS round trip
+            asm volatile("ds_read_b128 %0, %4\n\tds_read_b128 %1, %4 offset:16\n\tds_read_b128 %2, %4 offset:32\n\t"
+                         "ds_read_b128 %3, %4 offset:48\n\ts_waitcnt lgkmcnt(0)"
+                         : "=&v"(p0), "=&v"(p1), "=&v"(p2), "=&v"(p3) : "v"(lds_off(nparts)) : "memory");
+            const uint32_t pv[16] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w,
+                                     p2.x, p2.y, p2.z, p2.w, p3.x, p3.y, p3.z, p3.w};
+            float tn = 0.f;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) tn += __uint_as_float(pv[v]);
+            const float sn = 1.0f / sqrtf(tn / (float)cols + nm.eps);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                r[j].x = __float_as_uint(__uint_as_float(r[j].x) * sn * __uint_as_float(rw[j].x));
+                r[j].y = __float_as_uint(__uint_as_float(r[j].y) * sn * __uint_as_float(rw[j].y));
+                r[j].z = __float_as_uint(__uint_as_float(r[j].z) * sn * __uint_as_float(rw[j].z));
+                r[j].w = __float_as_uint(__uint_as_float(r[j].w) * sn * __uint_as_float(rw[j].w));
+            }
+        }
 #pragma unroll
         for (int g = 0; g < 2; ++g) {
             if (4 * KW * g >= nitem) break;

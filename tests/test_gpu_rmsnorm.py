@@ -192,3 +192,35 @@ def test_rmsnorm_dot_triple_in_graph(flh, orc, gpu):
         assert np.array_equal(bits(dy.download(np.float32, rows, gpu)), bits(ref)), k
         assert np.array_equal(bits(dxn.download(np.float32, st, gpu)), bits(refx)), k
     g.close()
+
+
+@pytest.mark.parametrize("cfg", ["1", "0"])
+@pytest.mark.parametrize("rows,n", [(20480, 4096), (28672, 4096), (300, 4096), (77, 8192)])
+def test_rmsnorm_stream_dot_kernels_agree(flh, orc, gpu, cfg, rows, n):
+    """Above 2^18 superblocks (and with FLH_SBL=0 at any size) the one-launch
+    RMSNORM -> dot runs on the four-lanes-per-superblock kernel: same bits as
+    the separate launches there too."""
+    print("[case] rmsnorm dot kernels", cfg, rows, n, flush=True)
+    rng = np.random.default_rng(rows + 3 * n)
+    x = (rng.standard_normal(n) * 2).astype(np.float32)
+    wn = (1 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+    w = sane_rows(Q4_K, rows, n, rng)
+    y0 = rng.standard_normal(rows).astype(np.float32)
+    st = col_stride_floats(n)
+    dx, dwn, dw = (flh.DeviceBuffer.from_array(a, gpu) for a in (x, wn, w))
+    outs = []
+    for fused in (True, False):
+        dxn = flh.DeviceBuffer.from_array(np.zeros(st, np.float32), gpu)
+        dy = flh.DeviceBuffer.from_array(y0, gpu)
+        with tuned(flh, FLH_SBL=cfg):
+            if fused:
+                flh.rmsnorm_stream_dot(Q4_K, dw, rows, n, dx, dwn, 1e-5, dxn, dy, gpu)
+            else:
+                flh.rmsnorm_act_q8(dx, dwn, dxn, n, 1e-5, gpu)
+                flh.stream_dot(Q4_K, dw, rows, n, dxn, dy, gpu)
+        outs.append((dxn.download(np.float32, st, gpu), dy.download(np.float32, rows, gpu)))
+    assert np.array_equal(bits(outs[0][0]), bits(outs[1][0]))
+    assert np.array_equal(bits(outs[0][1]), bits(outs[1][1]))
+    want = y0.copy()
+    orc.stream_dot(Q4_K, w, rows, n, outs[0][0], want, threads=8)
+    assert np.array_equal(bits(outs[0][1]), bits(want))
