@@ -1,6 +1,8 @@
 // flh_dot_sbl.hip -- single-column row-dots with one superblock (Q4_K, Q6_K
 // x q8_K) or four 32-weight blocks (Q8_0, Q5_0, IQ2_XXS, IQ3_XXS x q8_1) per
-// lane, and the routed (MoE) form of the same launch.
+// lane, the routed (MoE) form of the same launch, its RMSNORM -> ACT_Q8
+// prologue (NORM), and a several-column form for the 32-weight-block formats
+// (k_dot_sbl_nx, at the end of this file).
 //
 // The streaming kernel of flh_dot_kstream.hip splits a superblock over four
 // lanes, which costs every quarter its own scale decode, a DPP reduction and
@@ -43,7 +45,10 @@
 // staged bytes are the q8_K block's, and workgroup s % G also writes both
 // appendices of superblock s, so memory ends up as after a separate ACT_Q8
 // launch (with every appendix store in workgroup 0, that workgroup finished
-// ~2 us after the others).
+// ~2 us after the others).  With NORM the items come from the input column
+// with their norm weights and are normalised first (the sum of squares in the
+// order of the standalone RMSNORM kernel), and the owning workgroup also
+// stores y.
 #include "flh_kstream.h"
 #include "flh_internal.h"
 #include "flh_status.h"
