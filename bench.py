@@ -419,6 +419,8 @@ PROFILE_OPS["verify8"] = PROFILE_OPS["verify8_14336x4096"]
 for _f, _name in ((Q8_0, "q8_0"), (Q5_0, "q5_0"), (IQ2_XXS, "iq2_xxs"), (IQ3_XXS, "iq3_xxs")):
     for _n in (2, 4, 8):
         PROFILE_OPS[f"{_name}_verify{_n}"] = (_f, 14336, 4096, _n, "dot")
+PROFILE_OPS["norm_qkv"] = (Q4_K, 6144, 4096, 1, "norm")
+PROFILE_OPS["norm_gate_up"] = (Q4_K, 28672, 4096, 1, "norm")
 
 
 def profile_run(flh, B, s, staging, which="gate_up"):
@@ -443,8 +445,14 @@ def profile_run(flh, B, s, staging, which="gate_up"):
     x, st = B.activation(c, nx, 12, outliers=fmt == Q4_K)
     y = B.buf(nx * r * 4)
     m8 = flh.I8_MASK_DEFAULT | (1 << IQ2_XXS) | (1 << IQ3_XXS)
+    if kind == "norm":                      # RMSNORM -> ACT_Q8 -> dot, one launch
+        xn, _ = B.activation(c, 1, 13, outliers=False)
+        wn = B.buf(c * 4)
+        flh.fill_normal(wn, c, 14, s, mean=1.0, std=0.1)
     for i in range(64):
-        if kind == "fused":
+        if kind == "norm":
+            flh.rmsnorm_stream_dot(fmt, ws[i % len(ws)], r, c, x, wn, 1e-5, xn, y, s)
+        elif kind == "fused":
             flh.act_q8_stream_dot(fmt, ws[i % len(ws)], r, c, x, y, s)
         elif kind == "act":
             flh.act_q8(x, c, s)
