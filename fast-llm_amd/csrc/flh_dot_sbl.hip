@@ -1358,6 +1358,12 @@ int launch_dot_sbl(int fmt, const DotArgs & a, bool fuse, hipStream_t s, const N
     //    IQ3_XXS 18.3 -> 13.5 against 4 waves).
     // (NORM: against an RMSNORM launch of its own, at every size)
     if (fuse && !norm && !t.sbl_w && (uint64_t)a.rows * nsb > (1u << 18)) return FLH_ERR_UNSUPPORTED;
+    //  * unfused Q4_K rows of more than 16 superblocks: above 2^18
+    //    superblocks the four-lanes kernel streams them faster (us, this
+    //    kernel vs that one: 8192x14336 15.68 vs 14.86; 4096x14336 9.41 vs
+    //    9.64, 4096x8192 7.07 vs 7.20; 28672x4096, 16 per row, 13.31 vs 13.49)
+    if (!fuse && fmt == FMT_Q4_K && nsb > 16 && !t.sbl_w && (uint64_t)a.rows * nsb > (1u << 18))
+        return FLH_ERR_UNSUPPORTED;
     if (norm && (fmt != FMT_Q4_K || !fuse || ((uintptr_t)norm->x & 15) || ((uintptr_t)norm->wn & 15)))
         return FLH_ERR_UNSUPPORTED;
     // Q6_K: its 6-bit decode is VALU-heavy and a 12-14 KB chunk leaves room
