@@ -86,6 +86,24 @@ def test_sbl_matches_streaming_kernel(flh, orc, gpu):
     assert np.array_equal(bits(got1), bits(want))
 
 
+def test_wide_rows_both_kernels(flh, orc, gpu):
+    """8192 x 14336 (56 superblocks per row, above 2^18 superblocks): the
+    default launch goes to the streaming kernel, a forced FLH_SBL plan to this
+    one; both bitwise against the oracle, unfused and with ACT_Q8 fused."""
+    rows, cols = 8192, 14336
+    say("wide rows", rows, cols)
+    rng = np.random.default_rng(8192)
+    w = flh.quantize_host(Q4_K, normal_weights(rows, cols, rng))
+    xs = activations(1, cols, rng, outliers=True)
+    y0 = rng.standard_normal(rows).astype(np.float32)
+    for cfg in (None, "1,8,1,4"):
+        with tuned(flh, **({} if cfg is None else {"FLH_SBL": cfg})):
+            got, want = run_dot(flh, orc, gpu, Q4_K, w, rows, cols, xs, y0=y0)
+            assert np.array_equal(bits(got), bits(want)), cfg
+            got, want = fused_run(flh, orc, gpu, w, rows, cols, xs, y0)
+            assert np.array_equal(bits(got), bits(want)), cfg
+
+
 Q8_0 = 1
 
 
