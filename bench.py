@@ -322,6 +322,20 @@ def main():
                 if fmt == Q5_0 and r == 4096:
                     cpu_in[f"q5_0_{r}x{c}"] = host_case(flh, s, Q5_0, ws[0], r, c, x, st, 1)
                 del ws
+        # the down projection's shape (14336 columns: two four-block halves
+        # per lane) in each 32-weight-block format
+        x14, _ = B.activation(14336, 1, 41, outliers=False)
+        for fmt, fname in ((Q8_0, "q8_0"), (Q5_0, "q5_0"), (IQ2_XXS, "iq2_xxs"), (IQ3_XXS, "iq3_xxs")):
+            r, c = 4096, 14336
+            nb = r * flh.row_bytes(fmt, c)
+            ws = (B.weights(fmt, r, c, copies_for(nb), seed=61, staging=staging) if fmt == Q8_0
+                  else B.weights_random(fmt, r, c, copies_for(nb), seed=62 + fmt))
+            y = B.buf(r * 4)
+            m8 = flh.I8_MASK_DEFAULT | (1 << IQ2_XXS) | (1 << IQ3_XXS)
+            us = B.time_graph(lambda i: flh.stream_dot(fmt, ws[i % len(ws)], r, c, x14, y, s, i8_mask=m8), REPS)
+            op_entry(f"{fname}_{r}x{c}", us, nb)
+            del ws
+        del x14
         # several activation columns of the 32-weight-block formats (a
         # speculative-verify batch on a Q8_0 / Q5_0 / IQ model): 14336x4096
         # with 2, 4, 8 columns, one weight pass per launch

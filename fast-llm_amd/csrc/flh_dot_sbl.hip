@@ -570,11 +570,19 @@ __device__ __forceinline__ void sbl_iq(const uint8_t * st, uint32_t lane, uint32
 // whose activation is column p (per-slot x) or the token's; the pair's
 // expert is known only after routing, so its weight requests wait for that,
 // while the y and activation DMAs go out first.
-template <int FMT, bool FUSE, int W, bool MOE = false, bool NORM = false>
+//
+// H = 2 (32-weight-block formats, rows of more than 64 four-block halves):
+// a lane takes the halves 2l and 2l + 1 of its row, decoding them one after
+// the other against their own activation blocks and parking each half's
+// terms at its own position of the chains, so the fold reads the same chains
+// in the same order as with one half per lane.
+template <int FMT, bool FUSE, int W, bool MOE = false, bool NORM = false, int H = 1>
 __global__ __launch_bounds__(64 * W) void k_dot_sbl(DotArgs a, uint32_t rpc, uint32_t ni, uint32_t slot, uint32_t pre,
                                                     MoeArgs m, NormArgs nm) {
     static_assert(!NORM || (FUSE && (W == 4 || W == 8)), "RMSNORM rides on the fused quantisation, 16 % W == 0");
     static_assert(FMT == FMT_Q4_K || !FUSE, "only Q4_K fuses the quantisation");
+    static_assert(H == 1 || (H == 2 && FMT != FMT_Q4_K && FMT != FMT_Q6_K && !FUSE && !MOE),
+                  "two halves per lane: unfused 32-weight-block formats");
     static_assert(FMT != FMT_Q6_K || !MOE, "Q6_K experts run on the grouped streaming kernel");
     static_assert(!MOE || !FUSE, "the routed launch reads a ready appendix");
     static_assert(FMT == FMT_Q4_K || FMT == FMT_Q6_K || FMT == FMT_Q8_0 || FMT == FMT_Q5_0 ||
@@ -588,7 +596,8 @@ __global__ __launch_bounds__(64 * W) void k_dot_sbl(DotArgs a, uint32_t rpc, uin
     constexpr uint32_t TB = Q8 ? 4096 : 1024;                     // fold-term bytes of a wave
     extern __shared__ __attribute__((aligned(16))) uint8_t sm[];
     const uint32_t nsb = a.cols >> 8, rows = a.rows, cols = a.cols;
-    const uint32_t P = Q8 ? 2 * nsb : nsb;                        // lanes of a row
+    const uint32_t P = Q8 ? 2 * nsb : nsb;                        // lane shares (fold terms) of a row
+    const uint32_t PL = P / H;                                    // lanes of a row
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t G = gridDim.x, b = blockIdx.x;
@@ -833,21 +842,27 @@ __global__ __launch_bounds__(64 * W) void k_dot_sbl(DotArgs a, uint32_t rpc, uin
     lds_barrier();
     SBL_STAMP(1);
     typename std::conditional<Q8, XQ8, typename std::conditional<Q6, XQ6, XQ4>::type>::type X;
-    int xsum[4] = {0, 0, 0, 0};                                   // Q5_0: the blocks' activation sums
-    if constexpr (Q8) load_xq8(xs + 4 * SBL_X8 * (lane % P), X);
+    int xsum[H][4] = {};                                          // Q5_0: the blocks' activation sums
+    XQ8 X2;                                                       // H = 2: the second half's blocks
+    (void)X2;
+    if constexpr (Q8) load_xq8(xs + 4 * SBL_X8 * (H * (lane % PL)), X);
     else if constexpr (Q6) load_xq6(xs + SBL_XS * (lane % nsb), X);
     else load_xq4(xs + SBL_XS * (lane % nsb), X);
+    if constexpr (H == 2) load_xq8(xs + 4 * SBL_X8 * (2 * (lane % PL) + 1), X2);
     if constexpr (FMT == FMT_Q5_0) {
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            const u32x4a xa = X.q[2 * m], xb = X.q[2 * m + 1];
-            int t = 0;
-            t = dot4(0x01010101, (int)xa.x, t); t = dot4(0x01010101, (int)xa.y, t);
-            t = dot4(0x01010101, (int)xa.z, t); t = dot4(0x01010101, (int)xa.w, t);
-            t = dot4(0x01010101, (int)xb.x, t); t = dot4(0x01010101, (int)xb.y, t);
-            t = dot4(0x01010101, (int)xb.z, t); t = dot4(0x01010101, (int)xb.w, t);
-            xsum[m] = t;
-        }
+        for (int h = 0; h < H; ++h)
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                const XQ8 & XH = h ? X2 : X;
+                const u32x4a xa = XH.q[2 * m], xb = XH.q[2 * m + 1];
+                int t = 0;
+                t = dot4(0x01010101, (int)xa.x, t); t = dot4(0x01010101, (int)xa.y, t);
+                t = dot4(0x01010101, (int)xa.z, t); t = dot4(0x01010101, (int)xa.w, t);
+                t = dot4(0x01010101, (int)xb.x, t); t = dot4(0x01010101, (int)xb.y, t);
+                t = dot4(0x01010101, (int)xb.z, t); t = dot4(0x01010101, (int)xb.w, t);
+                xsum[h][m] = t;
+            }
     }
     // The rest of the prologue comes after the barrier: a request blocks its
     // wave while the CU's memory queue is full, and a wave stuck there would
@@ -871,31 +886,43 @@ __global__ __launch_bounds__(64 * W) void k_dot_sbl(DotArgs a, uint32_t rpc, uin
         if (i == 0) SBL_STAMP(2);
         if (i + 1 == nck) SBL_STAMP(3);
         if constexpr (Q8) {
-            float f[4];
-            int id[4];
-            if constexpr (FMT == FMT_Q8_0) {
-                uint32_t D[34];
-                lds_ld_q8h(st + B * lane, D);
-                sbl_q8_0(D, X, f, id);
-            } else if constexpr (FMT == FMT_Q5_0) {
-                uint32_t D[22];
-                lds_ld_q5h(st + B * lane, D);
-                sbl_q5_0(D, X, xsum, f, id);
-            } else {
-                sbl_iq<FMT>(st, lane, grid, X, f, id);
+            const uint32_t r = lane / PL, pos = lane - r * PL;
+            // H = 2: a lane past the chunk's rows decodes the first share
+            // (its terms are not parked) instead of reading past the chunk
+            const uint32_t ql = H == 2 && r >= rpc ? 0u : lane;
+            float f[H][4];
+            int id[H][4];
+#pragma unroll
+            for (int h = 0; h < H; ++h) {
+                const uint32_t vl = H * ql + h;                   // the lane's share of the chunk
+                const XQ8 & XH = h ? X2 : X;
+                if constexpr (FMT == FMT_Q8_0) {
+                    uint32_t D[34];
+                    lds_ld_q8h(st + B * vl, D);
+                    sbl_q8_0(D, XH, f[h], id[h]);
+                } else if constexpr (FMT == FMT_Q5_0) {
+                    uint32_t D[22];
+                    lds_ld_q5h(st + B * vl, D);
+                    sbl_q5_0(D, XH, xsum[h], f[h], id[h]);
+                } else {
+                    sbl_iq<FMT>(st, vl, grid, XH, f[h], id[h]);
+                }
             }
             if (i + 2 < nck) {                                    // refill this stage
                 issue(i + 2, st);
                 mark[sl] = ops;
             }
-            // chain (row r, accumulator k) = its P terms in position order,
+            // chain (row r, accumulator k) = its P terms in share order,
             // CS bytes per chain (16 bytes of padding spread the fold
             // lanes' reads over the banks)
-            const uint32_t r = lane / P, pos = lane - r * P, CS = 8 * P + 16;
+            const uint32_t CS = 8 * P + 16;
             if (r < rpc) {
 #pragma unroll
-                for (int k = 0; k < 4; ++k)
-                    lds_st64(T + (4 * r + k) * CS + 8 * pos, u32x2a{__float_as_uint(f[k]), __float_as_uint((float)id[k])});
+                for (int h = 0; h < H; ++h)
+#pragma unroll
+                    for (int k = 0; k < 4; ++k)
+                        lds_st64(T + (4 * r + k) * CS + 8 * (H * pos + h),
+                                 u32x2a{__float_as_uint(f[h][k]), __float_as_uint((float)id[h][k])});
             }
         } else {
             // Q4_K: terms (d * dk) * iacc and -(dmin * dk) * imin; Q6_K:
@@ -1332,13 +1359,17 @@ int launch_dot_sbl(int fmt, const DotArgs & a, bool fuse, hipStream_t s, const N
     const uint32_t nsb = a.cols >> 8, P = q8 ? 2 * nsb : nsb;
     const uint32_t B = fmt == FMT_Q4_K ? 144 : q6 ? 210 : fmt == FMT_Q8_0 ? 136 : fmt == FMT_Q5_0 ? 88
                                               : iq_block_bytes(fmt) / 2;
-    if (nsb < 1 || P > 64) return FLH_ERR_UNSUPPORTED;
+    // rows of more than 64 four-block halves (32-weight-block formats, more
+    // than 8192 columns): two halves per lane, whose 4 chains of P terms fit
+    // the wave's 4 KiB of fold terms up to 63 superblocks (16128 columns)
+    const uint32_t H = q8 && P > 64 ? 2 : 1, PL = P / H;
+    if (nsb < 1 || PL > 64 || (H == 2 && 4 * (8 * P + 16) > 4096)) return FLH_ERR_UNSUPPORTED;
     // chunks are whole rows moved in 16-byte pieces (IQ rows: nsb % 8 == 0)
     if ((P * B) & 15) return FLH_ERR_UNSUPPORTED;
     if ((uintptr_t)a.w & 15 || (a.estride & 15)) return FLH_ERR_UNSUPPORTED;
     if ((fuse || q8) && ((uintptr_t)a.x & 15)) return FLH_ERR_UNSUPPORTED;
     const Tune & t = tune();
-    const uint32_t rpc = 64 / P;
+    const uint32_t rpc = 64 / PL;
     const uint32_t ni = (rpc * P * B + 1023) / 1024, slot = ni * 1024;
     // Measured defaults (layer shapes, graph-replayed launches):
     //  * fused: 8 waves (the quantisation is shared by more waves), 4 of
@@ -1394,6 +1425,13 @@ int launch_dot_sbl(int fmt, const DotArgs & a, bool fuse, hipStream_t s, const N
     };
     auto unfused = [&](auto fmt_tag) {
         constexpr int F = decltype(fmt_tag)::value;
+        if constexpr (F != FMT_Q4_K && F != FMT_Q6_K) {
+            if (H == 2) {
+                if (W == 8) return go(k_dot_sbl<F, false, 8, false, false, 2>);
+                if (W == 6) return go(k_dot_sbl<F, false, 6, false, false, 2>);
+                return go(k_dot_sbl<F, false, 4, false, false, 2>);
+            }
+        }
         if (W == 8) return go(k_dot_sbl<F, false, 8>);
         if (W == 6) return go(k_dot_sbl<F, false, 6>);
         return go(k_dot_sbl<F, false, 4>);

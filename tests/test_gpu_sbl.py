@@ -107,13 +107,18 @@ def test_wide_rows_both_kernels(flh, orc, gpu):
 Q8_0 = 1
 
 
+# rows of 8448-16128 columns (more than 64 four-block halves) put two halves
+# on a lane; 16384 columns is past that plan and takes the other kernels
+B32_SHAPES = [(7, 256), (33, 512), (41, 768), (13, 2816), (1001, 4096), (70, 8192), (4096, 4096), (37, 8448),
+              (50, 14336), (9, 16128), (5, 16384)]
+
+
 @pytest.mark.parametrize("cfg", ["1", "1,8,1,0", "1,4,2,0,255", "1,6,1,3,1"])
-@pytest.mark.parametrize("rows,cols", [(7, 256), (33, 512), (41, 768), (13, 2816), (1001, 4096), (70, 8192),
-                                       (4096, 4096)])
+@pytest.mark.parametrize("rows,cols", B32_SHAPES)
 def test_sbl_q8_0_bitwise(flh, orc, gpu, cfg, rows, cols):
     """Q8_0 x q8_1 with half a 256-weight unit per lane: bitwise
     fl_dot_i8_q8_0 (src/runtime/quants.h:438-447) for every unit count per
-    row up to 32 (8192 columns)."""
+    row up to 63 (16128 columns; above 32, two halves per lane)."""
     say("sbl q8_0", cfg, rows, cols)
     rng = np.random.default_rng(rows * 5 + cols)
     w = sane_rows(Q8_0, rows, cols, rng)
@@ -125,15 +130,15 @@ def test_sbl_q8_0_bitwise(flh, orc, gpu, cfg, rows, cols):
 
 
 Q5_0, IQ2_XXS, IQ3_XXS = 2, 5, 6
-B32_MODE = {Q5_0: "int8", IQ2_XXS: "iq8", IQ3_XXS: "iq8"}
+B32_MODE = {Q8_0: "int8", Q5_0: "int8", IQ2_XXS: "iq8", IQ3_XXS: "iq8"}
 
 
 @pytest.mark.parametrize("cfg", ["1", "1,8,1,0", "1,4,2,0,255", "1,6,1,3,1"])
-@pytest.mark.parametrize("rows,cols", [(7, 256), (33, 512), (41, 768), (13, 2816), (1001, 4096), (70, 8192),
-                                       (4096, 4096)])
+@pytest.mark.parametrize("rows,cols", B32_SHAPES)
 def test_sbl_q5_0_bitwise(flh, orc, gpu, cfg, rows, cols):
     """Q5_0 x q8_1 with 4 blocks (88 bytes) per lane: bitwise fl_dot_i8_q5_0
-    (src/runtime/quants.h:449-466) for every lane count per row up to 64."""
+    (src/runtime/quants.h:449-466) for every lane count per row up to 64,
+    and two halves per lane above that."""
     say("sbl q5_0", cfg, rows, cols)
     rng = np.random.default_rng(rows * 7 + cols)
     w = sane_rows(Q5_0, rows, cols, rng)
@@ -146,7 +151,8 @@ def test_sbl_q5_0_bitwise(flh, orc, gpu, cfg, rows, cols):
 
 @pytest.mark.parametrize("fmt", [IQ2_XXS, IQ3_XXS])
 @pytest.mark.parametrize("cfg", ["1", "1,8,1,0", "1,4,2,0,255", "1,6,1,3,1"])
-@pytest.mark.parametrize("rows,cols", [(5, 2048), (33, 2048), (1001, 4096), (70, 8192), (4096, 4096)])
+@pytest.mark.parametrize("rows,cols", [(5, 2048), (33, 2048), (1001, 4096), (70, 8192), (4096, 4096), (21, 10240),
+                                       (50, 14336), (3, 16384)])
 def test_sbl_iq_bitwise(flh, orc, gpu, fmt, cfg, rows, cols):
     """IQ2_XXS / IQ3_XXS x q8_1 with half a superblock per lane (2-byte
     aligned pieces, codebook staged in LDS): bitwise against the oracle's
@@ -161,13 +167,14 @@ def test_sbl_iq_bitwise(flh, orc, gpu, fmt, cfg, rows, cols):
         assert np.array_equal(bits(got), bits(want))
 
 
-@pytest.mark.parametrize("fmt", [Q5_0, IQ2_XXS, IQ3_XXS])
-def test_sbl_b32_matches_register_kernel(flh, orc, gpu, fmt):
+@pytest.mark.parametrize("rows,cols", [(14336, 4096), (4096, 14336)])
+@pytest.mark.parametrize("fmt", [Q8_0, Q5_0, IQ2_XXS, IQ3_XXS])
+def test_sbl_b32_matches_register_kernel(flh, orc, gpu, fmt, rows, cols):
     """The LDS-staged and register kernels give the same bits (and both the
-    oracle's) on a 14336x4096 matrix and on an expert picked by an id slot."""
-    say("sbl b32 vs register", fmt)
-    rng = np.random.default_rng(900 + fmt)
-    rows, cols = 14336, 4096
+    oracle's) on a layer-sized matrix (4096x14336: two halves per lane) and
+    on an expert picked by an id slot."""
+    say("sbl b32 vs register", fmt, rows, cols)
+    rng = np.random.default_rng(900 + fmt + cols)
     w = sane_rows(fmt, rows, cols, rng)
     xs = activations(1, cols, rng, outliers=True)
     outs = []
