@@ -153,7 +153,7 @@ static int launch_moe_b32(int fmt, const MoeArgs & a, hipStream_t s) {
     const int rc = launch_moe_sbl(fmt, a, s);
     if (rc == FLH_ERR_UNSUPPORTED)
         return set_error(rc, "moe: this format needs 16-byte aligned weights, x and expert stride, and rows of "
-                             "at most 8192 columns (IQ: a multiple of 2048)");
+                             "at most 16128 columns (IQ: a multiple of 2048)");
     return rc;
 }
 

@@ -581,7 +581,7 @@ __global__ __launch_bounds__(64 * W) void k_dot_sbl(DotArgs a, uint32_t rpc, uin
                                                     MoeArgs m, NormArgs nm) {
     static_assert(!NORM || (FUSE && (W == 4 || W == 8)), "RMSNORM rides on the fused quantisation, 16 % W == 0");
     static_assert(FMT == FMT_Q4_K || !FUSE, "only Q4_K fuses the quantisation");
-    static_assert(H == 1 || (H == 2 && FMT != FMT_Q4_K && FMT != FMT_Q6_K && !FUSE && !MOE),
+    static_assert(H == 1 || (H == 2 && FMT != FMT_Q4_K && FMT != FMT_Q6_K && !FUSE),
                   "two halves per lane: unfused 32-weight-block formats");
     static_assert(FMT != FMT_Q6_K || !MOE, "Q6_K experts run on the grouped streaming kernel");
     static_assert(!MOE || !FUSE, "the routed launch reads a ready appendix");
@@ -1559,11 +1559,13 @@ int launch_moe_sbl(int fmt, const MoeArgs & m, hipStream_t s) {
         return FLH_ERR_UNSUPPORTED;
     const uint32_t nsb = m.cols >> 8, P = q8 ? 2 * nsb : nsb;
     const uint32_t B = fmt == FMT_Q4_K ? 144 : fmt == FMT_Q8_0 ? 136 : fmt == FMT_Q5_0 ? 88 : iq_block_bytes(fmt) / 2;
-    if (nsb < 1 || P > 64 || ((P * B) & 15)) return FLH_ERR_UNSUPPORTED;
+    // two four-block halves per lane above 64 (as launch_dot_sbl)
+    const uint32_t H = q8 && P > 64 ? 2 : 1, PL = P / H;
+    if (nsb < 1 || PL > 64 || (H == 2 && 4 * (8 * P + 16) > 4096) || ((P * B) & 15)) return FLH_ERR_UNSUPPORTED;
     if ((uintptr_t)m.w & 15 || (m.estride & 15)) return FLH_ERR_UNSUPPORTED;
     if (q8 && (((uintptr_t)m.x & 15) || (m.xstride & 3))) return FLH_ERR_UNSUPPORTED;
     const Tune & t = tune();
-    const uint32_t rpc = 64 / P;
+    const uint32_t rpc = 64 / PL;
     const uint32_t ni = (rpc * P * B + 1023) / 1024, slot = ni * 1024;
     uint32_t W = t.sbl_w ? t.sbl_w : nsb > 16 || (q8 && fmt != FMT_Q8_0) ? 8 : 4;
     const uint32_t pre = t.sbl_pre == 0xFFu ? W : t.sbl_pre ? t.sbl_pre : q8 ? W : W / 2;
@@ -1589,6 +1591,13 @@ int launch_moe_sbl(int fmt, const MoeArgs & m, hipStream_t s) {
     };
     auto routed = [&](auto fmt_tag) {
         constexpr int F = decltype(fmt_tag)::value;
+        if constexpr (F != FMT_Q4_K) {
+            if (H == 2) {
+                if (W == 8) return go(k_dot_sbl<F, false, 8, true, false, 2>);
+                if (W == 6) return go(k_dot_sbl<F, false, 6, true, false, 2>);
+                return go(k_dot_sbl<F, false, 4, true, false, 2>);
+            }
+        }
         if (W == 8) return go(k_dot_sbl<F, false, 8, true>);
         if (W == 6) return go(k_dot_sbl<F, false, 6, true>);
         return go(k_dot_sbl<F, false, 4, true>);

@@ -333,17 +333,19 @@ def test_moe_one_token_superblock_kernel(flh, orc, gpu, cfg, rows, cols, per_slo
 Q8_0, Q5_0, IQ2_XXS, IQ3_XXS = 1, 2, 5, 6
 
 
+@pytest.mark.parametrize("cols", [2048, 14336])
 @pytest.mark.parametrize("fmt", [Q8_0, Q5_0, IQ2_XXS, IQ3_XXS])
 @pytest.mark.parametrize("ntok,per_slot,fused", [(1, False, False), (3, True, False), (5, False, True),
                                                  (2, True, True)])
-def test_moe_block32_formats(flh, orc, gpu, fmt, ntok, per_slot, fused):
+def test_moe_block32_formats(flh, orc, gpu, fmt, ntok, per_slot, fused, cols):
     """Expert dots of the 32-weight-block formats (one workgroup row per
     routed pair): every pair's y equals the oracle's STREAM_DOT_IDX tile on
     the q8_1 int8 path, bit for bit, with the routing given as ids or fused
-    (ids then equal the reference router's; gates within the expf tolerance)."""
-    say("moe block32", fmt, ntok, per_slot, fused)
-    rng = np.random.default_rng(fmt * 11 + ntok * 3 + fused)
-    E, K, rows, cols = 8, 2, 200, 2048
+    (ids then equal the reference router's; gates within the expf tolerance).
+    14336 columns: a down projection, two four-block halves per lane."""
+    say("moe block32", fmt, ntok, per_slot, fused, cols)
+    rng = np.random.default_rng(fmt * 11 + ntok * 3 + fused + cols)
+    E, K, rows = 8, 2, 200 if cols == 2048 else 72
     logits, ids, gates = route(orc, ntok, E, K, rng)
     estride = rows * row_bytes(fmt, cols)
     w = sane_rows(fmt, rows * E, cols, rng)
