@@ -421,6 +421,8 @@ PROFILE_OPS = {
     "down": (Q4_K, 4096, 14336, 1, "dot"), "act_down": (Q4_K, 4096, 14336, 1, "act"),
     "q6k_vocab": (Q6_K, 128256, 4096, 1, "dot"), "q6k_down": (Q6_K, 4096, 14336, 1, "dot"),
     "q8_0": (Q8_0, 4096, 4096, 1, "dot"),
+    "q8_0_down": (Q8_0, 4096, 14336, 1, "dot"), "q5_0_down": (Q5_0, 4096, 14336, 1, "dot"),
+    "iq2_xxs_down": (IQ2_XXS, 4096, 14336, 1, "dot"), "iq3_xxs_down": (IQ3_XXS, 4096, 14336, 1, "dot"),
     "q5_0": (Q5_0, 4096, 4096, 1, "dot"), "q5_0_ffn": (Q5_0, 14336, 4096, 1, "dot"),
     "iq2_xxs": (IQ2_XXS, 4096, 4096, 1, "dot"), "iq2_xxs_ffn": (IQ2_XXS, 14336, 4096, 1, "dot"),
     "iq3_xxs": (IQ3_XXS, 4096, 4096, 1, "dot"), "iq3_xxs_ffn": (IQ3_XXS, 14336, 4096, 1, "dot"),

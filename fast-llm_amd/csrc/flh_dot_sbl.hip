@@ -572,7 +572,8 @@ __device__ __forceinline__ void sbl_iq(const uint8_t * st, uint32_t lane, uint32
 // while the y and activation DMAs go out first.
 //
 // H = 2 (32-weight-block formats, rows of more than 64 four-block halves):
-// a lane takes the halves 2l and 2l + 1 of its row, decoding them one after
+// a lane takes the halves l and l + PL of its row (PL = lanes of a row; the
+// lanes' reads stay one half apart, as with H = 1), decoding them one after
 // the other against their own activation blocks and parking each half's
 // terms at its own position of the chains, so the fold reads the same chains
 // in the same order as with one half per lane.
@@ -845,10 +846,10 @@ __global__ __launch_bounds__(64 * W) void k_dot_sbl(DotArgs a, uint32_t rpc, uin
     int xsum[H][4] = {};                                          // Q5_0: the blocks' activation sums
     XQ8 X2;                                                       // H = 2: the second half's blocks
     (void)X2;
-    if constexpr (Q8) load_xq8(xs + 4 * SBL_X8 * (H * (lane % PL)), X);
+    if constexpr (Q8) load_xq8(xs + 4 * SBL_X8 * (lane % PL), X);
     else if constexpr (Q6) load_xq6(xs + SBL_XS * (lane % nsb), X);
     else load_xq4(xs + SBL_XS * (lane % nsb), X);
-    if constexpr (H == 2) load_xq8(xs + 4 * SBL_X8 * (2 * (lane % PL) + 1), X2);
+    if constexpr (H == 2) load_xq8(xs + 4 * SBL_X8 * (lane % PL + PL), X2);
     if constexpr (FMT == FMT_Q5_0) {
 #pragma unroll
         for (int h = 0; h < H; ++h)
@@ -894,7 +895,7 @@ __global__ __launch_bounds__(64 * W) void k_dot_sbl(DotArgs a, uint32_t rpc, uin
             int id[H][4];
 #pragma unroll
             for (int h = 0; h < H; ++h) {
-                const uint32_t vl = H * ql + h;                   // the lane's share of the chunk
+                const uint32_t vl = ql + h * PL;                  // the lane's share of the chunk (rpc == 1 if H == 2)
                 const XQ8 & XH = h ? X2 : X;
                 if constexpr (FMT == FMT_Q8_0) {
                     uint32_t D[34];
@@ -921,7 +922,7 @@ __global__ __launch_bounds__(64 * W) void k_dot_sbl(DotArgs a, uint32_t rpc, uin
                 for (int h = 0; h < H; ++h)
 #pragma unroll
                     for (int k = 0; k < 4; ++k)
-                        lds_st64(T + (4 * r + k) * CS + 8 * (H * pos + h),
+                        lds_st64(T + (4 * r + k) * CS + 8 * (pos + h * PL),
                                  u32x2a{__float_as_uint(f[h][k]), __float_as_uint((float)id[h][k])});
             }
         } else {
