@@ -267,7 +267,7 @@ int flh_dequant(int fmt, const void * w, uint32_t rows, uint32_t cols,
  * are streamed once for all of its pairs (Q4_K, Q6_K: the q8_K int8 path);
  * Q8_0, Q5_0, IQ2_XXS and IQ3_XXS run the q8_1 int8 path one pair at a time,
  * as the reference's per-pair tiles do (16-byte aligned w, x and estride;
- * cols a multiple of 256, at most 8192; IQ: a multiple of 2048).  Every
+ * cols a multiple of 256, at most 16128; IQ: a multiple of 2048).  Every
  * output is bitwise equal to the per-pair STREAM_DOT_IDX tile. */
 int flh_moe_dot(int fmt, const void * w, uint64_t estride, uint32_t rows,
                 uint32_t cols, const uint32_t * ids, uint32_t ntok,
