@@ -7,9 +7,9 @@ STREAM_DOTs with their ACT_Q8 prologues, weights resident in HBM:
   ACT_Q8(x 4096) + gate/up 28672x4096, ACT_Q8(h 14336) + down 4096x14336.
 Steps rotate over L layer copies (L * 122.7 MB > 2x the 256 MB Infinity
 Cache) so HBM, not MALL, is measured.  The L layer steps are captured in
-one HIP graph, as a decode step would run its layers; the timed region is
-K steps (K // L launches of it, then K % L single-layer graphs) bracketed
-by stream syncs and HIP events.  value = weight bytes streamed / second (GB/s, 1e9).
+one HIP graph, as a decode step would run its layers: the timed region is
+one launch of a graph of K layer steps (step i on copy i % L), bracketed
+by stream syncs and HIP events; the W warmup steps are a graph of their own.  value = weight bytes streamed / second (GB/s, 1e9).
 
 Also reported (same JSON line):
   ops      -- per-op us and GB/s for every BASELINE config: Q8_0 4096^2,
@@ -176,30 +176,26 @@ def main():
             x, st = xin[name]
             flh.act_q8_stream_dot(Q4_K, W[name][l], r, c, x, yout[name], s)
 
-    # A decode step runs every layer back to back: one graph holds the L
-    # layer copies in order (one launch per L steps); single-layer graphs
-    # run the remainder, so exactly K steps are timed.
-    graphs = []
-    for l in range(L):
+    # A decode step runs every layer back to back: the K timed steps are one
+    # captured graph of K layer steps in order, rotating over the L copies
+    # (step i uses copy i % L), so every timed step is the same decode shape
+    # and one launch covers them; the W warmup steps are a graph of their own.
+    def steps_graph(k):
         with flh.Graph.capture(s) as g:
-            issue_layer(l)
-        graphs.append(g)
-    with flh.Graph.capture(s) as model:
-        for l in range(L):
-            issue_layer(l)
+            for i in range(k):
+                issue_layer(i % L)
+        return g
 
-    def run_steps(k):
-        for _ in range(k // L):
-            model.launch()
-        for i in range(k % L):
-            graphs[i].launch()
+    timed = steps_graph(args.steps)
+    warm = steps_graph(args.warmup) if args.warmup > 0 else None
 
-    run_steps(args.warmup)
+    if warm is not None:
+        warm.launch()
     s.sync()
     e0, e1 = flh.Event(), flh.Event()
     t0 = time.perf_counter()
     e0.record(s)
-    run_steps(args.steps)
+    timed.launch()
     e1.record(s)
     s.sync()
     wall = time.perf_counter() - t0
@@ -396,8 +392,7 @@ def main():
                 us = B.time_graph(lambda i: flh.stream_dot(Q4_K, ws[i % len(ws)], r, c, x, y, s,
                                                            nx=n, xstride=st, ystride=r), REPS)
                 op_entry(f"q4_K_verify_n{n}_{r}x{c}", us, nb, {"n": n})
-                if n == 8:
-                    cpu_in[f"q4_K_verify_n8_{r}x{c}"] = host_case(flh, s, Q4_K, ws[0], r, c, x, st, n)
+                cpu_in[f"q4_K_verify_n{n}_{r}x{c}"] = host_case(flh, s, Q4_K, ws[0], r, c, x, st, n)
         # MoE decode: 8 experts, top-2, d_model 4096, d_ff 14336
         result["moe"] = bench_moe(flh, B, s, staging, cpu_in)
         ops.update(result["moe"].pop("ops"))
@@ -539,14 +534,22 @@ def bench_moe(flh, B, s, staging, cpu_in):
                 sel.update(np.argsort(-ll[t], kind="stable")[:K].tolist())
             distinct.append(len(sel))
         nb = int(np.mean(distinct) * (gu_b + dn_b))
-        if ntok == 1:
-            # CPU figure: the two routed experts' gate/up and down dots of copy 0
-            sel = np.argsort(-lg[0].reshape(ntok, E)[0], kind="stable")[:K].tolist()
-            hx = x.download(np.float32, stD, s)
-            hh = h.download(np.float32, stF, s)          # a down input with its appendices
-            cpu_in["moe_q4_K_top2of8_batch1"] = [
-                (Q4_K, gu[0].download(np.uint8, gu_b, s, offset=e * gu_b), 2 * F, D, hx, stD, 1) for e in sel] + [
-                (Q4_K, dn[0].download(np.uint8, dn_b, s, offset=e * dn_b), D, F, hh, stF, 1) for e in sel]
+        # CPU figure: the reference runs every (token, slot) pair's gate/up
+        # and down dots on its own (src/model/decoder.cpp:941-996, no
+        # grouping); the routed experts of copy 0, each token's x and each
+        # pair's down input (a column with its appendices)
+        hx = x.download(np.float32, ntok * stD, s)
+        hh = h.download(np.float32, ntok * K * stF, s)
+        wgu, wdn, cases = {}, {}, []
+        for t in range(ntok):
+            for e in np.argsort(-lg[0].reshape(ntok, E)[t], kind="stable")[:K].tolist():
+                if e not in wgu:
+                    wgu[e] = gu[0].download(np.uint8, gu_b, s, offset=e * gu_b)
+                    wdn[e] = dn[0].download(np.uint8, dn_b, s, offset=e * dn_b)
+                p = len(cases) // 2
+                cases += [(Q4_K, wgu[e], 2 * F, D, hx[t * stD:(t + 1) * stD], stD, 1),
+                          (Q4_K, wdn[e], D, F, hh[p * stF:(p + 1) * stF], stF, 1)]
+        cpu_in[f"moe_q4_K_top2of8_batch{ntok}"] = cases
         out["ops"][f"moe_q4_K_top2of8_batch{ntok}"] = {
             "us": round(us, 3), "weight_bytes": nb, "distinct_experts": float(np.mean(distinct)),
             "GBs": round(nb / us / 1e3, 1), "pct_hbm": round(100 * nb / us / 1e3 / HBM_PEAK_GBS, 2)}
@@ -619,6 +622,8 @@ def cpu_baseline(flh, s, W, xin, cpu_in):
                 break
         return nbytes, reps, el
 
+    for case, (name, r, c) in zip(layer, LAYER):
+        cpu_in[f"q4_K_{name}_{r}x{c}"] = [case]
     nb, reps, el = rate(layer, T, 1.5)
     val = nb * reps / el / 1e9
     nb1, reps1, el1 = rate(layer, 1, 3.0)

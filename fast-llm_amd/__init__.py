@@ -160,6 +160,8 @@ _SIGS = {
     "flh_arena_destroy": (_I, [_P]),
     "flh_malloc": (_I, [_SZ, C.POINTER(_P)]),
     "flh_free": (_I, [_P]),
+    "flh_host_alloc": (_I, [_SZ, C.POINTER(_P)]),
+    "flh_host_free": (_I, [_P]),
     "flh_upload": (_I, [_P, _P, _SZ, _P]),
     "flh_download": (_I, [_P, _P, _SZ, _P]),
     "flh_zero": (_I, [_P, _SZ, _P]),
@@ -339,6 +341,33 @@ class Graph:
         if self.handle:
             check(lib().flh_graph_destroy(self.handle))
             self.handle = None
+
+
+class HostBuffer:
+    """Pinned host memory (flh_host_alloc): host-readable and device-visible,
+    the place for decode-op param blocks of a task table.  `view(ctype)`
+    gives a ctypes object over its first bytes."""
+
+    def __init__(self, nbytes: int):
+        h = C.c_void_p()
+        check(lib().flh_host_alloc(max(int(nbytes), 1), C.byref(h)))
+        self.ptr = h.value
+        self.nbytes = int(nbytes)
+
+    def view(self, ctype):
+        assert C.sizeof(ctype) <= self.nbytes
+        return ctype.from_address(self.ptr)
+
+    def close(self):
+        if self.ptr and lib():
+            lib().flh_host_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 class DeviceBuffer:

@@ -7,6 +7,7 @@
 #include <string.h>
 #include <stdlib.h>
 #include <string>
+#include <atomic>
 #include <mutex>
 #include "../../include/fastllm_hip.h"
 #include "flh_common.h"
@@ -71,12 +72,19 @@ static int validate_dot(int fmt, const void * w, uint64_t w_bytes, uint32_t rows
     return FLH_OK;
 }
 
-static Tune g_tune;
-const Tune & tune() { return g_tune; }
+// The launch tuning in force: an immutable Tune published through an atomic
+// pointer, so a launch on another thread that runs while flh_init re-reads
+// the overrides sees either the old or the new settings, never a mix.  A
+// replaced Tune is kept (a few dozen bytes per flh_init call), since a launch
+// may still hold a reference to it.
+static const Tune g_tune_default{};
+static std::atomic<const Tune *> g_tune{&g_tune_default};
+const Tune & tune() { return *g_tune.load(std::memory_order_acquire); }
 
 // Development overrides of the launch tuning (see struct Tune).
 void load_tune() {
-    Tune t;
+    Tune * tp = new Tune();
+    Tune & t = *tp;
     if (const char * e = getenv("FLH_FUSE_MAX_COLS")) t.fuse_max_cols = (uint32_t)strtoul(e, nullptr, 0);
     if (const char * e = getenv("FLH_KS_TUNE")) {
         unsigned a = 0, b = 0, c = 0, d = 0;
@@ -110,7 +118,7 @@ void load_tune() {
             t.sbl = on; t.sbl_w = w; t.sbl_wpc = g; t.sbl_gmax = m; t.sbl_pre = pre;
         }
     }
-    g_tune = t;
+    g_tune.store(tp, std::memory_order_release);
 }
 
 static int dispatch_dot(int fmt, const DotArgs & a, int fast, uint32_t i8_mask, uint32_t i8k_mask,
@@ -157,6 +165,19 @@ static int launch_moe_b32(int fmt, const MoeArgs & a, hipStream_t s) {
     return rc;
 }
 
+// The decode ops' param blocks are read here, on the host, so they must not
+// be plain device memory (reading one would fault the process).  Pointers
+// the runtime does not know (ordinary host memory) report an error or
+// "unregistered": both are host memory.
+static bool host_readable(const void * p) {
+    hipPointerAttribute_t at;
+    if (hipPointerGetAttributes(&at, p) != hipSuccess) {
+        (void)hipGetLastError();                                  // not a runtime allocation: host memory
+        return true;
+    }
+    return at.type != hipMemoryTypeDevice && at.type != hipMemoryTypeArray;
+}
+
 // freeze()-style validation of a whole task table (nothing is launched on error)
 static int validate_table(const flh_task * t, uint32_t n) {
     if (n && !t) return set_error(FLH_ERR_ARG, "null task table");
@@ -177,6 +198,9 @@ static int validate_table(const flh_task * t, uint32_t n) {
             case FLH_TASK_MERGE: case FLH_TASK_SIGNAL: break;
             case FLH_TASK_ROUTER_SEL: case FLH_TASK_SILU_MUL: case FLH_TASK_WMERGE: case FLH_TASK_RMSNORM:
                 if (!k.aux) return set_error(FLH_ERR_ARG, "decode op without aux param block");
+                if (!host_readable(k.aux))
+                    return set_error(FLH_ERR_ARG, "decode op param block (aux) is in device memory: the host reads "
+                                                  "it when the table is issued (use host, pinned or managed memory)");
                 break;
             default:
                 return set_error(FLH_ERR_UNSUPPORTED, "task kind not supported by the HIP backend");
@@ -276,6 +300,14 @@ int flh_malloc(size_t bytes, void ** out) {
     if (hipMalloc(out, bytes ? bytes : 256) != hipSuccess) return set_error(FLH_ERR_NOMEM, "hipMalloc failed");
     return FLH_OK;
 }
+int flh_host_alloc(size_t bytes, void ** out) {
+    if (int rc = need_init()) return rc;
+    if (!out) return set_error(FLH_ERR_ARG, "null out");
+    if (hipHostMalloc(out, bytes ? bytes : 256, hipHostMallocDefault) != hipSuccess)
+        return set_error(FLH_ERR_NOMEM, "hipHostMalloc failed");
+    return FLH_OK;
+}
+int flh_host_free(void * p) { return p ? hip_check(hipHostFree(p), "hipHostFree") : FLH_OK; }
 int flh_free(void * p) { return p ? hip_check(hipFree(p), "hipFree") : FLH_OK; }
 int flh_upload(void * dst, const void * src, size_t n, void * stream) {
     if (int rc = hip_check(hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, (hipStream_t)stream), "upload")) return rc;
@@ -422,15 +454,6 @@ int flh_exec_tasks(const flh_task * t, uint32_t n, int fast, uint32_t i8_mask, u
                    void * stream) {
     if (int rc = validate_table(t, n)) return rc;
     if (int rc = need_init()) return rc;
-    // the reference's GPU-default masks (src/runtime/kernels.h:927-940):
-    // Q6_K goes to the q8_K int8 path (the streaming kernel), not fp32 dequant
-    constexpr uint32_t kGpuI8 = (1u << FLH_FMT_Q8_0) | (1u << FLH_FMT_Q5_0) | (1u << FLH_FMT_Q4_K) |
-                                (1u << FLH_FMT_IQ2_XXS) | (1u << FLH_FMT_IQ3_XXS);
-    constexpr uint32_t kGpuI8K = 1u << FLH_FMT_Q4_K;
-    if (i8_mask == kGpuI8 && i8k_mask == kGpuI8K) {
-        i8_mask |= 1u << FLH_FMT_Q6_K;
-        i8k_mask |= 1u << FLH_FMT_Q6_K;
-    }
     hipStream_t s = (hipStream_t)stream;
     for (uint32_t i = 0; i < n; ++i) {
         const flh_task & k = t[i];

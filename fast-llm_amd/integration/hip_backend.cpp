@@ -38,6 +38,16 @@ struct HipBackend {
         return p;
     }
 
+    // The decoder's aux_alloc (src/model/decoder.cpp:779) for the decode-op
+    // param blocks (RmsNormP, RouterSelP, SiluMulP, WmergeP): flh_exec_tasks
+    // reads them on the host, so they live in pinned host memory, not in the
+    // device arena.  Freed by the caller with flh_host_free at shutdown.
+    void * aux_alloc(size_t bytes) {
+        void * p = nullptr;
+        check(flh_host_alloc(bytes, &p), "flh_host_alloc");
+        return p;
+    }
+
     // One token: the frozen task table in topological order (run_serial's
     // order, src/runtime/graph.cpp:116-148).  `tasks` is the host copy of
     // Graph::tasks_; all pointers inside refer to arena memory.

@@ -150,6 +150,12 @@ int flh_arena_destroy(flh_arena * a);
 /* Plain device buffers (outside any arena). */
 int flh_malloc(size_t bytes, void ** out);
 int flh_free(void * p);
+/* Pinned host memory (hipHostMalloc): host-readable and device-visible; the
+ * place for the decode-op param blocks a task table points to (see
+ * flh_exec_tasks).  No counterpart in the reference, whose managed arena
+ * is host-readable as it is (src/runtime/arena.cpp:54-63). */
+int flh_host_alloc(size_t bytes, void ** out);
+int flh_host_free(void * p);
 int flh_upload(void * dst_dev, const void * src_host, size_t n, void * stream);
 int flh_download(void * dst_host, const void * src_dev, size_t n, void * stream);
 /* device-to-device copy of n bytes on a stream (asynchronous) */
@@ -243,13 +249,18 @@ int flh_rmsnorm_stream_dot(int fmt, const void * w, uint64_t w_bytes, uint32_t r
  * STREAM_DOT row tiles of one matrix (same fmt/cols/x/nx/strides, w and y
  * contiguous) are fused into one launch, and an ACT_Q8 followed by its
  * single-column q8_K consumer runs as flh_act_q8_stream_dot; results are
- * unchanged.  Masks: when (i8_mask, i8k_mask) are exactly the reference's
- * GPU defaults (kI8MaskGpuDefault / kI8KMaskGpuDefault,
- * src/runtime/kernels.h:927-940), Q6_K is promoted to the q8_K int8 path
- * (both masks gain the Q6_K bit): the reference keeps Q6_K on fp32 dequant
- * only because its CUDA int8 Q6_K kernel measured slower; here the int8
- * kernel is the streaming one and the fp32 modes are correctness kernels.
- * Any other masks are used as given. */
+ * unchanged.  Masks are used as given, the same way as by every other entry
+ * point (the same dot gives the same bits through any of them): pass the
+ * reference's CPU masks (flh_default_masks) for the int8 parity path.  With
+ * the reference's GPU defaults (kI8MaskGpuDefault / kI8KMaskGpuDefault,
+ * src/runtime/kernels.h:927-940) Q6_K takes the fp32 dequant route, one
+ * thread per row: a correctness mode, not a throughput path.
+ * The param blocks that RMSNORM, ROUTER_SEL, SILU_MUL and WMERGE tasks point
+ * to through aux are read by the host when the table is issued, so they must
+ * be host-readable (host, pinned or managed memory; flh_host_alloc gives
+ * pinned memory): a block in device memory is rejected with FLH_ERR_ARG
+ * before anything is launched.  The buffers those blocks name, and every
+ * other Task pointer, are device memory. */
 int flh_exec_tasks(const flh_task * tasks, uint32_t n, int fast,
                    uint32_t i8_mask, uint32_t i8k_mask, void * stream);
 

@@ -1,7 +1,11 @@
 """RMSNORM -> ACT_Q8 on the device (flh_rmsnorm_act_q8, and RMSNORM + ACT_Q8
 task pairs in flh_exec_tasks) against the oracle's fl_op_rmsnorm
-(src/runtime/decode_params.h:101-106; oracle pinned to the reference in
-tests/test_oracle_math.py).
+(src/runtime/decode_params.h:101-106; oracle pinned to the reference's
+own outputs in tests/test_oracle_norm.py), and the decoder's whole
+norm -> quant -> matvec chain (src/model/decoder.cpp:874-880) against the
+reference's chain (tests/golden/golden_norm.npz, and oracle/_ref at the
+Llama-3-8B QKV and gate/up shapes) within 1e-3 * max|y|, the north-star
+tolerance.
 
 Bar: the reference sums the squares strictly in order on the CPU; the kernel
 sums them as a tree, so y may differ from the reference by the rounding of
@@ -224,3 +228,110 @@ def test_rmsnorm_stream_dot_kernels_agree(flh, orc, gpu, cfg, rows, n):
     want = y0.copy()
     orc.stream_dot(Q4_K, w, rows, n, outs[0][0], want, threads=8)
     assert np.array_equal(bits(outs[0][1]), bits(want))
+
+
+def test_param_blocks_device_memory_rejected(flh, orc, gpu):
+    """Decode-op param blocks are read by the host when the table is issued:
+    a block in device memory (where a binding that put everything in the
+    device arena would place it) is rejected with FLH_ERR_ARG before any
+    launch; the same block in pinned host memory (flh_host_alloc, where the
+    binding's aux_alloc puts it) runs the chain with the bits of a block in
+    ordinary host memory."""
+    print("[case] param block placement", flush=True)
+    n, rows = 4096, 64
+    rng = np.random.default_rng(6)
+    x = rng.standard_normal(n).astype(np.float32)
+    wn = (1 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+    w = sane_rows(Q4_K, rows, n, rng)
+    st = col_stride_floats(n)
+    dx = flh.DeviceBuffer.from_array(x, gpu)
+    dwn = flh.DeviceBuffer.from_array(wn, gpu)
+    dw = flh.DeviceBuffer.from_array(w, gpu)
+    T = flh.TaskKind
+
+    def run(aux_of):
+        dy = flh.DeviceBuffer.from_array(np.zeros(st, np.float32), gpu)
+        out = flh.DeviceBuffer.from_array(np.zeros(rows, np.float32), gpu)
+        p = flh.RmsNormP(dwn.ptr, dx.ptr, dy.ptr, 1e-5, n)
+        t0 = flh.Task(); t0.kind = int(T.RMSNORM); t0.aux = aux_of(p)
+        t1 = flh.Task(); t1.kind = int(T.ACT_Q8); t1.x = dy.ptr; t1.y = dy.ptr + flh.xq_offset(n)
+        t1.rows = n // 32; t1.cols = n
+        t2 = flh.Task(); t2.kind = int(T.STREAM_DOT); t2.fmt = Q4_K; t2.w = dw.ptr; t2.w_bytes = w.size
+        t2.x = dy.ptr; t2.y = out.ptr; t2.rows = rows; t2.cols = n
+        flh.exec_tasks([t0, t1, t2], gpu)
+        return dy.download(np.float32, st, gpu), out.download(np.float32, rows, gpu)
+
+    keep = []
+
+    def on_device(p):
+        b = flh.DeviceBuffer.from_array(np.frombuffer(bytes(p), np.uint8), gpu)
+        keep.append(b)
+        return b.ptr
+
+    def pinned(p):
+        h = flh.HostBuffer(ctypes.sizeof(p))
+        ctypes.memmove(h.ptr, ctypes.addressof(p), ctypes.sizeof(p))
+        keep.append(h)
+        return h.ptr
+
+    with pytest.raises(flh.FlhError) as e:
+        run(on_device)
+    assert e.value.code == flh.ERR_ARG and "param block" in str(e.value)
+    gpu.sync()
+    want = run(lambda p: keep.append(p) or ctypes.addressof(p))
+    got = run(pinned)
+    assert np.array_equal(bits(got[0]), bits(want[0])) and np.array_equal(bits(got[1]), bits(want[1]))
+
+
+def norm_dot_device(flh, gpu, x, wn, w, rows, cols):
+    """flh_rmsnorm_stream_dot: the normed column (with appendices) and y."""
+    st = col_stride_floats(cols)
+    dx = flh.DeviceBuffer.from_array(x, gpu)
+    dwn = flh.DeviceBuffer.from_array(wn, gpu)
+    dxn = flh.DeviceBuffer.from_array(np.zeros(st, np.float32), gpu)
+    dw = flh.DeviceBuffer.from_array(w, gpu)
+    dy = flh.DeviceBuffer.from_array(np.zeros(rows, np.float32), gpu)
+    flh.rmsnorm_stream_dot(Q4_K, dw, rows, cols, dx, dwn, 1e-5, dxn, dy, gpu)
+    return dxn.download(np.uint8, x_alloc_bytes(cols), gpu), dy.download(np.float32, rows, gpu)
+
+
+@pytest.mark.parametrize("i", [0, 1])
+def test_norm_chain_vs_reference_golden(flh, gpu, i):
+    """The device chain against the reference's own chain (golden vectors):
+    the normed column within the sequential-sum bound, the dot within
+    1e-3 * max|y_ref|."""
+    from norm_cases import CHAIN_CASES, chain_inputs, digest
+    import os
+    G = np.load(os.path.join(os.path.dirname(__file__), "golden", "golden_norm.npz"))
+    rows, cols, seed = CHAIN_CASES[i]
+    print("[case] norm chain golden", rows, cols, flush=True)
+    x, wn, w = chain_inputs(rows, cols, seed)
+    assert bytes(G[f"c{i}_digest"]) == digest(x, wn, w)
+    col, y = norm_dot_device(flh, gpu, x, wn, w, rows, cols)
+    want_col, want = G[f"c{i}_col"], G[f"c{i}_y"]
+    check_y(col[:4 * cols].view(np.float32), want_col[:4 * cols].view(np.float32), cols)
+    assert np.max(np.abs(y - want)) <= 1e-3 * np.max(np.abs(want))
+
+
+@pytest.mark.parametrize("rows", [6144, 28672])
+def test_norm_chain_vs_reference_full_shape(flh, gpu, rows):
+    """At the Llama-3-8B QKV and gate/up shapes (one launch on the device):
+    the reference's chain, run from its own compiled code (oracle/_ref; the
+    pinned oracle where that library is absent), against
+    flh_rmsnorm_stream_dot, within 1e-3 * max|y_ref|."""
+    from oracle import Oracle, REF_SO
+    import os
+    cols = 4096
+    print("[case] norm chain full", rows, cols, flush=True)
+    rng = np.random.default_rng(rows)
+    x = rng.standard_normal(cols).astype(np.float32)
+    x[rng.random(cols) < 0.01] *= 20.0
+    wn = (1 + 0.1 * rng.standard_normal(cols)).astype(np.float32)
+    w = sane_rows(Q4_K, rows, cols, rng)
+    ref = Oracle(ref=os.path.exists(REF_SO))
+    rcol = ref.act_q8(ref.rmsnorm(x, wn, 1e-5))
+    want = np.zeros(rows, np.float32)
+    ref.stream_dot(Q4_K, w, rows, cols, rcol.view(np.float32), want, threads=8)
+    col, y = norm_dot_device(flh, gpu, x, wn, w, rows, cols)
+    check_y(col[:4 * cols].view(np.float32), rcol[:4 * cols].view(np.float32), cols)
+    assert np.max(np.abs(y - want)) <= 1e-3 * np.max(np.abs(want))

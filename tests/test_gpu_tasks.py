@@ -157,28 +157,44 @@ def test_unsupported_kind_launches_nothing(flh, gpu):
     assert not np.any(d["y4"].download(np.float32, 600, gpu))
 
 
-def test_gpu_default_masks_take_q6k_int8(flh, orc, gpu):
-    """With the reference's GPU-default masks (kernels.h:927-940: Q6_K on fp32
-    dequant), the table runs Q6_K on the q8_K int8 path: every output equals
-    the CPU-default (i8k) result bit for bit.  Other masks are honoured: the
-    GPU i8 mask with a q8_K mask that also names Q6_K gives the same, and
-    dropping Q6_K from both masks still gives the fp32 dequant bits."""
+def test_masks_same_bits_every_entry_point(flh, orc, gpu):
+    """Masks are used as given by every entry point.  With the reference's
+    GPU-default masks (kernels.h:927-940: Q6_K off both int8 masks) the
+    table's Q6_K tiles take the fp32 dequant route, as the oracle's
+    exec_task_cpu does with those masks, and one Q6_K dot through the table
+    equals the same dot through flh_stream_dot with the same masks, bit for
+    bit; the other formats keep their int8 routes."""
     print("[case] task table gpu masks", flush=True)
     d = build(flh, gpu, np.random.default_rng(10), 1024)
-    want = expected(orc, d)
+    cols, st = d["cols"], d["st"]
     gpu_i8 = (1 << 1) | (1 << 2) | (1 << 3) | (1 << 5) | (1 << 6)
     gpu_i8k = 1 << 3
     zero_outputs(d, gpu)
     flh.exec_tasks(table(flh, d), gpu, i8_mask=gpu_i8, i8k_mask=gpu_i8k)
-    for g, w in zip(read(d, gpu), want):
-        assert np.array_equal(bits(g), bits(w))
-    # a non-default mask without Q6_K anywhere: the Q6_K tiles use fp32 dequant
-    zero_outputs(d, gpu)
-    flh.exec_tasks(table(flh, d), gpu, i8_mask=gpu_i8 & ~(1 << 5), i8k_mask=gpu_i8k)
-    y6 = read(d, gpu)[1]
-    cols = d["cols"]
-    xq = orc.act_q8_cols(d["xs"], d["st"])
+    y4, y6, y8, merged = read(d, gpu)
+    xq = orc.act_q8_cols(d["xs"], st)
+    x0, x1 = xq[:st], xq[st:]
     f6 = np.zeros(40, np.float32)
-    orc.stream_dot(Q6_K, d["w6"], 40, cols, xq[d["st"]:], f6, id_slot=2, estride=40 * row_bytes(Q6_K, cols),
-                   i8_mask=0, i8k_mask=0)
+    orc.stream_dot(Q6_K, d["w6"], 40, cols, x1, f6, id_slot=2, estride=40 * row_bytes(Q6_K, cols),
+                   i8_mask=gpu_i8, i8k_mask=gpu_i8k)
     assert np.array_equal(bits(y6), bits(f6))
+    w4 = np.zeros(600, np.float32)
+    orc.stream_dot(Q4_K, d["w4"], 600, cols, x0, w4, i8_mask=gpu_i8, i8k_mask=gpu_i8k)
+    assert np.array_equal(bits(y4), bits(w4))
+    # the same Q6_K expert dot through flh_stream_dot with the same masks
+    rb6 = row_bytes(Q6_K, cols)
+    dy = flh.DeviceBuffer(40 * 4)
+    dy.zero(gpu)
+    flh.stream_dot(Q6_K, d["dw6"].ptr + 2 * 40 * rb6, 40, cols, d["x"].ptr + 4 * st, dy, gpu,
+                   i8_mask=gpu_i8, i8k_mask=gpu_i8k, w_bytes=40 * rb6)
+    assert np.array_equal(bits(dy.download(np.float32, 40, gpu)), bits(y6))
+    # and with the CPU-default masks both give the q8_K int8 bits
+    zero_outputs(d, gpu)
+    flh.exec_tasks(table(flh, d), gpu)
+    dy.zero(gpu)
+    flh.stream_dot(Q6_K, d["dw6"].ptr + 2 * 40 * rb6, 40, cols, d["x"].ptr + 4 * st, dy, gpu, w_bytes=40 * rb6)
+    want = expected(orc, d)
+    assert np.array_equal(bits(read(d, gpu)[1]), bits(want[1]))
+    assert np.array_equal(bits(dy.download(np.float32, 40, gpu)), bits(want[1]))
+
+
