@@ -138,7 +138,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-ops", action="store_true", help="headline only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--profile", nargs="?", const="gate_up", choices=sorted(PROFILE_OPS),
+    ap.add_argument("--profile", nargs="?", const="gate_up", choices=sorted(PROFILE_OPS) + [PROFILE_ALL],
                     help="counter-collection run: a 256 MiB device copy (calibration) and "
                          "64 launches of one operation only (see PROFILE_OPS), no JSON line")
     args = ap.parse_args()
@@ -434,17 +434,35 @@ PROFILE_OPS["norm_qkv"] = (Q4_K, 6144, 4096, 1, "norm")
 PROFILE_OPS["norm_gate_up"] = (Q4_K, 28672, 4096, 1, "norm")
 
 
-def profile_run(flh, B, s, staging, which="gate_up"):
+PROFILE_OPS["chain"] = (Q4_K, 0, 4096, 1, "chain")
+PROFILE_OPS["moe1"] = (Q4_K, 0, 4096, 1, "moe")
+PROFILE_OPS["moe8"] = (Q4_K, 0, 4096, 8, "moe")
+PROFILE_OPS["act_q8_14336"] = (Q4_K, 0, 14336, 1, "act")
+PROFILE_OPS["rmsnorm_act_q8"] = (Q4_K, 0, 4096, 1, "rmsnorm")
+PROFILE_ALL = "all"
+
+
+def profile_run(flh, B, s, staging, which="gate_up", launches=64, calibrate=True):
     """What the committed counter profiles were collected on: 5 device copies
-    of 256 MiB (known HBM bytes: read 256 MiB + write 256 MiB each), then 64
-    launches of one operation of PROFILE_OPS."""
-    n = 256 << 20
-    src, dst = B.buf(n), B.buf(n)
-    src.zero(s)
-    for _ in range(5):
-        flh.copy(dst, src, n, s)
-    s.sync()
+    of 256 MiB (known HBM bytes: read 256 MiB + write 256 MiB each), then
+    `launches` launches of one operation of PROFILE_OPS, issued straight on
+    the stream (no graphs).  which="all": every operation of PROFILE_OPS in
+    turn, 16 launches each (the kernel statistics of every bench op line)."""
+    if calibrate:
+        n = 256 << 20
+        src, dst = B.buf(n), B.buf(n)
+        src.zero(s)
+        for _ in range(5):
+            flh.copy(dst, src, n, s)
+        s.sync()
+    if which == PROFILE_ALL:
+        for name in PROFILE_OPS:
+            print(f"profile op {name}", flush=True)
+            profile_run(flh, Bench(flh, s), s, staging, name, launches=16, calibrate=False)
+        return
     fmt, r, c, nx, kind = PROFILE_OPS[which]
+    if kind in ("chain", "moe", "act", "rmsnorm"):
+        return profile_glue(flh, B, s, staging, kind, c, nx, launches)
     if kind == "dot_nomfma":
         os.environ["FLH_NO_MFMA"] = "1"
         flh.init(0)
@@ -460,16 +478,83 @@ def profile_run(flh, B, s, staging, which="gate_up"):
         xn, _ = B.activation(c, 1, 13, outliers=False)
         wn = B.buf(c * 4)
         flh.fill_normal(wn, c, 14, s, mean=1.0, std=0.1)
-    for i in range(64):
+    for i in range(launches):
         if kind == "norm":
             flh.rmsnorm_stream_dot(fmt, ws[i % len(ws)], r, c, x, wn, 1e-5, xn, y, s)
         elif kind == "fused":
             flh.act_q8_stream_dot(fmt, ws[i % len(ws)], r, c, x, y, s)
-        elif kind == "act":
-            flh.act_q8(x, c, s)
         else:
             flh.stream_dot(fmt, ws[i % len(ws)], r, c, x, y, s, nx=nx, xstride=st, ystride=r, i8_mask=m8)
     s.sync()
+    if kind == "dot_nomfma":
+        del os.environ["FLH_NO_MFMA"]
+        flh.init(0)
+    for b in B.bufs:
+        b.close()
+    B.bufs.clear()
+
+
+def profile_glue(flh, B, s, staging, kind, cols, ntok, launches):
+    """--profile runs of the op lines that are not one matvec: the decoder's
+    5-launch chain of a layer, the MoE FFN (batch 1 or 8), ACT_Q8 of a
+    14336-wide column, RMSNORM -> ACT_Q8 of a 4096-wide one."""
+    if kind == "act":
+        x, _ = B.activation(cols, 1, 70, outliers=False)
+        for _ in range(launches):
+            flh.act_q8(x, cols, s)
+    elif kind == "rmsnorm":
+        x, _ = B.activation(cols, 1, 71, outliers=False)
+        wn = B.buf(cols * 4)
+        flh.fill_normal(wn, cols, 72, s, mean=1.0, std=0.1)
+        yr, _ = B.activation(cols, 1, 73, outliers=False)
+        for _ in range(launches):
+            flh.rmsnorm_act_q8(x, wn, yr, cols, 1e-5, s)
+    elif kind == "chain":
+        D_, F_ = 4096, 14336
+        L = 3
+        W = {name: B.weights(Q4_K, r, c, L, seed=101 + r + 7 * c, staging=staging) for name, r, c in LAYER}
+        x0, _ = B.activation(D_, 1, 80, outliers=True)
+        xo, _ = B.activation(D_, 1, 81, outliers=True)
+        wn1, wn2 = B.buf(D_ * 4), B.buf(D_ * 4)
+        flh.fill_normal(wn1, D_, 81, s, mean=1.0, std=0.1)
+        flh.fill_normal(wn2, D_, 82, s, mean=1.0, std=0.1)
+        xn1, _ = B.activation(D_, 1, 83, outliers=False)
+        xn2, _ = B.activation(D_, 1, 84, outliers=False)
+        h, _ = B.activation(F_, 1, 85, outliers=False)
+        y = {name: B.buf(r * 4) for name, r, c in LAYER}
+        gu = y["gate_up"]
+        for i in range(launches):
+            l = i % L
+            flh.rmsnorm_stream_dot(Q4_K, W["qkv"][l], 6144, D_, x0, wn1, 1e-5, xn1, y["qkv"], s)
+            flh.act_q8_stream_dot(Q4_K, W["o"][l], D_, D_, xo, y["o"], s)
+            flh.rmsnorm_stream_dot(Q4_K, W["gate_up"][l], 2 * F_, D_, x0, wn2, 1e-5, xn2, gu, s)
+            flh.silu_mul_act_q8(gu, gu.ptr + F_ * 4, h, F_, 1, 2 * F_, col_stride(flh, F_), s)
+            flh.stream_dot(Q4_K, W["down"][l], D_, F_, h, y["down"], s)
+    elif kind == "moe":
+        E, K, D, F = 8, 2, 4096, 14336
+        gu_b = 2 * F * flh.row_bytes(Q4_K, D)
+        dn_b = D * flh.row_bytes(Q4_K, F)
+        gu = B.weights(Q4_K, E * 2 * F, D, 1, seed=300, staging=staging)[0]
+        dn = B.weights(Q4_K, E * D, F, 1, seed=400, staging=staging)[0]
+        stD, stF = col_stride(flh, D), col_stride(flh, F)
+        x, _ = B.activation(D, ntok, 60, outliers=False)
+        lb = B.buf(ntok * E * 4)
+        lb.upload(np.random.default_rng(2).standard_normal(ntok * E).astype(np.float32), s)
+        ids, gates = B.buf(ntok * K * 4), B.buf(ntok * K * 4)
+        ygu, ydn = B.buf(ntok * K * 2 * F * 4), B.buf(ntok * K * D * 4)
+        h = B.buf(ntok * K * stF * 4)
+        h.zero(s)
+        yo = B.buf(ntok * D * 4)
+        for _ in range(launches):
+            flh.router_moe_dot(Q4_K, gu, gu_b, 2 * F, D, lb, ntok, E, K, 1, 1.0, ids, gates, x, stD,
+                               False, ygu, 2 * F, s)
+            flh.silu_mul_act_q8(ygu, ygu.ptr + F * 4, h, F, ntok * K, 2 * F, stF, s)
+            flh.moe_dot(Q4_K, dn, dn_b, D, F, ids, ntok, K, E, h, stF, True, ydn, D, s)
+            flh.wmerge(ydn, gates, None, None, yo, 1.0, K, D, 0, ntok, K * D, D, s)
+    s.sync()
+    for b in B.bufs:
+        b.close()
+    B.bufs.clear()
 
 
 def traffic_from_profile():
@@ -487,12 +572,13 @@ def traffic_from_profile():
 
 def bench_moe(flh, B, s, staging, cpu_in):
     """Mixtral-style MoE FFN: router + grouped gate/up (one launch) -> silu*up +
-    ACT_Q8 (one launch) -> grouped down -> weighted merge.  Two copies of the expert
-    set alternate."""
+    ACT_Q8 (one launch) -> grouped down -> weighted merge.  Three copies of the
+    expert set rotate, so the routed experts of consecutive steps (198 MB per
+    step at batch 1) cycle through more than 2x the 256 MB Infinity Cache."""
     E, K, D, F = 8, 2, 4096, 14336
     gu_b = 2 * F * flh.row_bytes(Q4_K, D)
     dn_b = D * flh.row_bytes(Q4_K, F)
-    copies = 2
+    copies = 3
     gu = [B.weights(Q4_K, E * 2 * F, D, 1, seed=300 + c, staging=staging)[0] for c in range(copies)]
     dn = [B.weights(Q4_K, E * D, F, 1, seed=400 + c, staging=staging)[0] for c in range(copies)]
     out = {"ops": {}}
