@@ -108,6 +108,7 @@ void load_tune() {
         if (got == 3) t.mf_kh = (int)k;
     }
     if (const char * e = getenv("FLH_MFMA_XC")) t.mf_xc = atoi(e) != 0;
+    if (const char * e = getenv("FLH_MFMA_OWN")) t.mf_own = atoi(e) != 0;
     if (const char * e = getenv("FLH_MFMA_MIN_COLS")) t.mf_min_cols = (uint32_t)atoi(e);
     if (const char * e = getenv("FLH_NO_MFMA")) t.no_mfma = atoi(e) != 0;
     if (const char * e = getenv("FLH_SBL_NX_DEP")) t.sbl_nx_dep = (uint32_t)atoi(e);

@@ -100,13 +100,15 @@ __device__ __forceinline__ uint32_t mf_sbh(uint32_t li, uint32_t h) { return 4 *
 template <int NC> __host__ __device__ constexpr uint32_t mf_xci() { return (19 * NC + 63) / 64; }
 template <int NC, bool XC> __host__ __device__ constexpr uint32_t mf_stg() { return XC ? MF_CHUNK + NC * MF_XB : MF_CHUNK; }
 template <int NC, bool XC> __host__ __device__ constexpr int mf_ni() { return XC ? MF_NI + (int)mf_xci<NC>() : MF_NI; }
-template <int NC, bool KH, bool XC = false>
+// OWN (register accumulators, whole activations only): the parked terms are
+// replaced by the per-(tile, accumulator class) sums AC[nrb / 16][4][16][NC].
+template <int NC, bool KH, bool XC = false, bool OWN = false>
 __host__ __device__ inline size_t mf_smem_bytes(uint32_t nrb, uint32_t nsb, int D) {
     const uint32_t nl = KH ? mf_nsbh(nsb, 0) : nsb;
+    const size_t terms = OWN ? (size_t)nrb * 4 * NC * 4 : (size_t)mf_ts<NC>(nrb) * nl * 8 + (size_t)mf_ths(nrb) * nl * 4;
     return (size_t)MF_WAVES * D * mf_stg<NC, XC>() +
-           (KH ? (size_t)nl * NC * MF_XB : XC ? 0 : (size_t)NC * mf_xs(nl)) + (size_t)mf_ts<NC>(nrb) * nl * 8 +
-           (size_t)mf_ths(nrb) * nl * 4 + (size_t)nrb * NC * 4 + (KH ? (size_t)nrb * NC * 4 : 0) +
-           (KH || XC ? (size_t)NC * nsb * 4 : 0) + (NC <= 8 ? 128 : 0);
+           (KH ? (size_t)nl * NC * MF_XB : XC ? 0 : (size_t)NC * mf_xs(nl)) + terms + (size_t)nrb * NC * 4 +
+           (KH ? (size_t)nrb * NC * 4 : 0) + (KH || XC ? (size_t)NC * nsb * 4 : 0) + (NC <= 8 ? 128 : 0);
 }
 
 // Column sources of one pass: activation column p at x(p) (fp32 x followed by
@@ -184,6 +186,25 @@ __device__ __forceinline__ void mf_ld_x8(uint32_t ax, uint32_t ab, u32x2 (&xw)[8
         : "=&v"(xw[0]), "=&v"(xw[1]), "=&v"(xw[2]), "=&v"(xw[3]), "=&v"(xw[4]), "=&v"(xw[5]), "=&v"(xw[6]),
           "=&v"(xw[7]), "=&v"(bp)
         : "v"(ax), "v"(ab));
+}
+
+// up to 4 dwords at LDS addresses a[i], one wait (hidden from the compiler's
+// wait-count pass, as mf_ld_x)
+template <int N>
+__device__ __forceinline__ void mf_ld_dk(const uint32_t (&a)[N], float (&v)[N]) {
+    uint32_t r[4];
+    if constexpr (N == 1) {
+        asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=&v"(r[0]) : "v"(a[0]));
+    } else if constexpr (N == 2) {
+        asm volatile("ds_read_b32 %0, %2\n\tds_read_b32 %1, %3\n\ts_waitcnt lgkmcnt(0)"
+                     : "=&v"(r[0]), "=&v"(r[1]) : "v"(a[0]), "v"(a[1]));
+    } else {
+        asm volatile("ds_read_b32 %0, %4\n\tds_read_b32 %1, %5\n\tds_read_b32 %2, %6\n\tds_read_b32 %3, %7\n\t"
+                     "s_waitcnt lgkmcnt(0)"
+                     : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]) : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]));
+    }
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = __uint_as_float(r[i]);
 }
 
 __device__ __forceinline__ void lds_st64(void * p, u32x2 v) {
@@ -331,7 +352,7 @@ __device__ __forceinline__ float mf_fold_h(const int * TI, const int * TM, const
 // 16-row tile of the batch; the batch's chunks q = (tile, sb), tile-major, are
 // dealt to the waves round-robin (with K halves: per half, the first half of
 // batch bt being half bt & 1, whose activations are staged already).
-template <int NC, int D, bool KH, typename COLS, bool XC = false>
+template <int NC, int D, bool KH, typename COLS, bool XC = false, bool OWN = false>
 __device__ __forceinline__ void mf_body(const uint8_t * __restrict__ w, uint32_t rows, uint32_t cols,
                                         const COLS & C, uint32_t nx, uint32_t nrbp, uint32_t g, uint32_t G,
                                         uint8_t * sm) {
@@ -354,10 +375,12 @@ __device__ __forceinline__ void mf_body(const uint8_t * __restrict__ w, uint32_t
     uint8_t * myst = sm + (size_t)wave * D * STG;
     const uint32_t XS = KH || XC ? 0u : mf_xs(NL);
     uint8_t * xr = sm + (size_t)MF_WAVES * D * STG;
+    static_assert(!OWN || (!KH && !XC), "register accumulators: whole activations staged");
     int * TI = (int *)(xr + (KH ? (size_t)NL * NC * MF_XB : (size_t)NC * XS));
     int * TM = TI + (size_t)mf_ts<NC>(nrb) * NL;
     uint32_t * TH = (uint32_t *)(TM + (size_t)mf_ts<NC>(nrb) * NL);
-    float * ysm = (float *)(TH + (size_t)mf_ths(nrb) * NL);
+    float * AC = (float *)TI;                                     // OWN: [nrb / 16][4][16][NC]
+    float * ysm = OWN ? AC + (size_t)nrb * 4 * NC : (float *)(TH + (size_t)mf_ths(nrb) * NL);
     float * yph = ysm + (size_t)nrb * NC;                         // KH: first half's sums
     float * dkt = KH ? yph + (size_t)nrb * NC : yph;              // KH, XC: q8_K scales [NC][nsb]
     uint8_t * zr = KH || XC ? (uint8_t *)(dkt + (size_t)NC * nsb) : (uint8_t *)yph;   // NC <= 8: zeros
@@ -433,9 +456,32 @@ __device__ __forceinline__ void mf_body(const uint8_t * __restrict__ w, uint32_t
     const uint32_t po0 = (lane % 9) * 16, po1 = ((64 + lane) % 9) * 16, po2 = ((128 + (lane >> 2)) % 9) * 16 + 4 * (lane & 3);
     // issue cursor: batch qbt, phase qph, tile qt, local superblock qsb
     // (q = wave + 8 i over the phase's chunks, tile-major)
-    uint32_t qbt = 0, qph = 0, qt = 0, qsb = wave, qnl = nl_of(half_of(0, 0));
+    // OWN: wave w owns accumulator class k = w % 4 (superblocks k, k + 4, ...
+    // of a tile, in order) of the tiles t = w / 4, w / 4 + 2, ...; otherwise
+    // the phase's chunks q = wave + 8 i, tile-major
+    const uint32_t own_k = wave & 3, own_t = wave >> 2;
+    auto cur_first = [&](uint32_t & t, uint32_t & sb, uint32_t nl) {
+        if constexpr (OWN) {
+            t = own_t;
+            sb = own_k;
+        } else {
+            t = 0;
+            sb = wave;
+            while (sb >= nl) { sb -= nl; ++t; }
+        }
+    };
+    auto cur_next = [&](uint32_t & t, uint32_t & sb, uint32_t nl) {
+        if constexpr (OWN) {
+            sb += 4;
+            if (sb >= nl) { sb = own_k; t += 2; }
+        } else {
+            sb += MF_WAVES;
+            while (sb >= nl) { sb -= nl; ++t; }
+        }
+    };
+    uint32_t qbt = 0, qph = 0, qt = 0, qsb = 0, qnl = nl_of(half_of(0, 0));
     uint32_t qnt = nbatch ? (nrow_of(0) + 15) >> 4 : 0;
-    while (qsb >= qnl) { qsb -= qnl; ++qt; }
+    cur_first(qt, qsb, qnl);
     uint32_t nissued = 0, ncons = 0;
     // K halves: this wave's DMA instructions so far (vm), and that count right
     // after each ring stage's chunk, the y DMA and the latest restaging: the
@@ -467,10 +513,8 @@ __device__ __forceinline__ void mf_body(const uint8_t * __restrict__ w, uint32_t
                 ++qbt;
                 qnt = qbt < nbatch ? (nrow_of(qbt) + 15) >> 4 : 0;
             }
-            qt = 0;
-            qsb = wave;
             qnl = nl_of(half_of(qbt, qph));
-            while (qsb >= qnl) { qsb -= qnl; ++qt; }
+            cur_first(qt, qsb, qnl);
         }
         if (qbt < nbatch) {
             const uint32_t tr0 = rbeg + qbt * nrb + 16 * qt;
@@ -496,8 +540,7 @@ __device__ __forceinline__ void mf_body(const uint8_t * __restrict__ w, uint32_t
                 ce0 = (nissued & 1) ? ce0 : vm;
             }
             ++nissued;
-            qsb += MF_WAVES;
-            while (qsb >= qnl) { qsb -= qnl; ++qt; }
+            cur_next(qt, qsb, qnl);
         }
     };
     // old y of a batch -> LDS (one 64-float DMA per wave; nrb * NC <= 512)
@@ -525,6 +568,39 @@ __device__ __forceinline__ void mf_body(const uint8_t * __restrict__ w, uint32_t
     MF_STAMP(1);
 
     const uint32_t fk = tid & 3, fp = (tid >> 2) % NC, frl0 = tid / (4 * NC);
+    // OWN: this lane's running sums of accumulator class own_k for its NCL
+    // (row r, column c0 + i) pairs of the current tile, in the reference's
+    // fmaf order (fl_dot_i8k_q4_K, src/runtime/quants.h:538-561), stored to
+    // AC after the class's last superblock of the tile
+    constexpr int NCL = NC == 4 ? 1 : NC == 8 ? 2 : 4;
+    float acc_o[NCL];
+#pragma unroll
+    for (int i = 0; i < NCL; ++i) acc_o[i] = 0.f;
+    auto own_step = [&](const int (&ti)[NCL], const float (&tm)[NCL], uint32_t c0, uint32_t hdx, uint32_t li,
+                        uint32_t nl, uint32_t t) {
+        const float d = h2f(hdx & 0xFFFFu), dmin = h2f(hdx >> 16);
+        uint32_t da[NCL];
+#pragma unroll
+        for (int i = 0; i < NCL; ++i) da[i] = lds_off(xr + (size_t)(c0 + i) * XS + (size_t)li * 292);
+        float dk[NCL];
+        mf_ld_dk<NCL>(da, dk);
+        if (li == own_k) {
+#pragma unroll
+            for (int i = 0; i < NCL; ++i) acc_o[i] = 0.f;
+        }
+#pragma unroll
+        for (int i = 0; i < NCL; ++i) {
+            acc_o[i] = fmaf(d * dk[i], (float)ti[i], acc_o[i]);
+            acc_o[i] = fmaf(-(dmin * dk[i]), tm[i], acc_o[i]);
+        }
+        if (li + 4 >= nl) {
+            float * ap = AC + ((size_t)(t * 4 + own_k) * 16 + r) * NC + c0;
+            if constexpr (NCL == 1) lds_st32(ap, __float_as_uint(acc_o[0]));
+            else if constexpr (NCL == 2) lds_st64(ap, u32x2{__float_as_uint(acc_o[0]), __float_as_uint(acc_o[1])});
+            else lds_st128(ap, u32x4a{__float_as_uint(acc_o[0]), __float_as_uint(acc_o[1]),
+                                      __float_as_uint(acc_o[2]), __float_as_uint(acc_o[3])});
+        }
+    };
     constexpr uint32_t FROWS = MF_WAVES * 64 / (4 * NC);         // rows folded per pass
     uint32_t slot = 0;
     for (uint32_t bt = 0; bt < nbatch; ++bt) {
@@ -534,8 +610,8 @@ __device__ __forceinline__ void mf_body(const uint8_t * __restrict__ w, uint32_t
         if (bt != 0) issue_y(bt);
         for (uint32_t ph = 0; ph < NPH; ++ph) {
             const uint32_t h = half_of(bt, ph), nl = nl_of(h);
-            uint32_t ct = 0, csb = wave;                           // consume cursor
-            while (csb >= nl) { csb -= nl; ++ct; }
+            uint32_t ct = 0, csb = 0;                              // consume cursor
+            cur_first(ct, csb, nl);
             // K halves: a slot is restaged right after its last use when one
             // wave consumes every chunk of that slot (one tile, or nl a
             // multiple of the wave count); otherwise after the half
@@ -555,8 +631,7 @@ __device__ __forceinline__ void mf_body(const uint8_t * __restrict__ w, uint32_t
                 ++ncons;
                 if (ncons == 1) MF_STAMP(2);
                 const uint32_t t = ct, li = csb;
-                csb += MF_WAVES;
-                while (csb >= nl) { csb -= nl; ++ct; }
+                cur_next(ct, csb, nl);
                 const uint8_t * rp = myst + slot * STG + 144 * r;
                 const uint8_t * xs_c = myst + slot * STG + MF_CHUNK + MF_XO;   // XC: column blocks, 304 B apart
                 const u32x4a hd = *(const u32x4a *)rp;
@@ -672,6 +747,13 @@ __device__ __forceinline__ void mf_body(const uint8_t * __restrict__ w, uint32_t
                     // leaves columns 4e + 2h, 4e + 2h + 1 in lane row 2h + e
                     const auto u = __builtin_amdgcn_permlane32_swap((uint32_t)pr[0], (uint32_t)pr[2], false, false);
                     const auto v = __builtin_amdgcn_permlane32_swap((uint32_t)pr[1], (uint32_t)pr[3], false, false);
+                    if constexpr (OWN) {
+                        // min terms: lane row j holds columns 4 (j & 1) + i
+                        const int ti[NCL] = {(int)(u[0] + u[1]), (int)(v[0] + v[1])};
+                        const float tm[NCL] = {(j >> 1) ? cm[2] : cm[0], (j >> 1) ? cm[3] : cm[1]};
+                        own_step(ti, tm, 4 * (j & 1) + 2 * (j >> 1), hd.x, li, nl, t);
+                        continue;
+                    }
                     const size_t e = (size_t)li * mf_ts<NC>(nrb) + rl * NC;
                     lds_st64(&TI[e + 4 * (j & 1) + 2 * (j >> 1)], u32x2{u[0] + u[1], v[0] + v[1]});
                     if (j < 2)
@@ -686,6 +768,13 @@ __device__ __forceinline__ void mf_body(const uint8_t * __restrict__ w, uint32_t
                     int pr[4];
 #pragma unroll
                     for (int i = 0; i < 4; ++i) pr[i] = __mul24(s0, a0[i]) + __mul24(s1, a1[i]);
+                    if constexpr (OWN) {
+                        // every lane row holds the min terms of columns 0..3
+                        const int ti[NCL] = {mf_rowsum_t(pr)};
+                        const float tm[NCL] = {j == 0 ? cm[0] : j == 1 ? cm[1] : j == 2 ? cm[2] : cm[3]};
+                        own_step(ti, tm, j, hd.x, li, nl, t);
+                        continue;
+                    }
                     const size_t e = (size_t)li * mf_ts<NC>(nrb) + rl * NC;
                     lds_st32(&TI[e + j], (uint32_t)mf_rowsum_t(pr));
                     if (j == 0)
@@ -708,6 +797,14 @@ __device__ __forceinline__ void mf_body(const uint8_t * __restrict__ w, uint32_t
                     ia[i] = 0;
 #pragma unroll
                     for (int k = 0; k < 8; ++k) ia[i] += __mul24(sc[k], acc[k][i]);
+                }
+                if constexpr (OWN) {
+                    if constexpr (NC == 16) {
+                        const int ti[NCL] = {ia[0], ia[1], ia[2], ia[3]};
+                        const float tm[NCL] = {cm[0], cm[1], cm[2], cm[3]};
+                        own_step(ti, tm, 4 * j, hd.x, li, nl, t);
+                    }
+                    continue;
                 }
                 if (4 * j < NC) {
                     const size_t e = (size_t)li * mf_ts<NC>(nrb) + rl * NC + 4 * j;
@@ -751,7 +848,17 @@ __device__ __forceinline__ void mf_body(const uint8_t * __restrict__ w, uint32_t
                 if (fok && fk == 0) C.y(fp)[row0 + frl] = ysm[frl * NC + fp] + (yph[frl * NC + fp] + s1);
             }
         }
-        if constexpr (!KH) {
+        if constexpr (OWN) {
+            // (a0 + a1) + (a2 + a3) of every (row, column), one per thread
+            const uint32_t frl = tid / NC, p = tid % NC;
+            if (frl < nrow && p < nx) {
+                const float * ap = AC + ((size_t)((frl >> 4) * 4) * 16 + (frl & 15)) * NC + p;
+                uint32_t aa[4] = {lds_off(ap), lds_off(ap + 16 * NC), lds_off(ap + 32 * NC), lds_off(ap + 48 * NC)};
+                float av[4];
+                mf_ld_dk<4>(aa, av);
+                C.y(p)[row0 + frl] = ysm[frl * NC + p] + ((av[0] + av[1]) + (av[2] + av[3]));
+            }
+        } else if constexpr (!KH) {
             // every row of the batch in one call (nrow <= nrb <= 512 / NC = 4 FROWS)
             const bool fok = fp < nx;
             const uint8_t * xp = XC ? (const uint8_t *)(dkt + (size_t)fp * nsb) : xr + (size_t)fp * XS;
@@ -781,12 +888,12 @@ __device__ __forceinline__ void mf_body(const uint8_t * __restrict__ w, uint32_t
     MF_STAMP(4);
 }
 
-template <int NC, int D, bool KH, bool XC = false>
+template <int NC, int D, bool KH, bool XC = false, bool OWN = false>
 __global__ __launch_bounds__(512) void k_dot_mfma(DotArgs a, uint32_t nrb) {
     extern __shared__ __attribute__((aligned(16))) uint8_t sm[];
     const uint8_t * w = a.w + (a.id_slot ? (size_t)(*a.id_slot) * a.estride : 0);
     const MfColsStrided C{a.x, a.y, a.xstride, a.ystride};
-    mf_body<NC, D, KH, MfColsStrided, XC>(w, a.rows, a.cols, C, a.nx, nrb, blockIdx.x, gridDim.x, sm);
+    mf_body<NC, D, KH, MfColsStrided, XC, OWN>(w, a.rows, a.cols, C, a.nx, nrb, blockIdx.x, gridDim.x, sm);
 }
 
 // Grouped expert matvec (MoE): the routed experts share the grid (moe_assign).  The workgroup collects
@@ -804,7 +911,7 @@ struct MfColsMoe {
     __device__ float * y(uint32_t p) const { return y0 + (size_t)lds_ld32(&yi[p]) * ys; }
 };
 
-template <int NC, int D, bool KH>
+template <int NC, int D, bool KH, bool OWN = false>
 __global__ __launch_bounds__(512) void k_moe_mfma(MoeArgs a, uint32_t nrbp) {
     extern __shared__ __attribute__((aligned(16))) uint8_t sm[];
     __shared__ uint32_t pairs[256];
@@ -833,7 +940,7 @@ __global__ __launch_bounds__(512) void k_moe_mfma(MoeArgs a, uint32_t nrbp) {
         }
         __syncthreads();
         const MfColsMoe C{a.x, a.y, a.xstride, a.ystride, cxi, cyi};
-        mf_body<NC, D, KH>(w, a.rows, a.cols, C, nx, nrbp, g, G, sm);
+        mf_body<NC, D, KH, MfColsMoe, false, OWN>(w, a.rows, a.cols, C, nx, nrbp, g, G, sm);
         __syncthreads();
     }
 }
@@ -842,11 +949,19 @@ __global__ __launch_bounds__(512) void k_moe_mfma(MoeArgs a, uint32_t nrbp) {
 // chunks each wave requests before the activations are staged (the rest of
 // its ring after its first chunk); 0 = the whole ring (measured best here)
 static uint32_t mf_pro() { return tune().mf_pro; }          // 0: the whole ring
-template <int NC, int D, bool KH, bool XC = false>
+// Register accumulators (a wave owns one accumulator class of its tiles, no
+// parked terms, no fold pass) where the whole activations are staged, a class
+// has a superblock (nsb >= 4) and a batch holds at least two 16-row tiles
+// (with one, the waves of the second tile parity would idle: verify N = 4 at
+// 4096x14336, 16 rows per workgroup, 10.95 -> 12.15 us); measured at
+// 14336x4096: N = 4 10.94 -> 10.24 us, N = 8 12.82 -> 11.33 us.
+// FLH_MFMA_OWN=0: the parked-term fold everywhere.
+static bool mf_own(uint32_t nsb, uint32_t nrb) { return tune().mf_own && nsb >= 4 && nrb >= 32; }
+template <int NC, int D, bool KH, bool XC = false, bool OWN = false>
 static int mf_launch_d(const DotArgs & a, uint32_t nrb, uint32_t grid, size_t smb, hipStream_t s) {
-    (void)hipFuncSetAttribute((const void *)k_dot_mfma<NC, D, KH, XC>, hipFuncAttributeMaxDynamicSharedMemorySize,
+    (void)hipFuncSetAttribute((const void *)k_dot_mfma<NC, D, KH, XC, OWN>, hipFuncAttributeMaxDynamicSharedMemorySize,
                               (int)smb);
-    hipLaunchKernelGGL((k_dot_mfma<NC, D, KH, XC>), dim3(grid), dim3(MF_WAVES * 64), smb, s, a,
+    hipLaunchKernelGGL((k_dot_mfma<NC, D, KH, XC, OWN>), dim3(grid), dim3(MF_WAVES * 64), smb, s, a,
                        nrb | (mf_pro() << 16));
     return hip_check(hipGetLastError(), "k_dot_mfma launch");
 }
@@ -930,6 +1045,8 @@ static int mf_launch(const DotArgs & a, hipStream_t s) {
     if (mf_plan_kh<NC>(a.rows, nsb, G, nrb, D, kh, smb, true, &xc)) return FLH_ERR_UNSUPPORTED;
     if (xc) return mf_launch_d<NC, 2, false, true>(a, nrb, G, smb, s);
     if (kh) return mf_launch_d<NC, 2, true>(a, nrb, G, smb, s);
+    if (D == 2 && mf_own(nsb, nrb))
+        return mf_launch_d<NC, 2, false, false, true>(a, nrb, G, mf_smem_bytes<NC, false, false, true>(nrb, nsb, 2), s);
     return D == 2 ? mf_launch_d<NC, 2, false>(a, nrb, G, smb, s) : mf_launch_d<NC, 3, false>(a, nrb, G, smb, s);
 }
 
@@ -942,11 +1059,12 @@ uint32_t mfma_min_cols(uint32_t cols) {
 
 uint32_t mfma_min_cols(uint32_t cols);
 
-template <int NC, int D, bool KH>
+template <int NC, int D, bool KH, bool OWN = false>
 static int mf_moe_launch_d(const MoeArgs & a, uint32_t nrb, uint32_t gx, size_t smb, hipStream_t s) {
     if (moe_rows(a) == 0) return FLH_OK;
-    (void)hipFuncSetAttribute((const void *)k_moe_mfma<NC, D, KH>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smb);
-    hipLaunchKernelGGL((k_moe_mfma<NC, D, KH>), dim3(gx, moe_rows(a)), dim3(MF_WAVES * 64), smb, s, a,
+    (void)hipFuncSetAttribute((const void *)k_moe_mfma<NC, D, KH, OWN>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)smb);
+    hipLaunchKernelGGL((k_moe_mfma<NC, D, KH, OWN>), dim3(gx, moe_rows(a)), dim3(MF_WAVES * 64), smb, s, a,
                        nrb | (mf_pro() << 16));
     return hip_check(hipGetLastError(), "k_moe_mfma launch");
 }
@@ -965,6 +1083,8 @@ static int mf_moe_launch(const MoeArgs & a, hipStream_t s, bool allow_kh) {
     size_t smb;
     if (mf_plan_kh<NC>(a.rows, nsb, gx, nrb, D, kh, smb, allow_kh)) return FLH_ERR_UNSUPPORTED;
     if (kh) return mf_moe_launch_d<NC, 2, true>(a, nrb, gx, smb, s);
+    if (D == 2 && mf_own(nsb, nrb))
+        return mf_moe_launch_d<NC, 2, false, true>(a, nrb, gx, mf_smem_bytes<NC, false, false, true>(nrb, nsb, 2), s);
     return D == 2 ? mf_moe_launch_d<NC, 2, false>(a, nrb, gx, smb, s) : mf_moe_launch_d<NC, 3, false>(a, nrb, gx, smb, s);
 }
 

@@ -88,6 +88,7 @@ struct Tune {
     uint32_t mf_D = 0, mf_nrb = 0;      // FLH_MFMA_TUNE = "D,nrb[,kh]" (0: planned)
     int mf_kh = -1;                     //   kh: 1 force K halves, 0 never, -1 planned
     bool mf_xc = true;                  // FLH_MFMA_XC=0: no activations-in-chunk mode
+    bool mf_own = true;                 // FLH_MFMA_OWN=0: parked terms and a fold pass, not register sums
     uint32_t mf_min_cols = 0;           // FLH_MFMA_MIN_COLS (0: 2 above 4096 columns, else 3)
     bool no_mfma = false;               // FLH_NO_MFMA=1: never the matrix-core kernels
     // superblock-per-lane single-column kernel, FLH_SBL = "on,waves,wgs_per_cu,max_wgs,pre"

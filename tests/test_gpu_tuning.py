@@ -49,7 +49,38 @@ CASES = [
     ("FLH_KQ_TUNE", "1,0,1", Q6_K, 257, 2048, 2, 4, False),
     ("FLH_MFMA_PRO", "1", Q4_K, 1000, 4096, 4, 0, False),            # matrix cores: 1-chunk prologue
     ("FLH_MFMA_MIN_COLS", "2", Q4_K, 1000, 4096, 2, 0, False),       # matrix cores at 2 columns
+    ("FLH_MFMA_OWN", "0", Q4_K, 14336, 4096, 8, 0, False),          # matrix cores: parked terms + fold
+    ("FLH_MFMA_OWN", "0", Q4_K, 1000, 4096, 3, 0, False),
+    ("FLH_MFMA_OWN", "0", Q4_K, 777, 2816, 16, 0, False),
 ]
+
+
+@pytest.mark.parametrize("ntok", [3, 8])
+def test_moe_register_sums_keep_bits(flh, gpu, ntok):
+    """The grouped matrix-core expert dots with register accumulators (the
+    default) and with parked terms and a fold pass (FLH_MFMA_OWN=0) give the
+    same bits for every (token, slot) pair."""
+    say("tuning moe own", ntok)
+    E, K, rows, cols = 6, 2, 1500, 4096
+    rng = np.random.default_rng(ntok)
+    from oracle import row_bytes
+    rb = rows * row_bytes(Q4_K, cols)
+    w = sane_rows(Q4_K, E * rows, cols, rng)
+    xs = activations(ntok, cols, rng, outliers=True)
+    st = col_stride_floats(cols)
+    ids = np.array([rng.permutation(E)[:K] for _ in range(ntok)], dtype=np.uint32).reshape(-1)
+    dx, _ = dev_cols(flh, gpu, xs, st)
+    flh.act_q8(dx, cols, gpu, nx=ntok, xstride=st)
+    dw = flh.DeviceBuffer.from_array(w, gpu)
+    did = flh.DeviceBuffer.from_array(ids, gpu)
+    out = []
+    for env in ({}, {"FLH_MFMA_OWN": "0"}):
+        dy = flh.DeviceBuffer(ntok * K * rows * 4)
+        dy.zero(gpu)
+        with tuned(flh, **env):
+            flh.moe_dot(Q4_K, dw, rb, rows, cols, did, ntok, K, E, dx, st, False, dy, rows, gpu)
+        out.append(dy.download(np.float32, ntok * K * rows, gpu))
+    assert np.array_equal(bits(out[0]), bits(out[1]))
 
 
 @pytest.mark.parametrize("name,value,fmt,rows,cols,nx,mis,fused", CASES)
