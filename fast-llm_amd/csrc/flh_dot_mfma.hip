@@ -975,7 +975,7 @@ size_t lds_limit();
 // fits.
 template <int NC>
 static int mf_plan_kh(uint32_t rows, uint32_t nsb, uint32_t G, uint32_t & nrb, int & D, bool & kh, size_t & smb,
-                      bool allow_kh = true, bool * xc = nullptr) {
+                      bool allow_kh = true, bool * xc = nullptr, bool * own = nullptr) {
     const size_t lim = lds_limit() - 4096;                    // the MoE kernel's static tables
     const uint32_t rpw = (rows + G - 1) / G;
     // a batch's old y values are one 64-float DMA per wave: nrb * NC <= 512
@@ -1005,6 +1005,18 @@ static int mf_plan_kh(uint32_t rows, uint32_t nsb, uint32_t G, uint32_t & nrb, i
         }
     }
     if (kh) D = 2;                                            // the K-halves waits assume it
+    // register accumulators: no parked terms, so the batch can stay large
+    if (own) *own = false;
+    if (own && !kh && D == 2) {
+        uint32_t n = nrb;
+        while (mf_smem_bytes<NC, false, false, true>(n, nsb, 2) > lim && n > 16) n -= 16;
+        if (mf_own(nsb, n) && mf_smem_bytes<NC, false, false, true>(n, nsb, 2) <= lim) {
+            nrb = n;
+            *own = true;
+            smb = mf_smem_bytes<NC, false, false, true>(n, nsb, 2);
+            return FLH_OK;
+        }
+    }
     auto bytes = [&]() { return kh ? mf_smem_bytes<NC, true>(nrb, nsb, D) : mf_smem_bytes<NC, false>(nrb, nsb, D); };
     while (bytes() > lim && nrb > 16) nrb -= 16;
     while (bytes() > lim && D > 2) --D;
@@ -1041,12 +1053,11 @@ static int mf_launch(const DotArgs & a, hipStream_t s) {
     int D;
     bool kh;
     size_t smb;
-    bool xc;
-    if (mf_plan_kh<NC>(a.rows, nsb, G, nrb, D, kh, smb, true, &xc)) return FLH_ERR_UNSUPPORTED;
+    bool xc, own;
+    if (mf_plan_kh<NC>(a.rows, nsb, G, nrb, D, kh, smb, true, &xc, &own)) return FLH_ERR_UNSUPPORTED;
     if (xc) return mf_launch_d<NC, 2, false, true>(a, nrb, G, smb, s);
     if (kh) return mf_launch_d<NC, 2, true>(a, nrb, G, smb, s);
-    if (D == 2 && mf_own(nsb, nrb))
-        return mf_launch_d<NC, 2, false, false, true>(a, nrb, G, mf_smem_bytes<NC, false, false, true>(nrb, nsb, 2), s);
+    if (own) return mf_launch_d<NC, 2, false, false, true>(a, nrb, G, smb, s);
     return D == 2 ? mf_launch_d<NC, 2, false>(a, nrb, G, smb, s) : mf_launch_d<NC, 3, false>(a, nrb, G, smb, s);
 }
 
@@ -1081,10 +1092,10 @@ static int mf_moe_launch(const MoeArgs & a, hipStream_t s, bool allow_kh) {
     int D;
     bool kh;
     size_t smb;
-    if (mf_plan_kh<NC>(a.rows, nsb, gx, nrb, D, kh, smb, allow_kh)) return FLH_ERR_UNSUPPORTED;
+    bool own;
+    if (mf_plan_kh<NC>(a.rows, nsb, gx, nrb, D, kh, smb, allow_kh, nullptr, &own)) return FLH_ERR_UNSUPPORTED;
     if (kh) return mf_moe_launch_d<NC, 2, true>(a, nrb, gx, smb, s);
-    if (D == 2 && mf_own(nsb, nrb))
-        return mf_moe_launch_d<NC, 2, false, true>(a, nrb, gx, mf_smem_bytes<NC, false, false, true>(nrb, nsb, 2), s);
+    if (own) return mf_moe_launch_d<NC, 2, false, true>(a, nrb, gx, smb, s);
     return D == 2 ? mf_moe_launch_d<NC, 2, false>(a, nrb, gx, smb, s) : mf_moe_launch_d<NC, 3, false>(a, nrb, gx, smb, s);
 }
 
