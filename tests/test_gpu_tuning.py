@@ -52,6 +52,9 @@ CASES = [
     ("FLH_MFMA_OWN", "0", Q4_K, 14336, 4096, 8, 0, False),          # matrix cores: parked terms + fold
     ("FLH_MFMA_OWN", "0", Q4_K, 1000, 4096, 3, 0, False),
     ("FLH_MFMA_OWN", "0", Q4_K, 777, 2816, 16, 0, False),
+    ("FLH_MFMA_OWN", "0", Q4_K, 4096, 14336, 4, 0, False),          # one tile per batch: split chains
+    ("FLH_MFMA_OWN", "0", Q4_K, 4096, 14336, 2, 0, False),
+    ("FLH_MFMA_OWN", "0", Q4_K, 3000, 4096, 8, 0, False),
 ]
 
 
