@@ -39,6 +39,26 @@ def test_mfma_multicol_bitwise(flh, orc, gpu, rows, cols, nx):
 
 
 @pytest.mark.parametrize("rows,cols,nx", [
+    (20000, 1024, 16), (7777, 2816, 5), (9000, 1280, 3), (12345, 4096, 4), (8200, 1024, 12), (16000, 3328, 8),
+])
+def test_mfma_register_accumulators_bitwise(flh, orc, gpu, rows, cols, nx):
+    """Shapes on the register-accumulator layout (two or more 16-row tiles per
+    batch): 16 columns at 4 superblocks per row, accumulator classes of unequal
+    length (11, 5, 13 superblocks per row), odd tile counts and partial last
+    tiles; bitwise against the oracle and against the parked-term layout."""
+    say("mfma own", rows, cols, nx)
+    rng = np.random.default_rng(rows + 3 * cols + nx)
+    w = sane_rows(Q4_K, rows, cols, rng)
+    xs = activations(nx, cols, rng, outliers=True)
+    y0 = rng.standard_normal((nx - 1) * (rows + 2) + rows).astype(np.float32)
+    got, want = run_dot(flh, orc, gpu, Q4_K, w, rows, cols, xs, ystride=rows + 2, y0=y0)
+    assert np.array_equal(bits(got), bits(want))
+    with tuned(flh, FLH_MFMA_OWN=0):
+        got2, _ = run_dot(flh, orc, gpu, Q4_K, w, rows, cols, xs, ystride=rows + 2, y0=y0)
+    assert np.array_equal(bits(got2), bits(got))
+
+
+@pytest.mark.parametrize("rows,cols,nx", [
     (4096, 14336, 8), (20000, 2304, 8), (1000, 2560, 5), (333, 2816, 16), (4100, 4096, 3), (40, 16384, 7),
 ])
 def test_mfma_k_halves_bitwise(flh, orc, gpu, rows, cols, nx):
