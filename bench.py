@@ -104,8 +104,9 @@ class Bench:
         self.flh.act_q8(x, cols, self.s, nx=nx, xstride=st)
         return x, st
 
-    def time_graph(self, issue, reps):
-        """Capture issue() `reps` times in one graph; return us per rep."""
+    def time_graph(self, issue, reps, replays=5):
+        """Capture issue() `reps` times in one graph; return us per rep, the
+        median over `replays` timed replays (after one untimed replay)."""
         flh = self.flh
         with flh.Graph.capture(self.s) as g:
             for i in range(reps):
@@ -113,18 +114,17 @@ class Bench:
         g.launch()                      # warm
         self.s.sync()
         e0, e1 = flh.Event(), flh.Event()
-        best = None
-        for _ in range(3):
+        ts = []
+        for _ in range(replays):
             e0.record(self.s)
             g.launch()
             e1.record(self.s)
             self.s.sync()
-            t = e0.elapsed_ms(e1) * 1e3 / reps
-            best = t if best is None else min(best, t)
+            ts.append(e0.elapsed_ms(e1) * 1e3 / reps)
         g.close()
         e0.close()
         e1.close()
-        return best
+        return sorted(ts)[len(ts) // 2]
 
 
 def copies_for(nbytes):
