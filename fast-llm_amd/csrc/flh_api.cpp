@@ -58,7 +58,7 @@ int need_device() { return need_init(); }
 // freeze()-style validation of one dot tile (src/runtime/graph.cpp:84-90)
 static int validate_dot(int fmt, const void * w, uint64_t w_bytes, uint32_t rows, uint32_t cols,
                         const float * x, float * y, uint32_t nx, const uint32_t * id_slot,
-                        uint64_t estride) {
+                        uint64_t estride, uint32_t ystride) {
     if (fmt < FLH_FMT_F32 || fmt > FLH_FMT_IQ3_XXS) return set_error(FLH_ERR_ARG, "unknown weight format");
     if (cols % blk_elems(fmt) != 0)
         return set_error(FLH_ERR_ARG, "STREAM_DOT cols not a multiple of the format block size");
@@ -69,6 +69,17 @@ static int validate_dot(int fmt, const void * w, uint64_t w_bytes, uint32_t rows
     if (rows && (!w || !x || !y)) return set_error(FLH_ERR_ARG, "null weight / activation / output pointer");
     if (((uintptr_t)w & 3) || (estride & 3) || ((uintptr_t)x & 3) || ((uintptr_t)y & 3))
         return set_error(FLH_ERR_ARG, "w, x, y and the expert stride must be 4-byte aligned");
+    // the columns' outputs are computed at once: overlapping ones would race
+    // (the reference's CPU loop would accumulate them in turn)
+    if (nx > 1 && ystride < rows) return set_error(FLH_ERR_ARG, "multi-column outputs overlap: ystride < rows");
+    return FLH_OK;
+}
+
+// Several activation columns quantised at once: each column's fp32 values
+// and appendices (x_alloc_bytes) must not overlap the next column's.
+static int validate_xstride(uint32_t cols, uint32_t nx, uint32_t xstride) {
+    if (nx > 1 && (uint64_t)xstride * 4 < x_alloc_bytes(cols))
+        return set_error(FLH_ERR_ARG, "act_q8: columns overlap: xstride * 4 < flh_x_alloc_bytes(cols)");
     return FLH_OK;
 }
 
@@ -190,7 +201,7 @@ static int validate_table(const flh_task * t, uint32_t n) {
                 if (k.kind == FLH_TASK_STREAM_DOT_IDX && (!k.aux || !k.aux2))
                     return set_error(FLH_ERR_ARG, "STREAM_DOT_IDX without id slot / stride");
                 if (int rc = validate_dot(k.fmt, k.w, k.w_bytes, k.rows, k.cols, (const float *)k.x,
-                                          (float *)k.y, k.nx ? k.nx : 1, slot, k.aux2)) return rc;
+                                          (float *)k.y, k.nx ? k.nx : 1, slot, k.aux2, k.ystride)) return rc;
                 break;
             }
             case FLH_TASK_ACT_Q8:
@@ -376,6 +387,7 @@ int flh_act_q8(float * x, void * y_q81, uint32_t cols, uint32_t nx, uint32_t xst
     if (!x || ((uintptr_t)x & 15) || (nx > 1 && (xstride & 3)))
         return set_error(FLH_ERR_ARG, "act_q8: x must be non-null and 16-byte aligned, xstride a multiple of 4");
     if (y_q81 && ((uintptr_t)y_q81 & 3)) return set_error(FLH_ERR_ARG, "act_q8: y must be 4-byte aligned");
+    if (int rc = validate_xstride(cols, nx, xstride)) return rc;
     return launch_act_q8(x, y_q81, cols, nx, xstride, (hipStream_t)stream);
 }
 
@@ -384,7 +396,7 @@ int flh_stream_dot(int fmt, const void * w, uint64_t w_bytes, uint32_t rows, uin
                    const uint32_t * id_slot, uint64_t estride, int fast, uint32_t i8_mask,
                    uint32_t i8k_mask, void * stream) {
     if (nx == 0) nx = 1;
-    if (int rc = validate_dot(fmt, w, w_bytes, rows, cols, x, y, nx, id_slot, estride)) return rc;
+    if (int rc = validate_dot(fmt, w, w_bytes, rows, cols, x, y, nx, id_slot, estride, ystride)) return rc;
     if (int rc = need_init()) return rc;
     DotArgs a{(const uint8_t *)w, id_slot, estride, x, y, rows, cols, nx, xstride, ystride};
     return dispatch_dot(fmt, a, fast, i8_mask, i8k_mask, (hipStream_t)stream);
@@ -395,9 +407,10 @@ int flh_act_q8_stream_dot(int fmt, const void * w, uint64_t w_bytes, uint32_t ro
                           const uint32_t * id_slot, uint64_t estride, int fast, uint32_t i8_mask,
                           uint32_t i8k_mask, void * stream) {
     if (nx == 0) nx = 1;
-    if (int rc = validate_dot(fmt, w, w_bytes, rows, cols, x, y, nx, id_slot, estride)) return rc;
+    if (int rc = validate_dot(fmt, w, w_bytes, rows, cols, x, y, nx, id_slot, estride, ystride)) return rc;
     if (((uintptr_t)x & 15) || (nx > 1 && (xstride & 3)))
         return set_error(FLH_ERR_ARG, "act_q8: x must be 16-byte aligned, xstride a multiple of 4");
+    if (int rc = validate_xstride(cols, nx, xstride)) return rc;
     if (int rc = need_init()) return rc;
     hipStream_t s = (hipStream_t)stream;
     DotArgs a{(const uint8_t *)w, id_slot, estride, x, y, rows, cols, nx, xstride, ystride};
@@ -433,7 +446,7 @@ static int rmsnorm_dot(int fmt, const DotArgs & a, const NormArgs & nm, int fast
 int flh_rmsnorm_stream_dot(int fmt, const void * w, uint64_t w_bytes, uint32_t rows, uint32_t cols, const float * x,
                            const float * wnorm, float eps, float * xn, float * y, int fast, uint32_t i8_mask,
                            uint32_t i8k_mask, void * stream) {
-    if (int rc = validate_dot(fmt, w, w_bytes, rows, cols, xn, y, 1, nullptr, 0)) return rc;
+    if (int rc = validate_dot(fmt, w, w_bytes, rows, cols, xn, y, 1, nullptr, 0, 0)) return rc;
     if (!x || !wnorm || ((uintptr_t)x & 15) || ((uintptr_t)wnorm & 15) || ((uintptr_t)xn & 15))
         return set_error(FLH_ERR_ARG, "rmsnorm dot: x, wnorm, xn non-null and 16-byte aligned");
     if (cols % 256) return set_error(FLH_ERR_ARG, "rmsnorm dot: cols must be a multiple of 256 (the q8_K appendix)");

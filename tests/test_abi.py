@@ -70,6 +70,12 @@ def test_validation_mirrors_freeze(flh):
     assert rc == flh.ERR_ARG
     rc = L.flh_stream_dot(3, p + 2, 144 * 3, 3, 256, p, p, 1, 0, 0, None, 0, 1, 0, 0, None)
     assert rc == flh.ERR_ARG and b"aligned" in L.flh_last_error()
+    # several columns whose outputs overlap (ystride < rows) would race on the device
+    rc = L.flh_stream_dot(3, p, 144 * 3, 3, 256, p, p, 2, 2048, 2, None, 0, 1, 0, 0, None)
+    assert rc == flh.ERR_ARG and b"overlap" in L.flh_last_error()
+    # several activation columns closer than one column's allocation (fp32 + appendices)
+    rc = L.flh_act_q8_stream_dot(3, p, 144 * 3, 3, 256, p, p, 2, 256, 3, None, 0, 1, 0, 0, None)
+    assert rc == flh.ERR_ARG and b"overlap" in L.flh_last_error()
     # valid arguments but no flh_init -> state error, never a silent no-op
     rc = L.flh_stream_dot(3, p, 144 * 3, 3, 256, p, p, 1, 0, 0, None, 0, 1, 0, 0, None)
     assert rc in (flh.ERR_STATE, flh.OK)
