@@ -188,7 +188,9 @@ int flh_graph_destroy(void * graph_exec);
  * gact_q8, src/runtime/kernels_gpu.h:881-891): for each of nx columns
  * x_p = x + p*xstride (16-B aligned, fl_x_alloc_bytes(cols) bytes each),
  * write the q8_1 appendix at y_q81 + p*xstride floats (NULL = the canonical
- * fl_xq_of(x_p, cols)) and the q8_K appendix at fl_xqk_of(x_p, cols). */
+ * fl_xq_of(x_p, cols)) and the q8_K appendix at fl_xqk_of(x_p, cols).
+ * nx > 1: columns are quantised at once, so xstride * 4 >= fl_x_alloc_bytes
+ * (cols) (FLH_ERR_ARG otherwise). */
 int flh_act_q8(float * x, void * y_q81, uint32_t cols, uint32_t nx,
                uint32_t xstride, void * stream);
 
@@ -198,7 +200,8 @@ int flh_act_q8(float * x, void * y_q81, uint32_t cols, uint32_t nx,
  * p < nx (0 means 1), W = w + (id_slot ? *id_slot * estride : 0) with the
  * id read ON THE DEVICE.  Validation as Graph::freeze
  * (src/runtime/graph.cpp:84-90): cols % block == 0, w_bytes == rows *
- * row_bytes, id_slot => estride != 0.
+ * row_bytes, id_slot => estride != 0; and, since the columns run at
+ * once, nx > 1 => ystride >= rows (overlapping outputs: FLH_ERR_ARG).
  * fast = 0: canonical fp32 dequant-dot (fl_dot_row_any order, bitwise);
  * fast = 1: q8_K path for K formats whose bit is in i8k_mask, else q8_1
  * path for formats in i8_mask, else the "fast" fp32 dequant order
