@@ -67,8 +67,14 @@ static int validate_dot(int fmt, const void * w, uint64_t w_bytes, uint32_t rows
     if (id_slot && estride == 0) return set_error(FLH_ERR_ARG, "STREAM_DOT_IDX without id slot / stride");
     if (nx > FLH_MAX_DOT_COLS) return set_error(FLH_ERR_ARG, "nx exceeds kMaxDotCols (16)");
     if (rows && (!w || !x || !y)) return set_error(FLH_ERR_ARG, "null weight / activation / output pointer");
-    if (((uintptr_t)w & 3) || (estride & 3) || ((uintptr_t)x & 3) || ((uintptr_t)y & 3))
-        return set_error(FLH_ERR_ARG, "w, x, y and the expert stride must be 4-byte aligned");
+    // weights: the 2-byte aligned block formats (Q8_0 34 B, Q5_0 22 B, Q6_K
+    // 210 B, IQ) reach any even address (a row tile of a matrix whose rows are
+    // 2 mod 4 bytes long); every kernel that needs more alignment declines
+    // and the register / fp32 kernels read them through aligned windows
+    const uint64_t wal = fmt == FLH_FMT_F32 || fmt == FLH_FMT_Q4_K ? 3 : 1;
+    if (((uintptr_t)w & wal) || (estride & wal))
+        return set_error(FLH_ERR_ARG, "w and the expert stride must be 4-byte aligned (F32, Q4_K) or 2-byte aligned");
+    if (((uintptr_t)x & 3) || ((uintptr_t)y & 3)) return set_error(FLH_ERR_ARG, "x and y must be 4-byte aligned");
     // the columns' outputs are computed at once: overlapping ones would race
     // (the reference's CPU loop would accumulate them in turn)
     if (nx > 1 && ystride < rows) return set_error(FLH_ERR_ARG, "multi-column outputs overlap: ystride < rows");

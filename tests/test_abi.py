@@ -70,6 +70,12 @@ def test_validation_mirrors_freeze(flh):
     assert rc == flh.ERR_ARG
     rc = L.flh_stream_dot(3, p + 2, 144 * 3, 3, 256, p, p, 1, 0, 0, None, 0, 1, 0, 0, None)
     assert rc == flh.ERR_ARG and b"aligned" in L.flh_last_error()
+    # 2-byte aligned block formats take weights at any even address (row tiles
+    # of rows 2 mod 4 bytes long), never at an odd one
+    rc = L.flh_stream_dot(1, p + 1, 34 * 8 * 3, 3, 256, p, p, 1, 0, 0, None, 0, 1, 0, 0, None)
+    assert rc == flh.ERR_ARG and b"aligned" in L.flh_last_error()
+    rc = L.flh_stream_dot(1, p + 2, 34 * 8 * 3, 3, 256, p, p, 1, 0, 0, None, 0, 1, 0, 0, None)
+    assert rc in (flh.ERR_STATE, flh.OK)
     # several columns whose outputs overlap (ystride < rows) would race on the device
     rc = L.flh_stream_dot(3, p, 144 * 3, 3, 256, p, p, 2, 2048, 2, None, 0, 1, 0, 0, None)
     assert rc == flh.ERR_ARG and b"overlap" in L.flh_last_error()
