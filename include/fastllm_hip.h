@@ -202,6 +202,8 @@ int flh_act_q8(float * x, void * y_q81, uint32_t cols, uint32_t nx,
  * (src/runtime/graph.cpp:84-90): cols % block == 0, w_bytes == rows *
  * row_bytes, id_slot => estride != 0; and, since the columns run at
  * once, nx > 1 => ystride >= rows (overlapping outputs: FLH_ERR_ARG).
+ * Alignment: x, y 4 bytes; w and estride 4 bytes for F32 / Q4_K, 2 bytes for
+ * the 2-byte block formats (a row tile of rows 2 mod 4 bytes long).
  * fast = 0: canonical fp32 dequant-dot (fl_dot_row_any order, bitwise);
  * fast = 1: q8_K path for K formats whose bit is in i8k_mask, else q8_1
  * path for formats in i8_mask, else the "fast" fp32 dequant order
