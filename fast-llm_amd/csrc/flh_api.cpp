@@ -56,6 +56,10 @@ static int need_init() {
 int need_device() { return need_init(); }
 
 // freeze()-style validation of one dot tile (src/runtime/graph.cpp:84-90)
+// Weight address / expert stride alignment: 4 bytes for F32 and Q4_K, 2 for
+// the 2-byte aligned block formats (see validate_dot)
+static uint64_t w_align_mask(int fmt) { return fmt == FLH_FMT_F32 || fmt == FLH_FMT_Q4_K ? 3 : 1; }
+
 static int validate_dot(int fmt, const void * w, uint64_t w_bytes, uint32_t rows, uint32_t cols,
                         const float * x, float * y, uint32_t nx, const uint32_t * id_slot,
                         uint64_t estride, uint32_t ystride) {
@@ -71,7 +75,7 @@ static int validate_dot(int fmt, const void * w, uint64_t w_bytes, uint32_t rows
     // 210 B, IQ) reach any even address (a row tile of a matrix whose rows are
     // 2 mod 4 bytes long); every kernel that needs more alignment declines
     // and the register / fp32 kernels read them through aligned windows
-    const uint64_t wal = fmt == FLH_FMT_F32 || fmt == FLH_FMT_Q4_K ? 3 : 1;
+    const uint64_t wal = w_align_mask(fmt);
     if (((uintptr_t)w & wal) || (estride & wal))
         return set_error(FLH_ERR_ARG, "w and the expert stride must be 4-byte aligned (F32, Q4_K) or 2-byte aligned");
     if (((uintptr_t)x & 3) || ((uintptr_t)y & 3)) return set_error(FLH_ERR_ARG, "x and y must be 4-byte aligned");
@@ -172,15 +176,24 @@ static int dispatch_dot(int fmt, const DotArgs & a, int fast, uint32_t i8_mask, 
 // Grouped expert dots of the 32-weight-block formats (Q8_0, Q5_0, IQ2_XXS,
 // IQ3_XXS x q8_1): the routed superblock-per-lane launch, one workgroup row
 // per (token, slot) pair (the reference runs these per pair too,
-// src/model/decoder.cpp:941-996).
+// src/model/decoder.cpp:941-996).  Shapes its LDS plan cannot hold (rows of
+// more than ~14.5K columns, weights or x not 16-byte aligned) run as the
+// reference's own per-pair STREAM_DOT_IDX tiles, the id read on the device,
+// on the q8_1 int8 path the routed launch computes (same bits); there the
+// ids must be < n_expert, as ROUTER_SEL writes them (the routed launch also
+// skips larger ones).
 static int launch_moe_b32(int fmt, const MoeArgs & a, hipStream_t s) {
     if (a.rows == 0 || a.ntok == 0 || a.top_k == 0) return FLH_OK;
     if (a.ntok * a.top_k > 256) return set_error(FLH_ERR_UNSUPPORTED, "moe: ntok*top_k > 256");
     const int rc = launch_moe_sbl(fmt, a, s);
-    if (rc == FLH_ERR_UNSUPPORTED)
-        return set_error(rc, "moe: this format needs 16-byte aligned weights, x and expert stride, and rows of "
-                             "at most 16128 columns (IQ: a multiple of 2048)");
-    return rc;
+    if (rc != FLH_ERR_UNSUPPORTED) return rc;
+    for (uint32_t p = 0; p < a.ntok * a.top_k; ++p) {
+        const uint32_t xi = a.x_per_slot ? p : p / a.top_k;
+        DotArgs d{a.w, a.ids + p, a.estride, a.x + (size_t)xi * a.xstride, a.y + (size_t)p * a.ystride,
+                  a.rows, a.cols, 1u, 0u, 0u};
+        if (int r = dispatch_dot(fmt, d, 1, 1u << fmt, 0u, s)) return r;
+    }
+    return FLH_OK;
 }
 
 // The decode ops' param blocks are read here, on the host, so they must not
@@ -587,7 +600,8 @@ int flh_moe_dot(int fmt, const void * w, uint64_t estride, uint32_t rows, uint32
         return set_error(FLH_ERR_UNSUPPORTED, "moe_dot: quantized weight formats only");
     if (cols % 256) return set_error(FLH_ERR_ARG, "moe_dot: cols not a multiple of 256");
     if (!w || !ids || !x || !y || n_expert == 0) return set_error(FLH_ERR_ARG, "moe_dot: null argument");
-    if (estride < (uint64_t)rows * flh_row_bytes(fmt, cols) || (estride & 3) || ((uintptr_t)w & 3))
+    if (estride < (uint64_t)rows * flh_row_bytes(fmt, cols) || (estride & w_align_mask(fmt)) ||
+        ((uintptr_t)w & w_align_mask(fmt)))
         return set_error(FLH_ERR_ARG, "moe_dot: expert stride smaller than one expert or misaligned");
     MoeArgs a{(const uint8_t *)w, estride, ids, x, y, rows, cols, ntok, top_k, n_expert, xstride, ystride,
               x_per_slot};
@@ -606,7 +620,8 @@ int flh_router_moe_dot(int fmt, const void * w, uint64_t estride, uint32_t rows,
     if (cols % 256) return set_error(FLH_ERR_ARG, "router_moe_dot: cols not a multiple of 256");
     if (!w || !logits || !ids || !gates || !x || !y || n_expert == 0 || top_k == 0 || top_k > n_expert)
         return set_error(FLH_ERR_ARG, "router_moe_dot: null argument or top_k outside 1..n_expert");
-    if (estride < (uint64_t)rows * flh_row_bytes(fmt, cols) || (estride & 3) || ((uintptr_t)w & 3))
+    if (estride < (uint64_t)rows * flh_row_bytes(fmt, cols) || (estride & w_align_mask(fmt)) ||
+        ((uintptr_t)w & w_align_mask(fmt)))
         return set_error(FLH_ERR_ARG, "router_moe_dot: expert stride smaller than one expert or misaligned");
     if (ntok == 0) return FLH_OK;
     hipStream_t s = (hipStream_t)stream;

@@ -681,9 +681,7 @@ static int launch_moe_t(const MoeArgs & a, hipStream_t s) {
     const uint32_t nsb = a.cols >> 8;
     const uint32_t P = 1u << ceil_log2(nsb), rpi = 64u / P;
     // experts split the chip: aim for ~8 workgroups per CU over all experts
-    const uint32_t per_e = (a.rows + 1) / 1;
     uint32_t nr = (uint32_t)(((uint64_t)a.rows * a.n_expert + num_cus() * 8u - 1) / (num_cus() * 8u));
-    (void)per_e;
     if (nr < 1) nr = 1;
     if (nr > 64u / NX) nr = 64u / NX;
     if (nr > rpi) nr = (nr / rpi) * rpi;

@@ -282,9 +282,12 @@ int flh_dequant(int fmt, const void * w, uint32_t rows, uint32_t cols,
  * xi = tok (x_per_slot = 0) or i (x_per_slot = 1).  Each expert's weights
  * are streamed once for all of its pairs (Q4_K, Q6_K: the q8_K int8 path);
  * Q8_0, Q5_0, IQ2_XXS and IQ3_XXS run the q8_1 int8 path one pair at a time,
- * as the reference's per-pair tiles do (16-byte aligned w, x and estride;
- * cols a multiple of 256, at most 16128; IQ: a multiple of 2048).  Every
- * output is bitwise equal to the per-pair STREAM_DOT_IDX tile. */
+ * as the reference's per-pair tiles do: one routed launch where its plan
+ * holds the shape (16-byte aligned w, x and estride, at most ~14.5K columns;
+ * IQ: a multiple of 2048), else one STREAM_DOT_IDX tile per pair (up to 16384
+ * columns; the ids must then be < n_expert, as ROUTER_SEL writes them).
+ * cols a multiple of 256.  Every output is bitwise equal to the per-pair
+ * STREAM_DOT_IDX tile. */
 int flh_moe_dot(int fmt, const void * w, uint64_t estride, uint32_t rows,
                 uint32_t cols, const uint32_t * ids, uint32_t ntok,
                 uint32_t top_k, uint32_t n_expert, const float * x,
