@@ -25,6 +25,9 @@
 #include "flh_status.h"
 #include <stdio.h>
 #include <stdlib.h>
+#include <atomic>
+#include <mutex>
+#include <unordered_map>
 
 namespace flh {
 
@@ -274,21 +277,48 @@ __global__ __launch_bounds__(256) void k_moe_kstream(MoeArgs a, uint32_t nr) {
 // has landed: the whole ring (layer step 41.7 -> 40.3 us).
 static uint32_t ks_pro(bool fuse) { return tune().ks_pro ? tune().ks_pro : fuse ? 2u : 1u; }
 
-static size_t g_lds_limit = 0;
+static std::atomic<size_t> g_lds_limit{0};
 size_t lds_limit() {
-    if (!g_lds_limit) {
+    size_t l = g_lds_limit.load(std::memory_order_relaxed);
+    if (!l) {
         int dev = 0;
         (void)hipGetDevice(&dev);
         int v = 0;
         if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || v <= 0)
             v = 65536;
-        g_lds_limit = (size_t)v;
+        l = (size_t)v;
+        g_lds_limit.store(l, std::memory_order_relaxed);
     }
-    return g_lds_limit;
+    return l;
+}
+
+// A kernel's static LDS (its __shared__ arrays), from the runtime, cached.
+size_t static_lds(const void * kern) {
+    static std::mutex mu;
+    static std::unordered_map<const void *, size_t> cache;
+    std::lock_guard<std::mutex> lk(mu);
+    auto it = cache.find(kern);
+    if (it != cache.end()) return it->second;
+    hipFuncAttributes fa{};
+    const size_t v = hipFuncGetAttributes(&fa, kern) == hipSuccess ? fa.sharedSizeBytes : 4096;
+    (void)hipGetLastError();
+    cache.emplace(kern, v);
+    return v;
+}
+
+// Before a launch: the dynamic LDS of a plan plus the kernel's static LDS
+// must fit one workgroup's LDS (a dispatch that asks for more is rejected by
+// the device, and the queue with it).  FLH_ERR_UNSUPPORTED (the caller takes
+// another kernel) otherwise.
+int lds_fits(const void * kern, size_t dyn, const char * what) {
+    if (dyn + static_lds(kern) <= lds_limit()) return FLH_OK;
+    return set_error(FLH_ERR_UNSUPPORTED, what);
 }
 
 template <int FMT, int NX, int D, bool FUSE, bool XREG>
 static int ks_launch_x(const DotArgs & a, uint32_t nr, uint32_t grid, size_t smb, hipStream_t s) {
+    if (int rc = lds_fits((const void *)k_dot_kstream<FMT, NX, D, FUSE, XREG>, smb, "k_dot_kstream: LDS over the limit"))
+        return rc;
     if (smb > 65536)
         (void)hipFuncSetAttribute((const void *)k_dot_kstream<FMT, NX, D, FUSE, XREG>,
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)smb);
@@ -354,6 +384,7 @@ static int ks_launch(const DotArgs & a, hipStream_t s) {
             if (ks_plan<FMT>(a.rows, 1, nsb, slots, 2, nr, D, smb, 8) == FLH_OK && D == 2) {
                 const uint32_t grid = a.rows < slots ? a.rows : slots;
                 auto go = [&](auto kern) {
+                    if (int rc = lds_fits((const void *)kern, smb, "k_dot_kstream: LDS over the limit")) return rc;
                     (void)hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smb);
                     hipLaunchKernelGGL(kern, dim3(grid), dim3(512), smb, s, a, nr | (ks_pro(FUSE) << 16), NormArgs{});
                     return hip_check(hipGetLastError(), "k_dot_kstream launch");
@@ -379,6 +410,8 @@ static int ks_launch(const DotArgs & a, hipStream_t s) {
 template <int FMT, int NX, int D, bool XREG>
 static int moe_launch_x(const MoeArgs & a, uint32_t nr, uint32_t gx, size_t smb, hipStream_t s) {
     if (moe_rows(a) == 0) return FLH_OK;
+    if (int rc = lds_fits((const void *)k_moe_kstream<FMT, NX, D, XREG>, smb, "k_moe_kstream: LDS over the limit"))
+        return rc;
     hipLaunchKernelGGL((k_moe_kstream<FMT, NX, D, XREG>), dim3(gx, moe_rows(a)), dim3(256), smb, s, a, nr | (ks_pro(false) << 16));
     return hip_check(hipGetLastError(), "k_moe_kstream launch");
 }
@@ -424,6 +457,7 @@ int launch_norm_dot_kstream(const DotArgs & a, const NormArgs & nm, hipStream_t 
     if (ks_plan<FMT_Q4_K>(a.rows, 1, nsb, slots, 2, nr, D, smb, 8) != FLH_OK || D != 2) return FLH_ERR_UNSUPPORTED;
     const uint32_t grid = a.rows < slots ? a.rows : slots;
     auto go = [&](auto kern) {
+        if (int rc = lds_fits((const void *)kern, smb, "k_dot_kstream: LDS over the limit")) return rc;
         (void)hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smb);
         hipLaunchKernelGGL(kern, dim3(grid), dim3(512), smb, s, a, nr | (ks_pro(true) << 16), nm);
         return hip_check(hipGetLastError(), "k_dot_kstream launch");

@@ -959,6 +959,7 @@ static uint32_t mf_pro() { return tune().mf_pro; }          // 0: the whole ring
 static bool mf_own(uint32_t nsb, uint32_t nrb) { return tune().mf_own && nsb >= 4 && nrb >= 32; }
 template <int NC, int D, bool KH, bool XC = false, bool OWN = false>
 static int mf_launch_d(const DotArgs & a, uint32_t nrb, uint32_t grid, size_t smb, hipStream_t s) {
+    if (int rc = lds_fits((const void *)k_dot_mfma<NC, D, KH, XC, OWN>, smb, "k_dot_mfma: LDS over the limit")) return rc;
     (void)hipFuncSetAttribute((const void *)k_dot_mfma<NC, D, KH, XC, OWN>, hipFuncAttributeMaxDynamicSharedMemorySize,
                               (int)smb);
     hipLaunchKernelGGL((k_dot_mfma<NC, D, KH, XC, OWN>), dim3(grid), dim3(MF_WAVES * 64), smb, s, a,
@@ -1073,6 +1074,7 @@ uint32_t mfma_min_cols(uint32_t cols);
 template <int NC, int D, bool KH, bool OWN = false>
 static int mf_moe_launch_d(const MoeArgs & a, uint32_t nrb, uint32_t gx, size_t smb, hipStream_t s) {
     if (moe_rows(a) == 0) return FLH_OK;
+    if (int rc = lds_fits((const void *)k_moe_mfma<NC, D, KH, OWN>, smb, "k_moe_mfma: LDS over the limit")) return rc;
     (void)hipFuncSetAttribute((const void *)k_moe_mfma<NC, D, KH, OWN>, hipFuncAttributeMaxDynamicSharedMemorySize,
                               (int)smb);
     hipLaunchKernelGGL((k_moe_mfma<NC, D, KH, OWN>), dim3(gx, moe_rows(a)), dim3(MF_WAVES * 64), smb, s, a,

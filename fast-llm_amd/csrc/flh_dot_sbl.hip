@@ -52,6 +52,7 @@
 #include "flh_kstream.h"
 #include "flh_internal.h"
 #include "flh_status.h"
+#include <algorithm>
 #include <type_traits>
 
 namespace flh {
@@ -1407,9 +1408,14 @@ int launch_dot_sbl(int fmt, const DotArgs & a, bool fuse, hipStream_t s, const N
     const uint32_t wdef = fuse || nsb > 16 || (q8 && fmt != FMT_Q8_0) ? 8 : 4;
     uint32_t W = t.sbl_w ? t.sbl_w : wdef;
     const uint32_t pre = t.sbl_pre == 0xFFu ? W : t.sbl_pre ? t.sbl_pre : q8 ? W : W / 2;
-    while (W > 4 && sbl_smem(q8, iq, W, slot, nsb) > lds_limit()) W -= 2;
+    // (NORM: its kernel's static LDS, the norm partials, comes on top; it
+    // runs 8 or 4 waves)
+    const size_t lim = lds_limit() - (norm ? std::max(static_lds((const void *)k_dot_sbl<FMT_Q4_K, true, 8, false, true>),
+                                                      static_lds((const void *)k_dot_sbl<FMT_Q4_K, true, 4, false, true>))
+                                           : 0);
+    while (W > 4 && (sbl_smem(q8, iq, W, slot, nsb) > lim || (norm && W != 8 && W != 4))) W -= 2;
     const size_t smb = sbl_smem(q8, iq, W, slot, nsb);
-    if (smb > lds_limit() || (W != 8 && W != 6 && W != 4)) return FLH_ERR_UNSUPPORTED;
+    if (smb > lim || (W != 8 && W != 6 && W != 4)) return FLH_ERR_UNSUPPORTED;
     if (fuse && (nsb + W - 1) / W > 8) return FLH_ERR_UNSUPPORTED;
     // NORM: the items' fp32 x and norm weights share the second ring stage
     if (norm && ((W != 8 && W != 4) || (nsb + W - 1) / W > 4 || 8 * 1024 > slot)) return FLH_ERR_UNSUPPORTED;
@@ -1419,6 +1425,7 @@ int launch_dot_sbl(int fmt, const DotArgs & a, bool fuse, hipStream_t s, const N
     if (t.sbl_gmax && G > t.sbl_gmax) G = t.sbl_gmax;
     if (G > C) G = C;
     auto go = [&](auto kern) {
+        if (int rc = lds_fits((const void *)kern, smb, "k_dot_sbl: LDS over the limit")) return rc;
         (void)hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smb);
         hipLaunchKernelGGL(kern, dim3(G), dim3(64 * W), smb, s, a, rpc, ni, slot, pre, MoeArgs{},
                            norm ? *norm : NormArgs{});
@@ -1520,6 +1527,7 @@ static int sbl_nx_go(int fmt, const DotArgs & a, hipStream_t s, bool dry) {
     if (t.sbl_gmax && G > t.sbl_gmax) G = t.sbl_gmax;
     if (G > C) G = C;
     auto go = [&](auto kern) {
+        if (int rc = lds_fits((const void *)kern, smb, "k_dot_sbl: LDS over the limit")) return rc;
         (void)hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smb);
         hipLaunchKernelGGL(kern, dim3(G), dim3(64 * W), smb, s, a, rpc, ni, slot, pre, NX, dep);
         return hip_check(hipGetLastError(), "k_dot_sbl_nx launch");
@@ -1586,6 +1594,7 @@ int launch_moe_sbl(int fmt, const MoeArgs & m, hipStream_t s) {
     a.cols = m.cols;
     a.nx = 1;
     auto go = [&](auto kern) {
+        if (int rc = lds_fits((const void *)kern, smb, "k_dot_sbl: LDS over the limit")) return rc;
         (void)hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smb);
         hipLaunchKernelGGL(kern, dim3(gx, pairs), dim3(64 * W), smb, s, a, rpc, ni, slot, pre, m, NormArgs{});
         return hip_check(hipGetLastError(), "k_dot_sbl (moe) launch");

@@ -115,6 +115,10 @@ int launch_dot_sbl_nx(int fmt, const DotArgs & a, hipStream_t s);
 int launch_norm_dot_kstream(const DotArgs & a, const NormArgs & nm, hipStream_t s);
 // largest dynamic LDS of one workgroup on the current device
 size_t lds_limit();
+// a kernel's static LDS, and whether a launch of it with dyn bytes of dynamic
+// LDS fits one workgroup (FLH_ERR_UNSUPPORTED with the message otherwise)
+size_t static_lds(const void * kern);
+int lds_fits(const void * kern, size_t dyn, const char * what);
 // ACT_Q8 fused into the kstream dot: quantises x (fp32) in-kernel, writes both
 // appendices (workgroup 0), then streams; same bytes and results as
 // launch_act_q8 followed by launch_dot_kstream

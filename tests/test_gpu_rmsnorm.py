@@ -89,7 +89,11 @@ def test_rmsnorm_task_pair_fuses(flh, orc, gpu):
 
 @pytest.mark.parametrize("cfg", ["1", "1,4", "1,8,1,5,2"])
 @pytest.mark.parametrize("rows,n", [(5, 256), (9, 1024), (50, 2048), (300, 4096), (6144, 4096), (28672, 4096),
-                                    (77, 8192), (33, 14336)])
+                                    (77, 8192), (33, 14336),
+                                    # 20 superblocks: the 8-wave plan needs exactly all of a
+                                    # workgroup's LDS, with no room for the prologue's static
+                                    # norm partials (the launcher now plans around them)
+                                    (9180, 5120)])
 def test_rmsnorm_stream_dot(flh, orc, gpu, cfg, rows, n):
     """RMSNORM -> ACT_Q8 -> Q4_K dot in one launch (flh_rmsnorm_stream_dot;
     14336 columns take the two-launch path): the normalised column, its
