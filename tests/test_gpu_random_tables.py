@@ -49,11 +49,10 @@ def make_table(seed):
 CASES = list(range(48))
 
 
-@pytest.mark.parametrize("seed", CASES)
-def test_random_task_table_bitwise(flh, orc, gpu, seed):
+def build(flh, gpu, seed, y_zero=False):
+    """The seeded table, its device buffers and host copies (old y zero with
+    y_zero, so that a captured graph can reset it with a fill kernel)."""
     cols, ncol, mats, order = make_table(seed)
-    print("[case] random table", seed, cols, ncol, [(m["fmt"], m["rows"], m["nx"], len(m["tiles"]), m["idx"])
-                                                      for m in mats], flush=True)
     rng = np.random.default_rng(10_000 + seed)
     st = col_stride_floats(cols)
     xs = activations(ncol, cols, rng, outliers=True)
@@ -62,16 +61,15 @@ def test_random_task_table_bitwise(flh, orc, gpu, seed):
         xb[p * st:p * st + cols] = xs[p]
     dx = flh.DeviceBuffer.from_array(xb, gpu)
     T = flh.TaskKind
-    tasks, outs = [], []
+    tasks = []
     for m in mats:
-        rb = row_bytes(m["fmt"], cols)
         nmat = 3 if m["idx"] else 1
         w = sane_rows(m["fmt"], nmat * m["rows"], cols, rng)
         m["w"] = w
         m["dw"] = flh.DeviceBuffer.from_array(w, gpu)
         m["slot"] = flh.DeviceBuffer.from_array(np.array([2], np.uint32), gpu) if m["idx"] else None
         ny = (m["nx"] - 1) * m["rows"] + m["rows"]
-        m["y0"] = rng.standard_normal(ny).astype(np.float32)
+        m["y0"] = np.zeros(ny, np.float32) if y_zero else rng.standard_normal(ny).astype(np.float32)
         m["dy"] = flh.DeviceBuffer.from_array(m["y0"], gpu)
     # ACT_Q8 of each column, then (for the column's first user with nx == 1)
     # that matrix's first tile right behind it
@@ -79,6 +77,7 @@ def test_random_task_table_bitwise(flh, orc, gpu, seed):
     for p in order:
         tasks.append(mk(flh, T.ACT_Q8, x=dx.ptr + 4 * p * st, y=dx.ptr + 4 * p * st + flh.xq_offset(cols),
                         rows=cols // 32, cols=cols))
+
     def tile(m, r0, r1):
         rb = row_bytes(m["fmt"], cols)
         kw = dict(fmt=m["fmt"], x=dx.ptr + 4 * m["p0"] * st, y=m["dy"].ptr + 4 * r0, rows=r1 - r0, cols=cols,
@@ -98,13 +97,55 @@ def test_random_task_table_bitwise(flh, orc, gpu, seed):
             if (id(m), k) not in placed:
                 tasks.append(tile(m, r0, r1))
     tasks.append(mk(flh, T.SIGNAL))
-    flh.exec_tasks(tasks, gpu, i8_mask=I8_ALL)
-    xq = orc.act_q8_cols(xs, st)
-    for m in mats:
+    return dict(cols=cols, st=st, xs=xs, dx=dx, mats=mats, tasks=tasks)
+
+
+def expected(orc, d):
+    cols, st = d["cols"], d["st"]
+    xq = orc.act_q8_cols(d["xs"], st)
+    out = []
+    for m in d["mats"]:
         rb = row_bytes(m["fmt"], cols)
         want = m["y0"].copy()
         off = 2 * m["rows"] * rb if m["idx"] else 0
         orc.stream_dot(m["fmt"], m["w"][off:off + m["rows"] * rb], m["rows"], cols, xq[m["p0"] * st:], want,
                        nx=m["nx"], xstride=st, ystride=m["rows"], i8_mask=I8_ALL, threads=8)
-        got = m["dy"].download(np.float32, want.size, gpu)
+        out.append(want)
+    return out
+
+
+def read(d, gpu):
+    return [m["dy"].download(np.float32, m["y0"].size, gpu) for m in d["mats"]]
+
+
+@pytest.mark.parametrize("seed", CASES)
+def test_random_task_table_bitwise(flh, orc, gpu, seed):
+    d = build(flh, gpu, seed)
+    print("[case] random table", seed, d["cols"], [(m["fmt"], m["rows"], m["nx"], len(m["tiles"]), m["idx"])
+                                                    for m in d["mats"]], flush=True)
+    flh.exec_tasks(d["tasks"], gpu, i8_mask=I8_ALL)
+    for m, got, want in zip(d["mats"], read(d, gpu), expected(orc, d)):
         assert np.array_equal(bits(got), bits(want)), (m["fmt"], m["rows"], m["nx"], m["tiles"], m["idx"])
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_task_table_graph_replays(flh, orc, gpu, seed):
+    """The table and the zeroing of its outputs captured in one HIP graph and
+    replayed four times with eager work in between: every replay gives the
+    oracle's bits (no memset nodes: outputs are cleared by a fill kernel)."""
+    d = build(flh, gpu, 100 + seed, y_zero=True)
+    print("[case] random table graph", seed, d["cols"], len(d["tasks"]), flush=True)
+    want = expected(orc, d)
+    with flh.Graph.capture(gpu) as g:
+        for m in d["mats"]:
+            m["dy"].zero(gpu)
+        flh.exec_tasks(d["tasks"], gpu, i8_mask=I8_ALL)
+    for rep in range(4):
+        g.launch()
+        gpu.sync()
+        for m, got, w in zip(d["mats"], read(d, gpu), want):
+            assert np.array_equal(bits(got), bits(w)), (rep, m["fmt"], m["rows"], m["nx"], m["idx"])
+        for m in d["mats"]:                      # eager work between replays
+            m["dy"].zero(gpu)
+        gpu.sync()
+    g.close()
