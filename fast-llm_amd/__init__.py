@@ -624,7 +624,7 @@ class Gguf:
         return list(self._tensors)
 
     def find(self, name: str) -> GgufTensor | None:
-        i = lib().flh_gguf_find(self.handle, name.encode())
+        i = lib().flh_gguf_find(self.handle, name.encode("utf-8", "surrogateescape"))
         return None if i < 0 else self._tensors[i]
 
     def data(self, t: GgufTensor) -> np.ndarray:
@@ -637,27 +637,27 @@ class Gguf:
         return lib().flh_gguf_n_shards(self.handle)
 
     def has(self, key: str) -> bool:
-        return bool(lib().flh_gguf_has(self.handle, key.encode()))
+        return bool(lib().flh_gguf_has(self.handle, key.encode("utf-8", "surrogateescape")))
 
     def kv_i(self, key: str, dflt: int) -> int:
-        return lib().flh_gguf_kv_i(self.handle, key.encode(), int(dflt))
+        return lib().flh_gguf_kv_i(self.handle, key.encode("utf-8", "surrogateescape"), int(dflt))
 
     def kv_f(self, key: str, dflt: float) -> float:
-        return lib().flh_gguf_kv_f(self.handle, key.encode(), float(dflt))
+        return lib().flh_gguf_kv_f(self.handle, key.encode("utf-8", "surrogateescape"), float(dflt))
 
     def kv_s(self, key: str, dflt: str = "") -> str:
         n = C.c_size_t()
-        p = lib().flh_gguf_kv_s(self.handle, key.encode(), dflt.encode(), C.byref(n))
+        p = lib().flh_gguf_kv_s(self.handle, key.encode("utf-8", "surrogateescape"), dflt.encode(), C.byref(n))
         return C.string_at(p, n.value).decode("utf-8", "surrogateescape")
 
     def kv_sarr(self, key: str) -> list | None:
         L = lib()
-        n = L.flh_gguf_kv_sarr_len(self.handle, key.encode())
+        n = L.flh_gguf_kv_sarr_len(self.handle, key.encode("utf-8", "surrogateescape"))
         if n < 0:
             return None
         out, ln = [], C.c_size_t()
         for i in range(n):
-            p = L.flh_gguf_kv_sarr_at(self.handle, key.encode(), i, C.byref(ln))
+            p = L.flh_gguf_kv_sarr_at(self.handle, key.encode("utf-8", "surrogateescape"), i, C.byref(ln))
             out.append(C.string_at(p, ln.value).decode("utf-8", "surrogateescape"))
         return out
 
@@ -672,7 +672,7 @@ class Gguf:
 
     def weight(self, name: str) -> WeightInfo:
         w = WeightInfo()
-        check(lib().flh_gguf_weight(self.handle, name.encode(), C.byref(w)))
+        check(lib().flh_gguf_weight(self.handle, name.encode("utf-8", "surrogateescape"), C.byref(w)))
         return w
 
     def upload(self, t: GgufTensor, dst, stream: Stream, dst_bytes: int | None = None) -> None:

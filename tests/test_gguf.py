@@ -201,3 +201,75 @@ def test_impossible_sizes_are_rejected(flh, tmp_path, dims, why):
     with pytest.raises(flh.FlhError) as e:
         flh.Gguf(str(p))
     assert e.value.code == flh.ERR_FORMAT, why
+
+
+def test_mutated_files_never_crash(flh, tmp_path):
+    """Seeded byte mutations of every fixture (bytes flipped, 4- and 8-byte
+    fields overwritten with boundary values, bytes cut or inserted in the
+    header region): each file either opens, and every tensor info, lookup and
+    metadata getter then works, or is rejected with an error code; the
+    walk runs in a child process so that a crash fails the test instead of
+    ending the session."""
+    import random
+    import struct
+    import subprocess
+    import sys
+    rnd = random.Random(2026)
+    blobs = [open(os.path.join(FIX, f), "rb").read() for f in sorted(os.listdir(FIX)) if f.endswith(".gguf")]
+    blobs = [b for b in blobs if len(b) > 24]
+    vals = [0, 1, 0x7F, 0x80, 0xFF, 0x7FFFFFFF, 0x80000000, 0xFFFFFFFF, 1 << 32, 1 << 40, (1 << 64) - 1]
+    paths = []
+    for i in range(400):
+        b = bytearray(rnd.choice(blobs))
+        for _ in range(rnd.randint(1, 6)):
+            hdr = min(len(b), 4096)
+            if hdr == 0:
+                break
+            pos, r = rnd.randrange(hdr), rnd.random()
+            if r < 0.4:
+                b[pos] = rnd.randrange(256)
+            elif r < 0.7 and pos + 8 <= len(b):
+                b[pos:pos + 8] = struct.pack("<Q", rnd.choice(vals))
+            elif r < 0.85 and pos + 4 <= len(b):
+                b[pos:pos + 4] = struct.pack("<I", rnd.choice(vals) & 0xFFFFFFFF)
+            elif r < 0.93:
+                del b[pos:pos + rnd.randint(1, 16)]
+            else:
+                b[pos:pos] = bytes(rnd.randrange(256) for _ in range(rnd.randint(1, 16)))
+        p = tmp_path / f"m{i}.gguf"
+        p.write_bytes(bytes(b))
+        paths.append(str(p))
+    code = r'''
+import sys
+sys.path.insert(0, sys.argv[1])
+import importlib
+flh = importlib.import_module("fast-llm_amd")
+n = 0
+for p in sys.argv[2:]:
+    try:
+        g = flh.Gguf(p)
+    except flh.FlhError:
+        continue
+    n += 1
+    with g:
+        g.alignment()
+        g.n_shards()
+        for t in g.tensors():
+            g.find(t.name)
+            g.data(t)
+            try:
+                g.weight(t.name)
+            except flh.FlhError:
+                pass
+        for k in ("general.architecture", "tokenizer.ggml.tokens", "general.alignment", "split.count"):
+            g.has(k)
+            g.kv_i(k, 0)
+            g.kv_f(k, 0.0)
+            g.kv_s(k, "")
+            g.kv_sarr(k)
+print("opened", n)
+'''
+    root = os.path.dirname(HERE)
+    r = subprocess.run([sys.executable, "-c", code, root] + paths, capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr[-2000:]
+    assert r.stdout.startswith("opened")
