@@ -504,7 +504,7 @@ int flh_exec_tasks(const flh_task * t, uint32_t n, int fast, uint32_t i8_mask, u
                         (q.nx ? q.nx : 1u) != a.nx || q.xstride != k.xstride || q.ystride != k.ystride ||
                         q.aux != k.aux || q.aux2 != k.aux2 ||
                         (const uint8_t *)q.w != a.w + (uint64_t)a.rows * flh_row_bytes(k.fmt, k.cols) ||
-                        (float *)q.y != a.y + a.rows)
+                        (float *)q.y != a.y + a.rows || (a.nx > 1 && a.rows + q.rows > k.ystride))
                         break;
                     a.rows += q.rows;
                     ++i;
