@@ -312,8 +312,11 @@ int flh_arena_alloc(flh_arena * a, size_t bytes, size_t align, void ** out) {
     if (!a || !out) return set_error(FLH_ERR_ARG, "null arena / out");
     if (align < 16) align = 16;
     if (align & (align - 1)) return set_error(FLH_ERR_ARG, "alignment must be a power of two");
-    const size_t off = (a->used + align - 1) & ~(align - 1);
-    if (off + bytes > a->cap) return set_error(FLH_ERR_NOMEM, "arena exhausted");
+    // aligned as an address (the base is only as aligned as hipMalloc makes it)
+    const uintptr_t base = (uintptr_t)a->base, at = base + a->used;
+    if (at > UINTPTR_MAX - (align - 1)) return set_error(FLH_ERR_NOMEM, "arena exhausted");
+    const size_t off = (size_t)(((at + align - 1) & ~(uintptr_t)(align - 1)) - base);
+    if (off > a->cap || bytes > a->cap - off) return set_error(FLH_ERR_NOMEM, "arena exhausted");
     a->used = off + bytes;
     *out = a->base + off;
     return FLH_OK;
@@ -356,6 +359,7 @@ int flh_zero(void * dst, size_t n, void * stream) { return launch_zero(dst, n, (
 // --------------------------------------------------------------- streams --
 int flh_stream_create(void ** out) {
     if (int rc = need_init()) return rc;
+    if (!out) return set_error(FLH_ERR_ARG, "null out");
     hipStream_t s;
     if (int rc = hip_check(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreate")) return rc;
     *out = (void *)s;
@@ -364,6 +368,7 @@ int flh_stream_create(void ** out) {
 int flh_stream_sync(void * s) { return hip_check(hipStreamSynchronize((hipStream_t)s), "hipStreamSynchronize"); }
 int flh_stream_destroy(void * s) { return s ? hip_check(hipStreamDestroy((hipStream_t)s), "hipStreamDestroy") : FLH_OK; }
 int flh_event_create(void ** out) {
+    if (!out) return set_error(FLH_ERR_ARG, "null out");
     hipEvent_t e;
     if (int rc = hip_check(hipEventCreate(&e), "hipEventCreate")) return rc;
     *out = (void *)e;
@@ -371,6 +376,7 @@ int flh_event_create(void ** out) {
 }
 int flh_event_record(void * e, void * s) { return hip_check(hipEventRecord((hipEvent_t)e, (hipStream_t)s), "hipEventRecord"); }
 int flh_event_elapsed_ms(void * a, void * b, float * ms) {
+    if (!ms) return set_error(FLH_ERR_ARG, "null ms");
     if (int rc = hip_check(hipEventSynchronize((hipEvent_t)b), "hipEventSynchronize")) return rc;
     return hip_check(hipEventElapsedTime(ms, (hipEvent_t)a, (hipEvent_t)b), "hipEventElapsedTime");
 }
@@ -384,8 +390,13 @@ int flh_graph_capture_begin(void * stream) {
 }
 int flh_graph_capture_end(void * stream, void ** graph_exec) {
     hipGraph_t g = nullptr;
+    // (with a null graph_exec the capture still ends, so the stream is usable)
     if (int rc = hip_check(hipStreamEndCapture((hipStream_t)stream, &g), "hipStreamEndCapture")) return rc;
     hipGraphExec_t ge = nullptr;
+    if (!graph_exec) {
+        (void)hipGraphDestroy(g);
+        return set_error(FLH_ERR_ARG, "null graph_exec");
+    }
     const int rc = hip_check(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0), "hipGraphInstantiate");
     (void)hipGraphDestroy(g);
     if (rc) return rc;

@@ -198,3 +198,32 @@ def test_masks_same_bits_every_entry_point(flh, orc, gpu):
     assert np.array_equal(bits(dy.download(np.float32, 40, gpu)), bits(want[1]))
 
 
+
+
+def test_arena_alignment_and_exhaustion(flh, gpu):
+    """flh_arena_alloc (Arena::alloc, src/runtime/arena.cpp:54-74): every
+    pointer is aligned as an address to the requested power of two, blocks
+    never overlap, and a request past the end (or one whose size would wrap)
+    is FLH_ERR_NOMEM, leaving the arena usable."""
+    a = flh.Arena(1 << 20)
+    try:
+        got = []
+        for i, (n, al) in enumerate([(1, 16), (100, 4096), (3, 64), (5000, 65536), (7, 256)]):
+            p = a.alloc(n, al)
+            assert p % al == 0, (n, al)
+            got.append((p, n))
+        got.sort()
+        for (p0, n0), (p1, _) in zip(got, got[1:]):
+            assert p0 + n0 <= p1
+        used = a.used
+        for n in (1 << 21, (1 << 64) - 1):
+            with pytest.raises(flh.FlhError) as e:
+                a.alloc(n, 16)
+            assert e.value.code == flh.ERR_NOMEM
+        assert a.used == used
+        with pytest.raises(flh.FlhError) as e:
+            a.alloc(16, 48)
+        assert e.value.code == flh.ERR_ARG
+        assert a.alloc(16, 16) % 16 == 0
+    finally:
+        a.close()
