@@ -7,8 +7,9 @@
 //    correctness mode, not a throughput path.
 //  * fast fp32 (fast = 1, format not routed to an int8 path): the
 //    reference's fixed 16-lane order (src/runtime/kernels.h:11-19):
-//    dot_row_fast / dot_row_fast_q8_0 / dot_row_fast_dequant, again one
-//    thread per (row, column), bitwise.
+//    dot_row_fast / dot_row_fast_q8_0 / dot_row_fast_dequant, bitwise; Q4_K
+//    and Q6_K (the reference GPU masks' Q6_K route) on one wave per row
+//    (k_dot_fastk), the other formats one thread per (row, column).
 //  * ROUTER_SEL / SILU_MUL / WMERGE / MERGE: the reference's single-thread
 //    canonical ops (src/runtime/decode_params.h:234-295,
 //    runtime_internal.h:274-281), one thread per token / element.  expf is
@@ -289,6 +290,88 @@ int launch_dot_i8_k(int fmt, const DotArgs & a, hipStream_t s) {
     return hip_check(hipGetLastError(), "k_dot_q81k launch");
 }
 
+// Fast fp32 order of the K formats (dot_row_fast_dequant: dequant_chunk of
+// each 256-element chunk, dot_row_fast's 16 partial sums and tree, chunk
+// sums added in order; src/runtime/kernels.h:59-104,162-254) on one wave per
+// row and all of its columns: a chunk on 16 lanes, lane j owning elements
+// j + 16 k (k = 0..15, so that its partial sum is the reference's L[j]),
+// four chunks per pass; the value of each element is computed as
+// dequant_chunk does (Q4_K: (d sc) q - (dmin m); Q6_K: (d sc) (q - 32)), and
+// every product and sum rounds on its own.  Bitwise equal to fast_dot.
+template <int FMT>
+__global__ __launch_bounds__(256) void k_dot_fastk(DotArgs a) {
+    static_assert(FMT == FMT_Q4_K || FMT == FMT_Q6_K, "K formats");
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t r = blockIdx.x * 4 + wave;
+    if (r >= a.rows) return;                                      // wave-uniform
+    const uint32_t j = lane & 15, cq = lane >> 4;
+    constexpr uint32_t BB = FMT == FMT_Q4_K ? 144 : 210;
+    const uint32_t nsb = a.cols >> 8, nx = a.nx;
+    const uint8_t * wr = a.w + (a.id_slot ? (size_t)(*a.id_slot) * a.estride : 0) + (size_t)r * nsb * BB;
+    float acc[16];
+#pragma unroll
+    for (int p = 0; p < 16; ++p) acc[p] = 0.f;
+    for (uint32_t c0 = 0; c0 < nsb; c0 += 4) {
+        const uint32_t c = c0 + cq;
+        const bool act = c < nsb;
+        float v[16];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) v[k] = 0.f;
+        if (act) {
+            const uint8_t * b = wr + (size_t)c * BB;
+            if constexpr (FMT == FMT_Q6_K) {
+                const float d = h2f(ld16u(b + 208));
+#pragma unroll
+                for (int k = 0; k < 16; ++k) {
+                    const uint32_t g = (k >> 1) & 3, l = 16 * (k & 1) + j;
+                    const uint8_t lb = b[64 * (k >> 3) + l + 32 * (g & 1)];
+                    const int q6 = ((g < 2) ? (lb & 0xF) : (lb >> 4)) | (((b[128 + 32 * (k >> 3) + l] >> (2 * g)) & 3) << 4);
+                    v[k] = d * (float)(int8_t)b[192 + k] * (float)(q6 - 32);
+                }
+            } else {
+                const float d = h2f(ld16u(b)), dmin = h2f(ld16u(b + 2));
+                const uint8_t * sp = b + 4;
+#pragma unroll
+                for (int k = 0; k < 16; ++k) {
+                    const int g = k >> 1;
+                    uint32_t sc, mn;
+                    if (g < 4) { sc = sp[g] & 63; mn = sp[g + 4] & 63; }
+                    else { sc = (sp[g + 4] & 0xF) | ((sp[g - 4] >> 6) << 4); mn = (sp[g + 4] >> 4) | ((sp[g] >> 6) << 4); }
+                    const uint8_t qb = b[16 + 32 * (k >> 2) + 16 * (k & 1) + j];
+                    const uint32_t nib = (k & 2) ? (qb >> 4) : (qb & 0xF);
+                    const float dd = d * (float)sc, mm = dmin * (float)mn;
+                    v[k] = dd * (float)nib - mm;
+                }
+            }
+        }
+#pragma unroll
+        for (int p = 0; p < 16; ++p) {
+            if ((uint32_t)p >= nx) continue;                      // uniform
+            const float * x = a.x + (size_t)p * a.xstride + 256 * (size_t)(act ? c : 0) + j;
+            float L = 0.f;
+#pragma unroll
+            for (int k = 0; k < 16; ++k) L = L + v[k] * (act ? x[16 * k] : 0.f);
+            // tree16 on the 16 lanes of the chunk: lane 0 ends with
+            // ((L0 + L4) + (L8 + L12)) + ... as dot_row_fast's
+            const float u = L + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(L), 0x104, 0xF, 0xF, false));
+            const float t = u + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(u), 0x108, 0xF, 0xF, false));
+            const float h2 = t + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(t), 0x101, 0xF, 0xF, false));
+            const float head = h2 + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(h2), 0x102, 0xF, 0xF, false));
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                if (c0 + q < nsb) acc[p] = acc[p] + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(head), 16 * q));
+        }
+    }
+    if (lane == 0) {
+#pragma unroll
+        for (int p = 0; p < 16; ++p) {
+            if ((uint32_t)p >= nx) continue;
+            float * y = a.y + (size_t)p * a.ystride + r;
+            *y = *y + acc[p];
+        }
+    }
+}
+
 template <bool FAST>
 __global__ void k_dot_f32(int fmt, DotArgs a) {
     const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -311,6 +394,12 @@ static int launch_f32(bool fast, int fmt, const DotArgs & a, hipStream_t s) {
         return set_error(FLH_ERR_UNSUPPORTED, "fp32 dot: format not supported");
     const uint64_t n = (uint64_t)a.rows * a.nx;
     if (n == 0) return FLH_OK;
+    if (fast && (fmt == FMT_Q4_K || fmt == FMT_Q6_K) && a.cols % 256 == 0 && a.nx <= 16) {
+        const dim3 gw((a.rows + 3) / 4);
+        if (fmt == FMT_Q4_K) hipLaunchKernelGGL(k_dot_fastk<FMT_Q4_K>, gw, dim3(256), 0, s, a);
+        else hipLaunchKernelGGL(k_dot_fastk<FMT_Q6_K>, gw, dim3(256), 0, s, a);
+        return hip_check(hipGetLastError(), "k_dot_fastk launch");
+    }
     const dim3 g((uint32_t)((n + 63) / 64));
     if (fast) hipLaunchKernelGGL(k_dot_f32<true>, g, dim3(64), 0, s, fmt, a);
     else      hipLaunchKernelGGL(k_dot_f32<false>, g, dim3(64), 0, s, fmt, a);
