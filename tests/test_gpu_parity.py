@@ -262,6 +262,22 @@ def test_fp32_modes_bitwise(flh, orc, gpu, mode, fmt):
     assert np.array_equal(bits(got), bits(want))
 
 
+@pytest.mark.parametrize("fmt", [Q4_K, Q6_K])
+@pytest.mark.parametrize("rows,cols,nx", [(1, 256, 1), (5, 768, 16), (301, 2816, 3), (64, 16384, 2),
+                                          (1027, 4096, 7), (3, 1280, 1)])
+def test_fast_fp32_k_formats_wave_per_row(flh, orc, gpu, fmt, rows, cols, nx):
+    """The fast fp32 order of the K formats on one wave per row (four chunks
+    per pass, partial last pass, 1-16 columns, a row of one superblock and of
+    64): bitwise against the oracle's dot_row_fast_dequant order, with old y."""
+    say("fast fp32 k", fmt, rows, cols, nx)
+    rng = np.random.default_rng(fmt + 3 * rows + cols + nx)
+    w = sane_rows(fmt, rows, cols, rng)
+    xs = activations(nx, cols, rng, outliers=True)
+    y0 = rng.standard_normal((nx - 1) * (rows + 1) + rows).astype(np.float32)
+    got, want = run_dot(flh, orc, gpu, fmt, w, rows, cols, xs, mode="f32fast", y0=y0, ystride=rows + 1)
+    assert np.array_equal(bits(got), bits(want))
+
+
 # ----------------------------------------------------- BASELINE shapes --
 @pytest.mark.parametrize("fmt,rows,cols", [
     (Q8_0, 4096, 4096),
