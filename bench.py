@@ -290,6 +290,10 @@ def main():
             us = B.time_graph(lambda i: flh.stream_dot(Q6_K, ws[i % len(ws)], r, c, x, y, s),
                               8 if r > 100000 else REPS)
             op_entry(f"q6_K_{name}_{r}x{c}", us, nb)
+            # the reference's GPU masks: Q6_K on the fast fp32 order
+            us = B.time_graph(lambda i: flh.stream_dot(Q6_K, ws[i % len(ws)], r, c, x, y, s, i8_mask=0, i8k_mask=0),
+                              4 if r > 100000 else 16)
+            op_entry(f"q6_K_{name}_{r}x{c}_fast_f32", us, nb, {"route": "fast fp32 order (GPU default masks)"})
             cpu_in[f"q6_K_{name}_{r}x{c}"] = host_case(flh, s, Q6_K, ws[0], r, c, x, st, 1)
             del ws
         # Q8_0
@@ -430,6 +434,8 @@ PROFILE_OPS["verify8"] = PROFILE_OPS["verify8_14336x4096"]
 for _f, _name in ((Q8_0, "q8_0"), (Q5_0, "q5_0"), (IQ2_XXS, "iq2_xxs"), (IQ3_XXS, "iq3_xxs")):
     for _n in (2, 4, 8):
         PROFILE_OPS[f"{_name}_verify{_n}"] = (_f, 14336, 4096, _n, "dot")
+PROFILE_OPS["q6k_vocab_f32fast"] = (Q6_K, 128256, 4096, 1, "dot_f32fast")
+PROFILE_OPS["q6k_down_f32fast"] = (Q6_K, 4096, 14336, 1, "dot_f32fast")
 PROFILE_OPS["norm_qkv"] = (Q4_K, 6144, 4096, 1, "norm")
 PROFILE_OPS["norm_gate_up"] = (Q4_K, 28672, 4096, 1, "norm")
 
@@ -483,6 +489,8 @@ def profile_run(flh, B, s, staging, which="gate_up", launches=64, calibrate=True
             flh.rmsnorm_stream_dot(fmt, ws[i % len(ws)], r, c, x, wn, 1e-5, xn, y, s)
         elif kind == "fused":
             flh.act_q8_stream_dot(fmt, ws[i % len(ws)], r, c, x, y, s)
+        elif kind == "dot_f32fast":         # the fast fp32 order (no int8 route)
+            flh.stream_dot(fmt, ws[i % len(ws)], r, c, x, y, s, nx=nx, xstride=st, ystride=r, i8_mask=0, i8k_mask=0)
         else:
             flh.stream_dot(fmt, ws[i % len(ws)], r, c, x, y, s, nx=nx, xstride=st, ystride=r, i8_mask=m8)
     s.sync()

@@ -18,6 +18,10 @@
 #include "flh_common.h"
 #include "flh_internal.h"
 #include "flh_status.h"
+#include "flh_kstream.h"
+
+#include <algorithm>
+#include <utility>
 
 namespace flh {
 
@@ -298,59 +302,177 @@ int launch_dot_i8_k(int fmt, const DotArgs & a, hipStream_t s) {
 // four chunks per pass; the value of each element is computed as
 // dequant_chunk does (Q4_K: (d sc) q - (dmin m); Q6_K: (d sc) (q - 32)), and
 // every product and sum rounds on its own.  Bitwise equal to fast_dot.
-template <int FMT>
-__global__ __launch_bounds__(256) void k_dot_fastk(DotArgs a) {
+//
+// Memory plan: the four superblocks of a pass arrive as one 16-byte load per
+// lane (the aligned 16-byte segments that cover them; a segment holding one
+// byte of the row lies in that byte's page), issued two passes ahead into two
+// registers used in turn (a register copy would wait for its load), and go
+// through a 1 KiB wave-private LDS buffer from which each lane picks its
+// bytes.  The per-subblock factors d sc (and dmin m) are computed once per
+// chunk, by lane k of the chunk's 16, and reach the other 15 lanes by DPP
+// row broadcasts.  The workgroup's four waves run R consecutive rows each,
+// tile by tile: a tile is T superblocks of the activations, staged in LDS by
+// the whole workgroup (chunks 272 floats apart, so the four chunks of a pass
+// read disjoint bank halves); a row's running sum waits in lane rr of a
+// register between its tiles, and y is read and written once, at the end.
+constexpr uint32_t FK_WBUF = 1024;      // staging bytes per wave (<= 64 segments)
+constexpr uint32_t FK_XPAD = 272;       // floats per staged activation chunk
+constexpr uint32_t FK_XT_BYTES = 32768; // activation tile budget, bytes
+
+template <int K> __device__ __forceinline__ float row_bcast(float v) {
+    // lane K of each 16-lane row, to the whole row (DPP row_newbcast)
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x150 + K, 0xF, 0xF, false));
+}
+template <typename F, int... K>
+__device__ __forceinline__ void static_for(F && f, std::integer_sequence<int, K...>) {
+    (f(std::integral_constant<int, K>()), ...);
+}
+
+template <int FMT, int NXT>
+__global__ __launch_bounds__(256) void k_dot_fastk(DotArgs a, uint32_t R, uint32_t T) {
+    // NXT: columns fixed at compile time (1), or 0 for a.nx of 1..16
     static_assert(FMT == FMT_Q4_K || FMT == FMT_Q6_K, "K formats");
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t r = blockIdx.x * 4 + wave;
-    if (r >= a.rows) return;                                      // wave-uniform
+    extern __shared__ __align__(16) uint8_t fk_smem[];
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // uniform, in an SGPR
     const uint32_t j = lane & 15, cq = lane >> 4;
     constexpr uint32_t BB = FMT == FMT_Q4_K ? 144 : 210;
-    const uint32_t nsb = a.cols >> 8, nx = a.nx;
-    const uint8_t * wr = a.w + (a.id_slot ? (size_t)(*a.id_slot) * a.estride : 0) + (size_t)r * nsb * BB;
-    float acc[16];
+    const uint32_t nsb = a.cols >> 8, nx = NXT ? NXT : a.nx;
+    constexpr int NP = NXT ? NXT : 16;                            // column slots
+    float * xs = reinterpret_cast<float *>(fk_smem + 4 * FK_WBUF);
+    uint8_t * wb = fk_smem + wave * FK_WBUF;
+    const uint32_t r0 = (blockIdx.x * 4 + wave) * R;
+    const uint32_t nr = r0 < a.rows ? min(R, a.rows - r0) : 0;    // rows of this wave (uniform)
+    const uint8_t * wr = a.w + (a.id_slot ? (size_t)(*a.id_slot) * a.estride : 0) + (size_t)r0 * nsb * BB;
+    const uint32_t ntile = (nsb + T - 1) / T;
+    auto tpass = [&](uint32_t t) { return (min(T, nsb - t * T) + 3) >> 2; };
+    const uint32_t NI = nr * ((nsb + 3) >> 2);                    // T % 4 == 0: no pass straddles tiles
+
+    // item = pass ps of tile t of row rr; cursor order t, rr, ps
+    struct Cur { uint32_t t, rr, ps; };
+    auto start = [&](const Cur & c) { return wr + ((size_t)c.rr * nsb + c.t * T + 4 * c.ps) * BB; };
+    auto len = [&](const Cur & c) { return min(4u, nsb - c.t * T - 4 * c.ps) * BB; };
+    auto advance = [&](Cur & c) {
+        if (++c.ps == tpass(c.t)) { c.ps = 0; if (++c.rr == nr) { c.rr = 0; ++c.t; } }
+    };
+    // every lane loads (lanes past the item's segments repeat its last one)
+    // and every step fetches (past the wave's last item, that item again),
+    // so the loads are unconditional and their counts known to the compiler
+    auto fetch = [&](const Cur & c, u32x4a & v) {
+        const uintptr_t A = (uintptr_t)start(c), a0 = A & ~(uintptr_t)15;
+        const uint32_t nseg = (uint32_t)((A + len(c) - a0 + 15) >> 4);
+        v = *reinterpret_cast<const __attribute__((address_space(1))) u32x4a *>(a0 + 16 * min(lane, nseg - 1));
+    };
+    Cur fc = {0, 0, 0}, cc = {0, 0, 0};                            // fetch / compute cursors
+    uint32_t nf = 0;                                              // items fetched
+    auto fetch_next = [&](u32x4a & v) { fetch(fc, v); if (++nf < NI) advance(fc); };
+    u32x4a vA = {0, 0, 0, 0}, vB = vA;
+    if (NI > 0) { fetch_next(vA); fetch_next(vB); }
+
+    // activation tile t, staged by the whole workgroup: every wave stages
+    // tiles 0 .. ntile - 1 in order (at its first item of the tile, or after
+    // its items when it has fewer tiles' worth), so the barriers pair up
+    uint32_t nt = 0;
+    auto stage = [&]() {
+        const uint32_t t = nt++;
+        if (t > 0) lds_barrier();                                 // all reads of tile t - 1 done
+        const uint32_t tc = min(T, nsb - t * T) * 256;
+        for (uint32_t p = 0; p < nx; ++p) {
+            const float * xp = a.x + (size_t)p * a.xstride + (size_t)t * T * 256;
+            for (uint32_t e0 = threadIdx.x; e0 < tc; e0 += 8 * 256) {   // 8 loads in flight
+                float r[8];
 #pragma unroll
-    for (int p = 0; p < 16; ++p) acc[p] = 0.f;
-    for (uint32_t c0 = 0; c0 < nsb; c0 += 4) {
-        const uint32_t c = c0 + cq;
-        const bool act = c < nsb;
-        float v[16];
+                for (int u = 0; u < 8; ++u) r[u] = e0 + 256 * u < tc ? xp[e0 + 256 * u] : 0.f;
 #pragma unroll
-        for (int k = 0; k < 16; ++k) v[k] = 0.f;
-        if (act) {
-            const uint8_t * b = wr + (size_t)c * BB;
-            if constexpr (FMT == FMT_Q6_K) {
-                const float d = h2f(ld16u(b + 208));
-#pragma unroll
-                for (int k = 0; k < 16; ++k) {
-                    const uint32_t g = (k >> 1) & 3, l = 16 * (k & 1) + j;
-                    const uint8_t lb = b[64 * (k >> 3) + l + 32 * (g & 1)];
-                    const int q6 = ((g < 2) ? (lb & 0xF) : (lb >> 4)) | (((b[128 + 32 * (k >> 3) + l] >> (2 * g)) & 3) << 4);
-                    v[k] = d * (float)(int8_t)b[192 + k] * (float)(q6 - 32);
-                }
-            } else {
-                const float d = h2f(ld16u(b)), dmin = h2f(ld16u(b + 2));
-                const uint8_t * sp = b + 4;
-#pragma unroll
-                for (int k = 0; k < 16; ++k) {
-                    const int g = k >> 1;
-                    uint32_t sc, mn;
-                    if (g < 4) { sc = sp[g] & 63; mn = sp[g + 4] & 63; }
-                    else { sc = (sp[g + 4] & 0xF) | ((sp[g - 4] >> 6) << 4); mn = (sp[g + 4] >> 4) | ((sp[g] >> 6) << 4); }
-                    const uint8_t qb = b[16 + 32 * (k >> 2) + 16 * (k & 1) + j];
-                    const uint32_t nib = (k & 2) ? (qb >> 4) : (qb & 0xF);
-                    const float dd = d * (float)sc, mm = dmin * (float)mn;
-                    v[k] = dd * (float)nib - mm;
-                }
+                for (int u = 0; u < 8; ++u)
+                    if (e0 + 256 * u < tc) xs[(p * T + (e0 >> 8) + u) * FK_XPAD + (e0 & 255)] = r[u];
             }
         }
+        lds_barrier();
+    };
+
+    float acc[NP], accv[NP];                                      // running sum (uniform) / per-row sums in lane rr
 #pragma unroll
-        for (int p = 0; p < 16; ++p) {
+    for (int p = 0; p < NP; ++p) { acc[p] = 0.f; accv[p] = 0.f; }
+
+    auto step = [&](u32x4a & seg) {
+        if (cc.rr == 0 && cc.ps == 0 && cc.t == nt) stage();
+        const uintptr_t A = (uintptr_t)start(cc);
+        const uint32_t sh = (uint32_t)(A & 15);
+        *reinterpret_cast<u32x4a *>(wb + 16 * lane) = seg;
+        fetch_next(seg);
+        __builtin_amdgcn_wave_barrier();
+        if (cc.ps == 0) {                                         // a row's segment starts
+#pragma unroll
+            for (int p = 0; p < NP; ++p)
+                if ((uint32_t)p < nx) acc[p] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(accv[p]), cc.rr));
+        }
+        const uint32_t cl = 4 * cc.ps + cq;                       // chunk within the tile
+        const uint32_t c0 = cc.t * T + 4 * cc.ps;
+        const bool act = c0 + cq < nsb;
+        const uint8_t * b = wb + sh + cq * BB;
+        float v[16];
+        if constexpr (FMT == FMT_Q6_K) {
+            // element k = 8 h + 2 g + o of the lane: 4 low bits from the low
+            // (g < 2) or high nibble of ql byte 64 h + 16 (o + 2 (g & 1)) + j,
+            // 2 high bits from bits 2 g of qh byte 128 + 32 h + 16 o + j.  Per
+            // half, the four ql bytes are packed into QL (byte m = o + 2 (g & 1))
+            // and the two qh bytes into Y so that byte m of Y's bits 0-1 (4-5)
+            // are the high bits of the low (high) nibble's element; then
+            // (q6 + 0x60) ^ 0x80 per byte is q6 - 32 as a signed byte.
+            const float d = h2f(*reinterpret_cast<const uint16_t *>(b + 208));
+            const float ddj = d * (float)(int8_t)b[192 + j];
+            uint32_t Q[4];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t QL = b[64 * h + j] | (b[64 * h + 16 + j] << 8) | (b[64 * h + 32 + j] << 16)
+                                  | ((uint32_t)b[64 * h + 48 + j] << 24);
+                const uint32_t QHP = b[128 + 32 * h + j] | (b[128 + 32 * h + 16 + j] << 8);
+                const uint32_t Y = QHP | (QHP << 14);
+                Q[2 * h] = (((QL & 0x0F0F0F0Fu) | ((Y << 4) & 0x30303030u)) + 0x60606060u) ^ 0x80808080u;
+                Q[2 * h + 1] = ((((QL >> 4) & 0x0F0F0F0Fu) | (Y & 0x30303030u)) + 0x60606060u) ^ 0x80808080u;
+            }
+            static_for([&](auto kc) {
+                constexpr int k = decltype(kc)::value;
+                constexpr int h = k >> 3, g = (k >> 1) & 3, o = k & 1, m = o + 2 * (g & 1);
+                const int q = (int8_t)(Q[2 * h + (g >> 1)] >> (8 * m));
+                v[k] = row_bcast<k>(ddj) * (float)q;
+            }, std::make_integer_sequence<int, 16>());
+        } else {
+            // element k: nibble (k & 2 ? high : low) of qs byte
+            // 16 + 32 (k >> 2) + 16 (k & 1) + j, subblock k >> 1
+            const float d = h2f(*reinterpret_cast<const uint16_t *>(b)), dmin = h2f(*reinterpret_cast<const uint16_t *>(b + 2));
+            const uint8_t * sp = b + 4;
+            const uint32_t g = j & 7;
+            uint32_t sc, mn;
+            if (g < 4) { sc = sp[g] & 63; mn = sp[g + 4] & 63; }
+            else { sc = (sp[g + 4] & 0xF) | ((sp[g - 4] >> 6) << 4); mn = (sp[g + 4] >> 4) | ((sp[g] >> 6) << 4); }
+            const float ddg = d * (float)sc, mmg = dmin * (float)mn;
+            uint32_t N[4];                    // low / high nibbles of bytes 4 t .. 4 t + 3 of the 8
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const uint32_t QS = b[16 + 64 * t + j] | (b[32 + 64 * t + j] << 8) | (b[48 + 64 * t + j] << 16)
+                                  | ((uint32_t)b[64 + 64 * t + j] << 24);
+                N[2 * t] = QS & 0x0F0F0F0Fu;
+                N[2 * t + 1] = (QS >> 4) & 0x0F0F0F0Fu;
+                // keep the masks out of sight so each nibble converts in one
+                // v_cvt_f32_ubyteN (folded, they become a shift, a mask and a convert)
+                asm volatile("" : "+v"(N[2 * t]), "+v"(N[2 * t + 1]));
+            }
+            static_for([&](auto kc) {
+                constexpr int k = decltype(kc)::value;
+                constexpr int m = 2 * (k >> 2) + (k & 1);             // byte of the 8
+                const uint32_t nib = (N[2 * (m >> 2) + ((k >> 1) & 1)] >> (8 * (m & 3))) & 0xFF;
+                v[k] = row_bcast<(k >> 1)>(ddg) * (float)nib - row_bcast<(k >> 1)>(mmg);
+            }, std::make_integer_sequence<int, 16>());
+        }
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
             if ((uint32_t)p >= nx) continue;                      // uniform
-            const float * x = a.x + (size_t)p * a.xstride + 256 * (size_t)(act ? c : 0) + j;
+            const float * x = xs + (p * T + (act ? cl : 0)) * FK_XPAD + j;
             float L = 0.f;
 #pragma unroll
-            for (int k = 0; k < 16; ++k) L = L + v[k] * (act ? x[16 * k] : 0.f);
+            for (int k = 0; k < 16; ++k) L = L + v[k] * x[16 * k];
             // tree16 on the 16 lanes of the chunk: lane 0 ends with
             // ((L0 + L4) + (L8 + L12)) + ... as dot_row_fast's
             const float u = L + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(L), 0x104, 0xF, 0xF, false));
@@ -361,13 +483,25 @@ __global__ __launch_bounds__(256) void k_dot_fastk(DotArgs a) {
             for (int q = 0; q < 4; ++q)
                 if (c0 + q < nsb) acc[p] = acc[p] + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(head), 16 * q));
         }
-    }
-    if (lane == 0) {
+        const Cur done = cc;
+        advance(cc);
+        if (cc.ps == 0) {                                         // the row's segment ends
 #pragma unroll
-        for (int p = 0; p < 16; ++p) {
+            for (int p = 0; p < NP; ++p)
+                if ((uint32_t)p < nx) accv[p] = lane == done.rr ? acc[p] : accv[p];
+        }
+    };
+
+    uint32_t it = 0;
+    for (; it + 1 < NI; it += 2) { step(vA); step(vB); }          // two registers in turn
+    if (it < NI) step(vA);
+    while (nt < ntile) stage();
+    if (lane < nr) {
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
             if ((uint32_t)p >= nx) continue;
-            float * y = a.y + (size_t)p * a.ystride + r;
-            *y = *y + acc[p];
+            float * y = a.y + (size_t)p * a.ystride + r0 + lane;
+            *y = *y + accv[p];
         }
     }
 }
@@ -395,10 +529,19 @@ static int launch_f32(bool fast, int fmt, const DotArgs & a, hipStream_t s) {
     const uint64_t n = (uint64_t)a.rows * a.nx;
     if (n == 0) return FLH_OK;
     if (fast && (fmt == FMT_Q4_K || fmt == FMT_Q6_K) && a.cols % 256 == 0 && a.nx <= 16) {
-        const dim3 gw((a.rows + 3) / 4);
-        if (fmt == FMT_Q4_K) hipLaunchKernelGGL(k_dot_fastk<FMT_Q4_K>, gw, dim3(256), 0, s, a);
-        else hipLaunchKernelGGL(k_dot_fastk<FMT_Q6_K>, gw, dim3(256), 0, s, a);
-        return hip_check(hipGetLastError(), "k_dot_fastk launch");
+        // T: superblocks per activation tile, a multiple of 4, within the
+        // tile budget (4 for 8 or more columns); R: rows per wave
+        const uint32_t nsb = a.cols / 256;
+        uint32_t T = std::max(4u, (uint32_t)(FK_XT_BYTES / (a.nx * FK_XPAD * 4)) & ~3u);
+        T = std::min(T, (nsb + 3) & ~3u);
+        uint32_t R = std::min(4u, std::max(1u, a.rows / 16384));
+        const size_t smem = 4 * FK_WBUF + (size_t)a.nx * T * FK_XPAD * 4;
+        const dim3 gw((uint32_t)((a.rows + 4ull * R - 1) / (4ull * R)));
+        const void * kern = fmt == FMT_Q4_K ? (a.nx == 1 ? (const void *)k_dot_fastk<FMT_Q4_K, 1> : (const void *)k_dot_fastk<FMT_Q4_K, 0>)
+                                            : (a.nx == 1 ? (const void *)k_dot_fastk<FMT_Q6_K, 1> : (const void *)k_dot_fastk<FMT_Q6_K, 0>);
+        if (int rc = lds_fits(kern, smem, "k_dot_fastk")) return rc;
+        void * args[] = {const_cast<DotArgs *>(&a), &R, &T};
+        return hip_check(hipLaunchKernel(kern, gw, dim3(256), args, smem, s), "k_dot_fastk launch");
     }
     const dim3 g((uint32_t)((n + 63) / 64));
     if (fast) hipLaunchKernelGGL(k_dot_f32<true>, g, dim3(64), 0, s, fmt, a);

@@ -1,0 +1,57 @@
+"""GPU parity of the fast fp32 order of Q4_K / Q6_K (k_dot_fastk in
+flh_f32.hip; the reference's dot_row_fast_dequant, src/runtime/kernels.h:
+59-104,162-254), the route the reference's GPU masks give Q6_K.
+
+Bar: bitwise against the oracle.  Seeded random cases cover what the
+kernel's plan varies with: rows per wave (1 to 4: up to 70000 rows, with a
+partial last workgroup), activation tiles (one tile, several, a last partial
+tile; 1 to 16 columns, the 16-column tile of 4 superblocks), rows of 1 to 64
+superblocks (partial last pass), output strides with padding, old y, and the
+expert-slot form (STREAM_DOT_IDX: the matrix is expert 2 of 3, the id read on
+the device).
+"""
+import numpy as np
+import pytest
+
+from oracle import Q4_K, Q6_K, row_bytes
+from util import sane_rows, activations
+from test_gpu_parity import run_dot, bits, say
+
+pytestmark = pytest.mark.gpu
+
+
+def make_cases(n=32, seed=77):
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        fmt = (Q4_K, Q6_K)[rng.integers(2)]
+        rows = int(np.exp(rng.uniform(0, np.log(70000))))
+        nsb = int(rng.integers(1, 65))
+        nx = 1 if rng.random() < 0.5 else int(rng.integers(2, 17))
+        while rows * nsb * max(1, nx // 4) > 1_200_000:   # the oracle's share stays small
+            rows = max(1, rows // 2)
+        pad = int(rng.integers(0, 3))
+        idx = rng.random() < 0.2
+        cases.append((i, fmt, rows, 256 * nsb, nx, pad, idx))
+    cases += [(100, Q6_K, 70001, 256, 1, 0, False), (101, Q4_K, 33000, 512, 1, 1, False),
+              (102, Q6_K, 40000, 1280, 3, 0, True), (103, Q6_K, 128, 16384, 1, 0, False),
+              (104, Q4_K, 37, 14336, 16, 2, False)]
+    return cases
+
+
+@pytest.mark.parametrize("i,fmt,rows,cols,nx,pad,idx", make_cases())
+def test_fastk_random_bitwise(flh, orc, gpu, i, fmt, rows, cols, nx, pad, idx):
+    say("fastk", i, fmt, rows, cols, nx, pad, idx)
+    rng = np.random.default_rng(500 + i)
+    w = sane_rows(fmt, rows, cols, rng)
+    xs = activations(nx, cols, rng, outliers=True)
+    ys = rows + pad
+    y0 = rng.standard_normal((nx - 1) * ys + rows).astype(np.float32)
+    if idx:
+        rb = rows * row_bytes(fmt, cols)
+        ww = np.concatenate([sane_rows(fmt, rows, cols, rng), sane_rows(fmt, rows, cols, rng), w])
+        got, want = run_dot(flh, orc, gpu, fmt, ww, rows, cols, xs, mode="f32fast", y0=y0, id_slot=2,
+                            estride=rb, ystride=ys)
+    else:
+        got, want = run_dot(flh, orc, gpu, fmt, w, rows, cols, xs, mode="f32fast", y0=y0, ystride=ys)
+    assert np.array_equal(bits(got), bits(want))
