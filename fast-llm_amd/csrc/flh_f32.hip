@@ -418,25 +418,29 @@ __global__ __launch_bounds__(256) void k_dot_fastk(DotArgs a, uint32_t R, uint32
             // 2 high bits from bits 2 g of qh byte 128 + 32 h + 16 o + j.  Per
             // half, the four ql bytes are packed into QL (byte m = o + 2 (g & 1))
             // and the two qh bytes into Y so that byte m of Y's bits 0-1 (4-5)
-            // are the high bits of the low (high) nibble's element; then
-            // (q6 + 0x60) ^ 0x80 per byte is q6 - 32 as a signed byte.
+            // are the high bits of the low (high) nibble's element.  Each byte
+            // of Q is then (q6 ^ 0x20) << 2, i.e. 4 (q6 - 32) as a signed byte,
+            // and the factor is d sc / 4: (d sc / 4) (4 (q6 - 32)) is the same
+            // product as (d sc) (q6 - 32), rounded once (d sc / 4 is exact:
+            // |d sc| >= 2^-24 or 0).
             const float d = h2f(*reinterpret_cast<const uint16_t *>(b + 208));
-            const float ddj = d * (float)(int8_t)b[192 + j];
+            const float dd4 = (d * (float)(int8_t)b[192 + j]) * 0.25f;
             uint32_t Q[4];
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 const uint32_t QL = b[64 * h + j] | (b[64 * h + 16 + j] << 8) | (b[64 * h + 32 + j] << 16)
                                   | ((uint32_t)b[64 * h + 48 + j] << 24);
                 const uint32_t QHP = b[128 + 32 * h + j] | (b[128 + 32 * h + 16 + j] << 8);
-                const uint32_t Y = QHP | (QHP << 14);
-                Q[2 * h] = (((QL & 0x0F0F0F0Fu) | ((Y << 4) & 0x30303030u)) + 0x60606060u) ^ 0x80808080u;
-                Q[2 * h + 1] = ((((QL >> 4) & 0x0F0F0F0Fu) | (Y & 0x30303030u)) + 0x60606060u) ^ 0x80808080u;
+                // bits 0-1 and 4-5 of each byte, bit 1 / 5 flipped (q6 ^ 0x20)
+                const uint32_t Y = ((QHP | (QHP << 14)) ^ 0x22222222u) & 0x33333333u;
+                Q[2 * h] = ((QL << 2) & 0x3C3C3C3Cu) | ((Y << 6) & 0xC0C0C0C0u);
+                Q[2 * h + 1] = ((QL >> 2) & 0x3C3C3C3Cu) | ((Y << 2) & 0xC0C0C0C0u);
             }
             static_for([&](auto kc) {
                 constexpr int k = decltype(kc)::value;
                 constexpr int h = k >> 3, g = (k >> 1) & 3, o = k & 1, m = o + 2 * (g & 1);
                 const int q = (int8_t)(Q[2 * h + (g >> 1)] >> (8 * m));
-                v[k] = row_bcast<k>(ddj) * (float)q;
+                v[k] = row_bcast<k>(dd4) * (float)q;
             }, std::make_integer_sequence<int, 16>());
         } else {
             // element k: nibble (k & 2 ? high : low) of qs byte
@@ -475,10 +479,12 @@ __global__ __launch_bounds__(256) void k_dot_fastk(DotArgs a, uint32_t R, uint32
             for (int k = 0; k < 16; ++k) L = L + v[k] * x[16 * k];
             // tree16 on the 16 lanes of the chunk: lane 0 ends with
             // ((L0 + L4) + (L8 + L12)) + ... as dot_row_fast's
-            const float u = L + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(L), 0x104, 0xF, 0xF, false));
-            const float t = u + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(u), 0x108, 0xF, 0xF, false));
-            const float h2 = t + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(t), 0x101, 0xF, 0xF, false));
-            const float head = h2 + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(h2), 0x102, 0xF, 0xF, false));
+            // (lanes past the row's end read 0: bound_ctrl, so the shift
+            // folds into the add as its DPP operand; lane 0 reads none of them)
+            const float u = L + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(L), 0x104, 0xF, 0xF, true));
+            const float t = u + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(u), 0x108, 0xF, 0xF, true));
+            const float h2 = t + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(t), 0x101, 0xF, 0xF, true));
+            const float head = h2 + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(h2), 0x102, 0xF, 0xF, true));
 #pragma unroll
             for (int q = 0; q < 4; ++q)
                 if (c0 + q < nsb) acc[p] = acc[p] + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(head), 16 * q));
