@@ -323,6 +323,15 @@ template <int K> __device__ __forceinline__ float row_bcast(float v) {
     // lane K of each 16-lane row, to the whole row (DPP row_newbcast)
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x150 + K, 0xF, 0xF, false));
 }
+// four bytes b0 | b1 << 8 | b2 << 16 | b3 << 24, built as two 16-bit pairs
+// (b0, b2) and (b1, b3): two v_perm_b32 and one shift-or
+typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack4(uint32_t b0, uint32_t b1, uint32_t b2, uint32_t b3) {
+    u16x2 e, o;
+    e.x = (uint16_t)b0; e.y = (uint16_t)b2;
+    o.x = (uint16_t)b1; o.y = (uint16_t)b3;
+    return __builtin_bit_cast(uint32_t, e) | (__builtin_bit_cast(uint32_t, o) << 8);
+}
 template <typename F, int... K>
 __device__ __forceinline__ void static_for(F && f, std::integer_sequence<int, K...>) {
     (f(std::integral_constant<int, K>()), ...);
@@ -428,8 +437,7 @@ __global__ __launch_bounds__(256) void k_dot_fastk(DotArgs a, uint32_t R, uint32
             uint32_t Q[4];
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-                const uint32_t QL = b[64 * h + j] | (b[64 * h + 16 + j] << 8) | (b[64 * h + 32 + j] << 16)
-                                  | ((uint32_t)b[64 * h + 48 + j] << 24);
+                const uint32_t QL = pack4(b[64 * h + j], b[64 * h + 16 + j], b[64 * h + 32 + j], b[64 * h + 48 + j]);
                 const uint32_t QHP = b[128 + 32 * h + j] | (b[128 + 32 * h + 16 + j] << 8);
                 // bits 0-1 and 4-5 of each byte, bit 1 / 5 flipped (q6 ^ 0x20)
                 const uint32_t Y = ((QHP | (QHP << 14)) ^ 0x22222222u) & 0x33333333u;
@@ -455,8 +463,7 @@ __global__ __launch_bounds__(256) void k_dot_fastk(DotArgs a, uint32_t R, uint32
             uint32_t N[4];                    // low / high nibbles of bytes 4 t .. 4 t + 3 of the 8
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
-                const uint32_t QS = b[16 + 64 * t + j] | (b[32 + 64 * t + j] << 8) | (b[48 + 64 * t + j] << 16)
-                                  | ((uint32_t)b[64 + 64 * t + j] << 24);
+                const uint32_t QS = pack4(b[16 + 64 * t + j], b[32 + 64 * t + j], b[48 + 64 * t + j], b[64 + 64 * t + j]);
                 N[2 * t] = QS & 0x0F0F0F0Fu;
                 N[2 * t + 1] = (QS >> 4) & 0x0F0F0F0Fu;
                 // keep the masks out of sight so each nibble converts in one
@@ -512,6 +519,112 @@ __global__ __launch_bounds__(256) void k_dot_fastk(DotArgs a, uint32_t R, uint32
     }
 }
 
+// Fast fp32 order of F32 weights (dot_row_fast, src/runtime/kernels.h:11-19,
+// 58-104: L[j] over the elements k < n16 with k % 16 == j in ascending k,
+// the 16-lane tree, then the tail k >= n16 in order, y += head + tail), the
+// route of every F32 matrix (e.g. an MoE router) under every mask: 16 lanes
+// per row, lane j running L[j]; a wave holds 4 rows, a workgroup 16.  A block
+// is 256 columns (16 elements per lane), its weights loaded as 16 dword loads
+// per lane one block ahead into two register sets used in turn; the
+// activations are staged in LDS by the workgroup in tiles of up to 32 KB
+// (every row of a wave reads the same address: a broadcast).  Elements past
+// n16 are masked out of the chains (their loads read a valid address).
+constexpr uint32_t F32R_XT_BYTES = 32768;
+
+template <int NXT>
+__global__ __launch_bounds__(256) void k_dot_f32row(DotArgs a, uint32_t T) {
+    // NXT: column slots (1, 2, 4, 8, 16; a.nx <= NXT); D: blocks in flight
+    constexpr int D = NXT <= 2 ? 4 : 2;
+    extern __shared__ __align__(16) uint8_t f32r_smem[];
+    float * xs = reinterpret_cast<float *>(f32r_smem);
+    const uint32_t lane = threadIdx.x & 63, j = lane & 15;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    constexpr int NP = NXT;
+    const uint32_t nx = NXT == 1 ? 1 : a.nx, cols = a.cols, n16 = cols & ~15u;
+    const uint32_t r = blockIdx.x * 16 + wave * 4 + (lane >> 4);
+    const uint32_t rw = min(blockIdx.x * 16 + wave * 4, a.rows - 1);   // the wave's first row (uniform)
+    const float * w0 = reinterpret_cast<const float *>(a.w + (a.id_slot ? (size_t)(*a.id_slot) * a.estride : 0))
+                     + (size_t)rw * cols;
+    const float * wr = w0 + (size_t)(min(r, a.rows - 1) - rw) * cols;
+    const uint32_t roff = (min(r, a.rows - 1) - rw) * cols;      // < 4 rows: 32 bits
+    const auto * wg = (const __attribute__((address_space(1))) float *)w0;
+    const uint32_t nblk = (n16 + 255) / 256;                      // blocks of 256 columns
+    using f16v = float __attribute__((ext_vector_type(16)));
+    auto fetch = [&](uint32_t kb, f16v & v) __attribute__((always_inline)) {                     // block min(kb, nblk - 1), clamped reads
+        const uint32_t c0 = min(kb, nblk - 1) * 256 + j;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) v[e] = wg[roff + min(c0 + 16 * e, cols - 1)];
+    };
+    float L[NP];
+#pragma unroll
+    for (int p = 0; p < NP; ++p) L[p] = 0.f;
+    uint32_t nt = 0;                                              // tiles staged
+    auto stage = [&](uint32_t t) __attribute__((always_inline)) {
+        if (t > 0) lds_barrier();
+        const uint32_t c0 = t * T, tc = min(T, n16 - c0);
+        for (uint32_t p = 0; p < nx; ++p) {
+            const float * xp = a.x + (size_t)p * a.xstride + c0;
+            for (uint32_t e0 = threadIdx.x; e0 < tc; e0 += 8 * 256) {
+                float v[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) v[u] = e0 + 256 * u < tc ? xp[e0 + 256 * u] : 0.f;
+#pragma unroll
+                for (int u = 0; u < 8; ++u)
+                    if (e0 + 256 * u < tc) xs[p * T + e0 + 256 * u] = v[u];
+            }
+        }
+        lds_barrier();
+    };
+    auto step = [&](uint32_t kb, f16v & v) __attribute__((always_inline)) {
+        if (kb * 256 == nt * T) stage(nt++);
+        const f16v w = v;
+        fetch(kb + D, v);
+        const uint32_t c = kb * 256 - (nt - 1) * T;               // column of the block within its tile
+        const bool full = kb * 256 + 256 <= n16;
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+            if ((uint32_t)p >= nx) continue;
+            const float * x = xs + p * T + c + j;
+            float l = L[p];
+            if (full) {
+#pragma unroll
+                for (int e = 0; e < 16; ++e) l = l + w[e] * x[16 * e];
+            } else {
+#pragma unroll
+                for (int e = 0; e < 16; ++e)
+                    if (kb * 256 + 16 * e < n16) l = l + w[e] * x[16 * e];   // uniform
+            }
+            L[p] = l;
+        }
+    };
+    f16v v[D];                                                    // block kb in v[kb % D]
+    if (nblk > 0) static_for([&](auto ic) { fetch(decltype(ic)::value, v[decltype(ic)::value]); },
+                             std::make_integer_sequence<int, D>());
+    uint32_t kb = 0;
+    for (; kb + D <= nblk; kb += D)
+        static_for([&](auto ic) { step(kb + decltype(ic)::value, v[decltype(ic)::value]); },
+                   std::make_integer_sequence<int, D>());
+    static_for([&](auto ic) { if (kb + decltype(ic)::value < nblk) step(kb + decltype(ic)::value, v[decltype(ic)::value]); },
+               std::make_integer_sequence<int, D>());
+    if (r >= a.rows) return;
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+        if ((uint32_t)p >= nx) continue;
+        const float Lp = L[p];
+        const float u = Lp + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(Lp), 0x104, 0xF, 0xF, true));
+        const float t = u + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(u), 0x108, 0xF, 0xF, true));
+        const float h2 = t + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(t), 0x101, 0xF, 0xF, true));
+        const float head = h2 + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(h2), 0x102, 0xF, 0xF, true));
+        if (j == 0) {
+            const float * x = a.x + (size_t)p * a.xstride;
+            float tail = 0.f;
+            for (uint32_t k = n16; k < cols; ++k) tail = tail + wr[k] * x[k];
+            float * y = a.y + (size_t)p * a.ystride + r;
+            *y = *y + (head + tail);
+        }
+    }
+}
+
 template <bool FAST>
 __global__ void k_dot_f32(int fmt, DotArgs a) {
     const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -548,6 +661,19 @@ static int launch_f32(bool fast, int fmt, const DotArgs & a, hipStream_t s) {
         if (int rc = lds_fits(kern, smem, "k_dot_fastk")) return rc;
         void * args[] = {const_cast<DotArgs *>(&a), &R, &T};
         return hip_check(hipLaunchKernel(kern, gw, dim3(256), args, smem, s), "k_dot_fastk launch");
+    }
+    if (fast && fmt == FMT_F32 && a.nx <= 16) {
+        // T: columns per activation tile, a multiple of 256 within the budget
+        uint32_t T = std::max(256u, (uint32_t)(F32R_XT_BYTES / (4 * a.nx)) & ~255u);
+        T = std::min(T, std::max(256u, ((a.cols & ~15u) + 255) & ~255u));
+        const size_t smem = (size_t)a.nx * T * 4;
+        const dim3 gw((a.rows + 15) / 16);
+        const void * kern = a.nx == 1 ? (const void *)k_dot_f32row<1> : a.nx == 2 ? (const void *)k_dot_f32row<2>
+                          : a.nx <= 4 ? (const void *)k_dot_f32row<4> : a.nx <= 8 ? (const void *)k_dot_f32row<8>
+                          : (const void *)k_dot_f32row<16>;
+        if (int rc = lds_fits(kern, smem, "k_dot_f32row")) return rc;
+        void * args[] = {const_cast<DotArgs *>(&a), &T};
+        return hip_check(hipLaunchKernel(kern, gw, dim3(256), args, smem, s), "k_dot_f32row launch");
     }
     const dim3 g((uint32_t)((n + 63) / 64));
     if (fast) hipLaunchKernelGGL(k_dot_f32<true>, g, dim3(64), 0, s, fmt, a);
