@@ -9,7 +9,8 @@
 //    reference's fixed 16-lane order (src/runtime/kernels.h:11-19):
 //    dot_row_fast / dot_row_fast_q8_0 / dot_row_fast_dequant, bitwise; Q4_K
 //    and Q6_K (the reference GPU masks' Q6_K route) on one wave per row
-//    (k_dot_fastk), the other formats one thread per (row, column).
+//    (k_dot_fastk), F32 weights (e.g. an MoE router) on 16 lanes per row
+//    (k_dot_f32row), the other formats one thread per (row, column).
 //  * ROUTER_SEL / SILU_MUL / WMERGE / MERGE: the reference's single-thread
 //    canonical ops (src/runtime/decode_params.h:234-295,
 //    runtime_internal.h:274-281), one thread per token / element.  expf is
