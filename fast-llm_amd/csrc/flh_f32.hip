@@ -653,7 +653,7 @@ static int launch_f32(bool fast, int fmt, const DotArgs & a, hipStream_t s) {
         // tile budget (4 for 8 or more columns); R: rows per wave
         const uint32_t nsb = a.cols / 256;
         uint32_t T = std::max(4u, (uint32_t)(FK_XT_BYTES / (a.nx * FK_XPAD * 4)) & ~3u);
-        T = std::min(T, (nsb + 3) & ~3u);
+        T = std::min(T, std::max(4u, (nsb + 3) & ~3u));          // >= 4 also for rows of no columns
         uint32_t R = std::min(4u, std::max(1u, a.rows / 16384));
         const size_t smem = 4 * FK_WBUF + (size_t)a.nx * T * FK_XPAD * 4;
         const dim3 gw((uint32_t)((a.rows + 4ull * R - 1) / (4ull * R)));

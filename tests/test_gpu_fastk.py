@@ -102,3 +102,18 @@ def test_f32_fast_random_bitwise(flh, orc, gpu, i, rows, cols, nx, pad, idx):
     orc.stream_dot(F32, ww, rows, cols, hx, want, nx=nx, xstride=st, ystride=ys, fast=True, i8_mask=0,
                    i8k_mask=0, id_slot=e, estride=estride, threads=8)
     assert np.array_equal(bits(got), bits(want))
+
+
+@pytest.mark.parametrize("fmt", [F32, Q4_K, Q6_K])
+def test_fast_rows_of_no_columns(flh, orc, gpu, fmt):
+    """cols = 0: every row's dot is 0 and y += 0 (-0 becomes +0), as the
+    reference's loop over an empty row."""
+    say("fast cols 0", fmt)
+    rows = 37
+    y0 = np.array([-0.0, 1.5, -2.0] * 12 + [3.0], dtype=np.float32)
+    dy = flh.DeviceBuffer.from_array(y0, gpu)
+    dw = flh.DeviceBuffer.from_array(np.zeros(16, dtype=np.uint8), gpu)
+    dx = flh.DeviceBuffer.from_array(np.zeros(64, dtype=np.float32), gpu)
+    flh.stream_dot(fmt, dw, rows, 0, dx, dy, gpu, fast=True, i8_mask=0, i8k_mask=0, w_bytes=0)
+    got = dy.download(np.float32, rows, gpu)
+    assert np.array_equal(bits(got), bits(y0 + np.float32(0.0)))
