@@ -146,6 +146,9 @@ void load_tune() {
 static int dispatch_dot(int fmt, const DotArgs & a, int fast, uint32_t i8_mask, uint32_t i8k_mask,
                         hipStream_t s) {
     if (!fast) return launch_dot_canonical(fmt, a, s);
+    // rows of no columns: every order's dot is +0 (y += 0); the fp32 kernels
+    // are the ones planned for it
+    if (a.cols == 0) return launch_dot_fast_f32(fmt, a, s);
     if ((fmt == FLH_FMT_Q4_K || fmt == FLH_FMT_Q6_K) && ((i8k_mask >> fmt) & 1u))
         return launch_dot_i8k(fmt, a, s);
     if (fmt != FLH_FMT_F32 && ((i8_mask >> fmt) & 1u)) {
@@ -446,7 +449,7 @@ int flh_act_q8_stream_dot(int fmt, const void * w, uint64_t w_bytes, uint32_t ro
     DotArgs a{(const uint8_t *)w, id_slot, estride, x, y, rows, cols, nx, xstride, ystride};
     // Fused when every workgroup re-reading the fp32 column is cheaper than a
     // separate ACT_Q8 launch.
-    if (fast && cols <= tune().fuse_max_cols && (fmt == FLH_FMT_Q4_K || fmt == FLH_FMT_Q6_K) && ((i8k_mask >> fmt) & 1u)) {
+    if (fast && cols > 0 && cols <= tune().fuse_max_cols && (fmt == FLH_FMT_Q4_K || fmt == FLH_FMT_Q6_K) && ((i8k_mask >> fmt) & 1u)) {
         const int rc = launch_act_dot_kstream(fmt, a, s);
         if (rc != FLH_ERR_UNSUPPORTED) return rc;
     }
@@ -461,7 +464,7 @@ static int rmsnorm_dot(int fmt, const DotArgs & a, const NormArgs & nm, int fast
     const float * xb = nm.x, * xe = nm.x + a.cols;
     const float * yb = a.x, * ye = (const float *)((const uint8_t *)a.x + x_alloc_bytes(a.cols));
     const bool overlap = xb < ye && yb < xe;
-    if (fast && !overlap && fmt == FLH_FMT_Q4_K && ((i8k_mask >> fmt) & 1u) && a.cols <= 8192) {
+    if (fast && !overlap && fmt == FLH_FMT_Q4_K && ((i8k_mask >> fmt) & 1u) && a.cols > 0 && a.cols <= 8192) {
         // the kernel the plain fused ACT_Q8 dot takes at this size (above 2^18
         // superblocks the four-lanes one)
         int rc = FLH_ERR_UNSUPPORTED;

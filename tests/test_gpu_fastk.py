@@ -15,9 +15,9 @@ the device).
 import numpy as np
 import pytest
 
-from oracle import F32, Q4_K, Q6_K, row_bytes, col_stride_floats
+from oracle import F32, Q8_0, Q5_0, Q4_K, Q6_K, IQ2_XXS, IQ3_XXS, row_bytes, col_stride_floats
 from util import sane_rows, activations, normal_weights
-from test_gpu_parity import run_dot, bits, say, dev_cols
+from test_gpu_parity import run_dot, bits, say, dev_cols, I8, I8K
 
 pytestmark = pytest.mark.gpu
 
@@ -104,16 +104,20 @@ def test_f32_fast_random_bitwise(flh, orc, gpu, i, rows, cols, nx, pad, idx):
     assert np.array_equal(bits(got), bits(want))
 
 
-@pytest.mark.parametrize("fmt", [F32, Q4_K, Q6_K])
-def test_fast_rows_of_no_columns(flh, orc, gpu, fmt):
-    """cols = 0: every row's dot is 0 and y += 0 (-0 becomes +0), as the
-    reference's loop over an empty row."""
-    say("fast cols 0", fmt)
+@pytest.mark.parametrize("fmt", [F32, Q8_0, Q5_0, Q4_K, Q6_K, IQ2_XXS, IQ3_XXS])
+@pytest.mark.parametrize("masks", [(0, 0), (I8, I8K), (I8 | 0b1100000, 0)])
+def test_rows_of_no_columns(flh, orc, gpu, fmt, masks):
+    """cols = 0 on every route (fp32, the default int8 masks, IQ on int8): every
+    row's dot is 0 and y += 0 (-0 becomes +0), as the reference's loop over an
+    empty row."""
+    say("cols 0", fmt, masks)
     rows = 37
     y0 = np.array([-0.0, 1.5, -2.0] * 12 + [3.0], dtype=np.float32)
     dy = flh.DeviceBuffer.from_array(y0, gpu)
     dw = flh.DeviceBuffer.from_array(np.zeros(16, dtype=np.uint8), gpu)
     dx = flh.DeviceBuffer.from_array(np.zeros(64, dtype=np.float32), gpu)
-    flh.stream_dot(fmt, dw, rows, 0, dx, dy, gpu, fast=True, i8_mask=0, i8k_mask=0, w_bytes=0)
+    flh.stream_dot(fmt, dw, rows, 0, dx, dy, gpu, fast=True, i8_mask=masks[0], i8k_mask=masks[1], w_bytes=0)
+    if fmt in (Q4_K, Q6_K) and masks == (I8, I8K):     # the fused ACT_Q8 entry point too
+        flh.act_q8_stream_dot(fmt, dw, rows, 0, dx, dy, gpu)
     got = dy.download(np.float32, rows, gpu)
     assert np.array_equal(bits(got), bits(y0 + np.float32(0.0)))
