@@ -612,7 +612,7 @@ int flh_moe_dot(int fmt, const void * w, uint64_t estride, uint32_t rows, uint32
     if (int rc = need_init()) return rc;
     if (fmt < FLH_FMT_Q8_0 || fmt > FLH_FMT_IQ3_XXS)
         return set_error(FLH_ERR_UNSUPPORTED, "moe_dot: quantized weight formats only");
-    if (cols % 256) return set_error(FLH_ERR_ARG, "moe_dot: cols not a multiple of 256");
+    if (cols % 256 || cols == 0) return set_error(FLH_ERR_ARG, "moe_dot: cols not a positive multiple of 256");
     if (!w || !ids || !x || !y || n_expert == 0) return set_error(FLH_ERR_ARG, "moe_dot: null argument");
     if (estride < (uint64_t)rows * flh_row_bytes(fmt, cols) || (estride & w_align_mask(fmt)) ||
         ((uintptr_t)w & w_align_mask(fmt)))
@@ -631,7 +631,7 @@ int flh_router_moe_dot(int fmt, const void * w, uint64_t estride, uint32_t rows,
     if (fmt < FLH_FMT_Q8_0 || fmt > FLH_FMT_IQ3_XXS)
         return set_error(FLH_ERR_UNSUPPORTED, "router_moe_dot: quantized weight formats only");
     const bool kf = fmt == FLH_FMT_Q4_K || fmt == FLH_FMT_Q6_K;
-    if (cols % 256) return set_error(FLH_ERR_ARG, "router_moe_dot: cols not a multiple of 256");
+    if (cols % 256 || cols == 0) return set_error(FLH_ERR_ARG, "router_moe_dot: cols not a positive multiple of 256");
     if (!w || !logits || !ids || !gates || !x || !y || n_expert == 0 || top_k == 0 || top_k > n_expert)
         return set_error(FLH_ERR_ARG, "router_moe_dot: null argument or top_k outside 1..n_expert");
     if (estride < (uint64_t)rows * flh_row_bytes(fmt, cols) || (estride & w_align_mask(fmt)) ||

@@ -286,7 +286,7 @@ int flh_dequant(int fmt, const void * w, uint32_t rows, uint32_t cols,
  * holds the shape (16-byte aligned w, x and estride, at most ~14.5K columns;
  * IQ: a multiple of 2048), else one STREAM_DOT_IDX tile per pair (up to 16384
  * columns; the ids must then be < n_expert, as ROUTER_SEL writes them).
- * cols a multiple of 256.  Every output is bitwise equal to the per-pair
+ * cols a positive multiple of 256 (0 is FLH_ERR_ARG).  Every output is bitwise equal to the per-pair
  * STREAM_DOT_IDX tile. */
 int flh_moe_dot(int fmt, const void * w, uint64_t estride, uint32_t rows,
                 uint32_t cols, const uint32_t * ids, uint32_t ntok,

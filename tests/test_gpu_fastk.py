@@ -121,3 +121,12 @@ def test_rows_of_no_columns(flh, orc, gpu, fmt, masks):
         flh.act_q8_stream_dot(fmt, dw, rows, 0, dx, dy, gpu)
     got = dy.download(np.float32, rows, gpu)
     assert np.array_equal(bits(got), bits(y0 + np.float32(0.0)))
+
+
+def test_moe_rejects_rows_of_no_columns(flh, gpu):
+    """The grouped expert entry points take cols as a positive multiple of 256:
+    0 is an argument error, nothing launched."""
+    d = flh.DeviceBuffer.from_array(np.zeros(64, dtype=np.float32), gpu)
+    ids = flh.DeviceBuffer.from_array(np.zeros(4, dtype=np.uint32), gpu)
+    with pytest.raises(flh.FlhError, match="positive multiple of 256"):
+        flh.moe_dot(Q4_K, d, 256, 4, 0, ids, 1, 1, 2, d, 64, False, d, 4, gpu)
