@@ -316,6 +316,13 @@ int launch_dot_i8_k(int fmt, const DotArgs & a, hipStream_t s) {
 // the whole workgroup (chunks 272 floats apart, so the four chunks of a pass
 // read disjoint bank halves); a row's running sum waits in lane rr of a
 // register between its tiles, and y is read and written once, at the end.
+__host__ __device__ constexpr uint32_t fk_chunk_bytes(int fmt) {
+    return fmt == FMT_Q4_K ? 144u : fmt == FMT_Q6_K ? 210u : fmt == FMT_Q5_0 ? 176u
+         : fmt == FMT_IQ2_XXS ? 66u : 98u;
+}
+__host__ __device__ constexpr uint32_t fk_grid_bytes(int fmt) {
+    return fmt == FMT_IQ2_XXS ? 2048u : fmt == FMT_IQ3_XXS ? 1024u : 0u;
+}
 constexpr uint32_t FK_WBUF = 1024;      // staging bytes per wave (<= 64 segments)
 constexpr uint32_t FK_XPAD = 272;       // floats per staged activation chunk
 constexpr uint32_t FK_XT_BYTES = 32768; // activation tile budget, bytes
@@ -341,27 +348,32 @@ __device__ __forceinline__ void static_for(F && f, std::integer_sequence<int, K.
 template <int FMT, int NXT>
 __global__ __launch_bounds__(256) void k_dot_fastk(DotArgs a, uint32_t R, uint32_t T) {
     // NXT: columns fixed at compile time (1), or 0 for a.nx of 1..16
-    static_assert(FMT == FMT_Q4_K || FMT == FMT_Q6_K, "K formats");
+    static_assert(FMT == FMT_Q4_K || FMT == FMT_Q6_K || FMT == FMT_Q5_0 || FMT == FMT_IQ2_XXS ||
+                  FMT == FMT_IQ3_XXS, "formats of the 256-element chunk order");
     extern __shared__ __align__(16) uint8_t fk_smem[];
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // uniform, in an SGPR
     const uint32_t j = lane & 15, cq = lane >> 4;
-    constexpr uint32_t BB = FMT == FMT_Q4_K ? 144 : 210;
-    const uint32_t nsb = a.cols >> 8, nx = NXT ? NXT : a.nx;
+    constexpr uint32_t BB = fk_chunk_bytes(FMT);                  // bytes of a 256-element chunk
+    constexpr uint32_t GB = fk_grid_bytes(FMT);                   // IQ codebook staged in LDS
+    const uint32_t cols = a.cols, nsb = (cols + 255) >> 8, nx = NXT ? NXT : a.nx;
+    // row bytes (Q5_0: the last chunk holds cols % 256 / 32 blocks)
+    const uint32_t RB = FMT == FMT_Q5_0 ? (cols / 32) * 22 : nsb * BB;
     constexpr int NP = NXT ? NXT : 16;                            // column slots
-    float * xs = reinterpret_cast<float *>(fk_smem + 4 * FK_WBUF);
+    uint8_t * gl = fk_smem + 4 * FK_WBUF;                         // codebook (IQ)
+    float * xs = reinterpret_cast<float *>(fk_smem + 4 * FK_WBUF + GB);
     uint8_t * wb = fk_smem + wave * FK_WBUF;
     const uint32_t r0 = (blockIdx.x * 4 + wave) * R;
     const uint32_t nr = r0 < a.rows ? min(R, a.rows - r0) : 0;    // rows of this wave (uniform)
-    const uint8_t * wr = a.w + (a.id_slot ? (size_t)(*a.id_slot) * a.estride : 0) + (size_t)r0 * nsb * BB;
+    const uint8_t * wr = a.w + (a.id_slot ? (size_t)(*a.id_slot) * a.estride : 0) + (size_t)r0 * RB;
     const uint32_t ntile = (nsb + T - 1) / T;
     auto tpass = [&](uint32_t t) { return (min(T, nsb - t * T) + 3) >> 2; };
     const uint32_t NI = nr * ((nsb + 3) >> 2);                    // T % 4 == 0: no pass straddles tiles
 
     // item = pass ps of tile t of row rr; cursor order t, rr, ps
     struct Cur { uint32_t t, rr, ps; };
-    auto start = [&](const Cur & c) { return wr + ((size_t)c.rr * nsb + c.t * T + 4 * c.ps) * BB; };
-    auto len = [&](const Cur & c) { return min(4u, nsb - c.t * T - 4 * c.ps) * BB; };
+    auto start = [&](const Cur & c) { return wr + (size_t)c.rr * RB + (c.t * T + 4 * c.ps) * BB; };
+    auto len = [&](const Cur & c) { return min(4 * BB, RB - (c.t * T + 4 * c.ps) * BB); };
     auto advance = [&](Cur & c) {
         if (++c.ps == tpass(c.t)) { c.ps = 0; if (++c.rr == nr) { c.rr = 0; ++c.t; } }
     };
@@ -386,7 +398,14 @@ __global__ __launch_bounds__(256) void k_dot_fastk(DotArgs a, uint32_t R, uint32
     auto stage = [&]() {
         const uint32_t t = nt++;
         if (t > 0) lds_barrier();                                 // all reads of tile t - 1 done
-        const uint32_t tc = min(T, nsb - t * T) * 256;
+        if constexpr (GB > 0) {
+            if (t == 0) {
+                const uint32_t * g = FMT == FMT_IQ2_XXS ? reinterpret_cast<const uint32_t *>(k_iq2_grid)
+                                                        : reinterpret_cast<const uint32_t *>(k_iq3_grid);
+                for (uint32_t i = threadIdx.x; i < GB / 4; i += 256) reinterpret_cast<uint32_t *>(gl)[i] = g[i];
+            }
+        }
+        const uint32_t tc = min(T * 256, cols - t * T * 256);     // elements of the tile
         for (uint32_t p = 0; p < nx; ++p) {
             const float * xp = a.x + (size_t)p * a.xstride + (size_t)t * T * 256;
             for (uint32_t e0 = threadIdx.x; e0 < tc; e0 += 8 * 256) {   // 8 loads in flight
@@ -422,7 +441,55 @@ __global__ __launch_bounds__(256) void k_dot_fastk(DotArgs a, uint32_t R, uint32
         const bool act = c0 + cq < nsb;
         const uint8_t * b = wb + sh + cq * BB;
         float v[16];
-        if constexpr (FMT == FMT_Q6_K) {
+        // elements of the lane's chain in this chunk (Q5_0: the row's last
+        // chunk may hold fewer than 256)
+        const uint32_t nk = FMT == FMT_Q5_0 ? (act ? min(16u, (cols - 256 * (c0 + cq)) / 16) : 0u) : 16u;
+        if constexpr (FMT == FMT_Q5_0) {
+            // block k >> 1 of the chunk, element 16 (k & 1) + j: nibble (k & 1 ?
+            // high : low) of qs byte j, bit 16 (k & 1) + j of qh, minus 16
+            // (dequant_chunk's d * q5); lane g < 8 reads block g's d and qh
+            const uint32_t g = j & 7;
+            const uint8_t * bg = b + 22 * g;
+            const float dg = h2f(*reinterpret_cast<const uint16_t *>(bg));
+            const uint32_t qhg = *reinterpret_cast<const uint16_t *>(bg + 2) |
+                                 ((uint32_t)*reinterpret_cast<const uint16_t *>(bg + 4) << 16);
+            uint32_t qs[8];
+#pragma unroll
+            for (int m = 0; m < 8; ++m) qs[m] = b[22 * m + 6 + j];
+            static_for([&](auto kc) {
+                constexpr int k = decltype(kc)::value;
+                const uint32_t qh = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)qhg, 0x150 + (k >> 1), 0xF, 0xF, false);
+                const uint32_t nib = (k & 1) ? (qs[k >> 1] >> 4) : (qs[k >> 1] & 0xF);
+                const int q = (int)(nib | (((qh >> (16 * (k & 1) + j)) & 1u) << 4)) - 16;
+                v[k] = row_bcast<(k >> 1)>(dg) * (float)q;
+            }, std::make_integer_sequence<int, 16>());
+        } else if constexpr (FMT == FMT_IQ2_XXS || FMT == FMT_IQ3_XXS) {
+            // group ib = k >> 1, element 16 (k & 1) + j: run l = 2 (k & 1) +
+            // (j >> 3), magnitude byte j & 7 (IQ2: of the 8-byte codebook entry
+            // of index byte l) or j & 3 (IQ3: of the 4-byte entry of index byte
+            // 2 l + ((j >> 2) & 1)), sign bit 16 (k & 1) + j of the group's four
+            // parity-widened 7-bit fields; value db * (+-magnitude).  Lane g < 8
+            // makes group g's db and sign bytes
+            const uint32_t g = j & 7;
+            const float d = h2f(*reinterpret_cast<const uint16_t *>(b));
+            const uint8_t * wp = FMT == FMT_IQ2_XXS ? b + 2 + 8 * g + 4 : b + 66 + 4 * g;
+            const uint32_t w1 = *reinterpret_cast<const uint16_t *>(wp) |
+                                ((uint32_t)*reinterpret_cast<const uint16_t *>(wp + 2) << 16);
+            const float dbg = FMT == FMT_IQ2_XXS ? (d * (0.5f + (float)(w1 >> 28))) * 0.25f
+                                                 : (d * (0.5f + (float)(w1 >> 28))) * 0.5f;
+            const uint32_t sgg = iq_sign8(w1) | (iq_sign8(w1 >> 7) << 8) | (iq_sign8(w1 >> 14) << 16) |
+                                 (iq_sign8(w1 >> 21) << 24);
+            static_for([&](auto kc) {
+                constexpr int k = decltype(kc)::value;
+                constexpr int ib = k >> 1;
+                uint32_t mag;
+                if constexpr (FMT == FMT_IQ2_XXS) mag = gl[8 * b[2 + 8 * ib + 2 * (k & 1) + (j >> 3)] + (j & 7)];
+                else mag = gl[4 * b[2 + 8 * ib + 4 * (k & 1) + (j >> 2)] + (j & 3)];
+                const uint32_t sg = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)sgg, 0x150 + ib, 0xF, 0xF, false);
+                const float m = (float)mag;
+                v[k] = row_bcast<ib>(dbg) * (((sg >> (16 * (k & 1) + j)) & 1u) ? -m : m);
+            }, std::make_integer_sequence<int, 16>());
+        } else if constexpr (FMT == FMT_Q6_K) {
             // element k = 8 h + 2 g + o of the lane: 4 low bits from the low
             // (g < 2) or high nibble of ql byte 64 h + 16 (o + 2 (g & 1)) + j,
             // 2 high bits from bits 2 g of qh byte 128 + 32 h + 16 o + j.  Per
@@ -483,8 +550,13 @@ __global__ __launch_bounds__(256) void k_dot_fastk(DotArgs a, uint32_t R, uint32
             if ((uint32_t)p >= nx) continue;                      // uniform
             const float * x = xs + (p * T + (act ? cl : 0)) * FK_XPAD + j;
             float L = 0.f;
+            if constexpr (FMT == FMT_Q5_0) {
 #pragma unroll
-            for (int k = 0; k < 16; ++k) L = L + v[k] * x[16 * k];
+                for (int k = 0; k < 16; ++k) L = (uint32_t)k < nk ? L + v[k] * x[16 * k] : L;
+            } else {
+#pragma unroll
+                for (int k = 0; k < 16; ++k) L = L + v[k] * x[16 * k];
+            }
             // tree16 on the 16 lanes of the chunk: lane 0 ends with
             // ((L0 + L4) + (L8 + L12)) + ... as dot_row_fast's
             // (lanes past the row's end read 0: bound_ctrl, so the shift
@@ -648,17 +720,24 @@ static int launch_f32(bool fast, int fmt, const DotArgs & a, hipStream_t s) {
         return set_error(FLH_ERR_UNSUPPORTED, "fp32 dot: format not supported");
     const uint64_t n = (uint64_t)a.rows * a.nx;
     if (n == 0) return FLH_OK;
-    if (fast && (fmt == FMT_Q4_K || fmt == FMT_Q6_K) && a.cols % 256 == 0 && a.nx <= 16) {
-        // T: superblocks per activation tile, a multiple of 4, within the
-        // tile budget (4 for 8 or more columns); R: rows per wave
-        const uint32_t nsb = a.cols / 256;
+    const bool chunked = fmt == FMT_Q4_K || fmt == FMT_Q6_K || fmt == FMT_Q5_0 || fmt == FMT_IQ2_XXS ||
+                         fmt == FMT_IQ3_XXS;
+    if (fast && chunked && a.nx <= 16) {
+        // T: chunks per activation tile, a multiple of 4, within the tile
+        // budget (4 for 8 or more columns); R: rows per wave
+        const uint32_t nsb = (a.cols + 255) / 256;
         uint32_t T = std::max(4u, (uint32_t)(FK_XT_BYTES / (a.nx * FK_XPAD * 4)) & ~3u);
         T = std::min(T, std::max(4u, (nsb + 3) & ~3u));          // >= 4 also for rows of no columns
         uint32_t R = std::min(4u, std::max(1u, a.rows / 16384));
-        const size_t smem = 4 * FK_WBUF + (size_t)a.nx * T * FK_XPAD * 4;
+        const size_t smem = 4 * FK_WBUF + fk_grid_bytes(fmt) + (size_t)a.nx * T * FK_XPAD * 4;
         const dim3 gw((uint32_t)((a.rows + 4ull * R - 1) / (4ull * R)));
-        const void * kern = fmt == FMT_Q4_K ? (a.nx == 1 ? (const void *)k_dot_fastk<FMT_Q4_K, 1> : (const void *)k_dot_fastk<FMT_Q4_K, 0>)
-                                            : (a.nx == 1 ? (const void *)k_dot_fastk<FMT_Q6_K, 1> : (const void *)k_dot_fastk<FMT_Q6_K, 0>);
+        const bool one = a.nx == 1;
+        const void * kern =
+            fmt == FMT_Q4_K ? (one ? (const void *)k_dot_fastk<FMT_Q4_K, 1> : (const void *)k_dot_fastk<FMT_Q4_K, 0>)
+          : fmt == FMT_Q6_K ? (one ? (const void *)k_dot_fastk<FMT_Q6_K, 1> : (const void *)k_dot_fastk<FMT_Q6_K, 0>)
+          : fmt == FMT_Q5_0 ? (one ? (const void *)k_dot_fastk<FMT_Q5_0, 1> : (const void *)k_dot_fastk<FMT_Q5_0, 0>)
+          : fmt == FMT_IQ2_XXS ? (one ? (const void *)k_dot_fastk<FMT_IQ2_XXS, 1> : (const void *)k_dot_fastk<FMT_IQ2_XXS, 0>)
+          : (one ? (const void *)k_dot_fastk<FMT_IQ3_XXS, 1> : (const void *)k_dot_fastk<FMT_IQ3_XXS, 0>);
         if (int rc = lds_fits(kern, smem, "k_dot_fastk")) return rc;
         void * args[] = {const_cast<DotArgs *>(&a), &R, &T};
         return hip_check(hipLaunchKernel(kern, gw, dim3(256), args, smem, s), "k_dot_fastk launch");

@@ -1,6 +1,7 @@
-"""GPU parity of the fast fp32 order of Q4_K / Q6_K (k_dot_fastk in
-flh_f32.hip; the reference's dot_row_fast_dequant, src/runtime/kernels.h:
-59-104,162-254), the route the reference's GPU masks give Q6_K, and of F32
+"""GPU parity of the fast fp32 order of the 256-element chunk formats (Q4_K,
+Q6_K, Q5_0, IQ2_XXS, IQ3_XXS: k_dot_fastk in flh_f32.hip; the reference's
+dot_row_fast_dequant, src/runtime/kernels.h:59-104,162-254), the route the
+reference's GPU masks give Q6_K and its CPU masks give the IQ formats, and of F32
 weights (k_dot_f32row; dot_row_fast, kernels.h:11-19,58-104), the route of
 every F32 matrix such as an MoE router.
 
@@ -22,11 +23,11 @@ from test_gpu_parity import run_dot, bits, say, dev_cols, I8, I8K
 pytestmark = pytest.mark.gpu
 
 
-def make_cases(n=32, seed=77):
+def make_cases(n=48, seed=77):
     rng = np.random.default_rng(seed)
     cases = []
     for i in range(n):
-        fmt = (Q4_K, Q6_K)[rng.integers(2)]
+        fmt = (Q4_K, Q6_K, Q4_K, Q6_K, Q5_0, IQ2_XXS, IQ3_XXS)[rng.integers(7)]
         rows = int(np.exp(rng.uniform(0, np.log(70000))))
         nsb = int(rng.integers(1, 65))
         nx = 1 if rng.random() < 0.5 else int(rng.integers(2, 17))
@@ -34,8 +35,13 @@ def make_cases(n=32, seed=77):
             rows = max(1, rows // 2)
         pad = int(rng.integers(0, 3))
         idx = rng.random() < 0.2
-        cases.append((i, fmt, rows, 256 * nsb, nx, pad, idx))
-    cases += [(100, Q6_K, 70001, 256, 1, 0, False), (101, Q4_K, 33000, 512, 1, 1, False),
+        cols = 256 * nsb
+        if fmt == Q5_0 and rng.random() < 0.6:              # a last chunk of 1-7 blocks
+            cols = 256 * (nsb - 1) + 32 * int(rng.integers(1, 8))
+        cases.append((i, fmt, rows, cols, nx, pad, idx))
+    cases += [(105, Q5_0, 300, 32, 1, 0, False), (106, Q5_0, 4096, 14336 + 96, 1, 0, False),
+              (107, IQ2_XXS, 4096, 4096, 1, 0, False), (108, IQ3_XXS, 40000, 4096, 2, 1, True),
+              (109, Q5_0, 77, 2816, 16, 2, False), (100, Q6_K, 70001, 256, 1, 0, False), (101, Q4_K, 33000, 512, 1, 1, False),
               (102, Q6_K, 40000, 1280, 3, 0, True), (103, Q6_K, 128, 16384, 1, 0, False),
               (104, Q4_K, 37, 14336, 16, 2, False)]
     return cases
