@@ -592,21 +592,25 @@ __global__ __launch_bounds__(256) void k_dot_fastk(DotArgs a, uint32_t R, uint32
     }
 }
 
-// Fast fp32 order of F32 weights (dot_row_fast, src/runtime/kernels.h:11-19,
-// 58-104: L[j] over the elements k < n16 with k % 16 == j in ascending k,
-// the 16-lane tree, then the tail k >= n16 in order, y += head + tail), the
-// route of every F32 matrix (e.g. an MoE router) under every mask: 16 lanes
-// per row, lane j running L[j]; a wave holds 4 rows, a workgroup 16.  A block
-// is 256 columns (16 elements per lane), its weights loaded as 16 dword loads
-// per lane one block ahead into two register sets used in turn; the
-// activations are staged in LDS by the workgroup in tiles of up to 32 KB
-// (every row of a wave reads the same address: a broadcast).  Elements past
-// n16 are masked out of the chains (their loads read a valid address).
+// Fast fp32 order of F32 and Q8_0 weights (dot_row_fast and
+// dot_row_fast_q8_0, src/runtime/kernels.h:11-19,58-130: L[j] over the
+// elements k < n16 with k % 16 == j in ascending k -- for Q8_0 the product
+// (d q) x of each element -- the 16-lane tree, then for F32 the tail k >= n16
+// in order, y += head + tail): the route of every F32 matrix (e.g. an MoE
+// router) under every mask, and of Q8_0 without its int8 bit.  16 lanes per
+// row, lane j running L[j]; a wave holds 4 rows, a workgroup 16.  A block is
+// 256 columns (16 elements per lane), loaded 2-4 blocks ahead into register
+// sets used in turn (F32: 16 dword loads per lane; Q8_0: 16 byte loads and the
+// 8 block scales); the activations are staged in LDS by the workgroup in
+// tiles of up to 32 KB (every row of a wave reads the same address: a
+// broadcast).  Elements past n16 are masked out of the chains (their loads
+// read a valid address).
 constexpr uint32_t F32R_XT_BYTES = 32768;
 
-template <int NXT>
+template <int FMT, int NXT>
 __global__ __launch_bounds__(256) void k_dot_f32row(DotArgs a, uint32_t T) {
     // NXT: column slots (1, 2, 4, 8, 16; a.nx <= NXT); D: blocks in flight
+    static_assert(FMT == FMT_F32 || FMT == FMT_Q8_0, "F32 / Q8_0");
     constexpr int D = NXT <= 2 ? 4 : 2;
     extern __shared__ __align__(16) uint8_t f32r_smem[];
     float * xs = reinterpret_cast<float *>(f32r_smem);
@@ -614,19 +618,32 @@ __global__ __launch_bounds__(256) void k_dot_f32row(DotArgs a, uint32_t T) {
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     constexpr int NP = NXT;
     const uint32_t nx = NXT == 1 ? 1 : a.nx, cols = a.cols, n16 = cols & ~15u;
+    const uint32_t RB = FMT == FMT_F32 ? cols * 4 : (cols / 32) * 34;          // row bytes
     const uint32_t r = blockIdx.x * 16 + wave * 4 + (lane >> 4);
     const uint32_t rw = min(blockIdx.x * 16 + wave * 4, a.rows - 1);   // the wave's first row (uniform)
-    const float * w0 = reinterpret_cast<const float *>(a.w + (a.id_slot ? (size_t)(*a.id_slot) * a.estride : 0))
-                     + (size_t)rw * cols;
-    const float * wr = w0 + (size_t)(min(r, a.rows - 1) - rw) * cols;
-    const uint32_t roff = (min(r, a.rows - 1) - rw) * cols;      // < 4 rows: 32 bits
-    const auto * wg = (const __attribute__((address_space(1))) float *)w0;
+    const uint8_t * w0 = a.w + (a.id_slot ? (size_t)(*a.id_slot) * a.estride : 0) + (size_t)rw * RB;
+    const uint32_t roff = (min(r, a.rows - 1) - rw) * RB;        // < 4 rows: 32 bits
+    const auto * wg = (const __attribute__((address_space(1))) uint8_t *)w0;
     const uint32_t nblk = (n16 + 255) / 256;                      // blocks of 256 columns
-    using f16v = float __attribute__((ext_vector_type(16)));
-    auto fetch = [&](uint32_t kb, f16v & v) __attribute__((always_inline)) {                     // block min(kb, nblk - 1), clamped reads
+    using u32x16 = uint32_t __attribute__((ext_vector_type(16)));
+    using u32x8 = uint32_t __attribute__((ext_vector_type(8)));
+    struct Blk { u32x16 q; u32x8 d; };                            // F32: q holds the values' bits
+    auto fetch = [&](uint32_t kb, Blk & v) __attribute__((always_inline)) {   // block min(kb, nblk - 1), clamped reads
         const uint32_t c0 = min(kb, nblk - 1) * 256 + j;
+        if constexpr (FMT == FMT_F32) {
 #pragma unroll
-        for (int e = 0; e < 16; ++e) v[e] = wg[roff + min(c0 + 16 * e, cols - 1)];
+            for (int e = 0; e < 16; ++e)
+                v.q[e] = *(const __attribute__((address_space(1))) uint32_t *)(wg + roff + 4 * min(c0 + 16 * e, cols - 1));
+        } else {
+            const uint32_t b0 = min(kb, nblk - 1) * 8, nb = cols / 32;
+#pragma unroll
+            for (int m = 0; m < 8; ++m) {
+                const uint32_t ob = roff + 34 * min(b0 + m, nb - 1);
+                v.d[m] = *(const __attribute__((address_space(1))) uint16_t *)(wg + ob);
+                v.q[2 * m] = wg[ob + 2 + j];
+                v.q[2 * m + 1] = wg[ob + 18 + j];
+            }
+        }
     };
     float L[NP];
 #pragma unroll
@@ -648,9 +665,16 @@ __global__ __launch_bounds__(256) void k_dot_f32row(DotArgs a, uint32_t T) {
         }
         lds_barrier();
     };
-    auto step = [&](uint32_t kb, f16v & v) __attribute__((always_inline)) {
+    auto step = [&](uint32_t kb, Blk & v) __attribute__((always_inline)) {
         if (kb * 256 == nt * T) stage(nt++);
-        const f16v w = v;
+        float w[16];
+        if constexpr (FMT == FMT_F32) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) w[e] = __uint_as_float(v.q[e]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) w[e] = h2f(v.d[e >> 1]) * (float)(int8_t)v.q[e];   // d q
+        }
         fetch(kb + D, v);
         const uint32_t c = kb * 256 - (nt - 1) * T;               // column of the block within its tile
         const bool full = kb * 256 + 256 <= n16;
@@ -670,7 +694,7 @@ __global__ __launch_bounds__(256) void k_dot_f32row(DotArgs a, uint32_t T) {
             L[p] = l;
         }
     };
-    f16v v[D];                                                    // block kb in v[kb % D]
+    Blk v[D];                                                     // block kb in v[kb % D]
     if (nblk > 0) static_for([&](auto ic) { fetch(decltype(ic)::value, v[decltype(ic)::value]); },
                              std::make_integer_sequence<int, D>());
     uint32_t kb = 0;
@@ -689,11 +713,14 @@ __global__ __launch_bounds__(256) void k_dot_f32row(DotArgs a, uint32_t T) {
         const float h2 = t + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(t), 0x101, 0xF, 0xF, true));
         const float head = h2 + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(h2), 0x102, 0xF, 0xF, true));
         if (j == 0) {
-            const float * x = a.x + (size_t)p * a.xstride;
             float tail = 0.f;
-            for (uint32_t k = n16; k < cols; ++k) tail = tail + wr[k] * x[k];
+            if constexpr (FMT == FMT_F32) {                       // Q8_0: cols % 32 == 0, no tail
+                const float * wr = reinterpret_cast<const float *>(w0 + roff);
+                const float * x = a.x + (size_t)p * a.xstride;
+                for (uint32_t k = n16; k < cols; ++k) tail = tail + wr[k] * x[k];
+            }
             float * y = a.y + (size_t)p * a.ystride + r;
-            *y = *y + (head + tail);
+            *y = *y + (FMT == FMT_F32 ? head + tail : head);
         }
     }
 }
@@ -742,15 +769,20 @@ static int launch_f32(bool fast, int fmt, const DotArgs & a, hipStream_t s) {
         void * args[] = {const_cast<DotArgs *>(&a), &R, &T};
         return hip_check(hipLaunchKernel(kern, gw, dim3(256), args, smem, s), "k_dot_fastk launch");
     }
-    if (fast && fmt == FMT_F32 && a.nx <= 16) {
+    if (fast && (fmt == FMT_F32 || fmt == FMT_Q8_0) && a.nx <= 16) {
         // T: columns per activation tile, a multiple of 256 within the budget
         uint32_t T = std::max(256u, (uint32_t)(F32R_XT_BYTES / (4 * a.nx)) & ~255u);
         T = std::min(T, std::max(256u, ((a.cols & ~15u) + 255) & ~255u));
         const size_t smem = (size_t)a.nx * T * 4;
         const dim3 gw((a.rows + 15) / 16);
-        const void * kern = a.nx == 1 ? (const void *)k_dot_f32row<1> : a.nx == 2 ? (const void *)k_dot_f32row<2>
-                          : a.nx <= 4 ? (const void *)k_dot_f32row<4> : a.nx <= 8 ? (const void *)k_dot_f32row<8>
-                          : (const void *)k_dot_f32row<16>;
+        const uint32_t slots = a.nx == 1 ? 0 : a.nx == 2 ? 1 : a.nx <= 4 ? 2 : a.nx <= 8 ? 3 : 4;
+        static const void * const kf32[5] = {(const void *)k_dot_f32row<FMT_F32, 1>, (const void *)k_dot_f32row<FMT_F32, 2>,
+                                             (const void *)k_dot_f32row<FMT_F32, 4>, (const void *)k_dot_f32row<FMT_F32, 8>,
+                                             (const void *)k_dot_f32row<FMT_F32, 16>};
+        static const void * const kq8[5] = {(const void *)k_dot_f32row<FMT_Q8_0, 1>, (const void *)k_dot_f32row<FMT_Q8_0, 2>,
+                                            (const void *)k_dot_f32row<FMT_Q8_0, 4>, (const void *)k_dot_f32row<FMT_Q8_0, 8>,
+                                            (const void *)k_dot_f32row<FMT_Q8_0, 16>};
+        const void * kern = fmt == FMT_F32 ? kf32[slots] : kq8[slots];
         if (int rc = lds_fits(kern, smem, "k_dot_f32row")) return rc;
         void * args[] = {const_cast<DotArgs *>(&a), &T};
         return hip_check(hipLaunchKernel(kern, gw, dim3(256), args, smem, s), "k_dot_f32row launch");

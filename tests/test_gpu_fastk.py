@@ -2,8 +2,9 @@
 Q6_K, Q5_0, IQ2_XXS, IQ3_XXS: k_dot_fastk in flh_f32.hip; the reference's
 dot_row_fast_dequant, src/runtime/kernels.h:59-104,162-254), the route the
 reference's GPU masks give Q6_K and its CPU masks give the IQ formats, and of F32
-weights (k_dot_f32row; dot_row_fast, kernels.h:11-19,58-104), the route of
-every F32 matrix such as an MoE router.
+and Q8_0 weights (k_dot_f32row; dot_row_fast / dot_row_fast_q8_0,
+kernels.h:11-19,58-130), the route of every F32 matrix such as an MoE
+router.
 
 Bar: bitwise against the oracle.  Seeded random cases cover what the
 kernel's plan varies with: rows per wave (1 to 4: up to 70000 rows, with a
@@ -66,29 +67,39 @@ def test_fastk_random_bitwise(flh, orc, gpu, i, fmt, rows, cols, nx, pad, idx):
 
 
 def make_f32_cases(n=28, seed=91):
-    """F32: columns of every kind (below 16, not a multiple of 16 or 256,
-    several activation tiles), 1-16 columns, padding, the expert-slot form,
-    router shapes (64 x 2048, 8 x 4096, 160 x 5120)."""
+    """F32 and Q8_0 (one chain per lane over the whole row): columns of every
+    kind (F32: below 16, not a multiple of 16 or 256; Q8_0: multiples of 32
+    that end in a partial 256-column block; several activation tiles), 1-16
+    columns, padding, the expert-slot form, router shapes (64 x 2048, 8 x 4096,
+    160 x 5120)."""
     rng = np.random.default_rng(seed)
     colset = [1, 7, 15, 16, 17, 255, 256, 257, 1000, 2048, 4096, 5120, 8191, 9000, 20000]
     cases = []
-    for i in range(n):
+    for i in range(2 * n):
+        fmt = F32 if i < n else Q8_0
         cols = colset[rng.integers(len(colset))]
+        if fmt == Q8_0:
+            cols = max(32, cols // 32 * 32)
         rows = int(np.exp(rng.uniform(0, np.log(3000))))
         nx = 1 if rng.random() < 0.5 else int(rng.integers(2, 17))
         while rows * cols * max(1, nx // 4) > 6_000_000:
             rows = max(1, rows // 2)
-        cases.append((i, rows, cols, nx, int(rng.integers(0, 3)), rng.random() < 0.2))
-    cases += [(100, 64, 2048, 1, 0, False), (101, 8, 4096, 1, 0, True), (102, 160, 5120, 1, 0, False),
-              (103, 64, 2048, 8, 1, False), (104, 17, 40000, 1, 0, False), (105, 33, 5000, 16, 2, False)]
+        cases.append((i, fmt, rows, cols, nx, int(rng.integers(0, 3)), rng.random() < 0.2))
+    cases += [(100, F32, 64, 2048, 1, 0, False), (101, F32, 8, 4096, 1, 0, True), (102, F32, 160, 5120, 1, 0, False),
+              (103, F32, 64, 2048, 8, 1, False), (104, F32, 17, 40000, 1, 0, False), (105, F32, 33, 5000, 16, 2, False),
+              (106, Q8_0, 4096, 4096, 1, 0, False), (107, Q8_0, 300, 14336, 3, 1, True), (108, Q8_0, 5, 32, 16, 0, False)]
     return cases
 
 
-@pytest.mark.parametrize("i,rows,cols,nx,pad,idx", make_f32_cases())
-def test_f32_fast_random_bitwise(flh, orc, gpu, i, rows, cols, nx, pad, idx):
-    say("f32 fast", i, rows, cols, nx, pad, idx)
+@pytest.mark.parametrize("i,fmt,rows,cols,nx,pad,idx", make_f32_cases())
+def test_f32_q8_0_fast_random_bitwise(flh, orc, gpu, i, fmt, rows, cols, nx, pad, idx):
+    say("f32/q8_0 fast", i, fmt, rows, cols, nx, pad, idx)
     rng = np.random.default_rng(900 + i)
-    w = normal_weights(rows, cols, rng, std=0.5).view(np.uint8).reshape(-1)
+    def weights():
+        if fmt == F32:
+            return normal_weights(rows, cols, rng, std=0.5).view(np.uint8).reshape(-1)
+        return sane_rows(fmt, rows, cols, rng)
+    w = weights()
     ys = rows + pad
     y0 = rng.standard_normal((nx - 1) * ys + rows).astype(np.float32)
     xs = activations(nx, cols, rng, outliers=True)
@@ -98,14 +109,14 @@ def test_f32_fast_random_bitwise(flh, orc, gpu, i, rows, cols, nx, pad, idx):
     e, estride, ww = None, 0, w
     if idx:
         e, estride = 1, w.size
-        ww = np.concatenate([normal_weights(rows, cols, rng).view(np.uint8).reshape(-1), w])
+        ww = np.concatenate([weights(), w])
     dw = flh.DeviceBuffer.from_array(ww, gpu)
     slot = None if e is None else flh.DeviceBuffer.from_array(np.array([e], dtype=np.uint32), gpu)
-    flh.stream_dot(F32, dw, rows, cols, dx, dy, gpu, nx=nx, xstride=st, ystride=ys, id_slot=slot,
+    flh.stream_dot(fmt, dw, rows, cols, dx, dy, gpu, nx=nx, xstride=st, ystride=ys, id_slot=slot,
                    estride=estride, fast=True, i8_mask=0, i8k_mask=0)
     got = dy.download(np.float32, y0.size, gpu)
     want = y0.copy()
-    orc.stream_dot(F32, ww, rows, cols, hx, want, nx=nx, xstride=st, ystride=ys, fast=True, i8_mask=0,
+    orc.stream_dot(fmt, ww, rows, cols, hx, want, nx=nx, xstride=st, ystride=ys, fast=True, i8_mask=0,
                    i8k_mask=0, id_slot=e, estride=estride, threads=8)
     assert np.array_equal(bits(got), bits(want))
 
