@@ -7,10 +7,10 @@
 //    correctness mode, not a throughput path.
 //  * fast fp32 (fast = 1, format not routed to an int8 path): the
 //    reference's fixed 16-lane order (src/runtime/kernels.h:11-19):
-//    dot_row_fast / dot_row_fast_q8_0 / dot_row_fast_dequant, bitwise; Q4_K
-//    and Q6_K (the reference GPU masks' Q6_K route) on one wave per row
-//    (k_dot_fastk), F32 weights (e.g. an MoE router) on 16 lanes per row
-//    (k_dot_f32row), the other formats one thread per (row, column).
+//    dot_row_fast / dot_row_fast_q8_0 / dot_row_fast_dequant, bitwise: the
+//    256-element chunk formats (Q4_K, Q6_K -- the reference GPU masks' Q6_K
+//    route --, Q5_0, IQ2_XXS, IQ3_XXS) on one wave per row (k_dot_fastk),
+//    F32 (e.g. an MoE router) and Q8_0 on 16 lanes per row (k_dot_f32row).
 //  * ROUTER_SEL / SILU_MUL / WMERGE / MERGE: the reference's single-thread
 //    canonical ops (src/runtime/decode_params.h:234-295,
 //    runtime_internal.h:274-281), one thread per token / element.  expf is
@@ -36,53 +36,6 @@ __device__ __forceinline__ int q5v(const uint8_t * b, uint32_t qh, int j) {
 }
 __device__ __forceinline__ uint32_t q5qh(const uint8_t * b) {
     return b[2] | (b[3] << 8) | (b[4] << 16) | ((uint32_t)b[5] << 24);
-}
-
-__device__ void dq_block(int fmt, const uint8_t * b, float * o) {
-    // value formulas of dequant_chunk (src/runtime/kernels.h:169-240); IQ
-    // formats: db * (+-v), the factors of the canonical IQ dots
-    if (fmt == FMT_IQ2_XXS || fmt == FMT_IQ3_XXS) {
-        for (int ib = 0; ib < 8; ++ib) {
-            const uint32_t w1 = iq_w1(fmt, b, ib);
-            const float db = iq_db(fmt, h2f(ld16u(b)), w1);
-            for (int e = 0; e < 32; ++e) o[32 * ib + e] = db * (float)iq_val(fmt, b, ib, w1, e);
-        }
-    } else if (fmt == FMT_Q5_0) {                 // one 32-element block
-        const float d = h2f(ld16u(b));
-        const uint32_t qh = q5qh(b);
-        for (int j = 0; j < 32; ++j) o[j] = d * (float)q5v(b, qh, j);
-    } else if (fmt == FMT_Q8_0) {
-        const float d = h2f(ld16u(b));
-        for (int j = 0; j < 32; ++j) o[j] = d * (float)(int8_t)b[2 + j];
-    } else if (fmt == FMT_Q4_K) {
-        const float d = h2f(ld16u(b)), dmin = h2f(ld16u(b + 2));
-        const uint8_t * s = b + 4;
-        for (int c = 0; c < 4; ++c) {
-            uint32_t sc[2], mn[2];
-            for (int t = 0; t < 2; ++t) {
-                const int g = 2 * c + t;
-                if (g < 4) { sc[t] = s[g] & 63; mn[t] = s[g + 4] & 63; }
-                else { sc[t] = (s[g + 4] & 0xF) | ((s[g - 4] >> 6) << 4);
-                       mn[t] = (s[g + 4] >> 4) | ((s[g] >> 6) << 4); }
-            }
-            const float d1 = d * (float)sc[0], m1 = dmin * (float)mn[0];
-            const float d2 = d * (float)sc[1], m2 = dmin * (float)mn[1];
-            const uint8_t * q = b + 16 + 32 * c;
-            for (int l = 0; l < 32; ++l) o[64 * c + l] = d1 * (float)(q[l] & 0xF) - m1;
-            for (int l = 0; l < 32; ++l) o[64 * c + 32 + l] = d2 * (float)(q[l] >> 4) - m2;
-        }
-    } else {
-        const float d = h2f(ld16u(b + 208));
-        const int8_t * sc = (const int8_t *)(b + 192);
-        for (int h = 0; h < 2; ++h)
-            for (int g = 0; g < 4; ++g)
-                for (int l = 0; l < 32; ++l) {
-                    const uint8_t lb = b[64 * h + l + 32 * (g & 1)];
-                    const int q6 = ((g < 2) ? (lb & 0xF) : (lb >> 4)) |
-                                   (((b[128 + 32 * h + l] >> (2 * g)) & 3) << 4);
-                    o[128 * h + 32 * g + l] = d * (float)sc[8 * h + 2 * g + l / 16] * (float)(q6 - 32);
-                }
-    }
 }
 
 __device__ float canon_dot(int fmt, const uint8_t * row, const float * x, uint32_t cols) {
@@ -170,55 +123,6 @@ __device__ float canon_dot(int fmt, const uint8_t * row, const float * x, uint32
     return acc;
 }
 
-__device__ float tree16(const float * L) {
-    float s[4];
-    for (int j = 0; j < 4; ++j) s[j] = (L[j] + L[4 + j]) + (L[8 + j] + L[12 + j]);
-    return (s[0] + s[1]) + (s[2] + s[3]);
-}
-
-__device__ float fast_dot(int fmt, const uint8_t * row, const float * x, uint32_t cols) {
-    if (fmt == FMT_F32) {
-        const float * r = (const float *)row;
-        const uint32_t n16 = cols & ~15u;
-        float L[16] = {0};
-        for (uint32_t k = 0; k < n16; k += 16)
-            for (int j = 0; j < 16; ++j) L[j] += r[k + j] * x[k + j];
-        const float head = tree16(L);
-        float tail = 0.f;
-        for (uint32_t k = n16; k < cols; ++k) tail += r[k] * x[k];
-        return head + tail;
-    }
-    if (fmt == FMT_Q8_0) {
-        float L[16] = {0};
-        for (uint32_t b = 0; b < cols / 32; ++b) {
-            const uint8_t * B = row + (size_t)b * 34;
-            const float d = h2f(ld16u(B));
-            for (int g = 0; g < 8; ++g)
-                for (int j = 0; j < 4; ++j)
-                    L[(g & 3) * 4 + j] += d * (float)(int8_t)B[2 + 4 * g + j] * x[b * 32 + 4 * g + j];
-        }
-        return tree16(L);
-    }
-    // dot_row_fast_dequant (src/runtime/kernels.h:244-254): 256-element chunks
-    // (the last one shorter for Q5_0), each dequantised then dotted in the
-    // 16-lane order; chunk sums chained in order
-    float acc = 0.f, buf[256];
-    for (uint32_t e = 0; e < cols; e += 256) {
-        const uint32_t n = cols - e < 256 ? cols - e : 256;
-        if (fmt == FMT_Q5_0) {
-            for (uint32_t b = 0; b < n / 32; ++b) dq_block(fmt, row + (size_t)(e / 32 + b) * 22, buf + 32 * b);
-        } else {
-            const uint32_t bb = fmt == FMT_Q4_K ? 144 : fmt == FMT_Q6_K ? 210 : iq_block_bytes(fmt);
-            dq_block(fmt, row + (size_t)(e / 256) * bb, buf);
-        }
-        float L[16] = {0};
-        for (uint32_t k = 0; k < n; k += 16)
-            for (int j = 0; j < 16; ++j) L[j] += buf[k + j] * x[e + k + j];
-        acc += tree16(L);
-    }
-    return acc;
-}
-
 // K formats on the q8_1 int8 path (i8 mask bit set, i8k bit clear):
 // fl_dot_i8_q4_K / fl_dot_i8_q6_K (src/runtime/quants.h:468-526), exact
 // integer group sums, two (Q4_K) or per-16 (Q6_K) fmaf terms per 32-element
@@ -301,8 +205,8 @@ int launch_dot_i8_k(int fmt, const DotArgs & a, hipStream_t s) {
 // row and all of its columns: a chunk on 16 lanes, lane j owning elements
 // j + 16 k (k = 0..15, so that its partial sum is the reference's L[j]),
 // four chunks per pass; the value of each element is computed as
-// dequant_chunk does (Q4_K: (d sc) q - (dmin m); Q6_K: (d sc) (q - 32)), and
-// every product and sum rounds on its own.  Bitwise equal to fast_dot.
+// dequant_chunk does (Q4_K: (d sc) q - (dmin m); Q6_K: (d sc) (q - 32); Q5_0:
+// d (q - 16); IQ: db (+-v)), and every product and sum rounds on its own.
 //
 // Memory plan: the four superblocks of a pass arrive as one 16-byte load per
 // lane (the aligned 16-byte segments that cover them; a segment holding one
@@ -725,8 +629,7 @@ __global__ __launch_bounds__(256) void k_dot_f32row(DotArgs a, uint32_t T) {
     }
 }
 
-template <bool FAST>
-__global__ void k_dot_f32(int fmt, DotArgs a) {
+__global__ void k_dot_canon(int fmt, DotArgs a) {
     const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= (uint64_t)a.rows * a.nx) return;
     const uint32_t r = (uint32_t)(t % a.rows), p = (uint32_t)(t / a.rows);
@@ -737,7 +640,7 @@ __global__ void k_dot_f32(int fmt, DotArgs a) {
                       : (uint64_t)(a.cols / 256) * (fmt == FMT_Q4_K ? 144 : fmt == FMT_Q6_K ? 210
                                                    : iq_block_bytes(fmt));
     const float * x = a.x + (size_t)p * a.xstride;
-    const float v = FAST ? fast_dot(fmt, w + r * rb, x, a.cols) : canon_dot(fmt, w + r * rb, x, a.cols);
+    const float v = canon_dot(fmt, w + r * rb, x, a.cols);
     float * y = a.y + (size_t)p * a.ystride + r;
     *y = *y + v;
 }
@@ -787,10 +690,9 @@ static int launch_f32(bool fast, int fmt, const DotArgs & a, hipStream_t s) {
         void * args[] = {const_cast<DotArgs *>(&a), &T};
         return hip_check(hipLaunchKernel(kern, gw, dim3(256), args, smem, s), "k_dot_f32row launch");
     }
-    const dim3 g((uint32_t)((n + 63) / 64));
-    if (fast) hipLaunchKernelGGL(k_dot_f32<true>, g, dim3(64), 0, s, fmt, a);
-    else      hipLaunchKernelGGL(k_dot_f32<false>, g, dim3(64), 0, s, fmt, a);
-    return hip_check(hipGetLastError(), "k_dot_f32 launch");
+    if (fast) return set_error(FLH_ERR_UNSUPPORTED, "fast fp32 dot: more than 16 columns");
+    hipLaunchKernelGGL(k_dot_canon, dim3((uint32_t)((n + 63) / 64)), dim3(64), 0, s, fmt, a);
+    return hip_check(hipGetLastError(), "k_dot_canon launch");
 }
 int launch_dot_canonical(int fmt, const DotArgs & a, hipStream_t s) { return launch_f32(false, fmt, a, s); }
 int launch_dot_fast_f32(int fmt, const DotArgs & a, hipStream_t s) { return launch_f32(true, fmt, a, s); }
