@@ -511,11 +511,10 @@ __global__ __launch_bounds__(256) void k_dot_fastk(DotArgs a, uint32_t R, uint32
 // read a valid address).
 constexpr uint32_t F32R_XT_BYTES = 32768;
 
-template <int FMT, int NXT>
+template <int FMT, int NXT, int D>
 __global__ __launch_bounds__(256) void k_dot_f32row(DotArgs a, uint32_t T) {
     // NXT: column slots (1, 2, 4, 8, 16; a.nx <= NXT); D: blocks in flight
     static_assert(FMT == FMT_F32 || FMT == FMT_Q8_0, "F32 / Q8_0");
-    constexpr int D = NXT <= 2 ? 4 : 2;
     extern __shared__ __align__(16) uint8_t f32r_smem[];
     float * xs = reinterpret_cast<float *>(f32r_smem);
     const uint32_t lane = threadIdx.x & 63, j = lane & 15;
@@ -549,9 +548,13 @@ __global__ __launch_bounds__(256) void k_dot_f32row(DotArgs a, uint32_t T) {
             }
         }
     };
-    float L[NP];
+    float L[NP], yv[NP];
 #pragma unroll
-    for (int p = 0; p < NP; ++p) L[p] = 0.f;
+    for (int p = 0; p < NP; ++p) {
+        L[p] = 0.f;
+        // the old y, requested before any weight (only this lane writes it)
+        yv[p] = (uint32_t)p < nx && r < a.rows ? a.y[(size_t)p * a.ystride + r] : 0.f;
+    }
     uint32_t nt = 0;                                              // tiles staged
     auto stage = [&](uint32_t t) __attribute__((always_inline)) {
         if (t > 0) lds_barrier();
@@ -623,8 +626,7 @@ __global__ __launch_bounds__(256) void k_dot_f32row(DotArgs a, uint32_t T) {
                 const float * x = a.x + (size_t)p * a.xstride;
                 for (uint32_t k = n16; k < cols; ++k) tail = tail + wr[k] * x[k];
             }
-            float * y = a.y + (size_t)p * a.ystride + r;
-            *y = *y + (FMT == FMT_F32 ? head + tail : head);
+            a.y[(size_t)p * a.ystride + r] = yv[p] + (FMT == FMT_F32 ? head + tail : head);
         }
     }
 }
@@ -679,12 +681,14 @@ static int launch_f32(bool fast, int fmt, const DotArgs & a, hipStream_t s) {
         const size_t smem = (size_t)a.nx * T * 4;
         const dim3 gw((a.rows + 15) / 16);
         const uint32_t slots = a.nx == 1 ? 0 : a.nx == 2 ? 1 : a.nx <= 4 ? 2 : a.nx <= 8 ? 3 : 4;
-        static const void * const kf32[5] = {(const void *)k_dot_f32row<FMT_F32, 1>, (const void *)k_dot_f32row<FMT_F32, 2>,
-                                             (const void *)k_dot_f32row<FMT_F32, 4>, (const void *)k_dot_f32row<FMT_F32, 8>,
-                                             (const void *)k_dot_f32row<FMT_F32, 16>};
-        static const void * const kq8[5] = {(const void *)k_dot_f32row<FMT_Q8_0, 1>, (const void *)k_dot_f32row<FMT_Q8_0, 2>,
-                                            (const void *)k_dot_f32row<FMT_Q8_0, 4>, (const void *)k_dot_f32row<FMT_Q8_0, 8>,
-                                            (const void *)k_dot_f32row<FMT_Q8_0, 16>};
+        static const void * const kf32[5] = {
+            (const void *)k_dot_f32row<FMT_F32, 1, 4>, (const void *)k_dot_f32row<FMT_F32, 2, 4>,
+            (const void *)k_dot_f32row<FMT_F32, 4, 2>, (const void *)k_dot_f32row<FMT_F32, 8, 2>,
+            (const void *)k_dot_f32row<FMT_F32, 16, 2>};
+        static const void * const kq8[5] = {
+            (const void *)k_dot_f32row<FMT_Q8_0, 1, 4>, (const void *)k_dot_f32row<FMT_Q8_0, 2, 4>,
+            (const void *)k_dot_f32row<FMT_Q8_0, 4, 2>, (const void *)k_dot_f32row<FMT_Q8_0, 8, 2>,
+            (const void *)k_dot_f32row<FMT_Q8_0, 16, 2>};
         const void * kern = fmt == FMT_F32 ? kf32[slots] : kq8[slots];
         if (int rc = lds_fits(kern, smem, "k_dot_f32row")) return rc;
         void * args[] = {const_cast<DotArgs *>(&a), &T};
