@@ -251,7 +251,7 @@ __device__ __forceinline__ void static_for(F && f, std::integer_sequence<int, K.
 
 template <int FMT, int NXT>
 __global__ __launch_bounds__(256) void k_dot_fastk(DotArgs a, uint32_t R, uint32_t T) {
-    // NXT: columns fixed at compile time (1), or 0 for a.nx of 1..16
+    // NXT: column slots (1, 2, 4; a.nx <= NXT)
     static_assert(FMT == FMT_Q4_K || FMT == FMT_Q6_K || FMT == FMT_Q5_0 || FMT == FMT_IQ2_XXS ||
                   FMT == FMT_IQ3_XXS, "formats of the 256-element chunk order");
     extern __shared__ __align__(16) uint8_t fk_smem[];
@@ -260,10 +260,10 @@ __global__ __launch_bounds__(256) void k_dot_fastk(DotArgs a, uint32_t R, uint32
     const uint32_t j = lane & 15, cq = lane >> 4;
     constexpr uint32_t BB = fk_chunk_bytes(FMT);                  // bytes of a 256-element chunk
     constexpr uint32_t GB = fk_grid_bytes(FMT);                   // IQ codebook staged in LDS
-    const uint32_t cols = a.cols, nsb = (cols + 255) >> 8, nx = NXT ? NXT : a.nx;
+    const uint32_t cols = a.cols, nsb = (cols + 255) >> 8, nx = NXT == 1 ? 1 : a.nx;
     // row bytes (Q5_0: the last chunk holds cols % 256 / 32 blocks)
     const uint32_t RB = FMT == FMT_Q5_0 ? (cols / 32) * 22 : nsb * BB;
-    constexpr int NP = NXT ? NXT : 16;                            // column slots
+    constexpr int NP = NXT;                                       // column slots
     uint8_t * gl = fk_smem + 4 * FK_WBUF;                         // codebook (IQ)
     float * xs = reinterpret_cast<float *>(fk_smem + 4 * FK_WBUF + GB);
     uint8_t * wb = fk_smem + wave * FK_WBUF;
@@ -654,7 +654,20 @@ static int launch_f32(bool fast, int fmt, const DotArgs & a, hipStream_t s) {
     if (n == 0) return FLH_OK;
     const bool chunked = fmt == FMT_Q4_K || fmt == FMT_Q6_K || fmt == FMT_Q5_0 || fmt == FMT_IQ2_XXS ||
                          fmt == FMT_IQ3_XXS;
-    if (fast && chunked && a.nx <= 16) {
+    if (fast && chunked && a.nx > 4 && a.nx <= 16) {
+        // more than 4 columns: groups of 4, each its own pass over the weights
+        // (per column the 4-column launch costs least: the activation tiles of
+        // 8 or 16 columns hold 4 chunks, and every tile drains the prefetch)
+        for (uint32_t p0 = 0; p0 < a.nx; p0 += 4) {
+            DotArgs g = a;
+            g.x = a.x + (size_t)p0 * a.xstride;
+            g.y = a.y + (size_t)p0 * a.ystride;
+            g.nx = std::min(4u, a.nx - p0);
+            if (int rc = launch_f32(true, fmt, g, s)) return rc;
+        }
+        return FLH_OK;
+    }
+    if (fast && chunked && a.nx <= 4) {
         // T: chunks per activation tile, a multiple of 4, within the tile
         // budget (4 for 8 or more columns); R: rows per wave
         const uint32_t nsb = (a.cols + 255) / 256;
@@ -663,13 +676,13 @@ static int launch_f32(bool fast, int fmt, const DotArgs & a, hipStream_t s) {
         uint32_t R = std::min(4u, std::max(1u, a.rows / 16384));
         const size_t smem = 4 * FK_WBUF + fk_grid_bytes(fmt) + (size_t)a.nx * T * FK_XPAD * 4;
         const dim3 gw((uint32_t)((a.rows + 4ull * R - 1) / (4ull * R)));
-        const bool one = a.nx == 1;
-        const void * kern =
-            fmt == FMT_Q4_K ? (one ? (const void *)k_dot_fastk<FMT_Q4_K, 1> : (const void *)k_dot_fastk<FMT_Q4_K, 0>)
-          : fmt == FMT_Q6_K ? (one ? (const void *)k_dot_fastk<FMT_Q6_K, 1> : (const void *)k_dot_fastk<FMT_Q6_K, 0>)
-          : fmt == FMT_Q5_0 ? (one ? (const void *)k_dot_fastk<FMT_Q5_0, 1> : (const void *)k_dot_fastk<FMT_Q5_0, 0>)
-          : fmt == FMT_IQ2_XXS ? (one ? (const void *)k_dot_fastk<FMT_IQ2_XXS, 1> : (const void *)k_dot_fastk<FMT_IQ2_XXS, 0>)
-          : (one ? (const void *)k_dot_fastk<FMT_IQ3_XXS, 1> : (const void *)k_dot_fastk<FMT_IQ3_XXS, 0>);
+        const uint32_t slots = a.nx == 1 ? 0 : a.nx == 2 ? 1 : 2;
+#define FLH_FK_ROW(F) {(const void *)k_dot_fastk<F, 1>, (const void *)k_dot_fastk<F, 2>, (const void *)k_dot_fastk<F, 4>}
+        static const void * const kfk[5][3] = {FLH_FK_ROW(FMT_Q4_K), FLH_FK_ROW(FMT_Q6_K), FLH_FK_ROW(FMT_Q5_0),
+                                               FLH_FK_ROW(FMT_IQ2_XXS), FLH_FK_ROW(FMT_IQ3_XXS)};
+#undef FLH_FK_ROW
+        const int fi = fmt == FMT_Q4_K ? 0 : fmt == FMT_Q6_K ? 1 : fmt == FMT_Q5_0 ? 2 : fmt == FMT_IQ2_XXS ? 3 : 4;
+        const void * kern = kfk[fi][slots];
         if (int rc = lds_fits(kern, smem, "k_dot_fastk")) return rc;
         void * args[] = {const_cast<DotArgs *>(&a), &R, &T};
         return hip_check(hipLaunchKernel(kern, gw, dim3(256), args, smem, s), "k_dot_fastk launch");
