@@ -207,7 +207,8 @@ int flh_act_q8(float * x, void * y_q81, uint32_t cols, uint32_t nx,
  * fast = 0: canonical fp32 dequant-dot (fl_dot_row_any order, bitwise);
  * fast = 1: q8_K path for K formats whose bit is in i8k_mask, else q8_1
  * path for formats in i8_mask, else the "fast" fp32 dequant order
- * (dot_row_fast_dequant / dot_row_fast_q8_0), exactly as exec_task_cpu.
+ * (dot_row_fast / dot_row_fast_q8_0 / dot_row_fast_dequant; F32 weights
+ * always), exactly as exec_task_cpu.  cols = 0: every row's dot is 0.
  * int8 paths read the appendices written by flh_act_q8. */
 int flh_stream_dot(int fmt, const void * w, uint64_t w_bytes, uint32_t rows,
                    uint32_t cols, const float * x, float * y, uint32_t nx,
@@ -258,8 +259,9 @@ int flh_rmsnorm_stream_dot(int fmt, const void * w, uint64_t w_bytes, uint32_t r
  * point (the same dot gives the same bits through any of them): pass the
  * reference's CPU masks (flh_default_masks) for the int8 parity path.  With
  * the reference's GPU defaults (kI8MaskGpuDefault / kI8KMaskGpuDefault,
- * src/runtime/kernels.h:927-940) Q6_K takes the fp32 dequant route, one
- * thread per row: a correctness mode, not a throughput path.
+ * src/runtime/kernels.h:927-940) Q6_K takes the fp32 dequant route (the
+ * same order on one wave per row, about 2x the int8 route's time at the
+ * vocab head); with the CPU masks IQ2_XXS / IQ3_XXS take it.
  * The param blocks that RMSNORM, ROUTER_SEL, SILU_MUL and WMERGE tasks point
  * to through aux are read by the host when the table is issued, so they must
  * be host-readable (host, pinned or managed memory; flh_host_alloc gives
