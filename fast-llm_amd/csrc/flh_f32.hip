@@ -513,7 +513,7 @@ constexpr uint32_t F32R_XT_BYTES = 32768;
 
 template <int FMT, int NXT, int D>
 __global__ __launch_bounds__(256) void k_dot_f32row(DotArgs a, uint32_t T) {
-    // NXT: column slots (1, 2, 4, 8, 16; a.nx <= NXT); D: blocks in flight
+    // NXT: column slots (1, 2, 4; a.nx <= NXT); D: blocks in flight
     static_assert(FMT == FMT_F32 || FMT == FMT_Q8_0, "F32 / Q8_0");
     extern __shared__ __align__(16) uint8_t f32r_smem[];
     float * xs = reinterpret_cast<float *>(f32r_smem);
@@ -654,10 +654,10 @@ static int launch_f32(bool fast, int fmt, const DotArgs & a, hipStream_t s) {
     if (n == 0) return FLH_OK;
     const bool chunked = fmt == FMT_Q4_K || fmt == FMT_Q6_K || fmt == FMT_Q5_0 || fmt == FMT_IQ2_XXS ||
                          fmt == FMT_IQ3_XXS;
-    if (fast && chunked && a.nx > 4 && a.nx <= 16) {
+    if (fast && (chunked || fmt == FMT_F32 || fmt == FMT_Q8_0) && a.nx > 4 && a.nx <= 16) {
         // more than 4 columns: groups of 4, each its own pass over the weights
         // (per column the 4-column launch costs least: the activation tiles of
-        // 8 or 16 columns hold 4 chunks, and every tile drains the prefetch)
+        // 8 or 16 columns are short, and every tile drains the prefetch)
         for (uint32_t p0 = 0; p0 < a.nx; p0 += 4) {
             DotArgs g = a;
             g.x = a.x + (size_t)p0 * a.xstride;
@@ -687,21 +687,19 @@ static int launch_f32(bool fast, int fmt, const DotArgs & a, hipStream_t s) {
         void * args[] = {const_cast<DotArgs *>(&a), &R, &T};
         return hip_check(hipLaunchKernel(kern, gw, dim3(256), args, smem, s), "k_dot_fastk launch");
     }
-    if (fast && (fmt == FMT_F32 || fmt == FMT_Q8_0) && a.nx <= 16) {
+    if (fast && (fmt == FMT_F32 || fmt == FMT_Q8_0) && a.nx <= 4) {
         // T: columns per activation tile, a multiple of 256 within the budget
         uint32_t T = std::max(256u, (uint32_t)(F32R_XT_BYTES / (4 * a.nx)) & ~255u);
         T = std::min(T, std::max(256u, ((a.cols & ~15u) + 255) & ~255u));
         const size_t smem = (size_t)a.nx * T * 4;
         const dim3 gw((a.rows + 15) / 16);
-        const uint32_t slots = a.nx == 1 ? 0 : a.nx == 2 ? 1 : a.nx <= 4 ? 2 : a.nx <= 8 ? 3 : 4;
-        static const void * const kf32[5] = {
+        const uint32_t slots = a.nx == 1 ? 0 : a.nx == 2 ? 1 : 2;
+        static const void * const kf32[3] = {
             (const void *)k_dot_f32row<FMT_F32, 1, 4>, (const void *)k_dot_f32row<FMT_F32, 2, 4>,
-            (const void *)k_dot_f32row<FMT_F32, 4, 2>, (const void *)k_dot_f32row<FMT_F32, 8, 2>,
-            (const void *)k_dot_f32row<FMT_F32, 16, 2>};
-        static const void * const kq8[5] = {
+            (const void *)k_dot_f32row<FMT_F32, 4, 2>};
+        static const void * const kq8[3] = {
             (const void *)k_dot_f32row<FMT_Q8_0, 1, 4>, (const void *)k_dot_f32row<FMT_Q8_0, 2, 4>,
-            (const void *)k_dot_f32row<FMT_Q8_0, 4, 2>, (const void *)k_dot_f32row<FMT_Q8_0, 8, 2>,
-            (const void *)k_dot_f32row<FMT_Q8_0, 16, 2>};
+            (const void *)k_dot_f32row<FMT_Q8_0, 4, 2>};
         const void * kern = fmt == FMT_F32 ? kf32[slots] : kq8[slots];
         if (int rc = lds_fits(kern, smem, "k_dot_f32row")) return rc;
         void * args[] = {const_cast<DotArgs *>(&a), &T};
