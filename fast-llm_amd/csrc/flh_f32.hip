@@ -688,6 +688,9 @@ static int launch_f32(bool fast, int fmt, const DotArgs & a, hipStream_t s) {
         return hip_check(hipLaunchKernel(kern, gw, dim3(256), args, smem, s), "k_dot_fastk launch");
     }
     if (fast && (fmt == FMT_F32 || fmt == FMT_Q8_0) && a.nx <= 4) {
+        // the kernel addresses a wave's 4 rows with 32-bit byte offsets
+        if ((uint64_t)a.cols * 4 * 4 >= (1ull << 32))
+            return set_error(FLH_ERR_UNSUPPORTED, "fast fp32 dot: F32 / Q8_0 rows longer than 2^28 columns");
         // T: columns per activation tile, a multiple of 256 within the budget
         uint32_t T = std::max(256u, (uint32_t)(F32R_XT_BYTES / (4 * a.nx)) & ~255u);
         T = std::min(T, std::max(256u, ((a.cols & ~15u) + 255) & ~255u));
