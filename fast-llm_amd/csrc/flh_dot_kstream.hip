@@ -335,17 +335,19 @@ static int ks_launch_d(const DotArgs & a, uint32_t nr, uint32_t grid, size_t smb
 
 // Returns FLH_ERR_UNSUPPORTED (without launching) when the shape does not fit
 // this kernel's LDS plan; the caller then uses the register-resident kernel.
-// LDS plan: at most 64 KiB per workgroup (two workgroups per CU); shrink the
-// batch first, then the ring depth; FLH_ERR_UNSUPPORTED if it cannot fit.
+// LDS plan: at most 64 KiB per workgroup (two workgroups per CU), or `capv`
+// when given (one workgroup per CU: several columns of wide rows, whose
+// activation records alone take 36-73 KB); shrink the batch first, then the
+// ring depth; FLH_ERR_UNSUPPORTED if it cannot fit.
 template <int FMT>
 static int ks_plan(uint32_t rows, uint32_t nx_t, uint32_t nsb, uint32_t slots, int Ddef,
-                   uint32_t & nr, int & D, size_t & smb, int KW = 4) {
+                   uint32_t & nr, int & D, size_t & smb, int KW = 4, size_t capv = 0) {
     const Tune & t = tune();
     nr = t.ks_nr ? t.ks_nr : (rows + slots - 1) / slots;
     if (nr < 1) nr = 1;
     if (nr > 64u / nx_t) nr = 64u / nx_t;
     D = t.ks_D ? (int)t.ks_D : Ddef;
-    const size_t cap = KW == 4 ? 65536 : 81920;                  // two workgroups per CU / one
+    const size_t cap = capv ? capv : KW == 4 ? 65536 : 81920;      // two workgroups per CU / one
     const size_t lim = lds_limit() < cap ? lds_limit() : cap;
     while (ks_smem_bytes<FMT>(nr, nx_t, nsb, D, KW) > lim && nr > 4) nr >>= 1;
     while (ks_smem_bytes<FMT>(nr, nx_t, nsb, D, KW) > lim && D > 2) --D;
@@ -394,11 +396,17 @@ static int ks_launch(const DotArgs & a, hipStream_t s) {
             }
         }
     }
-    const uint32_t slots = (uint32_t)num_cus() * (t.ks_wgs_per_cu ? t.ks_wgs_per_cu : 2);
+    uint32_t slots = (uint32_t)num_cus() * (t.ks_wgs_per_cu ? t.ks_wgs_per_cu : 2);
     uint32_t nr;
     int D;
     size_t smb;
-    if (ks_plan<FMT>(a.rows, NX, nsb, slots, 2, nr, D, smb)) return FLH_ERR_UNSUPPORTED;
+    if (ks_plan<FMT>(a.rows, NX, nsb, slots, 2, nr, D, smb)) {
+        // several columns of wide rows: one workgroup per CU (Q6_K 4096x14336,
+        // 2 / 4 columns: 30.2 / 33.5 us on the register kernel)
+        slots = (uint32_t)num_cus();
+        if (NX == 1 || ks_plan<FMT>(a.rows, NX, nsb, slots, 2, nr, D, smb, 4, lds_limit()))
+            return FLH_ERR_UNSUPPORTED;
+    }
     const uint32_t grid = a.rows < slots ? a.rows : slots;
     switch (D) {
         case 2: return ks_launch_d<FMT, NX, 2, FUSE>(a, nr, grid, smb, s);
@@ -412,6 +420,9 @@ static int moe_launch_x(const MoeArgs & a, uint32_t nr, uint32_t gx, size_t smb,
     if (moe_rows(a) == 0) return FLH_OK;
     if (int rc = lds_fits((const void *)k_moe_kstream<FMT, NX, D, XREG>, smb, "k_moe_kstream: LDS over the limit"))
         return rc;
+    if (smb > 65536)
+        (void)hipFuncSetAttribute((const void *)k_moe_kstream<FMT, NX, D, XREG>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)smb);
     hipLaunchKernelGGL((k_moe_kstream<FMT, NX, D, XREG>), dim3(gx, moe_rows(a)), dim3(256), smb, s, a, nr | (ks_pro(false) << 16));
     return hip_check(hipGetLastError(), "k_moe_kstream launch");
 }
@@ -427,11 +438,14 @@ static int moe_launch(const MoeArgs & a, hipStream_t s) {
     // experts that can be active at once share the chip
     const uint32_t pairs = a.ntok * a.top_k;
     const uint32_t active = pairs < a.n_expert ? pairs : a.n_expert;
-    const uint32_t gx = ((uint32_t)num_cus() * 2 + active - 1) / active;
+    uint32_t gx = ((uint32_t)num_cus() * 2 + active - 1) / active;
     uint32_t nr;
     int D;
     size_t smb;
-    if (ks_plan<FMT>(a.rows, NX, nsb, gx, 2, nr, D, smb)) return FLH_ERR_UNSUPPORTED;
+    if (ks_plan<FMT>(a.rows, NX, nsb, gx, 2, nr, D, smb)) {
+        gx = ((uint32_t)num_cus() + active - 1) / active;        // one workgroup per CU
+        if (NX == 1 || ks_plan<FMT>(a.rows, NX, nsb, gx, 2, nr, D, smb, 4, lds_limit())) return FLH_ERR_UNSUPPORTED;
+    }
     const uint32_t g = a.rows < gx ? a.rows : gx;
     switch (D) {
         case 2: return moe_launch_d<FMT, NX, 2>(a, nr, g, smb, s);
