@@ -652,12 +652,25 @@ int launch_dot_i8k(int fmt, const DotArgs & a0, hipStream_t s) {
             if (rc != FLH_ERR_UNSUPPORTED) return rc;
         }
     }
-    for (uint32_t p0 = 0; p0 < a0.nx; p0 += 4) {
+    for (uint32_t p0 = 0, g = 4; p0 < a0.nx; p0 += g) {
         DotArgs a = a0;
+        int rc = FLH_ERR_UNSUPPORTED;
+        if (fmt == FMT_Q6_K && a0.nx - p0 > 4) {                  // 5-8 columns in one streaming pass
+            a.nx = a0.nx - p0 < 8 ? a0.nx - p0 : 8;
+            a.x = a0.x + (size_t)p0 * a0.xstride;
+            a.y = a0.y + (size_t)p0 * a0.ystride;
+            rc = launch_dot_kstream(fmt, a, s);
+            if (rc != FLH_ERR_UNSUPPORTED) {
+                if (rc) return rc;
+                g = a.nx;
+                continue;
+            }
+        }
+        g = 4;
         a.nx = a0.nx - p0 < 4 ? a0.nx - p0 : 4;
         a.x = a0.x + (size_t)p0 * a0.xstride;
         a.y = a0.y + (size_t)p0 * a0.ystride;
-        int rc = launch_dot_kstream(fmt, a, s);
+        rc = launch_dot_kstream(fmt, a, s);
         if (rc != FLH_ERR_UNSUPPORTED) {
             if (rc) return rc;
             continue;

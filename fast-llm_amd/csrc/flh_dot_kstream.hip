@@ -503,15 +503,19 @@ int launch_moe_kstream(int fmt, const MoeArgs & a, hipStream_t s) {
 template <bool FUSE>
 static int ks_dispatch(int fmt, const DotArgs & a, hipStream_t s) {
     const uint32_t nsb = a.cols >> 8;
-    if (nsb == 0 || (a.cols & 255) || nsb > 64 || a.nx > 4) return FLH_ERR_UNSUPPORTED;
+    if (nsb == 0 || (a.cols & 255) || nsb > 64 || a.nx > (FUSE ? 4u : 8u)) return FLH_ERR_UNSUPPORTED;
     if ((uintptr_t)a.w & 15 || (a.estride & 15)) return FLH_ERR_UNSUPPORTED;
     if (FUSE && (((uintptr_t)a.x & 15) || (a.xstride & 3))) return FLH_ERR_UNSUPPORTED;
     if (fmt == FMT_Q4_K)
         return a.nx == 1 ? ks_launch<FMT_Q4_K, 1, FUSE>(a, s) : a.nx == 2 ? ks_launch<FMT_Q4_K, 2, FUSE>(a, s)
                                                                          : ks_launch<FMT_Q4_K, 4, FUSE>(a, s);
-    if (fmt == FMT_Q6_K)
+    if (fmt == FMT_Q6_K) {
+        if constexpr (!FUSE)       // 5-8 columns in one pass (Q6_K has no matrix-core kernel)
+            if (a.nx > 4) return ks_launch<FMT_Q6_K, 8, false>(a, s);
         return a.nx == 1 ? ks_launch<FMT_Q6_K, 1, FUSE>(a, s) : a.nx == 2 ? ks_launch<FMT_Q6_K, 2, FUSE>(a, s)
                                                                          : ks_launch<FMT_Q6_K, 4, FUSE>(a, s);
+    }
+    if (a.nx > 4) return FLH_ERR_UNSUPPORTED;
     if constexpr (!FUSE) {                    // Q8_0 x q8_1 (ACT_Q8 runs separately)
         if (fmt == FMT_Q8_0)
             return a.nx == 1 ? ks_launch<FMT_Q8_0, 1, false>(a, s) : a.nx == 2 ? ks_launch<FMT_Q8_0, 2, false>(a, s)
