@@ -132,6 +132,11 @@ void load_tune() {
     if (const char * e = getenv("FLH_MFMA_OWN")) t.mf_own = atoi(e) != 0;
     if (const char * e = getenv("FLH_MFMA_MIN_COLS")) t.mf_min_cols = (uint32_t)atoi(e);
     if (const char * e = getenv("FLH_NO_MFMA")) t.no_mfma = atoi(e) != 0;
+    if (const char * e = getenv("FLH_NO_Q6MF")) t.no_q6mf = atoi(e) != 0;
+    if (const char * e = getenv("FLH_Q6MF_MIN")) {
+        unsigned r = 0, c = 0;
+        if (sscanf(e, "%u,%u", &r, &c) == 2) { t.q6mf_rows = r; t.q6mf_cols = c; }
+    }
     if (const char * e = getenv("FLH_SBL_NX_DEP")) t.sbl_nx_dep = (uint32_t)atoi(e);
     if (const char * e = getenv("FLH_GGUF_THREADS")) t.gguf_threads = (uint32_t)strtoul(e, nullptr, 0);
     if (const char * e = getenv("FLH_SBL")) {

@@ -655,6 +655,21 @@ int launch_dot_i8k(int fmt, const DotArgs & a0, hipStream_t s) {
     for (uint32_t p0 = 0, g = 4; p0 < a0.nx; p0 += g) {
         DotArgs a = a0;
         int rc = FLH_ERR_UNSUPPORTED;
+        // 4-8 columns of tall matrices on the matrix cores: one 32-row tile per
+        // wave leaves too few tiles below 64K rows, and at 2-3 columns the
+        // streaming kernel's dot4 path is faster
+        if (fmt == FMT_Q6_K && a0.nx - p0 >= 2 && a0.nx - p0 >= tune().q6mf_cols &&
+            a0.rows >= tune().q6mf_rows && !tune().no_q6mf) {
+            a.nx = a0.nx - p0 < 8 ? a0.nx - p0 : 8;
+            a.x = a0.x + (size_t)p0 * a0.xstride;
+            a.y = a0.y + (size_t)p0 * a0.ystride;
+            rc = launch_dot_q6mf(a, s);
+            if (rc != FLH_ERR_UNSUPPORTED) {
+                if (rc) return rc;
+                g = a.nx;
+                continue;
+            }
+        }
         if (fmt == FMT_Q6_K && a0.nx - p0 > 4) {                  // 5-8 columns in one streaming pass
             a.nx = a0.nx - p0 < 8 ? a0.nx - p0 : 8;
             a.x = a0.x + (size_t)p0 * a0.xstride;

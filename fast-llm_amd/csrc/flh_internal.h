@@ -91,6 +91,8 @@ struct Tune {
     bool mf_own = true;                 // FLH_MFMA_OWN=0: parked terms and a fold pass, not register sums
     uint32_t mf_min_cols = 0;           // FLH_MFMA_MIN_COLS (0: 2 above 4096 columns, else 3)
     bool no_mfma = false;               // FLH_NO_MFMA=1: never the matrix-core kernels
+    bool no_q6mf = false;               // FLH_NO_Q6MF=1: several Q6_K columns off the matrix cores
+    uint32_t q6mf_rows = 65536, q6mf_cols = 4;  // FLH_Q6MF_MIN = "rows,cols": the smallest shape sent there
     // superblock-per-lane single-column kernel, FLH_SBL = "on,waves,wgs_per_cu,max_wgs,pre"
     // (0 = default; max_wgs caps the grid, for tests of long per-wave chunk
     // lists; pre = waves requesting a chunk before the activation lands, 0: half, 255: all)
@@ -140,6 +142,7 @@ int launch_dot_fast_f32(int fmt, const DotArgs & a, hipStream_t s);
 int launch_dequant(int fmt, const uint8_t * w, uint32_t rows, uint32_t cols,
                    float * out, hipStream_t s);
 int launch_moe_i8k(int fmt, const MoeArgs & a, hipStream_t s);
+int launch_dot_q6mf(const DotArgs & a, hipStream_t s);
 // LDS-staged grouped expert kernel; FLH_ERR_UNSUPPORTED if it does not fit
 int launch_moe_kstream(int fmt, const MoeArgs & a, hipStream_t s);
 int launch_moe_sbl(int fmt, const MoeArgs & a, hipStream_t s);

@@ -1,7 +1,7 @@
 """GPU parity of several activation columns over wide rows on the streaming
 kernel (flh_dot_kstream.hip), whose LDS plan for them holds one workgroup
-per CU: Q6_K (its only several-column int8 kernel; 5-8 columns in one pass)
-and Q4_K with the matrix-core kernel switched off.
+per CU: Q6_K (5-8 columns in one pass) and Q4_K, with the matrix-core
+kernels switched off.
 
 Bar: bitwise against the oracle (fl_dot_i8k_q6_K / fl_dot_i8k_q4_K per
 column, src/runtime/quants.h:538-594), with old y and padded output strides:
@@ -32,6 +32,6 @@ def test_kstream_wide_rows_bitwise(flh, orc, gpu, fmt, rows, cols, nx):
     w = sane_rows(fmt, rows, cols, rng)
     xs = activations(nx, cols, rng, outliers=True)
     y0 = rng.standard_normal((nx - 1) * (rows + 1) + rows).astype(np.float32)
-    with tuned(flh, FLH_NO_MFMA=1):
+    with tuned(flh, FLH_NO_MFMA=1, FLH_NO_Q6MF=1):
         got, want = run_dot(flh, orc, gpu, fmt, w, rows, cols, xs, ystride=rows + 1, y0=y0)
     assert np.array_equal(bits(got), bits(want))
