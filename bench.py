@@ -295,6 +295,16 @@ def main():
                               4 if r > 100000 else 16)
             op_entry(f"q6_K_{name}_{r}x{c}_fast_f32", us, nb, {"route": "fast fp32 order (GPU default masks)"})
             cpu_in[f"q6_K_{name}_{r}x{c}"] = host_case(flh, s, Q6_K, ws[0], r, c, x, st, 1)
+            if r > 100000:
+                # a speculative-verify batch through the vocab head: 4 and 8
+                # columns in one weight pass (the Q6_K matrix-core kernel)
+                for n in (4, 8):
+                    xn, stn = B.activation(c, n, 35 + n, outliers=False)
+                    yn = B.buf(n * r * 4)
+                    us = B.time_graph(lambda i: flh.stream_dot(Q6_K, ws[i % len(ws)], r, c, xn, yn, s, nx=n,
+                                                               xstride=stn, ystride=r), 8)
+                    op_entry(f"q6_K_vocab_verify_n{n}_{r}x{c}", us, nb, {"n": n})
+                    del xn, yn
             del ws
         # Q8_0
         r = c = 4096
@@ -434,6 +444,7 @@ PROFILE_OPS["verify8"] = PROFILE_OPS["verify8_14336x4096"]
 for _f, _name in ((Q8_0, "q8_0"), (Q5_0, "q5_0"), (IQ2_XXS, "iq2_xxs"), (IQ3_XXS, "iq3_xxs")):
     for _n in (2, 4, 8):
         PROFILE_OPS[f"{_name}_verify{_n}"] = (_f, 14336, 4096, _n, "dot")
+PROFILE_OPS["q6k_vocab_verify8"] = (Q6_K, 128256, 4096, 8, "dot")
 PROFILE_OPS["q6k_vocab_f32fast"] = (Q6_K, 128256, 4096, 1, "dot_f32fast")
 PROFILE_OPS["q6k_down_f32fast"] = (Q6_K, 4096, 14336, 1, "dot_f32fast")
 PROFILE_OPS["norm_qkv"] = (Q4_K, 6144, 4096, 1, "norm")

@@ -130,7 +130,7 @@ __global__ __launch_bounds__(64 * Q6MF_W) void k_dot_q6mf(DotArgs a, uint32_t nw
             const uintptr_t A = (uintptr_t)(w + (size_t)ra * RB + 210 * (size_t)sb), a0 = A & ~(uintptr_t)15;
             const uint32_t nseg = (uint32_t)((A + 210 - a0 + 15) >> 4);
             if (jj < 7 || lane < 32)                              // positions 480..511 are not in the stage
-                __builtin_amdgcn_global_load_lds(GPTR(a0 + 16 * (uintptr_t)min(seg, nseg - 1)), LPTR(dst + 1024 * jj), 16, 0, 2);
+                __builtin_amdgcn_global_load_lds(GPTR(a0 + 16 * (uintptr_t)min(seg, nseg - 1)), LPTR(dst + 1024 * jj), 16, 0, 0);
         }
     };
     uint32_t fk = 0, fsb = 0;                                     // next item to issue
