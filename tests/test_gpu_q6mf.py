@@ -50,3 +50,19 @@ def test_q6mf_expert_slot(flh, orc, gpu):
     with tuned(flh, FLH_Q6MF_MIN="1,2"):
         got, want = run_dot(flh, orc, gpu, Q6_K, w, rows, cols, xs, id_slot=2, estride=rb)
     assert np.array_equal(bits(got), bits(want))
+
+
+@pytest.mark.parametrize("nx", [4, 8, 11])
+def test_q6mf_default_routing(flh, orc, gpu, nx):
+    """Past the routing floor (64K rows, 4 columns) with the default tuning:
+    a vocab-height matrix, bitwise against the oracle and the streaming kernel."""
+    rows, cols = 65600, 512
+    say("q6mf routed", rows, cols, nx)
+    rng = np.random.default_rng(nx)
+    w = sane_rows(Q6_K, rows, cols, rng)
+    xs = activations(nx, cols, rng, outliers=True)
+    got, want = run_dot(flh, orc, gpu, Q6_K, w, rows, cols, xs)
+    assert np.array_equal(bits(got), bits(want))
+    with tuned(flh, FLH_NO_Q6MF=1):
+        got2, _ = run_dot(flh, orc, gpu, Q6_K, w, rows, cols, xs)
+    assert np.array_equal(bits(got2), bits(got))
