@@ -297,7 +297,8 @@ def main():
             cpu_in[f"q6_K_{name}_{r}x{c}"] = host_case(flh, s, Q6_K, ws[0], r, c, x, st, 1)
             if r > 100000:
                 # a speculative-verify batch through the vocab head: 4 and 8
-                # columns in one weight pass (the Q6_K matrix-core kernel)
+                # columns in one weight pass (4: the streaming kernel, 8: the Q6_K
+                # matrix-core kernel)
                 for n in (4, 8):
                     xn, stn = B.activation(c, n, 35 + n, outliers=False)
                     yn = B.buf(n * r * 4)

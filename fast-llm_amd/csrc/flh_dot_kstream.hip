@@ -510,7 +510,7 @@ static int ks_dispatch(int fmt, const DotArgs & a, hipStream_t s) {
         return a.nx == 1 ? ks_launch<FMT_Q4_K, 1, FUSE>(a, s) : a.nx == 2 ? ks_launch<FMT_Q4_K, 2, FUSE>(a, s)
                                                                          : ks_launch<FMT_Q4_K, 4, FUSE>(a, s);
     if (fmt == FMT_Q6_K) {
-        if constexpr (!FUSE)       // 5-8 columns in one pass (Q6_K has no matrix-core kernel)
+        if constexpr (!FUSE)       // 5-8 columns in one pass (Q6_K below the matrix-core kernel's row floor)
             if (a.nx > 4) return ks_launch<FMT_Q6_K, 8, false>(a, s);
         return a.nx == 1 ? ks_launch<FMT_Q6_K, 1, FUSE>(a, s) : a.nx == 2 ? ks_launch<FMT_Q6_K, 2, FUSE>(a, s)
                                                                          : ks_launch<FMT_Q6_K, 4, FUSE>(a, s);
