@@ -118,19 +118,28 @@ __global__ __launch_bounds__(64 * Q6MF_W) void k_dot_q6mf(DotArgs a, uint32_t nw
     const uint32_t ntw = w0 < T ? (T - w0 + nwt - 1) / nwt : 0;   // tiles of this wave (uniform)
     const uint32_t NI = ntw * nsb;
     // DMA of item (tile k of this wave, superblock sb) into stage st: position
-    // p = 64 j + lane holds segment p % 15 of row p / 15 (p < 480)
+    // p = 64 j + lane holds segment p % 15 of row p / 15 (p < 480).  A row's
+    // 210 bytes start 2-byte aligned, so from the 16-byte boundary below them
+    // they span at most 14 segments (offset <= 14, 14 + 210 <= 224): segment 14
+    // repeats segment 13, and no segment reads past the 16-byte granule that
+    // holds the superblock's last byte.  Per lane the row and the segment
+    // offset of each j are fixed; per item only the tile's row limit moves.
+    uint32_t prow[8], pseg[8];
+#pragma unroll
+    for (uint32_t jj = 0; jj < 8; ++jj) {
+        const uint32_t p = 64 * jj + lane;
+        prow[jj] = p < 480 ? p / 15 : 31;
+        pseg[jj] = p < 480 ? 16 * min(p % 15, 13u) : 0;
+    }
     auto issue = [&](uint32_t k, uint32_t sb, uint32_t st) {
-        const uint32_t r0 = (w0 + k * nwt) * 32;
+        const uint32_t r0 = (w0 + k * nwt) * 32, lim = rows - 1 - r0;   // r0 < rows: tile k exists
+        const uintptr_t base = (uintptr_t)(w + (size_t)r0 * RB + 210 * (size_t)sb);
         uint8_t * dst = ring + (size_t)st * Q6MF_SLOT;
 #pragma unroll
         for (uint32_t jj = 0; jj < 8; ++jj) {
-            const uint32_t p = 64 * jj + lane;
-            const uint32_t row = p < 480 ? p / 15 : 31, seg = p < 480 ? p % 15 : 0;
-            const uint32_t ra = min(r0 + row, rows - 1);
-            const uintptr_t A = (uintptr_t)(w + (size_t)ra * RB + 210 * (size_t)sb), a0 = A & ~(uintptr_t)15;
-            const uint32_t nseg = (uint32_t)((A + 210 - a0 + 15) >> 4);
+            const uintptr_t a0 = (base + __umul24(min(prow[jj], lim), RB)) & ~(uintptr_t)15;
             if (jj < 7 || lane < 32)                              // positions 480..511 are not in the stage
-                __builtin_amdgcn_global_load_lds(GPTR(a0 + 16 * (uintptr_t)min(seg, nseg - 1)), LPTR(dst + 1024 * jj), 16, 0, 0);
+                __builtin_amdgcn_global_load_lds(GPTR(a0 + pseg[jj]), LPTR(dst + 1024 * jj), 16, 0, 0);
         }
     };
     uint32_t fk = 0, fsb = 0;                                     // next item to issue
@@ -237,7 +246,7 @@ __global__ __launch_bounds__(64 * Q6MF_W) void k_dot_q6mf(DotArgs a, uint32_t nw
 // launched) when the shape does not fit the LDS plan.
 int launch_dot_q6mf(const DotArgs & a, hipStream_t s) {
     const uint32_t nsb = a.cols >> 8;
-    if (nsb == 0 || (a.cols & 255) || a.nx < 2 || a.nx > 8 || ((uintptr_t)a.x & 3) || ((uintptr_t)a.w & 1) ||
+    if (nsb == 0 || nsb * 210ull >= (1u << 24) || (a.cols & 255) || a.nx < 2 || a.nx > 8 || ((uintptr_t)a.x & 3) || ((uintptr_t)a.w & 1) ||
         (a.estride & 1))
         return FLH_ERR_UNSUPPORTED;
     if (a.rows == 0) return FLH_OK;
