@@ -655,9 +655,10 @@ int launch_dot_i8k(int fmt, const DotArgs & a0, hipStream_t s) {
     for (uint32_t p0 = 0, g = 4; p0 < a0.nx; p0 += g) {
         DotArgs a = a0;
         int rc = FLH_ERR_UNSUPPORTED;
-        // 5-8 columns of tall matrices on the matrix cores: one 32-row tile per
-        // wave leaves too few tiles below 64K rows, and at 2-4 columns the
-        // streaming kernel is as fast (vocab head, 4 columns: 95 us either way)
+        // 5-8 columns of matrices of 12288 rows or more on the matrix cores
+        // (14336x4096, 8 columns: 26.6 -> 21.8 us; 6144 rows: 14.6 against
+        // 16.8 us, too few tiles); at 2-4 columns the streaming kernel is as
+        // fast or faster
         if (fmt == FMT_Q6_K && a0.nx - p0 >= 2 && a0.nx - p0 >= tune().q6mf_cols &&
             a0.rows >= tune().q6mf_rows && !tune().no_q6mf) {
             a.nx = a0.nx - p0 < 8 ? a0.nx - p0 : 8;

@@ -18,7 +18,11 @@
 // of the tile per ring stage (32 rows x 15 aligned segments; a row's 210
 // bytes start 2-byte aligned, so the lane reads aligned dwords and realigns);
 // each wave owns its ring and runs its own 32-row tiles.  The activation
-// columns' q8_K blocks are staged once per workgroup.
+// columns' q8_K blocks are staged once per workgroup.  With fewer tiles than
+// waves on the chip (SPLIT), four waves share a tile: wave j streams the
+// superblocks sb = j mod 4, which are exactly the reference's chain a[j], and
+// wave 0 of the four adds the four chains through LDS in the reference's
+// (a0 + a1) + (a2 + a3), so the bits are the same either way.
 #include "flh_kstream.h"
 #include "flh_internal.h"
 #include "flh_status.h"
@@ -27,6 +31,7 @@ namespace flh {
 
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+typedef float f4v __attribute__((ext_vector_type(4)));
 
 constexpr uint32_t Q6MF_SLOT = 7680;       // ring stage: 32 rows x 15 segments
 constexpr uint32_t Q6MF_W = 8;             // waves per workgroup
@@ -75,7 +80,7 @@ __device__ __forceinline__ void q6mf_ld_x(uint32_t base, uint32_t dbase, u32x2v 
         : "v"(base), "v"(dbase) : "memory");
 }
 
-template <int NC, int D>
+template <int NC, int D, bool SPLIT>
 __global__ __launch_bounds__(64 * Q6MF_W) void k_dot_q6mf(DotArgs a, uint32_t nwt) {
     static_assert(NC == 4 || NC == 8, "column capacity");
     extern __shared__ __attribute__((aligned(16))) uint8_t q6_sm[];
@@ -114,9 +119,16 @@ __global__ __launch_bounds__(64 * Q6MF_W) void k_dot_q6mf(DotArgs a, uint32_t nw
         __syncthreads();
     }
 
-    const uint32_t T = (rows + 31) / 32, w0 = blockIdx.x * Q6MF_W + wave;
-    const uint32_t ntw = w0 < T ? (T - w0 + nwt - 1) / nwt : 0;   // tiles of this wave (uniform)
-    const uint32_t NI = ntw * nsb;
+    const uint32_t T = (rows + 31) / 32;
+    // tiles: a wave (SPLIT: a quad of waves) takes tiles tb, tb + tstride, ...;
+    // a split wave j streams superblocks j, j + 4, ... of its quad's tile
+    const uint32_t j4 = SPLIT ? (wave & 3) : 0;
+    const uint32_t tb = SPLIT ? blockIdx.x * (Q6MF_W / 4) + (wave >> 2) : blockIdx.x * Q6MF_W + wave;
+    const uint32_t tstride = SPLIT ? nwt / 4 : nwt;
+    const uint32_t sb0 = j4, sstep = SPLIT ? 4 : 1;
+    const uint32_t cnt = SPLIT ? (j4 < nsb ? (nsb - 1 - j4) / 4 + 1 : 0) : nsb;   // superblocks per tile
+    const uint32_t ntw = tb < T ? (T - tb + tstride - 1) / tstride : 0;   // tiles of this wave (uniform)
+    const uint32_t NI = ntw * cnt;
     // DMA of item (tile k of this wave, superblock sb) into stage st: position
     // p = 64 j + lane holds segment p % 15 of row p / 15 (p < 480).  A row's
     // 210 bytes start 2-byte aligned, so from the 16-byte boundary below them
@@ -131,8 +143,9 @@ __global__ __launch_bounds__(64 * Q6MF_W) void k_dot_q6mf(DotArgs a, uint32_t nw
         prow[jj] = p < 480 ? p / 15 : 31;
         pseg[jj] = p < 480 ? 16 * min(p % 15, 13u) : 0;
     }
-    auto issue = [&](uint32_t k, uint32_t sb, uint32_t st) {
-        const uint32_t r0 = (w0 + k * nwt) * 32, lim = rows - 1 - r0;   // r0 < rows: tile k exists
+    auto issue = [&](uint32_t k, uint32_t c, uint32_t st) __attribute__((always_inline)) {
+        const uint32_t r0 = (tb + k * tstride) * 32, lim = rows - 1 - r0;   // r0 < rows: tile k exists
+        const uint32_t sb = sb0 + sstep * c;
         const uintptr_t base = (uintptr_t)(w + (size_t)r0 * RB + 210 * (size_t)sb);
         uint8_t * dst = ring + (size_t)st * Q6MF_SLOT;
 #pragma unroll
@@ -142,101 +155,147 @@ __global__ __launch_bounds__(64 * Q6MF_W) void k_dot_q6mf(DotArgs a, uint32_t nw
                 __builtin_amdgcn_global_load_lds(GPTR(a0 + pseg[jj]), LPTR(dst + 1024 * jj), 16, 0, 0);
         }
     };
-    uint32_t fk = 0, fsb = 0;                                     // next item to issue
-    auto issue_next = [&](uint32_t st) {
-        issue(fk < ntw ? fk : (ntw ? ntw - 1 : 0), fk < ntw ? fsb : 0, st);
-        if (++fsb == nsb) { fsb = 0; ++fk; }
+    uint32_t fk = 0, fc = 0;                                      // next item to issue
+    auto issue_next = [&](uint32_t st) __attribute__((always_inline)) {
+        issue(fk < ntw ? fk : ntw - 1, fk < ntw ? fc : 0, st);
+        if (++fc == cnt) { fc = 0; ++fk; }
     };
-    if (NI == 0) return;                                          // no tile: nothing to stream
+    if (!SPLIT && NI == 0) return;                                // no tile: nothing to stream
+    if (NI != 0) {
 #pragma unroll
-    for (int d = 0; d + 1 < D; ++d) issue_next((uint32_t)d);
+        for (int d = 0; d + 1 < D; ++d) issue_next((uint32_t)d);
+    }
 
     const uint32_t r = lane & 31, h = lane >> 5;
-    float a4[4][4];
+    f4v a4[4];                                                   // [column][accumulator]
     int iacc[4];
-    uint32_t k = 0, sb = 0;
-    for (uint32_t it = 0; it < NI; ++it) {
-        const uint32_t st = it % D;
-        issue_next((it + D - 1) % D);
-        WAIT_VM(8 * (D - 1));
-        if (sb == 0) {
+    uint32_t it = 0;
+    auto item = [&](uint32_t k, uint32_t c) __attribute__((always_inline)) {
+    const uint32_t st = it % D;
+    issue_next((it + D - 1) % D);
+    WAIT_VM(8 * (D - 1));
+    const uint32_t sb = sb0 + sstep * c;
+    const uint32_t r0 = (tb + k * tstride) * 32, ra = min(r0 + r, rows - 1);
+    const uintptr_t A = (uintptr_t)(w + (size_t)ra * RB + 210 * (size_t)sb);
+    const uint32_t sh = (uint32_t)(A & 15);
+    const uint32_t rbase = lds_off(ring + (size_t)st * Q6MF_SLOT) + Q6MF_RSTRIDE * r + (sh & ~3u);
+    u32x2v R[18], S3[3];
+    q6mf_ld_runs(rbase + 8 * h, rbase + 192, R, S3);
+    u32x2v X[16];
+    u32x4a dk;
+    const uint32_t n = lane & 31;
+    const uint32_t xbase = n < NC ? lds_off(xq) + n * XQS + 256 * sb + 8 * h : lds_off(zr);
+    q6mf_ld_x(xbase, lds_off(xd) + 32 * sb + 16 * h, X, dk);
+    const uint32_t s8 = 8 * (sh & 3);
+    uint32_t W[12][2];
 #pragma unroll
-            for (int v = 0; v < 4; ++v)
+    for (int q = 0; q < 12; ++q) {
+        const uint32_t d2 = (q & 1) ? R[12 + (q >> 1)].y : R[12 + (q >> 1)].x;
+        W[q][0] = __builtin_amdgcn_alignbyte(R[q].y, R[q].x, s8 >> 3);
+        W[q][1] = __builtin_amdgcn_alignbyte(d2, R[q].y, s8 >> 3);
+    }
+    const uint32_t s0 = S3[0].x, s1 = S3[0].y, s2 = S3[1].x, s3 = S3[1].y, s4 = S3[2].x, s5 = S3[2].y;
+    const uint32_t SC[4] = {__builtin_amdgcn_alignbyte(s1, s0, s8 >> 3), __builtin_amdgcn_alignbyte(s2, s1, s8 >> 3),
+                            __builtin_amdgcn_alignbyte(s3, s2, s8 >> 3), __builtin_amdgcn_alignbyte(s4, s3, s8 >> 3)};
+    const float dw = h2f(__builtin_amdgcn_alignbyte(s5, s4, s8 >> 3) & 0xFFFFu);
 #pragma unroll
-                for (int q = 0; q < 4; ++q) a4[v][q] = 0.f;
+    for (int v = 0; v < 4; ++v) iacc[v] = 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int hh = i >> 3, s4i = (i >> 1) & 3, b = i & 1;
+        const int q = 4 * hh + 2 * (s4i & 1) + b, qq = 8 + 2 * hh + b;
+        uint32_t Bv[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const uint32_t qlw = W[q][t], qhw = W[qq][t];
+            const uint32_t nib = s4i < 2 ? (qlw & 0x0F0F0F0Fu) : ((qlw >> 4) & 0x0F0F0F0Fu);
+            const uint32_t hb = ((qhw >> (2 * s4i)) & 0x03030303u) << 4;
+            Bv[t] = ((nib | hb) + 0x60606060u) ^ 0x80808080u;  // q - 32 per byte
         }
-        const uint32_t r0 = (w0 + k * nwt) * 32, ra = min(r0 + r, rows - 1);
-        const uintptr_t A = (uintptr_t)(w + (size_t)ra * RB + 210 * (size_t)sb);
-        const uint32_t sh = (uint32_t)(A & 15);
-        const uint32_t rbase = lds_off(ring + (size_t)st * Q6MF_SLOT) + Q6MF_RSTRIDE * r + (sh & ~3u);
-        u32x2v R[18], S3[3];
-        q6mf_ld_runs(rbase + 8 * h, rbase + 192, R, S3);
-        u32x2v X[16];
-        u32x4a dk;
-        const uint32_t n = lane & 31;
-        const uint32_t xbase = n < NC ? lds_off(xq) + n * XQS + 256 * sb + 8 * h : lds_off(zr);
-        q6mf_ld_x(xbase, lds_off(xd) + 32 * sb + 16 * h, X, dk);
-        const uint32_t s8 = 8 * (sh & 3);
-        uint32_t W[12][2];
+        const long av = (long)(((uint64_t)X[i].y << 32) | X[i].x);
+        const long bv = (long)(((uint64_t)Bv[1] << 32) | Bv[0]);
+        const v16i c = {};
+        const v16i dd = __builtin_amdgcn_mfma_i32_32x32x16_i8(av, bv, c, 0, 0, 0);
+        const int sc = (int)(int8_t)((SC[i >> 2] >> (8 * (i & 3))) & 0xFFu);
 #pragma unroll
-        for (int q = 0; q < 12; ++q) {
-            const uint32_t d2 = (q & 1) ? R[12 + (q >> 1)].y : R[12 + (q >> 1)].x;
-            W[q][0] = __builtin_amdgcn_alignbyte(R[q].y, R[q].x, s8 >> 3);
-            W[q][1] = __builtin_amdgcn_alignbyte(d2, R[q].y, s8 >> 3);
-        }
-        const uint32_t s0 = S3[0].x, s1 = S3[0].y, s2 = S3[1].x, s3 = S3[1].y, s4 = S3[2].x, s5 = S3[2].y;
-        const uint32_t SC[4] = {__builtin_amdgcn_alignbyte(s1, s0, s8 >> 3), __builtin_amdgcn_alignbyte(s2, s1, s8 >> 3),
-                                __builtin_amdgcn_alignbyte(s3, s2, s8 >> 3), __builtin_amdgcn_alignbyte(s4, s3, s8 >> 3)};
-        const float dw = h2f(__builtin_amdgcn_alignbyte(s5, s4, s8 >> 3) & 0xFFFFu);
+        for (int v = 0; v < 4; ++v) iacc[v] += __mul24(sc, dd[v]);
+        if (i & 1) __builtin_amdgcn_sched_barrier(0);        // two sub-blocks' results live at a time
+    }
+    // the reference fold: a[sb & 3] = fmaf(d * dk, (float)iacc, a[sb & 3])
+    const float dkv[4] = {__uint_as_float(dk.x), __uint_as_float(dk.y), __uint_as_float(dk.z), __uint_as_float(dk.w)};
+    const uint32_t q3 = SPLIT ? 0 : (sb & 3);            // a split wave runs the chain sb & 3 alone
 #pragma unroll
-        for (int v = 0; v < 4; ++v) iacc[v] = 0;
+    for (int v = 0; v < 4; ++v) {
+        const float m = dw * dkv[v], f = (float)iacc[v];
+        if (q3 == 0) a4[v][0] = fmaf(m, f, a4[v][0]);              // uniform branches: a4 stays in registers
+        else if (q3 == 1) a4[v][1] = fmaf(m, f, a4[v][1]);
+        else if (q3 == 2) a4[v][2] = fmaf(m, f, a4[v][2]);
+        else a4[v][3] = fmaf(m, f, a4[v][3]);
+    }
+        ++it;
+    };
+    auto zero_acc = [&]() __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int hh = i >> 3, s4i = (i >> 1) & 3, b = i & 1;
-            const int q = 4 * hh + 2 * (s4i & 1) + b, qq = 8 + 2 * hh + b;
-            uint32_t Bv[2];
+        for (int v = 0; v < 4; ++v)
 #pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                const uint32_t qlw = W[q][t], qhw = W[qq][t];
-                const uint32_t nib = s4i < 2 ? (qlw & 0x0F0F0F0Fu) : ((qlw >> 4) & 0x0F0F0F0Fu);
-                const uint32_t hb = ((qhw >> (2 * s4i)) & 0x03030303u) << 4;
-                Bv[t] = ((nib | hb) + 0x60606060u) ^ 0x80808080u;  // q - 32 per byte
-            }
-            const long av = (long)(((uint64_t)X[i].y << 32) | X[i].x);
-            const long bv = (long)(((uint64_t)Bv[1] << 32) | Bv[0]);
-            const v16i c = {};
-            const v16i dd = __builtin_amdgcn_mfma_i32_32x32x16_i8(av, bv, c, 0, 0, 0);
-            const int sc = (int)(int8_t)((SC[i >> 2] >> (8 * (i & 3))) & 0xFFu);
+            for (int q = 0; q < 4; ++q) a4[v][q] = 0.f;
+    };
+    // y += (a0 + a1) + (a2 + a3) for the lane's row of tile k and its columns
+    auto store = [&](uint32_t k) __attribute__((always_inline)) {
+        const uint32_t r0 = (tb + k * tstride) * 32;
+        const uint32_t rr = r0 + r;
+        if (rr < rows) {
 #pragma unroll
-            for (int v = 0; v < 4; ++v) iacc[v] += __mul24(sc, dd[v]);
-            if (i & 1) __builtin_amdgcn_sched_barrier(0);        // two sub-blocks' results live at a time
-        }
-        // the reference fold: a[sb & 3] = fmaf(d * dk, (float)iacc, a[sb & 3])
-        const float dkv[4] = {__uint_as_float(dk.x), __uint_as_float(dk.y), __uint_as_float(dk.z), __uint_as_float(dk.w)};
-        const uint32_t q3 = sb & 3;
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const float cur = q3 == 0 ? a4[v][0] : q3 == 1 ? a4[v][1] : q3 == 2 ? a4[v][2] : a4[v][3];
-            const float nv = fmaf(dw * dkv[v], (float)iacc[v], cur);
-            a4[v][0] = q3 == 0 ? nv : a4[v][0];
-            a4[v][1] = q3 == 1 ? nv : a4[v][1];
-            a4[v][2] = q3 == 2 ? nv : a4[v][2];
-            a4[v][3] = q3 == 3 ? nv : a4[v][3];
-        }
-        if (++sb == nsb) {                                        // the tile's rows are done
-            const uint32_t rr = r0 + r;
-            if (rr < rows) {
-#pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    const uint32_t col = 4 * h + v;
-                    if (col < nx) {
-                        float * y = a.y + (size_t)col * a.ystride + rr;
-                        *y = *y + ((a4[v][0] + a4[v][1]) + (a4[v][2] + a4[v][3]));
-                    }
+            for (int v = 0; v < 4; ++v) {
+                const uint32_t col = 4 * h + v;
+                if (col < nx) {
+                    float * y = a.y + (size_t)col * a.ystride + rr;
+                    *y = *y + ((a4[v][0] + a4[v][1]) + (a4[v][2] + a4[v][3]));
                 }
             }
-            sb = 0;
-            ++k;
+        }
+    };
+    if constexpr (!SPLIT) {
+        uint32_t k = 0, c = 0;
+        for (uint32_t i = 0; i < NI; ++i) {
+            if (c == 0) zero_acc();
+            item(k, c);
+            if (++c == cnt) {                                     // the tile's rows are done
+                store(k);
+                c = 0;
+                ++k;
+            }
+        }
+    } else {
+        // every wave of the workgroup runs the same rounds (barriers); the
+        // quad's waves 1-3 leave their chain (4 floats per lane) in the ring
+        // stage their last item used, which their next DMA waits for the
+        // second barrier to overwrite, and wave 0 of the quad folds them in
+        const uint32_t R = (T + tstride - 1) / tstride;
+        uint8_t * quad = q6_sm + (size_t)(wave & ~3u) * D * Q6MF_SLOT;
+        for (uint32_t k = 0; k < R; ++k) {
+            zero_acc();
+            const bool live = k < ntw;
+            if (live)
+                for (uint32_t c = 0; c < cnt; ++c) item(k, c);
+            if (live && j4 != 0 && cnt != 0) {
+                float4 * pp = reinterpret_cast<float4 *>(ring + (size_t)((it - 1) % D) * Q6MF_SLOT) + lane;
+                *pp = make_float4(a4[0][0], a4[1][0], a4[2][0], a4[3][0]);
+            }
+            __syncthreads();
+            if (live && j4 == 0) {
+#pragma unroll
+                for (uint32_t jw = 1; jw < 4; ++jw) {
+                    const uint32_t cw = jw < nsb ? (nsb - 1 - jw) / 4 + 1 : 0;
+                    if (cw != 0) {
+                        const uint32_t stw = ((k + 1) * cw - 1) % D;
+                        const float4 pv = *(reinterpret_cast<const float4 *>(quad + ((size_t)jw * D + stw) * Q6MF_SLOT) + lane);
+                        a4[0][jw] = pv.x; a4[1][jw] = pv.y; a4[2][jw] = pv.z; a4[3][jw] = pv.w;
+                    }
+                }
+                store(k);
+            }
+            __syncthreads();
         }
     }
     WAIT_VM(0);                                                   // the spare DMAs of the last items
@@ -256,8 +315,12 @@ int launch_dot_q6mf(const DotArgs & a, hipStream_t s) {
     const size_t smb = q6mf_smem(NC, D, nsb);
     if (smb > lds_limit()) return FLH_ERR_UNSUPPORTED;
     const uint32_t T = (a.rows + 31) / 32;
+    // fewer tiles than waves on the chip: a quad of waves shares each tile,
+    // one wave per accumulator chain sb & 3
+    const bool split = T < (uint32_t)num_cus() * Q6MF_W;
+    const uint32_t per = split ? Q6MF_W / 4 : Q6MF_W;            // tiles in flight per workgroup
     uint32_t G = (uint32_t)num_cus();
-    if (G > (T + Q6MF_W - 1) / Q6MF_W) G = (T + Q6MF_W - 1) / Q6MF_W;
+    if (G > (T + per - 1) / per) G = (T + per - 1) / per;
     const uint32_t nwt = G * Q6MF_W;
     auto go = [&](auto kern) {
         if (int rc = lds_fits((const void *)kern, smb, "k_dot_q6mf: LDS over the limit")) return rc;
@@ -265,8 +328,12 @@ int launch_dot_q6mf(const DotArgs & a, hipStream_t s) {
         hipLaunchKernelGGL(kern, dim3(G), dim3(64 * Q6MF_W), smb, s, a, nwt);
         return hip_check(hipGetLastError(), "k_dot_q6mf launch");
     };
-    if (NC == 4) return D == 3 ? go(k_dot_q6mf<4, 3>) : go(k_dot_q6mf<4, 2>);
-    return D == 3 ? go(k_dot_q6mf<8, 3>) : go(k_dot_q6mf<8, 2>);
+    if (split) {
+        if (NC == 4) return D == 3 ? go(k_dot_q6mf<4, 3, true>) : go(k_dot_q6mf<4, 2, true>);
+        return D == 3 ? go(k_dot_q6mf<8, 3, true>) : go(k_dot_q6mf<8, 2, true>);
+    }
+    if (NC == 4) return D == 3 ? go(k_dot_q6mf<4, 3, false>) : go(k_dot_q6mf<4, 2, false>);
+    return D == 3 ? go(k_dot_q6mf<8, 3, false>) : go(k_dot_q6mf<8, 2, false>);
 }
 
 }  // namespace flh

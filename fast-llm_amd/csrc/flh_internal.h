@@ -92,7 +92,7 @@ struct Tune {
     uint32_t mf_min_cols = 0;           // FLH_MFMA_MIN_COLS (0: 2 above 4096 columns, else 3)
     bool no_mfma = false;               // FLH_NO_MFMA=1: never the matrix-core kernels
     bool no_q6mf = false;               // FLH_NO_Q6MF=1: several Q6_K columns off the matrix cores
-    uint32_t q6mf_rows = 65536, q6mf_cols = 5;  // FLH_Q6MF_MIN = "rows,cols": the smallest shape sent there
+    uint32_t q6mf_rows = 12288, q6mf_cols = 5;  // FLH_Q6MF_MIN = "rows,cols": the smallest shape sent there
     // superblock-per-lane single-column kernel, FLH_SBL = "on,waves,wgs_per_cu,max_wgs,pre"
     // (0 = default; max_wgs caps the grid, for tests of long per-wave chunk
     // lists; pre = waves requesting a chunk before the activation lands, 0: half, 255: all)

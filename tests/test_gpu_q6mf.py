@@ -52,11 +52,12 @@ def test_q6mf_expert_slot(flh, orc, gpu):
     assert np.array_equal(bits(got), bits(want))
 
 
-@pytest.mark.parametrize("nx", [4, 8, 11])
-def test_q6mf_default_routing(flh, orc, gpu, nx):
-    """Past the routing floor (64K rows, 4 columns) with the default tuning:
-    a vocab-height matrix, bitwise against the oracle and the streaming kernel."""
-    rows, cols = 65600, 512
+@pytest.mark.parametrize("rows,nx", [(65600, 5), (65600, 8), (65600, 11), (14336, 8), (12300, 6)])
+def test_q6mf_default_routing(flh, orc, gpu, rows, nx):
+    """Past the routing floor (12288 rows, 5 columns) with the default tuning:
+    a wave per tile (vocab height) and four waves per tile (fewer tiles than
+    waves on the chip), bitwise against the oracle and the streaming kernel."""
+    cols = 512
     say("q6mf routed", rows, cols, nx)
     rng = np.random.default_rng(nx)
     w = sane_rows(Q6_K, rows, cols, rng)
