@@ -307,6 +307,17 @@ def main():
                     op_entry(f"q6_K_vocab_verify_n{n}_{r}x{c}", us, nb, {"n": n})
                     del xn, yn
             del ws
+        # Q6_K speculative verify at an FFN-up shape: 8 columns, four waves of
+        # the matrix-core kernel per 32-row tile
+        r, c = 14336, 4096
+        nb = r * flh.row_bytes(Q6_K, c)
+        ws = B.weights(Q6_K, r, c, copies_for(nb), seed=78, staging=staging)
+        xn, stn = B.activation(c, 8, 43, outliers=False)
+        yn = B.buf(8 * r * 4)
+        us = B.time_graph(lambda i: flh.stream_dot(Q6_K, ws[i % len(ws)], r, c, xn, yn, s, nx=8, xstride=stn,
+                                                   ystride=r), REPS)
+        op_entry(f"q6_K_verify_n8_{r}x{c}", us, nb, {"n": 8})
+        del ws
         # Q8_0
         r = c = 4096
         nb = r * flh.row_bytes(Q8_0, c)
@@ -446,6 +457,7 @@ for _f, _name in ((Q8_0, "q8_0"), (Q5_0, "q5_0"), (IQ2_XXS, "iq2_xxs"), (IQ3_XXS
     for _n in (2, 4, 8):
         PROFILE_OPS[f"{_name}_verify{_n}"] = (_f, 14336, 4096, _n, "dot")
 PROFILE_OPS["q6k_vocab_verify8"] = (Q6_K, 128256, 4096, 8, "dot")
+PROFILE_OPS["q6k_verify8_14336x4096"] = (Q6_K, 14336, 4096, 8, "dot")
 PROFILE_OPS["q6k_vocab_f32fast"] = (Q6_K, 128256, 4096, 1, "dot_f32fast")
 PROFILE_OPS["q6k_down_f32fast"] = (Q6_K, 4096, 14336, 1, "dot_f32fast")
 PROFILE_OPS["norm_qkv"] = (Q4_K, 6144, 4096, 1, "norm")
