@@ -661,10 +661,14 @@ int launch_dot_i8k(int fmt, const DotArgs & a0, hipStream_t s) {
         // fast or faster
         if (fmt == FMT_Q6_K && a0.nx - p0 >= 2 && a0.nx - p0 >= tune().q6mf_cols &&
             a0.rows >= tune().q6mf_rows && !tune().no_q6mf) {
-            a.nx = a0.nx - p0 < 8 ? a0.nx - p0 : 8;
             a.x = a0.x + (size_t)p0 * a0.xstride;
             a.y = a0.y + (size_t)p0 * a0.ystride;
-            rc = launch_dot_q6mf(a, s);
+            a.nx = a0.nx - p0 < 16 ? a0.nx - p0 : 16;               // 9-16 columns in one pass where it fits
+            rc = a.nx > 8 ? launch_dot_q6mf(a, s) : FLH_ERR_UNSUPPORTED;
+            if (rc == FLH_ERR_UNSUPPORTED) {
+                a.nx = a0.nx - p0 < 8 ? a0.nx - p0 : 8;
+                rc = launch_dot_q6mf(a, s);
+            }
             if (rc != FLH_ERR_UNSUPPORTED) {
                 if (rc) return rc;
                 g = a.nx;

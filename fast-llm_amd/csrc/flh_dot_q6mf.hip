@@ -39,8 +39,8 @@ constexpr uint32_t Q6MF_RSTRIDE = 240;     // LDS bytes per row in a stage
 constexpr uint32_t Q6MF_ZERO = 272;        // zero bytes the A reads of columns >= NC use
 
 __host__ __device__ inline uint32_t q6mf_xqs(uint32_t nsb) { return 256 * nsb + 16; }
-__host__ __device__ inline size_t q6mf_smem(uint32_t NC, uint32_t D, uint32_t nsb) {
-    return (size_t)Q6MF_W * D * Q6MF_SLOT + (size_t)NC * q6mf_xqs(nsb) + Q6MF_ZERO + (size_t)32 * nsb;
+__host__ __device__ inline size_t q6mf_smem(uint32_t NC, uint32_t D, uint32_t nsb, uint32_t W) {
+    return (size_t)W * D * Q6MF_SLOT + (size_t)NC * q6mf_xqs(nsb) + Q6MF_ZERO + (size_t)4 * (NC < 8 ? 8 : NC) * nsb;
 }
 
 // The lane's 12 runs of 8 bytes (ql: 64hh + 32a + 16b + 8h, qh: 128 + 32hh +
@@ -80,24 +80,27 @@ __device__ __forceinline__ void q6mf_ld_x(uint32_t base, uint32_t dbase, u32x2v 
         : "v"(base), "v"(dbase) : "memory");
 }
 
-template <int NC, int D, bool SPLIT>
-__global__ __launch_bounds__(64 * Q6MF_W) void k_dot_q6mf(DotArgs a, uint32_t nwt) {
-    static_assert(NC == 4 || NC == 8, "column capacity");
+template <int NC, int D, bool SPLIT, int NW>
+__global__ __launch_bounds__(64 * NW) void k_dot_q6mf(DotArgs a, uint32_t nwt) {
+    static_assert(NC == 4 || NC == 8 || NC == 16, "column capacity");
+    static_assert(!SPLIT || (NC <= 8 && NW % 4 == 0), "a split workgroup holds whole quads");
+    constexpr int NCX = NC < 8 ? 8 : NC;                          // dk slots per superblock
+    constexpr int NCL = NC == 16 ? 8 : 4;                          // columns per lane
     extern __shared__ __attribute__((aligned(16))) uint8_t q6_sm[];
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t cols = a.cols, nsb = cols >> 8, rows = a.rows, nx = a.nx;
     const uint32_t RB = nsb * 210, XQS = q6mf_xqs(nsb);
     uint8_t * ring = q6_sm + (size_t)wave * D * Q6MF_SLOT;
-    uint8_t * xq = q6_sm + (size_t)Q6MF_W * D * Q6MF_SLOT;
+    uint8_t * xq = q6_sm + (size_t)NW * D * Q6MF_SLOT;
     uint8_t * zr = xq + (size_t)NC * XQS;
-    float * xd = reinterpret_cast<float *>(zr + Q6MF_ZERO);       // [nsb][8]
+    float * xd = reinterpret_cast<float *>(zr + Q6MF_ZERO);       // [nsb][NCX]
     const uint8_t * w = a.w + (a.id_slot ? (size_t)(*a.id_slot) * a.estride : 0);
 
     // activations: the NC columns' int8 values (zero for columns >= nx), dk
     {
         const uint32_t per = nsb * 64;                            // dwords of a column
-        for (uint32_t i = tid; i < NC * per; i += 64 * Q6MF_W) {
+        for (uint32_t i = tid; i < NC * per; i += 64 * NW) {
             const uint32_t n = i / per, q = i - n * per, sb = q >> 6, j = q & 63;
             uint32_t v = 0;
             if (n < nx) {
@@ -106,9 +109,9 @@ __global__ __launch_bounds__(64 * Q6MF_W) void k_dot_q6mf(DotArgs a, uint32_t nw
             }
             *reinterpret_cast<uint32_t *>(xq + (size_t)n * XQS + 256 * sb + 4 * j) = v;
         }
-        for (uint32_t i = tid; i < Q6MF_ZERO / 4; i += 64 * Q6MF_W) reinterpret_cast<uint32_t *>(zr)[i] = 0;
-        for (uint32_t i = tid; i < nsb * 8; i += 64 * Q6MF_W) {
-            const uint32_t sb = i >> 3, n = i & 7;
+        for (uint32_t i = tid; i < Q6MF_ZERO / 4; i += 64 * NW) reinterpret_cast<uint32_t *>(zr)[i] = 0;
+        for (uint32_t i = tid; i < nsb * NCX; i += 64 * NW) {
+            const uint32_t sb = i / NCX, n = i % NCX;
             float v = 0.f;
             if (n < nx) {
                 const uint8_t * app = reinterpret_cast<const uint8_t *>(a.x + (size_t)n * a.xstride) + xqk_off(cols);
@@ -123,7 +126,7 @@ __global__ __launch_bounds__(64 * Q6MF_W) void k_dot_q6mf(DotArgs a, uint32_t nw
     // tiles: a wave (SPLIT: a quad of waves) takes tiles tb, tb + tstride, ...;
     // a split wave j streams superblocks j, j + 4, ... of its quad's tile
     const uint32_t j4 = SPLIT ? (wave & 3) : 0;
-    const uint32_t tb = SPLIT ? blockIdx.x * (Q6MF_W / 4) + (wave >> 2) : blockIdx.x * Q6MF_W + wave;
+    const uint32_t tb = SPLIT ? blockIdx.x * (NW / 4) + (wave >> 2) : blockIdx.x * NW + wave;
     const uint32_t tstride = SPLIT ? nwt / 4 : nwt;
     const uint32_t sb0 = j4, sstep = SPLIT ? 4 : 1;
     const uint32_t cnt = SPLIT ? (j4 < nsb ? (nsb - 1 - j4) / 4 + 1 : 0) : nsb;   // superblocks per tile
@@ -167,8 +170,8 @@ __global__ __launch_bounds__(64 * Q6MF_W) void k_dot_q6mf(DotArgs a, uint32_t nw
     }
 
     const uint32_t r = lane & 31, h = lane >> 5;
-    f4v a4[4];                                                   // [column][accumulator]
-    int iacc[4];
+    f4v a4[NCL];                                                 // [column][accumulator]
+    int iacc[NCL];
     uint32_t it = 0;
     auto item = [&](uint32_t k, uint32_t c) __attribute__((always_inline)) {
     const uint32_t st = it % D;
@@ -185,7 +188,9 @@ __global__ __launch_bounds__(64 * Q6MF_W) void k_dot_q6mf(DotArgs a, uint32_t nw
     u32x4a dk;
     const uint32_t n = lane & 31;
     const uint32_t xbase = n < NC ? lds_off(xq) + n * XQS + 256 * sb + 8 * h : lds_off(zr);
-    q6mf_ld_x(xbase, lds_off(xd) + 32 * sb + 16 * h, X, dk);
+    q6mf_ld_x(xbase, lds_off(xd) + 4 * NCX * sb + 16 * h, X, dk);
+    u32x4a dk2 = dk;
+    if constexpr (NC == 16) dk2 = *reinterpret_cast<const u32x4a *>(xd + NCX * sb + 8 + 4 * h);   // columns 8 + 4h ..
     const uint32_t s8 = 8 * (sh & 3);
     uint32_t W[12][2];
 #pragma unroll
@@ -199,7 +204,7 @@ __global__ __launch_bounds__(64 * Q6MF_W) void k_dot_q6mf(DotArgs a, uint32_t nw
                             __builtin_amdgcn_alignbyte(s3, s2, s8 >> 3), __builtin_amdgcn_alignbyte(s4, s3, s8 >> 3)};
     const float dw = h2f(__builtin_amdgcn_alignbyte(s5, s4, s8 >> 3) & 0xFFFFu);
 #pragma unroll
-    for (int v = 0; v < 4; ++v) iacc[v] = 0;
+    for (int v = 0; v < NCL; ++v) iacc[v] = 0;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
         const int hh = i >> 3, s4i = (i >> 1) & 3, b = i & 1;
@@ -218,14 +223,15 @@ __global__ __launch_bounds__(64 * Q6MF_W) void k_dot_q6mf(DotArgs a, uint32_t nw
         const v16i dd = __builtin_amdgcn_mfma_i32_32x32x16_i8(av, bv, c, 0, 0, 0);
         const int sc = (int)(int8_t)((SC[i >> 2] >> (8 * (i & 3))) & 0xFFu);
 #pragma unroll
-        for (int v = 0; v < 4; ++v) iacc[v] += __mul24(sc, dd[v]);
+        for (int v = 0; v < NCL; ++v) iacc[v] += __mul24(sc, dd[v]);   // D row 4h + v (v < 4), 8 + 4h + v - 4
         if (i & 1) __builtin_amdgcn_sched_barrier(0);        // two sub-blocks' results live at a time
     }
     // the reference fold: a[sb & 3] = fmaf(d * dk, (float)iacc, a[sb & 3])
-    const float dkv[4] = {__uint_as_float(dk.x), __uint_as_float(dk.y), __uint_as_float(dk.z), __uint_as_float(dk.w)};
+    const float dkv[8] = {__uint_as_float(dk.x), __uint_as_float(dk.y), __uint_as_float(dk.z), __uint_as_float(dk.w),
+                          __uint_as_float(dk2.x), __uint_as_float(dk2.y), __uint_as_float(dk2.z), __uint_as_float(dk2.w)};
     const uint32_t q3 = SPLIT ? 0 : (sb & 3);            // a split wave runs the chain sb & 3 alone
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
+    for (int v = 0; v < NCL; ++v) {
         const float m = dw * dkv[v], f = (float)iacc[v];
         if (q3 == 0) a4[v][0] = fmaf(m, f, a4[v][0]);              // uniform branches: a4 stays in registers
         else if (q3 == 1) a4[v][1] = fmaf(m, f, a4[v][1]);
@@ -236,7 +242,7 @@ __global__ __launch_bounds__(64 * Q6MF_W) void k_dot_q6mf(DotArgs a, uint32_t nw
     };
     auto zero_acc = [&]() __attribute__((always_inline)) {
 #pragma unroll
-        for (int v = 0; v < 4; ++v)
+        for (int v = 0; v < NCL; ++v)
 #pragma unroll
             for (int q = 0; q < 4; ++q) a4[v][q] = 0.f;
     };
@@ -246,8 +252,8 @@ __global__ __launch_bounds__(64 * Q6MF_W) void k_dot_q6mf(DotArgs a, uint32_t nw
         const uint32_t rr = r0 + r;
         if (rr < rows) {
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const uint32_t col = 4 * h + v;
+            for (int v = 0; v < NCL; ++v) {
+                const uint32_t col = 4 * h + v + (v >= 4 ? 4 : 0);
                 if (col < nx) {
                     float * y = a.y + (size_t)col * a.ystride + rr;
                     *y = *y + ((a4[v][0] + a4[v][1]) + (a4[v][2] + a4[v][3]));
@@ -301,39 +307,44 @@ __global__ __launch_bounds__(64 * Q6MF_W) void k_dot_q6mf(DotArgs a, uint32_t nw
     WAIT_VM(0);                                                   // the spare DMAs of the last items
 }
 
-// 2..8 Q6_K columns with cols a multiple of 256; FLH_ERR_UNSUPPORTED (nothing
+// 2..16 Q6_K columns with cols a multiple of 256; FLH_ERR_UNSUPPORTED (nothing
 // launched) when the shape does not fit the LDS plan.
 int launch_dot_q6mf(const DotArgs & a, hipStream_t s) {
     const uint32_t nsb = a.cols >> 8;
-    if (nsb == 0 || nsb * 210ull >= (1u << 24) || (a.cols & 255) || a.nx < 2 || a.nx > 8 || ((uintptr_t)a.x & 3) || ((uintptr_t)a.w & 1) ||
-        (a.estride & 1))
+    if (nsb == 0 || nsb * 210ull >= (1u << 24) || (a.cols & 255) || a.nx < 2 || a.nx > 16 || ((uintptr_t)a.x & 3) ||
+        ((uintptr_t)a.w & 1) || (a.estride & 1))
         return FLH_ERR_UNSUPPORTED;
     if (a.rows == 0) return FLH_OK;
-    const uint32_t NC = a.nx <= 4 ? 4 : 8;
+    const uint32_t NC = a.nx <= 4 ? 4 : a.nx <= 8 ? 8 : 16;
+    // 16 columns: 6 waves, so the ring and the 16 columns' activations fit
+    const uint32_t W = NC == 16 ? 6 : Q6MF_W;
     // the deepest ring that fits: 3 superblocks in flight per wave where possible
-    const int D = q6mf_smem(NC, 3, nsb) <= lds_limit() ? 3 : 2;
-    const size_t smb = q6mf_smem(NC, D, nsb);
+    const int D = q6mf_smem(NC, 3, nsb, W) <= lds_limit() ? 3 : 2;
+    const size_t smb = q6mf_smem(NC, D, nsb, W);
     if (smb > lds_limit()) return FLH_ERR_UNSUPPORTED;
     const uint32_t T = (a.rows + 31) / 32;
     // fewer tiles than waves on the chip: a quad of waves shares each tile,
-    // one wave per accumulator chain sb & 3
-    const bool split = T < (uint32_t)num_cus() * Q6MF_W;
-    const uint32_t per = split ? Q6MF_W / 4 : Q6MF_W;            // tiles in flight per workgroup
+    // one wave per accumulator chain sb & 3 (up to 8 columns)
+    const bool split = T < (uint32_t)num_cus() * W;
+    if (split && NC == 16) return FLH_ERR_UNSUPPORTED;
+    const uint32_t per = split ? W / 4 : W;                       // tiles in flight per workgroup
     uint32_t G = (uint32_t)num_cus();
     if (G > (T + per - 1) / per) G = (T + per - 1) / per;
-    const uint32_t nwt = G * Q6MF_W;
+    const uint32_t nwt = G * W;
     auto go = [&](auto kern) {
         if (int rc = lds_fits((const void *)kern, smb, "k_dot_q6mf: LDS over the limit")) return rc;
         (void)hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smb);
-        hipLaunchKernelGGL(kern, dim3(G), dim3(64 * Q6MF_W), smb, s, a, nwt);
+        hipLaunchKernelGGL(kern, dim3(G), dim3(64 * W), smb, s, a, nwt);
         return hip_check(hipGetLastError(), "k_dot_q6mf launch");
     };
+    constexpr int W8 = (int)Q6MF_W;
+    if (NC == 16) return D == 3 ? go(k_dot_q6mf<16, 3, false, 6>) : go(k_dot_q6mf<16, 2, false, 6>);
     if (split) {
-        if (NC == 4) return D == 3 ? go(k_dot_q6mf<4, 3, true>) : go(k_dot_q6mf<4, 2, true>);
-        return D == 3 ? go(k_dot_q6mf<8, 3, true>) : go(k_dot_q6mf<8, 2, true>);
+        if (NC == 4) return D == 3 ? go(k_dot_q6mf<4, 3, true, W8>) : go(k_dot_q6mf<4, 2, true, W8>);
+        return D == 3 ? go(k_dot_q6mf<8, 3, true, W8>) : go(k_dot_q6mf<8, 2, true, W8>);
     }
-    if (NC == 4) return D == 3 ? go(k_dot_q6mf<4, 3, false>) : go(k_dot_q6mf<4, 2, false>);
-    return D == 3 ? go(k_dot_q6mf<8, 3, false>) : go(k_dot_q6mf<8, 2, false>);
+    if (NC == 4) return D == 3 ? go(k_dot_q6mf<4, 3, false, W8>) : go(k_dot_q6mf<4, 2, false, W8>);
+    return D == 3 ? go(k_dot_q6mf<8, 3, false, W8>) : go(k_dot_q6mf<8, 2, false, W8>);
 }
 
 }  // namespace flh

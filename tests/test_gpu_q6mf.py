@@ -52,11 +52,14 @@ def test_q6mf_expert_slot(flh, orc, gpu):
     assert np.array_equal(bits(got), bits(want))
 
 
-@pytest.mark.parametrize("rows,nx", [(65600, 5), (65600, 8), (65600, 11), (14336, 8), (12300, 6)])
+@pytest.mark.parametrize("rows,nx", [(65600, 5), (65600, 8), (65600, 11), (65600, 16), (50000, 9), (14336, 8),
+                                     (12300, 6), (14336, 13)])
 def test_q6mf_default_routing(flh, orc, gpu, rows, nx):
     """Past the routing floor (12288 rows, 5 columns) with the default tuning:
-    a wave per tile (vocab height) and four waves per tile (fewer tiles than
-    waves on the chip), bitwise against the oracle and the streaming kernel."""
+    a wave per tile (vocab height; 9-16 columns in one pass of six waves per
+    workgroup) and four waves per tile (fewer tiles than waves on the chip;
+    9-16 columns as two passes), bitwise against the oracle and the streaming
+    kernel."""
     cols = 512
     say("q6mf routed", rows, cols, nx)
     rng = np.random.default_rng(nx)
