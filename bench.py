@@ -296,10 +296,10 @@ def main():
             op_entry(f"q6_K_{name}_{r}x{c}_fast_f32", us, nb, {"route": "fast fp32 order (GPU default masks)"})
             cpu_in[f"q6_K_{name}_{r}x{c}"] = host_case(flh, s, Q6_K, ws[0], r, c, x, st, 1)
             if r > 100000:
-                # a speculative-verify batch through the vocab head: 4 and 8
-                # columns in one weight pass (4: the streaming kernel, 8: the Q6_K
-                # matrix-core kernel)
-                for n in (4, 8):
+                # a speculative-verify batch through the vocab head: 4, 8 and 16
+                # columns in one weight pass (4: the streaming kernel, 8 and 16:
+                # the Q6_K matrix-core kernel)
+                for n in (4, 8, 16):
                     xn, stn = B.activation(c, n, 35 + n, outliers=False)
                     yn = B.buf(n * r * 4)
                     us = B.time_graph(lambda i: flh.stream_dot(Q6_K, ws[i % len(ws)], r, c, xn, yn, s, nx=n,
